@@ -1,0 +1,147 @@
+/*
+ * ssa_hip.h -- C ABI of libssa_hip.so, the MI355X (gfx950) implementation of
+ * the SSA forward hot path (codebook routing, inverted index, candidate
+ * selection, gathered exact attention).
+ *
+ * Conventions
+ *   - Every pointer is device memory owned by the caller (the PyTorch caching
+ *     allocator in ssa_amd).  The library allocates nothing and never
+ *     synchronises: each call enqueues kernels on `stream` (a hipStream_t;
+ *     NULL = the default stream) and returns.
+ *   - Strides are in ELEMENTS; the last (feature) dimension is contiguous.
+ *   - Every function returns SSA_OK (0) or an error status; argument checks run
+ *     on the host before any launch.  ssa_last_error() gives the detail of the
+ *     last failure on the calling thread.
+ *   - Selections are bit-exact with the CPU oracle (oracle/ssa_oracle.c):
+ *     fp32 scoring in one canonical fmaf order, ties to the lowest index.
+ *
+ * Reference interfaces replaced (chenxingqiang/SSA):
+ *   CodebookRouter.forward        ssa/router.py:73-149
+ *     _select_candidates          ssa/router.py:151-214
+ *     _build_candidate_mask       ssa/router.py:216-259
+ *     get_code_assignment         ssa/router.py:261-275
+ *   sparse_exact_attention        ssa/attention.py:12-115
+ */
+#ifndef SSA_HIP_H
+#define SSA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* status codes */
+#define SSA_OK 0
+#define SSA_ERR_INVALID_ARGUMENT 1
+#define SSA_ERR_UNSUPPORTED 2
+#define SSA_ERR_WORKSPACE 3
+#define SSA_ERR_HIP 4
+
+/* element types of q / k / v / attention output */
+#define SSA_DTYPE_F32 0
+#define SSA_DTYPE_BF16 1
+
+/* index element types */
+#define SSA_INDEX_I32 0
+#define SSA_INDEX_I64 1
+
+/* candidate masks for ssa_select */
+#define SSA_MASK_NONE 0   /* causal_mask=None: every key is eligible            */
+#define SSA_MASK_CAUSAL 1 /* build_causal_mask(n): key j eligible iff j <= i     */
+#define SSA_MASK_DENSE 2  /* any bool [n][n] mask: eligible iff mask[i][j] != 0  */
+
+int ssa_version(void);
+const char* ssa_status_str(int status);
+const char* ssa_last_error(void);
+
+/* ---- stage (a): routing ------------------------------------------------- */
+
+/* Routing vectors: out[b][h][i] = normalize(mean_{gg<group}(x[b][i][h*group+gg] . w^T)).
+ * Replaces the W_qr / W_kr projection, the GQA mean and F.normalize of
+ * ssa/router.py:102-117 (group = h_q/h_kv for queries, 1 for keys).
+ *   x   [batch][n][h_in][d]  strides (x_sb, x_sn, x_sh)
+ *   w   fp32 [d_s][d] contiguous (nn.Linear weight)
+ *   out fp32 [batch][h_in/group][n][d_s] contiguous */
+int ssa_route_vectors(const void* x, int dtype, int64_t batch, int64_t n, int h_in, int group,
+                      int d, int64_t x_sb, int64_t x_sn, int64_t x_sh, const float* w, int d_s,
+                      float* out, void* stream);
+
+/* Row-wise F.normalize(x, dim=-1) of a fp32 [rows][d_s] matrix (the codebook,
+ * ssa/router.py:118). */
+int ssa_normalize_rows(const float* x, int64_t rows, int d_s, float* out, void* stream);
+
+/* Codebook scoring and top-`top` codes per row (score desc, code asc).
+ * Replaces einsum("shd,hcd->shc") / temperature and topk of ssa/router.py:121-130
+ * (keys, top = b) and :141 (queries, top = a).
+ *   xhat  fp32 [batch][h][rows][d_s]; chat fp32 [h][n_c][d_s] (normalized)
+ *   codes int32 [batch][h][rows][top] */
+int ssa_code_topk(const float* xhat, int64_t batch, int h, int64_t rows, const float* chat,
+                  int n_c, int d_s, float temperature, int top, int32_t* codes, void* stream);
+
+/* Stage (a) end to end: q_codes = top-a query codes, k_codes = top-b key codes.
+ * Replaces ssa/router.py:102-141.  The workspace holds the normalized routing
+ * vectors and codebook (ssa_route_workspace_bytes).
+ *   q [batch][n][h_q][d], k [batch][n][h_kv][d]; codebook fp32 [h_kv][n_c][d_s]
+ *   q_codes int32 [batch][h_kv][n][a]; k_codes int32 [batch][h_kv][n][b] */
+size_t ssa_route_workspace_bytes(int64_t batch, int64_t n, int h_kv, int n_c, int d_s);
+int ssa_route_codes(const void* q, const void* k, int dtype, int64_t batch, int64_t n, int h_q,
+                    int h_kv, int d, int64_t q_sb, int64_t q_sn, int64_t q_sh, int64_t k_sb,
+                    int64_t k_sn, int64_t k_sh, const float* w_qr, const float* w_kr,
+                    const float* codebook, int d_s, int n_c, int a, int b, float temperature,
+                    int32_t* q_codes, int32_t* k_codes, void* workspace, size_t workspace_bytes,
+                    void* stream);
+
+/* ---- stage (b): inverted index ------------------------------------------ */
+
+/* Bucket c of head h lists every key j with c in k_codes[b][h][j][:], ascending.
+ * No reference counterpart: it replaces the O(n^2) broadcast compare of
+ * _build_candidate_mask (ssa/router.py:241-257) and reproduces its set.
+ *   offsets  int32 [batch][h_kv][n_c+1]; postings int32 [batch][h_kv][n*b] */
+size_t ssa_index_workspace_bytes(int64_t batch, int64_t n, int h_kv, int b, int n_c);
+int ssa_build_index(const int32_t* k_codes, int64_t batch, int64_t n, int h_kv, int b, int n_c,
+                    int32_t* offsets, int32_t* postings, void* workspace, size_t workspace_bytes,
+                    void* stream);
+
+/* ---- stage (c): candidate selection ------------------------------------- */
+
+/* Top-k candidate keys per (query, kv head): union of the query's a buckets,
+ * masked, deduplicated, rescored as mean_g(q.k / score_div) in fp32, ranked
+ * (score desc, index asc); fewer than k candidates are followed by the lowest
+ * non-candidate indices; k > n pads with 0.  Replaces
+ * CodebookRouter._select_candidates (ssa/router.py:151-214).
+ *   out    [batch][n][h_kv][top_k], index type out_index_dtype
+ *   mask   (SSA_MASK_DENSE only) uint8 [batch][n][n], strides (mask_sb, mask_si); mask_sb may be 0
+ *   stats  (nullable) int32 [batch][h_kv][n][2] = (candidates, postings read)
+ * Limits: top_k <= 4096, g = h_q/h_kv <= 16, d <= 256, n < 2^31. */
+int ssa_select(const void* q, const void* k, int dtype, int64_t batch, int64_t n, int h_q,
+               int h_kv, int d, int64_t q_sb, int64_t q_sn, int64_t q_sh, int64_t k_sb,
+               int64_t k_sn, int64_t k_sh, const int32_t* q_codes, int a, const int32_t* offsets,
+               const int32_t* postings, int n_c, int b, int top_k, int mask_mode,
+               const uint8_t* mask, int64_t mask_sb, int64_t mask_si, float score_div, void* out,
+               int out_index_dtype, int32_t* stats, void* stream);
+
+/* ---- stage (d): gathered exact attention -------------------------------- */
+
+/* out[b][i][hq] = softmax_m(q[b][i][hq] . k[b][idx[b][i][h][m]][h] / scale_div) . v[...]
+ * with h = hq / (h_q/h_kv).  Replaces sparse_exact_attention (ssa/attention.py:12-115):
+ * `scale_div` is the reference's `scale` (a divisor); duplicates count twice.
+ * causal != 0 drops slots with idx > i (a row with no slot left outputs zeros).
+ * Indices outside [0, n) are dropped and set *error_flag (nullable) to 1.
+ *   idx [batch][n][h_kv][top_k] strides (idx_sb, idx_sn, idx_sh)
+ *   out [batch][n][h_q][d] strides (o_sb, o_sn, o_sh), type out_dtype
+ * Limits: d in {64, 128, 256}, g <= 16. */
+int ssa_sparse_attention(const void* q, const void* k, const void* v, int dtype, int64_t batch,
+                         int64_t n, int h_q, int h_kv, int d, int64_t q_sb, int64_t q_sn,
+                         int64_t q_sh, int64_t k_sb, int64_t k_sn, int64_t k_sh, int64_t v_sb,
+                         int64_t v_sn, int64_t v_sh, const void* idx, int idx_dtype, int top_k,
+                         int64_t idx_sb, int64_t idx_sn, int64_t idx_sh, float scale_div,
+                         int causal, void* out, int out_dtype, int64_t o_sb, int64_t o_sn,
+                         int64_t o_sh, int32_t* error_flag, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SSA_HIP_H */

@@ -1,0 +1,87 @@
+"""Stage 3 of SSA: exact softmax attention over selected keys (ssa/attention.py).
+
+``sparse_exact_attention`` runs the gathered-KV HIP kernel of libssa_hip;
+``dense_attention`` is the reference's plain PyTorch SDPA, kept for the
+``use_dense`` comparison path and k = n checks.
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+import torch.nn.functional as F
+
+from . import _lib, kernels
+
+
+def sparse_exact_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    indices: torch.Tensor,
+    scale: Optional[float] = None,
+    *,
+    causal: bool = False,
+    check_indices: bool = True,
+) -> torch.Tensor:
+    """softmax(q . K[indices]^T / scale) . V[indices] per (query, KV head).
+
+    Drop-in for ssa/attention.py:12-115: ``q [n, h_q, d]``, ``k, v [n, h_kv, d]``,
+    ``indices [n, h_kv, top_k]`` (int64 or int32; batched ``[B, ...]`` shapes
+    also accepted); ``scale`` is a divisor defaulting to sqrt(d); query head j
+    uses KV head ``j // (h_q // h_kv)``; duplicated indices count twice.
+
+    Keyword-only extensions: ``causal=True`` drops indices > query position (a
+    row left with no index outputs zeros); ``check_indices`` raises IndexError
+    (after a device sync) if any index is outside [0, n), as the reference's
+    gather does -- out-of-range slots are never read either way.
+    """
+    unbatched = q.dim() == 3
+    if unbatched:
+        q, k, v, indices = q.unsqueeze(0), k.unsqueeze(0), v.unsqueeze(0), indices.unsqueeze(0)
+    seq_len, num_q_heads, head_dim = q.shape[1], q.shape[2], q.shape[3]
+    num_kv_heads = k.shape[2]
+    assert num_q_heads % num_kv_heads == 0
+    if scale is None:
+        scale = head_dim**0.5
+    _lib.require_device(q, k, v, indices)
+    out_dtype = q.dtype
+    if q.dtype == torch.float16:
+        q, k, v = q.float(), k.float(), v.float()
+    q, k, v = (t if t.stride(-1) == 1 else t.contiguous() for t in (q, k, v))
+    if indices.stride(-1) != 1:
+        indices = indices.contiguous()
+    flag = torch.zeros(1, device=q.device, dtype=torch.int32) if check_indices else None
+    out = kernels.sparse_attention(q, k, v, indices, float(scale), causal, error_flag=flag)
+    if flag is not None and int(flag.item()) != 0:
+        raise IndexError(f"sparse_exact_attention: an index is outside [0, {seq_len})")
+    if out.dtype != out_dtype:
+        out = out.to(out_dtype)
+    return out[0] if unbatched else out
+
+
+def dense_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    causal_mask: Optional[torch.Tensor] = None,
+    scale: Optional[float] = None,
+) -> torch.Tensor:
+    """Dense scaled dot-product attention with GQA (ssa/attention.py:118-158).
+
+    ``q [n, h_q, d]``, ``k, v [n, h_kv, d]``, optional bool ``[n, n]`` mask
+    (True = allowed), ``scale`` a divisor defaulting to sqrt(d).
+    """
+    seq_len, num_q_heads, head_dim = q.shape
+    num_kv_heads = k.shape[1]
+    if scale is None:
+        scale = head_dim**0.5
+    g = num_q_heads // num_kv_heads
+    k_exp = k.unsqueeze(2).expand(-1, -1, g, -1).reshape(seq_len, num_q_heads, head_dim)
+    v_exp = v.unsqueeze(2).expand(-1, -1, g, -1).reshape(seq_len, num_q_heads, head_dim)
+    logits = torch.matmul(q.transpose(0, 1), k_exp.permute(1, 2, 0).contiguous()) / scale
+    if causal_mask is not None:
+        logits = logits.masked_fill(~causal_mask.unsqueeze(0), float("-inf"))
+    w = F.softmax(logits, dim=-1)
+    return torch.matmul(w, v_exp.transpose(0, 1).contiguous()).transpose(0, 1)

@@ -1,0 +1,67 @@
+// Shared device helpers and host-side status plumbing for libssa_hip.
+//
+// Arithmetic contract (identical to the CPU oracle, bit for bit):
+//   * inputs are widened exactly to fp32; every dot product is one fmaf chain
+//     in ascending index order from +0.0f;
+//   * division and sqrt are IEEE correctly rounded (the library is built with
+//     -fhip-fp32-correctly-rounded-divide-sqrt, -ffp-contract=off and no
+//     denormal flushing);
+//   * selections order by the 64-bit composite key
+//     (ordered_bits(score) << 32) | (0xFFFFFFFF - index): larger is better,
+//     so ties on score go to the lowest index.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "ssa_hip.h"
+
+namespace ssa {
+
+// ------------------------------------------------------------------ device
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t u) {
+  return __uint_as_float(static_cast<uint32_t>(u) << 16);
+}
+
+// Element loaders: T is the storage type (float or uint16_t holding bf16 bits).
+__device__ __forceinline__ float ld(const float* p) { return *p; }
+__device__ __forceinline__ float ld(const uint16_t* p) { return bf16_bits_to_f32(*p); }
+
+// Monotone map float -> uint32; -0.0 folds into +0.0.
+__device__ __forceinline__ uint32_t score_key(float s) {
+  uint32_t u = __float_as_uint(s);
+  if (u == 0x80000000u) u = 0u;
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ uint64_t composite_key(float s, uint32_t idx) {
+  return (static_cast<uint64_t>(score_key(s)) << 32) | static_cast<uint64_t>(0xFFFFFFFFu - idx);
+}
+
+__device__ __forceinline__ uint32_t key_index(uint64_t key) {
+  return 0xFFFFFFFFu - static_cast<uint32_t>(key & 0xFFFFFFFFull);
+}
+
+// fp32 fused multiply-add, single rounding (v_fma_f32).
+__device__ __forceinline__ float fma_rn(float a, float b, float c) { return __builtin_fmaf(a, b, c); }
+
+// ------------------------------------------------------------------ host
+
+// Records a human-readable detail for the last failing call on this thread.
+int fail(int status, const char* fmt, ...);
+
+// Maps a pending HIP launch error to SSA_ERR_HIP (and records its text).
+int check_launch(const char* what);
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Makes `bytes` of dynamic LDS available to `kernel` on the current device, or
+// fails with SSA_ERR_UNSUPPORTED when the device cannot provide it.
+int reserve_lds(const void* kernel, size_t bytes, const char* what);
+
+__host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+}  // namespace ssa

@@ -1,0 +1,375 @@
+// Stage (a): routing vectors and codebook top-codes.
+//
+// Replaces ssa/router.py:102-141 (projection, GQA mean, F.normalize, codebook
+// einsum / temperature, topk).  All arithmetic is exact-order fp32 so that the
+// selected codes are bit-identical with the CPU oracle.
+#include "ssa_common.h"
+
+namespace ssa {
+namespace {
+
+constexpr int kRouteThreads = 256;
+constexpr int kRouteRowsPerThread = 4;
+
+// One thread owns one routing coordinate s for kRouteRowsPerThread rows:
+//   out[b][h][i][s] = normalize_s( (sum_gg chain_t x[b][i][h*g+gg][t] * w[s][t]) / g )
+// W and a tile of x rows (one GQA head at a time) are staged in LDS as fp32.
+template <typename T>
+__global__ __launch_bounds__(kRouteThreads) void route_vectors_kernel(
+    const T* __restrict__ x, int64_t n, int h_in, int group, int d, int64_t sb, int64_t sn,
+    int64_t sh, const float* __restrict__ w, int d_s, int dsp, float* __restrict__ out) {
+  extern __shared__ __align__(16) float smem[];
+  const int dpad = d + 4;
+  const int rows_per_pass = kRouteThreads / dsp;
+  const int rb = rows_per_pass * kRouteRowsPerThread;
+  float* Ws = smem;                // [d_s][dpad]
+  float* Xs = Ws + d_s * dpad;     // [rb][dpad]
+  float* red = Xs + rb * dpad;     // [rb][d_s]
+
+  const int h_out = h_in / group;
+  const int64_t tiles = (n + rb - 1) / rb;
+  const int64_t bh = blockIdx.x / tiles;
+  const int64_t i0 = (blockIdx.x % tiles) * rb;
+  const int64_t b = bh / h_out;
+  const int h = static_cast<int>(bh % h_out);
+  const int tid = threadIdx.x;
+
+  for (int e = tid; e < d_s * d; e += kRouteThreads) Ws[(e / d) * dpad + (e % d)] = w[e];
+
+  const int r = tid / dsp;
+  const int s = tid % dsp;
+  const bool lane_ok = (r < rows_per_pass) && (s < d_s);
+  float sum[kRouteRowsPerThread];
+#pragma unroll
+  for (int u = 0; u < kRouteRowsPerThread; ++u) sum[u] = 0.0f;
+
+  for (int gg = 0; gg < group; ++gg) {
+    __syncthreads();
+    const T* xh = x + b * sb + static_cast<int64_t>(h * group + gg) * sh;
+    for (int e = tid; e < rb * d; e += kRouteThreads) {
+      const int rr = e / d, t = e % d;
+      const int64_t i = i0 + rr;
+      Xs[rr * dpad + t] = (i < n) ? ld(xh + i * sn + t) : 0.0f;
+    }
+    __syncthreads();
+    if (lane_ok) {
+      const float* wr = Ws + s * dpad;
+      float acc[kRouteRowsPerThread];
+#pragma unroll
+      for (int u = 0; u < kRouteRowsPerThread; ++u) acc[u] = 0.0f;
+      for (int t = 0; t < d; t += 4) {
+        const float4 wv = *reinterpret_cast<const float4*>(wr + t);
+#pragma unroll
+        for (int u = 0; u < kRouteRowsPerThread; ++u) {
+          const float4 xv =
+              *reinterpret_cast<const float4*>(Xs + (r + u * rows_per_pass) * dpad + t);
+          acc[u] = fma_rn(xv.x, wv.x, acc[u]);
+          acc[u] = fma_rn(xv.y, wv.y, acc[u]);
+          acc[u] = fma_rn(xv.z, wv.z, acc[u]);
+          acc[u] = fma_rn(xv.w, wv.w, acc[u]);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kRouteRowsPerThread; ++u) sum[u] = (gg == 0) ? acc[u] : sum[u] + acc[u];
+    }
+  }
+
+  float val[kRouteRowsPerThread];
+#pragma unroll
+  for (int u = 0; u < kRouteRowsPerThread; ++u) {
+    val[u] = sum[u] / static_cast<float>(group);
+    if (lane_ok) red[(r + u * rows_per_pass) * d_s + s] = val[u];
+  }
+  __syncthreads();
+  if (!lane_ok) return;
+#pragma unroll
+  for (int u = 0; u < kRouteRowsPerThread; ++u) {
+    const int rr = r + u * rows_per_pass;
+    if (i0 + rr >= n) continue;
+    const float* y = red + rr * d_s;
+    float nrm = 0.0f;
+    for (int v = 0; v < d_s; ++v) nrm = fma_rn(y[v], y[v], nrm);
+    const float den = fmaxf(sqrtf(nrm), 1e-12f);
+    out[(bh * n + i0 + rr) * d_s + s] = val[u] / den;
+  }
+}
+
+// Row-wise F.normalize: one thread per row.
+__global__ void normalize_rows_kernel(const float* __restrict__ x, int64_t rows, int d_s,
+                                      float* __restrict__ out) {
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (r >= rows) return;
+  const float* xr = x + r * d_s;
+  float nrm = 0.0f;
+  for (int s = 0; s < d_s; ++s) nrm = fma_rn(xr[s], xr[s], nrm);
+  const float den = fmaxf(sqrtf(nrm), 1e-12f);
+  for (int s = 0; s < d_s; ++s) out[r * d_s + s] = xr[s] / den;
+}
+
+constexpr int kTopRows = 64;   // rows (tokens) per block
+constexpr int kTopCodes = 64;  // codes per streamed tile
+constexpr int kTopThreads = 256;
+
+__host__ __device__ inline size_t code_topk_smem(int d_s, int top) {
+  return sizeof(float) * static_cast<size_t>(d_s) * ((kTopRows + 4) + (kTopCodes + 4)) +
+         sizeof(uint64_t) * (static_cast<size_t>(kTopRows) * kTopCodes +
+                             static_cast<size_t>(kTopRows) * top + kTopRows) +
+         sizeof(int) * 2 * kTopRows;
+}
+
+// Scores a 64-row tile against the codebook in 64-code tiles (each thread owns a
+// 4x4 register tile, one fmaf chain over s per score) and keeps each row's
+// top-`top` composite keys in LDS.  A score enters a row's candidate buffer only
+// if it beats the row's current top-th key; one thread per row merges the buffer
+// by insertion after each tile.
+__global__ __launch_bounds__(kTopThreads) void code_topk_kernel(
+    const float* __restrict__ xhat, int64_t rows, int h, const float* __restrict__ chat, int n_c,
+    int d_s, float temperature, int top, int32_t* __restrict__ codes) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  constexpr int rpad = kTopRows + 4, cpad = kTopCodes + 4;
+  float* Xs = reinterpret_cast<float*>(smem_raw);                // [d_s][rpad]
+  float* Cs = Xs + d_s * rpad;                                   // [d_s][cpad]
+  uint64_t* cand = reinterpret_cast<uint64_t*>(Cs + d_s * cpad);  // [rows][codes]
+  uint64_t* best = cand + kTopRows * kTopCodes;                  // [rows][top]
+  uint64_t* thr = best + kTopRows * top;                         // [rows]
+  int* cnt = reinterpret_cast<int*>(thr + kTopRows);             // [rows]
+  int* bcnt = cnt + kTopRows;                                    // [rows]
+
+  const int64_t tiles = (rows + kTopRows - 1) / kTopRows;
+  const int64_t bh = blockIdx.x / tiles;
+  const int64_t r0 = (blockIdx.x % tiles) * kTopRows;
+  const int hh = static_cast<int>(bh % h);
+  const float* xb = xhat + bh * rows * d_s;
+  const float* cb = chat + static_cast<int64_t>(hh) * n_c * d_s;
+  const int tid = threadIdx.x;
+
+  for (int e = tid; e < kTopRows * d_s; e += kTopThreads) {
+    const int r = e / d_s, s = e % d_s;
+    Xs[s * rpad + r] = (r0 + r < rows) ? xb[(r0 + r) * d_s + s] : 0.0f;
+  }
+  if (tid < kTopRows) {
+    thr[tid] = 0ull;
+    cnt[tid] = 0;
+    bcnt[tid] = 0;
+  }
+  const int rg = tid >> 4, cg = tid & 15;
+  const bool scale = (temperature != 1.0f);
+
+  for (int c0 = 0; c0 < n_c; c0 += kTopCodes) {
+    for (int e = tid; e < kTopCodes * d_s; e += kTopThreads) {
+      const int c = e / d_s, s = e % d_s;
+      Cs[s * cpad + c] = (c0 + c < n_c) ? cb[static_cast<int64_t>(c0 + c) * d_s + s] : 0.0f;
+    }
+    __syncthreads();
+    float acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
+    for (int s = 0; s < d_s; ++s) {
+      const float4 xv = *reinterpret_cast<const float4*>(Xs + s * rpad + rg * 4);
+      const float4 cv = *reinterpret_cast<const float4*>(Cs + s * cpad + cg * 4);
+      const float xa[4] = {xv.x, xv.y, xv.z, xv.w};
+      const float ca[4] = {cv.x, cv.y, cv.z, cv.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = fma_rn(xa[i], ca[j], acc[i][j]);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = rg * 4 + i;
+      if (r0 + r >= rows) continue;
+      const uint64_t th = thr[r];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int c = c0 + cg * 4 + j;
+        if (c >= n_c) continue;
+        float sc = acc[i][j];
+        if (scale) sc = sc / temperature;
+        const uint64_t key = composite_key(sc, static_cast<uint32_t>(c));
+        if (key > th) {
+          const int slot = atomicAdd(&cnt[r], 1);
+          cand[r * kTopCodes + slot] = key;
+        }
+      }
+    }
+    __syncthreads();
+    if (tid < kTopRows) {
+      const int r = tid;
+      int nb = bcnt[r];
+      const int nc = cnt[r];
+      uint64_t* bl = best + r * top;
+      for (int m = 0; m < nc; ++m) {
+        const uint64_t key = cand[r * kTopCodes + m];
+        if (nb == top && key <= bl[top - 1]) continue;
+        int p = (nb < top) ? nb++ : top - 1;
+        while (p > 0 && bl[p - 1] < key) {
+          bl[p] = bl[p - 1];
+          --p;
+        }
+        bl[p] = key;
+      }
+      bcnt[r] = nb;
+      cnt[r] = 0;
+      thr[r] = (nb == top) ? bl[top - 1] : 0ull;
+    }
+  }
+  __syncthreads();
+  for (int e = tid; e < kTopRows * top; e += kTopThreads) {
+    const int r = e / top, m = e % top;
+    if (r0 + r < rows) codes[(bh * rows + r0 + r) * top + m] = static_cast<int32_t>(key_index(best[r * top + m]));
+  }
+}
+
+int next_pow2(int v) {
+  int p = 1;
+  while (p < v) p <<= 1;
+  return p;
+}
+
+size_t route_vectors_smem(int d, int d_s) {
+  const int dsp = next_pow2(d_s);
+  const int rb = (kRouteThreads / dsp) * kRouteRowsPerThread;
+  return sizeof(float) * (static_cast<size_t>(d_s) * (d + 4) + static_cast<size_t>(rb) * (d + 4) +
+                          static_cast<size_t>(rb) * d_s);
+}
+
+int check_route_vectors(int dtype, int64_t batch, int64_t n, int h_in, int group, int d, int d_s) {
+  if (dtype != SSA_DTYPE_F32 && dtype != SSA_DTYPE_BF16)
+    return fail(SSA_ERR_UNSUPPORTED, "route_vectors: dtype %d not supported (f32, bf16)", dtype);
+  if (batch < 0 || n < 0 || h_in <= 0 || group <= 0 || d <= 0 || d_s <= 0)
+    return fail(SSA_ERR_INVALID_ARGUMENT, "route_vectors: non-positive shape");
+  if (h_in % group != 0)
+    return fail(SSA_ERR_INVALID_ARGUMENT, "num_q_heads must be divisible by num_kv_heads");
+  if (d % 4 != 0 || d_s > 256)
+    return fail(SSA_ERR_UNSUPPORTED, "route_vectors: need head_dim %% 4 == 0 and route_dim <= 256");
+  if (route_vectors_smem(d, d_s) > 64 * 1024)
+    return fail(SSA_ERR_UNSUPPORTED, "route_vectors: head_dim*route_dim too large for LDS");
+  return SSA_OK;
+}
+
+int launch_route_vectors(const void* x, int dtype, int64_t batch, int64_t n, int h_in, int group,
+                         int d, int64_t sb, int64_t sn, int64_t sh, const float* w, int d_s,
+                         float* out, hipStream_t st) {
+  if (batch == 0 || n == 0) return SSA_OK;
+  const int dsp = next_pow2(d_s);
+  const int rb = (kRouteThreads / dsp) * kRouteRowsPerThread;
+  const int64_t grid = batch * (h_in / group) * ceil_div(n, rb);
+  const size_t smem = route_vectors_smem(d, d_s);
+  if (dtype == SSA_DTYPE_BF16)
+    route_vectors_kernel<uint16_t><<<dim3(static_cast<unsigned>(grid)), kRouteThreads, smem, st>>>(
+        static_cast<const uint16_t*>(x), n, h_in, group, d, sb, sn, sh, w, d_s, dsp, out);
+  else
+    route_vectors_kernel<float><<<dim3(static_cast<unsigned>(grid)), kRouteThreads, smem, st>>>(
+        static_cast<const float*>(x), n, h_in, group, d, sb, sn, sh, w, d_s, dsp, out);
+  return check_launch("route_vectors_kernel");
+}
+
+int check_code_topk(int64_t batch, int h, int64_t rows, int n_c, int d_s, float temperature,
+                    int top) {
+  if (batch < 0 || h <= 0 || rows < 0 || n_c <= 0 || d_s <= 0)
+    return fail(SSA_ERR_INVALID_ARGUMENT, "code_topk: non-positive shape");
+  if (top <= 0 || top > n_c)
+    return fail(SSA_ERR_INVALID_ARGUMENT, "code_topk: top=%d must be in [1, num_codebook=%d]",
+                top, n_c);
+  if (top > 64) return fail(SSA_ERR_UNSUPPORTED, "code_topk: top=%d > 64", top);
+  if (d_s > 128) return fail(SSA_ERR_UNSUPPORTED, "code_topk: route_dim %d > 128", d_s);
+  if (!(temperature > 0.0f)) return fail(SSA_ERR_INVALID_ARGUMENT, "temperature must be > 0");
+  return SSA_OK;
+}
+
+int launch_code_topk(const float* xhat, int64_t batch, int h, int64_t rows, const float* chat,
+                     int n_c, int d_s, float temperature, int top, int32_t* codes, hipStream_t st) {
+  if (batch == 0 || rows == 0) return SSA_OK;
+  const int64_t grid = batch * h * ceil_div(rows, kTopRows);
+  const size_t smem = code_topk_smem(d_s, top);
+  if (int s = reserve_lds(reinterpret_cast<const void*>(code_topk_kernel), smem, "code_topk")) return s;
+  code_topk_kernel<<<dim3(static_cast<unsigned>(grid)), kTopThreads, smem, st>>>(
+      xhat, rows, h, chat, n_c, d_s, temperature, top, codes);
+  return check_launch("code_topk_kernel");
+}
+
+int launch_normalize(const float* x, int64_t rows, int d_s, float* out, hipStream_t st) {
+  if (rows == 0) return SSA_OK;
+  normalize_rows_kernel<<<dim3(static_cast<unsigned>(ceil_div(rows, 256))), 256, 0, st>>>(x, rows, d_s,
+                                                                                         out);
+  return check_launch("normalize_rows_kernel");
+}
+
+}  // namespace
+}  // namespace ssa
+
+using namespace ssa;
+
+extern "C" int ssa_route_vectors(const void* x, int dtype, int64_t batch, int64_t n, int h_in,
+                                 int group, int d, int64_t x_sb, int64_t x_sn, int64_t x_sh,
+                                 const float* w, int d_s, float* out, void* stream) {
+  int st = check_route_vectors(dtype, batch, n, h_in, group, d, d_s);
+  if (st) return st;
+  if (batch * n > 0 && (!x || !w || !out))
+    return fail(SSA_ERR_INVALID_ARGUMENT, "route_vectors: null pointer");
+  return launch_route_vectors(x, dtype, batch, n, h_in, group, d, x_sb, x_sn, x_sh, w, d_s, out,
+                              as_stream(stream));
+}
+
+extern "C" int ssa_normalize_rows(const float* x, int64_t rows, int d_s, float* out,
+                                  void* stream) {
+  if (rows < 0 || d_s <= 0) return fail(SSA_ERR_INVALID_ARGUMENT, "normalize_rows: bad shape");
+  if (rows > 0 && (!x || !out)) return fail(SSA_ERR_INVALID_ARGUMENT, "normalize_rows: null pointer");
+  return launch_normalize(x, rows, d_s, out, as_stream(stream));
+}
+
+extern "C" int ssa_code_topk(const float* xhat, int64_t batch, int h, int64_t rows,
+                             const float* chat, int n_c, int d_s, float temperature, int top,
+                             int32_t* codes, void* stream) {
+  int st = check_code_topk(batch, h, rows, n_c, d_s, temperature, top);
+  if (st) return st;
+  if (batch * rows > 0 && (!xhat || !chat || !codes))
+    return fail(SSA_ERR_INVALID_ARGUMENT, "code_topk: null pointer");
+  return launch_code_topk(xhat, batch, h, rows, chat, n_c, d_s, temperature, top, codes,
+                          as_stream(stream));
+}
+
+extern "C" size_t ssa_route_workspace_bytes(int64_t batch, int64_t n, int h_kv, int n_c,
+                                            int d_s) {
+  if (batch < 0 || n < 0 || h_kv <= 0 || n_c <= 0 || d_s <= 0) return 0;
+  const size_t vec = align_up(sizeof(float) * static_cast<size_t>(batch * h_kv * n * d_s), 256);
+  const size_t cb = align_up(sizeof(float) * static_cast<size_t>(h_kv) * n_c * d_s, 256);
+  return 2 * vec + cb;
+}
+
+extern "C" int ssa_route_codes(const void* q, const void* k, int dtype, int64_t batch, int64_t n,
+                               int h_q, int h_kv, int d, int64_t q_sb, int64_t q_sn, int64_t q_sh,
+                               int64_t k_sb, int64_t k_sn, int64_t k_sh, const float* w_qr,
+                               const float* w_kr, const float* codebook, int d_s, int n_c, int a,
+                               int b, float temperature, int32_t* q_codes, int32_t* k_codes,
+                               void* workspace, size_t workspace_bytes, void* stream) {
+  if (h_kv <= 0 || h_q <= 0 || h_q % h_kv != 0)
+    return fail(SSA_ERR_INVALID_ARGUMENT, "num_q_heads must be divisible by num_kv_heads");
+  const int g = h_q / h_kv;
+  int st = check_route_vectors(dtype, batch, n, h_q, g, d, d_s);
+  if (!st) st = check_route_vectors(dtype, batch, n, h_kv, 1, d, d_s);
+  if (!st) st = check_code_topk(batch, h_kv, n, n_c, d_s, temperature, a);
+  if (!st) st = check_code_topk(batch, h_kv, n, n_c, d_s, temperature, b);
+  if (st) return st;
+  const size_t need = ssa_route_workspace_bytes(batch, n, h_kv, n_c, d_s);
+  if (workspace_bytes < need)
+    return fail(SSA_ERR_WORKSPACE, "route_codes: workspace %zu < %zu bytes", workspace_bytes, need);
+  if (batch * n == 0) return SSA_OK;
+  if (!q || !k || !w_qr || !w_kr || !codebook || !q_codes || !k_codes || !workspace)
+    return fail(SSA_ERR_INVALID_ARGUMENT, "route_codes: null pointer");
+  hipStream_t s = as_stream(stream);
+  const size_t vec = align_up(sizeof(float) * static_cast<size_t>(batch * h_kv * n * d_s), 256);
+  float* qhat = static_cast<float*>(workspace);
+  float* khat = reinterpret_cast<float*>(static_cast<char*>(workspace) + vec);
+  float* chat = reinterpret_cast<float*>(static_cast<char*>(workspace) + 2 * vec);
+  if ((st = launch_route_vectors(q, dtype, batch, n, h_q, g, d, q_sb, q_sn, q_sh, w_qr, d_s, qhat, s)))
+    return st;
+  if ((st = launch_route_vectors(k, dtype, batch, n, h_kv, 1, d, k_sb, k_sn, k_sh, w_kr, d_s, khat, s)))
+    return st;
+  if ((st = launch_normalize(codebook, static_cast<int64_t>(h_kv) * n_c, d_s, chat, s))) return st;
+  if ((st = launch_code_topk(qhat, batch, h_kv, n, chat, n_c, d_s, temperature, a, q_codes, s)))
+    return st;
+  return launch_code_topk(khat, batch, h_kv, n, chat, n_c, d_s, temperature, b, k_codes, s);
+}

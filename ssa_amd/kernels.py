@@ -1,0 +1,175 @@
+"""Tensor-level wrappers over the libssa_hip entry points (one per C-ABI call).
+
+All sequence tensors are batched ``[B, n, heads, d]`` views whose last
+dimension is contiguous; other strides are passed through, so transposed
+layouts such as HF's ``[B, heads, n, d]`` (permuted) need no copy.  Outputs and
+workspaces come from the PyTorch caching allocator on the input's device, and
+every call is enqueued on the current stream without synchronising.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib
+from ._lib import call, ptr, stream_of
+
+
+def _check_rows(x: torch.Tensor, name: str) -> None:
+    if x.dim() != 4:
+        raise ValueError(f"{name} must be [B, n, heads, d], got shape {tuple(x.shape)}")
+    if x.stride(-1) != 1:
+        raise ValueError(f"{name} must have a contiguous last dimension")
+
+
+def _f32c(t: torch.Tensor) -> torch.Tensor:
+    return t.detach().to(torch.float32).contiguous()
+
+
+def route_vectors(x: torch.Tensor, w: torch.Tensor, group: int) -> torch.Tensor:
+    """normalize(mean_g(x . w^T)) -> float32 [B, heads/group, n, d_s] (ssa/router.py:102-117)."""
+    _check_rows(x, "x")
+    _lib.require_device(x, w)
+    B, n, h_in, d = x.shape
+    w = _f32c(w)
+    d_s = w.shape[0]
+    out = torch.empty((B, h_in // group, n, d_s), device=x.device, dtype=torch.float32)
+    call("ssa_route_vectors", ptr(x), _lib.elem_dtype(x), B, n, h_in, group, d,
+         x.stride(0), x.stride(1), x.stride(2), ptr(w), d_s, ptr(out), stream_of(x))
+    return out
+
+
+def normalize_rows(x: torch.Tensor) -> torch.Tensor:
+    """Row-wise F.normalize of a float32 matrix (ssa/router.py:118)."""
+    _lib.require_device(x)
+    x = _f32c(x)
+    out = torch.empty_like(x)
+    d_s = x.shape[-1]
+    call("ssa_normalize_rows", ptr(x), x.numel() // d_s, d_s, ptr(out), stream_of(x))
+    return out
+
+
+def code_topk(xhat: torch.Tensor, chat: torch.Tensor, top: int,
+              temperature: float = 1.0) -> torch.Tensor:
+    """Top-`top` codes per row, int32 [B, h, rows, top] (ssa/router.py:121-130,141)."""
+    _lib.require_device(xhat, chat)
+    xhat = xhat.contiguous()
+    chat = chat.contiguous()
+    B, h, rows, d_s = xhat.shape
+    n_c = chat.shape[1]
+    codes = torch.empty((B, h, rows, top), device=xhat.device, dtype=torch.int32)
+    call("ssa_code_topk", ptr(xhat), B, h, rows, ptr(chat), n_c, d_s, float(temperature), top,
+         ptr(codes), stream_of(xhat))
+    return codes
+
+
+def route_codes(q: torch.Tensor, k: torch.Tensor, w_qr: torch.Tensor, w_kr: torch.Tensor,
+                codebook: torch.Tensor, a: int, b: int,
+                temperature: float = 1.0) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Stage (a): (q_codes int32 [B,h_kv,n,a], k_codes int32 [B,h_kv,n,b])."""
+    _check_rows(q, "q")
+    _check_rows(k, "k")
+    _lib.require_device(q, k, w_qr, w_kr, codebook)
+    if q.dtype != k.dtype:
+        raise TypeError(f"q and k must share a dtype ({q.dtype} vs {k.dtype})")
+    B, n, h_q, d = q.shape
+    h_kv = k.shape[2]
+    w_qr, w_kr, codebook = _f32c(w_qr), _f32c(w_kr), _f32c(codebook)
+    n_c, d_s = codebook.shape[1], codebook.shape[2]
+    dev = q.device
+    q_codes = torch.empty((B, h_kv, n, a), device=dev, dtype=torch.int32)
+    k_codes = torch.empty((B, h_kv, n, b), device=dev, dtype=torch.int32)
+    ws_bytes = _lib.load().ssa_route_workspace_bytes(B, n, h_kv, n_c, d_s)
+    ws = torch.empty(max(int(ws_bytes), 1), device=dev, dtype=torch.uint8)
+    call("ssa_route_codes", ptr(q), ptr(k), _lib.elem_dtype(q), B, n, h_q, h_kv, d,
+         q.stride(0), q.stride(1), q.stride(2), k.stride(0), k.stride(1), k.stride(2),
+         ptr(w_qr), ptr(w_kr), ptr(codebook), d_s, n_c, a, b, float(temperature),
+         ptr(q_codes), ptr(k_codes), ptr(ws), ws_bytes, stream_of(q))
+    return q_codes, k_codes
+
+
+def build_index(k_codes: torch.Tensor, n_c: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Stage (b): offsets int32 [B,h,n_c+1], postings int32 [B,h,n*b] (ascending per bucket)."""
+    _lib.require_device(k_codes)
+    k_codes = k_codes.contiguous()
+    B, h, n, b = k_codes.shape
+    dev = k_codes.device
+    offsets = torch.empty((B, h, n_c + 1), device=dev, dtype=torch.int32)
+    postings = torch.empty((B, h, n * b), device=dev, dtype=torch.int32)
+    ws_bytes = _lib.load().ssa_index_workspace_bytes(B, n, h, b, n_c)
+    ws = torch.empty(max(int(ws_bytes), 1), device=dev, dtype=torch.uint8)
+    call("ssa_build_index", ptr(k_codes), B, n, h, b, n_c, ptr(offsets), ptr(postings), ptr(ws),
+         ws_bytes, stream_of(k_codes))
+    return offsets, postings
+
+
+def select(q: torch.Tensor, k: torch.Tensor, q_codes: torch.Tensor, offsets: torch.Tensor,
+           postings: torch.Tensor, b: int, top_k: int, mask_mode: int = _lib.MASK_CAUSAL,
+           mask: Optional[torch.Tensor] = None, score_div: Optional[float] = None,
+           index_dtype: torch.dtype = torch.int64,
+           with_stats: bool = False):
+    """Stage (c): candidate indices [B, n, h_kv, top_k] (ssa/router.py:151-214).
+
+    ``mask`` (MASK_DENSE) is a bool/uint8 ``[n, n]`` or ``[B, n, n]`` tensor with a
+    contiguous last dimension.  ``with_stats`` also returns int32 ``[B, h_kv, n, 2]``
+    (unique candidates, postings read) per row.
+    """
+    _check_rows(q, "q")
+    _check_rows(k, "k")
+    _lib.require_device(q, k, q_codes, offsets, postings, mask)
+    B, n, h_q, d = q.shape
+    h_kv = k.shape[2]
+    a = q_codes.shape[-1]
+    n_c = offsets.shape[-1] - 1
+    q_codes, offsets, postings = q_codes.contiguous(), offsets.contiguous(), postings.contiguous()
+    if score_div is None:
+        score_div = float(torch.tensor(d ** 0.5, dtype=torch.float32))
+    m_sb = m_si = 0
+    if mask_mode == _lib.MASK_DENSE:
+        if mask is None:
+            raise ValueError("MASK_DENSE needs a mask tensor")
+        if mask.dtype == torch.bool:
+            mask = mask.view(torch.uint8)
+        if mask.stride(-1) != 1:
+            mask = mask.contiguous()
+        if mask.dim() == 2:
+            m_sb, m_si = 0, mask.stride(0)
+        else:
+            m_sb, m_si = mask.stride(0), mask.stride(1)
+    out = torch.empty((B, n, h_kv, top_k), device=q.device, dtype=index_dtype)
+    stats = torch.empty((B, h_kv, n, 2), device=q.device, dtype=torch.int32) if with_stats else None
+    call("ssa_select", ptr(q), ptr(k), _lib.elem_dtype(q), B, n, h_q, h_kv, d,
+         q.stride(0), q.stride(1), q.stride(2), k.stride(0), k.stride(1), k.stride(2),
+         ptr(q_codes), a, ptr(offsets), ptr(postings), n_c, b, top_k, mask_mode, ptr(mask),
+         m_sb, m_si, float(score_div), ptr(out), _lib.index_dtype(out), ptr(stats),
+         stream_of(q))
+    return (out, stats) if with_stats else out
+
+
+def sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, idx: torch.Tensor,
+                     scale_div: Optional[float] = None, causal: bool = False,
+                     out: Optional[torch.Tensor] = None,
+                     error_flag: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Stage (d): gathered exact attention, [B, n, h_q, d] in q's dtype (ssa/attention.py:12-115)."""
+    for name, t in (("q", q), ("k", k), ("v", v), ("indices", idx)):
+        _check_rows(t, name)
+    _lib.require_device(q, k, v, idx)
+    if not (q.dtype == k.dtype == v.dtype):
+        raise TypeError(f"q, k, v must share a dtype ({q.dtype}, {k.dtype}, {v.dtype})")
+    B, n, h_q, d = q.shape
+    h_kv = k.shape[2]
+    top_k = idx.shape[-1]
+    if scale_div is None:
+        scale_div = math.sqrt(d)
+    if out is None:
+        out = torch.empty((B, n, h_q, d), device=q.device, dtype=q.dtype)
+    call("ssa_sparse_attention", ptr(q), ptr(k), ptr(v), _lib.elem_dtype(q), B, n, h_q, h_kv, d,
+         q.stride(0), q.stride(1), q.stride(2), k.stride(0), k.stride(1), k.stride(2),
+         v.stride(0), v.stride(1), v.stride(2), ptr(idx), _lib.index_dtype(idx), top_k,
+         idx.stride(0), idx.stride(1), idx.stride(2), float(scale_div), int(bool(causal)),
+         ptr(out), _lib.elem_dtype(out), out.stride(0), out.stride(1), out.stride(2),
+         ptr(error_flag), stream_of(q))
+    return out

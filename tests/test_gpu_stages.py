@@ -1,0 +1,208 @@
+"""Stage-by-stage parity of the HIP kernels against the CPU oracle.
+
+Selections (codes, index, candidates) must be bit-identical; attention outputs
+match within 1e-5 (fp32) / 1e-3 (bf16 inputs, fp32 output).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from tests.helpers import clustered_qk, f32, randn, router_params
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("h_in,group,d,d_s", [(8, 4, 128, 32), (6, 3, 64, 16), (2, 1, 64, 8),
+                                              (16, 8, 128, 32)])
+def test_route_vectors_bit_exact(dev, orc, dtype, h_in, group, d, d_s):
+    from ssa_amd import kernels
+
+    _say(f"route_vectors dtype={dtype} h_in={h_in} g={group} d={d} d_s={d_s}")
+    n = 300
+    x = randn((2, n, h_in, d), 1, dtype)
+    w = torch.nn.init.uniform_(torch.empty(d_s, d), -0.2, 0.2)
+    got = kernels.route_vectors(x.to(dev), w.to(dev), group).cpu().numpy()
+    for b in range(2):
+        ref = orc.route_vectors(f32(x[b]), f32(w), group)
+        np.testing.assert_array_equal(got[b], ref)
+
+
+def test_normalize_rows_bit_exact(dev, orc):
+    from ssa_amd import kernels
+
+    x = randn((4, 512, 32), 2)
+    x[0, 0] = 0.0  # eps clamp: 0 / 1e-12 = 0
+    got = kernels.normalize_rows(x.to(dev)).cpu().numpy()
+    np.testing.assert_array_equal(got, orc.normalize(f32(x)))
+
+
+@pytest.mark.parametrize("top,temperature,n_c,d_s", [(16, 1.0, 512, 32), (4, 1.0, 4096, 32),
+                                                     (8, 0.7, 130, 16), (64, 1.0, 1000, 8)])
+def test_code_topk_bit_exact(dev, orc, top, temperature, n_c, d_s):
+    from ssa_amd import kernels
+
+    _say(f"code_topk top={top} T={temperature} n_c={n_c} d_s={d_s}")
+    B, h, rows = 2, 3, 200
+    xhat = torch.from_numpy(orc.normalize(f32(randn((B, h, rows, d_s), 3))))
+    chat = torch.from_numpy(orc.normalize(f32(randn((h, n_c, d_s), 4))))
+    got = kernels.code_topk(xhat.to(dev), chat.to(dev), top, temperature).cpu().numpy()
+    for b in range(B):
+        ref = orc.code_topk(xhat[b].numpy(), chat.numpy(), top, temperature)
+        np.testing.assert_array_equal(got[b], ref)
+
+
+def test_code_topk_ties_lowest_index(dev, orc):
+    """Duplicated codebook rows tie exactly; the lower code id must come first."""
+    from ssa_amd import kernels
+
+    d_s, n_c = 16, 96
+    base = orc.normalize(f32(randn((1, 32, d_s), 5)))
+    chat = np.concatenate([base, base, base], axis=1)  # codes c, c+32, c+64 identical
+    xhat = orc.normalize(f32(randn((1, 1, 50, d_s), 6)))
+    got = kernels.code_topk(torch.from_numpy(xhat).to(dev), torch.from_numpy(chat).to(dev), 9).cpu().numpy()
+    ref = orc.code_topk(xhat[0], chat, 9)
+    np.testing.assert_array_equal(got[0], ref)
+    # every triple appears as c, c+32, c+64 in that order
+    assert (ref[0, :, 0] % 32 == ref[0, :, 1] % 32).all() and (ref[0, :, 0] < ref[0, :, 1]).all()
+
+
+@pytest.mark.parametrize("n,h_kv,b,n_c", [(700, 2, 4, 64), (5000, 3, 4, 4096), (3000, 1, 2, 7)])
+def test_build_index_bit_exact(dev, orc, n, h_kv, b, n_c):
+    from ssa_amd import kernels
+
+    _say(f"build_index n={n} h_kv={h_kv} b={b} n_c={n_c}")
+    g = torch.Generator().manual_seed(7)
+    B = 2
+    # distinct codes per key, skewed towards low code ids (heavy buckets)
+    scores = torch.rand(B, h_kv, n, n_c, generator=g) ** 4 + torch.linspace(1, 0, n_c)
+    kc = scores.topk(b, dim=-1).indices.to(torch.int32)
+    off, post = kernels.build_index(kc.to(dev), n_c)
+    off, post = off.cpu().numpy(), post.cpu().numpy()
+    for bb in range(B):
+        roff, rpost = orc.build_index(kc[bb].numpy(), n_c)
+        np.testing.assert_array_equal(off[bb], roff)
+        np.testing.assert_array_equal(post[bb], rpost)
+
+
+def _route_inputs(n, h_q, h_kv, d, d_s, n_c, seed, dtype, clustered):
+    if clustered:
+        q, k = clustered_qk(n, h_q, h_kv, d, 8, 0.3, seed, dtype)
+    else:
+        q, k = randn((n, h_q, d), seed, dtype), randn((n, h_kv, d), seed + 1, dtype)
+    w_qr, w_kr, cb = router_params(d, d_s, h_kv, n_c, seed + 2)
+    return q, k, w_qr, w_kr, cb
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("mode", ["causal", "none", "dense"])
+@pytest.mark.parametrize("clustered", [False, True])
+def test_router_pipeline_bit_exact(dev, orc, dtype, mode, clustered):
+    """Stages (a)-(c) through CodebookRouter vs the oracle, with per-row stats."""
+    from ssa_amd import CodebookRouter, build_causal_mask
+
+    _say(f"router pipeline dtype={dtype} mode={mode} clustered={clustered}")
+    n, h_q, h_kv, d, d_s, n_c, a, b, k = 777, 8, 2, 128, 32, 128, 16, 4, 64
+    q, kk, w_qr, w_kr, cb = _route_inputs(n, h_q, h_kv, d, d_s, n_c, 11, dtype, clustered)
+    r = CodebookRouter(head_dim=d, route_dim=d_s, num_kv_heads=h_kv, num_codebook=n_c,
+                       codes_per_key=b, codes_per_query=a, top_k=k)
+    with torch.no_grad():
+        r.W_qr.weight.copy_(w_qr)
+        r.W_kr.weight.copy_(w_kr)
+        r.codebook.copy_(cb)
+    r = r.to(dev)
+    if mode == "causal":
+        cm, omode, omask = build_causal_mask(n, device=dev), orc.MASK_CAUSAL, None
+    elif mode == "none":
+        cm, omode, omask = None, orc.MASK_NONE, None
+    else:
+        gm = torch.Generator().manual_seed(3)
+        m = (torch.rand(n, n, generator=gm) < 0.6) | torch.eye(n, dtype=torch.bool)
+        cm, omode, omask = m.to(dev), orc.MASK_DENSE, m.numpy().astype(np.uint8)
+    res = r.route(q.to(dev), kk.to(dev), causal_mask=cm, with_stats=True)
+    (ref, ncand, nraw), ex = orc.router_forward(f32(q), f32(kk), f32(w_qr), f32(w_kr), f32(cb),
+                                               a, b, k, omode, omask, with_stats=True)
+    np.testing.assert_array_equal(res.q_codes[0].cpu().numpy(), ex["q_codes"])
+    np.testing.assert_array_equal(res.k_codes[0].cpu().numpy(), ex["k_codes"])
+    np.testing.assert_array_equal(res.offsets[0].cpu().numpy(), ex["offsets"])
+    np.testing.assert_array_equal(res.postings[0].cpu().numpy(), ex["postings"])
+    np.testing.assert_array_equal(res.indices[0].cpu().numpy(), ref)
+    st = res.stats[0].cpu().numpy()  # [h, n, 2]
+    np.testing.assert_array_equal(st[..., 0].T, ncand)
+    np.testing.assert_array_equal(st[..., 1].T, nraw)
+
+
+@pytest.mark.parametrize("top_k", [1, 600, 1000, 4096])
+def test_select_k_edges(dev, orc, top_k):
+    """k > n pads zeros; k = n lists every index; k = 1."""
+    from ssa_amd import CodebookRouter
+
+    n = 1000 if top_k != 4096 else 2500
+    _say(f"select k edges n={n} top_k={top_k}")
+    q, kk, w_qr, w_kr, cb = _route_inputs(n, 4, 1, 64, 16, 64, 21, torch.float32, False)
+    r = CodebookRouter(head_dim=64, route_dim=16, num_kv_heads=1, num_codebook=64,
+                       codes_per_key=4, codes_per_query=8, top_k=top_k)
+    with torch.no_grad():
+        r.W_qr.weight.copy_(w_qr)
+        r.W_kr.weight.copy_(w_kr)
+        r.codebook.copy_(cb)
+    got = r.to(dev)(q.to(dev), kk.to(dev), causal_mask=True).cpu().numpy()
+    ref, _ = orc.router_forward(f32(q), f32(kk), f32(w_qr), f32(w_kr), f32(cb), 8, 4, top_k)
+    np.testing.assert_array_equal(got, ref)
+    if top_k >= n:
+        assert (np.sort(got[:, :, :n], axis=-1) == np.arange(n)).all()
+
+
+@pytest.mark.parametrize("dtype,d,g,tol", [(torch.float32, 64, 4, 1e-5), (torch.float32, 128, 3, 1e-5),
+                                           (torch.bfloat16, 128, 4, 1e-3), (torch.bfloat16, 64, 8, 1e-3),
+                                           (torch.bfloat16, 256, 16, 1e-3), (torch.float32, 256, 1, 1e-5)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_sparse_attention_vs_oracle(dev, orc, dtype, d, g, tol, causal):
+    from ssa_amd import kernels
+
+    _say(f"sparse_attention dtype={dtype} d={d} g={g} causal={causal}")
+    n, h_kv, top_k, B = 300, 2, 100, 2
+    h_q = h_kv * g
+    q = randn((B, n, h_q, d), 31, dtype)
+    k = randn((B, n, h_kv, d), 32, dtype)
+    v = randn((B, n, h_kv, d), 33, dtype)
+    gi = torch.Generator().manual_seed(34)
+    idx = torch.randint(0, n, (B, n, h_kv, top_k), generator=gi)
+    idx[..., :3] = 0  # duplicates count twice
+    out = torch.empty(B, n, h_q, d, device=dev, dtype=torch.float32)
+    kernels.sparse_attention(q.to(dev), k.to(dev), v.to(dev), idx.to(dev), None, causal, out=out)
+    got = out.cpu().numpy()
+    for b in range(B):
+        ref = orc.sparse_attention(f32(q[b]), f32(k[b]), f32(v[b]), idx[b].numpy(), causal=causal)
+        np.testing.assert_allclose(got[b], ref, rtol=tol, atol=tol)
+
+
+def test_sparse_attention_k_equals_n_is_causal_dense(dev, orc):
+    """Config 2 shape: fp32, n=2048, GQA 8/2, d=64, k=n, causal -> dense causal within 1e-5."""
+    from ssa_amd import dense_attention, sparse_exact_attention
+
+    n, h_q, h_kv, d = 2048, 8, 2, 64
+    q, k, v = randn((n, h_q, d), 41), randn((n, h_kv, d), 42), randn((n, h_kv, d), 43)
+    idx = torch.arange(n).view(1, 1, n).expand(n, h_kv, n).contiguous()
+    got = sparse_exact_attention(q.to(dev), k.to(dev), v.to(dev), idx.to(dev), causal=True).cpu().numpy()
+    ref = orc.dense_attention(f32(q), f32(k), f32(v), causal=True)
+    np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-5)
+    mask = torch.ones(n, n, dtype=torch.bool).tril()
+    td = dense_attention(q.to(dev), k.to(dev), v.to(dev), causal_mask=mask.to(dev)).cpu().numpy()
+    np.testing.assert_allclose(td, ref, rtol=1e-4, atol=1e-4)
+
+
+def test_sparse_attention_bad_index_raises(dev):
+    from ssa_amd import sparse_exact_attention
+
+    n = 64
+    q, k, v = randn((n, 4, 64), 1), randn((n, 2, 64), 2), randn((n, 2, 64), 3)
+    idx = torch.zeros(n, 2, 8, dtype=torch.int64)
+    idx[5, 1, 3] = n
+    with pytest.raises(IndexError):
+        sparse_exact_attention(q.to(dev), k.to(dev), v.to(dev), idx.to(dev))
