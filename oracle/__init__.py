@@ -199,7 +199,9 @@ def select(q, k, q_codes, offsets, postings, b: int, top_k: int, mask_mode: int 
 
 
 def sparse_attention(q, k, v, idx, scale=None, causal: bool = False, rows=None) -> np.ndarray:
-    """Stage (d) for one batch element in float64 (ssa/attention.py:12-115)."""
+    """Stage (d) for one batch element in float64 (ssa/attention.py:12-115).
+
+    idx is [n, h_kv, kk], or [len(rows), h_kv, kk] aligned with ``rows``."""
     q = _c(q, np.float32)
     k = _c(k, np.float32)
     v = _c(v, np.float32)

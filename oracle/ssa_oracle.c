@@ -302,7 +302,8 @@ HOT void oracle_select(const float* q, const float* k, int64_t n, int h_q, int h
 /* ---------------------------------------------------------------- stage (d) */
 
 /* Gathered exact attention for one batch element, in double precision.
- *   idx [n][h_kv][kk] int64; out [n_rows][h_q][d] double.
+ *   idx [n][h_kv][kk] int64, or [n_rows][h_kv][kk] aligned with `rows` when rows
+ *   is given; out [n_rows][h_q][d] double.
  * logits = q . K[idx] / scale_div (scale is a divisor, ssa/attention.py:37-38,107),
  * softmax over the kk slots (duplicates count twice, no mask: ssa/attention.py:109),
  * out = p . V[idx] (ssa/attention.py:112).  causal != 0 additionally drops slots with
@@ -322,7 +323,7 @@ void oracle_sparse_attention(const float* q, const float* k, const float* v, int
       int h = hq / g;
       int64_t i = rows ? rows[ri] : ri;
       const float* qr = q + (i * h_q + hq) * d;
-      const int64_t* ix = idx + (i * h_kv + h) * kk;
+      const int64_t* ix = idx + ((rows ? ri : i) * h_kv + h) * kk;
       double mx = -INFINITY;
       for (int m = 0; m < kk; ++m) {
         int64_t j = ix[m];
