@@ -75,10 +75,16 @@ int ssa_normalize_rows(const float* x, int64_t rows, int d_s, float* out, void* 
 /* Codebook scoring and top-`top` codes per row (score desc, code asc).
  * Replaces einsum("shd,hcd->shc") / temperature and topk of ssa/router.py:121-130
  * (keys, top = b) and :141 (queries, top = a).
- *   xhat  fp32 [batch][h][rows][d_s]; chat fp32 [h][n_c][d_s] (normalized)
- *   codes int32 [batch][h][rows][top] */
+ *   xhat  fp32 [batch][h][rows][d_s]; chat fp32 [h][n_c][d_s]
+ *   codes int32 [batch][h][rows][top]
+ * With a workspace (ssa_code_topk_workspace_bytes) and top <= 32, d_s <= 32,
+ * scores are screened on the matrix cores (bf16) with a proven error bound and
+ * the survivors rescored exactly; workspace = NULL scores every code exactly.
+ * Both give identical codes. */
+size_t ssa_code_topk_workspace_bytes(int64_t batch, int h, int64_t rows, int n_c);
 int ssa_code_topk(const float* xhat, int64_t batch, int h, int64_t rows, const float* chat,
-                  int n_c, int d_s, float temperature, int top, int32_t* codes, void* stream);
+                  int n_c, int d_s, float temperature, int top, int32_t* codes, void* workspace,
+                  size_t workspace_bytes, void* stream);
 
 /* Stage (a) end to end: q_codes = top-a query codes, k_codes = top-b key codes.
  * Replaces ssa/router.py:102-141.  The workspace holds the normalized routing

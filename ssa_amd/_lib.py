@@ -45,7 +45,9 @@ SIGNATURES = {
     "ssa_route_vectors": (
         _int, [_vp, _int, _i64, _i64, _int, _int, _int, _i64, _i64, _i64, _vp, _int, _vp, _vp]),
     "ssa_normalize_rows": (_int, [_vp, _i64, _int, _vp, _vp]),
-    "ssa_code_topk": (_int, [_vp, _i64, _int, _i64, _vp, _int, _int, _flt, _int, _vp, _vp]),
+    "ssa_code_topk_workspace_bytes": (_sz, [_i64, _int, _i64, _int]),
+    "ssa_code_topk": (
+        _int, [_vp, _i64, _int, _i64, _vp, _int, _int, _flt, _int, _vp, _vp, _sz, _vp]),
     "ssa_route_workspace_bytes": (_sz, [_i64, _i64, _int, _int, _int]),
     "ssa_route_codes": (
         _int,

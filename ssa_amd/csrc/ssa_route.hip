@@ -124,7 +124,8 @@ __host__ __device__ inline size_t code_topk_smem(int d_s, int top) {
 // by insertion after each tile.
 __global__ __launch_bounds__(kTopThreads) void code_topk_kernel(
     const float* __restrict__ xhat, int64_t rows, int h, const float* __restrict__ chat, int n_c,
-    int d_s, float temperature, int top, int32_t* __restrict__ codes) {
+    int d_s, float temperature, int top, int32_t* __restrict__ codes,
+    const uint8_t* __restrict__ only_flagged) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   constexpr int rpad = kTopRows + 4, cpad = kTopCodes + 4;
   float* Xs = reinterpret_cast<float*>(smem_raw);                // [d_s][rpad]
@@ -136,6 +137,8 @@ __global__ __launch_bounds__(kTopThreads) void code_topk_kernel(
   int* bcnt = cnt + kTopRows;                                    // [rows]
 
   const int64_t tiles = (rows + kTopRows - 1) / kTopRows;
+  // Fallback role: only the 64-row groups the MFMA filter could not settle.
+  if (only_flagged && !only_flagged[blockIdx.x]) return;
   const int64_t bh = blockIdx.x / tiles;
   const int64_t r0 = (blockIdx.x % tiles) * kTopRows;
   const int hh = static_cast<int>(bh % h);
@@ -222,6 +225,275 @@ __global__ __launch_bounds__(kTopThreads) void code_topk_kernel(
   }
 }
 
+
+// ---------------------------------------------------------------------------
+// Matrix-core filter for the top-`top` codes (top <= 32, d_s <= 32).
+//
+// Pass 1 scores 256 rows x all codes with one bf16 MFMA (16x16x32) per 16x16
+// tile (codes = A from LDS, rows = B in registers) and keeps, per lane and
+// row, the running maxima of M = 2Q disjoint code segments (Q = ceil(top/4)).
+// The Q-th largest of a lane's maxima, minimised over the 4 lanes holding the
+// row, is a lower bound L on the row's top-th largest approximate score: at
+// least 4Q >= top approximate scores are >= L.
+//
+// With unit routing vectors and codebook rows, |approx - exact| <= eps where
+// eps = 2^-7 * ||x|| * max_c ||c|| bounds the bf16 rounding of both operands
+// (2^-8), the MFMA accumulation and the exact fp32 chain (< 2^-16 together)
+// with a 2x margin.  Every code of the exact top-`top` therefore scores
+// approx >= L - 2 eps.  Pass 2 re-runs the MFMAs and collects those codes (at
+// most kMfCap per row); pass 3 rescores them in the canonical fp32 order and
+// keeps the exact top-`top` (score desc, code asc).  Rows that collect more
+// than kMfCap codes (or have non-finite inputs) flag their 64-row group, which
+// code_topk_kernel then recomputes exhaustively.
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float floatx4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kMfRows = 256;     // rows per block: 4 waves x 4 row tiles of 16
+constexpr int kMfChunk = 512;    // codes staged in LDS at a time
+constexpr int kMfCap = 64;       // candidate codes kept per row
+constexpr float kMfEps = 0.0078125f;
+
+__device__ __forceinline__ uint16_t bf16_rne(float f) {
+  uint32_t u = __float_as_uint(f);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__host__ __device__ inline int n_c_padded(int n_c) { return (n_c + 15) / 16 * 16; }
+
+__host__ __device__ inline size_t code_topk_mfma_smem(int top) {
+  const size_t chunk = static_cast<size_t>(kMfChunk) * 32 * sizeof(uint16_t);
+  const size_t lists = static_cast<size_t>(4) * top * 64 * sizeof(uint64_t);
+  return (chunk > lists ? chunk : lists) + sizeof(int) * 4 * 64 +
+         sizeof(uint16_t) * 4 * kMfCap * 64;
+}
+
+// bf16 copy of the normalized codebook, zero-padded to [h][n_c_pad][32], and the
+// largest row norm per head (NaN if any entry is not finite).
+__global__ __launch_bounds__(256) void codebook_prep_kernel(const float* __restrict__ chat, int n_c,
+                                                            int n_c_pad, int d_s,
+                                                            uint16_t* __restrict__ cbf,
+                                                            float* __restrict__ cmax) {
+  __shared__ float red[256];
+  __shared__ int bad;
+  const int hh = blockIdx.x;
+  if (threadIdx.x == 0) bad = 0;
+  __syncthreads();
+  float mx = 0.0f;
+  for (int c = threadIdx.x; c < n_c_pad; c += 256) {
+    const float* cr = chat + (static_cast<int64_t>(hh) * n_c + c) * d_s;
+    uint16_t* o = cbf + (static_cast<int64_t>(hh) * n_c_pad + c) * 32;
+    float nrm2 = 0.0f;
+#pragma unroll
+    for (int s = 0; s < 32; ++s) {
+      const float v = (c < n_c && s < d_s) ? cr[s] : 0.0f;
+      nrm2 = fma_rn(v, v, nrm2);
+      o[s] = bf16_rne(v);
+    }
+    if (!(nrm2 <= 3.0e38f)) bad = 1;
+    mx = fmaxf(mx, sqrtf(nrm2));
+  }
+  red[threadIdx.x] = mx;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if (static_cast<int>(threadIdx.x) < w) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + w]);
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) cmax[hh] = bad ? __builtin_nanf("") : red[0];
+}
+
+template <int N>
+__device__ __forceinline__ void sort_desc(float (&v)[N]) {
+#pragma unroll
+  for (int size = 2; size <= N; size <<= 1)
+#pragma unroll
+    for (int stride = size >> 1; stride > 0; stride >>= 1)
+#pragma unroll
+      for (int i = 0; i < N; ++i) {
+        const int j = i ^ stride;
+        if (j > i) {
+          const bool desc = (i & size) == 0;
+          const float a = v[i], b = v[j];
+          v[i] = desc ? fmaxf(a, b) : fminf(a, b);
+          v[j] = desc ? fminf(a, b) : fmaxf(a, b);
+        }
+      }
+}
+
+template <int Q>
+__global__ __launch_bounds__(256) void code_topk_mfma_kernel(
+    const float* __restrict__ xhat, int64_t rows, int h, const float* __restrict__ chat,
+    const uint16_t* __restrict__ cbf, const float* __restrict__ cmax, int n_c, int d_s,
+    float temperature, int top, int32_t* __restrict__ codes, uint8_t* __restrict__ flags) {
+  constexpr int M = 2 * Q;
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  const size_t chunk_bytes = static_cast<size_t>(kMfChunk) * 64;
+  const size_t list_bytes = static_cast<size_t>(4) * top * 64 * 8;
+  uint16_t* chunk = reinterpret_cast<uint16_t*>(smem_raw);             // [kMfChunk][32]
+  uint64_t* lists = reinterpret_cast<uint64_t*>(smem_raw);             // [4][top][64] (pass 3)
+  int* cnt = reinterpret_cast<int*>(smem_raw + (chunk_bytes > list_bytes ? chunk_bytes : list_bytes));
+  uint16_t* cand = reinterpret_cast<uint16_t*>(cnt + 4 * 64);          // [4][kMfCap][64]
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int q4 = lane >> 4, c16 = lane & 15;
+  const int n_c_pad = n_c_padded(n_c);
+  const int64_t tiles = (rows + kMfRows - 1) / kMfRows;
+  const int64_t bh = blockIdx.x / tiles;
+  const int64_t r0 = (blockIdx.x % tiles) * kMfRows + wave * 64;
+  const int hh = static_cast<int>(bh % h);
+  const float* xb = xhat + bh * rows * d_s;
+  const uint16_t* cbh = cbf + static_cast<int64_t>(hh) * n_c_pad * 32;
+
+  bf16x8_t bfrag[4];
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) {
+    const int64_t row = r0 + nt * 16 + c16;
+    uint16_t tmp[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int dim = q4 * 8 + e;
+      tmp[e] = bf16_rne((row < rows && dim < d_s) ? xb[row * d_s + dim] : 0.0f);
+    }
+    bfrag[nt] = __builtin_bit_cast(bf16x8_t, tmp);
+  }
+  float eps_l = 0.0f;
+  {
+    const int64_t row = r0 + lane;
+    if (row < rows) {
+      float nrm2 = 0.0f;
+      for (int s = 0; s < d_s; ++s) nrm2 = fma_rn(xb[row * d_s + s], xb[row * d_s + s], nrm2);
+      eps_l = kMfEps * sqrtf(nrm2) * cmax[hh] * 1.0001f;
+    }
+  }
+  const bool bad_l = !(eps_l <= 3.0e38f);
+  cnt[wave * 64 + lane] = 0;
+
+  float smax[4][M];
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+    for (int u = 0; u < M; ++u) smax[nt][u] = -INFINITY;
+
+  // ---- pass 1: segment maxima
+  for (int c0 = 0; c0 < n_c_pad; c0 += kMfChunk) {
+    const int nct = min(kMfChunk, n_c_pad - c0);
+    __syncthreads();
+    {
+      const uint4* src = reinterpret_cast<const uint4*>(cbh + static_cast<int64_t>(c0) * 32);
+      uint4* dst = reinterpret_cast<uint4*>(chunk);
+      for (int e = tid; e < nct * 4; e += 256) dst[e] = src[e];
+    }
+    __syncthreads();
+    const int ntile = nct / 16;
+    for (int t = 0; t < ntile; t += M) {
+#pragma unroll
+      for (int u = 0; u < M; ++u) {
+        if (t + u < ntile) {
+          const int tile = t + u;
+          const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(chunk + (tile * 16 + c16) * 32 + q4 * 8);
+          const int cbase = c0 + tile * 16 + q4 * 4;
+          const bool tail = (c0 + tile * 16 + 16 > n_c);
+#pragma unroll
+          for (int nt = 0; nt < 4; ++nt) {
+            const floatx4_t sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bfrag[nt], floatx4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            float m = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+            if (tail) {
+              m = -INFINITY;
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                if (cbase + e < n_c) m = fmaxf(m, sc[e]);
+            }
+            smax[nt][u] = fmaxf(smax[nt][u], m);
+          }
+        }
+      }
+    }
+  }
+
+  float thr[4];
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) {
+    sort_desc<M>(smax[nt]);
+    float lb = smax[nt][Q - 1];
+    lb = fminf(lb, __shfl_xor(lb, 16));
+    lb = fminf(lb, __shfl_xor(lb, 32));
+    const float er = __shfl(eps_l, nt * 16 + c16);
+    thr[nt] = lb - 2.0f * er;
+  }
+
+  // ---- pass 2: collect codes whose approximate score reaches the threshold
+  for (int c0 = 0; c0 < n_c_pad; c0 += kMfChunk) {
+    const int nct = min(kMfChunk, n_c_pad - c0);
+    __syncthreads();
+    {
+      const uint4* src = reinterpret_cast<const uint4*>(cbh + static_cast<int64_t>(c0) * 32);
+      uint4* dst = reinterpret_cast<uint4*>(chunk);
+      for (int e = tid; e < nct * 4; e += 256) dst[e] = src[e];
+    }
+    __syncthreads();
+    const int ntile = nct / 16;
+    for (int tile = 0; tile < ntile; ++tile) {
+      const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(chunk + (tile * 16 + c16) * 32 + q4 * 8);
+      const int cbase = c0 + tile * 16 + q4 * 4;
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) {
+        const floatx4_t sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bfrag[nt], floatx4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (sc[e] >= thr[nt] && cbase + e < n_c) {
+            const int r = nt * 16 + c16;
+            const int pos = atomicAdd(&cnt[wave * 64 + r], 1);
+            if (pos < kMfCap) cand[(wave * kMfCap + pos) * 64 + r] = static_cast<uint16_t>(cbase + e);
+          }
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- pass 3: exact rescoring of the collected codes (one lane per row)
+  const int64_t row = r0 + lane;
+  const int m = cnt[wave * 64 + lane];
+  const bool over = bad_l || m > kMfCap || m < top;
+  if (row < rows && !over) {
+    float xr[32];
+#pragma unroll
+    for (int s = 0; s < 32; ++s) xr[s] = (s < d_s) ? xb[row * d_s + s] : 0.0f;
+    const float* cb = chat + static_cast<int64_t>(hh) * n_c * d_s;
+    uint64_t* my = lists + static_cast<int64_t>(wave) * top * 64 + lane;  // entry p at my[p * 64]
+    const bool scale = (temperature != 1.0f);
+    int nb = 0;
+    for (int i = 0; i < m; ++i) {
+      const int c = cand[(wave * kMfCap + i) * 64 + lane];
+      const float4* cr = reinterpret_cast<const float4*>(cb + static_cast<int64_t>(c) * d_s);
+      float acc = 0.0f;
+#pragma unroll
+      for (int s4 = 0; s4 < 8; ++s4) {
+        if (s4 * 4 < d_s) {
+          const float4 cv = cr[s4];
+          acc = fma_rn(xr[s4 * 4 + 0], cv.x, acc);
+          acc = fma_rn(xr[s4 * 4 + 1], cv.y, acc);
+          acc = fma_rn(xr[s4 * 4 + 2], cv.z, acc);
+          acc = fma_rn(xr[s4 * 4 + 3], cv.w, acc);
+        }
+      }
+      if (scale) acc = acc / temperature;
+      const uint64_t key = composite_key(acc, static_cast<uint32_t>(c));
+      if (nb == top && key <= my[(top - 1) * 64]) continue;
+      int p = (nb < top) ? nb++ : top - 1;
+      while (p > 0 && my[(p - 1) * 64] < key) {
+        my[p * 64] = my[(p - 1) * 64];
+        --p;
+      }
+      my[p * 64] = key;
+    }
+    int32_t* out = codes + (bh * rows + row) * top;
+    for (int p = 0; p < top; ++p) out[p] = static_cast<int32_t>(key_index(my[p * 64]));
+  }
+  const bool any_over = __ballot(row < rows && over) != 0ull;
+  if (lane == 0 && r0 < rows) flags[bh * ((rows + 63) / 64) + r0 / 64] = any_over ? 1 : 0;
+}
+
 int next_pow2(int v) {
   int p = 1;
   while (p < v) p <<= 1;
@@ -279,15 +551,83 @@ int check_code_topk(int64_t batch, int h, int64_t rows, int n_c, int d_s, float 
   return SSA_OK;
 }
 
-int launch_code_topk(const float* xhat, int64_t batch, int h, int64_t rows, const float* chat,
-                     int n_c, int d_s, float temperature, int top, int32_t* codes, hipStream_t st) {
-  if (batch == 0 || rows == 0) return SSA_OK;
+// Workspace of the matrix-core path: bf16 codebook, per-head max norm, and a
+// fallback flag per 64-row group.
+struct TopkWorkspace {
+  uint16_t* cbf;
+  float* cmax;
+  uint8_t* flags;
+};
+
+size_t topk_workspace_bytes(int64_t batch, int h, int64_t rows, int n_c) {
+  return align_up(sizeof(uint16_t) * static_cast<size_t>(h) * n_c_padded(n_c) * 32, 256) +
+         align_up(sizeof(float) * static_cast<size_t>(h), 256) +
+         align_up(static_cast<size_t>(batch * h * ceil_div(rows, 64)), 256);
+}
+
+TopkWorkspace carve_topk(void* ws, int h, int n_c) {
+  char* p = static_cast<char*>(ws);
+  TopkWorkspace w;
+  w.cbf = reinterpret_cast<uint16_t*>(p);
+  p += align_up(sizeof(uint16_t) * static_cast<size_t>(h) * n_c_padded(n_c) * 32, 256);
+  w.cmax = reinterpret_cast<float*>(p);
+  p += align_up(sizeof(float) * static_cast<size_t>(h), 256);
+  w.flags = reinterpret_cast<uint8_t*>(p);
+  return w;
+}
+
+bool mfma_path_ok(int top, int d_s, int n_c) { return top <= 32 && d_s <= 32 && d_s % 4 == 0 && n_c <= 65535; }
+
+int launch_exact_topk(const float* xhat, int64_t batch, int h, int64_t rows, const float* chat,
+                      int n_c, int d_s, float temperature, int top, int32_t* codes,
+                      const uint8_t* only_flagged, hipStream_t st) {
   const int64_t grid = batch * h * ceil_div(rows, kTopRows);
   const size_t smem = code_topk_smem(d_s, top);
   if (int s = reserve_lds(reinterpret_cast<const void*>(code_topk_kernel), smem, "code_topk")) return s;
   code_topk_kernel<<<dim3(static_cast<unsigned>(grid)), kTopThreads, smem, st>>>(
-      xhat, rows, h, chat, n_c, d_s, temperature, top, codes);
+      xhat, rows, h, chat, n_c, d_s, temperature, top, codes, only_flagged);
   return check_launch("code_topk_kernel");
+}
+
+int launch_codebook_prep(const float* chat, int h, int n_c, int d_s, const TopkWorkspace& w,
+                         hipStream_t st) {
+  codebook_prep_kernel<<<dim3(static_cast<unsigned>(h)), 256, 0, st>>>(chat, n_c, n_c_padded(n_c),
+                                                                        d_s, w.cbf, w.cmax);
+  return check_launch("codebook_prep_kernel");
+}
+
+template <int Q>
+int launch_mfma_q(const float* xhat, int64_t batch, int h, int64_t rows, const float* chat, int n_c,
+                  int d_s, float temperature, int top, int32_t* codes, const TopkWorkspace& w,
+                  hipStream_t st) {
+  auto kern = code_topk_mfma_kernel<Q>;
+  const size_t smem = code_topk_mfma_smem(top);
+  if (int s = reserve_lds(reinterpret_cast<const void*>(kern), smem, "code_topk_mfma")) return s;
+  const int64_t grid = batch * h * ceil_div(rows, kMfRows);
+  kern<<<dim3(static_cast<unsigned>(grid)), 256, smem, st>>>(xhat, rows, h, chat, w.cbf, w.cmax,
+                                                             n_c, d_s, temperature, top, codes,
+                                                             w.flags);
+  return check_launch("code_topk_mfma_kernel");
+}
+
+// Top codes per row.  With a workspace (and top <= 32, d_s <= 32) the matrix-core
+// filter runs and the exact kernel recomputes only flagged groups; otherwise the
+// exact kernel handles every row.  `prepped` = the bf16 codebook is already in w.
+int launch_code_topk(const float* xhat, int64_t batch, int h, int64_t rows, const float* chat,
+                     int n_c, int d_s, float temperature, int top, int32_t* codes, void* ws,
+                     bool prepped, hipStream_t st) {
+  if (batch == 0 || rows == 0) return SSA_OK;
+  if (!ws || !mfma_path_ok(top, d_s, n_c))
+    return launch_exact_topk(xhat, batch, h, rows, chat, n_c, d_s, temperature, top, codes, nullptr, st);
+  const TopkWorkspace w = carve_topk(ws, h, n_c);
+  int s;
+  if (!prepped && (s = launch_codebook_prep(chat, h, n_c, d_s, w, st))) return s;
+  if (top <= 4) s = launch_mfma_q<1>(xhat, batch, h, rows, chat, n_c, d_s, temperature, top, codes, w, st);
+  else if (top <= 8) s = launch_mfma_q<2>(xhat, batch, h, rows, chat, n_c, d_s, temperature, top, codes, w, st);
+  else if (top <= 16) s = launch_mfma_q<4>(xhat, batch, h, rows, chat, n_c, d_s, temperature, top, codes, w, st);
+  else s = launch_mfma_q<8>(xhat, batch, h, rows, chat, n_c, d_s, temperature, top, codes, w, st);
+  if (s) return s;
+  return launch_exact_topk(xhat, batch, h, rows, chat, n_c, d_s, temperature, top, codes, w.flags, st);
 }
 
 int launch_normalize(const float* x, int64_t rows, int d_s, float* out, hipStream_t st) {
@@ -320,15 +660,24 @@ extern "C" int ssa_normalize_rows(const float* x, int64_t rows, int d_s, float* 
   return launch_normalize(x, rows, d_s, out, as_stream(stream));
 }
 
+extern "C" size_t ssa_code_topk_workspace_bytes(int64_t batch, int h, int64_t rows, int n_c) {
+  if (batch < 0 || h <= 0 || rows < 0 || n_c <= 0) return 0;
+  return topk_workspace_bytes(batch, h, rows, n_c);
+}
+
 extern "C" int ssa_code_topk(const float* xhat, int64_t batch, int h, int64_t rows,
                              const float* chat, int n_c, int d_s, float temperature, int top,
-                             int32_t* codes, void* stream) {
+                             int32_t* codes, void* workspace, size_t workspace_bytes,
+                             void* stream) {
   int st = check_code_topk(batch, h, rows, n_c, d_s, temperature, top);
   if (st) return st;
   if (batch * rows > 0 && (!xhat || !chat || !codes))
     return fail(SSA_ERR_INVALID_ARGUMENT, "code_topk: null pointer");
+  if (workspace && workspace_bytes < topk_workspace_bytes(batch, h, rows, n_c))
+    return fail(SSA_ERR_WORKSPACE, "code_topk: workspace %zu < %zu bytes", workspace_bytes,
+                topk_workspace_bytes(batch, h, rows, n_c));
   return launch_code_topk(xhat, batch, h, rows, chat, n_c, d_s, temperature, top, codes,
-                          as_stream(stream));
+                          workspace, false, as_stream(stream));
 }
 
 extern "C" size_t ssa_route_workspace_bytes(int64_t batch, int64_t n, int h_kv, int n_c,
@@ -336,7 +685,7 @@ extern "C" size_t ssa_route_workspace_bytes(int64_t batch, int64_t n, int h_kv, 
   if (batch < 0 || n < 0 || h_kv <= 0 || n_c <= 0 || d_s <= 0) return 0;
   const size_t vec = align_up(sizeof(float) * static_cast<size_t>(batch * h_kv * n * d_s), 256);
   const size_t cb = align_up(sizeof(float) * static_cast<size_t>(h_kv) * n_c * d_s, 256);
-  return 2 * vec + cb;
+  return 2 * vec + cb + topk_workspace_bytes(batch, h_kv, n, n_c);
 }
 
 extern "C" int ssa_route_codes(const void* q, const void* k, int dtype, int64_t batch, int64_t n,
@@ -364,12 +713,16 @@ extern "C" int ssa_route_codes(const void* q, const void* k, int dtype, int64_t 
   float* qhat = static_cast<float*>(workspace);
   float* khat = reinterpret_cast<float*>(static_cast<char*>(workspace) + vec);
   float* chat = reinterpret_cast<float*>(static_cast<char*>(workspace) + 2 * vec);
+  void* tws = static_cast<char*>(workspace) + 2 * vec +
+              align_up(sizeof(float) * static_cast<size_t>(h_kv) * n_c * d_s, 256);
   if ((st = launch_route_vectors(q, dtype, batch, n, h_q, g, d, q_sb, q_sn, q_sh, w_qr, d_s, qhat, s)))
     return st;
   if ((st = launch_route_vectors(k, dtype, batch, n, h_kv, 1, d, k_sb, k_sn, k_sh, w_kr, d_s, khat, s)))
     return st;
   if ((st = launch_normalize(codebook, static_cast<int64_t>(h_kv) * n_c, d_s, chat, s))) return st;
-  if ((st = launch_code_topk(qhat, batch, h_kv, n, chat, n_c, d_s, temperature, a, q_codes, s)))
+  if ((st = launch_code_topk(qhat, batch, h_kv, n, chat, n_c, d_s, temperature, a, q_codes, tws,
+                             false, s)))
     return st;
-  return launch_code_topk(khat, batch, h_kv, n, chat, n_c, d_s, temperature, b, k_codes, s);
+  return launch_code_topk(khat, batch, h_kv, n, chat, n_c, d_s, temperature, b, k_codes, tws,
+                          true, s);
 }

@@ -53,16 +53,23 @@ def normalize_rows(x: torch.Tensor) -> torch.Tensor:
 
 
 def code_topk(xhat: torch.Tensor, chat: torch.Tensor, top: int,
-              temperature: float = 1.0) -> torch.Tensor:
-    """Top-`top` codes per row, int32 [B, h, rows, top] (ssa/router.py:121-130,141)."""
+              temperature: float = 1.0, exhaustive: bool = False) -> torch.Tensor:
+    """Top-`top` codes per row, int32 [B, h, rows, top] (ssa/router.py:121-130,141).
+
+    ``exhaustive=True`` skips the matrix-core screen and scores every code in
+    fp32 (same result; used to cross-check the screen)."""
     _lib.require_device(xhat, chat)
     xhat = xhat.contiguous()
     chat = chat.contiguous()
     B, h, rows, d_s = xhat.shape
     n_c = chat.shape[1]
     codes = torch.empty((B, h, rows, top), device=xhat.device, dtype=torch.int32)
+    ws, ws_bytes = None, 0
+    if not exhaustive:
+        ws_bytes = int(_lib.load().ssa_code_topk_workspace_bytes(B, h, rows, n_c))
+        ws = torch.empty(max(ws_bytes, 1), device=xhat.device, dtype=torch.uint8)
     call("ssa_code_topk", ptr(xhat), B, h, rows, ptr(chat), n_c, d_s, float(temperature), top,
-         ptr(codes), stream_of(xhat))
+         ptr(codes), ptr(ws), ws_bytes, stream_of(xhat))
     return codes
 
 

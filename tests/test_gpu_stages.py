@@ -206,3 +206,38 @@ def test_sparse_attention_bad_index_raises(dev):
     idx[5, 1, 3] = n
     with pytest.raises(IndexError):
         sparse_exact_attention(q.to(dev), k.to(dev), v.to(dev), idx.to(dev))
+
+
+@pytest.mark.parametrize("top,n_c,d_s", [(4, 4096, 32), (16, 4096, 32), (32, 1000, 32),
+                                         (16, 777, 16), (8, 64, 8), (3, 4099, 32)])
+def test_code_topk_screen_equals_exhaustive_and_oracle(dev, orc, top, n_c, d_s):
+    """The matrix-core screen + exact rescoring returns the same codes as exhaustive
+    fp32 scoring and as the oracle, including ragged N_c."""
+    from ssa_amd import kernels
+
+    _say(f"code_topk screen top={top} n_c={n_c} d_s={d_s}")
+    B, h, rows = 1, 2, 3000
+    xhat = torch.from_numpy(orc.normalize(f32(randn((B, h, rows, d_s), 12))))
+    chat = torch.from_numpy(orc.normalize(f32(randn((h, n_c, d_s), 13))))
+    got = kernels.code_topk(xhat.to(dev), chat.to(dev), top).cpu().numpy()
+    exh = kernels.code_topk(xhat.to(dev), chat.to(dev), top, exhaustive=True).cpu().numpy()
+    np.testing.assert_array_equal(got, exh)
+    np.testing.assert_array_equal(got[0], orc.code_topk(xhat[0].numpy(), chat.numpy(), top))
+
+
+def test_code_topk_screen_overflow_falls_back(dev, orc):
+    """300 identical codebook rows tie exactly for every query: the screen keeps more
+    than its capacity, flags the rows and the exact kernel settles them."""
+    from ssa_amd import kernels
+
+    d_s, n_c, top = 32, 1024, 16
+    chat = orc.normalize(f32(randn((1, n_c, d_s), 14)))
+    chat[0, 100:400] = chat[0, 100]
+    xhat = orc.normalize(f32(randn((1, 1, 500, d_s), 15)))
+    xhat[0, 0, :250] = chat[0, 100]          # rows pointing at the tied block
+    xhat[0, 0, 250] = 0.0                    # a zero routing vector: every score ties at 0
+    got = kernels.code_topk(torch.from_numpy(xhat).to(dev), torch.from_numpy(chat).to(dev), top)
+    ref = orc.code_topk(xhat[0], chat, top)
+    np.testing.assert_array_equal(got.cpu().numpy()[0], ref)
+    assert (ref[0, 0] == np.arange(100, 116)).all()
+    assert (ref[0, 250] == np.arange(16)).all()
