@@ -231,16 +231,18 @@ __global__ __launch_bounds__(kTopThreads) void code_topk_kernel(
 //
 // Pass 1 scores 256 rows x all codes with one bf16 MFMA (16x16x32) per 16x16
 // tile (codes = A from LDS, rows = B in registers) and keeps, per lane and
-// row, the running maxima of M = 2Q disjoint code segments (Q = ceil(top/4)).
-// The Q-th largest of a lane's maxima, minimised over the 4 lanes holding the
-// row, is a lower bound L on the row's top-th largest approximate score: at
-// least 4Q >= top approximate scores are >= L.
+// row, the running maxima of M disjoint code segments; the 4 lanes holding a
+// row cover 4M >= top disjoint segments.  Each maximum is an actual
+// approximate score, so L = the top-th largest of those 4M maxima is a lower
+// bound on the row's top-th largest approximate score.
 //
-// With unit routing vectors and codebook rows, |approx - exact| <= eps where
-// eps = 2^-7 * ||x|| * max_c ||c|| bounds the bf16 rounding of both operands
-// (2^-8), the MFMA accumulation and the exact fp32 chain (< 2^-16 together)
-// with a 2x margin.  Every code of the exact top-`top` therefore scores
-// approx >= L - 2 eps.  Pass 2 re-runs the MFMAs and collects those codes (at
+// Error bound.  x~, c~ are the bf16 roundings (relative error <= 2^-9 each) and
+// the MFMA sums their exact products in fp32, so
+//   |approx - sum x c| <= sum|x c| (2^-8 + 2^-18) + 32 * 2^-23 sum|x~ c~|
+//   |exact  - sum x c| <= 32 * 2^-24 sum|x c|        (the canonical fmaf chain)
+// and with sum|x c| <= ||x|| ||c||:  |approx - exact| <= eps =
+// 1.02 * 2^-8 * ||x|| * max_c ||c||.  Every code of the exact top-`top` therefore
+// scores approx >= L - 2 eps.  Pass 2 re-runs the MFMAs and collects those codes (at
 // most kMfCap per row); pass 3 rescores them in the canonical fp32 order and
 // keeps the exact top-`top` (score desc, code asc).  Rows that collect more
 // than kMfCap codes (or have non-finite inputs) flag their 64-row group, which
@@ -251,7 +253,7 @@ typedef float floatx4_t __attribute__((ext_vector_type(4)));
 constexpr int kMfRows = 256;     // rows per block: 4 waves x 4 row tiles of 16
 constexpr int kMfChunk = 512;    // codes staged in LDS at a time
 constexpr int kMfCap = 64;       // candidate codes kept per row
-constexpr float kMfEps = 0.0078125f;
+constexpr float kMfEps = 0.0039844f;  // 1.02 * 2^-8
 
 __device__ __forceinline__ uint16_t bf16_rne(float f) {
   uint32_t u = __float_as_uint(f);
@@ -268,38 +270,47 @@ __host__ __device__ inline size_t code_topk_mfma_smem(int top) {
          sizeof(uint16_t) * 4 * kMfCap * 64;
 }
 
-// bf16 copy of the normalized codebook, zero-padded to [h][n_c_pad][32], and the
-// largest row norm per head (NaN if any entry is not finite).
+// bf16 copy of the codebook, zero-padded to [h][n_c_pad][32], and the largest
+// row norm per head accumulated by atomicMax on the (non-negative) float bits
+// into cmax_bits[h], which the caller zeroes first.  A non-finite entry stores
+// +inf bits, which makes the bound non-finite and sends every row of that head
+// to the exhaustive kernel.
 __global__ __launch_bounds__(256) void codebook_prep_kernel(const float* __restrict__ chat, int n_c,
                                                             int n_c_pad, int d_s,
                                                             uint16_t* __restrict__ cbf,
-                                                            float* __restrict__ cmax) {
+                                                            uint32_t* __restrict__ cmax_bits) {
   __shared__ float red[256];
-  __shared__ int bad;
-  const int hh = blockIdx.x;
-  if (threadIdx.x == 0) bad = 0;
-  __syncthreads();
-  float mx = 0.0f;
-  for (int c = threadIdx.x; c < n_c_pad; c += 256) {
+  const int hh = blockIdx.y;
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  float nrm = 0.0f;
+  if (c < n_c_pad) {
     const float* cr = chat + (static_cast<int64_t>(hh) * n_c + c) * d_s;
     uint16_t* o = cbf + (static_cast<int64_t>(hh) * n_c_pad + c) * 32;
     float nrm2 = 0.0f;
+    uint16_t tmp[32];
 #pragma unroll
     for (int s = 0; s < 32; ++s) {
       const float v = (c < n_c && s < d_s) ? cr[s] : 0.0f;
       nrm2 = fma_rn(v, v, nrm2);
-      o[s] = bf16_rne(v);
+      tmp[s] = bf16_rne(v);
     }
-    if (!(nrm2 <= 3.0e38f)) bad = 1;
-    mx = fmaxf(mx, sqrtf(nrm2));
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4)
+      reinterpret_cast<uint4*>(o)[s4] = __builtin_bit_cast(uint4, *reinterpret_cast<const uint16_t(*)[8]>(tmp + 8 * s4));
+    nrm = (nrm2 <= 3.0e38f) ? sqrtf(nrm2) : INFINITY;
   }
-  red[threadIdx.x] = mx;
+  red[threadIdx.x] = nrm;
   __syncthreads();
   for (int w = 128; w > 0; w >>= 1) {
     if (static_cast<int>(threadIdx.x) < w) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + w]);
     __syncthreads();
   }
-  if (threadIdx.x == 0) cmax[hh] = bad ? __builtin_nanf("") : red[0];
+  if (threadIdx.x == 0) atomicMax(&cmax_bits[hh], __float_as_uint(red[0]));
+}
+
+__global__ void zero_u32_kernel(uint32_t* __restrict__ p, int count) {
+  const int e = blockIdx.x * blockDim.x + threadIdx.x;
+  if (e < count) p[e] = 0u;
 }
 
 template <int N>
@@ -323,9 +334,9 @@ __device__ __forceinline__ void sort_desc(float (&v)[N]) {
 template <int Q>
 __global__ __launch_bounds__(256) void code_topk_mfma_kernel(
     const float* __restrict__ xhat, int64_t rows, int h, const float* __restrict__ chat,
-    const uint16_t* __restrict__ cbf, const float* __restrict__ cmax, int n_c, int d_s,
+    const uint16_t* __restrict__ cbf, const uint32_t* __restrict__ cmax_bits, int n_c, int d_s,
     float temperature, int top, int32_t* __restrict__ codes, uint8_t* __restrict__ flags) {
-  constexpr int M = 2 * Q;
+  constexpr int M = (2 * Q < 8) ? 2 * Q : 8;  // segment maxima per lane and row
   extern __shared__ __align__(16) unsigned char smem_raw[];
   const size_t chunk_bytes = static_cast<size_t>(kMfChunk) * 64;
   const size_t list_bytes = static_cast<size_t>(4) * top * 64 * 8;
@@ -362,7 +373,7 @@ __global__ __launch_bounds__(256) void code_topk_mfma_kernel(
     if (row < rows) {
       float nrm2 = 0.0f;
       for (int s = 0; s < d_s; ++s) nrm2 = fma_rn(xb[row * d_s + s], xb[row * d_s + s], nrm2);
-      eps_l = kMfEps * sqrtf(nrm2) * cmax[hh] * 1.0001f;
+      eps_l = kMfEps * sqrtf(nrm2) * __uint_as_float(cmax_bits[hh]) * 1.0001f;
     }
   }
   const bool bad_l = !(eps_l <= 3.0e38f);
@@ -410,16 +421,30 @@ __global__ __launch_bounds__(256) void code_topk_mfma_kernel(
     }
   }
 
+  // L per row = top-th largest of the 4M segment maxima of its 4 lanes: the
+  // maxima go through LDS (the candidate area, unused until pass 2) so that
+  // lane r of the wave can sort row r's 4M values.
+  float* segs = reinterpret_cast<float*>(cand) + static_cast<size_t>(wave) * 4 * M * 64;  // [4M][64]
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+    for (int u = 0; u < M; ++u) segs[(q4 * M + u) * 64 + nt * 16 + c16] = smax[nt][u];
+  __syncthreads();
+  float thr_l;
+  {
+    float v[4 * M];
+#pragma unroll
+    for (int i = 0; i < 4 * M; ++i) v[i] = segs[i * 64 + lane];
+    sort_desc<4 * M>(v);
+    float lb = v[0];
+#pragma unroll
+    for (int i = 1; i < 4 * M; ++i)
+      if (i == top - 1) lb = v[i];
+    thr_l = lb - 2.0f * eps_l;
+  }
   float thr[4];
 #pragma unroll
-  for (int nt = 0; nt < 4; ++nt) {
-    sort_desc<M>(smax[nt]);
-    float lb = smax[nt][Q - 1];
-    lb = fminf(lb, __shfl_xor(lb, 16));
-    lb = fminf(lb, __shfl_xor(lb, 32));
-    const float er = __shfl(eps_l, nt * 16 + c16);
-    thr[nt] = lb - 2.0f * er;
-  }
+  for (int nt = 0; nt < 4; ++nt) thr[nt] = __shfl(thr_l, nt * 16 + c16);
 
   // ---- pass 2: collect codes whose approximate score reaches the threshold
   for (int c0 = 0; c0 < n_c_pad; c0 += kMfChunk) {
@@ -555,7 +580,7 @@ int check_code_topk(int64_t batch, int h, int64_t rows, int n_c, int d_s, float 
 // fallback flag per 64-row group.
 struct TopkWorkspace {
   uint16_t* cbf;
-  float* cmax;
+  uint32_t* cmax_bits;
   uint8_t* flags;
 };
 
@@ -570,7 +595,7 @@ TopkWorkspace carve_topk(void* ws, int h, int n_c) {
   TopkWorkspace w;
   w.cbf = reinterpret_cast<uint16_t*>(p);
   p += align_up(sizeof(uint16_t) * static_cast<size_t>(h) * n_c_padded(n_c) * 32, 256);
-  w.cmax = reinterpret_cast<float*>(p);
+  w.cmax_bits = reinterpret_cast<uint32_t*>(p);
   p += align_up(sizeof(float) * static_cast<size_t>(h), 256);
   w.flags = reinterpret_cast<uint8_t*>(p);
   return w;
@@ -591,8 +616,10 @@ int launch_exact_topk(const float* xhat, int64_t batch, int h, int64_t rows, con
 
 int launch_codebook_prep(const float* chat, int h, int n_c, int d_s, const TopkWorkspace& w,
                          hipStream_t st) {
-  codebook_prep_kernel<<<dim3(static_cast<unsigned>(h)), 256, 0, st>>>(chat, n_c, n_c_padded(n_c),
-                                                                        d_s, w.cbf, w.cmax);
+  zero_u32_kernel<<<dim3(static_cast<unsigned>(ceil_div(h, 256))), 256, 0, st>>>(w.cmax_bits, h);
+  if (int s = check_launch("zero_u32_kernel")) return s;
+  codebook_prep_kernel<<<dim3(static_cast<unsigned>(ceil_div(n_c_padded(n_c), 256)), static_cast<unsigned>(h)),
+                         256, 0, st>>>(chat, n_c, n_c_padded(n_c), d_s, w.cbf, w.cmax_bits);
   return check_launch("codebook_prep_kernel");
 }
 
@@ -604,7 +631,7 @@ int launch_mfma_q(const float* xhat, int64_t batch, int h, int64_t rows, const f
   const size_t smem = code_topk_mfma_smem(top);
   if (int s = reserve_lds(reinterpret_cast<const void*>(kern), smem, "code_topk_mfma")) return s;
   const int64_t grid = batch * h * ceil_div(rows, kMfRows);
-  kern<<<dim3(static_cast<unsigned>(grid)), 256, smem, st>>>(xhat, rows, h, chat, w.cbf, w.cmax,
+  kern<<<dim3(static_cast<unsigned>(grid)), 256, smem, st>>>(xhat, rows, h, chat, w.cbf, w.cmax_bits,
                                                              n_c, d_s, temperature, top, codes,
                                                              w.flags);
   return check_launch("code_topk_mfma_kernel");
