@@ -119,7 +119,9 @@ def run_step(q, k, v, router, events=None):
     off, post = kernels.build_index(kc, router.num_codebook)
     if events:
         events[2].record()
-    idx = kernels.select(q, k, qc, off, post, router.codes_per_key, router.top_k)
+    # Same call as SSAAttention: stage (d) does not depend on the order of the
+    # selected keys, so the router lists them by index (same set as sorted).
+    idx = kernels.select(q, k, qc, off, post, router.codes_per_key, router.top_k, sorted=False)
     if events:
         events[3].record()
     out = kernels.sparse_attention(q, k, v, idx, None, True)
@@ -148,6 +150,27 @@ def time_gpu(cfg, q, k, v, router, steps, warmup):
     return wall, {key: sum(v_) / len(v_) for key, v_ in stage.items()}
 
 
+def time_sorted_select(q, k, router, reps=5):
+    """Stage (c) in reference order (keys by score, as torch.topk returns them)."""
+    import torch
+
+    from ssa_amd import kernels
+
+    qc, kc = kernels.route_codes(q, k, router.W_qr.weight, router.W_kr.weight, router.codebook,
+                                 router.codes_per_query, router.codes_per_key, router.temperature)
+    off, post = kernels.build_index(kc, router.num_codebook)
+    kernels.select(q, k, qc, off, post, router.codes_per_key, router.top_k, sorted=True)
+    ts = []
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        kernels.select(q, k, qc, off, post, router.codes_per_key, router.top_k, sorted=True)
+        e1.record()
+        torch.cuda.synchronize()
+        ts.append(e0.elapsed_time(e1))
+    return sorted(ts)[len(ts) // 2]
+
+
 def stats_sums(q, k, router):
     import torch
 
@@ -157,7 +180,7 @@ def stats_sums(q, k, router):
                                  router.codes_per_query, router.codes_per_key, router.temperature)
     off, post = kernels.build_index(kc, router.num_codebook)
     idx, st = kernels.select(q, k, qc, off, post, router.codes_per_key, router.top_k,
-                             with_stats=True)
+                             with_stats=True, sorted=False)
     st = st.to(torch.int64)
     C = int(st[..., 0].sum())
     R = int(st[..., 1].sum())
@@ -206,7 +229,7 @@ def cpu_baseline(cfg, q, k, v, router, inter, budget_s):
         rows = np.linspace(0, n - 1, sc).astype(np.int64)
         t0 = time.perf_counter()
         sel = oracle.select(qf, kf, qc, roff, rpost, cfg["b"], cfg["k"], oracle.MASK_CAUSAL,
-                            rows=rows)
+                            rows=rows, sorted=False)
         t_c1 = time.perf_counter() - t0
         t0 = time.perf_counter()
         oracle.sparse_attention(qf, kf, vf, sel, causal=True, rows=rows)
@@ -291,6 +314,8 @@ def main():
               "frac_hbm": alg["b_bytes"] / (st["b"] / 1000) / 1e9 / HBM_PEAK_GBS},
         "c": {"ms": st["c"], "gb": alg["c_bytes"] / 1e9,
               "frac_hbm": alg["c_bytes"] / (st["c"] / 1000) / 1e9 / HBM_PEAK_GBS,
+              "order": "index (same set as by score)",
+              "ms_sorted_by_score": time_sorted_select(q, k, router),
               "postings_read": R, "candidates": C, "rows": nrows, "rows_with_k_candidates": full_rows},
         "d": {"ms": st["d"], "gb": alg["d_bytes"] / 1e9, "frac_hbm": d_gbs / HBM_PEAK_GBS},
     }

@@ -117,16 +117,20 @@ int ssa_build_index(const int32_t* k_codes, int64_t batch, int64_t n, int h_kv, 
  * (score desc, index asc); fewer than k candidates are followed by the lowest
  * non-candidate indices; k > n pads with 0.  Replaces
  * CodebookRouter._select_candidates (ssa/router.py:151-214).
+ *   sorted != 0: selected keys by (score desc, index asc), as torch.topk orders
+ *                them; sorted == 0: the same set, selected keys ascending (rows
+ *                with at most k candidates then need no rescoring).  The filler
+ *                and padding are the same in both orders.
  *   out    [batch][n][h_kv][top_k], index type out_index_dtype
  *   mask   (SSA_MASK_DENSE only) uint8 [batch][n][n], strides (mask_sb, mask_si); mask_sb may be 0
  *   stats  (nullable) int32 [batch][h_kv][n][2] = (candidates, postings read)
- * Limits: top_k <= 4096, g = h_q/h_kv <= 16, d <= 256, n < 2^31. */
+ * Limits: top_k <= 4096, g = h_q/h_kv <= 16, d <= 256 (d % 8 == 0), n < 2^31. */
 int ssa_select(const void* q, const void* k, int dtype, int64_t batch, int64_t n, int h_q,
                int h_kv, int d, int64_t q_sb, int64_t q_sn, int64_t q_sh, int64_t k_sb,
                int64_t k_sn, int64_t k_sh, const int32_t* q_codes, int a, const int32_t* offsets,
                const int32_t* postings, int n_c, int b, int top_k, int mask_mode,
-               const uint8_t* mask, int64_t mask_sb, int64_t mask_si, float score_div, void* out,
-               int out_index_dtype, int32_t* stats, void* stream);
+               const uint8_t* mask, int64_t mask_sb, int64_t mask_si, float score_div, int sorted,
+               void* out, int out_index_dtype, int32_t* stats, void* stream);
 
 /* ---- stage (d): gathered exact attention -------------------------------- */
 

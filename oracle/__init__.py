@@ -68,7 +68,7 @@ def lib():
     L.oracle_build_index.argtypes = [_i32p, _int, _i64, _int, _int, _i32p, _i32p]
     L.oracle_select.argtypes = [
         _f32p, _f32p, _i64, _int, _int, _int, _i32p, _int, _i32p, _i32p, _int, _int, _int, _int,
-        _vp, _flt, _vp, _i64, _i64p, _vp, _vp,
+        _vp, _flt, _int, _vp, _i64, _i64p, _vp, _vp,
     ]
     L.oracle_sparse_attention.argtypes = [
         _f32p, _f32p, _f32p, _i64, _int, _int, _int, _i64p, _int, _dbl, _int, _vp, _i64, _f64p,
@@ -160,7 +160,8 @@ MASK_NONE, MASK_CAUSAL, MASK_DENSE = 0, 1, 2
 
 
 def select(q, k, q_codes, offsets, postings, b: int, top_k: int, mask_mode: int = MASK_CAUSAL,
-           mask=None, score_div: Optional[float] = None, rows=None, with_stats: bool = False):
+           mask=None, score_div: Optional[float] = None, rows=None, with_stats: bool = False,
+           sorted: bool = True):
     """Stage (c) for one batch element (ssa/router.py:151-259).
 
     q [n, h_q, d], k [n, h_kv, d] float32; q_codes [h_kv, n, a]; returns int64
@@ -191,7 +192,7 @@ def select(q, k, q_codes, offsets, postings, b: int, top_k: int, mask_mode: int 
     n_raw = np.empty((nr, h_kv), np.int32)
     lib().oracle_select(
         q, k, n, h_q, h_kv, d, qc, a, off, post, n_c, b, top_k, mask_mode,
-        mk.ctypes.data if mk is not None else None, float(score_div),
+        mk.ctypes.data if mk is not None else None, float(score_div), int(bool(sorted)),
         rows_a.ctypes.data if rows is not None else None, nr, out,
         n_cand.ctypes.data, n_raw.ctypes.data,
     )
@@ -238,7 +239,7 @@ def dense_attention(q, k, v, causal: bool = False, scale=None) -> np.ndarray:
 
 def router_forward(q, k, w_qr, w_kr, codebook, a: int, b: int, top_k: int,
                    mask_mode: int = MASK_CAUSAL, mask=None, temperature: float = 1.0,
-                   rows=None, with_stats: bool = False):
+                   rows=None, with_stats: bool = False, sorted: bool = True):
     """Whole CodebookRouter.forward for one batch element (ssa/router.py:73-149)."""
     q = _c(q, np.float32)
     k = _c(k, np.float32)
@@ -252,7 +253,7 @@ def router_forward(q, k, w_qr, w_kr, codebook, a: int, b: int, top_k: int,
     k_codes = code_topk(khat, chat, b, temperature)
     offsets, postings = build_index(k_codes, chat.shape[1])
     res = select(q, k, q_codes, offsets, postings, b, top_k, mask_mode, mask,
-                 rows=rows, with_stats=with_stats)
+                 rows=rows, with_stats=with_stats, sorted=sorted)
     extras = dict(qhat=qhat, khat=khat, chat=chat, q_codes=q_codes, k_codes=k_codes,
                   offsets=offsets, postings=postings)
     return res, extras

@@ -234,14 +234,21 @@ HOT static float rescore(const float* qrow /*[g][d]*/, const float* krow /*[d]*/
  *   out [n_rows][h_kv][top_k] int64
  *   n_cand (nullable) [n_rows][h_kv]: |candidate set|; n_raw (nullable): postings read
  *     (for causal: postings with j <= i)
+ *   sorted != 0 lists the selected keys by (score desc, index asc); 0 lists the
+ *     same set ascending (torch.topk(sorted=False)-style), before the filler
  * Candidate set (ssa/router.py:224-235): keys sharing >= 1 code with the query and
  * allowed by the mask.  Ranking by canonical rescoring; filler and pad as the
  * file header states. */
+static int cmp_asc_i64(const void* a, const void* b) {
+  int64_t x = *(const int64_t*)a, y = *(const int64_t*)b;
+  return (x > y) - (x < y);
+}
+
 HOT void oracle_select(const float* q, const float* k, int64_t n, int h_q, int h_kv, int d,
                        const int32_t* q_codes, int a, const int32_t* offsets,
                        const int32_t* postings, int n_c, int b, int top_k, int mask_mode,
-                       const uint8_t* mask, float score_div, const int64_t* rows, int64_t n_rows,
-                       int64_t* out, int32_t* n_cand, int32_t* n_raw) {
+                       const uint8_t* mask, float score_div, int sorted, const int64_t* rows,
+                       int64_t n_rows, int64_t* out, int32_t* n_cand, int32_t* n_raw) {
   int g = h_q / h_kv;
   int64_t k_eff = top_k < n ? top_k : n;
   int64_t nrow = rows ? n_rows : n;
@@ -285,6 +292,7 @@ HOT void oracle_select(const float* q, const float* k, int64_t n, int h_q, int h
       int64_t* o = out + rr * top_k;
       int64_t w = 0;
       for (; w < C && w < k_eff; ++w) o[w] = (int64_t)(0xFFFFFFFFu - (uint32_t)(keys[w] & 0xFFFFFFFFu));
+      if (!sorted) qsort(o, (size_t)w, sizeof(int64_t), cmp_asc_i64);
       for (int64_t j = 0; w < k_eff && j < n; ++j)
         if (!(bitmap[j >> 5] & (1u << (j & 31)))) o[w++] = j;
       for (; w < top_k; ++w) o[w] = 0;

@@ -15,7 +15,8 @@ from typing import Optional
 import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libssa_hip.so")
+# In-tree build; SSA_HIP_LIBRARY may point at another build of the same ABI.
+LIB_PATH = os.environ.get("SSA_HIP_LIBRARY") or os.path.join(_HERE, "libssa_hip.so")
 
 SSA_OK = 0
 SSA_ERR_INVALID_ARGUMENT = 1
@@ -58,8 +59,8 @@ SIGNATURES = {
     "ssa_select": (
         _int,
         [_vp, _vp, _int, _i64, _i64, _int, _int, _int, _i64, _i64, _i64, _i64, _i64, _i64,
-         _vp, _int, _vp, _vp, _int, _int, _int, _int, _vp, _i64, _i64, _flt, _vp, _int, _vp,
-         _vp]),
+         _vp, _int, _vp, _vp, _int, _int, _int, _int, _vp, _i64, _i64, _flt, _int, _vp, _int,
+         _vp, _vp]),
     "ssa_sparse_attention": (
         _int,
         [_vp, _vp, _vp, _int, _i64, _i64, _int, _int, _int, _i64, _i64, _i64, _i64, _i64, _i64,

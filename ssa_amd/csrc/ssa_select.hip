@@ -4,14 +4,21 @@
 // (ssa/router.py:151-259).  One 256-thread block per (batch, kv-head, query):
 //   1. the query's a buckets are clipped to keys j <= i (causal; postings
 //      ascend, so one binary search per bucket) and concatenated;
-//   2. postings stream through an n-bit LDS bitmap (atomicOr dedup); new keys
-//      queue in an LDS batch;
-//   3. each batch is rescored in the canonical fp32 order (one thread per key:
-//      g fmaf chains over d, / score_div, summed over the group, / g) and the
-//      composite keys that beat the running k-th best append to a top buffer,
-//      which a bitonic sort truncates back to k whenever it overflows;
-//   4. the final top buffer is sorted (score desc, index asc), then the lowest
-//      non-candidate indices fill the row up to min(k, n), then zeros pad to k.
+//   2. postings stream through an n-bit LDS bitmap (atomicOr dedup);
+//   3. candidates are rescored in the canonical fp32 order (one thread per key:
+//      g fmaf chains over d with the query operands in scalar registers,
+//      / score_div, summed over the group, / g); composite keys that beat the
+//      running k-th best append to a top buffer, which a bitonic sort
+//      truncates back to k whenever it overflows;
+//   4. the row is staged in LDS and stored with coalesced writes.
+// Two output orders:
+//   sorted   : selected keys by (score desc, index asc), as torch.topk returns
+//              them (ssa/router.py:204), then the lowest non-candidate indices
+//              up to min(k, n), then zeros;
+//   unsorted : the same index set, selected keys ascending, then the same
+//              filler.  Rows with at most k candidates need no scores at all in
+//              this order (their set is every candidate), so only rows with
+//              more than k candidates are rescored.
 #include "ssa_common.h"
 
 namespace ssa {
@@ -20,6 +27,10 @@ namespace {
 constexpr int kSelThreads = 256;
 constexpr int kSelBatch = 512;
 constexpr int kMaxA = 64;
+// Key-row 16-byte loads issued ahead of each rescoring group (4 x 8 features):
+// measured fastest at the headline shape against 1, 2 and 8, and against
+// broadcasting the query operands from LDS.
+constexpr int kRescoreLoads = 4;
 
 struct SelParams {
   const void* q;
@@ -32,7 +43,7 @@ struct SelParams {
   const int32_t* offsets;
   const int32_t* postings;
   int n_c, b;
-  int top_k, k_eff, sortn, mask_mode;
+  int top_k, k_eff, sortn, mask_mode, sorted;
   const uint8_t* mask;
   int64_t mask_sb, mask_si;
   float score_div;
@@ -47,13 +58,13 @@ __host__ __device__ inline int pow2_at_least(int v) {
   return p;
 }
 
-inline size_t select_smem(int64_t n, int d, int gmax, int sortn) {
+inline size_t select_smem(int64_t n, int sortn, int k_eff) {
   const size_t words = static_cast<size_t>((n + 31) / 32);
-  return sizeof(uint64_t) * sortn + sizeof(float) * static_cast<size_t>(d) * gmax +
-         sizeof(uint32_t) * words + sizeof(int32_t) * (kSelBatch + 2 * kMaxA + 1);
+  return sizeof(uint64_t) * sortn + sizeof(uint32_t) * words +
+         sizeof(int32_t) * (kSelBatch + k_eff + 2 * kMaxA + 1);
 }
 
-// 8 consecutive elements widened to fp32 (16-byte aligned for bf16, 32 for f32).
+// 8 consecutive elements widened to fp32 (16-byte aligned).
 __device__ __forceinline__ void load8(const uint16_t* p, float* o) {
   const uint4 u = *reinterpret_cast<const uint4*>(p);
   const uint32_t w[4] = {u.x, u.y, u.z, u.w};
@@ -113,17 +124,78 @@ __device__ int block_exclusive_scan(int v, int* scratch, int* total) {
   return base + x - v;
 }
 
-template <typename T, int GMAX>
-__global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams p) {
+// Writes, in ascending order, the first `limit` positions j < n whose bitmap bit
+// equals `want_set` to dst[0..]; returns how many were written.
+__device__ int scan_bits(const uint32_t* bitmap, int words, int64_t n, bool want_set, int32_t* dst,
+                         int limit, int* scratch) {
+  int filled = 0;
+  for (int w0 = 0; w0 < words && filled < limit; w0 += kSelThreads) {
+    const int w = w0 + threadIdx.x;
+    uint32_t bits = 0u;
+    if (w < words) {
+      bits = want_set ? bitmap[w] : ~bitmap[w];
+      if (w == words - 1 && (n & 31)) bits &= (1u << (n & 31)) - 1u;
+    }
+    int total = 0;
+    int rank = filled + block_exclusive_scan(__popc(bits), scratch, &total);
+    while (bits != 0u && rank < limit) {
+      const int bpos = __ffs(bits) - 1;
+      bits &= bits - 1u;
+      dst[rank++] = w * 32 + bpos;
+    }
+    filled += total;
+  }
+  return filled < limit ? filled : limit;
+}
+
+// Canonical rescoring of key row kr (per thread) against the group's query rows
+// (uniform: head gg at q0 + gg * q_sh): acc[gg] = fmaf chain over t ascending.
+// The query operands are loaded with uniform addresses from a read-only
+// argument, so they sit in scalar registers and the chains read no LDS.  D > 0
+// fixes the head dim so that each group of 16-byte key loads is issued before
+// the chains consume it; D == 0 walks a runtime d.
+template <typename T, int GMAX, int D>
+__device__ __forceinline__ void rescore_row(const T* kr, const T* q0, int64_t q_sh, int g, int d,
+                                            float (&acc)[GMAX]) {
+#pragma unroll
+  for (int gg = 0; gg < GMAX; ++gg) acc[gg] = 0.0f;
+  constexpr int G = kRescoreLoads;
+  const int dd = (D > 0) ? D : d;
+  // Rolled over groups: unrolling lets the compiler keep all D*GMAX query
+  // values live across the candidate loop.
+#pragma unroll 1
+  for (int t0 = 0; t0 < dd; t0 += 8 * G) {
+    float kv[G][8];
+#pragma unroll
+    for (int u = 0; u < G; ++u)
+      if (D > 0 || t0 + 8 * u < dd) load8(kr + t0 + 8 * u, kv[u]);
+#pragma unroll
+    for (int gg = 0; gg < GMAX; ++gg) {
+      if (gg >= g) continue;
+      const T* qgp = q0 + static_cast<int64_t>(gg) * q_sh + t0;
+#pragma unroll
+      for (int u = 0; u < G; ++u) {
+        if (D == 0 && t0 + 8 * u >= dd) continue;
+        float qv[8];
+        load8(qgp + 8 * u, qv);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[gg] = fma_rn(qv[e], kv[u][e], acc[gg]);
+      }
+    }
+  }
+}
+
+template <typename T, int GMAX, int D>
+__global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams p, const T* __restrict__ qg) {
   extern __shared__ __align__(16) unsigned char smem[];
   uint64_t* topbuf = reinterpret_cast<uint64_t*>(smem);
-  float* qs = reinterpret_cast<float*>(topbuf + p.sortn);  // [d][GMAX]
   const int words = static_cast<int>((p.n + 31) >> 5);
-  uint32_t* bitmap = reinterpret_cast<uint32_t*>(qs + p.d * GMAX);
+  uint32_t* bitmap = reinterpret_cast<uint32_t*>(topbuf + p.sortn);
   int32_t* batch = reinterpret_cast<int32_t*>(bitmap + words);
-  int32_t* seg_lo = batch + kSelBatch;
-  int32_t* seg_start = seg_lo + kMaxA;  // a + 1 entries
-  __shared__ int s_batch_cnt, s_top_cnt, s_cand_total, s_R, s_filled;
+  int32_t* stage = batch + kSelBatch;      // [k_eff] output row before the coalesced store
+  int32_t* seg_lo = stage + p.k_eff;
+  int32_t* seg_start = seg_lo + kMaxA;     // a + 1 entries
+  __shared__ int s_batch_cnt, s_top_cnt, s_cand, s_R;
   __shared__ uint64_t s_thr;
   __shared__ int s_scan[kSelThreads / 64];
 
@@ -133,14 +205,13 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams p) {
   const int64_t bh = row / p.n;
   const int h = static_cast<int>(bh % p.h_kv);
   const int64_t bb = bh / p.h_kv;
+  const T* q0 = qg + bb * p.q_sb + i * p.q_sn + static_cast<int64_t>(h * p.g) * p.q_sh;
+  const T* kbase = static_cast<const T*>(p.k) + bb * p.k_sb + static_cast<int64_t>(h) * p.k_sh;
+  const int32_t* pp = p.postings + bh * p.n * p.b;
+  const uint8_t* mrow =
+      (p.mask_mode == SSA_MASK_DENSE) ? p.mask + bb * p.mask_sb + i * p.mask_si : nullptr;
 
   for (int w = tid; w < words; w += kSelThreads) bitmap[w] = 0u;
-  const T* qrow = static_cast<const T*>(p.q) + bb * p.q_sb + i * p.q_sn;
-  for (int e = tid; e < p.d * GMAX; e += kSelThreads) {
-    const int t = e / GMAX, gg = e % GMAX;
-    qs[e] = (gg < p.g) ? ld(qrow + static_cast<int64_t>(h * p.g + gg) * p.q_sh + t) : 0.0f;
-  }
-  const int32_t* pp = p.postings + bh * p.n * p.b;
   if (tid < p.a) {
     const int32_t c = p.q_codes[(bh * p.n + i) * p.a + tid];
     int32_t lo = 0, hi = 0;
@@ -165,7 +236,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams p) {
   if (tid == 0) {
     s_batch_cnt = 0;
     s_top_cnt = 0;
-    s_cand_total = 0;
+    s_cand = 0;
     s_thr = 0ull;
     seg_start[0] = 0;
   }
@@ -176,143 +247,149 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams p) {
   }
   __syncthreads();
   const int R = s_R;
-  const uint8_t* mrow =
-      (p.mask_mode == SSA_MASK_DENSE) ? p.mask + bb * p.mask_sb + i * p.mask_si : nullptr;
-  const T* kbase = static_cast<const T*>(p.k) + bb * p.k_sb + static_cast<int64_t>(h) * p.k_sh;
 
-  for (int base = 0; base < R; base += kSelThreads) {
-    const int pidx = base + tid;
-    if (pidx < R) {
-      int lo_m = 0, hi_m = p.a;
-      while (hi_m - lo_m > 1) {
-        const int mid = (lo_m + hi_m) >> 1;
-        if (seg_start[mid] <= pidx) lo_m = mid;
-        else hi_m = mid;
-      }
-      const int32_t j = pp[seg_lo[lo_m] + (pidx - seg_start[lo_m])];
-      const bool allowed = (static_cast<uint32_t>(j) < static_cast<uint32_t>(p.n)) &&
-                           ((mrow == nullptr) || (mrow[j] != 0));
-      if (allowed) {
-        const uint32_t bit = 1u << (j & 31);
-        const uint32_t old = atomicOr(&bitmap[j >> 5], bit);
-        if (!(old & bit)) batch[atomicAdd(&s_batch_cnt, 1)] = j;
-      }
-    }
-    __syncthreads();
-    const int bc = s_batch_cnt;
-    __syncthreads();  // every thread holds bc before the next round appends again
-    const bool last = (base + kSelThreads >= R);
-    if (bc > kSelBatch - kSelThreads || (last && bc > 0)) {
-      const uint64_t thr = s_thr;
-      for (int e = tid; e < bc; e += kSelThreads) {
-        const int32_t j = batch[e];
-        const T* kr = kbase + static_cast<int64_t>(j) * p.k_sn;
-        float acc[GMAX];
-#pragma unroll
-        for (int gg = 0; gg < GMAX; ++gg) acc[gg] = 0.0f;
-        for (int t0 = 0; t0 < p.d; t0 += 8) {
-          float kv[8];
-          load8(kr + t0, kv);
-#pragma unroll
-          for (int u = 0; u < 8; ++u) {
-            const float* qv = qs + (t0 + u) * GMAX;
-#pragma unroll
-            for (int gg = 0; gg < GMAX; ++gg) acc[gg] = fma_rn(qv[gg], kv[u], acc[gg]);
+  // Union of the row's postings into the bitmap.  With `collect`, new keys also
+  // queue in the batch and are rescored whenever it fills (streaming top-k).
+  auto union_pass = [&](bool collect) {
+    for (int base = 0; base < R; base += kSelThreads) {
+      const int pidx = base + tid;
+      if (pidx < R) {
+        int lo_m = 0, hi_m = p.a;
+        while (hi_m - lo_m > 1) {
+          const int mid = (lo_m + hi_m) >> 1;
+          if (seg_start[mid] <= pidx) lo_m = mid;
+          else hi_m = mid;
+        }
+        const int32_t j = pp[seg_lo[lo_m] + (pidx - seg_start[lo_m])];
+        const bool allowed = (static_cast<uint32_t>(j) < static_cast<uint32_t>(p.n)) &&
+                             ((mrow == nullptr) || (mrow[j] != 0));
+        if (allowed) {
+          const uint32_t bit = 1u << (j & 31);
+          const uint32_t old = atomicOr(&bitmap[j >> 5], bit);
+          if (!(old & bit)) {
+            if (collect) batch[atomicAdd(&s_batch_cnt, 1)] = j;
+            else atomicAdd(&s_cand, 1);
           }
         }
-        float s = acc[0] / p.score_div;
+      }
+      __syncthreads();
+      if (!collect) continue;
+      const int bc = s_batch_cnt;
+      __syncthreads();  // every thread holds bc before the next round appends again
+      const bool last = (base + kSelThreads >= R);
+      if (bc > kSelBatch - kSelThreads || (last && bc > 0)) {
+        const uint64_t thr = s_thr;
+        for (int e = tid; e < bc; e += kSelThreads) {
+          const int32_t j = batch[e];
+          float acc[GMAX];
+          rescore_row<T, GMAX, D>(kbase + static_cast<int64_t>(j) * p.k_sn, q0, p.q_sh, p.g, p.d, acc);
+          float sc = acc[0] / p.score_div;
 #pragma unroll
-        for (int gg = 1; gg < GMAX; ++gg)
-          if (gg < p.g) s = s + acc[gg] / p.score_div;
-        s = s / static_cast<float>(p.g);
-        const uint64_t key = composite_key(s, static_cast<uint32_t>(j));
-        if (key > thr) topbuf[atomicAdd(&s_top_cnt, 1)] = key;
-      }
-      __syncthreads();
-      const int tc = s_top_cnt;
-      if (tc > p.k_eff) {
-        const int len = pow2_at_least(tc);
-        for (int e = tc + tid; e < len; e += kSelThreads) topbuf[e] = 0ull;
-        __syncthreads();
-        bitonic_desc(topbuf, len);
-      }
-      if (tid == 0) {
-        if (tc > p.k_eff) {
-          s_top_cnt = p.k_eff;
-          s_thr = topbuf[p.k_eff - 1];
+          for (int gg = 1; gg < GMAX; ++gg)
+            if (gg < p.g) sc = sc + acc[gg] / p.score_div;
+          sc = sc / static_cast<float>(p.g);
+          const uint64_t key = composite_key(sc, static_cast<uint32_t>(j));
+          if (key > thr) topbuf[atomicAdd(&s_top_cnt, 1)] = key;
         }
-        s_cand_total += bc;
-        s_batch_cnt = 0;
+        __syncthreads();
+        const int tc = s_top_cnt;
+        if (tc > p.k_eff) {
+          const int len = pow2_at_least(tc);
+          for (int e = tc + tid; e < len; e += kSelThreads) topbuf[e] = 0ull;
+          __syncthreads();
+          bitonic_desc(topbuf, len);
+        }
+        if (tid == 0) {
+          if (tc > p.k_eff) {
+            s_top_cnt = p.k_eff;
+            s_thr = topbuf[p.k_eff - 1];
+          }
+          s_cand += bc;
+          s_batch_cnt = 0;
+        }
+        __syncthreads();
+      }
+    }
+  };
+
+  int nsel = 0;  // selected candidates at the head of `stage`
+  if (!p.sorted) {
+    union_pass(false);
+    __syncthreads();
+    const int C = s_cand;
+    __syncthreads();  // every thread holds C before thread 0 may reset s_cand below
+    if (C <= p.k_eff) {
+      nsel = scan_bits(bitmap, words, p.n, true, stage, C, s_scan);
+    } else {
+      for (int w = tid; w < words; w += kSelThreads) bitmap[w] = 0u;
+      if (tid == 0) s_cand = 0;
+      __syncthreads();
+      union_pass(true);
+      // Selected set (top k_eff keys) in ascending index order, via the bitmap.
+      for (int w = tid; w < words; w += kSelThreads) bitmap[w] = 0u;
+      __syncthreads();
+      for (int e = tid; e < p.k_eff; e += kSelThreads) {
+        const uint32_t j = key_index(topbuf[e]);
+        atomicOr(&bitmap[j >> 5], 1u << (j & 31));
       }
       __syncthreads();
+      nsel = scan_bits(bitmap, words, p.n, true, stage, p.k_eff, s_scan);
+      // Restore the candidate bitmap for the filler: no filler is needed here.
     }
-  }
-
-  const int tc = s_top_cnt;
-  if (tc > 1) {
-    const int len = pow2_at_least(tc);
-    for (int e = tc + tid; e < len; e += kSelThreads) topbuf[e] = 0ull;
+  } else {
+    union_pass(true);
+    const int tc = s_top_cnt;
+    if (tc > 1) {
+      const int len = pow2_at_least(tc);
+      for (int e = tc + tid; e < len; e += kSelThreads) topbuf[e] = 0ull;
+      __syncthreads();
+      bitonic_desc(topbuf, len);
+    }
     __syncthreads();
-    bitonic_desc(topbuf, len);
+    nsel = tc < p.k_eff ? tc : p.k_eff;
+    for (int w = tid; w < nsel; w += kSelThreads) stage[w] = static_cast<int32_t>(key_index(topbuf[w]));
   }
+  __syncthreads();
+  if (nsel < p.k_eff) scan_bits(bitmap, words, p.n, false, stage + nsel, p.k_eff - nsel, s_scan);
   __syncthreads();
 
   const int64_t obase = ((bb * p.n + i) * p.h_kv + h) * p.top_k;
-  int64_t* out64 = static_cast<int64_t*>(p.out) + obase;
-  int32_t* out32 = static_cast<int32_t*>(p.out) + obase;
-  auto put = [&](int w, int64_t v) {
-    if (p.out_i64) out64[w] = v;
-    else out32[w] = static_cast<int32_t>(v);
-  };
-  const int nsel = tc < p.k_eff ? tc : p.k_eff;
-  for (int w = tid; w < nsel; w += kSelThreads) put(w, key_index(topbuf[w]));
-
-  const int need = p.k_eff - nsel;
-  if (need > 0) {
-    if (tid == 0) s_filled = 0;
-    __syncthreads();
-    for (int w0 = 0; w0 < words; w0 += kSelThreads) {
-      const int filled = s_filled;
-      if (filled >= need) break;
-      const int w = w0 + tid;
-      uint32_t zeros = 0u;
-      if (w < words) {
-        zeros = ~bitmap[w];
-        if (w == words - 1 && (p.n & 31)) zeros &= (1u << (p.n & 31)) - 1u;
-      }
-      int total = 0;
-      int rank = filled + block_exclusive_scan(__popc(zeros), s_scan, &total);
-      while (zeros != 0u && rank < need) {
-        const int bpos = __ffs(zeros) - 1;
-        zeros &= zeros - 1u;
-        put(nsel + rank, static_cast<int64_t>(w) * 32 + bpos);
-        ++rank;
-      }
-      __syncthreads();
-      if (tid == 0) s_filled = filled + total;
-      __syncthreads();
-    }
+  if (p.out_i64) {
+    int64_t* out64 = static_cast<int64_t*>(p.out) + obase;
+    for (int w = tid; w < p.top_k; w += kSelThreads) out64[w] = (w < p.k_eff) ? stage[w] : 0;
+  } else {
+    int32_t* out32 = static_cast<int32_t*>(p.out) + obase;
+    for (int w = tid; w < p.top_k; w += kSelThreads) out32[w] = (w < p.k_eff) ? stage[w] : 0;
   }
-  for (int w = p.k_eff + tid; w < p.top_k; w += kSelThreads) put(w, 0);
   if (p.stats && tid == 0) {
-    p.stats[(bh * p.n + i) * 2 + 0] = s_cand_total;
+    p.stats[(bh * p.n + i) * 2 + 0] = s_cand;
     p.stats[(bh * p.n + i) * 2 + 1] = R;
   }
 }
 
-template <typename T, int GMAX>
+template <typename T, int GMAX, int D>
 int launch_select(const SelParams& p, int64_t rows, size_t smem, hipStream_t st) {
-  auto kern = select_kernel<T, GMAX>;
+  auto kern = select_kernel<T, GMAX, D>;
   if (int s = reserve_lds(reinterpret_cast<const void*>(kern), smem, "select")) return s;
-  kern<<<dim3(static_cast<unsigned>(rows)), kSelThreads, smem, st>>>(p);
+  kern<<<dim3(static_cast<unsigned>(rows)), kSelThreads, smem, st>>>(p, static_cast<const T*>(p.q));
   return check_launch("select_kernel");
 }
 
+template <typename T, int GMAX>
+int dispatch_select_d(const SelParams& p, int64_t rows, size_t smem, hipStream_t st) {
+  switch (p.d) {
+    case 64: return launch_select<T, GMAX, 64>(p, rows, smem, st);
+    case 128: return launch_select<T, GMAX, 128>(p, rows, smem, st);
+    case 256: return launch_select<T, GMAX, 256>(p, rows, smem, st);
+    default: return launch_select<T, GMAX, 0>(p, rows, smem, st);
+  }
+}
+
 template <typename T>
-int dispatch_select(const SelParams& p, int64_t rows, hipStream_t st) {
-  if (p.g <= 4) return launch_select<T, 4>(p, rows, select_smem(p.n, p.d, 4, p.sortn), st);
-  if (p.g <= 8) return launch_select<T, 8>(p, rows, select_smem(p.n, p.d, 8, p.sortn), st);
-  return launch_select<T, 16>(p, rows, select_smem(p.n, p.d, 16, p.sortn), st);
+int dispatch_select(const SelParams& p, int64_t rows, size_t smem, hipStream_t st) {
+  if (p.g <= 4) return dispatch_select_d<T, 4>(p, rows, smem, st);
+  if (p.g <= 8) return dispatch_select_d<T, 8>(p, rows, smem, st);
+  return dispatch_select_d<T, 16>(p, rows, smem, st);
 }
 
 }  // namespace
@@ -325,8 +402,8 @@ extern "C" int ssa_select(const void* q, const void* k, int dtype, int64_t batch
                           int64_t k_sb, int64_t k_sn, int64_t k_sh, const int32_t* q_codes, int a,
                           const int32_t* offsets, const int32_t* postings, int n_c, int b,
                           int top_k, int mask_mode, const uint8_t* mask, int64_t mask_sb,
-                          int64_t mask_si, float score_div, void* out, int out_index_dtype,
-                          int32_t* stats, void* stream) {
+                          int64_t mask_si, float score_div, int sorted, void* out,
+                          int out_index_dtype, int32_t* stats, void* stream) {
   if (dtype != SSA_DTYPE_F32 && dtype != SSA_DTYPE_BF16)
     return fail(SSA_ERR_UNSUPPORTED, "select: dtype %d not supported (f32, bf16)", dtype);
   if (batch < 0 || n < 0 || h_q <= 0 || h_kv <= 0 || d <= 0 || a <= 0 || b <= 0 || n_c <= 0 ||
@@ -349,9 +426,9 @@ extern "C" int ssa_select(const void* q, const void* k, int dtype, int64_t batch
     return fail(SSA_ERR_INVALID_ARGUMENT, "select: out_index_dtype %d", out_index_dtype);
   if (!(score_div > 0.0f)) return fail(SSA_ERR_INVALID_ARGUMENT, "select: score_div must be > 0");
   const int vec = (dtype == SSA_DTYPE_BF16) ? 8 : 4;
-  if ((k_sn % vec) || (k_sh % vec) || (k_sb % vec) ||
-      (reinterpret_cast<uintptr_t>(k) % 16))
-    return fail(SSA_ERR_UNSUPPORTED, "select: k rows must be 16-byte aligned");
+  if ((k_sn % vec) || (k_sh % vec) || (k_sb % vec) || (reinterpret_cast<uintptr_t>(k) % 16) ||
+      (q_sn % vec) || (q_sh % vec) || (q_sb % vec) || (reinterpret_cast<uintptr_t>(q) % 16))
+    return fail(SSA_ERR_UNSUPPORTED, "select: q and k rows must be 16-byte aligned");
   if (batch == 0 || n == 0) return SSA_OK;
   if (!q || !k || !q_codes || !offsets || !postings || !out)
     return fail(SSA_ERR_INVALID_ARGUMENT, "select: null pointer");
@@ -374,6 +451,7 @@ extern "C" int ssa_select(const void* q, const void* k, int dtype, int64_t batch
   p.top_k = top_k;
   p.k_eff = static_cast<int>(top_k < n ? top_k : n);
   p.sortn = pow2_at_least(p.k_eff + kSelBatch);
+  p.sorted = sorted ? 1 : 0;
   p.mask_mode = mask_mode;
   p.mask = mask;
   p.mask_sb = mask_sb;
@@ -382,14 +460,13 @@ extern "C" int ssa_select(const void* q, const void* k, int dtype, int64_t batch
   p.out = out;
   p.out_i64 = (out_index_dtype == SSA_INDEX_I64);
   p.stats = stats;
-  const int gmax = g <= 4 ? 4 : (g <= 8 ? 8 : 16);
-  const size_t smem = select_smem(n, d, gmax, p.sortn);
+  const size_t smem = select_smem(n, p.sortn, p.k_eff);
   if (smem > 160 * 1024)
     return fail(SSA_ERR_UNSUPPORTED, "select: needs %zu bytes of LDS (n=%lld, top_k=%d)", smem,
                 static_cast<long long>(n), top_k);
   const int64_t rows = batch * h_kv * n;
   if (rows >= (int64_t(1) << 31)) return fail(SSA_ERR_UNSUPPORTED, "select: too many rows");
   hipStream_t st = as_stream(stream);
-  if (dtype == SSA_DTYPE_BF16) return dispatch_select<uint16_t>(p, rows, st);
-  return dispatch_select<float>(p, rows, st);
+  if (dtype == SSA_DTYPE_BF16) return dispatch_select<uint16_t>(p, rows, smem, st);
+  return dispatch_select<float>(p, rows, smem, st);
 }

@@ -117,12 +117,13 @@ def select(q: torch.Tensor, k: torch.Tensor, q_codes: torch.Tensor, offsets: tor
            postings: torch.Tensor, b: int, top_k: int, mask_mode: int = _lib.MASK_CAUSAL,
            mask: Optional[torch.Tensor] = None, score_div: Optional[float] = None,
            index_dtype: torch.dtype = torch.int64,
-           with_stats: bool = False):
+           with_stats: bool = False, sorted: bool = True):
     """Stage (c): candidate indices [B, n, h_kv, top_k] (ssa/router.py:151-214).
 
     ``mask`` (MASK_DENSE) is a bool/uint8 ``[n, n]`` or ``[B, n, n]`` tensor with a
     contiguous last dimension.  ``with_stats`` also returns int32 ``[B, h_kv, n, 2]``
-    (unique candidates, postings read) per row.
+    (unique candidates, postings read) per row.  ``sorted=False`` lists the same
+    selected set in ascending index order (then the same filler).
     """
     _check_rows(q, "q")
     _check_rows(k, "k")
@@ -151,8 +152,8 @@ def select(q: torch.Tensor, k: torch.Tensor, q_codes: torch.Tensor, offsets: tor
     call("ssa_select", ptr(q), ptr(k), _lib.elem_dtype(q), B, n, h_q, h_kv, d,
          q.stride(0), q.stride(1), q.stride(2), k.stride(0), k.stride(1), k.stride(2),
          ptr(q_codes), a, ptr(offsets), ptr(postings), n_c, b, top_k, mask_mode, ptr(mask),
-         m_sb, m_si, float(score_div), ptr(out), _lib.index_dtype(out), ptr(stats),
-         stream_of(q))
+         m_sb, m_si, float(score_div), int(bool(sorted)), ptr(out), _lib.index_dtype(out),
+         ptr(stats), stream_of(q))
     return (out, stats) if with_stats else out
 
 

@@ -92,6 +92,8 @@ class CodebookRouter(nn.Module):
         k_full: torch.Tensor,
         causal_mask: MaskArg = None,
         hard: bool = True,
+        *,
+        sorted: bool = True,
     ) -> torch.Tensor:
         """Candidate key indices (ssa/router.py:73-149).
 
@@ -102,6 +104,10 @@ class CodebookRouter(nn.Module):
                 or any bool ``[n, n]`` mask (True = allowed).
             hard: must be True; the reference's Gumbel branch cannot produce
                 indices (ssa/router.py:131-137 vs :253).
+            sorted: keyword-only; True (default) orders the selected keys by
+                score like torch.topk; False lists the same set in ascending
+                index order, which lets rows with at most top_k candidates skip
+                rescoring.
 
         Returns:
             int64 ``[n, h_kv, top_k]`` (``[B, n, h_kv, top_k]`` for batched input),
@@ -109,10 +115,12 @@ class CodebookRouter(nn.Module):
             than top_k candidates continue with the lowest non-candidate indices,
             and top_k > n pads with index 0.
         """
-        return self.route(q_full, k_full, causal_mask=causal_mask, hard=hard).indices_view
+        return self.route(q_full, k_full, causal_mask=causal_mask, hard=hard,
+                          sorted=sorted).indices_view
 
     def route(self, q_full: torch.Tensor, k_full: torch.Tensor, causal_mask: MaskArg = None,
-              hard: bool = True, with_stats: bool = False, index_dtype=torch.int64):
+              hard: bool = True, with_stats: bool = False, index_dtype=torch.int64,
+              sorted: bool = True):
         """Run stages (a)-(c) and keep the intermediates (a RouteResult)."""
         if not hard:
             raise NotImplementedError(
@@ -138,7 +146,8 @@ class CodebookRouter(nn.Module):
         if mask is not None:
             mask = mask.to(q.device)
         res = kernels.select(q, k, q_codes, offsets, postings, self.codes_per_key, self.top_k,
-                             mode, mask, index_dtype=index_dtype, with_stats=with_stats)
+                             mode, mask, index_dtype=index_dtype, with_stats=with_stats,
+                             sorted=sorted)
         idx, stats = res if with_stats else (res, None)
         out = RouteResult(q_codes, k_codes, offsets, postings, idx, stats)
         out.indices_view = idx[0] if unbatched else idx

@@ -120,7 +120,10 @@ class SSAAttention(nn.Module):
             mask = build_causal_mask(n, device=hidden_states.device)
             out = torch.stack([dense_attention(q[b], k[b], v[b], causal_mask=mask) for b in range(B)])
         else:
-            indices = self.router(q, k, causal_mask=True, hard=True)
+            # Stage 3 does not depend on the order of the selected keys, so the
+            # router lists them by index and skips rescoring rows whose
+            # candidates all fit in top_k.
+            indices = self.router(q, k, causal_mask=True, hard=True, sorted=False)
             out = sparse_exact_attention(q, k, v, indices, causal=self.causal_attention,
                                          check_indices=False)
         return self.o_proj(out.reshape(B, n, -1).to(hidden_states.dtype))

@@ -102,11 +102,12 @@ def _route_inputs(n, h_q, h_kv, d, d_s, n_c, seed, dtype, clustered):
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("mode", ["causal", "none", "dense"])
 @pytest.mark.parametrize("clustered", [False, True])
-def test_router_pipeline_bit_exact(dev, orc, dtype, mode, clustered):
+@pytest.mark.parametrize("sorted_", [True, False])
+def test_router_pipeline_bit_exact(dev, orc, dtype, mode, clustered, sorted_):
     """Stages (a)-(c) through CodebookRouter vs the oracle, with per-row stats."""
     from ssa_amd import CodebookRouter, build_causal_mask
 
-    _say(f"router pipeline dtype={dtype} mode={mode} clustered={clustered}")
+    _say(f"router pipeline dtype={dtype} mode={mode} clustered={clustered} sorted={sorted_}")
     n, h_q, h_kv, d, d_s, n_c, a, b, k = 777, 8, 2, 128, 32, 128, 16, 4, 64
     q, kk, w_qr, w_kr, cb = _route_inputs(n, h_q, h_kv, d, d_s, n_c, 11, dtype, clustered)
     r = CodebookRouter(head_dim=d, route_dim=d_s, num_kv_heads=h_kv, num_codebook=n_c,
@@ -124,9 +125,10 @@ def test_router_pipeline_bit_exact(dev, orc, dtype, mode, clustered):
         gm = torch.Generator().manual_seed(3)
         m = (torch.rand(n, n, generator=gm) < 0.6) | torch.eye(n, dtype=torch.bool)
         cm, omode, omask = m.to(dev), orc.MASK_DENSE, m.numpy().astype(np.uint8)
-    res = r.route(q.to(dev), kk.to(dev), causal_mask=cm, with_stats=True)
+    res = r.route(q.to(dev), kk.to(dev), causal_mask=cm, with_stats=True, sorted=sorted_)
     (ref, ncand, nraw), ex = orc.router_forward(f32(q), f32(kk), f32(w_qr), f32(w_kr), f32(cb),
-                                               a, b, k, omode, omask, with_stats=True)
+                                               a, b, k, omode, omask, with_stats=True,
+                                               sorted=sorted_)
     np.testing.assert_array_equal(res.q_codes[0].cpu().numpy(), ex["q_codes"])
     np.testing.assert_array_equal(res.k_codes[0].cpu().numpy(), ex["k_codes"])
     np.testing.assert_array_equal(res.offsets[0].cpu().numpy(), ex["offsets"])
@@ -138,12 +140,13 @@ def test_router_pipeline_bit_exact(dev, orc, dtype, mode, clustered):
 
 
 @pytest.mark.parametrize("top_k", [1, 600, 1000, 4096])
-def test_select_k_edges(dev, orc, top_k):
+@pytest.mark.parametrize("sorted_", [True, False])
+def test_select_k_edges(dev, orc, top_k, sorted_):
     """k > n pads zeros; k = n lists every index; k = 1."""
     from ssa_amd import CodebookRouter
 
     n = 1000 if top_k != 4096 else 2500
-    _say(f"select k edges n={n} top_k={top_k}")
+    _say(f"select k edges n={n} top_k={top_k} sorted={sorted_}")
     q, kk, w_qr, w_kr, cb = _route_inputs(n, 4, 1, 64, 16, 64, 21, torch.float32, False)
     r = CodebookRouter(head_dim=64, route_dim=16, num_kv_heads=1, num_codebook=64,
                        codes_per_key=4, codes_per_query=8, top_k=top_k)
@@ -151,8 +154,9 @@ def test_select_k_edges(dev, orc, top_k):
         r.W_qr.weight.copy_(w_qr)
         r.W_kr.weight.copy_(w_kr)
         r.codebook.copy_(cb)
-    got = r.to(dev)(q.to(dev), kk.to(dev), causal_mask=True).cpu().numpy()
-    ref, _ = orc.router_forward(f32(q), f32(kk), f32(w_qr), f32(w_kr), f32(cb), 8, 4, top_k)
+    got = r.to(dev)(q.to(dev), kk.to(dev), causal_mask=True, sorted=sorted_).cpu().numpy()
+    ref, _ = orc.router_forward(f32(q), f32(kk), f32(w_qr), f32(w_kr), f32(cb), 8, 4, top_k,
+                                sorted=sorted_)
     np.testing.assert_array_equal(got, ref)
     if top_k >= n:
         assert (np.sort(got[:, :, :n], axis=-1) == np.arange(n)).all()
