@@ -61,7 +61,13 @@ def build_causal_mask(seq_len: int, device=None) -> torch.Tensor:
 
 
 def expand_kv_for_gqa(kv: torch.Tensor, num_q_heads: int, num_kv_heads: int) -> torch.Tensor:
-    """Repeat each KV head for its query group (ssa/utils.py:89-106)."""
+    """KV heads repeated to num_q_heads (ssa/utils.py:89-106).
+
+    Same layout as the reference helper: the KV heads are tiled, so expanded
+    head j is KV head ``j % num_kv_heads``.  The attention functions pair query
+    head j with KV head ``j // (num_q_heads // num_kv_heads)`` instead; no
+    reference code path calls this helper.
+    """
     assert num_q_heads % num_kv_heads == 0, "num_q_heads must be divisible by num_kv_heads"
     g = num_q_heads // num_kv_heads
     return kv.unsqueeze(-3).expand(*kv.shape[:-2], g, kv.shape[-2], kv.shape[-1]).reshape(
