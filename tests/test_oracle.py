@@ -237,3 +237,43 @@ def test_brute_force_catches_planted_mistakes():
     q_head0 = np.repeat(q[:, ::g], g, axis=1)  # every group member replaced by head 0
     assert not np.array_equal(oracle.brute_select(q_head0, k, qc, kc, 6, True), good)
     assert np.array_equal(oracle.brute_select(q, k, qc, kc, 6, True), good)
+
+
+@pytest.mark.parametrize("mistake", ["sign", "mask", "kv_transposed", "scale_multiplier",
+                                     "w_swapped", "group_index"])
+def test_checks_catch_planted_mistakes(mistake):
+    """Plausible mistakes, planted in the oracle's inputs or call, are caught by
+    the independent checks: the brute-force selection, the float64 attention
+    restatement, or the golden vectors' codes."""
+    q, k, w_qr, w_kr, cb, a, b = _tiny_router_case(91)
+    (good, _, _), ex = oracle.router_forward(q, k, w_qr, w_kr, cb, a, b, 6, with_stats=True)
+    qc, kc = ex["q_codes"], ex["k_codes"]
+    ref = oracle.brute_select(q, k, qc, kc, 6, True)
+    np.testing.assert_array_equal(good, ref)
+    idx = good
+    att_ref = oracle.np_sparse_attention64(q, k, k[:, :, ::-1].copy(), idx)
+    v = k[:, :, ::-1].copy()
+    if mistake == "sign":
+        bad = oracle.router_forward(-q, k, w_qr, w_kr, cb, a, b, 6, with_stats=False)[0]
+        assert not np.array_equal(bad, ref)
+    elif mistake == "mask":
+        bad = oracle.router_forward(q, k, w_qr, w_kr, cb, a, b, 6, oracle.MASK_NONE)[0]
+        assert not np.array_equal(bad, ref)
+    elif mistake == "kv_transposed":
+        bad = oracle.sparse_attention(q, v, k, idx)
+        assert not np.allclose(bad, att_ref, rtol=1e-3, atol=1e-3)
+        np.testing.assert_allclose(oracle.sparse_attention(q, k, v, idx), att_ref, rtol=1e-9, atol=1e-9)
+    elif mistake == "scale_multiplier":
+        d = q.shape[-1]
+        bad = oracle.sparse_attention(q, k, v, idx, scale=1.0 / d ** 0.5)
+        assert not np.allclose(bad, att_ref, rtol=1e-3, atol=1e-3)
+    elif mistake == "w_swapped":
+        bad = oracle.router_forward(q, k, w_kr, w_qr, cb, a, b, 6)[1]["q_codes"]
+        assert not np.array_equal(bad, qc)
+    elif mistake == "group_index":
+        # query head j paired with kv head j % h_kv instead of j // g
+        h_kv = k.shape[1]
+        g = q.shape[1] // h_kv
+        perm = np.array([(j % h_kv) * g + j // h_kv for j in range(q.shape[1])])
+        bad = oracle.router_forward(q[:, perm], k, w_qr, w_kr, cb, a, b, 6)[0]
+        assert not np.array_equal(bad, ref)
