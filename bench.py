@@ -108,7 +108,7 @@ def algorithmic(cfg, n, stats_sum=None):
 
 
 def run_step(q, k, v, router, events=None):
-    from ssa_amd import kernels, sparse_exact_attention  # noqa: F401
+    from ssa_amd import kernels
 
     if events:
         events[0].record()
@@ -119,7 +119,7 @@ def run_step(q, k, v, router, events=None):
     off, post = kernels.build_index(kc, router.num_codebook)
     if events:
         events[2].record()
-    # Same call as SSAAttention: stage (d) does not depend on the order of the
+    # Same calls as SSAAttention: stage (d) does not depend on the order of the
     # selected keys, so the router lists them by index (same set as sorted).
     idx = kernels.select(q, k, qc, off, post, router.codes_per_key, router.top_k, sorted=False)
     if events:

@@ -139,6 +139,11 @@ int ssa_select(const void* q, const void* k, int dtype, int64_t batch, int64_t n
  * `scale_div` is the reference's `scale` (a divisor); duplicates count twice.
  * causal != 0 drops slots with idx > i (a row with no slot left outputs zeros).
  * Indices outside [0, n) are dropped and set *error_flag (nullable) to 1.
+ * row_order (nullable) int32 [batch][h_kv][n]: a permutation of 0..n-1 per
+ *   (batch, kv head) giving the order in which query rows are processed (e.g.
+ *   grouped by routing code so that rows sharing candidates run together and
+ *   hit in cache).  Results do not depend on it; a row never listed is not
+ *   written, and an entry outside [0, n) is skipped and sets *error_flag.
  *   idx [batch][n][h_kv][top_k] strides (idx_sb, idx_sn, idx_sh)
  *   out [batch][n][h_q][d] strides (o_sb, o_sn, o_sh), type out_dtype
  * Limits: d in {64, 128, 256}, g <= 16. */
@@ -147,7 +152,8 @@ int ssa_sparse_attention(const void* q, const void* k, const void* v, int dtype,
                          int64_t q_sh, int64_t k_sb, int64_t k_sn, int64_t k_sh, int64_t v_sb,
                          int64_t v_sn, int64_t v_sh, const void* idx, int idx_dtype, int top_k,
                          int64_t idx_sb, int64_t idx_sn, int64_t idx_sh, float scale_div,
-                         int causal, void* out, int out_dtype, int64_t o_sb, int64_t o_sn,
+                         int causal, const int32_t* row_order, void* out, int out_dtype,
+                         int64_t o_sb, int64_t o_sn,
                          int64_t o_sh, int32_t* error_flag, void* stream);
 
 #ifdef __cplusplus

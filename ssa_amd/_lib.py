@@ -64,8 +64,8 @@ SIGNATURES = {
     "ssa_sparse_attention": (
         _int,
         [_vp, _vp, _vp, _int, _i64, _i64, _int, _int, _int, _i64, _i64, _i64, _i64, _i64, _i64,
-         _i64, _i64, _i64, _vp, _int, _int, _i64, _i64, _i64, _flt, _int, _vp, _int, _i64, _i64,
-         _i64, _vp, _vp]),
+         _i64, _i64, _i64, _vp, _int, _int, _i64, _i64, _i64, _flt, _int, _vp, _vp, _int, _i64,
+         _i64, _i64, _vp, _vp]),
 }
 
 _lib = None

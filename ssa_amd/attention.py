@@ -24,6 +24,7 @@ def sparse_exact_attention(
     *,
     causal: bool = False,
     check_indices: bool = True,
+    row_order: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """softmax(q . K[indices]^T / scale) . V[indices] per (query, KV head).
 
@@ -36,6 +37,9 @@ def sparse_exact_attention(
     row left with no index outputs zeros); ``check_indices`` raises IndexError
     (after a device sync) if any index is outside [0, n), as the reference's
     gather does -- out-of-range slots are never read either way.
+    ``row_order`` (int32 [B, h_kv, n], e.g. ``CodebookRouter.route(...,
+    with_order=True).order``) sets the order rows are processed in, for cache
+    locality; it does not change the result.
     """
     unbatched = q.dim() == 3
     if unbatched:
@@ -53,7 +57,10 @@ def sparse_exact_attention(
     if indices.stride(-1) != 1:
         indices = indices.contiguous()
     flag = torch.zeros(1, device=q.device, dtype=torch.int32) if check_indices else None
-    out = kernels.sparse_attention(q, k, v, indices, float(scale), causal, error_flag=flag)
+    if row_order is not None and unbatched and row_order.dim() == 2:
+        row_order = row_order.unsqueeze(0)
+    out = kernels.sparse_attention(q, k, v, indices, float(scale), causal, error_flag=flag,
+                                   row_order=row_order)
     if flag is not None and int(flag.item()) != 0:
         raise IndexError(f"sparse_exact_attention: an index is outside [0, {seq_len})")
     if out.dtype != out_dtype:

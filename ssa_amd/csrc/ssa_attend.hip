@@ -53,7 +53,40 @@ struct AttParams {
   int64_t o_sb, o_sn, o_sh;
   int32_t* err;
   int64_t rows;
+  const int32_t* order;  // nullable [B*h_kv][n]: query index processed at each position
 };
+
+// Row processed by wave slot `lrow` (in (b*h_kv + h)*n + position order): the query
+// index is the position itself, or order[lrow] when a processing order is given.
+// An order entry outside [0, n) drops the row and raises the error flag.
+struct AttRow {
+  int64_t i, bh;
+  bool ok;
+};
+__device__ __forceinline__ AttRow att_row(const AttParams& p, int64_t lrow) {
+  AttRow r;
+  r.ok = lrow < p.rows;
+  const int64_t l = r.ok ? lrow : 0;
+#if SSA_ATT_HMINOR
+  const int64_t nbh = p.rows / p.n;
+  r.bh = l % nbh;
+  r.i = l / nbh;
+#else
+  r.bh = l / p.n;
+  r.i = l - r.bh * p.n;
+#endif
+  if (p.order) {
+    const int64_t o = p.order[r.bh * p.n + r.i];
+    if (o < 0 || o >= p.n) {
+      if (r.ok && p.err) p.err[0] = 1;
+      r.ok = false;
+      r.i = 0;
+    } else {
+      r.i = o;
+    }
+  }
+  return r;
+}
 
 __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
   uint32_t u = __float_as_uint(f);
@@ -201,11 +234,10 @@ __global__ __launch_bounds__(kAttThreads, (AttMinBlocks<T, D, GMAX>::value)) voi
   const int lane = threadIdx.x & 63;
   const int q4 = lane >> 4;
   const int c16 = lane & 15;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * kAttWaves + wave;  // (b*h_kv + h)*n + i
-  const bool row_ok = row < p.rows;
-  const int64_t rr = row_ok ? row : 0;
-  const int64_t i = rr % p.n;
-  const int64_t bh = rr / p.n;
+  const AttRow ar = att_row(p, static_cast<int64_t>(blockIdx.x) * kAttWaves + wave);
+  const bool row_ok = ar.ok;
+  const int64_t i = ar.i;
+  const int64_t bh = ar.bh;
   const int h = static_cast<int>(bh % p.h_kv);
   const int64_t bb = bh / p.h_kv;
 
@@ -381,9 +413,292 @@ __global__ __launch_bounds__(kAttThreads, (AttMinBlocks<T, D, GMAX>::value)) voi
   }
 }
 
+// ---- bf16, g <= 8, d <= 128: P.V on the matrix cores ----------------------
+//
+// Per chunk of 32 selected keys (one wave, one (batch, kv head, query) row):
+//   S^T = K . Q^T  two 16x16x32 MFMA tiles per 32 dims: A = 16 gathered K rows
+//                  (lane (q4, c16): key 16t + c16, dims 8*q4 ..), B = the group's
+//                  q rows.  Lane (q4, c16) gets head c16's scores of keys
+//                  16t + 4*q4 + e, i.e. eight keys of one head;
+//   softmax        online in the exp2 domain, per head, max and sum reduced
+//                  across the four lanes that hold a head's keys;
+//   P              split as P = P_hi + P_lo, both bf16 (relative error of the
+//                  sum ~2^-17): head r's P_hi is row r and its P_lo row 8 + r of
+//                  the 16-row P^T operand, so one MFMA covers both for g <= 8;
+//   O^T += V^T P^T one 16x16x32 MFMA per 16 features: A = V^T, read from the
+//                  chunk's V rows staged in LDS with ds_read_b64_tr_b16 (each
+//                  lane gets four rows of one feature column), B = P^T;
+//   output         O = (row r + row 8 + r) / l, four contiguous features per lane
+//                  and tile.
+// V values of dropped slots are zeroed, so 0 * inf never reaches the sums.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16_t* lds_v4i16_ptr;
+
+constexpr int kMfChunk = 32;
+#ifndef SSA_ATT_KLDS
+#define SSA_ATT_KLDS 0
+#endif
+#ifndef SSA_ATT_NT
+#define SSA_ATT_NT 0
+#endif
+#ifndef SSA_ATT_HMINOR
+#define SSA_ATT_HMINOR 0
+#endif
+
+template <int D>
+struct MfShape {
+  static constexpr int KB = D / 32;           // 32-dim blocks of Q.K
+  static constexpr int NT = D / 16;           // 16-feature tiles of P.V
+  static constexpr int ROW_B = 2 * D + 32;    // bytes per staged V row (32 B pad: tr reads of
+                                              // four consecutive rows hit disjoint banks)
+  static constexpr int SEGS = D / 8;          // 16-byte segments per V row
+  static constexpr int KPI = 64 / SEGS;       // V rows per wave-wide load
+  static constexpr int NVI = kMfChunk / KPI;  // V loads per lane per chunk
+};
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  const bf16x2_t v = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
+  return __builtin_bit_cast(uint32_t, v);
+}
+// lane p of each 16-lane row reads lane p - 8 (lanes p < 8 read 0)
+__device__ __forceinline__ uint32_t dpp_from_minus8(uint32_t x) {
+  return __builtin_amdgcn_update_dpp(0u, x, 0x118, 0xF, 0xF, false);
+}
+// lane p of each 16-lane row reads lane p + 8 (lanes p >= 8 read 0)
+__device__ __forceinline__ float dpp_from_plus8(float x) {
+  return __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(x), 0x108, 0xF, 0xF, false));
+}
+
+template <int D>
+#ifndef SSA_ATT_MINW
+#define SSA_ATT_MINW 2
+#endif
+__global__ __launch_bounds__(kAttThreads, SSA_ATT_MINW) void sparse_attention_mfma_kernel(AttParams p) {
+  using S = MfShape<D>;
+  __shared__ __align__(16) unsigned char vlds[kAttWaves][kMfChunk * S::ROW_B];
+#if SSA_ATT_KLDS
+  __shared__ __align__(16) unsigned char klds[kAttWaves][kMfChunk * S::ROW_B];
+#endif
+
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int q4 = lane >> 4;
+  const int c16 = lane & 15;
+  const AttRow ar = att_row(p, static_cast<int64_t>(blockIdx.x) * kAttWaves + wave);
+  const bool row_ok = ar.ok;
+  const int64_t i = ar.i;
+  const int64_t bh = ar.bh;
+  const int h = static_cast<int>(bh % p.h_kv);
+  const int64_t bb = bh / p.h_kv;
+
+  const uint16_t* qh = static_cast<const uint16_t*>(p.q) + bb * p.q_sb + i * p.q_sn +
+                       static_cast<int64_t>(h * p.g + (c16 < p.g ? c16 : 0)) * p.q_sh;
+  bf16x8_t qf[S::KB];
+#pragma unroll
+  for (int kb = 0; kb < S::KB; ++kb)
+    qf[kb] = (row_ok && c16 < p.g) ? *reinterpret_cast<const bf16x8_t*>(qh + kb * 32 + q4 * 8)
+                                   : bf16x8_t{};
+
+  const uint16_t* kbase = static_cast<const uint16_t*>(p.k) + bb * p.k_sb + static_cast<int64_t>(h) * p.k_sh;
+  const uint16_t* vbase = static_cast<const uint16_t*>(p.v) + bb * p.v_sb + static_cast<int64_t>(h) * p.v_sh;
+  const int64_t ibase = bb * p.idx_sb + i * p.idx_sn + static_cast<int64_t>(h) * p.idx_sh;
+  unsigned char* vs = vlds[wave];
+  const int vseg = lane % S::SEGS;
+  const int vkey0 = lane / S::SEGS;
+
+  auto load_idx = [&](int ch) -> int {
+    const int slot = ch * kMfChunk + lane;
+    if (!row_ok || lane >= kMfChunk || slot >= p.top_k) return -1;
+    const int64_t j = p.idx_i64 ? static_cast<const int64_t*>(p.idx)[ibase + slot]
+                                : static_cast<int64_t>(static_cast<const int32_t*>(p.idx)[ibase + slot]);
+    if (j < 0 || j >= p.n) {
+      if (p.err) p.err[0] = 1;
+      return -2;
+    }
+    return static_cast<int>(j);
+  };
+
+  const bool hi_row = c16 < p.g;
+  const bool lo_row = c16 >= 8 && c16 < 8 + p.g;
+  float m_run = -INFINITY;
+  float l_run = 0.0f;
+  floatx4_t oacc[S::NT];
+#pragma unroll
+  for (int t = 0; t < S::NT; ++t) oacc[t] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+
+  const int nchunks = (p.top_k + kMfChunk - 1) / kMfChunk;
+  int j_next = (nchunks > 0) ? load_idx(0) : -1;
+  for (int ch = 0; ch < nchunks; ++ch) {
+    const int j = j_next;
+    const bool ok = j >= 0 && !(p.causal && j > i);
+    const int jsafe = ok ? j : 0;
+    const uint64_t okbits = __ballot(ok);
+
+#if SSA_ATT_KLDS
+    // K rows staged like V (whole 128-byte lines per load), fragments read from LDS.
+    uint4 kv[S::NVI];
+#pragma unroll
+    for (int r = 0; r < S::NVI; ++r) {
+      const int kk = vkey0 + S::KPI * r;
+      const int jk = __shfl(jsafe, kk);
+      const bool okk = (okbits >> kk) & 1ull;
+      kv[r] = okk ? *reinterpret_cast<const uint4*>(kbase + static_cast<int64_t>(jk) * p.k_sn + vseg * 8)
+                  : make_uint4(0u, 0u, 0u, 0u);
+    }
+#else
+    // Gathers: K straight into the A fragments, V rows into registers.
+    bf16x8_t kf[2][S::KB];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int jt = __shfl(jsafe, 16 * t + c16);
+      const bool okt = (okbits >> (16 * t + c16)) & 1ull;
+      const uint16_t* kr = kbase + static_cast<int64_t>(jt) * p.k_sn + q4 * 8;
+#pragma unroll
+      for (int kb = 0; kb < S::KB; ++kb)
+#if SSA_ATT_NT
+        kf[t][kb] = okt ? __builtin_nontemporal_load(reinterpret_cast<const bf16x8_t*>(kr + kb * 32)) : bf16x8_t{};
+#else
+        kf[t][kb] = okt ? *reinterpret_cast<const bf16x8_t*>(kr + kb * 32) : bf16x8_t{};
+#endif
+    }
+#endif
+    uint4 vv[S::NVI];
+#pragma unroll
+    for (int r = 0; r < S::NVI; ++r) {
+      const int kk = vkey0 + S::KPI * r;
+      const int jv = __shfl(jsafe, kk);
+      const bool okv = (okbits >> kk) & 1ull;
+#if SSA_ATT_NT
+      typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+      vv[r] = okv ? __builtin_bit_cast(uint4, __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(vbase + static_cast<int64_t>(jv) * p.v_sn + vseg * 8)))
+                  : make_uint4(0u, 0u, 0u, 0u);
+#else
+      vv[r] = okv ? *reinterpret_cast<const uint4*>(vbase + static_cast<int64_t>(jv) * p.v_sn + vseg * 8)
+                  : make_uint4(0u, 0u, 0u, 0u);
+#endif
+    }
+    if (ch + 1 < nchunks) j_next = load_idx(ch + 1);
+
+#if SSA_ATT_KLDS
+    unsigned char* ks = klds[wave];
+#pragma unroll
+    for (int r = 0; r < S::NVI; ++r)
+      *reinterpret_cast<uint4*>(ks + (vkey0 + S::KPI * r) * S::ROW_B + vseg * 16) = kv[r];
+    wave_lds_sync();
+    bf16x8_t kf[2][S::KB];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int kb = 0; kb < S::KB; ++kb)
+        kf[t][kb] = *reinterpret_cast<const bf16x8_t*>(ks + (16 * t + c16) * S::ROW_B + (kb * 32 + q4 * 8) * 2);
+#endif
+    // Scores of eight keys of head c16 (keys 16t + 4*q4 + e).
+    float sc[8];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      floatx4_t s = {0.f, 0.f, 0.f, 0.f};
+      if ((okbits >> (16 * t)) & 0xFFFFull) {
+#pragma unroll
+        for (int kb = 0; kb < S::KB; ++kb) s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[t][kb], qf[kb], s, 0, 0, 0);
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int key = 16 * t + 4 * q4 + e;
+        sc[4 * t + e] = ((okbits >> key) & 1ull) ? s[e] * p.qk_scale_log2 : -INFINITY;
+      }
+    }
+    float mx = sc[0];
+#pragma unroll
+    for (int x = 1; x < 8; ++x) mx = fmaxf(mx, sc[x]);
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float mnew = fmaxf(m_run, mx);
+    const bool dead = (mnew == -INFINITY);
+    const float alpha = dead ? 1.0f : exp2f(m_run - mnew);
+    m_run = mnew;
+    float pr[8];
+    float ps = 0.0f;
+#pragma unroll
+    for (int x = 0; x < 8; ++x) {
+      pr[x] = dead ? 0.0f : exp2f(sc[x] - mnew);
+      ps += pr[x];
+    }
+    l_run = l_run * alpha + ps;
+
+    // P^T operand: rows c16 < g take P_hi of head c16, rows 8 + r take P_lo of head r.
+    uint32_t pb[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const uint32_t hi = pack_bf16x2(pr[2 * w], pr[2 * w + 1]);
+      const uint32_t lo = pack_bf16x2(pr[2 * w] - __uint_as_float(hi << 16),
+                                      pr[2 * w + 1] - __uint_as_float(hi & 0xFFFF0000u));
+      const uint32_t lo_in = dpp_from_minus8(lo);
+      pb[w] = hi_row ? hi : (lo_row ? lo_in : 0u);
+    }
+    // (cross-lane reads happen in every lane, before any lane-dependent select)
+    const float alpha_in = __uint_as_float(dpp_from_minus8(__float_as_uint(alpha)));
+    const float a_row = hi_row ? alpha : alpha_in;
+#pragma unroll
+    for (int t = 0; t < S::NT; ++t) oacc[t] *= a_row;
+
+    // Stage the chunk's V rows, then O^T += V^T . P^T.
+#pragma unroll
+    for (int r = 0; r < S::NVI; ++r)
+      *reinterpret_cast<uint4*>(vs + (vkey0 + S::KPI * r) * S::ROW_B + vseg * 16) = vv[r];
+    wave_lds_sync();
+    const bf16x8_t pbv = __builtin_bit_cast(bf16x8_t, make_uint4(pb[0], pb[1], pb[2], pb[3]));
+    const unsigned char* tr0 = vs + (4 * q4 + (c16 >> 2)) * S::ROW_B + (c16 & 3) * 8;
+    const unsigned char* tr1 = tr0 + 16 * S::ROW_B;
+#pragma unroll
+    for (int t = 0; t < S::NT; ++t) {
+      const v4i16_t a0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_ptr)(tr0 + t * 32));
+      const v4i16_t a1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_ptr)(tr1 + t * 32));
+      const bf16x8_t av = __builtin_bit_cast(
+          bf16x8_t, make_uint4(__builtin_bit_cast(uint2, a0).x, __builtin_bit_cast(uint2, a0).y,
+                               __builtin_bit_cast(uint2, a1).x, __builtin_bit_cast(uint2, a1).y));
+      oacc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, pbv, oacc[t], 0, 0, 0);
+    }
+    wave_lds_sync();
+  }
+
+  // l: partial sums of the four lanes holding a head's keys; O: hi row + lo row.
+  float lt = l_run + __shfl_xor(l_run, 16);
+  lt += __shfl_xor(lt, 32);
+#pragma unroll
+  for (int t = 0; t < S::NT; ++t)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) oacc[t][e] += dpp_from_plus8(oacc[t][e]);
+  if (!row_ok || !hi_row) return;
+  const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+  const int64_t ob = bb * p.o_sb + i * p.o_sn + static_cast<int64_t>(h * p.g + c16) * p.o_sh + 4 * q4;
+  if (p.out_bf16) {
+    uint16_t* dst = static_cast<uint16_t*>(p.out) + ob;
+#pragma unroll
+    for (int t = 0; t < S::NT; ++t)
+      *reinterpret_cast<uint2*>(dst + 16 * t) =
+          make_uint2(static_cast<uint32_t>(f32_to_bf16_rne(oacc[t][0] * inv)) |
+                         (static_cast<uint32_t>(f32_to_bf16_rne(oacc[t][1] * inv)) << 16),
+                     static_cast<uint32_t>(f32_to_bf16_rne(oacc[t][2] * inv)) |
+                         (static_cast<uint32_t>(f32_to_bf16_rne(oacc[t][3] * inv)) << 16));
+  } else {
+    float* dst = static_cast<float*>(p.out) + ob;
+#pragma unroll
+    for (int t = 0; t < S::NT; ++t)
+      *reinterpret_cast<float4*>(dst + 16 * t) =
+          make_float4(oacc[t][0] * inv, oacc[t][1] * inv, oacc[t][2] * inv, oacc[t][3] * inv);
+  }
+}
+
 template <typename T, int D>
 int launch_att_d(const AttParams& p, hipStream_t st) {
   const int64_t blocks = ceil_div(p.rows, kAttWaves);
+  if constexpr (sizeof(T) == 2 && D <= 128) {
+    if (p.g <= 8) {
+      sparse_attention_mfma_kernel<D><<<dim3(static_cast<unsigned>(blocks)), kAttThreads, 0, st>>>(p);
+      return check_launch("sparse_attention_mfma_kernel");
+    }
+  }
   if (p.g <= 4) sparse_attention_kernel<T, D, 4><<<dim3(static_cast<unsigned>(blocks)), kAttThreads, 0, st>>>(p);
   else if (p.g <= 8) sparse_attention_kernel<T, D, 8><<<dim3(static_cast<unsigned>(blocks)), kAttThreads, 0, st>>>(p);
   else sparse_attention_kernel<T, D, 16><<<dim3(static_cast<unsigned>(blocks)), kAttThreads, 0, st>>>(p);
@@ -410,7 +725,8 @@ extern "C" int ssa_sparse_attention(const void* q, const void* k, const void* v,
                                     int64_t k_sn, int64_t k_sh, int64_t v_sb, int64_t v_sn,
                                     int64_t v_sh, const void* idx, int idx_dtype, int top_k,
                                     int64_t idx_sb, int64_t idx_sn, int64_t idx_sh,
-                                    float scale_div, int causal, void* out, int out_dtype,
+                                    float scale_div, int causal, const int32_t* row_order,
+                                    void* out, int out_dtype,
                                     int64_t o_sb, int64_t o_sn, int64_t o_sh, int32_t* error_flag,
                                     void* stream) {
   if (dtype != SSA_DTYPE_F32 && dtype != SSA_DTYPE_BF16)
@@ -462,6 +778,7 @@ extern "C" int ssa_sparse_attention(const void* q, const void* k, const void* v,
   p.o_sb = o_sb; p.o_sn = o_sn; p.o_sh = o_sh;
   p.err = error_flag;
   p.rows = batch * h_kv * n;
+  p.order = row_order;
   if (ceil_div(p.rows, kAttWaves) >= (int64_t(1) << 31))
     return fail(SSA_ERR_UNSUPPORTED, "sparse_attention: too many rows");
   hipStream_t st = as_stream(stream);

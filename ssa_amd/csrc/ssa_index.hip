@@ -7,9 +7,9 @@
 //
 // Three kernels per (batch, kv-head) pair "bh", keys cut into tiles of
 // `tile_keys` keys (tile_keys*b entries):
-//   1. index_hist    : per-tile LDS histogram of codes -> hist[bh][c][tile]
+//   1. index_hist    : per-tile LDS histogram of codes -> hist[bh][tile][c]
 //   2. index_scan    : exclusive scan of hist in (code, tile) order -> base
-//                      positions; offsets[bh][c] = base[c][0]
+//                      positions; offsets[bh][c] = base of (c, tile 0)
 //   3. index_scatter : one wave per tile walks its entries in order; lanes that
 //                      share a code rank themselves by ballot (lowest lane =
 //                      lowest key first) and advance an LDS cursor per code.
@@ -44,43 +44,57 @@ __global__ __launch_bounds__(kHistThreads) void index_hist_kernel(
     if (static_cast<uint32_t>(c) < static_cast<uint32_t>(n_c)) atomicAdd(&lds_hist[c], 1);
   }
   __syncthreads();
-  int32_t* hb = hist + bh * static_cast<int64_t>(n_c) * tiles;
-  for (int c = threadIdx.x; c < n_c; c += kHistThreads) hb[static_cast<int64_t>(c) * tiles + tile] = lds_hist[c];
+  int32_t* hb = hist + (bh * tiles + tile) * static_cast<int64_t>(n_c);
+  for (int c = threadIdx.x; c < n_c; c += kHistThreads) hb[c] = lds_hist[c];
 }
 
-// Exclusive scan over hist[bh][0 .. n_c*tiles) in place; writes offsets.
+// Bucket base positions, in place: hist[bh][tile][c] (keys of code c in tile)
+// becomes the number of entries before them in (code, tile) order, i.e. where
+// tile `tile` starts writing bucket c; offsets[bh][c] = start of bucket c.  One
+// block per bh, one code per thread per round of kScanThreads codes (coalesced
+// over codes), with a running carry across rounds.
 __global__ __launch_bounds__(kScanThreads) void index_scan_kernel(int32_t* __restrict__ hist,
                                                                   int n_c, int64_t tiles,
                                                                   int32_t* __restrict__ offsets) {
-  __shared__ int32_t part[kScanThreads];
+  __shared__ int32_t wsum[kScanThreads / 64];
   const int64_t bh = blockIdx.x;
-  const int64_t total = static_cast<int64_t>(n_c) * tiles;
-  int32_t* hb = hist + bh * total;
-  const int64_t per = ceil_div(total, kScanThreads);
-  const int64_t s0 = threadIdx.x * per;
-  int64_t s1 = s0 + per;
-  if (s1 > total) s1 = total;
-  int32_t local = 0;
-  for (int64_t e = s0; e < s1; ++e) local += hb[e];
-  part[threadIdx.x] = local;
-  __syncthreads();
-  // Hillis-Steele inclusive scan of the per-thread sums.
-  for (int off = 1; off < kScanThreads; off <<= 1) {
-    const int32_t v = (static_cast<int>(threadIdx.x) >= off) ? part[threadIdx.x - off] : 0;
-    __syncthreads();
-    part[threadIdx.x] += v;
-    __syncthreads();
-  }
-  int32_t run = part[threadIdx.x] - local;
-  for (int64_t e = s0; e < s1; ++e) {
-    const int32_t v = hb[e];
-    hb[e] = run;
-    run += v;
-  }
-  __syncthreads();
+  int32_t* hb = hist + bh * tiles * static_cast<int64_t>(n_c);
   int32_t* ob = offsets + bh * (n_c + 1);
-  for (int c = threadIdx.x; c < n_c; c += kScanThreads) ob[c] = hb[static_cast<int64_t>(c) * tiles];
-  if (threadIdx.x == kScanThreads - 1) ob[n_c] = part[kScanThreads - 1];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  int32_t carry = 0;
+  for (int c0 = 0; c0 < n_c; c0 += kScanThreads) {
+    const int c = c0 + static_cast<int>(threadIdx.x);
+    int32_t tot = 0;
+    if (c < n_c)
+      for (int64_t t = 0; t < tiles; ++t) tot += hb[t * n_c + c];
+    int32_t x = tot;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int32_t y = __shfl_up(x, off, 64);
+      if (lane >= off) x += y;
+    }
+    if (lane == 63) wsum[wave] = x;
+    __syncthreads();
+    int32_t before = carry, round = 0;
+    for (int w = 0; w < kScanThreads / 64; ++w) {
+      const int32_t v = wsum[w];
+      if (w < wave) before += v;
+      round += v;
+    }
+    __syncthreads();  // wsum is rewritten next round
+    if (c < n_c) {
+      int32_t run = before + x - tot;
+      ob[c] = run;
+      for (int64_t t = 0; t < tiles; ++t) {
+        const int32_t v = hb[t * n_c + c];
+        hb[t * n_c + c] = run;
+        run += v;
+      }
+    }
+    carry += round;
+  }
+  if (threadIdx.x == 0) ob[n_c] = carry;
 }
 
 // One wave per (tile, bh).  Entries are visited in index order e = j*b + r, 64
@@ -94,8 +108,8 @@ __global__ __launch_bounds__(64) void index_scatter_kernel(
   const int64_t tile = blockIdx.x;
   const int64_t bh = blockIdx.y;
   const int lane = threadIdx.x;
-  const int32_t* bb = base + bh * static_cast<int64_t>(n_c) * tiles;
-  for (int c = lane; c < n_c; c += 64) cursor[c] = bb[static_cast<int64_t>(c) * tiles + tile];
+  const int32_t* bb = base + (bh * tiles + tile) * static_cast<int64_t>(n_c);
+  for (int c = lane; c < n_c; c += 64) cursor[c] = bb[c];
   __syncthreads();
   const int64_t e0 = tile * tile_keys * b;
   int64_t e1 = (tile + 1) * tile_keys * b;

@@ -160,8 +160,12 @@ def select(q: torch.Tensor, k: torch.Tensor, q_codes: torch.Tensor, offsets: tor
 def sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, idx: torch.Tensor,
                      scale_div: Optional[float] = None, causal: bool = False,
                      out: Optional[torch.Tensor] = None,
-                     error_flag: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """Stage (d): gathered exact attention, [B, n, h_q, d] in q's dtype (ssa/attention.py:12-115)."""
+                     error_flag: Optional[torch.Tensor] = None,
+                     row_order: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Stage (d): gathered exact attention, [B, n, h_q, d] in q's dtype (ssa/attention.py:12-115).
+
+    ``row_order`` (int32 [B, h_kv, n], a permutation of 0..n-1 per head) only sets
+    the order in which rows are processed; results are the same."""
     for name, t in (("q", q), ("k", k), ("v", v), ("indices", idx)):
         _check_rows(t, name)
     _lib.require_device(q, k, v, idx)
@@ -174,10 +178,15 @@ def sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, idx: tor
         scale_div = math.sqrt(d)
     if out is None:
         out = torch.empty((B, n, h_q, d), device=q.device, dtype=q.dtype)
+    if row_order is not None:
+        _lib.require_device(row_order)
+        if row_order.dtype != torch.int32 or tuple(row_order.shape) != (B, h_kv, n):
+            raise ValueError(f"row_order must be int32 [{B}, {h_kv}, {n}]")
+        row_order = row_order.contiguous()
     call("ssa_sparse_attention", ptr(q), ptr(k), ptr(v), _lib.elem_dtype(q), B, n, h_q, h_kv, d,
          q.stride(0), q.stride(1), q.stride(2), k.stride(0), k.stride(1), k.stride(2),
          v.stride(0), v.stride(1), v.stride(2), ptr(idx), _lib.index_dtype(idx), top_k,
          idx.stride(0), idx.stride(1), idx.stride(2), float(scale_div), int(bool(causal)),
-         ptr(out), _lib.elem_dtype(out), out.stride(0), out.stride(1), out.stride(2),
+         ptr(row_order), ptr(out), _lib.elem_dtype(out), out.stride(0), out.stride(1), out.stride(2),
          ptr(error_flag), stream_of(q))
     return out

@@ -120,8 +120,13 @@ class CodebookRouter(nn.Module):
 
     def route(self, q_full: torch.Tensor, k_full: torch.Tensor, causal_mask: MaskArg = None,
               hard: bool = True, with_stats: bool = False, index_dtype=torch.int64,
-              sorted: bool = True):
-        """Run stages (a)-(c) and keep the intermediates (a RouteResult)."""
+              sorted: bool = True, with_order: bool = False):
+        """Run stages (a)-(c) and keep the intermediates (a RouteResult).
+
+        ``with_order`` also returns ``order`` (int32 [B, h_kv, n]): per head, the
+        query positions grouped by their best code (ascending within a code).
+        Processing rows in this order lets rows that share candidate keys run
+        together; it changes no result."""
         if not hard:
             raise NotImplementedError(
                 "hard=False (Gumbel-softmax assignment) is not supported: the reference's one-hot "
@@ -150,6 +155,8 @@ class CodebookRouter(nn.Module):
                              sorted=sorted)
         idx, stats = res if with_stats else (res, None)
         out = RouteResult(q_codes, k_codes, offsets, postings, idx, stats)
+        if with_order:
+            out.order = query_order(q_codes, self.num_codebook)
         out.indices_view = idx[0] if unbatched else idx
         return out
 
@@ -166,15 +173,25 @@ class CodebookRouter(nn.Module):
         return out[0] if unbatched else out
 
 
+def query_order(q_codes: torch.Tensor, num_codebook: int) -> torch.Tensor:
+    """Query positions per (batch, kv head) grouped by their best code: the
+    inverted index of each query's first code, int32 [B, h_kv, n]."""
+    B, h, n, _ = q_codes.shape
+    _, post = kernels.build_index(q_codes[..., :1].contiguous(), num_codebook)
+    return post.view(B, h, n)
+
+
 class RouteResult:
     """Intermediates of one routing pass, in kernel layouts (batched):
     q_codes int32 [B, h_kv, n, a], k_codes int32 [B, h_kv, n, b],
     offsets int32 [B, h_kv, N_c + 1], postings int32 [B, h_kv, n * b],
     indices [B, n, h_kv, top_k], stats int32 [B, h_kv, n, 2] or None
-    (unique candidates, postings read); indices_view is the reference-shaped
-    view returned by forward()."""
+    (unique candidates, postings read), order int32 [B, h_kv, n] or None (see
+    query_order); indices_view is the reference-shaped view returned by
+    forward()."""
 
-    __slots__ = ("q_codes", "k_codes", "offsets", "postings", "indices", "stats", "indices_view")
+    __slots__ = ("q_codes", "k_codes", "offsets", "postings", "indices", "stats", "order",
+                 "indices_view")
 
     def __init__(self, q_codes, k_codes, offsets, postings, indices, stats):
         self.q_codes = q_codes
@@ -183,4 +200,5 @@ class RouteResult:
         self.postings = postings
         self.indices = indices
         self.stats = stats
+        self.order = None
         self.indices_view = indices

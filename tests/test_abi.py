@@ -127,7 +127,8 @@ def _attention(L, **kw):
              d=128, q_sb=1024 * 32 * 128, q_sn=32 * 128, q_sh=128, k_sb=1024 * 8 * 128,
              k_sn=8 * 128, k_sh=128, v_sb=1024 * 8 * 128, v_sn=8 * 128, v_sh=128, idx=FAKE,
              idx_dtype=_lib.INDEX_I64, top_k=512, idx_sb=1024 * 8 * 512, idx_sn=8 * 512,
-             idx_sh=512, scale_div=11.3137, causal=1, out=FAKE, out_dtype=_lib.DTYPE_BF16,
+             idx_sh=512, scale_div=11.3137, causal=1, row_order=NULL, out=FAKE,
+             out_dtype=_lib.DTYPE_BF16,
              o_sb=1024 * 32 * 128, o_sn=32 * 128, o_sh=128, error_flag=NULL, stream=NULL)
     a.update(kw)
     st = L.ssa_sparse_attention(*a.values())

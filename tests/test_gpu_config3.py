@@ -20,6 +20,7 @@ pytestmark = pytest.mark.gpu
 @pytest.fixture(scope="module")
 def c3(dev):
     from ssa_amd import kernels
+    from ssa_amd.router import query_order
 
     print("config3: generating workload", flush=True)
     cfg = dict(bench.CONFIGS["c3"])
@@ -33,10 +34,25 @@ def c3(dev):
     idx_s2 = kernels.select(q, k, qc, off, post, cfg["b"], cfg["k"], sorted=True)
     out = torch.empty(q.shape, device=dev, dtype=torch.float32)
     kernels.sparse_attention(q, k, v, idx_u, None, True, out=out)
+    order = query_order(qc, cfg["n_c"])
+    out_ord = torch.empty_like(out)
+    kernels.sparse_attention(q, k, v, idx_u, None, True, out=out_ord, row_order=order)
     torch.cuda.synchronize()
     print("config3: GPU pipeline done", flush=True)
     return dict(cfg=cfg, q=q, k=k, v=v, router=router, qc=qc, kc=kc, off=off, post=post,
-                idx_s=idx_s, idx_u=idx_u, idx_s2=idx_s2, idx_u2=idx_u2, stats=st, out=out)
+                idx_s=idx_s, idx_u=idx_u, idx_s2=idx_s2, idx_u2=idx_u2, stats=st, out=out,
+                order=order, out_ord=out_ord)
+
+
+def test_c3_row_order_changes_nothing(c3):
+    """Processing rows grouped by code gives bit-identical outputs; the order is
+    a permutation of the positions of every (batch, kv head)."""
+    order = c3["order"][0].to(torch.int64)
+    n = c3["cfg"]["n"]
+    assert torch.equal(order.sort(-1).values, torch.arange(n, device=order.device).expand_as(order))
+    first = c3["qc"][0][:, :, 0].gather(1, order)        # best code along the order
+    assert bool((first[:, 1:] >= first[:, :-1]).all()), "order groups rows by ascending code"
+    assert torch.equal(c3["out"], c3["out_ord"])
 
 
 def test_c3_select_deterministic(c3):
