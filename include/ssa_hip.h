@@ -146,7 +146,7 @@ int ssa_select(const void* q, const void* k, int dtype, int64_t batch, int64_t n
  *   written, and an entry outside [0, n) is skipped and sets *error_flag.
  *   idx [batch][n][h_kv][top_k] strides (idx_sb, idx_sn, idx_sh)
  *   out [batch][n][h_q][d] strides (o_sb, o_sn, o_sh), type out_dtype
- * Limits: d in {64, 128, 256}, g <= 16. */
+ * Limits: d a multiple of 8 in [8, 256], g <= 16. */
 int ssa_sparse_attention(const void* q, const void* k, const void* v, int dtype, int64_t batch,
                          int64_t n, int h_q, int h_kv, int d, int64_t q_sb, int64_t q_sn,
                          int64_t q_sh, int64_t k_sb, int64_t k_sn, int64_t k_sh, int64_t v_sb,

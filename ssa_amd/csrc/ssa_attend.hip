@@ -2,14 +2,14 @@
 // ssa/attention.py:12-115).
 //
 // One wave per (batch, kv head h, query i); the g = h_q/h_kv query heads of
-// the group share the row's k gathered keys.  Keys stream in chunks of 64:
-//   * Q.K^T on the matrix cores: A = the group's q rows (heads padded to 16),
-//     B = 16 gathered K rows per MFMA, loaded straight from HBM into the B
-//     fragment (each lane reads 16 contiguous bytes of one K row);
-//   * online softmax in the exp2 domain (running max / sum per head);
-//   * P.V on the vector ALUs: each lane owns d/16 feature columns of a quarter
-//     of the chunk's keys, so one wave-wide load moves four whole V rows; the
-//     chunk's probabilities are broadcast from LDS.
+// the group share the row's k gathered keys, which stream in chunks of 32 with
+// an online softmax in the exp2 domain.  Two kernels:
+//   * sparse_attention_mfma_kernel (bf16, g <= 8, d in {64, 128}): Q.K^T and
+//     P.V both on the matrix cores (see the comment at the kernel);
+//   * sparse_attention_kernel (fp32 inputs, g up to 16, any head dim that is a
+//     multiple of 8 up to 256, padded to 32/64/128/256): Q.K^T on the matrix
+//     cores, P.V on the vector ALUs in fp32 (each lane owns d/16 feature
+//     columns of a quarter of the chunk's keys; P is broadcast from LDS).
 // `scale_div` is the reference's `scale` (a divisor).  Duplicated indices count
 // twice, as in the reference.
 #include "ssa_common.h"
@@ -42,6 +42,7 @@ struct AttParams {
   const void* v;
   int64_t n;
   int h_q, h_kv, g;
+  int d;  // head dim (<= the kernel's padded width D; dims >= d read as zero)
   int64_t q_sb, q_sn, q_sh, k_sb, k_sn, k_sh, v_sb, v_sn, v_sh;
   const void* idx;
   int idx_i64, top_k;
@@ -67,16 +68,10 @@ __device__ __forceinline__ AttRow att_row(const AttParams& p, int64_t lrow) {
   AttRow r;
   r.ok = lrow < p.rows;
   const int64_t l = r.ok ? lrow : 0;
-#if SSA_ATT_HMINOR
-  const int64_t nbh = p.rows / p.n;
-  r.bh = l % nbh;
-  r.i = l / nbh;
-#else
   r.bh = l / p.n;
   r.i = l - r.bh * p.n;
-#endif
   if (p.order) {
-    const int64_t o = p.order[r.bh * p.n + r.i];
+    const int64_t o = p.order[l];
     if (o < 0 || o >= p.n) {
       if (r.ok && p.err) p.err[0] = 1;
       r.ok = false;
@@ -121,19 +116,20 @@ template <int D>
 struct QkFrag<uint16_t, D> {
   static constexpr int KB = D / 32;
   bf16x8_t a[KB];
-  __device__ void load_q(const uint16_t* qh, bool ok, int q4) {
+  __device__ void load_q(const uint16_t* qh, bool ok, int q4, int d) {
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
-      if (ok) a[kb] = *reinterpret_cast<const bf16x8_t*>(qh + kb * 32 + q4 * 8);
+      if (ok && kb * 32 + q4 * 8 < d) a[kb] = *reinterpret_cast<const bf16x8_t*>(qh + kb * 32 + q4 * 8);
       else a[kb] = bf16x8_t{};
     }
   }
   struct BFrag {
     bf16x8_t v[KB];
   };
-  __device__ void load_k(BFrag& f, const uint16_t* kr, int q4) const {
+  __device__ void load_k(BFrag& f, const uint16_t* kr, int q4, int d) const {
 #pragma unroll
-    for (int kb = 0; kb < KB; ++kb) f.v[kb] = *reinterpret_cast<const bf16x8_t*>(kr + kb * 32 + q4 * 8);
+    for (int kb = 0; kb < KB; ++kb)
+      f.v[kb] = (kb * 32 + q4 * 8 < d) ? *reinterpret_cast<const bf16x8_t*>(kr + kb * 32 + q4 * 8) : bf16x8_t{};
   }
   __device__ floatx4_t dot(const BFrag& f, int q4) const {
     (void)q4;
@@ -148,19 +144,21 @@ template <int D>
 struct QkFrag<float, D> {
   static constexpr int KB = D / 16;
   float4 a[KB];
-  __device__ void load_q(const float* qh, bool ok, int q4) {
+  __device__ void load_q(const float* qh, bool ok, int q4, int d) {
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
-      if (ok) a[kb] = *reinterpret_cast<const float4*>(qh + kb * 16 + q4 * 4);
+      if (ok && kb * 16 + q4 * 4 < d) a[kb] = *reinterpret_cast<const float4*>(qh + kb * 16 + q4 * 4);
       else a[kb] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
   }
   struct BFrag {
     float4 v[KB];
   };
-  __device__ void load_k(BFrag& f, const float* kr, int q4) const {
+  __device__ void load_k(BFrag& f, const float* kr, int q4, int d) const {
 #pragma unroll
-    for (int kb = 0; kb < KB; ++kb) f.v[kb] = *reinterpret_cast<const float4*>(kr + kb * 16 + q4 * 4);
+    for (int kb = 0; kb < KB; ++kb)
+      f.v[kb] = (kb * 16 + q4 * 4 < d) ? *reinterpret_cast<const float4*>(kr + kb * 16 + q4 * 4)
+                                       : make_float4(0.f, 0.f, 0.f, 0.f);
   }
   __device__ floatx4_t dot(const BFrag& f, int q4) const {
     (void)q4;
@@ -182,16 +180,28 @@ struct VSlice {
   static constexpr int BYTES = DQ * static_cast<int>(sizeof(T));
   static constexpr int WORDS = BYTES / 4;
   uint32_t w[WORDS];
-  __device__ __forceinline__ void load(const T* ptr) {
+  // Only the first `nvalid` features exist (the head dim ends inside or before
+  // this slice); the rest read as zero.  The head dim is a multiple of 8, so
+  // each 16-byte piece is wholly inside or wholly outside it.
+  __device__ __forceinline__ void load(const T* ptr, int nvalid) {
+    if (nvalid <= 0) {
+#pragma unroll
+      for (int i = 0; i < WORDS; ++i) w[i] = 0u;
+      return;
+    }
     if constexpr (BYTES % 16 == 0) {
+      constexpr int PE = 16 / static_cast<int>(sizeof(T));  // features per piece
 #pragma unroll
       for (int i = 0; i < BYTES / 16; ++i) {
-        const uint4 u = reinterpret_cast<const uint4*>(ptr)[i];
+        const uint4 u = (i * PE < nvalid) ? reinterpret_cast<const uint4*>(ptr)[i] : make_uint4(0u, 0u, 0u, 0u);
         w[4 * i] = u.x; w[4 * i + 1] = u.y; w[4 * i + 2] = u.z; w[4 * i + 3] = u.w;
       }
-    } else {
+    } else if constexpr (BYTES == 8) {
       const uint2 u = *reinterpret_cast<const uint2*>(ptr);
       w[0] = u.x; w[1] = u.y;
+    } else {
+      static_assert(BYTES == 4, "V slices are 4, 8 or a multiple of 16 bytes");
+      w[0] = *reinterpret_cast<const uint32_t*>(ptr);
     }
   }
   __device__ __forceinline__ float at(int e) const {
@@ -244,7 +254,8 @@ __global__ __launch_bounds__(kAttThreads, (AttMinBlocks<T, D, GMAX>::value)) voi
   const T* qh = static_cast<const T*>(p.q) + bb * p.q_sb + i * p.q_sn +
                 static_cast<int64_t>(h * p.g + (c16 < p.g ? c16 : 0)) * p.q_sh;
   QkFrag<T, D> frag;
-  frag.load_q(qh, row_ok && c16 < p.g, q4);
+  frag.load_q(qh, row_ok && c16 < p.g, q4, p.d);
+  const int vvalid = p.d - c16 * DQ;  // features of this lane's V / output slice that exist
 
   const T* kbase = static_cast<const T*>(p.k) + bb * p.k_sb + static_cast<int64_t>(h) * p.k_sh;
   const T* vbase = static_cast<const T*>(p.v) + bb * p.v_sb + static_cast<int64_t>(h) * p.v_sh + c16 * DQ;
@@ -289,13 +300,13 @@ __global__ __launch_bounds__(kAttThreads, (AttMinBlocks<T, D, GMAX>::value)) voi
 #pragma unroll
     for (int tile = 0; tile < kTiles; ++tile) {
       const int jt = __shfl(jsafe, tile * 16 + c16);
-      if ((okbits >> (tile * 16)) & 0xFFFFull) frag.load_k(kf[tile], kbase + static_cast<int64_t>(jt) * p.k_sn, q4);
+      if ((okbits >> (tile * 16)) & 0xFFFFull) frag.load_k(kf[tile], kbase + static_cast<int64_t>(jt) * p.k_sn, q4, p.d);
     }
     VS vv[KPB];
 #pragma unroll
     for (int r = 0; r < KPB; ++r) {
       const int jv = __shfl(jsafe, 4 * r + q4);
-      vv[r].load(vbase + static_cast<int64_t>(jv) * p.v_sn);
+      vv[r].load(vbase + static_cast<int64_t>(jv) * p.v_sn, vvalid);
     }
     if (ch + 1 < nchunks) j_next = load_idx(ch + 1);
 
@@ -345,7 +356,7 @@ __global__ __launch_bounds__(kAttThreads, (AttMinBlocks<T, D, GMAX>::value)) voi
 #pragma unroll
         for (int r = 0; r < KPB; ++r) {
           const int jv = __shfl(jsafe, 4 * (b0 + r) + q4);
-          vv[r].load(vbase + static_cast<int64_t>(jv) * p.v_sn);
+          vv[r].load(vbase + static_cast<int64_t>(jv) * p.v_sn, vvalid);
         }
       }
 #pragma unroll
@@ -385,7 +396,7 @@ __global__ __launch_bounds__(kAttThreads, (AttMinBlocks<T, D, GMAX>::value)) voi
   // Each lane stores DQ contiguous outputs with vector stores (DQ*2 or DQ*4 bytes).
 #pragma unroll
   for (int gg = 0; gg < GMAX; ++gg) {
-    if ((gg & 3) != q4 || gg >= p.g) continue;
+    if ((gg & 3) != q4 || gg >= p.g || vvalid <= 0) continue;
     const float ls = lsum_s[wave][gg];
     const float inv = ls > 0.0f ? 1.0f / ls : 0.0f;
     const int64_t ob = bb * p.o_sb + i * p.o_sn + static_cast<int64_t>(h * p.g + gg) * p.o_sh + c16 * DQ;
@@ -399,16 +410,24 @@ __global__ __launch_bounds__(kAttThreads, (AttMinBlocks<T, D, GMAX>::value)) voi
       if constexpr (DQ % 8 == 0) {
 #pragma unroll
         for (int e = 0; e < DQ / 8; ++e)
-          reinterpret_cast<uint4*>(dst)[e] = make_uint4(packed[4 * e], packed[4 * e + 1], packed[4 * e + 2], packed[4 * e + 3]);
-      } else {
+          if (e * 8 < vvalid)
+            reinterpret_cast<uint4*>(dst)[e] = make_uint4(packed[4 * e], packed[4 * e + 1], packed[4 * e + 2], packed[4 * e + 3]);
+      } else if constexpr (DQ == 4) {
         reinterpret_cast<uint2*>(dst)[0] = make_uint2(packed[0], packed[1]);
+      } else {
+        reinterpret_cast<uint32_t*>(dst)[0] = packed[0];
       }
     } else {
       float* dst = static_cast<float*>(p.out) + ob;
+      if constexpr (DQ % 4 == 0) {
 #pragma unroll
-      for (int e = 0; e < DQ / 4; ++e)
-        reinterpret_cast<float4*>(dst)[e] = make_float4(oacc[gg][4 * e] * inv, oacc[gg][4 * e + 1] * inv,
-                                                        oacc[gg][4 * e + 2] * inv, oacc[gg][4 * e + 3] * inv);
+        for (int e = 0; e < DQ / 4; ++e)
+          if (e * 4 < vvalid)
+            reinterpret_cast<float4*>(dst)[e] = make_float4(oacc[gg][4 * e] * inv, oacc[gg][4 * e + 1] * inv,
+                                                            oacc[gg][4 * e + 2] * inv, oacc[gg][4 * e + 3] * inv);
+      } else {
+        reinterpret_cast<float2*>(dst)[0] = make_float2(oacc[gg][0] * inv, oacc[gg][1] * inv);
+      }
     }
   }
 }
@@ -436,15 +455,6 @@ typedef short v4i16_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4i16_t* lds_v4i16_ptr;
 
 constexpr int kMfChunk = 32;
-#ifndef SSA_ATT_KLDS
-#define SSA_ATT_KLDS 0
-#endif
-#ifndef SSA_ATT_NT
-#define SSA_ATT_NT 0
-#endif
-#ifndef SSA_ATT_HMINOR
-#define SSA_ATT_HMINOR 0
-#endif
 
 template <int D>
 struct MfShape {
@@ -471,15 +481,9 @@ __device__ __forceinline__ float dpp_from_plus8(float x) {
 }
 
 template <int D>
-#ifndef SSA_ATT_MINW
-#define SSA_ATT_MINW 2
-#endif
-__global__ __launch_bounds__(kAttThreads, SSA_ATT_MINW) void sparse_attention_mfma_kernel(AttParams p) {
+__global__ __launch_bounds__(kAttThreads, 2) void sparse_attention_mfma_kernel(AttParams p) {
   using S = MfShape<D>;
   __shared__ __align__(16) unsigned char vlds[kAttWaves][kMfChunk * S::ROW_B];
-#if SSA_ATT_KLDS
-  __shared__ __align__(16) unsigned char klds[kAttWaves][kMfChunk * S::ROW_B];
-#endif
 
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -535,18 +539,6 @@ __global__ __launch_bounds__(kAttThreads, SSA_ATT_MINW) void sparse_attention_mf
     const int jsafe = ok ? j : 0;
     const uint64_t okbits = __ballot(ok);
 
-#if SSA_ATT_KLDS
-    // K rows staged like V (whole 128-byte lines per load), fragments read from LDS.
-    uint4 kv[S::NVI];
-#pragma unroll
-    for (int r = 0; r < S::NVI; ++r) {
-      const int kk = vkey0 + S::KPI * r;
-      const int jk = __shfl(jsafe, kk);
-      const bool okk = (okbits >> kk) & 1ull;
-      kv[r] = okk ? *reinterpret_cast<const uint4*>(kbase + static_cast<int64_t>(jk) * p.k_sn + vseg * 8)
-                  : make_uint4(0u, 0u, 0u, 0u);
-    }
-#else
     // Gathers: K straight into the A fragments, V rows into registers.
     bf16x8_t kf[2][S::KB];
 #pragma unroll
@@ -556,43 +548,19 @@ __global__ __launch_bounds__(kAttThreads, SSA_ATT_MINW) void sparse_attention_mf
       const uint16_t* kr = kbase + static_cast<int64_t>(jt) * p.k_sn + q4 * 8;
 #pragma unroll
       for (int kb = 0; kb < S::KB; ++kb)
-#if SSA_ATT_NT
-        kf[t][kb] = okt ? __builtin_nontemporal_load(reinterpret_cast<const bf16x8_t*>(kr + kb * 32)) : bf16x8_t{};
-#else
         kf[t][kb] = okt ? *reinterpret_cast<const bf16x8_t*>(kr + kb * 32) : bf16x8_t{};
-#endif
     }
-#endif
     uint4 vv[S::NVI];
 #pragma unroll
     for (int r = 0; r < S::NVI; ++r) {
       const int kk = vkey0 + S::KPI * r;
       const int jv = __shfl(jsafe, kk);
       const bool okv = (okbits >> kk) & 1ull;
-#if SSA_ATT_NT
-      typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
-      vv[r] = okv ? __builtin_bit_cast(uint4, __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(vbase + static_cast<int64_t>(jv) * p.v_sn + vseg * 8)))
-                  : make_uint4(0u, 0u, 0u, 0u);
-#else
       vv[r] = okv ? *reinterpret_cast<const uint4*>(vbase + static_cast<int64_t>(jv) * p.v_sn + vseg * 8)
                   : make_uint4(0u, 0u, 0u, 0u);
-#endif
     }
     if (ch + 1 < nchunks) j_next = load_idx(ch + 1);
 
-#if SSA_ATT_KLDS
-    unsigned char* ks = klds[wave];
-#pragma unroll
-    for (int r = 0; r < S::NVI; ++r)
-      *reinterpret_cast<uint4*>(ks + (vkey0 + S::KPI * r) * S::ROW_B + vseg * 16) = kv[r];
-    wave_lds_sync();
-    bf16x8_t kf[2][S::KB];
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int kb = 0; kb < S::KB; ++kb)
-        kf[t][kb] = *reinterpret_cast<const bf16x8_t*>(ks + (16 * t + c16) * S::ROW_B + (kb * 32 + q4 * 8) * 2);
-#endif
     // Scores of eight keys of head c16 (keys 16t + 4*q4 + e).
     float sc[8];
 #pragma unroll
@@ -693,8 +661,8 @@ __global__ __launch_bounds__(kAttThreads, SSA_ATT_MINW) void sparse_attention_mf
 template <typename T, int D>
 int launch_att_d(const AttParams& p, hipStream_t st) {
   const int64_t blocks = ceil_div(p.rows, kAttWaves);
-  if constexpr (sizeof(T) == 2 && D <= 128) {
-    if (p.g <= 8) {
+  if constexpr (sizeof(T) == 2 && D >= 64 && D <= 128) {
+    if (p.g <= 8 && p.d == D) {
       sparse_attention_mfma_kernel<D><<<dim3(static_cast<unsigned>(blocks)), kAttThreads, 0, st>>>(p);
       return check_launch("sparse_attention_mfma_kernel");
     }
@@ -707,11 +675,11 @@ int launch_att_d(const AttParams& p, hipStream_t st) {
 
 template <typename T>
 int launch_att(const AttParams& p, int d, hipStream_t st) {
-  switch (d) {
-    case 64: return launch_att_d<T, 64>(p, st);
-    case 128: return launch_att_d<T, 128>(p, st);
-    default: return launch_att_d<T, 256>(p, st);
-  }
+  // Padded width: the smallest of 32, 64, 128, 256 that holds d.
+  if (d <= 32) return launch_att_d<T, 32>(p, st);
+  if (d <= 64) return launch_att_d<T, 64>(p, st);
+  if (d <= 128) return launch_att_d<T, 128>(p, st);
+  return launch_att_d<T, 256>(p, st);
 }
 
 }  // namespace
@@ -741,8 +709,8 @@ extern "C" int ssa_sparse_attention(const void* q, const void* k, const void* v,
     return fail(SSA_ERR_INVALID_ARGUMENT, "num_q_heads must be divisible by num_kv_heads");
   if (h_q / h_kv > 16)
     return fail(SSA_ERR_UNSUPPORTED, "sparse_attention: group size %d > 16", h_q / h_kv);
-  if (d != 64 && d != 128 && d != 256)
-    return fail(SSA_ERR_UNSUPPORTED, "sparse_attention: head_dim %d not in {64, 128, 256}", d);
+  if (d < 8 || d > 256 || d % 8 != 0)
+    return fail(SSA_ERR_UNSUPPORTED, "sparse_attention: head_dim %d (need a multiple of 8 in [8, 256])", d);
   if (!(scale_div > 0.0f) && !(scale_div < 0.0f))
     return fail(SSA_ERR_INVALID_ARGUMENT, "sparse_attention: scale must be non-zero");
   const int vec = (dtype == SSA_DTYPE_BF16) ? 8 : 4;
@@ -764,6 +732,7 @@ extern "C" int ssa_sparse_attention(const void* q, const void* k, const void* v,
   p.h_q = h_q;
   p.h_kv = h_kv;
   p.g = h_q / h_kv;
+  p.d = d;
   p.q_sb = q_sb; p.q_sn = q_sn; p.q_sh = q_sh;
   p.k_sb = k_sb; p.k_sn = k_sn; p.k_sh = k_sh;
   p.v_sb = v_sb; p.v_sn = v_sn; p.v_sh = v_sh;

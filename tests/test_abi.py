@@ -141,7 +141,8 @@ def _attention(L, **kw):
     (dict(idx_dtype=3), _lib.SSA_ERR_INVALID_ARGUMENT, "idx dtype"),
     (dict(h_kv=7), _lib.SSA_ERR_INVALID_ARGUMENT, "divisible"),
     (dict(h_q=8 * 32), _lib.SSA_ERR_UNSUPPORTED, "group size"),
-    (dict(d=96), _lib.SSA_ERR_UNSUPPORTED, "head_dim"),
+    (dict(d=260), _lib.SSA_ERR_UNSUPPORTED, "head_dim"),
+    (dict(d=20), _lib.SSA_ERR_UNSUPPORTED, "head_dim"),
     (dict(scale_div=0.0), _lib.SSA_ERR_INVALID_ARGUMENT, "scale"),
     (dict(v=MISALIGNED), _lib.SSA_ERR_UNSUPPORTED, "aligned"),
     (dict(o_sn=32 * 128 + 2), _lib.SSA_ERR_UNSUPPORTED, "output"),

@@ -164,7 +164,11 @@ def test_select_k_edges(dev, orc, top_k, sorted_):
 
 @pytest.mark.parametrize("dtype,d,g,tol", [(torch.float32, 64, 4, 1e-5), (torch.float32, 128, 3, 1e-5),
                                            (torch.bfloat16, 128, 4, 1e-3), (torch.bfloat16, 64, 8, 1e-3),
-                                           (torch.bfloat16, 256, 16, 1e-3), (torch.float32, 256, 1, 1e-5)])
+                                           (torch.bfloat16, 256, 16, 1e-3), (torch.float32, 256, 1, 1e-5),
+                                           # head dims below / between the padded widths
+                                           (torch.bfloat16, 8, 1, 1e-3), (torch.float32, 16, 2, 1e-5),
+                                           (torch.bfloat16, 32, 4, 1e-3), (torch.bfloat16, 96, 2, 1e-3),
+                                           (torch.bfloat16, 136, 4, 1e-3), (torch.float32, 200, 2, 1e-5)])
 @pytest.mark.parametrize("causal", [False, True])
 def test_sparse_attention_vs_oracle(dev, orc, dtype, d, g, tol, causal):
     from ssa_amd import kernels
