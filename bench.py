@@ -100,14 +100,16 @@ def algorithmic(cfg, n, stats_sum=None):
     out["b_bytes"] = 3 * rows * b * 4 + h_kv * B * (n_c + 1) * 4
     if stats_sum is not None:
         R, C = stats_sum
-        out["c_bytes"] = R * 4 + C * d * s + rows * (g * d * s + 3 * a * 4 + k * 8)
+        out["c_bytes"] = R * 4 + C * d * s + rows * (g * d * s + 3 * a * 4 + k * 4)
         out["c_flops"] = C * 2 * d * g
-    out["d_bytes"] = rows * (k * 8 + 2 * k * d * s + 2 * g * d * s)
+    out["d_bytes"] = rows * (k * 4 + 2 * k * d * s + 2 * g * d * s)
     out["d_flops"] = 4 * rows * g * k * d
     return out
 
 
 def run_step(q, k, v, router, events=None):
+    import torch
+
     from ssa_amd import kernels
 
     if events:
@@ -120,8 +122,10 @@ def run_step(q, k, v, router, events=None):
     if events:
         events[2].record()
     # Same calls as SSAAttention: stage (d) does not depend on the order of the
-    # selected keys, so the router lists them by index (same set as sorted).
-    idx = kernels.select(q, k, qc, off, post, router.codes_per_key, router.top_k, sorted=False)
+    # selected keys, so the router lists them by index (same set as sorted),
+    # and the indices pass to stage (d) as int32.
+    idx = kernels.select(q, k, qc, off, post, router.codes_per_key, router.top_k, sorted=False,
+                         index_dtype=torch.int32)
     if events:
         events[3].record()
     out = kernels.sparse_attention(q, k, v, idx, None, True)

@@ -583,13 +583,14 @@ __global__ __launch_bounds__(kAttThreads, 2) void sparse_attention_mfma_kernel(A
     mx = fmaxf(mx, __shfl_xor(mx, 32));
     const float mnew = fmaxf(m_run, mx);
     const bool dead = (mnew == -INFINITY);
-    const float alpha = dead ? 1.0f : exp2f(m_run - mnew);
+    // v_exp_f32 directly: weights below 2^-126 (denormal) do not matter here.
+    const float alpha = dead ? 1.0f : __builtin_amdgcn_exp2f(m_run - mnew);
     m_run = mnew;
     float pr[8];
     float ps = 0.0f;
 #pragma unroll
     for (int x = 0; x < 8; ++x) {
-      pr[x] = dead ? 0.0f : exp2f(sc[x] - mnew);
+      pr[x] = dead ? 0.0f : __builtin_amdgcn_exp2f(sc[x] - mnew);
       ps += pr[x];
     }
     l_run = l_run * alpha + ps;

@@ -122,8 +122,10 @@ class SSAAttention(nn.Module):
         else:
             # Stage 3 does not depend on the order of the selected keys, so the
             # router lists them by index and skips rescoring rows whose
-            # candidates all fit in top_k.
-            indices = self.router(q, k, causal_mask=True, hard=True, sorted=False)
+            # candidates all fit in top_k; inside the layer the indices stay
+            # int32 (half the bytes of the public int64 output).
+            indices = self.router.route(q, k, causal_mask=True, hard=True, sorted=False,
+                                        index_dtype=torch.int32).indices
             out = sparse_exact_attention(q, k, v, indices, causal=self.causal_attention,
                                          check_indices=False)
         return self.o_proj(out.reshape(B, n, -1).to(hidden_states.dtype))
