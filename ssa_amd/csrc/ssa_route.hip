@@ -94,6 +94,115 @@ __global__ __launch_bounds__(kRouteThreads) void route_vectors_kernel(
   }
 }
 
+// route_dim <= 32: 64-row tiles, each thread a 2-row x 4-coordinate register
+// tile (eight coordinate groups x 32 row pairs), so every 4-dim step reads two
+// x and four w float4s from LDS for 32 fmaf.  Same per-score chains as above:
+// one fmaf chain over t ascending per head, the group summed in head order,
+// then / group and normalized.  x rows are staged with 4-element vector loads
+// (strides and base aligned to 4 elements).
+constexpr int kRvRows = 64;
+
+__device__ __forceinline__ float4 load4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+__device__ __forceinline__ float4 load4(const uint16_t* p) {
+  const uint2 u = *reinterpret_cast<const uint2*>(p);
+  return make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xFFFF0000u),
+                     __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xFFFF0000u));
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void route_vectors_tile_kernel(
+    const T* __restrict__ x, int64_t n, int h_in, int group, int d, int64_t sb, int64_t sn,
+    int64_t sh, const float* __restrict__ w, int d_s, float* __restrict__ out) {
+  extern __shared__ __align__(16) float smem[];
+  const int dpad = d + 4;
+  float* Ws = smem;                   // [32][dpad], coordinates >= d_s are zero
+  float* Xs = Ws + 32 * dpad;         // [kRvRows][dpad]
+  float* red = Xs + kRvRows * dpad;   // [kRvRows][32]
+  const int h_out = h_in / group;
+  const int64_t tiles = (n + kRvRows - 1) / kRvRows;
+  const int64_t bh = blockIdx.x / tiles;
+  const int64_t i0 = (blockIdx.x % tiles) * kRvRows;
+  const int64_t b = bh / h_out;
+  const int h = static_cast<int>(bh % h_out);
+  const int tid = threadIdx.x;
+  const int cg = tid & 7;   // coordinates 4*cg .. 4*cg+3
+  const int rg = tid >> 3;  // rows 2*rg, 2*rg+1
+  const int d4 = d / 4;
+
+  for (int e = tid; e < 32 * d4; e += 256) {
+    const int sc = e / d4, t = 4 * (e % d4);
+    *reinterpret_cast<float4*>(Ws + sc * dpad + t) =
+        (sc < d_s) ? *reinterpret_cast<const float4*>(w + static_cast<int64_t>(sc) * d + t)
+                   : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  float sum[2][4];
+  for (int gg = 0; gg < group; ++gg) {
+    __syncthreads();
+    const T* xh = x + b * sb + static_cast<int64_t>(h * group + gg) * sh;
+    for (int e = tid; e < kRvRows * d4; e += 256) {
+      const int rr = e / d4, t = 4 * (e % d4);
+      const int64_t i = i0 + rr;
+      *reinterpret_cast<float4*>(Xs + rr * dpad + t) = (i < n) ? load4(xh + i * sn + t)
+                                                                : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    __syncthreads();
+    float acc[2][4];
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) acc[r][c] = 0.0f;
+    const float* xr = Xs + (2 * rg) * dpad;
+    const float* wr = Ws + (4 * cg) * dpad;
+    for (int t = 0; t < d; t += 4) {
+      float4 xv[2], wv[4];
+#pragma unroll
+      for (int r = 0; r < 2; ++r) xv[r] = *reinterpret_cast<const float4*>(xr + r * dpad + t);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) wv[c] = *reinterpret_cast<const float4*>(wr + c * dpad + t);
+#pragma unroll
+      for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          acc[r][c] = fma_rn(xv[r].x, wv[c].x, acc[r][c]);
+          acc[r][c] = fma_rn(xv[r].y, wv[c].y, acc[r][c]);
+          acc[r][c] = fma_rn(xv[r].z, wv[c].z, acc[r][c]);
+          acc[r][c] = fma_rn(xv[r].w, wv[c].w, acc[r][c]);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) sum[r][c] = (gg == 0) ? acc[r][c] : sum[r][c] + acc[r][c];
+  }
+  float val[2][4];
+#pragma unroll
+  for (int r = 0; r < 2; ++r)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      val[r][c] = sum[r][c] / static_cast<float>(group);
+      red[(2 * rg + r) * 32 + 4 * cg + c] = val[r][c];
+    }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int64_t i = i0 + 2 * rg + r;
+    if (i >= n) continue;
+    const float* y = red + (2 * rg + r) * 32;
+    float nrm = 0.0f;
+    for (int v = 0; v < d_s; ++v) nrm = fma_rn(y[v], y[v], nrm);
+    const float den = fmaxf(sqrtf(nrm), 1e-12f);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int sc = 4 * cg + c;
+      if (sc < d_s) out[(bh * n + i) * d_s + sc] = val[r][c] / den;
+    }
+  }
+}
+
+size_t route_vectors_tile_smem(int d) {
+  return sizeof(float) * (static_cast<size_t>(32 + kRvRows) * (d + 4) + static_cast<size_t>(kRvRows) * 32);
+}
+
 // Row-wise F.normalize: one thread per row.
 __global__ void normalize_rows_kernel(const float* __restrict__ x, int64_t rows, int d_s,
                                       float* __restrict__ out) {
@@ -251,7 +360,6 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float floatx4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kMfRows = 256;     // rows per block: 4 waves x 4 row tiles of 16
-constexpr int kMfChunk = 512;    // codes staged in LDS at a time
 constexpr int kMfCap = 64;       // candidate codes kept per row
 constexpr float kMfEps = 0.0039844f;  // 1.02 * 2^-8
 
@@ -264,10 +372,8 @@ __device__ __forceinline__ uint16_t bf16_rne(float f) {
 __host__ __device__ inline int n_c_padded(int n_c) { return (n_c + 15) / 16 * 16; }
 
 __host__ __device__ inline size_t code_topk_mfma_smem(int top) {
-  const size_t chunk = static_cast<size_t>(kMfChunk) * 32 * sizeof(uint16_t);
   const size_t lists = static_cast<size_t>(4) * top * 64 * sizeof(uint64_t);
-  return (chunk > lists ? chunk : lists) + sizeof(int) * 4 * 64 +
-         sizeof(uint16_t) * 4 * kMfCap * 64;
+  return lists + sizeof(int) * 4 * 64 + sizeof(uint16_t) * 4 * kMfCap * 64;
 }
 
 // bf16 copy of the codebook, zero-padded to [h][n_c_pad][32], and the largest
@@ -338,11 +444,9 @@ __global__ __launch_bounds__(256) void code_topk_mfma_kernel(
     float temperature, int top, int32_t* __restrict__ codes, uint8_t* __restrict__ flags) {
   constexpr int M = (2 * Q < 8) ? 2 * Q : 8;  // segment maxima per lane and row
   extern __shared__ __align__(16) unsigned char smem_raw[];
-  const size_t chunk_bytes = static_cast<size_t>(kMfChunk) * 64;
   const size_t list_bytes = static_cast<size_t>(4) * top * 64 * 8;
-  uint16_t* chunk = reinterpret_cast<uint16_t*>(smem_raw);             // [kMfChunk][32]
   uint64_t* lists = reinterpret_cast<uint64_t*>(smem_raw);             // [4][top][64] (pass 3)
-  int* cnt = reinterpret_cast<int*>(smem_raw + (chunk_bytes > list_bytes ? chunk_bytes : list_bytes));
+  int* cnt = reinterpret_cast<int*>(smem_raw + list_bytes);
   uint16_t* cand = reinterpret_cast<uint16_t*>(cnt + 4 * 64);          // [4][kMfCap][64]
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -385,38 +489,44 @@ __global__ __launch_bounds__(256) void code_topk_mfma_kernel(
 #pragma unroll
     for (int u = 0; u < M; ++u) smax[nt][u] = -INFINITY;
 
-  // ---- pass 1: segment maxima
-  for (int c0 = 0; c0 < n_c_pad; c0 += kMfChunk) {
-    const int nct = min(kMfChunk, n_c_pad - c0);
-    __syncthreads();
-    {
-      const uint4* src = reinterpret_cast<const uint4*>(cbh + static_cast<int64_t>(c0) * 32);
-      uint4* dst = reinterpret_cast<uint4*>(chunk);
-      for (int e = tid; e < nct * 4; e += 256) dst[e] = src[e];
+  // ---- pass 1: segment maxima.  Codebook fragments come straight from the
+  // (L2-resident) bf16 codebook: lane (q4, c16) reads 16 bytes of code
+  // tile*16 + c16.  Eight tiles per step, each feeding four independent MFMAs
+  // (one per 16-row tile); tile u of a step updates segment u % M.  Codes past
+  // n_c occur only in the last tile, which alone is masked.
+  const int ntile_full = n_c / 16;
+  const int ntile = n_c_pad / 16;
+  auto frag = [&](int tile) -> bf16x8_t {
+    return *reinterpret_cast<const bf16x8_t*>(cbh + (static_cast<int64_t>(tile) * 16 + c16) * 32 + q4 * 8);
+  };
+  {
+    int t = 0;
+    for (; t + 8 <= ntile_full; t += 8) {
+      bf16x8_t a[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) a[u] = frag(t + u);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        floatx4_t sc[4];
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt)
+          sc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[u], bfrag[nt], floatx4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt)
+          smax[nt][u % M] = fmaxf(smax[nt][u % M], fmaxf(fmaxf(sc[nt][0], sc[nt][1]), fmaxf(sc[nt][2], sc[nt][3])));
+      }
     }
-    __syncthreads();
-    const int ntile = nct / 16;
-    for (int t = 0; t < ntile; t += M) {
+    for (; t < ntile; ++t) {
+      const bf16x8_t a = frag(t);
+      const int cbase = t * 16 + q4 * 4;
 #pragma unroll
-      for (int u = 0; u < M; ++u) {
-        if (t + u < ntile) {
-          const int tile = t + u;
-          const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(chunk + (tile * 16 + c16) * 32 + q4 * 8);
-          const int cbase = c0 + tile * 16 + q4 * 4;
-          const bool tail = (c0 + tile * 16 + 16 > n_c);
+      for (int nt = 0; nt < 4; ++nt) {
+        const floatx4_t sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bfrag[nt], floatx4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        float m = -INFINITY;
 #pragma unroll
-          for (int nt = 0; nt < 4; ++nt) {
-            const floatx4_t sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bfrag[nt], floatx4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-            float m = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-            if (tail) {
-              m = -INFINITY;
-#pragma unroll
-              for (int e = 0; e < 4; ++e)
-                if (cbase + e < n_c) m = fmaxf(m, sc[e]);
-            }
-            smax[nt][u] = fmaxf(smax[nt][u], m);
-          }
-        }
+        for (int e = 0; e < 4; ++e)
+          if (cbase + e < n_c) m = fmaxf(m, sc[e]);
+        smax[nt][t % M] = fmaxf(smax[nt][t % M], m);
       }
     }
   }
@@ -447,31 +557,42 @@ __global__ __launch_bounds__(256) void code_topk_mfma_kernel(
   for (int nt = 0; nt < 4; ++nt) thr[nt] = __shfl(thr_l, nt * 16 + c16);
 
   // ---- pass 2: collect codes whose approximate score reaches the threshold
-  for (int c0 = 0; c0 < n_c_pad; c0 += kMfChunk) {
-    const int nct = min(kMfChunk, n_c_pad - c0);
-    __syncthreads();
-    {
-      const uint4* src = reinterpret_cast<const uint4*>(cbh + static_cast<int64_t>(c0) * 32);
-      uint4* dst = reinterpret_cast<uint4*>(chunk);
-      for (int e = tid; e < nct * 4; e += 256) dst[e] = src[e];
-    }
-    __syncthreads();
-    const int ntile = nct / 16;
-    for (int tile = 0; tile < ntile; ++tile) {
-      const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(chunk + (tile * 16 + c16) * 32 + q4 * 8);
-      const int cbase = c0 + tile * 16 + q4 * 4;
+  // (a uniform branch skips the appends when no lane has such a code).
+  auto collect = [&](const floatx4_t& sc, int nt, int cbase) {
+    const bool hit = (sc[0] >= thr[nt]) || (sc[1] >= thr[nt]) || (sc[2] >= thr[nt]) || (sc[3] >= thr[nt]);
+    if (__ballot(hit)) {
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt) {
-        const floatx4_t sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bfrag[nt], floatx4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          if (sc[e] >= thr[nt] && cbase + e < n_c) {
-            const int r = nt * 16 + c16;
-            const int pos = atomicAdd(&cnt[wave * 64 + r], 1);
-            if (pos < kMfCap) cand[(wave * kMfCap + pos) * 64 + r] = static_cast<uint16_t>(cbase + e);
-          }
+      for (int e = 0; e < 4; ++e) {
+        if (sc[e] >= thr[nt] && cbase + e < n_c) {
+          const int r = nt * 16 + c16;
+          const int pos = atomicAdd(&cnt[wave * 64 + r], 1);
+          if (pos < kMfCap) cand[(wave * kMfCap + pos) * 64 + r] = static_cast<uint16_t>(cbase + e);
         }
       }
+    }
+  };
+  {
+    int t = 0;
+    for (; t + 8 <= ntile; t += 8) {
+      bf16x8_t a[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) a[u] = frag(t + u);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        floatx4_t sc[4];
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt)
+          sc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[u], bfrag[nt], floatx4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) collect(sc[nt], nt, (t + u) * 16 + q4 * 4);
+      }
+    }
+    for (; t < ntile; ++t) {
+      const bf16x8_t a = frag(t);
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt)
+        collect(__builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bfrag[nt], floatx4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0),
+                nt, t * 16 + q4 * 4);
     }
   }
   __syncthreads();
@@ -550,6 +671,21 @@ int launch_route_vectors(const void* x, int dtype, int64_t batch, int64_t n, int
                          int d, int64_t sb, int64_t sn, int64_t sh, const float* w, int d_s,
                          float* out, hipStream_t st) {
   if (batch == 0 || n == 0) return SSA_OK;
+  const int esz = (dtype == SSA_DTYPE_BF16) ? 2 : 4;
+  const bool vec4 = (sb % 4 == 0) && (sn % 4 == 0) && (sh % 4 == 0) &&
+                    (reinterpret_cast<uintptr_t>(x) % (4 * esz) == 0) &&
+                    (reinterpret_cast<uintptr_t>(w) % 16 == 0);
+  if (d_s <= 32 && vec4 && route_vectors_tile_smem(d) <= 64 * 1024) {
+    const int64_t grid = batch * (h_in / group) * ceil_div(n, kRvRows);
+    const size_t smem = route_vectors_tile_smem(d);
+    if (dtype == SSA_DTYPE_BF16)
+      route_vectors_tile_kernel<uint16_t><<<dim3(static_cast<unsigned>(grid)), 256, smem, st>>>(
+          static_cast<const uint16_t*>(x), n, h_in, group, d, sb, sn, sh, w, d_s, out);
+    else
+      route_vectors_tile_kernel<float><<<dim3(static_cast<unsigned>(grid)), 256, smem, st>>>(
+          static_cast<const float*>(x), n, h_in, group, d, sb, sn, sh, w, d_s, out);
+    return check_launch("route_vectors_tile_kernel");
+  }
   const int dsp = next_pow2(d_s);
   const int rb = (kRouteThreads / dsp) * kRouteRowsPerThread;
   const int64_t grid = batch * (h_in / group) * ceil_div(n, rb);
