@@ -268,11 +268,11 @@ def cpu_baseline(cfg, q, k, v, router, inter, budget_s):
     }
 
 
-def measured_traffic(workload, kernel="sparse_attention_kernel"):
+def measured_traffic(workload, kernel="sparse_attention_mfma_kernel"):
     """HBM bytes per launch of `kernel` at `workload`, from the committed rocprofv3
     FETCH_SIZE / WRITE_SIZE summary (profiles/<kernel>_<workload>_traffic.md, line
     ``traffic_bytes <kernel> <workload> <bytes>``); None when no such profile exists."""
-    path = os.path.join(ROOT, "profiles", f"{kernel.replace('_kernel', '')}_{workload}_traffic.md")
+    path = os.path.join(ROOT, "profiles", f"sparse_attention_{workload}_traffic.md")
     try:
         with open(path) as f:
             for line in f:
@@ -361,7 +361,7 @@ def main():
                    "batch": cfg["B"], "seq_len": cfg["n"], "h_q": cfg["h_q"], "h_kv": cfg["h_kv"],
                    "head_dim": cfg["d"], "route_dim": cfg["d_s"], "num_codebook": cfg["n_c"],
                    "codes_per_query": cfg["a"], "codes_per_key": cfg["b"], "top_k": cfg["k"]},
-        "roofline": {"bound": "hbm", "kernel": "sparse_attention_kernel (stage d)",
+        "roofline": {"bound": "hbm", "kernel": "sparse_attention_mfma_kernel (stage d)",
                      "achieved": d_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": d_gbs / HBM_PEAK_GBS, "traffic": traffic,
                      "traffic_source": traffic_src,
