@@ -52,6 +52,9 @@ def parse():
     p.add_argument("--copy-probe-gib", type=float, default=0.0,
                    help="also run one device copy of this size (PMC byte calibration)")
     p.add_argument("--sweep", default="", help="comma list of n for a tokens/s vs n sweep")
+    p.add_argument("--sweep-nc", default="scaled", choices=("scaled", "fixed"),
+                   help="codebook size in the sweep: scaled with n (constant bucket size; the "
+                        "config's N_c at its own n) or fixed at the config's N_c")
     return p.parse_args()
 
 
@@ -374,11 +377,27 @@ def main():
         sweep = {}
         for n_ in [int(x) for x in args.sweep.split(",")]:
             c2 = dict(cfg, n=n_)
+            if args.sweep_nc == "scaled":
+                c2["n_c"] = max(16, cfg["n_c"] * n_ // cfg["n"])
             q2, k2, v2, r2 = make_workload(c2, args.seed, dev)
             w2, s2 = time_gpu(c2, q2, k2, v2, r2, max(3, args.steps // 2), 1)
-            sweep[n_] = {"ms": 1000 * w2 / max(3, args.steps // 2), "stages_ms": s2}
+            ms2 = 1000 * w2 / max(3, args.steps // 2)
+            sweep[n_] = {"ms": ms2, "tokens_per_s": c2["B"] * n_ / (ms2 / 1000), "num_codebook": c2["n_c"],
+                         "stages_ms": s2}
             print(f"sweep n={n_}: {sweep[n_]['ms']:.3f} ms", file=sys.stderr, flush=True)
             del q2, k2, v2, r2
+        ns = sorted(sweep)
+        ts = [sweep[x]["ms"] for x in ns]
+        if len(ns) >= 3:  # least-squares t = alpha * n + beta and its R^2
+            mn, mt = sum(ns) / len(ns), sum(ts) / len(ts)
+            sxx = sum((x - mn) ** 2 for x in ns)
+            alpha = sum((x - mn) * (t - mt) for x, t in zip(ns, ts)) / sxx
+            beta = mt - alpha * mn
+            ss_res = sum((t - (alpha * x + beta)) ** 2 for x, t in zip(ns, ts))
+            ss_tot = sum((t - mt) ** 2 for t in ts)
+            sweep["fit"] = {"ms_per_token": alpha, "ms_offset": beta,
+                            "r2": 1.0 - ss_res / ss_tot if ss_tot > 0 else 1.0}
+        sweep["num_codebook_policy"] = args.sweep_nc
         line["sweep"] = sweep
     print(json.dumps(line), flush=True)
 
