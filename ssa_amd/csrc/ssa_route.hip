@@ -371,9 +371,26 @@ __device__ __forceinline__ uint16_t bf16_rne(float f) {
 
 __host__ __device__ inline int n_c_padded(int n_c) { return (n_c + 15) / 16 * 16; }
 
-__host__ __device__ inline size_t code_topk_mfma_smem(int top) {
+// Template instance per `top` (Q = 1, 2, 4, 8) and its segment maxima per lane
+// and row (M).  The 4M maxima of a row must be >= top; for top <= 16, M = 2Q
+// capped at 8.  For top 17..32 the screen keeps 32 per lane: with only 8 (4M =
+// top) the bound L would be the smallest maximum and collect about 140 codes per
+// row at N_c = 8192, overflowing kMfCap everywhere; with 32 it collects about 45.
+__host__ __device__ constexpr int mf_q(int top) { return top <= 4 ? 1 : top <= 8 ? 2 : top <= 16 ? 4 : 8; }
+__host__ __device__ constexpr int mf_segments(int q) { return q >= 8 ? 32 : (2 * q < 8 ? 2 * q : 8); }
+
+// LDS: one region used first for the segment maxima ([4 waves][4M][64] fp32),
+// then for the pass-3 lists ([4][top][64] u64) followed by the pass-2
+// candidates ([4][kMfCap][64] u16); the per-row counters come after it.
+__host__ __device__ inline size_t code_topk_mfma_region(int top) {
   const size_t lists = static_cast<size_t>(4) * top * 64 * sizeof(uint64_t);
-  return lists + sizeof(int) * 4 * 64 + sizeof(uint16_t) * 4 * kMfCap * 64;
+  const size_t cand = sizeof(uint16_t) * 4 * kMfCap * 64;
+  const size_t segs = sizeof(float) * 4 * 4 * mf_segments(mf_q(top)) * 64;
+  return lists + cand > segs ? lists + cand : segs;
+}
+
+__host__ __device__ inline size_t code_topk_mfma_smem(int top) {
+  return code_topk_mfma_region(top) + sizeof(int) * 4 * 64;
 }
 
 // bf16 copy of the codebook, zero-padded to [h][n_c_pad][32], and the largest
@@ -437,17 +454,38 @@ __device__ __forceinline__ void sort_desc(float (&v)[N]) {
       }
 }
 
+// v and w sorted descending: v becomes the N largest of v and w, sorted
+// descending.  max(v[i], w[N-1-i]) holds those N values as a bitonic sequence,
+// which the half-cleaner cascade sorts.
+template <int N>
+__device__ __forceinline__ void merge_top_desc(float (&v)[N], const float (&w)[N]) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = fmaxf(v[i], w[N - 1 - i]);
+#pragma unroll
+  for (int stride = N >> 1; stride > 0; stride >>= 1)
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int j = i ^ stride;
+      if (j > i) {
+        const float a = v[i], b = v[j];
+        v[i] = fmaxf(a, b);
+        v[j] = fminf(a, b);
+      }
+    }
+}
+
 template <int Q>
 __global__ __launch_bounds__(256) void code_topk_mfma_kernel(
     const float* __restrict__ xhat, int64_t rows, int h, const float* __restrict__ chat,
     const uint16_t* __restrict__ cbf, const uint32_t* __restrict__ cmax_bits, int n_c, int d_s,
     float temperature, int top, int32_t* __restrict__ codes, uint8_t* __restrict__ flags) {
-  constexpr int M = (2 * Q < 8) ? 2 * Q : 8;  // segment maxima per lane and row
+  constexpr int M = mf_segments(Q);  // segment maxima per lane and row
+  constexpr int G = M > 8 ? M / 8 : 1;  // 8-tile groups per pass-1 step
   extern __shared__ __align__(16) unsigned char smem_raw[];
   const size_t list_bytes = static_cast<size_t>(4) * top * 64 * 8;
-  uint64_t* lists = reinterpret_cast<uint64_t*>(smem_raw);             // [4][top][64] (pass 3)
-  int* cnt = reinterpret_cast<int*>(smem_raw + list_bytes);
-  uint16_t* cand = reinterpret_cast<uint16_t*>(cnt + 4 * 64);          // [4][kMfCap][64]
+  uint64_t* lists = reinterpret_cast<uint64_t*>(smem_raw);               // [4][top][64] (pass 3)
+  uint16_t* cand = reinterpret_cast<uint16_t*>(smem_raw + list_bytes);   // [4][kMfCap][64] (pass 2)
+  int* cnt = reinterpret_cast<int*>(smem_raw + code_topk_mfma_region(top));
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int q4 = lane >> 4, c16 = lane & 15;
@@ -491,67 +529,92 @@ __global__ __launch_bounds__(256) void code_topk_mfma_kernel(
 
   // ---- pass 1: segment maxima.  Codebook fragments come straight from the
   // (L2-resident) bf16 codebook: lane (q4, c16) reads 16 bytes of code
-  // tile*16 + c16.  Eight tiles per step, each feeding four independent MFMAs
-  // (one per 16-row tile); tile u of a step updates segment u % M.  Codes past
-  // n_c occur only in the last tile, which alone is masked.
+  // tile*16 + c16.  Eight tiles per group, each feeding four independent MFMAs
+  // (one per 16-row tile); a step of G groups covers 8G tiles and tile j of the
+  // step updates segment j % M.  The remaining full 8-tile groups and the last
+  // (at most 8) tiles use segments 0..7; only the last tile can hold codes past
+  // n_c and is masked.  Any tile-to-segment map keeps the segments of one lane
+  // disjoint, which is all the bound needs.
   const int ntile_full = n_c / 16;
   const int ntile = n_c_pad / 16;
   auto frag = [&](int tile) -> bf16x8_t {
     return *reinterpret_cast<const bf16x8_t*>(cbh + (static_cast<int64_t>(tile) * 16 + c16) * 32 + q4 * 8);
   };
+  auto group8 = [&](int t, int seg0) {
+    bf16x8_t a[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) a[u] = frag(t + u);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      floatx4_t sc[4];
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt)
+        sc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[u], bfrag[nt], floatx4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt)
+        smax[nt][(seg0 + u) % M] =
+            fmaxf(smax[nt][(seg0 + u) % M], fmaxf(fmaxf(sc[nt][0], sc[nt][1]), fmaxf(sc[nt][2], sc[nt][3])));
+    }
+  };
   {
     int t = 0;
-    for (; t + 8 <= ntile_full; t += 8) {
-      bf16x8_t a[8];
+    for (; t + 8 * G <= ntile_full; t += 8 * G) {
 #pragma unroll
-      for (int u = 0; u < 8; ++u) a[u] = frag(t + u);
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        floatx4_t sc[4];
-#pragma unroll
-        for (int nt = 0; nt < 4; ++nt)
-          sc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[u], bfrag[nt], floatx4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-#pragma unroll
-        for (int nt = 0; nt < 4; ++nt)
-          smax[nt][u % M] = fmaxf(smax[nt][u % M], fmaxf(fmaxf(sc[nt][0], sc[nt][1]), fmaxf(sc[nt][2], sc[nt][3])));
-      }
+      for (int gi = 0; gi < G; ++gi) group8(t + 8 * gi, 8 * gi);
     }
-    for (; t < ntile; ++t) {
-      const bf16x8_t a = frag(t);
-      const int cbase = t * 16 + q4 * 4;
+    if (G > 1)
+      for (; t + 8 <= ntile_full; t += 8) group8(t, 0);
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt) {
-        const floatx4_t sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bfrag[nt], floatx4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-        float m = -INFINITY;
+    for (int u = 0; u < 8; ++u) {
+      if (t + u < ntile) {
+        const bf16x8_t a = frag(t + u);
+        const int cbase = (t + u) * 16 + q4 * 4;
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (cbase + e < n_c) m = fmaxf(m, sc[e]);
-        smax[nt][t % M] = fmaxf(smax[nt][t % M], m);
+        for (int nt = 0; nt < 4; ++nt) {
+          const floatx4_t sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bfrag[nt], floatx4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+          float m = -INFINITY;
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (cbase + e < n_c) m = fmaxf(m, sc[e]);
+          smax[nt][u % M] = fmaxf(smax[nt][u % M], m);
+        }
       }
     }
   }
 
   // L per row = top-th largest of the 4M segment maxima of its 4 lanes: the
-  // maxima go through LDS (the candidate area, unused until pass 2) so that
-  // lane r of the wave can sort row r's 4M values.
-  float* segs = reinterpret_cast<float*>(cand) + static_cast<size_t>(wave) * 4 * M * 64;  // [4M][64]
+  // maxima go through LDS (the start of the shared region, unused until pass 2)
+  // so that lane r of the wave can sort row r's 4M values.
+  float* segs = reinterpret_cast<float*>(smem_raw) + static_cast<size_t>(wave) * 4 * M * 64;  // [4M][64]
 #pragma unroll
   for (int nt = 0; nt < 4; ++nt)
 #pragma unroll
     for (int u = 0; u < M; ++u) segs[(q4 * M + u) * 64 + nt * 16 + c16] = smax[nt][u];
   __syncthreads();
+  // Chunks of at most 32 values are sorted and merged keeping the largest 32
+  // (top <= 32), so every register index stays static.
   float thr_l;
   {
-    float v[4 * M];
+    constexpr int C = (4 * M < 32) ? 4 * M : 32;
+    float v[C];
 #pragma unroll
-    for (int i = 0; i < 4 * M; ++i) v[i] = segs[i * 64 + lane];
-    sort_desc<4 * M>(v);
+    for (int i = 0; i < C; ++i) v[i] = segs[i * 64 + lane];
+    sort_desc<C>(v);
+#pragma unroll
+    for (int k = 1; k < 4 * M / C; ++k) {
+      float w[C];
+#pragma unroll
+      for (int i = 0; i < C; ++i) w[i] = segs[(k * C + i) * 64 + lane];
+      sort_desc<C>(w);
+      merge_top_desc<C>(v, w);
+    }
     float lb = v[0];
 #pragma unroll
-    for (int i = 1; i < 4 * M; ++i)
+    for (int i = 1; i < C; ++i)
       if (i == top - 1) lb = v[i];
     thr_l = lb - 2.0f * eps_l;
   }
+  __syncthreads();  // pass 2 writes candidates over other waves' maxima
   float thr[4];
 #pragma unroll
   for (int nt = 0; nt < 4; ++nt) thr[nt] = __shfl(thr_l, nt * 16 + c16);

@@ -217,6 +217,7 @@ def test_sparse_attention_bad_index_raises(dev):
 
 
 @pytest.mark.parametrize("top,n_c,d_s", [(4, 4096, 32), (16, 4096, 32), (32, 1000, 32),
+                                         (32, 8192, 32), (24, 2050, 32), (17, 300, 20),
                                          (16, 777, 16), (8, 64, 8), (3, 4099, 32)])
 def test_code_topk_screen_equals_exhaustive_and_oracle(dev, orc, top, n_c, d_s):
     """The matrix-core screen + exact rescoring returns the same codes as exhaustive
