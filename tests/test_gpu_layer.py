@@ -1,0 +1,76 @@
+"""The SSAAttention layer end to end on the GPU, and the int32 index handoff the
+layer uses between stages (c) and (d).
+
+The layer's forward (ssa/ssa_layer.py:68-138) is checked against the CPU oracle
+fed with the layer's own projections: candidate indices bit-exact, the output
+after o_proj within the stated tolerances.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from tests.helpers import f32, randn
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-4), (torch.bfloat16, 2e-2)])
+@pytest.mark.parametrize("causal_attention", [True, False])
+def test_layer_forward_matches_oracle(dev, orc, dtype, tol, causal_attention):
+    """B=2, n=300, hidden 256, GQA 4/2, d=64, d_s=16, N_c=64, b=2, a=8, k=32, RoPE.
+    Tolerance relative to max|ref|: 1e-4 for fp32, 2e-2 for bf16 (bf16 o_proj)."""
+    from ssa_amd import SSAAttention, precompute_rope_freqs
+
+    _say(f"layer forward dtype={dtype} causal_attention={causal_attention}")
+    B, n, hidden, h_q, h_kv, d, d_s, n_c, b, a, k = 2, 300, 256, 4, 2, 64, 16, 64, 2, 8, 32
+    torch.manual_seed(5)
+    layer = SSAAttention(hidden_size=hidden, num_q_heads=h_q, num_kv_heads=h_kv, head_dim=d,
+                         route_dim=d_s, num_codebook=n_c, codes_per_key=b, codes_per_query=a,
+                         top_k=k, causal_attention=causal_attention)
+    layer = layer.to(dev, dtype).eval()
+    x = randn((B, n, hidden), 51, dtype).to(dev)
+    freqs = precompute_rope_freqs(d, n, 1e6).to(dev)
+    with torch.no_grad():
+        got = layer(x, freqs=freqs).float().cpu().numpy()
+        q, kk, v = layer.project(x, None, freqs)
+        r = layer.router
+        idx32 = r.route(q, kk, causal_mask=True, sorted=False, index_dtype=torch.int32).indices
+        idx64 = r.route(q, kk, causal_mask=True, sorted=False).indices
+    assert idx32.dtype == torch.int32 and idx64.dtype == torch.int64
+    assert torch.equal(idx32.to(torch.int64), idx64)
+    w_o = f32(layer.o_proj.weight)
+    for bb in range(B):
+        qf, kf, vf = f32(q[bb]), f32(kk[bb]), f32(v[bb])
+        ref_idx, _ = orc.router_forward(qf, kf, f32(r.W_qr.weight), f32(r.W_kr.weight),
+                                        f32(r.codebook), a, b, k, orc.MASK_CAUSAL, sorted=False)
+        np.testing.assert_array_equal(idx64[bb].cpu().numpy(), ref_idx)
+        att = orc.sparse_attention(qf, kf, vf, ref_idx, causal=causal_attention)
+        ref = att.reshape(n, h_q * d).astype(np.float64) @ w_o.T.astype(np.float64)
+        err = float(np.abs(got[bb] - ref).max())
+        assert err <= tol * float(np.abs(ref).max()), (bb, err)
+
+
+@pytest.mark.parametrize("dtype,d,g", [(torch.bfloat16, 128, 4), (torch.bfloat16, 64, 8),
+                                       (torch.float32, 64, 2), (torch.bfloat16, 96, 2)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_attention_int32_indices_equal_int64(dev, dtype, d, g, causal):
+    """Both attention kernels read int32 and int64 indices to bit-identical outputs."""
+    from ssa_amd import kernels
+
+    _say(f"attention int32 vs int64 dtype={dtype} d={d} g={g} causal={causal}")
+    B, n, h_kv, top_k = 2, 400, 2, 96
+    q = randn((B, n, h_kv * g, d), 61, dtype).to(dev)
+    k = randn((B, n, h_kv, d), 62, dtype).to(dev)
+    v = randn((B, n, h_kv, d), 63, dtype).to(dev)
+    gi = torch.Generator().manual_seed(64)
+    idx = torch.randint(0, n, (B, n, h_kv, top_k), generator=gi).to(dev)
+    o64 = torch.empty(q.shape, device=dev, dtype=torch.float32)
+    o32 = torch.empty_like(o64)
+    kernels.sparse_attention(q, k, v, idx, None, causal, out=o64)
+    kernels.sparse_attention(q, k, v, idx.to(torch.int32), None, causal, out=o32)
+    assert torch.equal(o64, o32)
