@@ -110,6 +110,17 @@ int ssa_build_index(const int32_t* k_codes, int64_t batch, int64_t n, int h_kv, 
                     int32_t* offsets, int32_t* postings, void* workspace, size_t workspace_bytes,
                     void* stream);
 
+/* Processing order for ssa_sparse_attention's row_order: the query positions of
+ * each (batch, kv head) sorted by their best code q_codes[b][h][i][0] (stable,
+ * so ascending positions within a code).  Rows of one code share most of their
+ * candidates, so processing them together keeps the gathered K/V rows in cache.
+ * No reference counterpart (the reference has no processing order; results do
+ * not depend on it).  q_codes must lie in [0, n_c), as ssa_route_codes writes.
+ *   q_codes int32 [batch][h_kv][n][a]; order int32 [batch][h_kv][n] */
+size_t ssa_query_order_workspace_bytes(int64_t batch, int64_t n, int h_kv, int n_c);
+int ssa_query_order(const int32_t* q_codes, int64_t batch, int64_t n, int h_kv, int a, int n_c,
+                    int32_t* order, void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---- stage (c): candidate selection ------------------------------------- */
 
 /* Top-k candidate keys per (query, kv head): union of the query's a buckets,

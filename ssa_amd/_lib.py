@@ -56,6 +56,8 @@ SIGNATURES = {
          _vp, _vp, _vp, _int, _int, _int, _int, _flt, _vp, _vp, _vp, _sz, _vp]),
     "ssa_index_workspace_bytes": (_sz, [_i64, _i64, _int, _int, _int]),
     "ssa_build_index": (_int, [_vp, _i64, _i64, _int, _int, _int, _vp, _vp, _vp, _sz, _vp]),
+    "ssa_query_order_workspace_bytes": (_sz, [_i64, _i64, _int, _int]),
+    "ssa_query_order": (_int, [_vp, _i64, _i64, _int, _int, _int, _vp, _vp, _sz, _vp]),
     "ssa_select": (
         _int,
         [_vp, _vp, _int, _i64, _i64, _int, _int, _int, _i64, _i64, _i64, _i64, _i64, _i64,

@@ -435,37 +435,64 @@ __global__ __launch_bounds__(kAttThreads, (AttMinBlocks<T, D, GMAX>::value)) voi
 // ---- bf16, g <= 8, d <= 128: P.V on the matrix cores ----------------------
 //
 // Per chunk of 32 selected keys (one wave, one (batch, kv head, query) row):
-//   S^T = K . Q^T  two 16x16x32 MFMA tiles per 32 dims: A = 16 gathered K rows
-//                  (lane (q4, c16): key 16t + c16, dims 8*q4 ..), B = the group's
-//                  q rows.  Lane (q4, c16) gets head c16's scores of keys
-//                  16t + 4*q4 + e, i.e. eight keys of one head;
+//   gathers        K and V rows go straight to the wave's LDS slices with
+//                  global_load_lds_dwordx4: each wave-wide load moves whole rows
+//                  (1 KB = 4 rows at d = 128), the shape the texture path moves
+//                  fastest (a load touching 16 rows x 64 B moves bytes about 3x
+//                  slower from L2).  Row slots are XOR-swizzled (mf_swz) so the
+//                  fragment reads below are free of bank conflicts;
+//   pipelining     the chunk's fragments are read out of LDS, then the next
+//                  chunk's loads are issued into the same slices and fly while
+//                  this chunk computes;
+//   S^T = K . Q^T  two 16x16x32 MFMA tiles per 32 dims: A = 16 K rows (lane
+//                  (q4, c16): key 16t + c16, dims 8*q4 .. of each 32-dim block,
+//                  one ds_read_b128), B = the group's q rows.  Lane (q4, c16)
+//                  gets head c16's scores of keys 16t + 4*q4 + e;
 //   softmax        online in the exp2 domain, per head, max and sum reduced
 //                  across the four lanes that hold a head's keys;
 //   P              split as P = P_hi + P_lo, both bf16 (relative error of the
 //                  sum ~2^-17): head r's P_hi is row r and its P_lo row 8 + r of
 //                  the 16-row P^T operand, so one MFMA covers both for g <= 8;
-//   O^T += V^T P^T one 16x16x32 MFMA per 16 features: A = V^T, read from the
-//                  chunk's V rows staged in LDS with ds_read_b64_tr_b16 (each
-//                  lane gets four rows of one feature column), B = P^T;
+//   O^T += V^T P^T one 16x16x32 MFMA per 16 features: A = V^T, read with
+//                  ds_read_b64_tr_b16 (each lane gets four rows of one feature
+//                  column), B = P^T;
 //   output         O = (row r + row 8 + r) / l, four contiguous features per lane
 //                  and tile.
-// V values of dropped slots are zeroed, so 0 * inf never reaches the sums.
+// Dropped slots (causal, past top_k, out of range) load a zero row, so
+// 0 * inf never reaches the sums.
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef short v4i16_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4i16_t* lds_v4i16_ptr;
+typedef __attribute__((address_space(3))) bf16x8_t* lds_bf16x8_ptr;
+typedef __attribute__((address_space(3))) void* lds_void_ptr;
 
 constexpr int kMfChunk = 32;
+
+// Source of dropped slots: one zero row (vector loads only).
+__device__ __align__(16) uint16_t kZeroRow[256];
 
 template <int D>
 struct MfShape {
   static constexpr int KB = D / 32;           // 32-dim blocks of Q.K
   static constexpr int NT = D / 16;           // 16-feature tiles of P.V
-  static constexpr int ROW_B = 2 * D + 32;    // bytes per staged V row (32 B pad: tr reads of
-                                              // four consecutive rows hit disjoint banks)
-  static constexpr int SEGS = D / 8;          // 16-byte segments per V row
-  static constexpr int KPI = 64 / SEGS;       // V rows per wave-wide load
-  static constexpr int NVI = kMfChunk / KPI;  // V loads per lane per chunk
+  static constexpr int ROW = 2 * D;           // bytes per staged row
+  static constexpr int SEGS = D / 8;          // 16-byte segments per row
+  static constexpr int KPI = 64 / SEGS;       // rows per wave-wide load (KPI * ROW = 1 KB)
+  static constexpr int NLD = kMfChunk / KPI;  // loads per chunk, each for K and V
+  static constexpr int RPL = 256 / ROW;       // rows per 256-byte bank line
 };
+
+// LDS slot of segment s of chunk row `key` is s ^ mf_swz(key).  With u = key /
+// RPL (rows of one bank line share u), swz = 2*(u mod SEGS/2) + (u / (SEGS/2)
+// mod 2): the 16 rows of a K fragment read (one segment each) hit 16 distinct
+// 16-byte bank groups, and the four rows of a transposing V read (two adjacent
+// segments each) hit four distinct 32-byte groups.
+template <int D>
+__device__ __forceinline__ int mf_swz(int key) {
+  using S = MfShape<D>;
+  const int u = key / S::RPL;
+  return ((u & (S::SEGS / 2 - 1)) << 1) | ((u / (S::SEGS / 2)) & 1);
+}
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   const bf16x2_t v = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
@@ -480,12 +507,16 @@ __device__ __forceinline__ float dpp_from_plus8(float x) {
   return __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(x), 0x108, 0xF, 0xF, false));
 }
 
+// s_waitcnt encodings (gfx9): vmcnt(0) alone, lgkmcnt(0) alone.
+constexpr int kWaitVm0 = 0x0F70;
+constexpr int kWaitLgkm0 = 0xC07F;
+
 template <int D>
 __global__ __launch_bounds__(kAttThreads, 2) void sparse_attention_mfma_kernel(AttParams p) {
   using S = MfShape<D>;
-  __shared__ __align__(16) unsigned char vlds[kAttWaves][kMfChunk * S::ROW_B];
+  __shared__ __align__(16) unsigned char kv_lds[kAttWaves][2][kMfChunk * S::ROW];
 
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int q4 = lane >> 4;
   const int c16 = lane & 15;
@@ -507,9 +538,8 @@ __global__ __launch_bounds__(kAttThreads, 2) void sparse_attention_mfma_kernel(A
   const uint16_t* kbase = static_cast<const uint16_t*>(p.k) + bb * p.k_sb + static_cast<int64_t>(h) * p.k_sh;
   const uint16_t* vbase = static_cast<const uint16_t*>(p.v) + bb * p.v_sb + static_cast<int64_t>(h) * p.v_sh;
   const int64_t ibase = bb * p.idx_sb + i * p.idx_sn + static_cast<int64_t>(h) * p.idx_sh;
-  unsigned char* vs = vlds[wave];
-  const int vseg = lane % S::SEGS;
-  const int vkey0 = lane / S::SEGS;
+  unsigned char* kl = kv_lds[wave][0];
+  unsigned char* vl = kv_lds[wave][1];
 
   auto load_idx = [&](int ch) -> int {
     const int slot = ch * kMfChunk + lane;
@@ -522,6 +552,34 @@ __global__ __launch_bounds__(kAttThreads, 2) void sparse_attention_mfma_kernel(A
     }
     return static_cast<int>(j);
   };
+  // Load r of a chunk: lane l fetches the segment stored in slot l % SEGS of
+  // chunk row KPI*r + l / SEGS; the LDS address is the load's base + 16*l.
+  const int lrow = lane / S::SEGS;
+  const int lslot = lane % S::SEGS;
+  // Row strides fit 32 bits (checked on the host); jsafe is 0 for dropped slots.
+  const uint32_t ksn = static_cast<uint32_t>(p.k_sn), vsn = static_cast<uint32_t>(p.v_sn);
+  auto issue = [&](int jsafe, uint64_t okb) {
+    uint32_t jr[S::NLD];
+#pragma unroll
+    for (int r = 0; r < S::NLD; ++r) jr[r] = static_cast<uint32_t>(__shfl(jsafe, S::KPI * r + lrow));
+#pragma unroll
+    for (int r = 0; r < S::NLD; ++r) {
+      const int key = S::KPI * r + lrow;
+      const int seg8 = (lslot ^ mf_swz<D>(key)) * 8;
+      const bool okr = (okb >> key) & 1ull;
+      const uint16_t* ks = kbase + static_cast<uint64_t>(jr[r]) * ksn + seg8;
+      const uint16_t* vsrc = vbase + static_cast<uint64_t>(jr[r]) * vsn + seg8;
+      __builtin_amdgcn_global_load_lds(okr ? ks : kZeroRow + seg8, (lds_void_ptr)(kl + r * 1024), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(okr ? vsrc : kZeroRow + seg8, (lds_void_ptr)(vl + r * 1024), 16, 0, 0);
+    }
+  };
+  auto chunk_ok = [&](int j) { return j >= 0 && !(p.causal && j > i); };
+
+  // Fragment addresses (fixed per lane): K tile t, block kb; V^T tile t (rows
+  // 4*q4 + c16/4, +16 for the second half of the chunk).
+  const int vkey = 4 * q4 + (c16 >> 2);
+  const int vswz = mf_swz<D>(vkey);
+  const int kswz = mf_swz<D>(c16);
 
   const bool hi_row = c16 < p.g;
   const bool lo_row = c16 >= 8 && c16 < 8 + p.g;
@@ -532,48 +590,57 @@ __global__ __launch_bounds__(kAttThreads, 2) void sparse_attention_mfma_kernel(A
   for (int t = 0; t < S::NT; ++t) oacc[t] = floatx4_t{0.f, 0.f, 0.f, 0.f};
 
   const int nchunks = (p.top_k + kMfChunk - 1) / kMfChunk;
-  int j_next = (nchunks > 0) ? load_idx(0) : -1;
+  uint64_t okbits = 0;
+  int j_next = -1;
+  if (nchunks > 0) {
+    const int j0 = load_idx(0);
+    const bool ok0 = chunk_ok(j0);
+    okbits = __ballot(ok0);
+    issue(ok0 ? j0 : 0, okbits);
+    if (nchunks > 1) j_next = load_idx(1);
+  }
   for (int ch = 0; ch < nchunks; ++ch) {
-    const int j = j_next;
-    const bool ok = j >= 0 && !(p.causal && j > i);
-    const int jsafe = ok ? j : 0;
-    const uint64_t okbits = __ballot(ok);
-
-    // Gathers: K straight into the A fragments, V rows into registers.
+    // This chunk's rows are in LDS once its loads have completed.
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);
     bf16x8_t kf[2][S::KB];
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int jt = __shfl(jsafe, 16 * t + c16);
-      const bool okt = (okbits >> (16 * t + c16)) & 1ull;
-      const uint16_t* kr = kbase + static_cast<int64_t>(jt) * p.k_sn + q4 * 8;
+    for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int kb = 0; kb < S::KB; ++kb)
-        kf[t][kb] = okt ? *reinterpret_cast<const bf16x8_t*>(kr + kb * 32) : bf16x8_t{};
-    }
-    uint4 vv[S::NVI];
+        kf[t][kb] = *(lds_bf16x8_ptr)(kl + (16 * t + c16) * S::ROW + (((kb * 4 + q4) ^ kswz) << 4));
+    bf16x8_t vt[S::NT];
 #pragma unroll
-    for (int r = 0; r < S::NVI; ++r) {
-      const int kk = vkey0 + S::KPI * r;
-      const int jv = __shfl(jsafe, kk);
-      const bool okv = (okbits >> kk) & 1ull;
-      vv[r] = okv ? *reinterpret_cast<const uint4*>(vbase + static_cast<int64_t>(jv) * p.v_sn + vseg * 8)
-                  : make_uint4(0u, 0u, 0u, 0u);
+    for (int t = 0; t < S::NT; ++t) {
+      const int off = vkey * S::ROW + (((2 * t + ((c16 & 3) >> 1)) ^ vswz) << 4) + (c16 & 1) * 8;
+      const v4i16_t a0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_ptr)(vl + off));
+      const v4i16_t a1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_ptr)(vl + off + 16 * S::ROW));
+      vt[t] = __builtin_bit_cast(
+          bf16x8_t, make_uint4(__builtin_bit_cast(uint2, a0).x, __builtin_bit_cast(uint2, a0).y,
+                               __builtin_bit_cast(uint2, a1).x, __builtin_bit_cast(uint2, a1).y));
     }
-    if (ch + 1 < nchunks) j_next = load_idx(ch + 1);
+    // The slices are free once the reads have returned: start the next chunk.
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+    const uint64_t okb = okbits;
+    if (ch + 1 < nchunks) {
+      const bool okn = chunk_ok(j_next);
+      okbits = __ballot(okn);
+      issue(okn ? j_next : 0, okbits);
+      if (ch + 2 < nchunks) j_next = load_idx(ch + 2);
+    }
 
     // Scores of eight keys of head c16 (keys 16t + 4*q4 + e).
     float sc[8];
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       floatx4_t s = {0.f, 0.f, 0.f, 0.f};
-      if ((okbits >> (16 * t)) & 0xFFFFull) {
+      if ((okb >> (16 * t)) & 0xFFFFull) {
 #pragma unroll
         for (int kb = 0; kb < S::KB; ++kb) s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[t][kb], qf[kb], s, 0, 0, 0);
       }
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int key = 16 * t + 4 * q4 + e;
-        sc[4 * t + e] = ((okbits >> key) & 1ull) ? s[e] * p.qk_scale_log2 : -INFINITY;
+        sc[4 * t + e] = ((okb >> key) & 1ull) ? s[e] * p.qk_scale_log2 : -INFINITY;
       }
     }
     float mx = sc[0];
@@ -608,27 +675,12 @@ __global__ __launch_bounds__(kAttThreads, 2) void sparse_attention_mfma_kernel(A
     // (cross-lane reads happen in every lane, before any lane-dependent select)
     const float alpha_in = __uint_as_float(dpp_from_minus8(__float_as_uint(alpha)));
     const float a_row = hi_row ? alpha : alpha_in;
-#pragma unroll
-    for (int t = 0; t < S::NT; ++t) oacc[t] *= a_row;
-
-    // Stage the chunk's V rows, then O^T += V^T . P^T.
-#pragma unroll
-    for (int r = 0; r < S::NVI; ++r)
-      *reinterpret_cast<uint4*>(vs + (vkey0 + S::KPI * r) * S::ROW_B + vseg * 16) = vv[r];
-    wave_lds_sync();
     const bf16x8_t pbv = __builtin_bit_cast(bf16x8_t, make_uint4(pb[0], pb[1], pb[2], pb[3]));
-    const unsigned char* tr0 = vs + (4 * q4 + (c16 >> 2)) * S::ROW_B + (c16 & 3) * 8;
-    const unsigned char* tr1 = tr0 + 16 * S::ROW_B;
 #pragma unroll
     for (int t = 0; t < S::NT; ++t) {
-      const v4i16_t a0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_ptr)(tr0 + t * 32));
-      const v4i16_t a1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_ptr)(tr1 + t * 32));
-      const bf16x8_t av = __builtin_bit_cast(
-          bf16x8_t, make_uint4(__builtin_bit_cast(uint2, a0).x, __builtin_bit_cast(uint2, a0).y,
-                               __builtin_bit_cast(uint2, a1).x, __builtin_bit_cast(uint2, a1).y));
-      oacc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, pbv, oacc[t], 0, 0, 0);
+      oacc[t] *= a_row;
+      oacc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vt[t], pbv, oacc[t], 0, 0, 0);
     }
-    wave_lds_sync();
   }
 
   // l: partial sums of the four lanes holding a head's keys; O: hi row + lo row.
@@ -663,7 +715,8 @@ template <typename T, int D>
 int launch_att_d(const AttParams& p, hipStream_t st) {
   const int64_t blocks = ceil_div(p.rows, kAttWaves);
   if constexpr (sizeof(T) == 2 && D >= 64 && D <= 128) {
-    if (p.g <= 8 && p.d == D) {
+    if (p.g <= 8 && p.d == D && p.k_sn >= 0 && p.k_sn < (int64_t(1) << 31) && p.v_sn >= 0 &&
+        p.v_sn < (int64_t(1) << 31)) {
       sparse_attention_mfma_kernel<D><<<dim3(static_cast<unsigned>(blocks)), kAttThreads, 0, st>>>(p);
       return check_launch("sparse_attention_mfma_kernel");
     }

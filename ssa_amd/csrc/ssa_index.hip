@@ -27,8 +27,15 @@ int64_t tile_keys_for(int64_t n) {
   return tk < 1024 ? 1024 : tk;
 }
 
+// Entry e = j*b + r of a head is code r of key j, stored at j*cstride + r
+// (cstride = b for k_codes; the query order reads q_codes[...][0] with b = 1,
+// cstride = a).
+__device__ __forceinline__ int64_t code_at(int64_t e, int b, int cstride) {
+  return (cstride == b) ? e : (e / b) * cstride + e % b;
+}
+
 __global__ __launch_bounds__(kHistThreads) void index_hist_kernel(
-    const int32_t* __restrict__ k_codes, int64_t n, int b, int n_c, int64_t tile_keys,
+    const int32_t* __restrict__ k_codes, int64_t n, int b, int cstride, int n_c, int64_t tile_keys,
     int64_t tiles, int32_t* __restrict__ hist) {
   extern __shared__ int32_t lds_hist[];
   const int64_t tile = blockIdx.x;
@@ -38,9 +45,9 @@ __global__ __launch_bounds__(kHistThreads) void index_hist_kernel(
   const int64_t e0 = tile * tile_keys * b;
   int64_t e1 = (tile + 1) * tile_keys * b;
   if (e1 > n * b) e1 = n * b;
-  const int32_t* kc = k_codes + bh * n * b;
+  const int32_t* kc = k_codes + bh * n * cstride;
   for (int64_t e = e0 + threadIdx.x; e < e1; e += kHistThreads) {
-    const int32_t c = kc[e];
+    const int32_t c = kc[code_at(e, b, cstride)];
     if (static_cast<uint32_t>(c) < static_cast<uint32_t>(n_c)) atomicAdd(&lds_hist[c], 1);
   }
   __syncthreads();
@@ -101,7 +108,7 @@ __global__ __launch_bounds__(kScanThreads) void index_scan_kernel(int32_t* __res
 // per round; lanes holding the same code are ranked by lane order, so every
 // bucket receives its keys in ascending j.
 __global__ __launch_bounds__(64) void index_scatter_kernel(
-    const int32_t* __restrict__ k_codes, int64_t n, int b, int n_c, int code_bits,
+    const int32_t* __restrict__ k_codes, int64_t n, int b, int cstride, int n_c, int code_bits,
     int64_t tile_keys, int64_t tiles, const int32_t* __restrict__ base,
     int32_t* __restrict__ postings) {
   extern __shared__ int32_t cursor[];
@@ -114,13 +121,13 @@ __global__ __launch_bounds__(64) void index_scatter_kernel(
   const int64_t e0 = tile * tile_keys * b;
   int64_t e1 = (tile + 1) * tile_keys * b;
   if (e1 > n * b) e1 = n * b;
-  const int32_t* kc = k_codes + bh * n * b;
+  const int32_t* kc = k_codes + bh * n * cstride;
   int32_t* post = postings + bh * n * b;
   const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   for (int64_t r0 = e0; r0 < e1; r0 += 64) {
     const int64_t e = r0 + lane;
     int32_t c = -1;
-    if (e < e1) c = kc[e];
+    if (e < e1) c = kc[code_at(e, b, cstride)];
     const bool ok = static_cast<uint32_t>(c) < static_cast<uint32_t>(n_c);
     uint64_t peers = __ballot(ok);
     for (int bit = 0; bit < code_bits; ++bit) {
@@ -145,6 +152,32 @@ __global__ void fill_i32_kernel(int32_t* __restrict__ p, int64_t count, int32_t 
   if (e < count) p[e] = v;
 }
 
+// The three index kernels over entries (j, r < b) of every (batch, head); `hist`
+// is the workspace, `offsets` receives the bucket starts.
+int run_index(const int32_t* codes, int64_t bh, int64_t n, int b, int cstride, int n_c,
+              int32_t* offsets, int32_t* postings, int32_t* hist, hipStream_t st) {
+  const int64_t tk = tile_keys_for(n);
+  const int64_t tiles = ceil_div(n, tk);
+  int code_bits = 0;
+  while ((1 << code_bits) < n_c) ++code_bits;
+  index_hist_kernel<<<dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(bh)), kHistThreads,
+                      sizeof(int32_t) * n_c, st>>>(codes, n, b, cstride, n_c, tk, tiles, hist);
+  int s = check_launch("index_hist_kernel");
+  if (s) return s;
+  index_scan_kernel<<<dim3(static_cast<unsigned>(bh)), kScanThreads, 0, st>>>(hist, n_c, tiles,
+                                                                               offsets);
+  if ((s = check_launch("index_scan_kernel"))) return s;
+  index_scatter_kernel<<<dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(bh)), 64,
+                         sizeof(int32_t) * n_c, st>>>(codes, n, b, cstride, n_c, code_bits, tk,
+                                                      tiles, hist, postings);
+  return check_launch("index_scatter_kernel");
+}
+
+size_t hist_bytes(int64_t bh, int64_t n, int n_c) {
+  const int64_t tiles = ceil_div(n, tile_keys_for(n));
+  return align_up(sizeof(int32_t) * static_cast<size_t>(bh) * n_c * tiles, 256);
+}
+
 }  // namespace
 }  // namespace ssa
 
@@ -153,8 +186,7 @@ using namespace ssa;
 extern "C" size_t ssa_index_workspace_bytes(int64_t batch, int64_t n, int h_kv, int b, int n_c) {
   (void)b;
   if (batch < 0 || n < 0 || h_kv <= 0 || n_c <= 0) return 0;
-  const int64_t tiles = ceil_div(n, tile_keys_for(n));
-  return align_up(sizeof(int32_t) * static_cast<size_t>(batch * h_kv) * n_c * tiles, 256);
+  return hist_bytes(batch * h_kv, n, n_c);
 }
 
 extern "C" int ssa_build_index(const int32_t* k_codes, int64_t batch, int64_t n, int h_kv, int b,
@@ -178,20 +210,30 @@ extern "C" int ssa_build_index(const int32_t* k_codes, int64_t batch, int64_t n,
     fill_i32_kernel<<<dim3(static_cast<unsigned>(ceil_div(count, 256))), 256, 0, st>>>(offsets, count, 0);
     return check_launch("fill_i32_kernel");
   }
-  const int64_t tk = tile_keys_for(n);
-  const int64_t tiles = ceil_div(n, tk);
+  return run_index(k_codes, bh, n, b, b, n_c, offsets, postings, static_cast<int32_t*>(workspace), st);
+}
+
+extern "C" size_t ssa_query_order_workspace_bytes(int64_t batch, int64_t n, int h_kv, int n_c) {
+  if (batch < 0 || n < 0 || h_kv <= 0 || n_c <= 0) return 0;
+  return hist_bytes(batch * h_kv, n, n_c) +
+         align_up(sizeof(int32_t) * static_cast<size_t>(batch * h_kv) * (n_c + 1), 256);
+}
+
+extern "C" int ssa_query_order(const int32_t* q_codes, int64_t batch, int64_t n, int h_kv, int a,
+                               int n_c, int32_t* order, void* workspace, size_t workspace_bytes,
+                               void* stream) {
+  if (batch < 0 || n < 0 || h_kv <= 0 || a <= 0 || n_c <= 0)
+    return fail(SSA_ERR_INVALID_ARGUMENT, "query_order: bad shape");
+  if (n_c > 16384) return fail(SSA_ERR_UNSUPPORTED, "query_order: num_codebook %d > 16384", n_c);
+  if (n * a >= (int64_t(1) << 31))
+    return fail(SSA_ERR_UNSUPPORTED, "query_order: n*a must be < 2^31");
+  const size_t need = ssa_query_order_workspace_bytes(batch, n, h_kv, n_c);
+  if (workspace_bytes < need)
+    return fail(SSA_ERR_WORKSPACE, "query_order: workspace %zu < %zu bytes", workspace_bytes, need);
+  if (batch == 0 || n == 0) return SSA_OK;
+  if (!q_codes || !order || !workspace) return fail(SSA_ERR_INVALID_ARGUMENT, "query_order: null pointer");
+  const int64_t bh = batch * h_kv;
   int32_t* hist = static_cast<int32_t*>(workspace);
-  int code_bits = 0;
-  while ((1 << code_bits) < n_c) ++code_bits;
-  index_hist_kernel<<<dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(bh)), kHistThreads,
-                      sizeof(int32_t) * n_c, st>>>(k_codes, n, b, n_c, tk, tiles, hist);
-  int s = check_launch("index_hist_kernel");
-  if (s) return s;
-  index_scan_kernel<<<dim3(static_cast<unsigned>(bh)), kScanThreads, 0, st>>>(hist, n_c, tiles,
-                                                                               offsets);
-  if ((s = check_launch("index_scan_kernel"))) return s;
-  index_scatter_kernel<<<dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(bh)), 64,
-                         sizeof(int32_t) * n_c, st>>>(k_codes, n, b, n_c, code_bits, tk, tiles,
-                                                      hist, postings);
-  return check_launch("index_scatter_kernel");
+  int32_t* offsets = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + hist_bytes(bh, n, n_c));
+  return run_index(q_codes, bh, n, 1, a, n_c, offsets, order, hist, as_stream(stream));
 }

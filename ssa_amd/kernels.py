@@ -113,6 +113,20 @@ def build_index(k_codes: torch.Tensor, n_c: int) -> Tuple[torch.Tensor, torch.Te
     return offsets, postings
 
 
+def query_order(q_codes: torch.Tensor, n_c: int) -> torch.Tensor:
+    """Query positions per (batch, kv head) sorted stably by their best code
+    ``q_codes[..., 0]``: int32 [B, h, n], a processing order for sparse_attention."""
+    _lib.require_device(q_codes)
+    q_codes = q_codes.contiguous()
+    B, h, n, a = q_codes.shape
+    order = torch.empty((B, h, n), device=q_codes.device, dtype=torch.int32)
+    ws_bytes = _lib.load().ssa_query_order_workspace_bytes(B, n, h, n_c)
+    ws = torch.empty(max(int(ws_bytes), 1), device=q_codes.device, dtype=torch.uint8)
+    call("ssa_query_order", ptr(q_codes), B, n, h, a, n_c, ptr(order), ptr(ws), ws_bytes,
+         stream_of(q_codes))
+    return order
+
+
 def select(q: torch.Tensor, k: torch.Tensor, q_codes: torch.Tensor, offsets: torch.Tensor,
            postings: torch.Tensor, b: int, top_k: int, mask_mode: int = _lib.MASK_CAUSAL,
            mask: Optional[torch.Tensor] = None, score_div: Optional[float] = None,

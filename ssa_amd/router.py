@@ -176,9 +176,7 @@ class CodebookRouter(nn.Module):
 def query_order(q_codes: torch.Tensor, num_codebook: int) -> torch.Tensor:
     """Query positions per (batch, kv head) grouped by their best code: the
     inverted index of each query's first code, int32 [B, h_kv, n]."""
-    B, h, n, _ = q_codes.shape
-    _, post = kernels.build_index(q_codes[..., :1].contiguous(), num_codebook)
-    return post.view(B, h, n)
+    return kernels.query_order(q_codes, num_codebook)
 
 
 class RouteResult:

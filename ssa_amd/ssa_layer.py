@@ -123,11 +123,13 @@ class SSAAttention(nn.Module):
             # Stage 3 does not depend on the order of the selected keys, so the
             # router lists them by index and skips rescoring rows whose
             # candidates all fit in top_k; inside the layer the indices stay
-            # int32 (half the bytes of the public int64 output).
-            indices = self.router.route(q, k, causal_mask=True, hard=True, sorted=False,
-                                        index_dtype=torch.int32).indices
-            out = sparse_exact_attention(q, k, v, indices, causal=self.causal_attention,
-                                         check_indices=False)
+            # int32 (half the bytes of the public int64 output), and the rows
+            # of each head are attended grouped by best code, so rows sharing
+            # candidate keys run together (no result depends on that order).
+            res = self.router.route(q, k, causal_mask=True, hard=True, sorted=False,
+                                    index_dtype=torch.int32, with_order=True)
+            out = sparse_exact_attention(q, k, v, res.indices, causal=self.causal_attention,
+                                         check_indices=False, row_order=res.order)
         return self.o_proj(out.reshape(B, n, -1).to(hidden_states.dtype))
 
 

@@ -57,7 +57,7 @@ def L():
 
 def test_header_parses_every_entry_point():
     decls = _declarations()
-    assert len(decls) == 13
+    assert len(decls) == 15
     assert set(decls) == set(_lib.SIGNATURES)
 
 
@@ -165,6 +165,21 @@ def test_index_rejects(L):
     assert st == _lib.SSA_ERR_INVALID_ARGUMENT
     st = L.ssa_build_index(NULL, 1, 1024, 8, 4, 4096, FAKE, FAKE, FAKE, ws, NULL)
     assert st == _lib.SSA_ERR_INVALID_ARGUMENT and b"null" in L.ssa_last_error()
+
+
+def test_query_order_rejects(L):
+    ws = L.ssa_query_order_workspace_bytes(1, 1024, 8, 4096)
+    assert ws > L.ssa_index_workspace_bytes(1, 1024, 8, 1, 4096)  # histogram + bucket starts
+    st = L.ssa_query_order(FAKE, 1, 1024, 8, 16, 16385, FAKE, FAKE, 1 << 30, NULL)
+    assert st == _lib.SSA_ERR_UNSUPPORTED and b"16384" in L.ssa_last_error()
+    st = L.ssa_query_order(FAKE, 1, 1024, 8, 16, 4096, FAKE, FAKE, ws - 1, NULL)
+    assert st == _lib.SSA_ERR_WORKSPACE and b"workspace" in L.ssa_last_error()
+    st = L.ssa_query_order(FAKE, 1, 1024, 8, 0, 4096, FAKE, FAKE, ws, NULL)
+    assert st == _lib.SSA_ERR_INVALID_ARGUMENT
+    st = L.ssa_query_order(FAKE, 1, 1024, 8, 16, 4096, NULL, FAKE, ws, NULL)
+    assert st == _lib.SSA_ERR_INVALID_ARGUMENT and b"null" in L.ssa_last_error()
+    st = L.ssa_query_order(FAKE, 1, 1 << 27, 8, 16, 4096, FAKE, FAKE, 1 << 62, NULL)
+    assert st == _lib.SSA_ERR_UNSUPPORTED and b"2^31" in L.ssa_last_error()
 
 
 def test_route_rejects(L):
