@@ -458,8 +458,8 @@ __global__ __launch_bounds__(kAttThreads, (AttMinBlocks<T, D, GMAX>::value)) voi
 //                  column), B = P^T;
 //   output         O = (row r + row 8 + r) / l, four contiguous features per lane
 //                  and tile.
-// Dropped slots (causal, past top_k, out of range) load a zero row, so
-// 0 * inf never reaches the sums.
+// Dropped slots (causal, past top_k, out of range) load zeros, so 0 * inf
+// never reaches the sums.
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef short v4i16_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4i16_t* lds_v4i16_ptr;
@@ -467,9 +467,17 @@ typedef __attribute__((address_space(3))) bf16x8_t* lds_bf16x8_ptr;
 typedef __attribute__((address_space(3))) void* lds_void_ptr;
 
 constexpr int kMfChunk = 32;
+// Waves per block and blocks per CU of the matrix-core kernel.  Each wave keeps
+// one chunk (16 KB at d = 128) of K and V in flight in its LDS slices, so the
+// bytes in flight per CU are LDS-bound.
+constexpr int kMfWaves = 4;
+constexpr int kMfMinBlocks = 2;
 
-// Source of dropped slots: one zero row (vector loads only).
-__device__ __align__(16) uint16_t kZeroRow[256];
+// Raw buffer descriptor word 3 for gfx9-family loads (32-bit data format),
+// and a byte offset past any buffer this kernel builds (an out-of-range buffer
+// load returns zeros, also into LDS).
+constexpr int kBufferWord3 = 0x00020000;
+constexpr uint32_t kOobOffset = 0x7FFFFFF0u;
 
 template <int D>
 struct MfShape {
@@ -480,6 +488,8 @@ struct MfShape {
   static constexpr int KPI = 64 / SEGS;       // rows per wave-wide load (KPI * ROW = 1 KB)
   static constexpr int NLD = kMfChunk / KPI;  // loads per chunk, each for K and V
   static constexpr int RPL = 256 / ROW;       // rows per 256-byte bank line
+  static constexpr int SWZ_PERIOD = (D == 128) ? 4 : 2;  // mf_swz of load r repeats with this period
+  static_assert(D == 64 || D == 128, "matrix-core attention kernel: d = 64 or 128");
 };
 
 // LDS slot of segment s of chunk row `key` is s ^ mf_swz(key).  With u = key /
@@ -507,20 +517,48 @@ __device__ __forceinline__ float dpp_from_plus8(float x) {
   return __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(x), 0x108, 0xF, 0xF, false));
 }
 
+// Issue one chunk's K and V loads: load r moves chunk rows KPI*r .. KPI*r +
+// KPI - 1 into LDS at base + r KB, lane l fetching the segment of row KPI*r +
+// l / SEGS that belongs in slot l % SEGS (seg16[r % SWZ_PERIOD], in bytes).
+// jsafe (lanes < 32) is the chunk's key index per slot, negative for a dropped
+// slot.  FULL: no dropped slot in the chunk; SAME: K and V share the row stride.
+template <int D, bool FULL, bool SAME>
+__device__ __forceinline__ void mf_issue(__amdgpu_buffer_rsrc_t krs, __amdgpu_buffer_rsrc_t vrs,
+                                         unsigned char* kl, unsigned char* vl, int jsafe, int lrow,
+                                         uint32_t ksn2, uint32_t vsn2,
+                                         const uint32_t (&seg16)[MfShape<D>::SWZ_PERIOD]) {
+  using S = MfShape<D>;
+  int jr[S::NLD];
+#pragma unroll
+  for (int r = 0; r < S::NLD; ++r) jr[r] = __shfl(jsafe, S::KPI * r + lrow);
+#pragma unroll
+  for (int r = 0; r < S::NLD; ++r) {
+    const uint32_t sg = seg16[r % S::SWZ_PERIOD];
+    uint32_t ko = __umul24(static_cast<uint32_t>(jr[r]), ksn2) + sg;
+    uint32_t vo = SAME ? ko : __umul24(static_cast<uint32_t>(jr[r]), vsn2) + sg;
+    if (!FULL) {
+      ko = jr[r] >= 0 ? ko : kOobOffset;
+      vo = jr[r] >= 0 ? vo : kOobOffset;
+    }
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_void_ptr)(kl + r * 1024), 16, static_cast<int>(ko), 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_void_ptr)(vl + r * 1024), 16, static_cast<int>(vo), 0, 0, 0);
+  }
+}
+
 // s_waitcnt encodings (gfx9): vmcnt(0) alone, lgkmcnt(0) alone.
 constexpr int kWaitVm0 = 0x0F70;
 constexpr int kWaitLgkm0 = 0xC07F;
 
 template <int D>
-__global__ __launch_bounds__(kAttThreads, 2) void sparse_attention_mfma_kernel(AttParams p) {
+__global__ __launch_bounds__(64 * kMfWaves, kMfMinBlocks) void sparse_attention_mfma_kernel(AttParams p) {
   using S = MfShape<D>;
-  __shared__ __align__(16) unsigned char kv_lds[kAttWaves][2][kMfChunk * S::ROW];
+  __shared__ __align__(16) unsigned char kv_lds[kMfWaves][2][kMfChunk * S::ROW];
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int q4 = lane >> 4;
   const int c16 = lane & 15;
-  const AttRow ar = att_row(p, static_cast<int64_t>(blockIdx.x) * kAttWaves + wave);
+  const AttRow ar = att_row(p, static_cast<int64_t>(blockIdx.x) * kMfWaves + wave);
   const bool row_ok = ar.ok;
   const int64_t i = ar.i;
   const int64_t bh = ar.bh;
@@ -554,23 +592,28 @@ __global__ __launch_bounds__(kAttThreads, 2) void sparse_attention_mfma_kernel(A
   };
   // Load r of a chunk: lane l fetches the segment stored in slot l % SEGS of
   // chunk row KPI*r + l / SEGS; the LDS address is the load's base + 16*l.
+  // Loads go through buffer descriptors of this head's K and V rows with 32-bit
+  // byte offsets (the host checks that every row fits below 2^31 bytes and that
+  // n and the row strides fit 24 bits); a dropped slot (jsafe < 0) gets an
+  // offset past the end, which loads zeros.
   const int lrow = lane / S::SEGS;
   const int lslot = lane % S::SEGS;
-  // Row strides fit 32 bits (checked on the host); jsafe is 0 for dropped slots.
-  const uint32_t ksn = static_cast<uint32_t>(p.k_sn), vsn = static_cast<uint32_t>(p.v_sn);
-  auto issue = [&](int jsafe, uint64_t okb) {
-    uint32_t jr[S::NLD];
+  const uint32_t ksn2 = 2u * static_cast<uint32_t>(p.k_sn), vsn2 = 2u * static_cast<uint32_t>(p.v_sn);
+  const int kbytes = static_cast<int>((p.n - 1) * p.k_sn * 2 + 2 * D);
+  const int vbytes = static_cast<int>((p.n - 1) * p.v_sn * 2 + 2 * D);
+  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(kbase), 0, kbytes, kBufferWord3);
+  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(vbase), 0, vbytes, kBufferWord3);
+  uint32_t seg16[S::SWZ_PERIOD];
 #pragma unroll
-    for (int r = 0; r < S::NLD; ++r) jr[r] = static_cast<uint32_t>(__shfl(jsafe, S::KPI * r + lrow));
-#pragma unroll
-    for (int r = 0; r < S::NLD; ++r) {
-      const int key = S::KPI * r + lrow;
-      const int seg8 = (lslot ^ mf_swz<D>(key)) * 8;
-      const bool okr = (okb >> key) & 1ull;
-      const uint16_t* ks = kbase + static_cast<uint64_t>(jr[r]) * ksn + seg8;
-      const uint16_t* vsrc = vbase + static_cast<uint64_t>(jr[r]) * vsn + seg8;
-      __builtin_amdgcn_global_load_lds(okr ? ks : kZeroRow + seg8, (lds_void_ptr)(kl + r * 1024), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(okr ? vsrc : kZeroRow + seg8, (lds_void_ptr)(vl + r * 1024), 16, 0, 0);
+  for (int r = 0; r < S::SWZ_PERIOD; ++r) seg16[r] = static_cast<uint32_t>((lslot ^ mf_swz<D>(S::KPI * r + lrow)) << 4);
+  const bool same_stride = ksn2 == vsn2;
+  auto issue = [&](int jsafe, bool full) {
+    if (same_stride) {
+      if (full) mf_issue<D, true, true>(krs, vrs, kl, vl, jsafe, lrow, ksn2, vsn2, seg16);
+      else mf_issue<D, false, true>(krs, vrs, kl, vl, jsafe, lrow, ksn2, vsn2, seg16);
+    } else {
+      if (full) mf_issue<D, true, false>(krs, vrs, kl, vl, jsafe, lrow, ksn2, vsn2, seg16);
+      else mf_issue<D, false, false>(krs, vrs, kl, vl, jsafe, lrow, ksn2, vsn2, seg16);
     }
   };
   auto chunk_ok = [&](int j) { return j >= 0 && !(p.causal && j > i); };
@@ -596,7 +639,7 @@ __global__ __launch_bounds__(kAttThreads, 2) void sparse_attention_mfma_kernel(A
     const int j0 = load_idx(0);
     const bool ok0 = chunk_ok(j0);
     okbits = __ballot(ok0);
-    issue(ok0 ? j0 : 0, okbits);
+    issue(ok0 ? j0 : -1, static_cast<uint32_t>(okbits) == 0xFFFFFFFFu);
     if (nchunks > 1) j_next = load_idx(1);
   }
   for (int ch = 0; ch < nchunks; ++ch) {
@@ -624,12 +667,13 @@ __global__ __launch_bounds__(kAttThreads, 2) void sparse_attention_mfma_kernel(A
     if (ch + 1 < nchunks) {
       const bool okn = chunk_ok(j_next);
       okbits = __ballot(okn);
-      issue(okn ? j_next : 0, okbits);
+      issue(okn ? j_next : -1, static_cast<uint32_t>(okbits) == 0xFFFFFFFFu);
       if (ch + 2 < nchunks) j_next = load_idx(ch + 2);
     }
 
     // Scores of eight keys of head c16 (keys 16t + 4*q4 + e).
     float sc[8];
+    const bool full = static_cast<uint32_t>(okb) == 0xFFFFFFFFu;
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       floatx4_t s = {0.f, 0.f, 0.f, 0.f};
@@ -638,10 +682,15 @@ __global__ __launch_bounds__(kAttThreads, 2) void sparse_attention_mfma_kernel(A
         for (int kb = 0; kb < S::KB; ++kb) s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[t][kb], qf[kb], s, 0, 0, 0);
       }
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int key = 16 * t + 4 * q4 + e;
-        sc[4 * t + e] = ((okb >> key) & 1ull) ? s[e] * p.qk_scale_log2 : -INFINITY;
-      }
+      for (int e = 0; e < 4; ++e) sc[4 * t + e] = s[e] * p.qk_scale_log2;
+    }
+    if (!full) {
+      const uint32_t mine = static_cast<uint32_t>(okb >> (4 * q4));  // bit 16t + e: key 16t + 4*q4 + e
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (!((mine >> (16 * t + e)) & 1u)) sc[4 * t + e] = -INFINITY;
     }
     float mx = sc[0];
 #pragma unroll
@@ -649,15 +698,17 @@ __global__ __launch_bounds__(kAttThreads, 2) void sparse_attention_mfma_kernel(A
     mx = fmaxf(mx, __shfl_xor(mx, 16));
     mx = fmaxf(mx, __shfl_xor(mx, 32));
     const float mnew = fmaxf(m_run, mx);
-    const bool dead = (mnew == -INFINITY);
+    // A head with no valid key yet (mnew = -inf) subtracts 0 instead: its
+    // weights exp2(-inf) are 0 and alpha multiplies an all-zero state.
     // v_exp_f32 directly: weights below 2^-126 (denormal) do not matter here.
-    const float alpha = dead ? 1.0f : __builtin_amdgcn_exp2f(m_run - mnew);
+    const float mref = (mnew == -INFINITY) ? 0.0f : mnew;
+    const float alpha = __builtin_amdgcn_exp2f(m_run - mref);
     m_run = mnew;
     float pr[8];
     float ps = 0.0f;
 #pragma unroll
     for (int x = 0; x < 8; ++x) {
-      pr[x] = dead ? 0.0f : __builtin_amdgcn_exp2f(sc[x] - mnew);
+      pr[x] = __builtin_amdgcn_exp2f(sc[x] - mref);
       ps += pr[x];
     }
     l_run = l_run * alpha + ps;
@@ -676,11 +727,13 @@ __global__ __launch_bounds__(kAttThreads, 2) void sparse_attention_mfma_kernel(A
     const float alpha_in = __uint_as_float(dpp_from_minus8(__float_as_uint(alpha)));
     const float a_row = hi_row ? alpha : alpha_in;
     const bf16x8_t pbv = __builtin_bit_cast(bf16x8_t, make_uint4(pb[0], pb[1], pb[2], pb[3]));
+    // Rescale only when some head's running max moved (alpha = 1 otherwise).
+    if (__ballot(a_row != 1.0f)) {
 #pragma unroll
-    for (int t = 0; t < S::NT; ++t) {
-      oacc[t] *= a_row;
-      oacc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vt[t], pbv, oacc[t], 0, 0, 0);
+      for (int t = 0; t < S::NT; ++t) oacc[t] *= a_row;
     }
+#pragma unroll
+    for (int t = 0; t < S::NT; ++t) oacc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vt[t], pbv, oacc[t], 0, 0, 0);
   }
 
   // l: partial sums of the four lanes holding a head's keys; O: hi row + lo row.
@@ -715,9 +768,12 @@ template <typename T, int D>
 int launch_att_d(const AttParams& p, hipStream_t st) {
   const int64_t blocks = ceil_div(p.rows, kAttWaves);
   if constexpr (sizeof(T) == 2 && D >= 64 && D <= 128) {
-    if (p.g <= 8 && p.d == D && p.k_sn >= 0 && p.k_sn < (int64_t(1) << 31) && p.v_sn >= 0 &&
-        p.v_sn < (int64_t(1) << 31)) {
-      sparse_attention_mfma_kernel<D><<<dim3(static_cast<unsigned>(blocks)), kAttThreads, 0, st>>>(p);
+    // 32-bit buffer offsets: rows below 2^31 bytes, n and byte strides below 2^24.
+    const auto fits = [&](int64_t sn) {
+      return sn >= 0 && 2 * sn < (int64_t(1) << 24) && (p.n - 1) * sn * 2 + 2 * D < (int64_t(1) << 31);
+    };
+    if (p.g <= 8 && p.d == D && p.n < (int64_t(1) << 24) && fits(p.k_sn) && fits(p.v_sn)) {
+      sparse_attention_mfma_kernel<D><<<dim3(static_cast<unsigned>(ceil_div(p.rows, kMfWaves))), 64 * kMfWaves, 0, st>>>(p);
       return check_launch("sparse_attention_mfma_kernel");
     }
   }
@@ -802,7 +858,7 @@ extern "C" int ssa_sparse_attention(const void* q, const void* k, const void* v,
   p.err = error_flag;
   p.rows = batch * h_kv * n;
   p.order = row_order;
-  if (ceil_div(p.rows, kAttWaves) >= (int64_t(1) << 31))
+  if (p.rows >= (int64_t(1) << 31))
     return fail(SSA_ERR_UNSUPPORTED, "sparse_attention: too many rows");
   hipStream_t st = as_stream(stream);
   if (dtype == SSA_DTYPE_BF16) return launch_att<uint16_t>(p, d, st);

@@ -74,3 +74,32 @@ def test_attention_int32_indices_equal_int64(dev, dtype, d, g, causal):
     kernels.sparse_attention(q, k, v, idx, None, causal, out=o64)
     kernels.sparse_attention(q, k, v, idx.to(torch.int32), None, causal, out=o32)
     assert torch.equal(o64, o32)
+
+
+@pytest.mark.parametrize("d,g", [(128, 4), (64, 8)])
+def test_attention_k_v_with_different_row_strides(dev, orc, d, g):
+    """K and V as views with different row strides (K sliced out of a wider
+    tensor), and a top_k that leaves a partial last chunk: the same output as
+    contiguous copies, and the oracle's within the bf16 tolerance."""
+    from ssa_amd import kernels
+
+    _say(f"attention strided K/V d={d} g={g}")
+    B, n, h_kv, top_k = 2, 333, 2, 77
+    q = randn((B, n, h_kv * g, d), 71, torch.bfloat16).to(dev)
+    kw = randn((B, n, 3 * h_kv, d), 72, torch.bfloat16).to(dev)
+    k = kw[:, :, h_kv:2 * h_kv]                      # row stride 3*h_kv*d
+    v = randn((B, n, h_kv, d), 73, torch.bfloat16).to(dev)
+    gi = torch.Generator().manual_seed(74)
+    idx = torch.randint(0, n, (B, n, h_kv, top_k), generator=gi).to(dev)
+    assert k.stride(1) != v.stride(1)
+    for causal in (False, True):
+        o = torch.empty(q.shape, device=dev, dtype=torch.float32)
+        oc = torch.empty_like(o)
+        kernels.sparse_attention(q, k, v, idx, None, causal, out=o)
+        kernels.sparse_attention(q, k.contiguous(), v, idx, None, causal, out=oc)
+        assert torch.equal(o, oc)
+        got = o.cpu().numpy()
+        for bb in range(B):
+            ref = orc.sparse_attention(f32(q[bb]), f32(k[bb]), f32(v[bb]), idx[bb].cpu().numpy(),
+                                       causal=causal)
+            np.testing.assert_allclose(got[bb], ref, rtol=1e-3, atol=1e-3)
