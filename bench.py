@@ -102,9 +102,11 @@ def algorithmic(cfg, n, stats_sum=None):
     out["a_bytes"] = B * n * (h_q + h_kv) * d * s + h_kv * n_c * d_s * 4 + rows * (a + b) * 4
     out["b_bytes"] = 3 * rows * b * 4 + h_kv * B * (n_c + 1) * 4
     if stats_sum is not None:
-        R, C = stats_sum
-        out["c_bytes"] = R * 4 + C * d * s + rows * (g * d * s + 3 * a * 4 + k * 4)
-        out["c_flops"] = C * 2 * d * g
+        # index order: postings, the K rows of the rescored rows' candidates and
+        # their query rows, q_codes and bucket bounds, the output row
+        R, C_r, heavy = stats_sum
+        out["c_bytes"] = R * 4 + C_r * d * s + heavy * g * d * s + rows * (3 * a * 4 + k * 4)
+        out["c_flops"] = C_r * 2 * d * g
     out["d_bytes"] = rows * (k * 4 + 2 * k * d * s + 2 * g * d * s)
     out["d_flops"] = 4 * rows * g * k * d
     return out
@@ -193,8 +195,9 @@ def stats_sums(q, k, router):
     st = st.to(torch.int64)
     C = int(st[..., 0].sum())
     R = int(st[..., 1].sum())
-    full = int((st[..., 0] >= router.top_k).sum())
-    return R, C, full, st[..., 0].numel(), (qc, kc, off, post, idx)
+    heavy = st[..., 0] > router.top_k      # index order rescores only these rows
+    C_r = int(st[..., 0][heavy].sum())
+    return R, C, int(heavy.sum()), C_r, st[..., 0].numel(), (qc, kc, off, post, idx)
 
 
 def cpu_baseline(cfg, q, k, v, router, inter, budget_s):
@@ -325,8 +328,8 @@ def main():
     print(f"workload ready: {args.config} n={cfg['n']}", file=sys.stderr, flush=True)
     wall, st = time_gpu(cfg, q, k, v, router, args.steps, args.warmup)
     ms_step = 1000.0 * wall / args.steps
-    R, C, full_rows, nrows, inter = stats_sums(q, k, router)
-    alg = algorithmic(cfg, cfg["n"], (R, C))
+    R, C, heavy_rows, C_r, nrows, inter = stats_sums(q, k, router)
+    alg = algorithmic(cfg, cfg["n"], (R, C_r, heavy_rows))
     tokens = cfg["B"] * cfg["n"]
     t_d = st["d"] / 1000.0
     d_gbs = alg["d_bytes"] / t_d / 1e9
@@ -344,7 +347,8 @@ def main():
               "frac_hbm": alg["c_bytes"] / (st["c"] / 1000) / 1e9 / HBM_PEAK_GBS,
               "order": "index (same set as by score)",
               "ms_sorted_by_score": time_sorted_select(q, k, router),
-              "postings_read": R, "candidates": C, "rows": nrows, "rows_with_k_candidates": full_rows},
+              "postings_read": R, "candidates": C, "rows": nrows,
+              "rows_rescored": heavy_rows, "candidates_rescored": C_r},
         "d": {"ms": st["d"], "gb": alg["d_bytes"] / 1e9, "frac_hbm": d_gbs / HBM_PEAK_GBS},
     }
     line = {

@@ -134,14 +134,21 @@ int ssa_query_order(const int32_t* q_codes, int64_t batch, int64_t n, int h_kv, 
  *                and padding are the same in both orders.
  *   out    [batch][n][h_kv][top_k], index type out_index_dtype
  *   mask   (SSA_MASK_DENSE only) uint8 [batch][n][n], strides (mask_sb, mask_si); mask_sb may be 0
- *   stats  (nullable) int32 [batch][h_kv][n][2] = (candidates, postings read)
+ *   stats  (nullable) int32 [batch][h_kv][n][2] = (candidates, postings read
+ *          inside the mask window: j <= i when causal, all otherwise)
+ *   workspace (nullable, ssa_select_workspace_bytes): with it, index order runs
+ *          one wave per row and hands the rows with more than k candidates to a
+ *          second pass (a list of such rows); without it, one block per row.
+ *          Results are the same either way.
  * Limits: top_k <= 4096, g = h_q/h_kv <= 16, d <= 256 (d % 8 == 0), n < 2^31. */
+size_t ssa_select_workspace_bytes(int64_t batch, int64_t n, int h_kv);
 int ssa_select(const void* q, const void* k, int dtype, int64_t batch, int64_t n, int h_q,
                int h_kv, int d, int64_t q_sb, int64_t q_sn, int64_t q_sh, int64_t k_sb,
                int64_t k_sn, int64_t k_sh, const int32_t* q_codes, int a, const int32_t* offsets,
                const int32_t* postings, int n_c, int b, int top_k, int mask_mode,
                const uint8_t* mask, int64_t mask_sb, int64_t mask_si, float score_div, int sorted,
-               void* out, int out_index_dtype, int32_t* stats, void* stream);
+               void* out, int out_index_dtype, int32_t* stats, void* workspace,
+               size_t workspace_bytes, void* stream);
 
 /* ---- stage (d): gathered exact attention -------------------------------- */
 

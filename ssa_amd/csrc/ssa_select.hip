@@ -2,9 +2,9 @@
 //
 // Replaces CodebookRouter._select_candidates / _build_candidate_mask
 // (ssa/router.py:151-259).  One 256-thread block per (batch, kv-head, query):
-//   1. the query's a buckets are clipped to keys j <= i (causal; postings
-//      ascend, so one binary search per bucket) and concatenated;
-//   2. postings stream through an n-bit LDS bitmap (atomicOr dedup);
+//   1. the query's a buckets are concatenated (a wave scan of their sizes);
+//   2. postings stream through an n-bit LDS bitmap (atomicOr dedup), keys
+//      outside the mask (j > i when causal) skipped;
 //   3. candidates are rescored in the canonical fp32 order (one thread per key:
 //      g fmaf chains over d with the query operands in scalar registers,
 //      / score_div, summed over the group, / g); composite keys that beat the
@@ -125,15 +125,18 @@ __device__ int block_exclusive_scan(int v, int* scratch, int* total) {
 }
 
 // Writes, in ascending order, the first `limit` positions j < n whose bitmap bit
-// equals `want_set` to dst[0..]; returns how many were written.
-__device__ int scan_bits(const uint32_t* bitmap, int words, int64_t n, bool want_set, int32_t* dst,
-                         int limit, int* scratch) {
+// equals `want_set` to dst[0..]; returns how many were written.  Only words
+// below `live` are stored; the rest read as zero.
+__device__ int scan_bits(const uint32_t* bitmap, int words, int live, int64_t n, bool want_set,
+                         int32_t* dst, int limit, int* scratch) {
   int filled = 0;
-  for (int w0 = 0; w0 < words && filled < limit; w0 += kSelThreads) {
+  const int wend = want_set ? live : words;
+  for (int w0 = 0; w0 < wend && filled < limit; w0 += kSelThreads) {
     const int w = w0 + threadIdx.x;
     uint32_t bits = 0u;
-    if (w < words) {
-      bits = want_set ? bitmap[w] : ~bitmap[w];
+    if (w < wend) {
+      const uint32_t stored = (w < live) ? bitmap[w] : 0u;
+      bits = want_set ? stored : ~stored;
       if (w == words - 1 && (n & 31)) bits &= (1u << (n & 31)) - 1u;
     }
     int total = 0;
@@ -185,8 +188,12 @@ __device__ __forceinline__ void rescore_row(const T* kr, const T* q0, int64_t q_
   }
 }
 
+// One row ((b * h_kv + h) * n + i) by the whole block.  `heavy`: the row is
+// known to have more than k_eff candidates (index order only), so the counting
+// pass is skipped.
 template <typename T, int GMAX, int D>
-__global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams p, const T* __restrict__ qg) {
+__device__ __forceinline__ void select_row(const SelParams& p, const T* __restrict__ qg, int64_t row,
+                                           bool heavy) {
   extern __shared__ __align__(16) unsigned char smem[];
   uint64_t* topbuf = reinterpret_cast<uint64_t*>(smem);
   const int words = static_cast<int>((p.n + 31) >> 5);
@@ -200,7 +207,6 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams p, const 
   __shared__ int s_scan[kSelThreads / 64];
 
   const int tid = threadIdx.x;
-  const int64_t row = blockIdx.x;  // ((b * h_kv + h) * n + i)
   const int64_t i = row % p.n;
   const int64_t bh = row / p.n;
   const int h = static_cast<int>(bh % p.h_kv);
@@ -211,48 +217,55 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams p, const 
   const uint8_t* mrow =
       (p.mask_mode == SSA_MASK_DENSE) ? p.mask + bb * p.mask_sb + i * p.mask_si : nullptr;
 
-  for (int w = tid; w < words; w += kSelThreads) bitmap[w] = 0u;
-  if (tid < p.a) {
-    const int32_t c = p.q_codes[(bh * p.n + i) * p.a + tid];
-    int32_t lo = 0, hi = 0;
-    if (static_cast<uint32_t>(c) < static_cast<uint32_t>(p.n_c)) {
-      const int32_t* off = p.offsets + bh * (p.n_c + 1);
-      const int32_t total = static_cast<int32_t>(p.n * p.b);
-      lo = min(max(off[c], 0), total);
-      hi = min(max(off[c + 1], lo), total);
-      if (p.mask_mode == SSA_MASK_CAUSAL) {
-        int32_t L = lo, H = hi;
-        while (L < H) {
-          const int32_t mid = (L + H) >> 1;
-          if (pp[mid] <= i) L = mid + 1;
-          else H = mid;
-        }
-        hi = L;
+  // Under the causal mask every candidate is <= i: only words up to i / 32 are
+  // ever set, so only those are cleared and scanned.
+  const int live = (p.mask_mode == SSA_MASK_CAUSAL) ? static_cast<int>(i >> 5) + 1 : words;
+  for (int w = tid; w < live; w += kSelThreads) bitmap[w] = 0u;
+  // Buckets are read whole and filtered by the mask in the union pass (no
+  // dependent search over the postings); a wave scan turns their sizes into
+  // start positions in the concatenated list.
+  if (tid < 64) {
+    int32_t lo = 0, len = 0;
+    if (tid < p.a) {
+      const int32_t c = p.q_codes[(bh * p.n + i) * p.a + tid];
+      if (static_cast<uint32_t>(c) < static_cast<uint32_t>(p.n_c)) {
+        const int32_t* off = p.offsets + bh * (p.n_c + 1);
+        const int32_t total = static_cast<int32_t>(p.n * p.b);
+        lo = min(max(off[c], 0), total);
+        len = min(max(off[c + 1], lo), total) - lo;
       }
     }
-    seg_lo[tid] = lo;
-    seg_start[tid + 1] = hi - lo;
-  }
-  if (tid == 0) {
-    s_batch_cnt = 0;
-    s_top_cnt = 0;
-    s_cand = 0;
-    s_thr = 0ull;
-    seg_start[0] = 0;
+    int32_t x = len;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int32_t y = __shfl_up(x, o, 64);
+      if (tid >= o) x += y;
+    }
+    if (tid < p.a) {
+      seg_lo[tid] = lo;
+      seg_start[tid + 1] = x;
+    }
+    if (tid == 0) {
+      seg_start[0] = 0;
+      s_R = 0;
+      s_batch_cnt = 0;
+      s_top_cnt = 0;
+      s_cand = 0;
+      s_thr = 0ull;
+    }
   }
   __syncthreads();
-  if (tid == 0) {
-    for (int m = 1; m <= p.a; ++m) seg_start[m] += seg_start[m - 1];
-    s_R = seg_start[p.a];
-  }
-  __syncthreads();
-  const int R = s_R;
+  const int R = seg_start[p.a];
+  const bool causal = p.mask_mode == SSA_MASK_CAUSAL;
 
   // Union of the row's postings into the bitmap.  With `collect`, new keys also
   // queue in the batch and are rescored whenever it fills (streaming top-k).
-  auto union_pass = [&](bool collect) {
+  // `count_raw` tallies the postings inside the causal window (all postings
+  // otherwise) for the stats.
+  auto union_pass = [&](bool collect, bool count_raw) {
     for (int base = 0; base < R; base += kSelThreads) {
       const int pidx = base + tid;
+      bool in_window = false;
       if (pidx < R) {
         int lo_m = 0, hi_m = p.a;
         while (hi_m - lo_m > 1) {
@@ -261,7 +274,8 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams p, const 
           else hi_m = mid;
         }
         const int32_t j = pp[seg_lo[lo_m] + (pidx - seg_start[lo_m])];
-        const bool allowed = (static_cast<uint32_t>(j) < static_cast<uint32_t>(p.n)) &&
+        in_window = !causal || j <= i;
+        const bool allowed = (static_cast<uint32_t>(j) < static_cast<uint32_t>(p.n)) && in_window &&
                              ((mrow == nullptr) || (mrow[j] != 0));
         if (allowed) {
           const uint32_t bit = 1u << (j & 31);
@@ -271,6 +285,10 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams p, const 
             else atomicAdd(&s_cand, 1);
           }
         }
+      }
+      if (count_raw) {
+        const uint64_t m = __ballot(in_window);
+        if ((tid & 63) == 0) atomicAdd(&s_R, __popcll(m));
       }
       __syncthreads();
       if (!collect) continue;
@@ -313,31 +331,37 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams p, const 
   };
 
   int nsel = 0;  // selected candidates at the head of `stage`
+  const bool want_stats = p.stats != nullptr;
   if (!p.sorted) {
-    union_pass(false);
-    __syncthreads();
-    const int C = s_cand;
-    __syncthreads();  // every thread holds C before thread 0 may reset s_cand below
-    if (C <= p.k_eff) {
-      nsel = scan_bits(bitmap, words, p.n, true, stage, C, s_scan);
-    } else {
-      for (int w = tid; w < words; w += kSelThreads) bitmap[w] = 0u;
-      if (tid == 0) s_cand = 0;
+    int C = p.k_eff + 1;
+    if (!heavy) {
+      union_pass(false, want_stats);
       __syncthreads();
-      union_pass(true);
+      C = s_cand;
+      __syncthreads();  // every thread holds C before thread 0 may reset s_cand below
+    }
+    if (C <= p.k_eff) {
+      nsel = scan_bits(bitmap, words, live, p.n, true, stage, C, s_scan);
+    } else {
+      if (!heavy) {
+        for (int w = tid; w < live; w += kSelThreads) bitmap[w] = 0u;
+        if (tid == 0) s_cand = 0;
+        __syncthreads();
+      }
+      union_pass(true, heavy && want_stats);
       // Selected set (top k_eff keys) in ascending index order, via the bitmap.
-      for (int w = tid; w < words; w += kSelThreads) bitmap[w] = 0u;
+      for (int w = tid; w < live; w += kSelThreads) bitmap[w] = 0u;
       __syncthreads();
       for (int e = tid; e < p.k_eff; e += kSelThreads) {
         const uint32_t j = key_index(topbuf[e]);
         atomicOr(&bitmap[j >> 5], 1u << (j & 31));
       }
       __syncthreads();
-      nsel = scan_bits(bitmap, words, p.n, true, stage, p.k_eff, s_scan);
+      nsel = scan_bits(bitmap, words, live, p.n, true, stage, p.k_eff, s_scan);
       // Restore the candidate bitmap for the filler: no filler is needed here.
     }
   } else {
-    union_pass(true);
+    union_pass(true, want_stats);
     const int tc = s_top_cnt;
     if (tc > 1) {
       const int len = pow2_at_least(tc);
@@ -350,7 +374,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams p, const 
     for (int w = tid; w < nsel; w += kSelThreads) stage[w] = static_cast<int32_t>(key_index(topbuf[w]));
   }
   __syncthreads();
-  if (nsel < p.k_eff) scan_bits(bitmap, words, p.n, false, stage + nsel, p.k_eff - nsel, s_scan);
+  if (nsel < p.k_eff) scan_bits(bitmap, words, live, p.n, false, stage + nsel, p.k_eff - nsel, s_scan);
   __syncthreads();
 
   const int64_t obase = ((bb * p.n + i) * p.h_kv + h) * p.top_k;
@@ -363,33 +387,208 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams p, const 
   }
   if (p.stats && tid == 0) {
     p.stats[(bh * p.n + i) * 2 + 0] = s_cand;
-    p.stats[(bh * p.n + i) * 2 + 1] = R;
+    p.stats[(bh * p.n + i) * 2 + 1] = s_R;
   }
 }
 
 template <typename T, int GMAX, int D>
-int launch_select(const SelParams& p, int64_t rows, size_t smem, hipStream_t st) {
+__global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams p, const T* __restrict__ qg) {
+  select_row<T, GMAX, D>(p, qg, blockIdx.x, false);
+}
+
+// The rows select_light_kernel listed (more than k_eff candidates, index
+// order): each block takes the next listed row until the list is exhausted.
+// ctr[0] = listed rows, ctr[1] = next list position (both from the light pass).
+template <typename T, int GMAX, int D>
+__global__ __launch_bounds__(kSelThreads) void select_heavy_kernel(SelParams p, const T* __restrict__ qg,
+                                                                   const int32_t* __restrict__ list,
+                                                                   int32_t* __restrict__ ctr) {
+  __shared__ int s_next;
+  const int listed = ctr[0];
+  for (;;) {
+    if (threadIdx.x == 0) s_next = atomicAdd(&ctr[1], 1);
+    __syncthreads();
+    const int r = s_next;
+    __syncthreads();  // every thread holds r before thread 0 takes the next one
+    if (r >= listed) break;
+    select_row<T, GMAX, D>(p, qg, list[r], true);
+    __syncthreads();  // the next row reuses the LDS
+  }
+}
+
+// Index-order rows, one wave per row, no block barriers: the row's buckets go
+// through the wave's LDS bitmap; a row with at most k_eff candidates writes its
+// candidates ascending and the filler directly; a row with more is appended
+// to `list` (ctr[0] counts them) for select_heavy_kernel.
+constexpr int kLightWaves = 4;
+
+__device__ __forceinline__ int wave_excl_scan(int v, int lane, int* total) {
+  int x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  *total = __shfl(x, 63);
+  return x - v;
+}
+
+__global__ __launch_bounds__(64 * kLightWaves) void select_light_kernel(SelParams p, int64_t rows,
+                                                                        int32_t* __restrict__ list,
+                                                                        int32_t* __restrict__ ctr) {
+  extern __shared__ __align__(16) uint32_t lbits[];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * kLightWaves + wave;
+  if (row >= rows) return;
+  const int words = static_cast<int>((p.n + 31) >> 5);
+  uint32_t* bm = lbits + static_cast<int64_t>(wave) * words;
+  const int64_t i = row % p.n;
+  const int64_t bh = row / p.n;
+  const int h = static_cast<int>(bh % p.h_kv);
+  const int64_t bb = bh / p.h_kv;
+  const int32_t* pp = p.postings + bh * p.n * p.b;
+  const bool causal = p.mask_mode == SSA_MASK_CAUSAL;
+  const uint8_t* mrow = (p.mask_mode == SSA_MASK_DENSE) ? p.mask + bb * p.mask_sb + i * p.mask_si : nullptr;
+  const int live = causal ? static_cast<int>(i >> 5) + 1 : words;
+  for (int w = lane; w < live; w += 64) bm[w] = 0u;
+
+  int32_t lo = 0, len = 0;
+  if (lane < p.a) {
+    const int32_t c = p.q_codes[(bh * p.n + i) * p.a + lane];
+    if (static_cast<uint32_t>(c) < static_cast<uint32_t>(p.n_c)) {
+      const int32_t* off = p.offsets + bh * (p.n_c + 1);
+      const int32_t total = static_cast<int32_t>(p.n * p.b);
+      lo = min(max(off[c], 0), total);
+      len = min(max(off[c + 1], lo), total) - lo;
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+  int fresh = 0, seen = 0;  // per lane: new keys, postings inside the window
+  for (int m = 0; m < p.a; ++m) {
+    const int lo_m = __shfl(lo, m), len_m = __shfl(len, m);
+    for (int base = 0; base < len_m; base += 64) {
+      if (base + lane < len_m) {
+        const int32_t j = pp[lo_m + base + lane];
+        const bool in_window = !causal || j <= i;
+        seen += in_window ? 1 : 0;
+        if (static_cast<uint32_t>(j) < static_cast<uint32_t>(p.n) && in_window &&
+            (mrow == nullptr || mrow[j] != 0)) {
+          const uint32_t bit = 1u << (j & 31);
+          if (!(atomicOr(&bm[j >> 5], bit) & bit)) ++fresh;
+        }
+      }
+    }
+  }
+  int C = 0, raw = 0;
+  wave_excl_scan(fresh, lane, &C);
+  if (p.stats) wave_excl_scan(seen, lane, &raw);
+  if (p.stats && lane == 0) {
+    p.stats[(bh * p.n + i) * 2 + 0] = C;
+    p.stats[(bh * p.n + i) * 2 + 1] = raw;
+  }
+  if (C > p.k_eff) {
+    if (lane == 0) list[atomicAdd(&ctr[0], 1)] = static_cast<int32_t>(row);
+    return;
+  }
+  __builtin_amdgcn_wave_barrier();
+
+  const int64_t obase = ((bb * p.n + i) * p.h_kv + h) * p.top_k;
+  int32_t* o32 = static_cast<int32_t*>(p.out) + obase;
+  int64_t* o64 = static_cast<int64_t*>(p.out) + obase;
+  auto put = [&](int pos, int32_t v) {
+    if (p.out_i64) o64[pos] = v;
+    else o32[pos] = v;
+  };
+  // Candidates ascending, then the lowest non-candidates up to k_eff.
+  int filled = 0;
+  for (int w0 = 0; w0 < live && filled < C; w0 += 64) {
+    const int w = w0 + lane;
+    uint32_t bits = (w < live) ? bm[w] : 0u;
+    int total = 0;
+    int pos = filled + wave_excl_scan(__popc(bits), lane, &total);
+    while (bits != 0u) {
+      put(pos++, w * 32 + __ffs(bits) - 1);
+      bits &= bits - 1u;
+    }
+    filled += total;
+  }
+  for (int w0 = 0; filled < p.k_eff; w0 += 64) {
+    const int w = w0 + lane;
+    uint32_t bits = 0u;
+    if (w < words) {
+      bits = ~((w < live) ? bm[w] : 0u);
+      if (w == words - 1 && (p.n & 31)) bits &= (1u << (p.n & 31)) - 1u;
+    }
+    int total = 0;
+    int pos = filled + wave_excl_scan(__popc(bits), lane, &total);
+    while (bits != 0u && pos < p.k_eff) {
+      put(pos++, w * 32 + __ffs(bits) - 1);
+      bits &= bits - 1u;
+    }
+    filled += total;
+  }
+  for (int w = p.k_eff + lane; w < p.top_k; w += 64) put(w, 0);
+}
+
+__global__ void zero_ctr_kernel(int32_t* __restrict__ ctr) {
+  if (threadIdx.x < 2) ctr[threadIdx.x] = 0;
+}
+
+size_t light_smem(int64_t n) { return sizeof(uint32_t) * kLightWaves * static_cast<size_t>((n + 31) / 32); }
+
+int heavy_grid(int64_t rows) {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (cus[dev] == 0) {
+    int c = 0;
+    if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) c = 256;
+    cus[dev] = c;
+  }
+  const int64_t g = static_cast<int64_t>(cus[dev]) * 8;
+  return static_cast<int>(rows < g ? rows : g);
+}
+
+// ws (nullable): index order through the light/heavy pair; otherwise one block
+// per row.
+template <typename T, int GMAX, int D>
+int launch_select(const SelParams& p, int64_t rows, size_t smem, int32_t* ws, hipStream_t st) {
   auto kern = select_kernel<T, GMAX, D>;
   if (int s = reserve_lds(reinterpret_cast<const void*>(kern), smem, "select")) return s;
-  kern<<<dim3(static_cast<unsigned>(rows)), kSelThreads, smem, st>>>(p, static_cast<const T*>(p.q));
-  return check_launch("select_kernel");
+  const T* qg = static_cast<const T*>(p.q);
+  if (ws == nullptr || p.sorted || light_smem(p.n) > 64 * 1024) {
+    kern<<<dim3(static_cast<unsigned>(rows)), kSelThreads, smem, st>>>(p, qg);
+    return check_launch("select_kernel");
+  }
+  int32_t* ctr = ws;
+  int32_t* list = ws + 64;
+  zero_ctr_kernel<<<1, 64, 0, st>>>(ctr);
+  if (int s = check_launch("zero_ctr_kernel")) return s;
+  select_light_kernel<<<dim3(static_cast<unsigned>(ceil_div(rows, kLightWaves))), 64 * kLightWaves,
+                        light_smem(p.n), st>>>(p, rows, list, ctr);
+  if (int s = check_launch("select_light_kernel")) return s;
+  auto hk = select_heavy_kernel<T, GMAX, D>;
+  if (int s = reserve_lds(reinterpret_cast<const void*>(hk), smem, "select")) return s;
+  hk<<<dim3(static_cast<unsigned>(heavy_grid(rows))), kSelThreads, smem, st>>>(p, qg, list, ctr);
+  return check_launch("select_heavy_kernel");
 }
 
 template <typename T, int GMAX>
-int dispatch_select_d(const SelParams& p, int64_t rows, size_t smem, hipStream_t st) {
+int dispatch_select_d(const SelParams& p, int64_t rows, size_t smem, int32_t* ws, hipStream_t st) {
   switch (p.d) {
-    case 64: return launch_select<T, GMAX, 64>(p, rows, smem, st);
-    case 128: return launch_select<T, GMAX, 128>(p, rows, smem, st);
-    case 256: return launch_select<T, GMAX, 256>(p, rows, smem, st);
-    default: return launch_select<T, GMAX, 0>(p, rows, smem, st);
+    case 64: return launch_select<T, GMAX, 64>(p, rows, smem, ws, st);
+    case 128: return launch_select<T, GMAX, 128>(p, rows, smem, ws, st);
+    case 256: return launch_select<T, GMAX, 256>(p, rows, smem, ws, st);
+    default: return launch_select<T, GMAX, 0>(p, rows, smem, ws, st);
   }
 }
 
 template <typename T>
-int dispatch_select(const SelParams& p, int64_t rows, size_t smem, hipStream_t st) {
-  if (p.g <= 4) return dispatch_select_d<T, 4>(p, rows, smem, st);
-  if (p.g <= 8) return dispatch_select_d<T, 8>(p, rows, smem, st);
-  return dispatch_select_d<T, 16>(p, rows, smem, st);
+int dispatch_select(const SelParams& p, int64_t rows, size_t smem, int32_t* ws, hipStream_t st) {
+  if (p.g <= 4) return dispatch_select_d<T, 4>(p, rows, smem, ws, st);
+  if (p.g <= 8) return dispatch_select_d<T, 8>(p, rows, smem, ws, st);
+  return dispatch_select_d<T, 16>(p, rows, smem, ws, st);
 }
 
 }  // namespace
@@ -397,13 +596,19 @@ int dispatch_select(const SelParams& p, int64_t rows, size_t smem, hipStream_t s
 
 using namespace ssa;
 
+extern "C" size_t ssa_select_workspace_bytes(int64_t batch, int64_t n, int h_kv) {
+  if (batch < 0 || n < 0 || h_kv <= 0) return 0;
+  return align_up(256 + sizeof(int32_t) * static_cast<size_t>(batch * h_kv * n), 256);
+}
+
 extern "C" int ssa_select(const void* q, const void* k, int dtype, int64_t batch, int64_t n,
                           int h_q, int h_kv, int d, int64_t q_sb, int64_t q_sn, int64_t q_sh,
                           int64_t k_sb, int64_t k_sn, int64_t k_sh, const int32_t* q_codes, int a,
                           const int32_t* offsets, const int32_t* postings, int n_c, int b,
                           int top_k, int mask_mode, const uint8_t* mask, int64_t mask_sb,
                           int64_t mask_si, float score_div, int sorted, void* out,
-                          int out_index_dtype, int32_t* stats, void* stream) {
+                          int out_index_dtype, int32_t* stats, void* workspace,
+                          size_t workspace_bytes, void* stream) {
   if (dtype != SSA_DTYPE_F32 && dtype != SSA_DTYPE_BF16)
     return fail(SSA_ERR_UNSUPPORTED, "select: dtype %d not supported (f32, bf16)", dtype);
   if (batch < 0 || n < 0 || h_q <= 0 || h_kv <= 0 || d <= 0 || a <= 0 || b <= 0 || n_c <= 0 ||
@@ -429,6 +634,9 @@ extern "C" int ssa_select(const void* q, const void* k, int dtype, int64_t batch
   if ((k_sn % vec) || (k_sh % vec) || (k_sb % vec) || (reinterpret_cast<uintptr_t>(k) % 16) ||
       (q_sn % vec) || (q_sh % vec) || (q_sb % vec) || (reinterpret_cast<uintptr_t>(q) % 16))
     return fail(SSA_ERR_UNSUPPORTED, "select: q and k rows must be 16-byte aligned");
+  if (workspace && workspace_bytes < ssa_select_workspace_bytes(batch, n, h_kv))
+    return fail(SSA_ERR_WORKSPACE, "select: workspace %zu < %zu bytes", workspace_bytes,
+                ssa_select_workspace_bytes(batch, n, h_kv));
   if (batch == 0 || n == 0) return SSA_OK;
   if (!q || !k || !q_codes || !offsets || !postings || !out)
     return fail(SSA_ERR_INVALID_ARGUMENT, "select: null pointer");
@@ -467,6 +675,7 @@ extern "C" int ssa_select(const void* q, const void* k, int dtype, int64_t batch
   const int64_t rows = batch * h_kv * n;
   if (rows >= (int64_t(1) << 31)) return fail(SSA_ERR_UNSUPPORTED, "select: too many rows");
   hipStream_t st = as_stream(stream);
-  if (dtype == SSA_DTYPE_BF16) return dispatch_select<uint16_t>(p, rows, smem, st);
-  return dispatch_select<float>(p, rows, smem, st);
+  int32_t* ws = static_cast<int32_t*>(workspace);
+  if (dtype == SSA_DTYPE_BF16) return dispatch_select<uint16_t>(p, rows, smem, ws, st);
+  return dispatch_select<float>(p, rows, smem, ws, st);
 }

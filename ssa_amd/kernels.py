@@ -131,13 +131,15 @@ def select(q: torch.Tensor, k: torch.Tensor, q_codes: torch.Tensor, offsets: tor
            postings: torch.Tensor, b: int, top_k: int, mask_mode: int = _lib.MASK_CAUSAL,
            mask: Optional[torch.Tensor] = None, score_div: Optional[float] = None,
            index_dtype: torch.dtype = torch.int64,
-           with_stats: bool = False, sorted: bool = True):
+           with_stats: bool = False, sorted: bool = True, use_workspace: bool = True):
     """Stage (c): candidate indices [B, n, h_kv, top_k] (ssa/router.py:151-214).
 
     ``mask`` (MASK_DENSE) is a bool/uint8 ``[n, n]`` or ``[B, n, n]`` tensor with a
     contiguous last dimension.  ``with_stats`` also returns int32 ``[B, h_kv, n, 2]``
-    (unique candidates, postings read) per row.  ``sorted=False`` lists the same
-    selected set in ascending index order (then the same filler).
+    (unique candidates, postings read inside the mask window) per row.
+    ``sorted=False`` lists the same selected set in ascending index order (then
+    the same filler).  ``use_workspace=False`` runs the one-block-per-row kernel
+    for every row (same results).
     """
     _check_rows(q, "q")
     _check_rows(k, "k")
@@ -163,11 +165,15 @@ def select(q: torch.Tensor, k: torch.Tensor, q_codes: torch.Tensor, offsets: tor
             m_sb, m_si = mask.stride(0), mask.stride(1)
     out = torch.empty((B, n, h_kv, top_k), device=q.device, dtype=index_dtype)
     stats = torch.empty((B, h_kv, n, 2), device=q.device, dtype=torch.int32) if with_stats else None
+    ws_bytes, ws = 0, None
+    if use_workspace:
+        ws_bytes = int(_lib.load().ssa_select_workspace_bytes(B, n, h_kv))
+        ws = torch.empty(max(ws_bytes, 1), device=q.device, dtype=torch.uint8)
     call("ssa_select", ptr(q), ptr(k), _lib.elem_dtype(q), B, n, h_q, h_kv, d,
          q.stride(0), q.stride(1), q.stride(2), k.stride(0), k.stride(1), k.stride(2),
          ptr(q_codes), a, ptr(offsets), ptr(postings), n_c, b, top_k, mask_mode, ptr(mask),
          m_sb, m_si, float(score_div), int(bool(sorted)), ptr(out), _lib.index_dtype(out),
-         ptr(stats), stream_of(q))
+         ptr(stats), ptr(ws), ws_bytes, stream_of(q))
     return (out, stats) if with_stats else out
 
 

@@ -57,7 +57,7 @@ def L():
 
 def test_header_parses_every_entry_point():
     decls = _declarations()
-    assert len(decls) == 15
+    assert len(decls) == 16
     assert set(decls) == set(_lib.SIGNATURES)
 
 
@@ -87,7 +87,8 @@ def _select(L, **kw):
              q_sb=1024 * 32 * 128, q_sn=32 * 128, q_sh=128, k_sb=1024 * 8 * 128, k_sn=8 * 128,
              k_sh=128, q_codes=FAKE, a=16, offsets=FAKE, postings=FAKE, n_c=4096, b=4, top_k=512,
              mask_mode=_lib.MASK_CAUSAL, mask=NULL, mask_sb=0, mask_si=0, score_div=11.3137,
-             sorted=0, out=FAKE, out_index_dtype=_lib.INDEX_I64, stats=NULL, stream=NULL)
+             sorted=0, out=FAKE, out_index_dtype=_lib.INDEX_I64, stats=NULL, workspace=NULL,
+             workspace_bytes=0, stream=NULL)
     a.update(kw)
     st = L.ssa_select(*a.values())
     return st, (L.ssa_last_error() or b"").decode()
@@ -110,11 +111,20 @@ def _select(L, **kw):
     (dict(postings=NULL), _lib.SSA_ERR_INVALID_ARGUMENT, "null"),
     (dict(n=1 << 29, b=4), _lib.SSA_ERR_UNSUPPORTED, "2^31"),
     (dict(n=1 << 26, b=4), _lib.SSA_ERR_UNSUPPORTED, "LDS"),
+    (dict(workspace=FAKE, workspace_bytes=1024), _lib.SSA_ERR_WORKSPACE, "workspace"),
 ])
 def test_select_rejects(L, kw, status, text):
     st, msg = _select(L, **kw)
     assert st == status, msg
     assert text in msg
+
+
+def test_select_workspace_size(L):
+    # counters (256 B) + one int32 per (batch, kv head, query) row, 256-byte aligned
+    assert L.ssa_select_workspace_bytes(2, 1000, 8) == 256 + 2 * 8 * 1000 * 4
+    assert L.ssa_select_workspace_bytes(1, 1, 1) == 512
+    assert _select(L, workspace=FAKE, workspace_bytes=L.ssa_select_workspace_bytes(1, 1024, 8),
+                   postings=NULL)[0] == _lib.SSA_ERR_INVALID_ARGUMENT
 
 
 def test_select_empty_is_noop(L):

@@ -31,6 +31,9 @@ def c3(dev):
     idx_s, st = kernels.select(q, k, qc, off, post, cfg["b"], cfg["k"], with_stats=True, sorted=True)
     idx_u = kernels.select(q, k, qc, off, post, cfg["b"], cfg["k"], sorted=False)
     idx_u2 = kernels.select(q, k, qc, off, post, cfg["b"], cfg["k"], sorted=False)
+    idx_ub, st_ub = kernels.select(q, k, qc, off, post, cfg["b"], cfg["k"], sorted=False,
+                                   with_stats=True, use_workspace=False)
+    _, st_u = kernels.select(q, k, qc, off, post, cfg["b"], cfg["k"], sorted=False, with_stats=True)
     idx_s2 = kernels.select(q, k, qc, off, post, cfg["b"], cfg["k"], sorted=True)
     out = torch.empty(q.shape, device=dev, dtype=torch.float32)
     kernels.sparse_attention(q, k, v, idx_u, None, True, out=out)
@@ -40,7 +43,8 @@ def c3(dev):
     torch.cuda.synchronize()
     print("config3: GPU pipeline done", flush=True)
     return dict(cfg=cfg, q=q, k=k, v=v, router=router, qc=qc, kc=kc, off=off, post=post,
-                idx_s=idx_s, idx_u=idx_u, idx_s2=idx_s2, idx_u2=idx_u2, stats=st, out=out,
+                idx_s=idx_s, idx_u=idx_u, idx_s2=idx_s2, idx_u2=idx_u2, idx_ub=idx_ub, st_u=st_u,
+                st_ub=st_ub, stats=st, out=out,
                 order=order, out_ord=out_ord)
 
 
@@ -53,6 +57,14 @@ def test_c3_row_order_changes_nothing(c3):
     first = c3["qc"][0][:, :, 0].gather(1, order)        # best code along the order
     assert bool((first[:, 1:] >= first[:, :-1]).all()), "order groups rows by ascending code"
     assert torch.equal(c3["out"], c3["out_ord"])
+
+
+def test_c3_select_light_heavy_equals_block_path(c3):
+    """Index order through the wave-per-row pass plus the listed heavy rows gives
+    the same indices and stats as one block per row."""
+    assert torch.equal(c3["idx_u"], c3["idx_ub"])
+    assert torch.equal(c3["st_u"], c3["st_ub"])
+    assert torch.equal(c3["st_u"], c3["stats"])  # sorted order counts the same
 
 
 def test_c3_select_deterministic(c3):
