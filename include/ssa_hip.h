@@ -136,12 +136,17 @@ int ssa_query_order(const int32_t* q_codes, int64_t batch, int64_t n, int h_kv, 
  *   mask   (SSA_MASK_DENSE only) uint8 [batch][n][n], strides (mask_sb, mask_si); mask_sb may be 0
  *   stats  (nullable) int32 [batch][h_kv][n][2] = (candidates, postings read
  *          inside the mask window: j <= i when causal, all otherwise)
- *   workspace (nullable, ssa_select_workspace_bytes): with it, index order runs
- *          one wave per row and hands the rows with more than k candidates to a
- *          second pass (a list of such rows); without it, one block per row.
- *          Results are the same either way.
+ *   workspace (nullable): with it, index order runs one wave per row; a row
+ *          with more than k candidates leaves its candidate list in the
+ *          workspace, which bf16 inputs with d = 64 or 128 then screen on the
+ *          matrix cores (approximate scores with a proven error bound; only the
+ *          keys near the k-th score are rescored exactly), and the remaining
+ *          such rows (lists that do not fit, other types) take an exact
+ *          one-block-per-row pass.  ssa_select_workspace_bytes(.., top_k) is
+ *          the recommended size, (.., 0) the minimum (no lists).  Without a
+ *          workspace, one block per row.  Results are identical in every case.
  * Limits: top_k <= 4096, g = h_q/h_kv <= 16, d <= 256 (d % 8 == 0), n < 2^31. */
-size_t ssa_select_workspace_bytes(int64_t batch, int64_t n, int h_kv);
+size_t ssa_select_workspace_bytes(int64_t batch, int64_t n, int h_kv, int top_k);
 int ssa_select(const void* q, const void* k, int dtype, int64_t batch, int64_t n, int h_q,
                int h_kv, int d, int64_t q_sb, int64_t q_sn, int64_t q_sh, int64_t k_sb,
                int64_t k_sn, int64_t k_sh, const int32_t* q_codes, int a, const int32_t* offsets,

@@ -13,12 +13,11 @@
 // `scale_div` is the reference's `scale` (a divisor).  Duplicated indices count
 // twice, as in the reference.
 #include "ssa_common.h"
+#include "ssa_rows.h"
 
 namespace ssa {
 namespace {
 
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef float floatx4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kAttWaves = 4;
 constexpr int kAttThreads = 64 * kAttWaves;
@@ -463,46 +462,11 @@ __global__ __launch_bounds__(kAttThreads, (AttMinBlocks<T, D, GMAX>::value)) voi
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef short v4i16_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4i16_t* lds_v4i16_ptr;
-typedef __attribute__((address_space(3))) bf16x8_t* lds_bf16x8_ptr;
-typedef __attribute__((address_space(3))) void* lds_void_ptr;
-
-constexpr int kMfChunk = 32;
 // Waves per block and blocks per CU of the matrix-core kernel.  Each wave keeps
 // one chunk (16 KB at d = 128) of K and V in flight in its LDS slices, so the
 // bytes in flight per CU are LDS-bound.
 constexpr int kMfWaves = 4;
 constexpr int kMfMinBlocks = 2;
-
-// Raw buffer descriptor word 3 for gfx9-family loads (32-bit data format),
-// and a byte offset past any buffer this kernel builds (an out-of-range buffer
-// load returns zeros, also into LDS).
-constexpr int kBufferWord3 = 0x00020000;
-constexpr uint32_t kOobOffset = 0x7FFFFFF0u;
-
-template <int D>
-struct MfShape {
-  static constexpr int KB = D / 32;           // 32-dim blocks of Q.K
-  static constexpr int NT = D / 16;           // 16-feature tiles of P.V
-  static constexpr int ROW = 2 * D;           // bytes per staged row
-  static constexpr int SEGS = D / 8;          // 16-byte segments per row
-  static constexpr int KPI = 64 / SEGS;       // rows per wave-wide load (KPI * ROW = 1 KB)
-  static constexpr int NLD = kMfChunk / KPI;  // loads per chunk, each for K and V
-  static constexpr int RPL = 256 / ROW;       // rows per 256-byte bank line
-  static constexpr int SWZ_PERIOD = (D == 128) ? 4 : 2;  // mf_swz of load r repeats with this period
-  static_assert(D == 64 || D == 128, "matrix-core attention kernel: d = 64 or 128");
-};
-
-// LDS slot of segment s of chunk row `key` is s ^ mf_swz(key).  With u = key /
-// RPL (rows of one bank line share u), swz = 2*(u mod SEGS/2) + (u / (SEGS/2)
-// mod 2): the 16 rows of a K fragment read (one segment each) hit 16 distinct
-// 16-byte bank groups, and the four rows of a transposing V read (two adjacent
-// segments each) hit four distinct 32-byte groups.
-template <int D>
-__device__ __forceinline__ int mf_swz(int key) {
-  using S = MfShape<D>;
-  const int u = key / S::RPL;
-  return ((u & (S::SEGS / 2 - 1)) << 1) | ((u / (S::SEGS / 2)) & 1);
-}
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   const bf16x2_t v = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
@@ -544,10 +508,6 @@ __device__ __forceinline__ void mf_issue(__amdgpu_buffer_rsrc_t krs, __amdgpu_bu
     __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_void_ptr)(vl + r * 1024), 16, static_cast<int>(vo), 0, 0, 0);
   }
 }
-
-// s_waitcnt encodings (gfx9): vmcnt(0) alone, lgkmcnt(0) alone.
-constexpr int kWaitVm0 = 0x0F70;
-constexpr int kWaitLgkm0 = 0xC07F;
 
 template <int D>
 __global__ __launch_bounds__(64 * kMfWaves, kMfMinBlocks) void sparse_attention_mfma_kernel(AttParams p) {

@@ -1,0 +1,88 @@
+// Gathers of whole bf16 rows (K / V rows picked by index) into LDS, shared by
+// the attention kernel and the candidate screen of stage (c).
+//
+// A wave-wide buffer_load_dwordx4 ... lds moves 1 KB: lane l's 16 bytes land
+// at the load's LDS base + 16*l.  Loads that move whole rows (4 rows of 256 B
+// at d = 128) are the shape the texture path moves fastest; a load touching
+// 16 rows x 64 B moves bytes about 3x slower from L2.
+#pragma once
+
+#include "ssa_common.h"
+
+namespace ssa {
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float floatx4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) bf16x8_t* lds_bf16x8_ptr;
+typedef __attribute__((address_space(3))) void* lds_void_ptr;
+
+constexpr int kMfChunk = 32;  // keys gathered per chunk
+
+// Raw buffer descriptor word 3 for gfx9-family loads (32-bit data format),
+// and a byte offset past any buffer this kernel builds (an out-of-range buffer
+// load returns zeros, also into LDS).
+constexpr int kBufferWord3 = 0x00020000;
+constexpr uint32_t kOobOffset = 0x7FFFFFF0u;
+
+template <int D>
+struct MfShape {
+  static constexpr int KB = D / 32;           // 32-dim blocks of Q.K
+  static constexpr int NT = D / 16;           // 16-feature tiles of P.V
+  static constexpr int ROW = 2 * D;           // bytes per staged row
+  static constexpr int SEGS = D / 8;          // 16-byte segments per row
+  static constexpr int KPI = 64 / SEGS;       // rows per wave-wide load (KPI * ROW = 1 KB)
+  static constexpr int NLD = kMfChunk / KPI;  // loads per chunk, each for K and V
+  static constexpr int RPL = 256 / ROW;       // rows per 256-byte bank line
+  static constexpr int SWZ_PERIOD = (D == 128) ? 4 : 2;  // mf_swz of load r repeats with this period
+  static_assert(D == 64 || D == 128, "row gathers: d = 64 or 128");
+};
+
+// LDS slot of segment s of chunk row `key` is s ^ mf_swz(key).  With u = key /
+// RPL (rows of one bank line share u), swz = 2*(u mod SEGS/2) + (u / (SEGS/2)
+// mod 2): the 16 rows of a K fragment read (one segment each) hit 16 distinct
+// 16-byte bank groups, and the four rows of a transposing V read (two adjacent
+// segments each) hit four distinct 32-byte groups.
+template <int D>
+__device__ __forceinline__ int mf_swz(int key) {
+  using S = MfShape<D>;
+  const int u = key / S::RPL;
+  return ((u & (S::SEGS / 2 - 1)) << 1) | ((u / (S::SEGS / 2)) & 1);
+}
+
+// Byte offset within its row of the segment lane `lane` fetches in load r of a
+// chunk (slot lane % SEGS of chunk row KPI*r + lane / SEGS); periodic in r.
+template <int D>
+__device__ __forceinline__ void row_seg16(int lane, uint32_t (&seg16)[MfShape<D>::SWZ_PERIOD]) {
+  using S = MfShape<D>;
+#pragma unroll
+  for (int r = 0; r < S::SWZ_PERIOD; ++r)
+    seg16[r] = static_cast<uint32_t>(((lane % S::SEGS) ^ mf_swz<D>(S::KPI * r + lane / S::SEGS)) << 4);
+}
+
+// One chunk of rows of one tensor into LDS at `l` (load r at l + r KB).
+// jsafe (lanes < kMfChunk): the row index per chunk slot, negative for a slot
+// that must read as zeros; sn2: the row stride in bytes.
+template <int D>
+__device__ __forceinline__ void row_issue(__amdgpu_buffer_rsrc_t rs, unsigned char* l, int jsafe, int lane,
+                                          uint32_t sn2, const uint32_t (&seg16)[MfShape<D>::SWZ_PERIOD]) {
+  using S = MfShape<D>;
+  int jr[S::NLD];
+#pragma unroll
+  for (int r = 0; r < S::NLD; ++r) jr[r] = __shfl(jsafe, S::KPI * r + lane / S::SEGS);
+#pragma unroll
+  for (int r = 0; r < S::NLD; ++r) {
+    const uint32_t o = jr[r] >= 0 ? __umul24(static_cast<uint32_t>(jr[r]), sn2) + seg16[r % S::SWZ_PERIOD]
+                                  : kOobOffset;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_ptr)(l + r * 1024), 16, static_cast<int>(o), 0, 0, 0);
+  }
+}
+
+// s_waitcnt encodings (gfx9): vmcnt(0) alone, lgkmcnt(0) alone; vmcnt(N) for
+// N < 16 is kWaitVmBase | N.
+constexpr int kWaitVm0 = 0x0F70;
+constexpr int kWaitVmBase = 0x0F70;
+constexpr int kWaitLgkm0 = 0xC07F;
+
+}  // namespace
+}  // namespace ssa

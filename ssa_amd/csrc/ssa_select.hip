@@ -20,6 +20,7 @@
 //              this order (their set is every candidate), so only rows with
 //              more than k candidates are rescored.
 #include "ssa_common.h"
+#include "ssa_rows.h"
 
 namespace ssa {
 namespace {
@@ -50,6 +51,7 @@ struct SelParams {
   void* out;
   int out_i64;
   int32_t* stats;
+  int64_t rows;  // batch * h_kv * n
 };
 
 __host__ __device__ inline int pow2_at_least(int v) {
@@ -396,30 +398,65 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams p, const 
   select_row<T, GMAX, D>(p, qg, blockIdx.x, false);
 }
 
-// The rows select_light_kernel listed (more than k_eff candidates, index
-// order): each block takes the next listed row until the list is exhausted.
-// ctr[0] = listed rows, ctr[1] = next list position (both from the light pass).
+// Workspace of index order (carve_sel_ws).  Rows with more than k candidates
+// are listed in kShards shards (light-pass block b writes shard b % kShards),
+// each with its own counters and slice of the list space, so no counter is hit
+// by more than a 1/kShards share of the rows.
+//   ctr    int32: [0] rows for the exact pass, [1] its cursor; shard s at
+//          ctr + 16 + 4 s: [0] screened rows, [2..3] int64 list entries used
+//   exact  int32 [rows]: rows for select_heavy_kernel
+//   scr    int32 [kShards][shard_rows][3]: (row, list offset, candidates)
+//   cand   int32 [kShards][cap]: screened rows' candidates, ascending
+//   approx float [kShards][cap]: their approximate scores
+constexpr int kShards = 64;
+constexpr int kScrWaves = 4;    // waves per block of the screen
+constexpr int kScrBorder = 64;  // keys near the k-th score rescored exactly per row (more: exact pass)
+constexpr int kScrRegs = 48;    // scores held per lane: rows of at most 64 * kScrRegs candidates
+
+struct SelWs {
+  int32_t* ctr;
+  int32_t* exact;
+  int32_t* scr;
+  int32_t* cand;
+  float* approx;
+  float* emax;         // [kShards][shard_rows]: the screen's error bound per row (inf: exact pass)
+  int64_t shard_rows;  // scr entries per shard
+  int64_t cap;         // list entries per shard (0: no screen)
+};
+
+constexpr size_t kSelCtrBytes = 2048;
+static_assert(sizeof(int32_t) * (16 + 4 * kShards) <= kSelCtrBytes, "counter region too small");
+
+// Appends a row for the exact pass (every row is appended at most once, so the
+// list of `rows` entries cannot overflow; the check keeps any write in bounds).
+__device__ __forceinline__ void push_exact(const SelWs& w, int64_t rows, int64_t row) {
+  const int x = atomicAdd(&w.ctr[0], 1);
+  if (x >= 0 && x < rows) w.exact[x] = static_cast<int32_t>(row);
+}
+
+// The rows listed for the exact pass: each block takes the next listed row
+// until the list is exhausted (ctr[0] rows, cursor ctr[1]).
 template <typename T, int GMAX, int D>
 __global__ __launch_bounds__(kSelThreads) void select_heavy_kernel(SelParams p, const T* __restrict__ qg,
-                                                                   const int32_t* __restrict__ list,
-                                                                   int32_t* __restrict__ ctr) {
+                                                                   SelWs w) {
   __shared__ int s_next;
-  const int listed = ctr[0];
+  const int listed = static_cast<int>(min(static_cast<int64_t>(w.ctr[0]), p.rows));
   for (;;) {
-    if (threadIdx.x == 0) s_next = atomicAdd(&ctr[1], 1);
+    if (threadIdx.x == 0) s_next = atomicAdd(&w.ctr[1], 1);
     __syncthreads();
     const int r = s_next;
     __syncthreads();  // every thread holds r before thread 0 takes the next one
     if (r >= listed) break;
-    select_row<T, GMAX, D>(p, qg, list[r], true);
+    select_row<T, GMAX, D>(p, qg, w.exact[r], true);
     __syncthreads();  // the next row reuses the LDS
   }
 }
 
 // Index-order rows, one wave per row, no block barriers: the row's buckets go
 // through the wave's LDS bitmap; a row with at most k_eff candidates writes its
-// candidates ascending and the filler directly; a row with more is appended
-// to `list` (ctr[0] counts them) for select_heavy_kernel.
+// candidates ascending and the filler directly.  A row with more writes its
+// candidate list into the workspace for select_screen_kernel when it fits
+// (w.cap), and is listed for the exact pass otherwise.
 constexpr int kLightWaves = 4;
 
 __device__ __forceinline__ int wave_excl_scan(int v, int lane, int* total) {
@@ -433,9 +470,7 @@ __device__ __forceinline__ int wave_excl_scan(int v, int lane, int* total) {
   return x - v;
 }
 
-__global__ __launch_bounds__(64 * kLightWaves) void select_light_kernel(SelParams p, int64_t rows,
-                                                                        int32_t* __restrict__ list,
-                                                                        int32_t* __restrict__ ctr) {
+__global__ __launch_bounds__(64 * kLightWaves) void select_light_kernel(SelParams p, int64_t rows, SelWs w) {
   extern __shared__ __align__(16) uint32_t lbits[];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -451,7 +486,7 @@ __global__ __launch_bounds__(64 * kLightWaves) void select_light_kernel(SelParam
   const bool causal = p.mask_mode == SSA_MASK_CAUSAL;
   const uint8_t* mrow = (p.mask_mode == SSA_MASK_DENSE) ? p.mask + bb * p.mask_sb + i * p.mask_si : nullptr;
   const int live = causal ? static_cast<int>(i >> 5) + 1 : words;
-  for (int w = lane; w < live; w += 64) bm[w] = 0u;
+  for (int x = lane; x < live; x += 64) bm[x] = 0u;
 
   int32_t lo = 0, len = 0;
   if (lane < p.a) {
@@ -487,11 +522,53 @@ __global__ __launch_bounds__(64 * kLightWaves) void select_light_kernel(SelParam
     p.stats[(bh * p.n + i) * 2 + 0] = C;
     p.stats[(bh * p.n + i) * 2 + 1] = raw;
   }
+  __builtin_amdgcn_wave_barrier();
+
   if (C > p.k_eff) {
-    if (lane == 0) list[atomicAdd(&ctr[0], 1)] = static_cast<int32_t>(row);
+    const int shard = static_cast<int>(blockIdx.x % kShards);
+    int32_t* sc = w.ctr + 16 + 4 * shard;
+    int64_t off = -1;
+    if (w.cap > 0 && C <= 64 * kScrRegs) {
+      // whole 128-byte lines per row (32 entries), so no two rows share a line
+      const unsigned long long cpad = static_cast<unsigned long long>((C + 31) & ~31);
+      unsigned long long o = 0ull;
+      if (lane == 0) o = atomicAdd(reinterpret_cast<unsigned long long*>(sc + 2), cpad);
+      const uint32_t olo = static_cast<uint32_t>(__shfl(static_cast<int>(o & 0xFFFFFFFFull), 0));
+      const uint32_t ohi = static_cast<uint32_t>(__shfl(static_cast<int>(o >> 32), 0));
+      o = (static_cast<unsigned long long>(ohi) << 32) | olo;
+      if (o + cpad <= static_cast<unsigned long long>(w.cap))
+        off = static_cast<int64_t>(shard) * w.cap + static_cast<int64_t>(o);
+    }
+    if (off < 0) {
+      if (lane == 0) push_exact(w, p.rows, row);
+      return;
+    }
+    int32_t* dst = w.cand + off;
+    int filled = 0;
+    for (int w0 = 0; w0 < live && filled < C; w0 += 64) {
+      const int x = w0 + lane;
+      uint32_t bits = (x < live) ? bm[x] : 0u;
+      int total = 0;
+      int pos = filled + wave_excl_scan(__popc(bits), lane, &total);
+      while (bits != 0u) {
+        dst[pos++] = x * 32 + __ffs(bits) - 1;
+        bits &= bits - 1u;
+      }
+      filled += total;
+    }
+    if (lane == 0) {
+      const int slot = atomicAdd(&sc[0], 1);
+      if (slot >= 0 && slot < w.shard_rows) {
+        int32_t* ent = w.scr + (static_cast<int64_t>(shard) * w.shard_rows + slot) * 3;
+        ent[0] = static_cast<int32_t>(row);
+        ent[1] = static_cast<int32_t>(off - static_cast<int64_t>(shard) * w.cap);
+        ent[2] = C;
+      } else {
+        push_exact(w, p.rows, row);  // not reached: shard_rows bounds a shard
+      }
+    }
     return;
   }
-  __builtin_amdgcn_wave_barrier();
 
   const int64_t obase = ((bb * p.n + i) * p.h_kv + h) * p.top_k;
   int32_t* o32 = static_cast<int32_t*>(p.out) + obase;
@@ -503,41 +580,510 @@ __global__ __launch_bounds__(64 * kLightWaves) void select_light_kernel(SelParam
   // Candidates ascending, then the lowest non-candidates up to k_eff.
   int filled = 0;
   for (int w0 = 0; w0 < live && filled < C; w0 += 64) {
-    const int w = w0 + lane;
-    uint32_t bits = (w < live) ? bm[w] : 0u;
+    const int x = w0 + lane;
+    uint32_t bits = (x < live) ? bm[x] : 0u;
     int total = 0;
     int pos = filled + wave_excl_scan(__popc(bits), lane, &total);
     while (bits != 0u) {
-      put(pos++, w * 32 + __ffs(bits) - 1);
+      put(pos++, x * 32 + __ffs(bits) - 1);
       bits &= bits - 1u;
     }
     filled += total;
   }
   for (int w0 = 0; filled < p.k_eff; w0 += 64) {
-    const int w = w0 + lane;
+    const int x = w0 + lane;
     uint32_t bits = 0u;
-    if (w < words) {
-      bits = ~((w < live) ? bm[w] : 0u);
-      if (w == words - 1 && (p.n & 31)) bits &= (1u << (p.n & 31)) - 1u;
+    if (x < words) {
+      bits = ~((x < live) ? bm[x] : 0u);
+      if (x == words - 1 && (p.n & 31)) bits &= (1u << (p.n & 31)) - 1u;
     }
     int total = 0;
     int pos = filled + wave_excl_scan(__popc(bits), lane, &total);
     while (bits != 0u && pos < p.k_eff) {
-      put(pos++, w * 32 + __ffs(bits) - 1);
+      put(pos++, x * 32 + __ffs(bits) - 1);
       bits &= bits - 1u;
     }
     filled += total;
   }
-  for (int w = p.k_eff + lane; w < p.top_k; w += 64) put(w, 0);
+  for (int x = p.k_eff + lane; x < p.top_k; x += 64) put(x, 0);
+}
+
+// ---- rows with more than k candidates: matrix-core screen (bf16) -----------
+//
+// One wave per listed row.  Approximate scores A_j = (k_j . q_s) / score_div /
+// g with q_s = sum_g q_g split as q_s = hi + lo in bf16 (|q_s - hi - lo| <=
+// 2^-18 |q_s|): K rows are gathered whole into LDS (row_issue) and one 16x16x32
+// MFMA per 32 dims scores 16 keys against the columns (hi, lo); a second one
+// against |K| and the column up(sum_g |q_g|) (rounded up to bf16) gives P_j >=
+// sum_t |k_jt| sum_g |q_gt|.
+//
+// Bound.  With u = 2^-24, the canonical fp32 score E_j (g fmaf chains of d
+// terms, / score_div, summed, / g) is within (d + g + 3) u P/sd/g of the real
+// value, and A_j within (4.04 d + 64 + g + 8) u P/sd/g (MFMA sums of exact
+// products with per-add error <= 2u, the dropped 2^-18 remainder, the fp32
+// head sum of q_s).  So |A_j - E_j| <= e_j = (6 d + 2 g + 100) u * 1.02 *
+// P_j (1 + 4 d u) / sd / g + 1e-30, and e = max_j e_j.
+//
+// Selection.  T = the k-th largest A.  Every key with A_j > T + 2e has E_j
+// above the k-th largest exact score and is selected; every key with A_j <
+// T - 2e is below it and is not; the keys between (at most kScrBorder, else
+// the row takes the exact pass) are rescored in the canonical order and the
+// best (k - #above) of them by (score desc, index asc) complete the set.  The
+// row is written in index order.  Non-finite scores or bounds send the row to
+// the exact pass.
+
+
+__device__ __forceinline__ uint16_t bf16_rne_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+// Smallest bf16 >= f for finite f >= 0.
+__device__ __forceinline__ uint16_t bf16_up_bits(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return static_cast<uint16_t>((u >> 16) + ((u & 0xFFFFu) ? 1u : 0u));
+}
+__device__ __forceinline__ float key_to_score(uint32_t key) {
+  return __uint_as_float((key & 0x80000000u) ? (key & 0x7FFFFFFFu) : ~key);
+}
+// lane p of each 16-lane row reads lane p + 1 (lane 15 reads 0)
+__device__ __forceinline__ float dpp_from_plus1(float x) {
+  return __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(x), 0x101, 0xF, 0xF, false));
+}
+
+// Static assignment of listed rows to waves: wave gw of the grid serves shard
+// gw % kShards, entries r, r + per, ... with r = gw / kShards and per = (waves
+// in the grid) / kShards (the grid holds whole shards of waves).
+struct ScrEntry {
+  int64_t row, off;  // off: list position of the row's first candidate
+  int C;
+  bool ok;
+};
+__device__ __forceinline__ ScrEntry scr_entry(const SelParams& p, const SelWs& w, int shard, int e) {
+  const int32_t* ent = w.scr + (static_cast<int64_t>(shard) * w.shard_rows + e) * 3;
+  ScrEntry x;
+  x.row = ent[0];
+  x.off = static_cast<int64_t>(shard) * w.cap + ent[1];
+  x.C = ent[2];
+  x.ok = x.row >= 0 && x.row < p.rows && ent[1] >= 0 && x.C > p.k_eff && x.C <= 64 * kScrRegs &&
+         static_cast<int64_t>(ent[1]) + x.C <= w.cap;
+  return x;
+}
+
+template <int D, int GMAX>
+__global__ __launch_bounds__(64 * kScrWaves) void select_screen_kernel(SelParams p, SelWs w) {
+  using S = MfShape<D>;
+  __shared__ __align__(16) unsigned char kst[kScrWaves][kMfChunk * S::ROW];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int q4 = lane >> 4, c16 = lane & 15;
+  unsigned char* kl = kst[wave];
+  uint32_t seg16[S::SWZ_PERIOD];
+  row_seg16<D>(lane, seg16);
+  const int kswz = mf_swz<D>(c16);
+  const uint32_t ksn2 = 2u * static_cast<uint32_t>(p.k_sn);
+  const int kbytes = static_cast<int>((p.n - 1) * p.k_sn * 2 + 2 * D);
+  const int gw = static_cast<int>(blockIdx.x) * kScrWaves + wave;
+  const int shard = gw % kShards;
+  const int per = static_cast<int>(gridDim.x) * kScrWaves / kShards;
+  const int listed = min(w.ctr[16 + 4 * shard], static_cast<int>(w.shard_rows));
+  const float gf = static_cast<float>(p.g);
+  const float ce = (6.0f * D + 2.0f * static_cast<float>(p.g) + 100.0f) * 5.9604645e-8f * 1.02f *
+                   (1.0f + 4.0f * D * 5.9604645e-8f);
+  for (int e = gw / kShards; e < listed; e += per) {
+    const ScrEntry x = scr_entry(p, w, shard, e);
+    if (!x.ok) continue;  // the pick pass sends the row to the exact pass
+    const int C = x.C;
+    const int64_t off = x.off;
+    const int64_t i = x.row % p.n;
+    const int64_t bh = x.row / p.n;
+    const int h = static_cast<int>(bh % p.h_kv);
+    const int64_t bb = bh / p.h_kv;
+    const uint16_t* q0 = static_cast<const uint16_t*>(p.q) + bb * p.q_sb + i * p.q_sn +
+                         static_cast<int64_t>(h * p.g) * p.q_sh;
+    const uint16_t* kbase = static_cast<const uint16_t*>(p.k) + bb * p.k_sb + static_cast<int64_t>(h) * p.k_sh;
+    const __amdgpu_buffer_rsrc_t krs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(kbase), 0, kbytes, kBufferWord3);
+
+    // B operands (lane (q4, c16): column c16, dims 8*q4 .. +8 of each 32-dim
+    // block): column 0 = bf16 hi of the head sum q_s, column 1 = its bf16 lo;
+    // qa column 0 = sum_g |q_g| rounded up to bf16.  The group's q rows pass
+    // through the K buffer (free between rows): one wave-wide load per 64/SEGS
+    // heads (lane l: head l / SEGS, segment l % SEGS), then LDS reads.
+#pragma unroll
+    for (int g0 = 0; g0 < GMAX; g0 += S::KPI) {
+      const int gg = g0 + lane / S::SEGS;
+      if (g0 < p.g) {
+        const uint4 v = (gg < p.g) ? *reinterpret_cast<const uint4*>(q0 + static_cast<int64_t>(gg) * p.q_sh +
+                                                                      (lane % S::SEGS) * 8)
+                                   : make_uint4(0u, 0u, 0u, 0u);
+        *reinterpret_cast<uint4*>(kl + (g0 / S::KPI) * 1024 + lane * 16) = v;
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+    __builtin_amdgcn_wave_barrier();
+    bf16x8_t qf[S::KB], qa[S::KB];
+#pragma unroll
+    for (int kb = 0; kb < S::KB; ++kb) {
+      float sv[8], sa[8];
+#pragma unroll
+      for (int xx = 0; xx < 8; ++xx) sv[xx] = sa[xx] = 0.0f;
+      for (int gg = 0; gg < p.g; ++gg) {  // head gg, segment kb*4 + q4 at byte gg*ROW + seg*16
+        const uint4 u = *reinterpret_cast<const uint4*>(kl + gg * S::ROW + (kb * 4 + q4) * 16);
+        const uint32_t wq[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int xx = 0; xx < 8; ++xx) {
+          const float v = __uint_as_float((xx & 1) ? (wq[xx >> 1] & 0xFFFF0000u) : (wq[xx >> 1] << 16));
+          sv[xx] += v;
+          sa[xx] += fabsf(v);
+        }
+      }
+      uint16_t hv[8], av[8];
+#pragma unroll
+      for (int xx = 0; xx < 8; ++xx) {
+        const uint16_t hi = bf16_rne_bits(sv[xx]);
+        const uint16_t lo = bf16_rne_bits(sv[xx] - __uint_as_float(static_cast<uint32_t>(hi) << 16));
+        hv[xx] = (c16 == 0) ? hi : (c16 == 1) ? lo : static_cast<uint16_t>(0);
+        av[xx] = (c16 == 0) ? bf16_up_bits(sa[xx] * (1.0f + 9.5367432e-7f)) : static_cast<uint16_t>(0);
+      }
+      qf[kb] = __builtin_bit_cast(bf16x8_t, hv);
+      qa[kb] = __builtin_bit_cast(bf16x8_t, av);
+    }
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);  // q reads done before the K rows land in the buffer
+
+    // 32-candidate chunks: the rows of chunk c + 1 are in flight while chunk c
+    // is scored (as in the attention kernel).
+    float emax = 0.0f;
+    bool bad = false;
+    const int nch = (C + kMfChunk - 1) / kMfChunk;
+    auto idx_at = [&](int ch) -> int {
+      const int pos = ch * kMfChunk + lane;
+      return (lane < kMfChunk && pos < C) ? w.cand[off + pos] : -1;
+    };
+    row_issue<D>(krs, kl, idx_at(0), lane, ksn2, seg16);
+    int jn = (nch > 1) ? idx_at(1) : -1;
+    for (int ch = 0; ch < nch; ++ch) {
+      __builtin_amdgcn_s_waitcnt(kWaitVm0);
+      bf16x8_t kf[2][S::KB];
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int kb = 0; kb < S::KB; ++kb)
+          kf[t][kb] = *(lds_bf16x8_ptr)(kl + (16 * t + c16) * S::ROW + (((kb * 4 + q4) ^ kswz) << 4));
+      __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+      if (ch + 1 < nch) {
+        row_issue<D>(krs, kl, jn, lane, ksn2, seg16);
+        jn = (ch + 2 < nch) ? idx_at(ch + 2) : -1;
+      }
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        floatx4_t sv = {0.f, 0.f, 0.f, 0.f}, pv = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kb = 0; kb < S::KB; ++kb) {
+          sv = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[t][kb], qf[kb], sv, 0, 0, 0);
+          uint4 ak = __builtin_bit_cast(uint4, kf[t][kb]);
+          ak.x &= 0x7FFF7FFFu; ak.y &= 0x7FFF7FFFu; ak.z &= 0x7FFF7FFFu; ak.w &= 0x7FFF7FFFu;
+          pv = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, ak), qa[kb], pv, 0, 0, 0);
+        }
+#pragma unroll
+        for (int e4 = 0; e4 < 4; ++e4) {
+          const float slo = dpp_from_plus1(sv[e4]);  // column 1 (lo) of the same keys
+          const int pos = ch * kMfChunk + 16 * t + 4 * q4 + e4;
+          if (c16 == 0 && pos < C) {
+            const float a = ((sv[e4] + slo) / p.score_div) / gf;
+            const float ej = ce * pv[e4] / p.score_div / gf + 1e-30f;
+            w.approx[off + pos] = a;
+            emax = fmaxf(emax, ej);
+            bad = bad || !(fabsf(a) <= 3.0e38f) || !(ej <= 3.0e38f);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) emax = fmaxf(emax, __shfl_xor(emax, o));
+    bad = __ballot(bad) != 0ull;
+    if (lane == 0) w.emax[static_cast<int64_t>(shard) * w.shard_rows + e] = bad ? INFINITY : emax;
+  }
+}
+
+// Per listed row, from the screen's scores (a separate kernel, so they are
+// visible): the band holding the k_eff-th largest score, the keys above and
+// below it by more than 2 e, the exact rescoring of the keys between, and the
+// row in index order.
+// Bin of a score in [lo, hi] (scale = 256 / (hi - lo)): monotone in a, in
+// [0, 255] also when scale overflows to infinity.
+__device__ __forceinline__ int band_bin(float a, float lo, float scale) {
+  const float t = (a - lo) * scale;
+  return (t >= 255.0f) ? 255 : (t >= 0.0f) ? static_cast<int>(t) : 0;
+}
+
+template <int D, int GMAX>
+__global__ __launch_bounds__(64 * kScrWaves) void select_pick_kernel(SelParams p, SelWs w) {
+  __shared__ __align__(16) float avs[kScrWaves][64 * kScrRegs];  // position pos at [pos]
+  __shared__ int32_t hst[kScrWaves][256];
+  __shared__ int32_t bps[kScrWaves][kScrBorder];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  float* av = avs[wave];
+  int32_t* hs = hst[wave];
+  int32_t* bp = bps[wave];
+  const int gw = static_cast<int>(blockIdx.x) * kScrWaves + wave;
+  const int shard = gw % kShards;
+  const int per = static_cast<int>(gridDim.x) * kScrWaves / kShards;
+  const int listed = min(w.ctr[16 + 4 * shard], static_cast<int>(w.shard_rows));
+  const float gf = static_cast<float>(p.g);
+  for (int e = gw / kShards; e < listed; e += per) {
+    const ScrEntry x = scr_entry(p, w, shard, e);
+    if (x.row < 0 || x.row >= p.rows) continue;  // cannot happen: the light pass wrote every entry
+    const float emax = w.emax[static_cast<int64_t>(shard) * w.shard_rows + e];
+    if (!x.ok || !(emax <= 3.0e38f)) {
+      if (lane == 0) push_exact(w, p.rows, x.row);
+      continue;
+    }
+    const int C = x.C;
+    const int64_t off = x.off;
+    const int64_t row = x.row;
+    const int64_t i = row % p.n;
+    const int64_t bh = row / p.n;
+    const int h = static_cast<int>(bh % p.h_kv);
+    const int64_t bb = bh / p.h_kv;
+    const int R = (C + 63) / 64;  // positions lane + 64 r, r < R
+
+    // The row's scores into LDS (coalesced), with their range.
+    float amin = INFINITY, amax = -INFINITY;
+#pragma unroll 8
+    for (int r = 0; r < R; ++r) {
+      const int pos = lane + 64 * r;
+      const float a = (pos < C) ? w.approx[off + pos] : -INFINITY;
+      av[pos] = a;
+      if (pos < C) {
+        amin = fminf(amin, a);
+        amax = fmaxf(amax, a);
+      }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      amin = fminf(amin, __shfl_xor(amin, o));
+      amax = fmaxf(amax, __shfl_xor(amax, o));
+    }
+
+    // Band [lo, hi] holding the k_eff-th largest score: 256 bins over the band
+    // (bin = floor((a - lo) * 256 / (hi - lo)), monotone in a), keep the bin
+    // where the count from the top reaches the rank, shrink the band to the
+    // smallest and largest score in that bin; at most two passes.
+    float lo = amin, hi = amax;
+    int kk = p.k_eff;
+    for (int pass = 0; pass < 2 && hi > lo; ++pass) {
+      const float scale = 256.0f / (hi - lo);
+      for (int xx = lane; xx < 256; xx += 64) hs[xx] = 0;
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll 4
+      for (int r = 0; r < R; ++r) {
+        const float a = av[lane + 64 * r];
+        if (a >= lo && a <= hi) atomicAdd(&hs[band_bin(a, lo, scale)], 1);
+      }
+      __builtin_amdgcn_wave_barrier();
+      int c4[4], tot = 0;
+#pragma unroll
+      for (int xx = 0; xx < 4; ++xx) {
+        c4[xx] = hs[255 - 4 * lane - xx];  // lanes walk the bins from the top
+        tot += c4[xx];
+      }
+      int all = 0;
+      const int before = wave_excl_scan(tot, lane, &all);
+      int bin = -1, nk = 0, inbin = 0;
+      if (before < kk && kk <= before + tot) {
+        int acc = before;
+#pragma unroll
+        for (int xx = 0; xx < 4; ++xx) {
+          if (bin < 0 && kk <= acc + c4[xx]) {
+            bin = 255 - 4 * lane - xx;
+            nk = kk - acc;
+            inbin = c4[xx];
+          }
+          acc += c4[xx];
+        }
+      }
+      const int src = __ffsll(static_cast<unsigned long long>(__ballot(bin >= 0))) - 1;
+      if (src < 0) break;  // cannot happen: kk <= keys in the band
+      bin = __shfl(bin, src);
+      nk = __shfl(nk, src);
+      inbin = __shfl(inbin, src);
+      float blo = INFINITY, bhi = -INFINITY;
+#pragma unroll 4
+      for (int r = 0; r < R; ++r) {
+        const float a = av[lane + 64 * r];
+        if (a >= lo && a <= hi && band_bin(a, lo, scale) == bin) {
+          blo = fminf(blo, a);
+          bhi = fmaxf(bhi, a);
+        }
+      }
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) {
+        blo = fminf(blo, __shfl_xor(blo, o));
+        bhi = fmaxf(bhi, __shfl_xor(bhi, o));
+      }
+      lo = blo;
+      hi = bhi;
+      kk = nk;
+      __builtin_amdgcn_wave_barrier();
+      if (inbin <= 32) break;
+    }
+    const float e2 = 2.0f * 1.02f * emax + 2e-30f;
+    const float thr_in = hi + e2, thr_out = lo - e2;
+
+    // Classify: keys surely in the top k_eff go to the selection mask (bit pos
+    // of word pos / 32, in hs), keys within 2 e of the band to bp (ascending).
+    uint32_t* sm = reinterpret_cast<uint32_t*>(hs);
+    int m_in = 0, nb = 0;
+    for (int r = 0; r < R; ++r) {
+      const int pos = lane + 64 * r;
+      const float a = av[pos];
+      const bool in = a > thr_in;
+      const bool border = pos < C && !in && a >= thr_out;
+      m_in += in ? 1 : 0;
+      const uint64_t imask = __ballot(in);
+      const uint64_t bmask = __ballot(border);
+      if (lane < 2) sm[2 * r + lane] = static_cast<uint32_t>(imask >> (32 * lane));
+      if (border) {
+        const int sl = nb + __popcll(bmask & below);
+        if (sl < kScrBorder) bp[sl] = pos;
+      }
+      nb += __popcll(bmask);
+    }
+    int n_in = 0;
+    wave_excl_scan(m_in, lane, &n_in);
+    const int need = p.k_eff - n_in;
+    if (nb > kScrBorder || need < 0 || need > nb) {
+      if (lane == 0) push_exact(w, p.rows, row);
+      __builtin_amdgcn_wave_barrier();
+      continue;
+    }
+
+    // The group's q rows into the score area (free now): head gg at gg * D.
+    const uint16_t* q0 = static_cast<const uint16_t*>(p.q) + bb * p.q_sb + i * p.q_sn +
+                         static_cast<int64_t>(h * p.g) * p.q_sh;
+    uint16_t* ql = reinterpret_cast<uint16_t*>(av);
+    for (int t = lane; t < p.g * (D / 8); t += 64) {
+      const int gg = t / (D / 8), sg = t % (D / 8);
+      *reinterpret_cast<uint4*>(ql + gg * D + sg * 8) =
+          *reinterpret_cast<const uint4*>(q0 + static_cast<int64_t>(gg) * p.q_sh + sg * 8);
+    }
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+    __builtin_amdgcn_wave_barrier();
+
+    // Exact scores of the borderline keys (one per lane, the canonical order:
+    // per head an fmaf chain over ascending dims from +0) and their ranks.
+    uint64_t key = 0ull;
+    if (lane < nb) {
+      const int32_t j = w.cand[off + bp[lane]];
+      const uint16_t* kr = static_cast<const uint16_t*>(p.k) + bb * p.k_sb + static_cast<int64_t>(h) * p.k_sh +
+                           static_cast<int64_t>(j) * p.k_sn;
+      float acc[GMAX];
+#pragma unroll
+      for (int gg = 0; gg < GMAX; ++gg) acc[gg] = 0.0f;
+      constexpr int KL = 8;  // 16-byte loads in flight per lane: half a D = 128 row
+#pragma unroll 1
+      for (int t0 = 0; t0 < D; t0 += 8 * KL) {
+        float kv[KL][8];
+#pragma unroll
+        for (int u = 0; u < KL; ++u) load8(kr + t0 + 8 * u, kv[u]);
+#pragma unroll
+        for (int gg = 0; gg < GMAX; ++gg) {
+          if (gg >= p.g) continue;
+#pragma unroll
+          for (int u = 0; u < KL; ++u) {
+            float qv[8];
+            load8(ql + gg * D + t0 + 8 * u, qv);  // same address in every lane: a broadcast
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[gg] = fma_rn(qv[e], kv[u][e], acc[gg]);
+          }
+        }
+      }
+      float sc = acc[0] / p.score_div;
+#pragma unroll
+      for (int gg = 1; gg < GMAX; ++gg)
+        if (gg < p.g) sc = sc + acc[gg] / p.score_div;
+      sc = sc / gf;
+      key = composite_key(sc, static_cast<uint32_t>(j));
+    }
+    int rank = 0;
+    for (int b = 0; b < nb; ++b) {
+      const uint64_t kb = (static_cast<uint64_t>(static_cast<uint32_t>(__shfl(static_cast<int>(key >> 32), b))) << 32) |
+                          static_cast<uint32_t>(__shfl(static_cast<int>(key & 0xFFFFFFFFull), b));
+      rank += (kb > key) ? 1 : 0;
+    }
+    if (lane < nb && rank < need) atomicOr(&sm[bp[lane] >> 5], 1u << (bp[lane] & 31));
+    __builtin_amdgcn_wave_barrier();
+
+    // The selected keys in index order.
+    const int64_t obase = ((bb * p.n + i) * p.h_kv + h) * p.top_k;
+    int32_t* o32 = static_cast<int32_t*>(p.out) + obase;
+    int64_t* o64 = static_cast<int64_t*>(p.out) + obase;
+    int filled = 0;
+    for (int r0 = 0; r0 < R; r0 += 8) {
+      int32_t jv[8];  // eight list words in flight at once
+#pragma unroll
+      for (int u = 0; u < 8; ++u) jv[u] = w.cand[off + min(lane + 64 * (r0 + u), C - 1)];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int r = r0 + u;
+        if (r >= R) break;
+        const uint64_t smask = static_cast<uint64_t>(sm[2 * r]) | (static_cast<uint64_t>(sm[2 * r + 1]) << 32);
+        const bool sel = (smask >> lane) & 1ull;
+        const int o = filled + __popcll(smask & below);
+        if (sel && o < p.k_eff) {
+          if (p.out_i64) o64[o] = jv[u];
+          else o32[o] = jv[u];
+        }
+        filled += __popcll(smask);
+      }
+    }
+    __builtin_amdgcn_wave_barrier();  // av, hs and bp are rewritten by the next row
+  }
 }
 
 __global__ void zero_ctr_kernel(int32_t* __restrict__ ctr) {
-  if (threadIdx.x < 2) ctr[threadIdx.x] = 0;
+  for (int x = threadIdx.x; x < static_cast<int>(kSelCtrBytes / 4); x += blockDim.x) ctr[x] = 0;
 }
 
 size_t light_smem(int64_t n) { return sizeof(uint32_t) * kLightWaves * static_cast<size_t>((n + 31) / 32); }
 
-int heavy_grid(int64_t rows) {
+// Rows of the light-pass blocks of one shard (block b -> shard b % kShards).
+int64_t shard_rows_for(int64_t rows) { return ceil_div(ceil_div(rows, kLightWaves), kShards) * kLightWaves; }
+
+size_t sel_ws_fixed(int64_t rows) {
+  return kSelCtrBytes + align_up(sizeof(int32_t) * static_cast<size_t>(rows), 256) +
+         align_up(3 * sizeof(int32_t) * static_cast<size_t>(kShards * shard_rows_for(rows)), 256) +
+         align_up(sizeof(float) * static_cast<size_t>(kShards * shard_rows_for(rows)), 256);
+}
+
+SelWs carve_sel_ws(void* ws, size_t bytes, int64_t rows, bool screen) {
+  char* c = static_cast<char*>(ws);
+  SelWs w{};
+  w.ctr = reinterpret_cast<int32_t*>(c);
+  c += kSelCtrBytes;
+  w.exact = reinterpret_cast<int32_t*>(c);
+  c += align_up(sizeof(int32_t) * static_cast<size_t>(rows), 256);
+  w.shard_rows = shard_rows_for(rows);
+  w.scr = reinterpret_cast<int32_t*>(c);
+  c += align_up(3 * sizeof(int32_t) * static_cast<size_t>(kShards * w.shard_rows), 256);
+  w.emax = reinterpret_cast<float*>(c);
+  c += align_up(sizeof(float) * static_cast<size_t>(kShards * w.shard_rows), 256);
+  const size_t fixed = sel_ws_fixed(rows);
+  // per shard: cap candidates and cap scores
+  int64_t cap = (screen && bytes > fixed + 256) ? static_cast<int64_t>((bytes - fixed - 256) / (8 * kShards)) : 0;
+  if (cap > (int64_t(1) << 31) / kShards - 1) cap = (int64_t(1) << 31) / kShards - 1;
+  cap &= ~int64_t(31);  // shard slices start on 128-byte lines
+  if (cap < 0) cap = 0;
+  w.cand = reinterpret_cast<int32_t*>(c);
+  w.approx = reinterpret_cast<float*>(c + align_up(sizeof(int32_t) * static_cast<size_t>(cap * kShards), 256));
+  w.cap = cap;
+  return w;
+}
+
+int persistent_grid(int64_t work, int per_cu) {
   static int cus[64] = {0};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
@@ -546,14 +1092,35 @@ int heavy_grid(int64_t rows) {
     if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) c = 256;
     cus[dev] = c;
   }
-  const int64_t g = static_cast<int64_t>(cus[dev]) * 8;
-  return static_cast<int>(rows < g ? rows : g);
+  const int64_t g = static_cast<int64_t>(cus[dev]) * per_cu;
+  return static_cast<int>(work < g ? (work > 0 ? work : 1) : g);
 }
 
-// ws (nullable): index order through the light/heavy pair; otherwise one block
-// per row.
+// Grid of the screen (WHICH = 0) or pick (1) kernel: as many blocks as fit on
+// the device at once, rounded up to whole shards of waves (the grid's wave
+// count is a multiple of kShards).
+template <int D, int GMAX, int WHICH>
+int shard_grid() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (cached[dev] == 0) {
+    int per_cu = 0;
+    const void* f = (WHICH == 0) ? reinterpret_cast<const void*>(select_screen_kernel<D, GMAX>)
+                                 : reinterpret_cast<const void*>(select_pick_kernel<D, GMAX>);
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, f, 64 * kScrWaves, 0) != hipSuccess || per_cu <= 0)
+      per_cu = 2;
+    constexpr int kBlocksPerShardSet = kShards / kScrWaves;
+    cached[dev] = static_cast<int>(ceil_div(persistent_grid(int64_t(1) << 40, per_cu), kBlocksPerShardSet) *
+                                   kBlocksPerShardSet);
+  }
+  return cached[dev];
+}
+
+// ws (nullable): index order through the light pass, the screen (bf16, d = 64 or
+// 128) and the exact pass for the rest; otherwise one block per row.
 template <typename T, int GMAX, int D>
-int launch_select(const SelParams& p, int64_t rows, size_t smem, int32_t* ws, hipStream_t st) {
+int launch_select(const SelParams& p, int64_t rows, size_t smem, void* ws, size_t ws_bytes, hipStream_t st) {
   auto kern = select_kernel<T, GMAX, D>;
   if (int s = reserve_lds(reinterpret_cast<const void*>(kern), smem, "select")) return s;
   const T* qg = static_cast<const T*>(p.q);
@@ -561,34 +1128,48 @@ int launch_select(const SelParams& p, int64_t rows, size_t smem, int32_t* ws, hi
     kern<<<dim3(static_cast<unsigned>(rows)), kSelThreads, smem, st>>>(p, qg);
     return check_launch("select_kernel");
   }
-  int32_t* ctr = ws;
-  int32_t* list = ws + 64;
-  zero_ctr_kernel<<<1, 64, 0, st>>>(ctr);
+  constexpr bool kScreenable = sizeof(T) == 2 && (D == 64 || D == 128);
+  // 32-bit buffer offsets of the screen's K gathers
+  const bool screen = kScreenable && p.n < (int64_t(1) << 24) && 2 * p.k_sn < (int64_t(1) << 24) &&
+                      (p.n - 1) * p.k_sn * 2 + 2 * p.d < (int64_t(1) << 31);
+  const SelWs w = carve_sel_ws(ws, ws_bytes, rows, screen);
+  zero_ctr_kernel<<<1, 256, 0, st>>>(w.ctr);
   if (int s = check_launch("zero_ctr_kernel")) return s;
   select_light_kernel<<<dim3(static_cast<unsigned>(ceil_div(rows, kLightWaves))), 64 * kLightWaves,
-                        light_smem(p.n), st>>>(p, rows, list, ctr);
+                        light_smem(p.n), st>>>(p, rows, w);
   if (int s = check_launch("select_light_kernel")) return s;
+  if constexpr (kScreenable) {
+    if (w.cap > 0) {
+      constexpr int DS = (D == 64) ? 64 : 128;
+      select_screen_kernel<DS, GMAX><<<dim3(static_cast<unsigned>(shard_grid<DS, GMAX, 0>())), 64 * kScrWaves, 0,
+                                      st>>>(p, w);
+      if (int s = check_launch("select_screen_kernel")) return s;
+      select_pick_kernel<DS, GMAX><<<dim3(static_cast<unsigned>(shard_grid<DS, GMAX, 1>())), 64 * kScrWaves, 0,
+                                    st>>>(p, w);
+      if (int s = check_launch("select_pick_kernel")) return s;
+    }
+  }
   auto hk = select_heavy_kernel<T, GMAX, D>;
   if (int s = reserve_lds(reinterpret_cast<const void*>(hk), smem, "select")) return s;
-  hk<<<dim3(static_cast<unsigned>(heavy_grid(rows))), kSelThreads, smem, st>>>(p, qg, list, ctr);
+  hk<<<dim3(static_cast<unsigned>(persistent_grid(rows, 8))), kSelThreads, smem, st>>>(p, qg, w);
   return check_launch("select_heavy_kernel");
 }
 
 template <typename T, int GMAX>
-int dispatch_select_d(const SelParams& p, int64_t rows, size_t smem, int32_t* ws, hipStream_t st) {
+int dispatch_select_d(const SelParams& p, int64_t rows, size_t smem, void* ws, size_t wb, hipStream_t st) {
   switch (p.d) {
-    case 64: return launch_select<T, GMAX, 64>(p, rows, smem, ws, st);
-    case 128: return launch_select<T, GMAX, 128>(p, rows, smem, ws, st);
-    case 256: return launch_select<T, GMAX, 256>(p, rows, smem, ws, st);
-    default: return launch_select<T, GMAX, 0>(p, rows, smem, ws, st);
+    case 64: return launch_select<T, GMAX, 64>(p, rows, smem, ws, wb, st);
+    case 128: return launch_select<T, GMAX, 128>(p, rows, smem, ws, wb, st);
+    case 256: return launch_select<T, GMAX, 256>(p, rows, smem, ws, wb, st);
+    default: return launch_select<T, GMAX, 0>(p, rows, smem, ws, wb, st);
   }
 }
 
 template <typename T>
-int dispatch_select(const SelParams& p, int64_t rows, size_t smem, int32_t* ws, hipStream_t st) {
-  if (p.g <= 4) return dispatch_select_d<T, 4>(p, rows, smem, ws, st);
-  if (p.g <= 8) return dispatch_select_d<T, 8>(p, rows, smem, ws, st);
-  return dispatch_select_d<T, 16>(p, rows, smem, ws, st);
+int dispatch_select(const SelParams& p, int64_t rows, size_t smem, void* ws, size_t wb, hipStream_t st) {
+  if (p.g <= 4) return dispatch_select_d<T, 4>(p, rows, smem, ws, wb, st);
+  if (p.g <= 8) return dispatch_select_d<T, 8>(p, rows, smem, ws, wb, st);
+  return dispatch_select_d<T, 16>(p, rows, smem, ws, wb, st);
 }
 
 }  // namespace
@@ -596,9 +1177,13 @@ int dispatch_select(const SelParams& p, int64_t rows, size_t smem, int32_t* ws, 
 
 using namespace ssa;
 
-extern "C" size_t ssa_select_workspace_bytes(int64_t batch, int64_t n, int h_kv) {
-  if (batch < 0 || n < 0 || h_kv <= 0) return 0;
-  return align_up(256 + sizeof(int32_t) * static_cast<size_t>(batch * h_kv * n), 256);
+extern "C" size_t ssa_select_workspace_bytes(int64_t batch, int64_t n, int h_kv, int top_k) {
+  if (batch < 0 || n < 0 || h_kv <= 0 || top_k < 0) return 0;
+  const int64_t rows = batch * h_kv * n;
+  const int64_t k_eff = top_k < n ? top_k : n;
+  // fixed part, then room for candidate lists and their scores: one entry
+  // (8 bytes) per output slot
+  return sel_ws_fixed(rows) + 256 + align_up(static_cast<size_t>(rows) * static_cast<size_t>(k_eff), 256) * 8;
 }
 
 extern "C" int ssa_select(const void* q, const void* k, int dtype, int64_t batch, int64_t n,
@@ -634,9 +1219,9 @@ extern "C" int ssa_select(const void* q, const void* k, int dtype, int64_t batch
   if ((k_sn % vec) || (k_sh % vec) || (k_sb % vec) || (reinterpret_cast<uintptr_t>(k) % 16) ||
       (q_sn % vec) || (q_sh % vec) || (q_sb % vec) || (reinterpret_cast<uintptr_t>(q) % 16))
     return fail(SSA_ERR_UNSUPPORTED, "select: q and k rows must be 16-byte aligned");
-  if (workspace && workspace_bytes < ssa_select_workspace_bytes(batch, n, h_kv))
+  if (workspace && workspace_bytes < ssa_select_workspace_bytes(batch, n, h_kv, 0))
     return fail(SSA_ERR_WORKSPACE, "select: workspace %zu < %zu bytes", workspace_bytes,
-                ssa_select_workspace_bytes(batch, n, h_kv));
+                ssa_select_workspace_bytes(batch, n, h_kv, 0));
   if (batch == 0 || n == 0) return SSA_OK;
   if (!q || !k || !q_codes || !offsets || !postings || !out)
     return fail(SSA_ERR_INVALID_ARGUMENT, "select: null pointer");
@@ -668,6 +1253,7 @@ extern "C" int ssa_select(const void* q, const void* k, int dtype, int64_t batch
   p.out = out;
   p.out_i64 = (out_index_dtype == SSA_INDEX_I64);
   p.stats = stats;
+  p.rows = batch * h_kv * n;
   const size_t smem = select_smem(n, p.sortn, p.k_eff);
   if (smem > 160 * 1024)
     return fail(SSA_ERR_UNSUPPORTED, "select: needs %zu bytes of LDS (n=%lld, top_k=%d)", smem,
@@ -675,7 +1261,6 @@ extern "C" int ssa_select(const void* q, const void* k, int dtype, int64_t batch
   const int64_t rows = batch * h_kv * n;
   if (rows >= (int64_t(1) << 31)) return fail(SSA_ERR_UNSUPPORTED, "select: too many rows");
   hipStream_t st = as_stream(stream);
-  int32_t* ws = static_cast<int32_t*>(workspace);
-  if (dtype == SSA_DTYPE_BF16) return dispatch_select<uint16_t>(p, rows, smem, ws, st);
-  return dispatch_select<float>(p, rows, smem, ws, st);
+  if (dtype == SSA_DTYPE_BF16) return dispatch_select<uint16_t>(p, rows, smem, workspace, workspace_bytes, st);
+  return dispatch_select<float>(p, rows, smem, workspace, workspace_bytes, st);
 }

@@ -10,7 +10,7 @@ every call is enqueued on the current stream without synchronising.
 from __future__ import annotations
 
 import math
-from typing import Optional, Tuple
+from typing import Optional, Tuple, Union
 
 import torch
 
@@ -131,7 +131,7 @@ def select(q: torch.Tensor, k: torch.Tensor, q_codes: torch.Tensor, offsets: tor
            postings: torch.Tensor, b: int, top_k: int, mask_mode: int = _lib.MASK_CAUSAL,
            mask: Optional[torch.Tensor] = None, score_div: Optional[float] = None,
            index_dtype: torch.dtype = torch.int64,
-           with_stats: bool = False, sorted: bool = True, use_workspace: bool = True):
+           with_stats: bool = False, sorted: bool = True, use_workspace: Union[bool, int] = True):
     """Stage (c): candidate indices [B, n, h_kv, top_k] (ssa/router.py:151-214).
 
     ``mask`` (MASK_DENSE) is a bool/uint8 ``[n, n]`` or ``[B, n, n]`` tensor with a
@@ -139,7 +139,8 @@ def select(q: torch.Tensor, k: torch.Tensor, q_codes: torch.Tensor, offsets: tor
     (unique candidates, postings read inside the mask window) per row.
     ``sorted=False`` lists the same selected set in ascending index order (then
     the same filler).  ``use_workspace=False`` runs the one-block-per-row kernel
-    for every row (same results).
+    for every row; an int gives the workspace size in bytes instead of the
+    recommended ``ssa_select_workspace_bytes(B, n, h_kv, top_k)`` (same results).
     """
     _check_rows(q, "q")
     _check_rows(k, "k")
@@ -166,9 +167,12 @@ def select(q: torch.Tensor, k: torch.Tensor, q_codes: torch.Tensor, offsets: tor
     out = torch.empty((B, n, h_kv, top_k), device=q.device, dtype=index_dtype)
     stats = torch.empty((B, h_kv, n, 2), device=q.device, dtype=torch.int32) if with_stats else None
     ws_bytes, ws = 0, None
-    if use_workspace:
-        ws_bytes = int(_lib.load().ssa_select_workspace_bytes(B, n, h_kv))
-        ws = torch.empty(max(ws_bytes, 1), device=q.device, dtype=torch.uint8)
+    if use_workspace is True:
+        ws_bytes = int(_lib.load().ssa_select_workspace_bytes(B, n, h_kv, top_k))
+    elif use_workspace is not False:
+        ws_bytes = int(use_workspace)
+    if ws_bytes > 0:
+        ws = torch.empty(ws_bytes, device=q.device, dtype=torch.uint8)
     call("ssa_select", ptr(q), ptr(k), _lib.elem_dtype(q), B, n, h_q, h_kv, d,
          q.stride(0), q.stride(1), q.stride(2), k.stride(0), k.stride(1), k.stride(2),
          ptr(q_codes), a, ptr(offsets), ptr(postings), n_c, b, top_k, mask_mode, ptr(mask),

@@ -120,10 +120,14 @@ def test_select_rejects(L, kw, status, text):
 
 
 def test_select_workspace_size(L):
-    # counters (256 B) + one int32 per (batch, kv head, query) row, 256-byte aligned
-    assert L.ssa_select_workspace_bytes(2, 1000, 8) == 256 + 2 * 8 * 1000 * 4
-    assert L.ssa_select_workspace_bytes(1, 1, 1) == 512
-    assert _select(L, workspace=FAKE, workspace_bytes=L.ssa_select_workspace_bytes(1, 1024, 8),
+    # counters and per-row lists (at least 16 bytes per row), then 8 bytes per
+    # output slot for candidate lists and their scores
+    rows = 2 * 8 * 1000
+    fixed = L.ssa_select_workspace_bytes(2, 1000, 8, 0)
+    assert fixed >= rows * 16
+    assert L.ssa_select_workspace_bytes(2, 1000, 8, 64) == fixed + rows * 64 * 8
+    assert L.ssa_select_workspace_bytes(2, 1000, 8, 5000) == fixed + rows * 1000 * 8  # k <= n
+    assert _select(L, workspace=FAKE, workspace_bytes=L.ssa_select_workspace_bytes(1, 1024, 8, 0),
                    postings=NULL)[0] == _lib.SSA_ERR_INVALID_ARGUMENT
 
 
