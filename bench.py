@@ -129,10 +129,10 @@ def run_step(q, k, v, router, events=None):
         events[2].record()
     # Same calls as SSAAttention: stage (d) does not depend on the order of the
     # selected keys, so the router lists them by index (same set as sorted),
-    # the indices pass to stage (d) as int32, and stage (d) processes the rows
-    # of each head grouped by best code (results do not depend on the order).
+    # the indices pass to stage (d) as int32, and stages (c) and (d) process the
+    # rows of each head grouped by best code (results do not depend on the order).
     idx = kernels.select(q, k, qc, off, post, router.codes_per_key, router.top_k, sorted=False,
-                         index_dtype=torch.int32)
+                         index_dtype=torch.int32, row_order=order)
     if events:
         events[3].record()
     out = kernels.sparse_attention(q, k, v, idx, None, True, row_order=order)

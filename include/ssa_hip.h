@@ -145,6 +145,11 @@ int ssa_query_order(const int32_t* q_codes, int64_t batch, int64_t n, int h_kv, 
  *          one-block-per-row pass.  ssa_select_workspace_bytes(.., top_k) is
  *          the recommended size, (.., 0) the minimum (no lists).  Without a
  *          workspace, one block per row.  Results are identical in every case.
+ *   row_order (nullable) int32 [batch][h_kv][n]: the order in which query rows
+ *          are processed, as for ssa_sparse_attention (ssa_query_order groups
+ *          rows that share buckets and candidate keys, which then hit in
+ *          cache).  Results do not depend on it; a row never listed is not
+ *          written and an entry outside [0, n) is skipped.
  * Limits: top_k <= 4096, g = h_q/h_kv <= 16, d <= 256 (d % 8 == 0), n < 2^31. */
 size_t ssa_select_workspace_bytes(int64_t batch, int64_t n, int h_kv, int top_k);
 int ssa_select(const void* q, const void* k, int dtype, int64_t batch, int64_t n, int h_q,
@@ -152,8 +157,8 @@ int ssa_select(const void* q, const void* k, int dtype, int64_t batch, int64_t n
                int64_t k_sn, int64_t k_sh, const int32_t* q_codes, int a, const int32_t* offsets,
                const int32_t* postings, int n_c, int b, int top_k, int mask_mode,
                const uint8_t* mask, int64_t mask_sb, int64_t mask_si, float score_div, int sorted,
-               void* out, int out_index_dtype, int32_t* stats, void* workspace,
-               size_t workspace_bytes, void* stream);
+               const int32_t* row_order, void* out, int out_index_dtype, int32_t* stats,
+               void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---- stage (d): gathered exact attention -------------------------------- */
 

@@ -51,8 +51,18 @@ struct SelParams {
   void* out;
   int out_i64;
   int32_t* stats;
-  int64_t rows;  // batch * h_kv * n
+  int64_t rows;         // batch * h_kv * n
+  const int32_t* order;  // nullable [rows]: position t of head bh runs query order[bh * n + t]
 };
+
+// Row ((b * h_kv + h) * n + i) processed in slot t of the launch (t = bh * n + u):
+// i = u, or order[t] when an order is given; -1 for an order entry outside [0, n).
+__device__ __forceinline__ int64_t row_of_slot(const SelParams& p, int64_t t) {
+  if (p.order == nullptr) return t;
+  const int32_t o = p.order[t];
+  if (static_cast<uint32_t>(o) >= static_cast<uint64_t>(p.n)) return -1;
+  return (t / p.n) * p.n + o;
+}
 
 __host__ __device__ inline int pow2_at_least(int v) {
   int p = 1;
@@ -395,7 +405,8 @@ __device__ __forceinline__ void select_row(const SelParams& p, const T* __restri
 
 template <typename T, int GMAX, int D>
 __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams p, const T* __restrict__ qg) {
-  select_row<T, GMAX, D>(p, qg, blockIdx.x, false);
+  const int64_t row = row_of_slot(p, blockIdx.x);
+  if (row >= 0) select_row<T, GMAX, D>(p, qg, row, false);
 }
 
 // Workspace of index order (carve_sel_ws).  Rows with more than k candidates
@@ -456,8 +467,9 @@ __global__ __launch_bounds__(kSelThreads) void select_heavy_kernel(SelParams p, 
 // through the wave's LDS bitmap; a row with at most k_eff candidates writes its
 // candidates ascending and the filler directly.  A row with more writes its
 // candidate list into the workspace for select_screen_kernel when it fits
-// (w.cap), and is listed for the exact pass otherwise.
-constexpr int kLightWaves = 4;
+// (w.cap), and is listed for the exact pass otherwise.  One wave per block, so
+// no row waits for a longer one before its LDS is released.
+constexpr int kLightWaves = 1;
 
 __device__ __forceinline__ int wave_excl_scan(int v, int lane, int* total) {
   int x = v;
@@ -474,8 +486,10 @@ __global__ __launch_bounds__(64 * kLightWaves) void select_light_kernel(SelParam
   extern __shared__ __align__(16) uint32_t lbits[];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * kLightWaves + wave;
-  if (row >= rows) return;
+  const int64_t slot = static_cast<int64_t>(blockIdx.x) * kLightWaves + wave;
+  if (slot >= rows) return;
+  const int64_t row = row_of_slot(p, slot);
+  if (row < 0) return;
   const int words = static_cast<int>((p.n + 31) >> 5);
   uint32_t* bm = lbits + static_cast<int64_t>(wave) * words;
   const int64_t i = row % p.n;
@@ -1191,8 +1205,8 @@ extern "C" int ssa_select(const void* q, const void* k, int dtype, int64_t batch
                           int64_t k_sb, int64_t k_sn, int64_t k_sh, const int32_t* q_codes, int a,
                           const int32_t* offsets, const int32_t* postings, int n_c, int b,
                           int top_k, int mask_mode, const uint8_t* mask, int64_t mask_sb,
-                          int64_t mask_si, float score_div, int sorted, void* out,
-                          int out_index_dtype, int32_t* stats, void* workspace,
+                          int64_t mask_si, float score_div, int sorted, const int32_t* row_order,
+                          void* out, int out_index_dtype, int32_t* stats, void* workspace,
                           size_t workspace_bytes, void* stream) {
   if (dtype != SSA_DTYPE_F32 && dtype != SSA_DTYPE_BF16)
     return fail(SSA_ERR_UNSUPPORTED, "select: dtype %d not supported (f32, bf16)", dtype);
@@ -1254,6 +1268,7 @@ extern "C" int ssa_select(const void* q, const void* k, int dtype, int64_t batch
   p.out_i64 = (out_index_dtype == SSA_INDEX_I64);
   p.stats = stats;
   p.rows = batch * h_kv * n;
+  p.order = row_order;
   const size_t smem = select_smem(n, p.sortn, p.k_eff);
   if (smem > 160 * 1024)
     return fail(SSA_ERR_UNSUPPORTED, "select: needs %zu bytes of LDS (n=%lld, top_k=%d)", smem,

@@ -131,7 +131,8 @@ def select(q: torch.Tensor, k: torch.Tensor, q_codes: torch.Tensor, offsets: tor
            postings: torch.Tensor, b: int, top_k: int, mask_mode: int = _lib.MASK_CAUSAL,
            mask: Optional[torch.Tensor] = None, score_div: Optional[float] = None,
            index_dtype: torch.dtype = torch.int64,
-           with_stats: bool = False, sorted: bool = True, use_workspace: Union[bool, int] = True):
+           with_stats: bool = False, sorted: bool = True, use_workspace: Union[bool, int] = True,
+           row_order: Optional[torch.Tensor] = None):
     """Stage (c): candidate indices [B, n, h_kv, top_k] (ssa/router.py:151-214).
 
     ``mask`` (MASK_DENSE) is a bool/uint8 ``[n, n]`` or ``[B, n, n]`` tensor with a
@@ -141,6 +142,8 @@ def select(q: torch.Tensor, k: torch.Tensor, q_codes: torch.Tensor, offsets: tor
     the same filler).  ``use_workspace=False`` runs the one-block-per-row kernel
     for every row; an int gives the workspace size in bytes instead of the
     recommended ``ssa_select_workspace_bytes(B, n, h_kv, top_k)`` (same results).
+    ``row_order`` (int32 [B, h_kv, n], a permutation of 0..n-1 per head, e.g.
+    ``query_order``) only sets the order in which rows are processed.
     """
     _check_rows(q, "q")
     _check_rows(k, "k")
@@ -164,6 +167,11 @@ def select(q: torch.Tensor, k: torch.Tensor, q_codes: torch.Tensor, offsets: tor
             m_sb, m_si = 0, mask.stride(0)
         else:
             m_sb, m_si = mask.stride(0), mask.stride(1)
+    if row_order is not None:
+        _lib.require_device(row_order)
+        if row_order.dtype != torch.int32 or tuple(row_order.shape) != (B, h_kv, n):
+            raise ValueError(f"row_order must be int32 [{B}, {h_kv}, {n}]")
+        row_order = row_order.contiguous()
     out = torch.empty((B, n, h_kv, top_k), device=q.device, dtype=index_dtype)
     stats = torch.empty((B, h_kv, n, 2), device=q.device, dtype=torch.int32) if with_stats else None
     ws_bytes, ws = 0, None
@@ -176,7 +184,7 @@ def select(q: torch.Tensor, k: torch.Tensor, q_codes: torch.Tensor, offsets: tor
     call("ssa_select", ptr(q), ptr(k), _lib.elem_dtype(q), B, n, h_q, h_kv, d,
          q.stride(0), q.stride(1), q.stride(2), k.stride(0), k.stride(1), k.stride(2),
          ptr(q_codes), a, ptr(offsets), ptr(postings), n_c, b, top_k, mask_mode, ptr(mask),
-         m_sb, m_si, float(score_div), int(bool(sorted)), ptr(out), _lib.index_dtype(out),
+         m_sb, m_si, float(score_div), int(bool(sorted)), ptr(row_order), ptr(out), _lib.index_dtype(out),
          ptr(stats), ptr(ws), ws_bytes, stream_of(q))
     return (out, stats) if with_stats else out
 

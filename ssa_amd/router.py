@@ -125,8 +125,9 @@ class CodebookRouter(nn.Module):
 
         ``with_order`` also returns ``order`` (int32 [B, h_kv, n]): per head, the
         query positions grouped by their best code (ascending within a code).
-        Processing rows in this order lets rows that share candidate keys run
-        together; it changes no result."""
+        Selection already runs its rows in this order, and attention can too:
+        rows that share buckets and candidate keys then run together.  It
+        changes no result."""
         if not hard:
             raise NotImplementedError(
                 "hard=False (Gumbel-softmax assignment) is not supported: the reference's one-hot "
@@ -150,13 +151,13 @@ class CodebookRouter(nn.Module):
         offsets, postings = kernels.build_index(k_codes, self.num_codebook)
         if mask is not None:
             mask = mask.to(q.device)
+        order = query_order(q_codes, self.num_codebook) if with_order else None
         res = kernels.select(q, k, q_codes, offsets, postings, self.codes_per_key, self.top_k,
                              mode, mask, index_dtype=index_dtype, with_stats=with_stats,
-                             sorted=sorted)
+                             sorted=sorted, row_order=order)
         idx, stats = res if with_stats else (res, None)
         out = RouteResult(q_codes, k_codes, offsets, postings, idx, stats)
-        if with_order:
-            out.order = query_order(q_codes, self.num_codebook)
+        out.order = order
         out.indices_view = idx[0] if unbatched else idx
         return out
 

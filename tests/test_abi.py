@@ -87,7 +87,7 @@ def _select(L, **kw):
              q_sb=1024 * 32 * 128, q_sn=32 * 128, q_sh=128, k_sb=1024 * 8 * 128, k_sn=8 * 128,
              k_sh=128, q_codes=FAKE, a=16, offsets=FAKE, postings=FAKE, n_c=4096, b=4, top_k=512,
              mask_mode=_lib.MASK_CAUSAL, mask=NULL, mask_sb=0, mask_si=0, score_div=11.3137,
-             sorted=0, out=FAKE, out_index_dtype=_lib.INDEX_I64, stats=NULL, workspace=NULL,
+             sorted=0, row_order=NULL, out=FAKE, out_index_dtype=_lib.INDEX_I64, stats=NULL, workspace=NULL,
              workspace_bytes=0, stream=NULL)
     a.update(kw)
     st = L.ssa_select(*a.values())

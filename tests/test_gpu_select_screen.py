@@ -154,3 +154,30 @@ def test_screen_int64_output(dev, orc):
     got32, _ = _select(c, 32, _lib.MASK_CAUSAL, index_dtype=torch.int32)
     got64, _ = _select(c, 32, _lib.MASK_CAUSAL, index_dtype=torch.int64)
     assert got64.dtype == torch.int64 and torch.equal(got32.to(torch.int64), got64)
+
+
+@pytest.mark.parametrize("sorted_,ws", [(False, True), (False, False), (True, True)])
+def test_select_row_order(dev, orc, sorted_, ws):
+    """Rows processed in query order (grouped by best code) or reversed: the same
+    indices and stats.  An order entry outside [0, n) skips its slot, so the one
+    query it displaced is not written and every other row is unchanged."""
+    _say(f"select row order sorted={sorted_} ws={ws}")
+    from ssa_amd import _lib, kernels
+
+    B, n, h_kv, top_k = 2, 1500, 2, 64
+    c = _case(orc, dev, B, n, h_kv, 4, 128, 64, 4, 2, 23)
+    kw = dict(sorted=sorted_, with_stats=True, use_workspace=ws)
+    args = (c["q"], c["k"], c["qc"], c["off"], c["post"], c["b"], top_k, _lib.MASK_CAUSAL)
+    ref, st_ref = kernels.select(*args, **kw)
+    order = kernels.query_order(c["qc"], c["n_c"])
+    for o in (order, order.flip(-1).contiguous()):
+        got, st = kernels.select(*args, row_order=o, **kw)
+        assert torch.equal(got, ref) and torch.equal(st, st_ref)
+    bad = order.clone()
+    skipped = int(bad[1, 0, 700])
+    bad[1, 0, 700] = n
+    got = kernels.select(*args, row_order=bad, sorted=sorted_, use_workspace=ws)
+    keep = torch.ones(n, dtype=torch.bool, device=dev)
+    keep[skipped] = False
+    assert torch.equal(got[0], ref[0]) and torch.equal(got[1, :, 1], ref[1, :, 1])
+    assert torch.equal(got[1, keep, 0], ref[1, keep, 0])
