@@ -638,13 +638,16 @@ __global__ __launch_bounds__(64 * kLightWaves) void select_light_kernel(SelParam
 // head sum of q_s).  So |A_j - E_j| <= e_j = (6 d + 2 g + 100) u * 1.02 *
 // P_j (1 + 4 d u) / sd / g + 1e-30, and e = max_j e_j.
 //
-// Selection.  T = the k-th largest A.  Every key with A_j > T + 2e has E_j
-// above the k-th largest exact score and is selected; every key with A_j <
-// T - 2e is below it and is not; the keys between (at most kScrBorder, else
-// the row takes the exact pass) are rescored in the canonical order and the
-// best (k - #above) of them by (score desc, index asc) complete the set.  The
-// row is written in index order.  Non-finite scores or bounds send the row to
-// the exact pass.
+// Selection (select_pick_kernel).  T = the k-th largest A lies in a band
+// [lo, hi] of A values found by at most two 256-bin histogram passes.  At
+// least k keys have A >= lo, so the k-th largest exact score E* >= lo - e;
+// fewer than k keys have A > hi, so E* <= hi + e.  Every key with A_j > hi + 2e
+// then has E_j > E* and is selected; every key with A_j < lo - 2e has E_j < E*
+// and is not.  The keys between (at most kScrBorder, else the row takes the
+// exact pass) are rescored in the canonical order, and the best (k - #above)
+// of them by (score desc, index asc) complete the set: the selected set's
+// members among them are exactly those.  The row is written in index order.
+// Non-finite scores or bounds send the row to the exact pass.
 
 
 __device__ __forceinline__ uint16_t bf16_rne_bits(float f) {
