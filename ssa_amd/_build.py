@@ -33,6 +33,8 @@ HIPCC_FLAGS = [
     "-fhip-fp32-correctly-rounded-divide-sqrt",
     "-fno-gpu-flush-denormals-to-zero",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # matrix-core results in VGPRs, read by the VALU without v_accvgpr copies
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wall",
 ]
 

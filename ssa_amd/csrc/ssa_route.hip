@@ -203,6 +203,90 @@ size_t route_vectors_tile_smem(int d) {
   return sizeof(float) * (static_cast<size_t>(32 + kRvRows) * (d + 4) + static_cast<size_t>(kRvRows) * 32);
 }
 
+// route_dim == 32, head_dim a multiple of 8: one lane per output row, all 32
+// coordinates in registers.  W is the same for every lane, so its
+// entries are wave-uniform scalar loads (s_load) and every fmaf takes its W
+// operand from an SGPR: no LDS traffic.  The lane reads its own x row in
+// 8-element pieces, one piece ahead of the one being multiplied.  Same per-score
+// chains as the kernels above: one fmaf chain over t ascending per head, the
+// group summed in head order, then / group and normalized.
+constexpr int kRrThreads = 256;
+
+struct Piece8 {
+  float v[8];
+};
+__device__ __forceinline__ Piece8 load8(const uint16_t* p) {
+  const uint4 u = *reinterpret_cast<const uint4*>(p);
+  Piece8 r;
+  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    r.v[2 * e] = __uint_as_float(w[e] << 16);
+    r.v[2 * e + 1] = __uint_as_float(w[e] & 0xFFFF0000u);
+  }
+  return r;
+}
+__device__ __forceinline__ Piece8 load8(const float* p) {
+  const float4 a = reinterpret_cast<const float4*>(p)[0];
+  const float4 b = reinterpret_cast<const float4*>(p)[1];
+  return Piece8{{a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w}};
+}
+
+template <typename T>
+__global__ __launch_bounds__(kRrThreads) void route_vectors_row_kernel(
+    const T* __restrict__ x, int64_t n, int h_in, int group, int d, int64_t sb, int64_t sn,
+    int64_t sh, const float* __restrict__ w, float* __restrict__ out) {
+  constexpr int d_s = 32;
+  const int h_out = h_in / group;
+  const int64_t tiles = (n + kRrThreads - 1) / kRrThreads;
+  const int64_t bh = blockIdx.x / tiles;
+  const int64_t i = (blockIdx.x % tiles) * kRrThreads + threadIdx.x;
+  const int64_t b = bh / h_out;
+  const int h = static_cast<int>(bh % h_out);
+  const int64_t ic = i < n ? i : n - 1;  // lanes past n compute row n-1 and store nothing
+  const T* xb = x + b * sb + static_cast<int64_t>(h) * group * sh + ic * sn;
+  const int pieces = d / 8;
+  const int total = group * pieces;
+
+  float sum[32], acc[32];
+#pragma unroll
+  for (int s = 0; s < 32; ++s) sum[s] = acc[s] = 0.0f;
+  Piece8 cur = load8(xb);
+  for (int c = 0; c < total; ++c) {
+    const int gg = c / pieces;
+    const int t0 = (c - gg * pieces) * 8;
+    const int cn = c + 1 < total ? c + 1 : c;
+    const int ggn = cn / pieces;
+    const Piece8 nxt = load8(xb + static_cast<int64_t>(ggn) * sh + (cn - ggn * pieces) * 8);
+#pragma unroll
+    for (int s = 0; s < d_s; ++s) {
+      const float* ws = w + static_cast<int64_t>(s) * d + t0;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[s] = fma_rn(cur.v[e], ws[e], acc[s]);
+    }
+    if (t0 + 8 == d) {  // head gg complete: fold its chain into the group sum
+#pragma unroll
+      for (int s = 0; s < 32; ++s) {
+        sum[s] = (gg == 0) ? acc[s] : sum[s] + acc[s];
+        acc[s] = 0.0f;
+      }
+    }
+    cur = nxt;
+  }
+  float nrm = 0.0f;
+#pragma unroll
+  for (int s = 0; s < d_s; ++s) {
+    sum[s] = sum[s] / static_cast<float>(group);
+    nrm = fma_rn(sum[s], sum[s], nrm);
+  }
+  const float den = fmaxf(sqrtf(nrm), 1e-12f);
+  if (i < n) {
+    float* o = out + (bh * n + i) * d_s;
+#pragma unroll
+    for (int s = 0; s < d_s; ++s) o[s] = sum[s] / den;
+  }
+}
+
 // Row-wise F.normalize: one thread per row.
 __global__ void normalize_rows_kernel(const float* __restrict__ x, int64_t rows, int d_s,
                                       float* __restrict__ out) {
@@ -351,16 +435,18 @@ __global__ __launch_bounds__(kTopThreads) void code_topk_kernel(
 //   |exact  - sum x c| <= 32 * 2^-24 sum|x c|        (the canonical fmaf chain)
 // and with sum|x c| <= ||x|| ||c||:  |approx - exact| <= eps =
 // 1.02 * 2^-8 * ||x|| * max_c ||c||.  Every code of the exact top-`top` therefore
-// scores approx >= L - 2 eps.  Pass 2 re-runs the MFMAs and collects those codes (at
-// most kMfCap per row); pass 3 rescores them in the canonical fp32 order and
-// keeps the exact top-`top` (score desc, code asc).  Rows that collect more
-// than kMfCap codes (or have non-finite inputs) flag their 64-row group, which
-// code_topk_kernel then recomputes exhaustively.
+// scores approx >= L - 2 eps.  Pass 2 re-runs the MFMAs and collects those codes:
+// each lane appends the hits of its own (row, code quarter) to a private LDS
+// list with a register counter (at most mf_cap per list), so no atomics and no
+// LDS round trips; a lane visits the append code only for the scores that hit.
+// Pass 3 rescores a row's four lists in the canonical fp32 order and keeps the
+// exact top-`top` (score desc, code asc).  Rows with an overflowing list (or
+// non-finite inputs) flag their 64-row group, which code_topk_kernel then
+// recomputes exhaustively.
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float floatx4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kMfRows = 256;     // rows per block: 4 waves x 4 row tiles of 16
-constexpr int kMfCap = 64;       // candidate codes kept per row
 constexpr float kMfEps = 0.0039844f;  // 1.02 * 2^-8
 
 __device__ __forceinline__ uint16_t bf16_rne(float f) {
@@ -375,22 +461,29 @@ __host__ __device__ inline int n_c_padded(int n_c) { return (n_c + 15) / 16 * 16
 // and row (M).  The 4M maxima of a row must be >= top; for top <= 16, M = 2Q
 // capped at 8.  For top 17..32 the screen keeps 32 per lane: with only 8 (4M =
 // top) the bound L would be the smallest maximum and collect about 140 codes per
-// row at N_c = 8192, overflowing kMfCap everywhere; with 32 it collects about 45.
+// row at N_c = 8192; with 32 it collects about 45.  mf_cap: list capacity per
+// (row, code quarter).  At config 3 a row collects about 6 codes for top 4 and
+// 25 for top 16 (at most 10 and 19 in one quarter in a sample of 8192 rows).
 __host__ __device__ constexpr int mf_q(int top) { return top <= 4 ? 1 : top <= 8 ? 2 : top <= 16 ? 4 : 8; }
 __host__ __device__ constexpr int mf_segments(int q) { return q >= 8 ? 32 : (2 * q < 8 ? 2 * q : 8); }
+__host__ __device__ constexpr int mf_cap(int q) { return q <= 1 ? 16 : q <= 2 ? 20 : q <= 4 ? 24 : 32; }
 
 // LDS: one region used first for the segment maxima ([4 waves][4M][64] fp32),
-// then for the pass-3 lists ([4][top][64] u64) followed by the pass-2
-// candidates ([4][kMfCap][64] u16); the per-row counters come after it.
+// then for the pass-3 lists ([4][top][64] u64, top > 16 only: smaller tops keep
+// them in registers) followed by the pass-2 candidates ([4 waves][4 row
+// tiles][mf_cap][64 lanes] u16); the list counts ([4][4][64] int) come after it.
+__host__ __device__ constexpr size_t mf_list_bytes(int top) {
+  return mf_q(top) >= 8 ? static_cast<size_t>(4) * top * 64 * sizeof(uint64_t) : 0;
+}
 __host__ __device__ inline size_t code_topk_mfma_region(int top) {
-  const size_t lists = static_cast<size_t>(4) * top * 64 * sizeof(uint64_t);
-  const size_t cand = sizeof(uint16_t) * 4 * kMfCap * 64;
+  const size_t lists = mf_list_bytes(top);
+  const size_t cand = sizeof(uint16_t) * 4 * 4 * mf_cap(mf_q(top)) * 64;
   const size_t segs = sizeof(float) * 4 * 4 * mf_segments(mf_q(top)) * 64;
   return lists + cand > segs ? lists + cand : segs;
 }
 
 __host__ __device__ inline size_t code_topk_mfma_smem(int top) {
-  return code_topk_mfma_region(top) + sizeof(int) * 4 * 64;
+  return code_topk_mfma_region(top) + sizeof(int) * 4 * 4 * 64;
 }
 
 // bf16 copy of the codebook, zero-padded to [h][n_c_pad][32], and the largest
@@ -435,6 +528,12 @@ __global__ void zero_u32_kernel(uint32_t* __restrict__ p, int count) {
   const int e = blockIdx.x * blockDim.x + threadIdx.x;
   if (e < count) p[e] = 0u;
 }
+
+// NaN-propagating maximum (v_maximum3_f32 on gfx950).  Unlike fmaxf it needs no
+// canonicalizing v_max of each matrix-core result first, so the screen's
+// running maxima cost one instruction per two scores.  A NaN score can only
+// come from a non-finite input row or code, whose group is flagged anyway.
+__device__ __forceinline__ float vmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
 
 template <int N>
 __device__ __forceinline__ void sort_desc(float (&v)[N]) {
@@ -481,11 +580,12 @@ __global__ __launch_bounds__(256) void code_topk_mfma_kernel(
     float temperature, int top, int32_t* __restrict__ codes, uint8_t* __restrict__ flags) {
   constexpr int M = mf_segments(Q);  // segment maxima per lane and row
   constexpr int G = M > 8 ? M / 8 : 1;  // 8-tile groups per pass-1 step
+  constexpr int CAP = mf_cap(Q);
   extern __shared__ __align__(16) unsigned char smem_raw[];
-  const size_t list_bytes = static_cast<size_t>(4) * top * 64 * 8;
-  uint64_t* lists = reinterpret_cast<uint64_t*>(smem_raw);               // [4][top][64] (pass 3)
-  uint16_t* cand = reinterpret_cast<uint16_t*>(smem_raw + list_bytes);   // [4][kMfCap][64] (pass 2)
-  int* cnt = reinterpret_cast<int*>(smem_raw + code_topk_mfma_region(top));
+  const size_t list_bytes = mf_list_bytes(top);
+  uint64_t* lists = reinterpret_cast<uint64_t*>(smem_raw);               // [4][top][64] (pass 3, Q = 8)
+  uint16_t* cand = reinterpret_cast<uint16_t*>(smem_raw + list_bytes);   // [4][4][CAP][64] (pass 2)
+  int* qcnt = reinterpret_cast<int*>(smem_raw + code_topk_mfma_region(top));  // [4][4][64]
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int q4 = lane >> 4, c16 = lane & 15;
@@ -519,7 +619,6 @@ __global__ __launch_bounds__(256) void code_topk_mfma_kernel(
     }
   }
   const bool bad_l = !(eps_l <= 3.0e38f);
-  cnt[wave * 64 + lane] = 0;
 
   float smax[4][M];
 #pragma unroll
@@ -540,10 +639,16 @@ __global__ __launch_bounds__(256) void code_topk_mfma_kernel(
   auto frag = [&](int tile) -> bf16x8_t {
     return *reinterpret_cast<const bf16x8_t*>(cbh + (static_cast<int64_t>(tile) * 16 + c16) * 32 + q4 * 8);
   };
-  auto group8 = [&](int t, int seg0) {
-    bf16x8_t a[8];
+  // The next 8-tile group's fragments load while the current group's MFMAs run;
+  // the prefetch start is clamped to the last full group, so every load is in
+  // range (the extra one near the end re-reads a group already used).  Q = 8
+  // (128 segment maxima in registers) loads each group just before use.
+  constexpr bool PF = Q < 8;
+  auto load8 = [&](bf16x8_t (&a)[8], int t) {
 #pragma unroll
     for (int u = 0; u < 8; ++u) a[u] = frag(t + u);
+  };
+  auto group8 = [&](const bf16x8_t (&a)[8], int seg0) {
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       floatx4_t sc[4];
@@ -553,30 +658,45 @@ __global__ __launch_bounds__(256) void code_topk_mfma_kernel(
 #pragma unroll
       for (int nt = 0; nt < 4; ++nt)
         smax[nt][(seg0 + u) % M] =
-            fmaxf(smax[nt][(seg0 + u) % M], fmaxf(fmaxf(sc[nt][0], sc[nt][1]), fmaxf(sc[nt][2], sc[nt][3])));
+            vmax(vmax(vmax(sc[nt][0], sc[nt][1]), sc[nt][2]), vmax(sc[nt][3], smax[nt][(seg0 + u) % M]));
     }
   };
+  const int last8 = ntile_full - 8;  // first tile of the last full group (used when >= 0)
   {
     int t = 0;
+    bf16x8_t a[8];
+    if (PF && ntile_full >= 8) load8(a, 0);
+    auto step = [&](int tg, int seg0) {  // group at tile tg; `a` holds it when PF
+      if constexpr (PF) {
+        bf16x8_t an[8];
+        load8(an, min(tg + 8, last8));
+        group8(a, seg0);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) a[u] = an[u];
+      } else {
+        load8(a, tg);
+        group8(a, seg0);
+      }
+    };
     for (; t + 8 * G <= ntile_full; t += 8 * G) {
 #pragma unroll
-      for (int gi = 0; gi < G; ++gi) group8(t + 8 * gi, 8 * gi);
+      for (int gi = 0; gi < G; ++gi) step(t + 8 * gi, 8 * gi);
     }
     if (G > 1)
-      for (; t + 8 <= ntile_full; t += 8) group8(t, 0);
+      for (; t + 8 <= ntile_full; t += 8) step(t, 0);
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       if (t + u < ntile) {
-        const bf16x8_t a = frag(t + u);
+        const bf16x8_t af = frag(t + u);
         const int cbase = (t + u) * 16 + q4 * 4;
 #pragma unroll
         for (int nt = 0; nt < 4; ++nt) {
-          const floatx4_t sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bfrag[nt], floatx4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+          const floatx4_t sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bfrag[nt], floatx4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
           float m = -INFINITY;
 #pragma unroll
           for (int e = 0; e < 4; ++e)
-            if (cbase + e < n_c) m = fmaxf(m, sc[e]);
-          smax[nt][u % M] = fmaxf(smax[nt][u % M], m);
+            if (cbase + e < n_c) m = vmax(m, sc[e]);
+          smax[nt][u % M] = vmax(smax[nt][u % M], m);
         }
       }
     }
@@ -613,33 +733,41 @@ __global__ __launch_bounds__(256) void code_topk_mfma_kernel(
     for (int i = 1; i < C; ++i)
       if (i == top - 1) lb = v[i];
     thr_l = lb - 2.0f * eps_l;
+    if (r0 + lane >= rows) thr_l = INFINITY;  // padding rows collect nothing
   }
   __syncthreads();  // pass 2 writes candidates over other waves' maxima
   float thr[4];
 #pragma unroll
   for (int nt = 0; nt < 4; ++nt) thr[nt] = __shfl(thr_l, nt * 16 + c16);
 
-  // ---- pass 2: collect codes whose approximate score reaches the threshold
-  // (a uniform branch skips the appends when no lane has such a code).
-  auto collect = [&](const floatx4_t& sc, int nt, int cbase) {
-    const bool hit = (sc[0] >= thr[nt]) || (sc[1] >= thr[nt]) || (sc[2] >= thr[nt]) || (sc[3] >= thr[nt]);
-    if (__ballot(hit)) {
+  // ---- pass 2: collect codes whose approximate score reaches the threshold.
+  // Lane (q4, c16) owns the list of row nt*16 + c16 and code quarter q4 of row
+  // tile nt; qc[nt] counts its hits (past CAP the last slot is overwritten and
+  // the count flags the row).  Each score's append is skipped by a uniform
+  // branch unless some lane hits with that score.
+  uint16_t* cl = cand + static_cast<size_t>(wave) * 4 * CAP * 64 + lane;  // list nt: cl[(nt*CAP + pos)*64]
+  int qc[4] = {0, 0, 0, 0};
+  auto collect = [&](const floatx4_t& sc, int nt, int cbase, bool partial) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        if (sc[e] >= thr[nt] && cbase + e < n_c) {
-          const int r = nt * 16 + c16;
-          const int pos = atomicAdd(&cnt[wave * 64 + r], 1);
-          if (pos < kMfCap) cand[(wave * kMfCap + pos) * 64 + r] = static_cast<uint16_t>(cbase + e);
-        }
+    for (int e = 0; e < 4; ++e) {
+      const bool hit = sc[e] >= thr[nt] && (!partial || cbase + e < n_c);
+      if (__builtin_expect(hit, 0)) {
+        cl[(nt * CAP + min(qc[nt], CAP - 1)) * 64] = static_cast<uint16_t>(cbase + e);
+        ++qc[nt];
       }
     }
   };
   {
+    // full 8-tile groups (prefetched as in pass 1), then the remaining tiles,
+    // including the one that can hold codes past n_c, with the code check
     int t = 0;
-    for (; t + 8 <= ntile; t += 8) {
-      bf16x8_t a[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) a[u] = frag(t + u);
+    bf16x8_t a[8], an[8];
+    if (PF && ntile_full >= 8) load8(a, 0);
+    for (; t + 8 <= ntile_full; t += 8) {
+      if constexpr (PF)
+        load8(an, min(t + 8, last8));
+      else
+        load8(a, t);
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
         floatx4_t sc[4];
@@ -647,57 +775,119 @@ __global__ __launch_bounds__(256) void code_topk_mfma_kernel(
         for (int nt = 0; nt < 4; ++nt)
           sc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[u], bfrag[nt], floatx4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 #pragma unroll
-        for (int nt = 0; nt < 4; ++nt) collect(sc[nt], nt, (t + u) * 16 + q4 * 4);
+        for (int nt = 0; nt < 4; ++nt) collect(sc[nt], nt, (t + u) * 16 + q4 * 4, false);
+      }
+      if constexpr (PF) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) a[u] = an[u];
       }
     }
     for (; t < ntile; ++t) {
-      const bf16x8_t a = frag(t);
+      const bf16x8_t af = frag(t);
 #pragma unroll
       for (int nt = 0; nt < 4; ++nt)
-        collect(__builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bfrag[nt], floatx4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0),
-                nt, t * 16 + q4 * 4);
+        collect(__builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bfrag[nt], floatx4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0),
+                nt, t * 16 + q4 * 4, true);
     }
   }
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) qcnt[(wave * 4 + nt) * 64 + lane] = qc[nt];
   __syncthreads();
 
-  // ---- pass 3: exact rescoring of the collected codes (one lane per row)
+  // ---- pass 3: exact rescoring of the collected codes (one lane per row).
+  // Row `lane` is row tile lane / 16, column lane % 16; its four quarter lists
+  // belong to lanes q*16 + lane % 16 of that row tile.
   const int64_t row = r0 + lane;
-  const int m = cnt[wave * 64 + lane];
-  const bool over = bad_l || m > kMfCap || m < top;
+  const int rt = lane >> 4, rc = lane & 15;
+  int qn[4], m = 0;
+  bool list_over = false;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    qn[q] = qcnt[(wave * 4 + rt) * 64 + q * 16 + rc];
+    list_over = list_over || qn[q] > CAP;
+    m += qn[q];
+  }
+  const bool over = bad_l || list_over || m < top;
   if (row < rows && !over) {
     float xr[32];
 #pragma unroll
     for (int s = 0; s < 32; ++s) xr[s] = (s < d_s) ? xb[row * d_s + s] : 0.0f;
     const float* cb = chat + static_cast<int64_t>(hh) * n_c * d_s;
-    uint64_t* my = lists + static_cast<int64_t>(wave) * top * 64 + lane;  // entry p at my[p * 64]
     const bool scale = (temperature != 1.0f);
-    int nb = 0;
-    for (int i = 0; i < m; ++i) {
-      const int c = cand[(wave * kMfCap + i) * 64 + lane];
+    const uint16_t* rl = cand + (static_cast<size_t>(wave) * 4 + rt) * CAP * 64 + rc;
+    const int b1 = qn[0], b2 = b1 + qn[1], b3 = b2 + qn[2];  // list starts in row order
+    auto code_at = [&](int i) -> int {  // entry i of the row: list q, position j
+      const int q = (i >= b1 ? 1 : 0) + (i >= b2 ? 1 : 0) + (i >= b3 ? 1 : 0);
+      const int j = i - (q == 0 ? 0 : q == 1 ? b1 : q == 2 ? b2 : b3);
+      return rl[(j * 64) + q * 16];
+    };
+    auto code_row = [&](int c, float4 (&cv)[8]) {
       const float4* cr = reinterpret_cast<const float4*>(cb + static_cast<int64_t>(c) * d_s);
+#pragma unroll
+      for (int s4 = 0; s4 < 8; ++s4) cv[s4] = (s4 * 4 < d_s) ? cr[s4] : make_float4(0.f, 0.f, 0.f, 0.f);
+    };
+    auto exact_key = [&](int c, const float4 (&cv)[8]) -> uint64_t {
       float acc = 0.0f;
 #pragma unroll
       for (int s4 = 0; s4 < 8; ++s4) {
         if (s4 * 4 < d_s) {
-          const float4 cv = cr[s4];
-          acc = fma_rn(xr[s4 * 4 + 0], cv.x, acc);
-          acc = fma_rn(xr[s4 * 4 + 1], cv.y, acc);
-          acc = fma_rn(xr[s4 * 4 + 2], cv.z, acc);
-          acc = fma_rn(xr[s4 * 4 + 3], cv.w, acc);
+          acc = fma_rn(xr[s4 * 4 + 0], cv[s4].x, acc);
+          acc = fma_rn(xr[s4 * 4 + 1], cv[s4].y, acc);
+          acc = fma_rn(xr[s4 * 4 + 2], cv[s4].z, acc);
+          acc = fma_rn(xr[s4 * 4 + 3], cv[s4].w, acc);
         }
       }
       if (scale) acc = acc / temperature;
-      const uint64_t key = composite_key(acc, static_cast<uint32_t>(c));
-      if (nb == top && key <= my[(top - 1) * 64]) continue;
-      int p = (nb < top) ? nb++ : top - 1;
-      while (p > 0 && my[(p - 1) * 64] < key) {
-        my[p * 64] = my[(p - 1) * 64];
-        --p;
-      }
-      my[p * 64] = key;
-    }
+      return composite_key(acc, static_cast<uint32_t>(c));
+    };
+    // The next candidate's code row loads while the current one is scored.
+    int c = code_at(0);
+    float4 cv[8];
+    code_row(c, cv);
     int32_t* out = codes + (bh * rows + row) * top;
-    for (int p = 0; p < top; ++p) out[p] = static_cast<int32_t>(key_index(my[p * 64]));
+    if constexpr (Q <= 4) {
+      // top <= 16: a sorted register list (static indices), insertion by a
+      // compare-and-shift pass from the bottom
+      constexpr int TM = 4 * Q;
+      uint64_t best[TM];
+#pragma unroll
+      for (int p = 0; p < TM; ++p) best[p] = 0ull;  // below every key
+      for (int i = 0; i < m; ++i) {
+        const int cn = code_at(min(i + 1, m - 1));
+        float4 cvn[8];
+        code_row(cn, cvn);
+        const uint64_t key = exact_key(c, cv);
+#pragma unroll
+        for (int p = TM - 1; p > 0; --p) best[p] = key > best[p - 1] ? best[p - 1] : (key > best[p] ? key : best[p]);
+        best[0] = key > best[0] ? key : best[0];
+        c = cn;
+#pragma unroll
+        for (int s4 = 0; s4 < 8; ++s4) cv[s4] = cvn[s4];
+      }
+#pragma unroll
+      for (int p = 0; p < TM; ++p)
+        if (p < top) out[p] = static_cast<int32_t>(key_index(best[p]));
+    } else {
+      uint64_t* my = lists + static_cast<int64_t>(wave) * top * 64 + lane;  // entry p at my[p * 64]
+      int nb = 0;
+      for (int i = 0; i < m; ++i) {
+        const int cn = code_at(min(i + 1, m - 1));
+        float4 cvn[8];
+        code_row(cn, cvn);
+        const uint64_t key = exact_key(c, cv);
+        c = cn;
+#pragma unroll
+        for (int s4 = 0; s4 < 8; ++s4) cv[s4] = cvn[s4];
+        if (nb == top && key <= my[(top - 1) * 64]) continue;
+        int p = (nb < top) ? nb++ : top - 1;
+        while (p > 0 && my[(p - 1) * 64] < key) {
+          my[p * 64] = my[(p - 1) * 64];
+          --p;
+        }
+        my[p * 64] = key;
+      }
+      for (int p = 0; p < top; ++p) out[p] = static_cast<int32_t>(key_index(my[p * 64]));
+    }
   }
   const bool any_over = __ballot(row < rows && over) != 0ull;
   if (lane == 0 && r0 < rows) flags[bh * ((rows + 63) / 64) + r0 / 64] = any_over ? 1 : 0;
@@ -738,6 +928,20 @@ int launch_route_vectors(const void* x, int dtype, int64_t batch, int64_t n, int
   const bool vec4 = (sb % 4 == 0) && (sn % 4 == 0) && (sh % 4 == 0) &&
                     (reinterpret_cast<uintptr_t>(x) % (4 * esz) == 0) &&
                     (reinterpret_cast<uintptr_t>(w) % 16 == 0);
+  // 16-byte pieces of 8 elements: element strides and the base aligned to them
+  const int64_t pe = 16 / esz;
+  const bool piece8 = (d % 8 == 0) && (sb % pe == 0) && (sn % pe == 0) && (sh % pe == 0) &&
+                      (reinterpret_cast<uintptr_t>(x) % 16 == 0);
+  if (d_s == 32 && piece8) {
+    const int64_t grid = batch * (h_in / group) * ceil_div(n, kRrThreads);
+    if (dtype == SSA_DTYPE_BF16)
+      route_vectors_row_kernel<uint16_t><<<dim3(static_cast<unsigned>(grid)), kRrThreads, 0, st>>>(
+          static_cast<const uint16_t*>(x), n, h_in, group, d, sb, sn, sh, w, out);
+    else
+      route_vectors_row_kernel<float><<<dim3(static_cast<unsigned>(grid)), kRrThreads, 0, st>>>(
+          static_cast<const float*>(x), n, h_in, group, d, sb, sn, sh, w, out);
+    return check_launch("route_vectors_row_kernel");
+  }
   if (d_s <= 32 && vec4 && route_vectors_tile_smem(d) <= 64 * 1024) {
     const int64_t grid = batch * (h_in / group) * ceil_div(n, kRvRows);
     const size_t smem = route_vectors_tile_smem(d);
