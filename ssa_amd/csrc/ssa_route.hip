@@ -287,6 +287,84 @@ __global__ __launch_bounds__(kRrThreads) void route_vectors_row_kernel(
   }
 }
 
+// GQA groups (group > 1), route_dim == 32, head_dim a multiple of 8: 64 rows
+// per block and the group's heads spread over the block's 4 waves (wave w
+// takes heads w, w+4, ...), so a head's chain runs in a wave of its own with W
+// in SGPRs as above.  Each round of 4 heads passes its per-head chains through
+// LDS, where thread t (row t / 4, coordinates 8 (t % 4) .. +7) adds them to the
+// group sum in head order, which keeps the sum bit-identical with one thread
+// per row.  The norm is then the canonical chain over the row's 32 means.
+constexpr int kRsRows = 64;
+
+template <typename T>
+__global__ __launch_bounds__(256) void route_vectors_split_kernel(
+    const T* __restrict__ x, int64_t n, int h_in, int group, int d, int64_t sb, int64_t sn,
+    int64_t sh, const float* __restrict__ w, float* __restrict__ out) {
+  constexpr int d_s = 32;
+  __shared__ float part[4][kRsRows][d_s + 1];  // per-wave head chains, padded rows
+  __shared__ float mean[kRsRows][d_s + 1];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int h_out = h_in / group;
+  const int64_t tiles = (n + kRsRows - 1) / kRsRows;
+  const int64_t bh = blockIdx.x / tiles;
+  const int64_t i0 = (blockIdx.x % tiles) * kRsRows;
+  const int64_t b = bh / h_out;
+  const int h = static_cast<int>(bh % h_out);
+  const int64_t ic = (i0 + lane < n) ? i0 + lane : n - 1;  // rows past n: row n-1, not stored
+  const T* xr = x + b * sb + static_cast<int64_t>(h) * group * sh + ic * sn;
+  const int cr = threadIdx.x >> 2, cs0 = 8 * (threadIdx.x & 3);
+  const int pieces = d / 8;
+  float sum[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) sum[k] = 0.0f;
+  for (int r0 = 0; r0 < group; r0 += 4) {
+    const int gg = r0 + wave;
+    if (gg < group) {  // wave-uniform
+      float acc[d_s];
+#pragma unroll
+      for (int s = 0; s < d_s; ++s) acc[s] = 0.0f;
+      const T* xh = xr + static_cast<int64_t>(gg) * sh;
+      Piece8 cur = load8(xh);
+#pragma unroll 1
+      for (int c = 0; c < pieces; ++c) {
+        const Piece8 nxt = load8(xh + (c + 1 < pieces ? c + 1 : c) * 8);
+        const float* wc = w + c * 8;
+#pragma unroll
+        for (int s = 0; s < d_s; ++s) {
+          const float* ws = wc + static_cast<int64_t>(s) * d;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[s] = fma_rn(cur.v[e], ws[e], acc[s]);
+        }
+        cur = nxt;
+      }
+#pragma unroll
+      for (int s = 0; s < d_s; ++s) part[wave][lane][s] = acc[s];
+    }
+    __syncthreads();
+    for (int j = 0; j < 4 && r0 + j < group; ++j) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) sum[k] = (r0 + j == 0) ? part[j][cr][cs0 + k] : sum[k] + part[j][cr][cs0 + k];
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    sum[k] = sum[k] / static_cast<float>(group);
+    mean[cr][cs0 + k] = sum[k];
+  }
+  __syncthreads();
+  float nrm = 0.0f;
+#pragma unroll
+  for (int s = 0; s < d_s; ++s) nrm = fma_rn(mean[cr][s], mean[cr][s], nrm);
+  const float den = fmaxf(sqrtf(nrm), 1e-12f);
+  if (i0 + cr < n) {
+    float* o = out + (bh * n + i0 + cr) * d_s + cs0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) o[k] = sum[k] / den;
+  }
+}
+
+
 // Row-wise F.normalize: one thread per row.
 __global__ void normalize_rows_kernel(const float* __restrict__ x, int64_t rows, int d_s,
                                       float* __restrict__ out) {
@@ -573,8 +651,10 @@ __device__ __forceinline__ void merge_top_desc(float (&v)[N], const float (&w)[N
     }
 }
 
+// Top <= 4 fits 128 VGPRs and 36 KB of LDS: 4 blocks per CU, so the grid of a
+// config-3 head set (1024 blocks) runs in one round.
 template <int Q>
-__global__ __launch_bounds__(256) void code_topk_mfma_kernel(
+__global__ __launch_bounds__(256, Q == 1 ? 4 : 1) void code_topk_mfma_kernel(
     const float* __restrict__ xhat, int64_t rows, int h, const float* __restrict__ chat,
     const uint16_t* __restrict__ cbf, const uint32_t* __restrict__ cmax_bits, int n_c, int d_s,
     float temperature, int top, int32_t* __restrict__ codes, uint8_t* __restrict__ flags) {
@@ -857,12 +937,12 @@ __global__ __launch_bounds__(256) void code_topk_mfma_kernel(
         float4 cvn[8];
         code_row(cn, cvn);
         const uint64_t key = exact_key(c, cv);
-#pragma unroll
-        for (int p = TM - 1; p > 0; --p) best[p] = key > best[p - 1] ? best[p - 1] : (key > best[p] ? key : best[p]);
-        best[0] = key > best[0] ? key : best[0];
         c = cn;
 #pragma unroll
         for (int s4 = 0; s4 < 8; ++s4) cv[s4] = cvn[s4];
+#pragma unroll
+        for (int p = TM - 1; p > 0; --p) best[p] = key > best[p - 1] ? best[p - 1] : (key > best[p] ? key : best[p]);
+        best[0] = key > best[0] ? key : best[0];
       }
 #pragma unroll
       for (int p = 0; p < TM; ++p)
@@ -932,6 +1012,16 @@ int launch_route_vectors(const void* x, int dtype, int64_t batch, int64_t n, int
   const int64_t pe = 16 / esz;
   const bool piece8 = (d % 8 == 0) && (sb % pe == 0) && (sn % pe == 0) && (sh % pe == 0) &&
                       (reinterpret_cast<uintptr_t>(x) % 16 == 0);
+  if (d_s == 32 && piece8 && group > 1) {
+    const int64_t grid = batch * (h_in / group) * ceil_div(n, kRsRows);
+    if (dtype == SSA_DTYPE_BF16)
+      route_vectors_split_kernel<uint16_t><<<dim3(static_cast<unsigned>(grid)), 256, 0, st>>>(
+          static_cast<const uint16_t*>(x), n, h_in, group, d, sb, sn, sh, w, out);
+    else
+      route_vectors_split_kernel<float><<<dim3(static_cast<unsigned>(grid)), 256, 0, st>>>(
+          static_cast<const float*>(x), n, h_in, group, d, sb, sn, sh, w, out);
+    return check_launch("route_vectors_split_kernel");
+  }
   if (d_s == 32 && piece8) {
     const int64_t grid = batch * (h_in / group) * ceil_div(n, kRrThreads);
     if (dtype == SSA_DTYPE_BF16)
