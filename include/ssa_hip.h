@@ -184,6 +184,29 @@ int ssa_sparse_attention(const void* q, const void* k, const void* v, int dtype,
                          int64_t o_sb, int64_t o_sn,
                          int64_t o_sh, int32_t* error_flag, void* stream);
 
+/* Gradients of ssa_sparse_attention with respect to q, k and v, given the
+ * forward output `out` and the output gradient `dout`.  Replaces the autograd
+ * backward of sparse_exact_attention (gather -> einsum -> / scale -> softmax ->
+ * einsum, ssa/attention.py:64-113), which the reference's training path runs
+ * (tests/test_integration.py:32-49).  Same arguments as ssa_sparse_attention
+ * for q, k, v, idx, scale_div, causal and row_order (duplicated slots count
+ * once each, dropped slots not at all; an index outside [0, n) sets
+ * *error_flag).  out and dout: [batch][n][h_q][d] with their own strides and
+ * types (out_dtype, dout_dtype: f32 or bf16).
+ *   dq fp32 [batch][n][h_q][d] contiguous: each processed row writes its own
+ *      (a row never listed in row_order is not written);
+ *   dk, dv fp32 [batch][n][h_kv][d] contiguous: zeroed, then accumulated.
+ * Arithmetic is fp32 (softmax recomputed from q and k).
+ * Limits: d in [1, 256], g <= 16. */
+int ssa_sparse_attention_backward(
+    const void* q, const void* k, const void* v, int dtype, int64_t batch, int64_t n, int h_q,
+    int h_kv, int d, int64_t q_sb, int64_t q_sn, int64_t q_sh, int64_t k_sb, int64_t k_sn,
+    int64_t k_sh, int64_t v_sb, int64_t v_sn, int64_t v_sh, const void* idx, int idx_dtype,
+    int top_k, int64_t idx_sb, int64_t idx_sn, int64_t idx_sh, float scale_div, int causal,
+    const int32_t* row_order, const void* out, int out_dtype, int64_t o_sb, int64_t o_sn,
+    int64_t o_sh, const void* dout, int dout_dtype, int64_t do_sb, int64_t do_sn, int64_t do_sh,
+    float* dq, float* dk, float* dv, int32_t* error_flag, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -76,6 +76,10 @@ def lib():
     L.oracle_dense_attention.argtypes = [
         _f32p, _f32p, _f32p, _i64, _int, _int, _int, _dbl, _int, _f64p,
     ]
+    L.oracle_sparse_attention_backward.argtypes = [
+        _f32p, _f32p, _f32p, _i64, _int, _int, _int, _i64p, _int, _dbl, _int, _f64p, _f64p,
+        _f64p, _f64p,
+    ]
     _lib = L
     return L
 
@@ -222,6 +226,27 @@ def sparse_attention(q, k, v, idx, scale=None, causal: bool = False, rows=None) 
         rows_a.ctypes.data if rows is not None else None, nr, out,
     )
     return out
+
+
+def sparse_attention_backward(q, k, v, idx, dout, scale=None, causal: bool = False):
+    """Gradients (dq, dk, dv) of ``sparse_attention`` in float64 for one batch
+    element, given the output gradient ``dout`` [n, h_q, d] (the autograd
+    backward of ssa/attention.py:64-113).  Indices must lie in [0, n)."""
+    q = _c(q, np.float32)
+    k = _c(k, np.float32)
+    v = _c(v, np.float32)
+    ix = _c(idx, np.int64)
+    do = _c(dout, np.float64)
+    n, h_q, d = q.shape
+    h_kv = k.shape[1]
+    kk = ix.shape[-1]
+    scale = (d ** 0.5) if scale is None else float(scale)
+    dq = np.empty((n, h_q, d), np.float64)
+    dk = np.empty((n, h_kv, d), np.float64)
+    dv = np.empty((n, h_kv, d), np.float64)
+    lib().oracle_sparse_attention_backward(q, k, v, n, h_q, h_kv, d, ix, kk, scale,
+                                           int(bool(causal)), do, dq, dk, dv)
+    return dq, dk, dv
 
 
 def dense_attention(q, k, v, causal: bool = False, scale=None) -> np.ndarray:

@@ -18,6 +18,9 @@
  *                         top-k with filler and zero pad
  *   oracle_sparse_attention  gathered exact softmax . V     ssa/attention.py:12-115
  *   oracle_dense_attention   dense SDPA with GQA expand     ssa/attention.py:118-158
+ *   oracle_sparse_attention_backward  d/dq, d/dk, d/dv of   ssa/attention.py:64-113
+ *                         oracle_sparse_attention (the reference's autograd of
+ *                         gather -> einsum -> / scale -> softmax -> einsum)
  *
  * Canonical arithmetic contract (the HIP kernels reproduce it bit for bit):
  *   - every score is fp32; inputs (bf16 or fp32) are widened exactly to fp32;
@@ -359,6 +362,92 @@ void oracle_sparse_attention(const float* q, const float* k, const float* v, int
       for (int t = 0; t < d; ++t) o[t] /= den;
     }
     free(lg);
+  }
+}
+
+/* Gradients of oracle_sparse_attention for one batch element (double precision),
+ * given dout [n][h_q][d]: the chain rule through ssa/attention.py:64-113 (gather
+ * :70-100, logits / scale :107, softmax :109, p . V :112).  With p the softmax
+ * of a (query, head) row over its slots, o = sum p v and D = dout . o:
+ *   dv[idx_m] += p_m dout;  ds_m = p_m (dout . v[idx_m] - D);
+ *   dq += ds_m k[idx_m] / scale;  dk[idx_m] += ds_m q / scale.
+ * A slot repeated in idx contributes once per slot; causal != 0 drops slots
+ * with idx > i.  Indices must lie in [0, n).  dq [n][h_q][d], dk, dv
+ * [n][h_kv][d] are overwritten.  One thread per kv head (dk, dv of a head are
+ * written by its thread only). */
+void oracle_sparse_attention_backward(const float* q, const float* k, const float* v, int64_t n,
+                                      int h_q, int h_kv, int d, const int64_t* idx, int kk,
+                                      double scale_div, int causal, const double* dout,
+                                      double* dq, double* dk, double* dv) {
+  int g = h_q / h_kv;
+  memset(dq, 0, sizeof(double) * (size_t)(n * h_q * d));
+  memset(dk, 0, sizeof(double) * (size_t)(n * h_kv * d));
+  memset(dv, 0, sizeof(double) * (size_t)(n * h_kv * d));
+#pragma omp parallel
+  {
+    double* pr = (double*)malloc(sizeof(double) * (size_t)(kk > 0 ? kk : 1));
+    double* o = (double*)malloc(sizeof(double) * (size_t)d);
+#pragma omp for schedule(static)
+    for (int h = 0; h < h_kv; ++h) {
+      for (int64_t i = 0; i < n; ++i) {
+        const int64_t* ix = idx + (i * h_kv + h) * kk;
+        for (int hq = h * g; hq < (h + 1) * g; ++hq) {
+          const float* qr = q + (i * h_q + hq) * d;
+          const double* dor = dout + (i * h_q + hq) * d;
+          double mx = -INFINITY;
+          for (int m = 0; m < kk; ++m) {
+            int64_t j = ix[m];
+            if (causal && j > i) {
+              pr[m] = -INFINITY;
+              continue;
+            }
+            const float* kr = k + (j * h_kv + h) * d;
+            double acc = 0.0;
+            for (int t = 0; t < d; ++t) acc += (double)qr[t] * (double)kr[t];
+            pr[m] = acc / scale_div;
+            if (pr[m] > mx) mx = pr[m];
+          }
+          if (mx == -INFINITY) continue;  /* no slot: zero output, zero gradients */
+          double den = 0.0;
+          for (int m = 0; m < kk; ++m) {
+            if (pr[m] == -INFINITY) {
+              pr[m] = 0.0;
+              continue;
+            }
+            pr[m] = exp(pr[m] - mx);
+            den += pr[m];
+          }
+          for (int t = 0; t < d; ++t) o[t] = 0.0;
+          for (int m = 0; m < kk; ++m) {
+            pr[m] /= den;
+            if (pr[m] == 0.0) continue;
+            const float* vr = v + (ix[m] * h_kv + h) * d;
+            for (int t = 0; t < d; ++t) o[t] += pr[m] * (double)vr[t];
+          }
+          double dd = 0.0;
+          for (int t = 0; t < d; ++t) dd += dor[t] * o[t];
+          double* dqr = dq + (i * h_q + hq) * d;
+          for (int m = 0; m < kk; ++m) {
+            int64_t j = ix[m];
+            if (causal && j > i) continue;
+            const float* kr = k + (j * h_kv + h) * d;
+            const float* vr = v + (j * h_kv + h) * d;
+            double dp = 0.0;
+            for (int t = 0; t < d; ++t) dp += dor[t] * (double)vr[t];
+            double ds = pr[m] * (dp - dd);
+            double* dkr = dk + (j * h_kv + h) * d;
+            double* dvr = dv + (j * h_kv + h) * d;
+            for (int t = 0; t < d; ++t) {
+              dqr[t] += ds * (double)kr[t] / scale_div;
+              dkr[t] += ds * (double)qr[t] / scale_div;
+              dvr[t] += pr[m] * dor[t];
+            }
+          }
+        }
+      }
+    }
+    free(pr);
+    free(o);
   }
 }
 

@@ -69,6 +69,11 @@ SIGNATURES = {
         [_vp, _vp, _vp, _int, _i64, _i64, _int, _int, _int, _i64, _i64, _i64, _i64, _i64, _i64,
          _i64, _i64, _i64, _vp, _int, _int, _i64, _i64, _i64, _flt, _int, _vp, _vp, _int, _i64,
          _i64, _i64, _vp, _vp]),
+    "ssa_sparse_attention_backward": (
+        _int,
+        [_vp, _vp, _vp, _int, _i64, _i64, _int, _int, _int, _i64, _i64, _i64, _i64, _i64, _i64,
+         _i64, _i64, _i64, _vp, _int, _int, _i64, _i64, _i64, _flt, _int, _vp, _vp, _int, _i64,
+         _i64, _i64, _vp, _int, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp]),
 }
 
 _lib = None

@@ -15,6 +15,35 @@ import torch.nn.functional as F
 from . import _lib, kernels
 
 
+class _SparseAttention(torch.autograd.Function):
+    """Stage (d) with its HIP backward (ssa_sparse_attention_backward): gradients
+    flow to q, k and v as through the reference's gather/softmax/einsum
+    (ssa/attention.py:64-113); the indices get none, as in the reference."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, indices, scale, causal, row_order, flag):
+        # The backward's D = dO . o uses an fp32 copy of the output: a bf16 one
+        # would carry its 2^-9 rounding into every gradient.
+        out32 = torch.empty(q.shape, device=q.device, dtype=torch.float32)
+        kernels.sparse_attention(q, k, v, indices, scale, causal, out=out32, error_flag=flag,
+                                 row_order=row_order)
+        ctx.scale, ctx.causal = scale, causal
+        ctx.has_order = row_order is not None
+        saved = [q, k, v, indices, out32] + ([row_order] if row_order is not None else [])
+        ctx.save_for_backward(*saved)
+        return out32 if q.dtype == torch.float32 else out32.to(q.dtype)
+
+    @staticmethod
+    def backward(ctx, dout):
+        q, k, v, indices, out, *rest = ctx.saved_tensors
+        order = rest[0] if ctx.has_order else None
+        if dout.stride(-1) != 1:
+            dout = dout.contiguous()
+        dq, dk, dv = kernels.sparse_attention_backward(q, k, v, indices, out, dout, ctx.scale,
+                                                       ctx.causal, row_order=order)
+        return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), None, None, None, None, None
+
+
 def sparse_exact_attention(
     q: torch.Tensor,
     k: torch.Tensor,
@@ -40,6 +69,8 @@ def sparse_exact_attention(
     ``row_order`` (int32 [B, h_kv, n], e.g. ``CodebookRouter.route(...,
     with_order=True).order``) sets the order rows are processed in, for cache
     locality; it does not change the result.
+
+    Differentiable in q, k and v (HIP backward kernel); not in ``indices``.
     """
     unbatched = q.dim() == 3
     if unbatched:
@@ -59,8 +90,11 @@ def sparse_exact_attention(
     flag = torch.zeros(1, device=q.device, dtype=torch.int32) if check_indices else None
     if row_order is not None and unbatched and row_order.dim() == 2:
         row_order = row_order.unsqueeze(0)
-    out = kernels.sparse_attention(q, k, v, indices, float(scale), causal, error_flag=flag,
-                                   row_order=row_order)
+    if torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad):
+        out = _SparseAttention.apply(q, k, v, indices, float(scale), bool(causal), row_order, flag)
+    else:
+        out = kernels.sparse_attention(q, k, v, indices, float(scale), causal, error_flag=flag,
+                                       row_order=row_order)
     if flag is not None and int(flag.item()) != 0:
         raise IndexError(f"sparse_exact_attention: an index is outside [0, {seq_len})")
     if out.dtype != out_dtype:

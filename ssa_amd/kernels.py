@@ -222,3 +222,42 @@ def sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, idx: tor
          ptr(row_order), ptr(out), _lib.elem_dtype(out), out.stride(0), out.stride(1), out.stride(2),
          ptr(error_flag), stream_of(q))
     return out
+
+
+def sparse_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, idx: torch.Tensor,
+                              out: torch.Tensor, dout: torch.Tensor,
+                              scale_div: Optional[float] = None, causal: bool = False,
+                              error_flag: Optional[torch.Tensor] = None,
+                              row_order: Optional[torch.Tensor] = None
+                              ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Gradients of stage (d) w.r.t. q, k, v (fp32, shapes of q, k, v), given the
+    forward output ``out`` and its gradient ``dout`` (the autograd backward of
+    ssa/attention.py:64-113)."""
+    for name, t in (("q", q), ("k", k), ("v", v), ("indices", idx), ("out", out), ("dout", dout)):
+        _check_rows(t, name)
+    _lib.require_device(q, k, v, idx, out, dout)
+    if not (q.dtype == k.dtype == v.dtype):
+        raise TypeError(f"q, k, v must share a dtype ({q.dtype}, {k.dtype}, {v.dtype})")
+    B, n, h_q, d = q.shape
+    h_kv = k.shape[2]
+    top_k = idx.shape[-1]
+    if tuple(out.shape) != (B, n, h_q, d) or tuple(dout.shape) != (B, n, h_q, d):
+        raise ValueError("out and dout must have q's shape")
+    if scale_div is None:
+        scale_div = math.sqrt(d)
+    dq = torch.zeros((B, n, h_q, d), device=q.device, dtype=torch.float32)
+    dk = torch.empty((B, n, h_kv, d), device=q.device, dtype=torch.float32)
+    dv = torch.empty((B, n, h_kv, d), device=q.device, dtype=torch.float32)
+    if row_order is not None:
+        _lib.require_device(row_order)
+        if row_order.dtype != torch.int32 or tuple(row_order.shape) != (B, h_kv, n):
+            raise ValueError(f"row_order must be int32 [{B}, {h_kv}, {n}]")
+        row_order = row_order.contiguous()
+    call("ssa_sparse_attention_backward", ptr(q), ptr(k), ptr(v), _lib.elem_dtype(q), B, n, h_q,
+         h_kv, d, q.stride(0), q.stride(1), q.stride(2), k.stride(0), k.stride(1), k.stride(2),
+         v.stride(0), v.stride(1), v.stride(2), ptr(idx), _lib.index_dtype(idx), top_k,
+         idx.stride(0), idx.stride(1), idx.stride(2), float(scale_div), int(bool(causal)),
+         ptr(row_order), ptr(out), _lib.elem_dtype(out), out.stride(0), out.stride(1),
+         out.stride(2), ptr(dout), _lib.elem_dtype(dout), dout.stride(0), dout.stride(1),
+         dout.stride(2), ptr(dq), ptr(dk), ptr(dv), ptr(error_flag), stream_of(q))
+    return dq, dk, dv
