@@ -51,6 +51,8 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline budget")
     p.add_argument("--copy-probe-gib", type=float, default=0.0,
                    help="also run one device copy of this size (PMC byte calibration)")
+    p.add_argument("--backward", action="store_true",
+                   help="also time the stage-(d) backward (dq, dk, dv) on the workload's indices")
     p.add_argument("--sweep", default="", help="comma list of n for a tokens/s vs n sweep")
     p.add_argument("--sweep-nc", default="scaled", choices=("scaled", "fixed"),
                    help="codebook size in the sweep: scaled with n (constant bucket size; the "
@@ -198,6 +200,42 @@ def stats_sums(q, k, router):
     heavy = st[..., 0] > router.top_k      # index order rescores only these rows
     C_r = int(st[..., 0][heavy].sum())
     return R, C, int(heavy.sum()), C_r, st[..., 0].numel(), (qc, kc, off, post, idx)
+
+
+def time_backward(cfg, q, k, v, inter, reps=3):
+    """Stage (d) backward (ssa_sparse_attention_backward) on the forward's indices
+    and query order, with an fp32 forward output and a seeded bf16 output
+    gradient; median of `reps` launches (HIP events on the launch stream)."""
+    import torch
+
+    from ssa_amd import kernels
+
+    qc, kc, off, post, _ = inter
+    order = kernels.query_order(qc, cfg["n_c"])
+    idx = kernels.select(q, k, qc, off, post, cfg["b"], cfg["k"], sorted=False,
+                         index_dtype=torch.int32, row_order=order)
+    out32 = torch.empty(q.shape, device=q.device, dtype=torch.float32)
+    kernels.sparse_attention(q, k, v, idx, None, True, out=out32, row_order=order)
+    gen = torch.Generator(device=q.device).manual_seed(7)
+    dout = torch.randn(q.shape, generator=gen, device=q.device).to(q.dtype)
+    ts = []
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        kernels.sparse_attention_backward(q, k, v, idx, out32, dout, None, True, row_order=order)
+        e1.record()
+        torch.cuda.synchronize()
+        ts.append(e0.elapsed_time(e1))
+    ms = sorted(ts)[len(ts) // 2]
+    B, n, h_q, h_kv, d, kk = cfg["B"], cfg["n"], cfg["h_q"], cfg["h_kv"], cfg["d"], cfg["k"]
+    s = 2 if cfg["dtype"] == "bf16" else 4
+    rows = B * n * h_kv
+    g = h_q // h_kv
+    # per row: K gathered twice (two passes) and V once, indices twice, q/dO
+    # (input type) and o (fp32) read, dq written, dk and dv read-modify-written
+    byt = rows * (3 * kk * d * s + 2 * kk * 4 + g * d * (2 * s + 4) + g * d * 4 + 2 * kk * d * 8)
+    return {"ms": ms, "tokens_per_s": B * n / (ms / 1000), "kernel": "sparse_attention_bwd_kernel",
+            "algorithmic_gb": byt / 1e9, "gbs": byt / (ms / 1000) / 1e9}
 
 
 def cpu_baseline(cfg, q, k, v, router, inter, budget_s):
@@ -377,6 +415,8 @@ def main():
                      "algorithmic_bytes": alg["d_bytes"]},
         "stages": stages,
     }
+    if args.backward:
+        line["backward"] = time_backward(cfg, q, k, v, inter)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(cfg, q, k, v, router, inter, args.cpu_seconds)
     if args.sweep:

@@ -296,6 +296,40 @@ __global__ __launch_bounds__(kRrThreads) void route_vectors_row_kernel(
 // per row.  The norm is then the canonical chain over the row's 32 means.
 constexpr int kRsRows = 64;
 
+// One 128-byte line of a row, raw (8 x 16 bytes); pieces past the row end are
+// not loaded.
+struct Line128 {
+  uint4 u[8];
+};
+template <typename T>
+__device__ __forceinline__ Line128 load_line(const T* p, int left) {
+  Line128 l;
+  const int np = min(128 / static_cast<int>(sizeof(T)), left) * static_cast<int>(sizeof(T)) / 16;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) l.u[k] = k < np ? reinterpret_cast<const uint4*>(p)[k] : make_uint4(0u, 0u, 0u, 0u);
+  return l;
+}
+// 8-element piece pi of a line: bf16 elements 8 pi .. 8 pi + 7 (one uint4), or
+// fp32 elements 8 pi .. 8 pi + 7 (two uint4).
+template <typename T>
+__device__ __forceinline__ Piece8 line_piece(const Line128& l, int pi) {
+  Piece8 r;
+  if constexpr (sizeof(T) == 2) {
+    const uint32_t w[4] = {l.u[pi].x, l.u[pi].y, l.u[pi].z, l.u[pi].w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      r.v[2 * e] = __uint_as_float(w[e] << 16);
+      r.v[2 * e + 1] = __uint_as_float(w[e] & 0xFFFF0000u);
+    }
+  } else {
+    const uint4 a = l.u[2 * pi], b = l.u[2 * pi + 1];
+    const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r.v[e] = __uint_as_float(w[e]);
+  }
+  return r;
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void route_vectors_split_kernel(
     const T* __restrict__ x, int64_t n, int h_in, int group, int d, int64_t sb, int64_t sn,
@@ -313,7 +347,6 @@ __global__ __launch_bounds__(256) void route_vectors_split_kernel(
   const int64_t ic = (i0 + lane < n) ? i0 + lane : n - 1;  // rows past n: row n-1, not stored
   const T* xr = x + b * sb + static_cast<int64_t>(h) * group * sh + ic * sn;
   const int cr = threadIdx.x >> 2, cs0 = 8 * (threadIdx.x & 3);
-  const int pieces = d / 8;
   float sum[8];
 #pragma unroll
   for (int k = 0; k < 8; ++k) sum[k] = 0.0f;
@@ -323,17 +356,29 @@ __global__ __launch_bounds__(256) void route_vectors_split_kernel(
       float acc[d_s];
 #pragma unroll
       for (int s = 0; s < d_s; ++s) acc[s] = 0.0f;
+      // The lane reads its head row a whole 128-byte line at a time, one line
+      // ahead of the one being multiplied: every line is fetched once (16-byte
+      // pieces spread over time re-fetched lines evicted in between).
       const T* xh = xr + static_cast<int64_t>(gg) * sh;
-      Piece8 cur = load8(xh);
+      constexpr int CE = 128 / sizeof(T);  // elements per line
+      const int nlines = (d + CE - 1) / CE;
+      Line128 cur = load_line(xh, d), nxt{};
 #pragma unroll 1
-      for (int c = 0; c < pieces; ++c) {
-        const Piece8 nxt = load8(xh + (c + 1 < pieces ? c + 1 : c) * 8);
-        const float* wc = w + c * 8;
+      for (int c = 0; c < nlines; ++c) {
+        if (c + 1 < nlines) nxt = load_line(xh + (c + 1) * CE, d - (c + 1) * CE);
+        const int np = min(CE, d - c * CE) / 8;  // pieces of this line inside the row
 #pragma unroll
-        for (int s = 0; s < d_s; ++s) {
-          const float* ws = wc + static_cast<int64_t>(s) * d;
+        for (int pi = 0; pi < CE / 8; ++pi) {
+          if (pi < np) {  // uniform
+            const Piece8 pc = line_piece<T>(cur, pi);
+            const float* wc = w + c * CE + pi * 8;
 #pragma unroll
-          for (int e = 0; e < 8; ++e) acc[s] = fma_rn(cur.v[e], ws[e], acc[s]);
+            for (int s = 0; s < d_s; ++s) {
+              const float* ws = wc + static_cast<int64_t>(s) * d;
+#pragma unroll
+              for (int e = 0; e < 8; ++e) acc[s] = fma_rn(pc.v[e], ws[e], acc[s]);
+            }
+          }
         }
         cur = nxt;
       }
