@@ -459,27 +459,11 @@ __global__ __launch_bounds__(kAttThreads, (AttMinBlocks<T, D, GMAX>::value)) voi
 //                  and tile.
 // Dropped slots (causal, past top_k, out of range) load zeros, so 0 * inf
 // never reaches the sums.
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef short v4i16_t __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) v4i16_t* lds_v4i16_ptr;
 // Waves per block and blocks per CU of the matrix-core kernel.  Each wave keeps
 // one chunk (16 KB at d = 128) of K and V in flight in its LDS slices, so the
 // bytes in flight per CU are LDS-bound.
 constexpr int kMfWaves = 4;
 constexpr int kMfMinBlocks = 2;
-
-__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
-  const bf16x2_t v = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
-  return __builtin_bit_cast(uint32_t, v);
-}
-// lane p of each 16-lane row reads lane p - 8 (lanes p < 8 read 0)
-__device__ __forceinline__ uint32_t dpp_from_minus8(uint32_t x) {
-  return __builtin_amdgcn_update_dpp(0u, x, 0x118, 0xF, 0xF, false);
-}
-// lane p of each 16-lane row reads lane p + 8 (lanes p >= 8 read 0)
-__device__ __forceinline__ float dpp_from_plus8(float x) {
-  return __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(x), 0x108, 0xF, 0xF, false));
-}
 
 // Issue one chunk's K and V loads: load r moves chunk rows KPI*r .. KPI*r +
 // KPI - 1 into LDS at base + r KB, lane l fetching the segment of row KPI*r +

@@ -19,6 +19,7 @@
 // g-head sums for dk[idx_t] and dv[idx_t] with fp32 atomics (many rows select
 // the same key).  All arithmetic is fp32; dq, dk and dv are fp32 buffers.
 #include "ssa_common.h"
+#include "ssa_rows.h"
 
 namespace ssa {
 namespace {
@@ -39,7 +40,8 @@ struct BwdParams {
   const void* idx;
   int idx_i64, top_k;
   int64_t idx_sb, idx_sn, idx_sh;
-  float inv_scale;  // 1 / scale_div
+  float inv_scale;      // 1 / scale_div
+  float qk_scale_log2;  // log2(e) / scale_div
   int causal;
   float* dq;  // [B][n][h_q][d]
   float* dk;  // [B][n][h_kv][d]
@@ -208,6 +210,296 @@ __global__ __launch_bounds__(64 * kBwdWaves) void sparse_attention_bwd_kernel(Bw
   }
 }
 
+// ---------------------------------------------------------------------------
+// Matrix-core backward (bf16 q/k/v/dO, d = 64 or 128, g <= 8).  One wave per
+// (batch, kv head, query) row, 32-key chunks gathered whole into the wave's LDS
+// as in the forward kernel (buffer loads straight to LDS, XOR-swizzled rows):
+//   pass 1   S^T = K Q^T (MFMA) per chunk, running max and sum of exp2 per head;
+//   pass 2   S^T again and dP^T = V dO^T (MFMA, same layout: lane (q4, c16) holds
+//            keys 16t + 4 q4 + e of head c16), p = exp2(s - m) / l,
+//            ds = p (dP - D);
+//            dQ^T += K^T dS^T like the forward's O^T += V^T P^T (A = K^T from
+//            transposing LDS reads, B = dS split into bf16 hi (rows < g) and lo
+//            (rows 8 + r));
+//            dV_chunk = P^T dO and dK_chunk = dS^T Q: P and dS go through LDS to
+//            [key][head], A = [hi | lo] over heads (k = 0..7 hi, 8..15 lo), B =
+//            dO / Q rows by head (stored transposed in LDS once per row), and the
+//            16 x 16 result tiles go to dv / dk with fp32 atomics.
+// The hi/lo splits keep about 16 mantissa bits of p and ds; q, k, v and dO are
+// exact in bf16.
+constexpr int kBwMfWaves = 2;
+
+template <int D>
+__global__ __launch_bounds__(64 * kBwMfWaves, 2) void sparse_attention_bwd_mfma_kernel(BwdParams p) {
+  using S = MfShape<D>;
+  constexpr int KB = S::KB, NT = S::NT;
+  __shared__ __align__(16) unsigned char kv_lds[kBwMfWaves][2][kMfChunk * S::ROW];
+  __shared__ __align__(16) float tr_lds[kBwMfWaves][kMfChunk][16];      // P or dS as [key][head]
+  __shared__ __align__(16) uint16_t hd_lds[kBwMfWaves][2][D][8];        // Q, dO as [dim][head] (bf16)
+
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int q4 = lane >> 4, c16 = lane & 15;
+  const int64_t lrow = static_cast<int64_t>(blockIdx.x) * kBwMfWaves + wave;
+  if (lrow >= p.rows) return;  // wave-uniform; the kernel has no block barrier
+  const int64_t bh = lrow / p.n;
+  int64_t i = lrow - bh * p.n;
+  if (p.order) {
+    const int64_t oi = p.order[lrow];
+    if (oi < 0 || oi >= p.n) {
+      if (lane == 0 && p.err) p.err[0] = 1;
+      return;
+    }
+    i = oi;
+  }
+  const int h = static_cast<int>(bh % p.h_kv);
+  const int64_t bb = bh / p.h_kv;
+  const int g = p.g;
+  const bool col_ok = c16 < g;
+
+  // q and dO fragments (B operands of S^T and dP^T): head c16, dims kb*32 + q4*8 + 0..7
+  const int hq = h * g + (col_ok ? c16 : 0);
+  const uint16_t* qh = static_cast<const uint16_t*>(p.q) + bb * p.q_sb + i * p.q_sn + static_cast<int64_t>(hq) * p.q_sh;
+  const uint16_t* dh = static_cast<const uint16_t*>(p.dout) + bb * p.do_sb + i * p.do_sn + static_cast<int64_t>(hq) * p.do_sh;
+  bf16x8_t qf[KB], df[KB];
+  float dpart = 0.0f;  // this lane's share of D = dO . o for head c16
+#pragma unroll
+  for (int kb = 0; kb < KB; ++kb) {
+    qf[kb] = col_ok ? *reinterpret_cast<const bf16x8_t*>(qh + kb * 32 + q4 * 8) : bf16x8_t{};
+    df[kb] = col_ok ? *reinterpret_cast<const bf16x8_t*>(dh + kb * 32 + q4 * 8) : bf16x8_t{};
+    const uint4 qu = __builtin_bit_cast(uint4, qf[kb]), du = __builtin_bit_cast(uint4, df[kb]);
+    const uint32_t qw[4] = {qu.x, qu.y, qu.z, qu.w}, dw[4] = {du.x, du.y, du.z, du.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int dim = kb * 32 + q4 * 8 + e;
+      const uint16_t qv = static_cast<uint16_t>((e & 1) ? (qw[e >> 1] >> 16) : (qw[e >> 1] & 0xFFFFu));
+      const uint16_t dv = static_cast<uint16_t>((e & 1) ? (dw[e >> 1] >> 16) : (dw[e >> 1] & 0xFFFFu));
+      if (col_ok) dpart = fma_rn(bf16_bits_to_f32(dv), ld_any(p.o, bb * p.o_sb + i * p.o_sn + static_cast<int64_t>(hq) * p.o_sh + dim, p.o_bf16), dpart);
+      if (c16 < 8) {  // head slots 0..7 of the [dim][head] copies (zero past g)
+        hd_lds[wave][0][dim][c16] = col_ok ? qv : static_cast<uint16_t>(0);
+        hd_lds[wave][1][dim][c16] = col_ok ? dv : static_cast<uint16_t>(0);
+      }
+    }
+  }
+  dpart += __shfl_xor(dpart, 16);
+  dpart += __shfl_xor(dpart, 32);
+  const float dcol = dpart;  // D of head c16 (lanes of column c16)
+
+  const uint16_t* kbase = static_cast<const uint16_t*>(p.k) + bb * p.k_sb + static_cast<int64_t>(h) * p.k_sh;
+  const uint16_t* vbase = static_cast<const uint16_t*>(p.v) + bb * p.v_sb + static_cast<int64_t>(h) * p.v_sh;
+  const unsigned char* ib = static_cast<const unsigned char*>(p.idx) +
+                            (bb * p.idx_sb + i * p.idx_sn + h * p.idx_sh) * (p.idx_i64 ? 8 : 4);
+  unsigned char* kl = kv_lds[wave][0];
+  unsigned char* vl = kv_lds[wave][1];
+  const uint32_t ksn2 = 2u * static_cast<uint32_t>(p.k_sn), vsn2 = 2u * static_cast<uint32_t>(p.v_sn);
+  const int kbytes = static_cast<int>((p.n - 1) * p.k_sn * 2 + 2 * D);
+  const int vbytes = static_cast<int>((p.n - 1) * p.v_sn * 2 + 2 * D);
+  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(kbase), 0, kbytes, kBufferWord3);
+  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(vbase), 0, vbytes, kBufferWord3);
+  uint32_t seg16[S::SWZ_PERIOD];
+  row_seg16<D>(lane, seg16);
+  const int kswz = mf_swz<D>(c16);
+  // key of chunk slot `lane` (lanes < 32), -1 past top_k, -2 out of range (flagged)
+  auto load_idx = [&](int ch) -> int {
+    const int slot = ch * kMfChunk + lane;
+    if (lane >= kMfChunk || slot >= p.top_k) return -1;
+    const int64_t j = p.idx_i64 ? reinterpret_cast<const int64_t*>(ib)[slot]
+                                : static_cast<int64_t>(reinterpret_cast<const int32_t*>(ib)[slot]);
+    if (j < 0 || j >= p.n) {
+      if (p.err) p.err[0] = 1;
+      return -2;
+    }
+    return static_cast<int>(j);
+  };
+  auto chunk_ok = [&](int j) { return j >= 0 && !(p.causal && j > i); };
+  auto read_k = [&](const unsigned char* l, bf16x8_t (&f)[2][KB]) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb)
+        f[t][kb] = *(lds_bf16x8_ptr)(l + (16 * t + c16) * S::ROW + (((kb * 4 + q4) ^ kswz) << 4));
+  };
+  // valid bit of the lane's score x = 4t + e (key slot 16t + 4 q4 + e)
+  auto valid = [&](uint64_t okb, int x) { return ((okb >> (4 * q4 + 16 * (x >> 2) + (x & 3))) & 1ull) != 0; };
+  const int nchunks = (p.top_k + kMfChunk - 1) / kMfChunk;
+
+  // ---- pass 1: running max (log2 domain) and sum per head over the row's slots
+  float m_run = -INFINITY, l_run = 0.0f;
+  {
+    int jn = nchunks > 0 ? load_idx(0) : -1;
+    uint64_t okn = __ballot(chunk_ok(jn));
+    if (nchunks > 0) row_issue<D>(krs, kl, chunk_ok(jn) ? jn : -1, lane, ksn2, seg16);
+    jn = nchunks > 1 ? load_idx(1) : -1;
+    for (int ch = 0; ch < nchunks; ++ch) {
+      __builtin_amdgcn_s_waitcnt(kWaitVm0);
+      bf16x8_t kf[2][KB];
+      read_k(kl, kf);
+      __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+      const uint64_t okb = okn;
+      if (ch + 1 < nchunks) {
+        okn = __ballot(chunk_ok(jn));
+        row_issue<D>(krs, kl, chunk_ok(jn) ? jn : -1, lane, ksn2, seg16);
+        jn = ch + 2 < nchunks ? load_idx(ch + 2) : -1;
+      }
+      float sc[8];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        floatx4_t sv = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) sv = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[t][kb], qf[kb], sv, 0, 0, 0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sc[4 * t + e] = valid(okb, 4 * t + e) ? sv[e] * p.qk_scale_log2 : -INFINITY;
+      }
+      float mx = sc[0];
+#pragma unroll
+      for (int x = 1; x < 8; ++x) mx = fmaxf(mx, sc[x]);
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float mnew = fmaxf(m_run, mx);
+      const float mref = (mnew == -INFINITY) ? 0.0f : mnew;
+      float ps = 0.0f;
+#pragma unroll
+      for (int x = 0; x < 8; ++x) ps += exp2f(sc[x] - mref);
+      l_run = l_run * exp2f(m_run - mref) + ps;
+      m_run = mnew;
+    }
+  }
+  float l_tot = l_run + __shfl_xor(l_run, 16);
+  l_tot += __shfl_xor(l_tot, 32);
+  const float inv_l = (l_tot > 0.0f && col_ok) ? 1.0f / l_tot : 0.0f;  // 0: no slot, or an unused column
+  const float mref = (m_run == -INFINITY) ? 0.0f : m_run;
+
+  // ---- pass 2
+  const bool hi_row = c16 < g;
+  const bool lo_row = c16 >= 8 && c16 < 8 + g;
+  floatx4_t dqacc[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) dqacc[t] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+  float* dkb = p.dk + (bb * p.n * p.h_kv + h) * p.d;
+  float* dvb = p.dv + (bb * p.n * p.h_kv + h) * p.d;
+  const int64_t krow = static_cast<int64_t>(p.h_kv) * p.d;
+  float* tr = &tr_lds[wave][0][0];
+  // A operand over heads from the [key][head] copy: k = 0..7 bf16 hi of heads
+  // 0..7 (lanes q4 = 0), 8..15 their lo (q4 = 1), 16..31 zero
+  auto heads_operand = [&](int t) -> bf16x8_t {
+    if (q4 >= 2) return bf16x8_t{};
+    const float4 a = *reinterpret_cast<const float4*>(tr + (16 * t + c16) * 16);
+    const float4 b = *reinterpret_cast<const float4*>(tr + (16 * t + c16) * 16 + 4);
+    const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    uint32_t w[4];
+#pragma unroll
+    for (int x = 0; x < 4; ++x) {
+      const uint32_t hi = pack_bf16x2(v[2 * x], v[2 * x + 1]);
+      const uint32_t lo = pack_bf16x2(v[2 * x] - __uint_as_float(hi << 16), v[2 * x + 1] - __uint_as_float(hi & 0xFFFF0000u));
+      w[x] = q4 == 0 ? hi : lo;
+    }
+    return __builtin_bit_cast(bf16x8_t, make_uint4(w[0], w[1], w[2], w[3]));
+  };
+  // B operand by head from the [dim][head] copy of Q (which = 0) or dO (1):
+  // k = 8 q4 + e holds head e for q4 < 2 (hi and lo rows of A meet the same
+  // head row), zero for q4 >= 2; column c16 = dim 16 dt + c16
+  auto head_rows = [&](int which, int dt) -> bf16x8_t {
+    if (q4 >= 2) return bf16x8_t{};
+    return *reinterpret_cast<const bf16x8_t*>(&hd_lds[wave][which][16 * dt + c16][0]);
+  };
+  int jc = nchunks > 0 ? load_idx(0) : -1;
+  uint64_t okn = __ballot(chunk_ok(jc));
+  if (nchunks > 0) {
+    row_issue<D>(krs, kl, chunk_ok(jc) ? jc : -1, lane, ksn2, seg16);
+    row_issue<D>(vrs, vl, chunk_ok(jc) ? jc : -1, lane, vsn2, seg16);
+  }
+  int jn = nchunks > 1 ? load_idx(1) : -1;
+  for (int ch = 0; ch < nchunks; ++ch) {
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);
+    bf16x8_t kf[2][KB], vf[2][KB], kt[NT];
+    read_k(kl, kf);
+    read_k(vl, vf);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) kt[t] = rows_transposed<D>(kl, t, q4, c16);
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+    const uint64_t okb = okn;
+    const int jcur = jc;
+    if (ch + 1 < nchunks) {
+      okn = __ballot(chunk_ok(jn));
+      row_issue<D>(krs, kl, chunk_ok(jn) ? jn : -1, lane, ksn2, seg16);
+      row_issue<D>(vrs, vl, chunk_ok(jn) ? jn : -1, lane, vsn2, seg16);
+      jc = jn;
+      jn = ch + 2 < nchunks ? load_idx(ch + 2) : -1;
+    }
+    float pr[8], ds[8];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      floatx4_t sv = {0.f, 0.f, 0.f, 0.f}, dv = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        sv = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[t][kb], qf[kb], sv, 0, 0, 0);
+        dv = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[t][kb], df[kb], dv, 0, 0, 0);
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int x = 4 * t + e;
+        pr[x] = valid(okb, x) ? exp2f(sv[e] * p.qk_scale_log2 - mref) * inv_l : 0.0f;
+        ds[x] = pr[x] * (dv[e] - dcol);
+      }
+    }
+    // dQ^T += K^T dS^T (B: rows c16 < g dS_hi of head c16, rows 8 + r dS_lo of head r)
+    uint32_t db[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const uint32_t hi = pack_bf16x2(ds[2 * w], ds[2 * w + 1]);
+      const uint32_t lo = pack_bf16x2(ds[2 * w] - __uint_as_float(hi << 16), ds[2 * w + 1] - __uint_as_float(hi & 0xFFFF0000u));
+      const uint32_t lo_in = dpp_from_minus8(lo);
+      db[w] = hi_row ? hi : (lo_row ? lo_in : 0u);
+    }
+    const bf16x8_t dsb = __builtin_bit_cast(bf16x8_t, make_uint4(db[0], db[1], db[2], db[3]));
+#pragma unroll
+    for (int t = 0; t < NT; ++t) dqacc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kt[t], dsb, dqacc[t], 0, 0, 0);
+
+    // dV and dK tiles; P then dS pass through tr as [key][head]
+#pragma unroll
+    for (int pass = 0; pass < 2; ++pass) {
+      const float* src = pass == 0 ? pr : ds;
+#pragma unroll
+      for (int x = 0; x < 8; ++x) tr[(16 * (x >> 2) + 4 * q4 + (x & 3)) * 16 + c16] = src[x];
+      __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+      __builtin_amdgcn_wave_barrier();
+      const bf16x8_t a0 = heads_operand(0), a1 = heads_operand(1);
+      __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+      __builtin_amdgcn_wave_barrier();  // tr is rewritten by the next pass
+      float* dst = pass == 0 ? dvb : dkb;
+      const float mul = pass == 0 ? 1.0f : p.inv_scale;
+      const int which = pass == 0 ? 1 : 0;  // P^T dO, then dS^T Q
+#pragma unroll
+      for (int dt = 0; dt < NT; ++dt) {
+        const bf16x8_t bop = head_rows(which, dt);
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const floatx4_t c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(t == 0 ? a0 : a1, bop, floatx4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int slot = 16 * t + 4 * q4 + e;
+            const int j = __shfl(jcur, slot);
+            if ((okb >> slot) & 1ull) unsafeAtomicAdd(dst + j * krow + 16 * dt + c16, c[e] * mul);
+          }
+        }
+      }
+    }
+  }
+
+  // dQ: hi row + lo row, / scale; lanes c16 < g hold dims 16t + 4 q4 + e of head c16
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) dqacc[t][e] += dpp_from_plus8(dqacc[t][e]);
+  if (!hi_row) return;
+  float* dqb = p.dq + ((bb * p.n + i) * p.h_q + h * g + c16) * p.d + 4 * q4;
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+    *reinterpret_cast<float4*>(dqb + 16 * t) =
+        make_float4(dqacc[t][0] * p.inv_scale, dqacc[t][1] * p.inv_scale, dqacc[t][2] * p.inv_scale,
+                    dqacc[t][3] * p.inv_scale);
+}
+
 template <typename T, int GMAX>
 int launch_bwd_g(const BwdParams& p, hipStream_t st) {
   const dim3 grid(static_cast<unsigned>(ceil_div(p.rows, kBwdWaves)));
@@ -221,8 +513,32 @@ int launch_bwd_g(const BwdParams& p, hipStream_t st) {
   return check_launch("sparse_attention_bwd_kernel");
 }
 
+// The matrix-core kernel: bf16 inputs and output gradient, d = 64 or 128,
+// g <= 8, q and dO rows 16-byte aligned, and K/V rows addressable by 32-bit
+// buffer offsets (rows below 2^31 bytes, n and byte strides below 2^24).
+bool bwd_mfma_ok(const BwdParams& p, const void* q, const void* dout) {
+  const auto fits = [&](int64_t sn) {
+    return sn >= 0 && 2 * sn < (int64_t(1) << 24) && (p.n - 1) * sn * 2 + 2 * p.d < (int64_t(1) << 31);
+  };
+  const bool aligned = (p.q_sb % 8 == 0) && (p.q_sn % 8 == 0) && (p.q_sh % 8 == 0) &&
+                       (p.do_sb % 8 == 0) && (p.do_sn % 8 == 0) && (p.do_sh % 8 == 0) &&
+                       (reinterpret_cast<uintptr_t>(q) % 16 == 0) && (reinterpret_cast<uintptr_t>(dout) % 16 == 0);
+  return p.do_bf16 && (p.d == 64 || p.d == 128) && p.g <= 8 && aligned && p.n < (int64_t(1) << 24) &&
+         fits(p.k_sn) && fits(p.v_sn);
+}
+
 template <typename T>
 int launch_bwd(const BwdParams& p, hipStream_t st) {
+  if constexpr (sizeof(T) == 2) {
+    if (bwd_mfma_ok(p, p.q, p.dout)) {
+      const dim3 grid(static_cast<unsigned>(ceil_div(p.rows, kBwMfWaves)));
+      if (p.d == 64)
+        sparse_attention_bwd_mfma_kernel<64><<<grid, 64 * kBwMfWaves, 0, st>>>(p);
+      else
+        sparse_attention_bwd_mfma_kernel<128><<<grid, 64 * kBwMfWaves, 0, st>>>(p);
+      return check_launch("sparse_attention_bwd_mfma_kernel");
+    }
+  }
   if (p.g <= 4) return launch_bwd_g<T, 4>(p, st);
   if (p.g <= 8) return launch_bwd_g<T, 8>(p, st);
   return launch_bwd_g<T, 16>(p, st);
@@ -274,6 +590,7 @@ extern "C" int ssa_sparse_attention_backward(
   p.idx = idx; p.idx_i64 = idx_dtype == SSA_INDEX_I64; p.top_k = top_k;
   p.idx_sb = idx_sb; p.idx_sn = idx_sn; p.idx_sh = idx_sh;
   p.inv_scale = 1.0f / scale_div;
+  p.qk_scale_log2 = static_cast<float>(1.4426950408889634 / static_cast<double>(scale_div));
   p.causal = causal ? 1 : 0;
   p.dq = dq; p.dk = dk; p.dv = dv;
   p.err = error_flag;

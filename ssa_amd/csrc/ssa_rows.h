@@ -78,6 +78,39 @@ __device__ __forceinline__ void row_issue(__amdgpu_buffer_rsrc_t rs, unsigned ch
   }
 }
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16_t* lds_v4i16_ptr;
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  const bf16x2_t v = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
+  return __builtin_bit_cast(uint32_t, v);
+}
+// lane p of each 16-lane row reads lane p - 8 (lanes p < 8 read 0)
+__device__ __forceinline__ uint32_t dpp_from_minus8(uint32_t x) {
+  return __builtin_amdgcn_update_dpp(0u, x, 0x118, 0xF, 0xF, false);
+}
+// lane p of each 16-lane row reads lane p + 8 (lanes p >= 8 read 0)
+__device__ __forceinline__ float dpp_from_plus8(float x) {
+  return __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(x), 0x108, 0xF, 0xF, false));
+}
+
+// V^T (or K^T) fragment of 16-feature tile t from a chunk's rows in LDS at `l`
+// (the A operand of O^T += V^T P^T): within each 16-lane group, lane p receives
+// element p mod 4 from the rows addressed by lanes p / 4 + 4e, which matches
+// the key order of a P^T operand built from the S^T layout (lane (q4, c16):
+// keys 16t' + 4 q4 + e).
+template <int D>
+__device__ __forceinline__ bf16x8_t rows_transposed(const unsigned char* l, int t, int q4, int c16) {
+  using S = MfShape<D>;
+  const int vkey = 4 * q4 + (c16 >> 2);
+  const int off = vkey * S::ROW + (((2 * t + ((c16 & 3) >> 1)) ^ mf_swz<D>(vkey)) << 4) + (c16 & 1) * 8;
+  const v4i16_t a0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_ptr)(l + off));
+  const v4i16_t a1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_ptr)(l + off + 16 * S::ROW));
+  return __builtin_bit_cast(bf16x8_t, make_uint4(__builtin_bit_cast(uint2, a0).x, __builtin_bit_cast(uint2, a0).y,
+                                                 __builtin_bit_cast(uint2, a1).x, __builtin_bit_cast(uint2, a1).y));
+}
+
 // s_waitcnt encodings (gfx9): vmcnt(0) alone, lgkmcnt(0) alone; vmcnt(N) for
 // N < 16 is kWaitVmBase | N.
 constexpr int kWaitVm0 = 0x0F70;
