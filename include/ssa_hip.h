@@ -160,6 +160,22 @@ int ssa_select(const void* q, const void* k, int dtype, int64_t batch, int64_t n
                const int32_t* row_order, void* out, int out_index_dtype, int32_t* stats,
                void* workspace, size_t workspace_bytes, void* stream);
 
+/* ssa_select for a block of n_q query rows at key positions q_pos0 .. q_pos0 +
+ * n_q - 1 against all n keys (0 <= q_pos0, q_pos0 + n_q <= n): q, q_codes,
+ * out, stats and row_order hold n_q rows ([batch][n_q]..., [batch][h_kv][n_q]...);
+ * the causal window and the dense mask use the key position.  n_q = n with
+ * q_pos0 = 0 is ssa_select.  No reference counterpart: it serves incremental
+ * decoding (new tokens against a key cache, ssa_design.md:225-234) and chunked
+ * prefill.  Workspace: ssa_select_workspace_bytes(batch, n_q, h_kv, top_k). */
+int ssa_select_block(const void* q, const void* k, int dtype, int64_t batch, int64_t n,
+                     int64_t n_q, int64_t q_pos0, int h_q, int h_kv, int d, int64_t q_sb,
+                     int64_t q_sn, int64_t q_sh, int64_t k_sb, int64_t k_sn, int64_t k_sh,
+                     const int32_t* q_codes, int a, const int32_t* offsets,
+                     const int32_t* postings, int n_c, int b, int top_k, int mask_mode,
+                     const uint8_t* mask, int64_t mask_sb, int64_t mask_si, float score_div,
+                     int sorted, const int32_t* row_order, void* out, int out_index_dtype,
+                     int32_t* stats, void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---- stage (d): gathered exact attention -------------------------------- */
 
 /* out[b][i][hq] = softmax_m(q[b][i][hq] . k[b][idx[b][i][h][m]][h] / scale_div) . v[...]
@@ -183,6 +199,19 @@ int ssa_sparse_attention(const void* q, const void* k, const void* v, int dtype,
                          int causal, const int32_t* row_order, void* out, int out_dtype,
                          int64_t o_sb, int64_t o_sn,
                          int64_t o_sh, int32_t* error_flag, void* stream);
+
+/* ssa_sparse_attention for a block of n_q query rows at key positions q_pos0
+ * .. q_pos0 + n_q - 1 (0 <= q_pos0, q_pos0 + n_q <= n): q, idx, out and
+ * row_order hold n_q rows; `causal` compares indices with the key position.
+ * n_q = n with q_pos0 = 0 is ssa_sparse_attention.  No reference counterpart:
+ * it serves incremental decoding and chunked prefill. */
+int ssa_sparse_attention_block(
+    const void* q, const void* k, const void* v, int dtype, int64_t batch, int64_t n, int64_t n_q,
+    int64_t q_pos0, int h_q, int h_kv, int d, int64_t q_sb, int64_t q_sn, int64_t q_sh, int64_t k_sb,
+    int64_t k_sn, int64_t k_sh, int64_t v_sb, int64_t v_sn, int64_t v_sh, const void* idx,
+    int idx_dtype, int top_k, int64_t idx_sb, int64_t idx_sn, int64_t idx_sh, float scale_div,
+    int causal, const int32_t* row_order, void* out, int out_dtype, int64_t o_sb, int64_t o_sn,
+    int64_t o_sh, int32_t* error_flag, void* stream);
 
 /* Gradients of ssa_sparse_attention with respect to q, k and v, given the
  * forward output `out` and the output gradient `dout`.  Replaces the autograd

@@ -64,11 +64,21 @@ SIGNATURES = {
          _vp, _int, _vp, _vp, _int, _int, _int, _int, _vp, _i64, _i64, _flt, _int, _vp, _vp,
          _int, _vp, _vp, _sz, _vp]),
     "ssa_select_workspace_bytes": (_sz, [_i64, _i64, _int, _int]),
+    "ssa_select_block": (
+        _int,
+        [_vp, _vp, _int, _i64, _i64, _i64, _i64, _int, _int, _int, _i64, _i64, _i64, _i64, _i64,
+         _i64, _vp, _int, _vp, _vp, _int, _int, _int, _int, _vp, _i64, _i64, _flt, _int, _vp, _vp,
+         _int, _vp, _vp, _sz, _vp]),
     "ssa_sparse_attention": (
         _int,
         [_vp, _vp, _vp, _int, _i64, _i64, _int, _int, _int, _i64, _i64, _i64, _i64, _i64, _i64,
          _i64, _i64, _i64, _vp, _int, _int, _i64, _i64, _i64, _flt, _int, _vp, _vp, _int, _i64,
          _i64, _i64, _vp, _vp]),
+    "ssa_sparse_attention_block": (
+        _int,
+        [_vp, _vp, _vp, _int, _i64, _i64, _i64, _i64, _int, _int, _int, _i64, _i64, _i64, _i64,
+         _i64, _i64, _i64, _i64, _i64, _vp, _int, _int, _i64, _i64, _i64, _flt, _int, _vp, _vp,
+         _int, _i64, _i64, _i64, _vp, _vp]),
     "ssa_sparse_attention_backward": (
         _int,
         [_vp, _vp, _vp, _int, _i64, _i64, _int, _int, _int, _i64, _i64, _i64, _i64, _i64, _i64,

@@ -53,32 +53,35 @@ struct AttParams {
   int64_t o_sb, o_sn, o_sh;
   int32_t* err;
   int64_t rows;
-  const int32_t* order;  // nullable [B*h_kv][n]: query index processed at each position
+  const int32_t* order;  // nullable [B*h_kv][n_q]: query row processed at each slot
+  int64_t n_q, q_pos0;   // query rows (q, idx, out) and the key position of row 0
 };
 
-// Row processed by wave slot `lrow` (in (b*h_kv + h)*n + position order): the query
-// index is the position itself, or order[lrow] when a processing order is given.
-// An order entry outside [0, n) drops the row and raises the error flag.
+// Row processed by wave slot `lrow` (in (b*h_kv + h)*n_q + slot order): the query
+// row r is the slot itself, or order[lrow] when a processing order is given; it
+// sits at key position i = q_pos0 + r (the causal cut).  An order entry outside
+// [0, n_q) drops the row and raises the error flag.
 struct AttRow {
-  int64_t i, bh;
+  int64_t r, i, bh;
   bool ok;
 };
 __device__ __forceinline__ AttRow att_row(const AttParams& p, int64_t lrow) {
   AttRow r;
   r.ok = lrow < p.rows;
   const int64_t l = r.ok ? lrow : 0;
-  r.bh = l / p.n;
-  r.i = l - r.bh * p.n;
+  r.bh = l / p.n_q;
+  r.r = l - r.bh * p.n_q;
   if (p.order) {
     const int64_t o = p.order[l];
-    if (o < 0 || o >= p.n) {
+    if (o < 0 || o >= p.n_q) {
       if (r.ok && p.err) p.err[0] = 1;
       r.ok = false;
-      r.i = 0;
+      r.r = 0;
     } else {
-      r.i = o;
+      r.r = o;
     }
   }
+  r.i = p.q_pos0 + r.r;
   return r;
 }
 
@@ -245,12 +248,13 @@ __global__ __launch_bounds__(kAttThreads, (AttMinBlocks<T, D, GMAX>::value)) voi
   const int c16 = lane & 15;
   const AttRow ar = att_row(p, static_cast<int64_t>(blockIdx.x) * kAttWaves + wave);
   const bool row_ok = ar.ok;
-  const int64_t i = ar.i;
+  const int64_t i = ar.i;  // key position (causal cut)
+  const int64_t qr = ar.r;  // query row (q, idx, out)
   const int64_t bh = ar.bh;
   const int h = static_cast<int>(bh % p.h_kv);
   const int64_t bb = bh / p.h_kv;
 
-  const T* qh = static_cast<const T*>(p.q) + bb * p.q_sb + i * p.q_sn +
+  const T* qh = static_cast<const T*>(p.q) + bb * p.q_sb + qr * p.q_sn +
                 static_cast<int64_t>(h * p.g + (c16 < p.g ? c16 : 0)) * p.q_sh;
   QkFrag<T, D> frag;
   frag.load_q(qh, row_ok && c16 < p.g, q4, p.d);
@@ -258,7 +262,7 @@ __global__ __launch_bounds__(kAttThreads, (AttMinBlocks<T, D, GMAX>::value)) voi
 
   const T* kbase = static_cast<const T*>(p.k) + bb * p.k_sb + static_cast<int64_t>(h) * p.k_sh;
   const T* vbase = static_cast<const T*>(p.v) + bb * p.v_sb + static_cast<int64_t>(h) * p.v_sh + c16 * DQ;
-  const int64_t ibase = bb * p.idx_sb + i * p.idx_sn + static_cast<int64_t>(h) * p.idx_sh;
+  const int64_t ibase = bb * p.idx_sb + qr * p.idx_sn + static_cast<int64_t>(h) * p.idx_sh;
 
   // Index of this lane's slot in chunk ch, range-checked on load: -1 = no slot,
   // -2 = outside [0, n) (reported through the error flag).
@@ -398,7 +402,7 @@ __global__ __launch_bounds__(kAttThreads, (AttMinBlocks<T, D, GMAX>::value)) voi
     if ((gg & 3) != q4 || gg >= p.g || vvalid <= 0) continue;
     const float ls = lsum_s[wave][gg];
     const float inv = ls > 0.0f ? 1.0f / ls : 0.0f;
-    const int64_t ob = bb * p.o_sb + i * p.o_sn + static_cast<int64_t>(h * p.g + gg) * p.o_sh + c16 * DQ;
+    const int64_t ob = bb * p.o_sb + qr * p.o_sn + static_cast<int64_t>(h * p.g + gg) * p.o_sh + c16 * DQ;
     if (p.out_bf16) {
       uint32_t packed[DQ / 2];
 #pragma unroll
@@ -504,12 +508,13 @@ __global__ __launch_bounds__(64 * kMfWaves, kMfMinBlocks) void sparse_attention_
   const int c16 = lane & 15;
   const AttRow ar = att_row(p, static_cast<int64_t>(blockIdx.x) * kMfWaves + wave);
   const bool row_ok = ar.ok;
-  const int64_t i = ar.i;
+  const int64_t i = ar.i;  // key position (causal cut)
+  const int64_t qr = ar.r;  // query row (q, idx, out)
   const int64_t bh = ar.bh;
   const int h = static_cast<int>(bh % p.h_kv);
   const int64_t bb = bh / p.h_kv;
 
-  const uint16_t* qh = static_cast<const uint16_t*>(p.q) + bb * p.q_sb + i * p.q_sn +
+  const uint16_t* qh = static_cast<const uint16_t*>(p.q) + bb * p.q_sb + qr * p.q_sn +
                        static_cast<int64_t>(h * p.g + (c16 < p.g ? c16 : 0)) * p.q_sh;
   bf16x8_t qf[S::KB];
 #pragma unroll
@@ -519,7 +524,7 @@ __global__ __launch_bounds__(64 * kMfWaves, kMfMinBlocks) void sparse_attention_
 
   const uint16_t* kbase = static_cast<const uint16_t*>(p.k) + bb * p.k_sb + static_cast<int64_t>(h) * p.k_sh;
   const uint16_t* vbase = static_cast<const uint16_t*>(p.v) + bb * p.v_sb + static_cast<int64_t>(h) * p.v_sh;
-  const int64_t ibase = bb * p.idx_sb + i * p.idx_sn + static_cast<int64_t>(h) * p.idx_sh;
+  const int64_t ibase = bb * p.idx_sb + qr * p.idx_sn + static_cast<int64_t>(h) * p.idx_sh;
   unsigned char* kl = kv_lds[wave][0];
   unsigned char* vl = kv_lds[wave][1];
 
@@ -689,7 +694,7 @@ __global__ __launch_bounds__(64 * kMfWaves, kMfMinBlocks) void sparse_attention_
     for (int e = 0; e < 4; ++e) oacc[t][e] += dpp_from_plus8(oacc[t][e]);
   if (!row_ok || !hi_row) return;
   const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
-  const int64_t ob = bb * p.o_sb + i * p.o_sn + static_cast<int64_t>(h * p.g + c16) * p.o_sh + 4 * q4;
+  const int64_t ob = bb * p.o_sb + qr * p.o_sn + static_cast<int64_t>(h * p.g + c16) * p.o_sh + 4 * q4;
   if (p.out_bf16) {
     uint16_t* dst = static_cast<uint16_t*>(p.out) + ob;
 #pragma unroll
@@ -741,16 +746,17 @@ int launch_att(const AttParams& p, int d, hipStream_t st) {
 
 using namespace ssa;
 
-extern "C" int ssa_sparse_attention(const void* q, const void* k, const void* v, int dtype,
-                                    int64_t batch, int64_t n, int h_q, int h_kv, int d,
-                                    int64_t q_sb, int64_t q_sn, int64_t q_sh, int64_t k_sb,
-                                    int64_t k_sn, int64_t k_sh, int64_t v_sb, int64_t v_sn,
-                                    int64_t v_sh, const void* idx, int idx_dtype, int top_k,
-                                    int64_t idx_sb, int64_t idx_sn, int64_t idx_sh,
-                                    float scale_div, int causal, const int32_t* row_order,
-                                    void* out, int out_dtype,
-                                    int64_t o_sb, int64_t o_sn, int64_t o_sh, int32_t* error_flag,
-                                    void* stream) {
+extern "C" int ssa_sparse_attention_block(
+    const void* q, const void* k, const void* v, int dtype, int64_t batch, int64_t n, int64_t n_q,
+    int64_t q_pos0, int h_q, int h_kv, int d, int64_t q_sb, int64_t q_sn, int64_t q_sh, int64_t k_sb,
+    int64_t k_sn, int64_t k_sh, int64_t v_sb, int64_t v_sn, int64_t v_sh, const void* idx,
+    int idx_dtype, int top_k, int64_t idx_sb, int64_t idx_sn, int64_t idx_sh, float scale_div,
+    int causal, const int32_t* row_order, void* out, int out_dtype, int64_t o_sb, int64_t o_sn,
+    int64_t o_sh, int32_t* error_flag, void* stream) {
+  if (n_q < 0 || q_pos0 < 0 || q_pos0 + n_q > n)
+    return fail(SSA_ERR_INVALID_ARGUMENT, "sparse_attention: query rows [%lld, %lld) outside the %lld keys",
+                static_cast<long long>(q_pos0), static_cast<long long>(q_pos0 + n_q),
+                static_cast<long long>(n));
   if (dtype != SSA_DTYPE_F32 && dtype != SSA_DTYPE_BF16)
     return fail(SSA_ERR_UNSUPPORTED, "sparse_attention: dtype %d not supported (f32, bf16)", dtype);
   if (out_dtype != SSA_DTYPE_F32 && out_dtype != SSA_DTYPE_BF16)
@@ -775,7 +781,7 @@ extern "C" int ssa_sparse_attention(const void* q, const void* k, const void* v,
     return fail(SSA_ERR_UNSUPPORTED, "sparse_attention: q/k/v rows must be 16-byte aligned");
   if ((o_sb % vec) || (o_sn % vec) || (o_sh % vec) || (reinterpret_cast<uintptr_t>(out) % 16))
     return fail(SSA_ERR_UNSUPPORTED, "sparse_attention: output rows must be 16-byte aligned");
-  if (batch == 0 || n == 0) return SSA_OK;
+  if (batch == 0 || n == 0 || n_q == 0) return SSA_OK;
   if (!q || !k || !v || !out || (top_k > 0 && !idx))
     return fail(SSA_ERR_INVALID_ARGUMENT, "sparse_attention: null pointer");
   AttParams p{};
@@ -800,11 +806,29 @@ extern "C" int ssa_sparse_attention(const void* q, const void* k, const void* v,
   p.out_bf16 = (out_dtype == SSA_DTYPE_BF16);
   p.o_sb = o_sb; p.o_sn = o_sn; p.o_sh = o_sh;
   p.err = error_flag;
-  p.rows = batch * h_kv * n;
+  p.rows = batch * h_kv * n_q;
   p.order = row_order;
+  p.n_q = n_q;
+  p.q_pos0 = q_pos0;
   if (p.rows >= (int64_t(1) << 31))
     return fail(SSA_ERR_UNSUPPORTED, "sparse_attention: too many rows");
   hipStream_t st = as_stream(stream);
   if (dtype == SSA_DTYPE_BF16) return launch_att<uint16_t>(p, d, st);
   return launch_att<float>(p, d, st);
+}
+
+extern "C" int ssa_sparse_attention(const void* q, const void* k, const void* v, int dtype,
+                                    int64_t batch, int64_t n, int h_q, int h_kv, int d,
+                                    int64_t q_sb, int64_t q_sn, int64_t q_sh, int64_t k_sb,
+                                    int64_t k_sn, int64_t k_sh, int64_t v_sb, int64_t v_sn,
+                                    int64_t v_sh, const void* idx, int idx_dtype, int top_k,
+                                    int64_t idx_sb, int64_t idx_sn, int64_t idx_sh,
+                                    float scale_div, int causal, const int32_t* row_order,
+                                    void* out, int out_dtype,
+                                    int64_t o_sb, int64_t o_sn, int64_t o_sh, int32_t* error_flag,
+                                    void* stream) {
+  return ssa_sparse_attention_block(q, k, v, dtype, batch, n, n, 0, h_q, h_kv, d, q_sb, q_sn, q_sh,
+                                    k_sb, k_sn, k_sh, v_sb, v_sn, v_sh, idx, idx_dtype, top_k,
+                                    idx_sb, idx_sn, idx_sh, scale_div, causal, row_order, out,
+                                    out_dtype, o_sb, o_sn, o_sh, error_flag, stream);
 }

@@ -51,17 +51,20 @@ struct SelParams {
   void* out;
   int out_i64;
   int32_t* stats;
-  int64_t rows;         // batch * h_kv * n
-  const int32_t* order;  // nullable [rows]: position t of head bh runs query order[bh * n + t]
+  int64_t n_q, q_pos0;   // query rows (q, q_codes, out, stats) and the position of row 0
+  int64_t rows;          // batch * h_kv * n_q
+  const int32_t* order;  // nullable [rows]: slot t of head bh runs query row order[bh * n_q + t]
 };
 
-// Row ((b * h_kv + h) * n + i) processed in slot t of the launch (t = bh * n + u):
-// i = u, or order[t] when an order is given; -1 for an order entry outside [0, n).
+// Row ((b * h_kv + h) * n_q + r) processed in slot t of the launch
+// (t = bh * n_q + u): r = u, or order[t] when an order is given; -1 for an order
+// entry outside [0, n_q).  Query row r sits at key position q_pos0 + r (the
+// causal window and the dense mask use the position).
 __device__ __forceinline__ int64_t row_of_slot(const SelParams& p, int64_t t) {
   if (p.order == nullptr) return t;
   const int32_t o = p.order[t];
-  if (static_cast<uint32_t>(o) >= static_cast<uint64_t>(p.n)) return -1;
-  return (t / p.n) * p.n + o;
+  if (static_cast<uint32_t>(o) >= static_cast<uint64_t>(p.n_q)) return -1;
+  return (t / p.n_q) * p.n_q + o;
 }
 
 __host__ __device__ inline int pow2_at_least(int v) {
@@ -219,11 +222,12 @@ __device__ __forceinline__ void select_row(const SelParams& p, const T* __restri
   __shared__ int s_scan[kSelThreads / 64];
 
   const int tid = threadIdx.x;
-  const int64_t i = row % p.n;
-  const int64_t bh = row / p.n;
+  const int64_t r = row % p.n_q;
+  const int64_t i = p.q_pos0 + r;
+  const int64_t bh = row / p.n_q;
   const int h = static_cast<int>(bh % p.h_kv);
   const int64_t bb = bh / p.h_kv;
-  const T* q0 = qg + bb * p.q_sb + i * p.q_sn + static_cast<int64_t>(h * p.g) * p.q_sh;
+  const T* q0 = qg + bb * p.q_sb + r * p.q_sn + static_cast<int64_t>(h * p.g) * p.q_sh;
   const T* kbase = static_cast<const T*>(p.k) + bb * p.k_sb + static_cast<int64_t>(h) * p.k_sh;
   const int32_t* pp = p.postings + bh * p.n * p.b;
   const uint8_t* mrow =
@@ -239,7 +243,7 @@ __device__ __forceinline__ void select_row(const SelParams& p, const T* __restri
   if (tid < 64) {
     int32_t lo = 0, len = 0;
     if (tid < p.a) {
-      const int32_t c = p.q_codes[(bh * p.n + i) * p.a + tid];
+      const int32_t c = p.q_codes[(bh * p.n_q + r) * p.a + tid];
       if (static_cast<uint32_t>(c) < static_cast<uint32_t>(p.n_c)) {
         const int32_t* off = p.offsets + bh * (p.n_c + 1);
         const int32_t total = static_cast<int32_t>(p.n * p.b);
@@ -389,7 +393,7 @@ __device__ __forceinline__ void select_row(const SelParams& p, const T* __restri
   if (nsel < p.k_eff) scan_bits(bitmap, words, live, p.n, false, stage + nsel, p.k_eff - nsel, s_scan);
   __syncthreads();
 
-  const int64_t obase = ((bb * p.n + i) * p.h_kv + h) * p.top_k;
+  const int64_t obase = ((bb * p.n_q + r) * p.h_kv + h) * p.top_k;
   if (p.out_i64) {
     int64_t* out64 = static_cast<int64_t*>(p.out) + obase;
     for (int w = tid; w < p.top_k; w += kSelThreads) out64[w] = (w < p.k_eff) ? stage[w] : 0;
@@ -398,8 +402,8 @@ __device__ __forceinline__ void select_row(const SelParams& p, const T* __restri
     for (int w = tid; w < p.top_k; w += kSelThreads) out32[w] = (w < p.k_eff) ? stage[w] : 0;
   }
   if (p.stats && tid == 0) {
-    p.stats[(bh * p.n + i) * 2 + 0] = s_cand;
-    p.stats[(bh * p.n + i) * 2 + 1] = s_R;
+    p.stats[(bh * p.n_q + r) * 2 + 0] = s_cand;
+    p.stats[(bh * p.n_q + r) * 2 + 1] = s_R;
   }
 }
 
@@ -492,8 +496,9 @@ __global__ __launch_bounds__(64 * kLightWaves) void select_light_kernel(SelParam
   if (row < 0) return;
   const int words = static_cast<int>((p.n + 31) >> 5);
   uint32_t* bm = lbits + static_cast<int64_t>(wave) * words;
-  const int64_t i = row % p.n;
-  const int64_t bh = row / p.n;
+  const int64_t r = row % p.n_q;
+  const int64_t i = p.q_pos0 + r;
+  const int64_t bh = row / p.n_q;
   const int h = static_cast<int>(bh % p.h_kv);
   const int64_t bb = bh / p.h_kv;
   const int32_t* pp = p.postings + bh * p.n * p.b;
@@ -504,7 +509,7 @@ __global__ __launch_bounds__(64 * kLightWaves) void select_light_kernel(SelParam
 
   int32_t lo = 0, len = 0;
   if (lane < p.a) {
-    const int32_t c = p.q_codes[(bh * p.n + i) * p.a + lane];
+    const int32_t c = p.q_codes[(bh * p.n_q + r) * p.a + lane];
     if (static_cast<uint32_t>(c) < static_cast<uint32_t>(p.n_c)) {
       const int32_t* off = p.offsets + bh * (p.n_c + 1);
       const int32_t total = static_cast<int32_t>(p.n * p.b);
@@ -533,8 +538,8 @@ __global__ __launch_bounds__(64 * kLightWaves) void select_light_kernel(SelParam
   wave_excl_scan(fresh, lane, &C);
   if (p.stats) wave_excl_scan(seen, lane, &raw);
   if (p.stats && lane == 0) {
-    p.stats[(bh * p.n + i) * 2 + 0] = C;
-    p.stats[(bh * p.n + i) * 2 + 1] = raw;
+    p.stats[(bh * p.n_q + r) * 2 + 0] = C;
+    p.stats[(bh * p.n_q + r) * 2 + 1] = raw;
   }
   __builtin_amdgcn_wave_barrier();
 
@@ -584,7 +589,7 @@ __global__ __launch_bounds__(64 * kLightWaves) void select_light_kernel(SelParam
     return;
   }
 
-  const int64_t obase = ((bb * p.n + i) * p.h_kv + h) * p.top_k;
+  const int64_t obase = ((bb * p.n_q + r) * p.h_kv + h) * p.top_k;
   int32_t* o32 = static_cast<int32_t*>(p.out) + obase;
   int64_t* o64 = static_cast<int64_t*>(p.out) + obase;
   auto put = [&](int pos, int32_t v) {
@@ -712,11 +717,11 @@ __global__ __launch_bounds__(64 * kScrWaves) void select_screen_kernel(SelParams
     if (!x.ok) continue;  // the pick pass sends the row to the exact pass
     const int C = x.C;
     const int64_t off = x.off;
-    const int64_t i = x.row % p.n;
-    const int64_t bh = x.row / p.n;
+    const int64_t r = x.row % p.n_q;
+    const int64_t bh = x.row / p.n_q;
     const int h = static_cast<int>(bh % p.h_kv);
     const int64_t bb = bh / p.h_kv;
-    const uint16_t* q0 = static_cast<const uint16_t*>(p.q) + bb * p.q_sb + i * p.q_sn +
+    const uint16_t* q0 = static_cast<const uint16_t*>(p.q) + bb * p.q_sb + r * p.q_sn +
                          static_cast<int64_t>(h * p.g) * p.q_sh;
     const uint16_t* kbase = static_cast<const uint16_t*>(p.k) + bb * p.k_sb + static_cast<int64_t>(h) * p.k_sh;
     const __amdgpu_buffer_rsrc_t krs =
@@ -861,8 +866,8 @@ __global__ __launch_bounds__(64 * kScrWaves) void select_pick_kernel(SelParams p
     const int C = x.C;
     const int64_t off = x.off;
     const int64_t row = x.row;
-    const int64_t i = row % p.n;
-    const int64_t bh = row / p.n;
+    const int64_t r = row % p.n_q;
+    const int64_t bh = row / p.n_q;
     const int h = static_cast<int>(bh % p.h_kv);
     const int64_t bb = bh / p.h_kv;
     const int R = (C + 63) / 64;  // positions lane + 64 r, r < R
@@ -979,7 +984,7 @@ __global__ __launch_bounds__(64 * kScrWaves) void select_pick_kernel(SelParams p
     }
 
     // The group's q rows into the score area (free now): head gg at gg * D.
-    const uint16_t* q0 = static_cast<const uint16_t*>(p.q) + bb * p.q_sb + i * p.q_sn +
+    const uint16_t* q0 = static_cast<const uint16_t*>(p.q) + bb * p.q_sb + r * p.q_sn +
                          static_cast<int64_t>(h * p.g) * p.q_sh;
     uint16_t* ql = reinterpret_cast<uint16_t*>(av);
     for (int t = lane; t < p.g * (D / 8); t += 64) {
@@ -1035,7 +1040,7 @@ __global__ __launch_bounds__(64 * kScrWaves) void select_pick_kernel(SelParams p
     __builtin_amdgcn_wave_barrier();
 
     // The selected keys in index order.
-    const int64_t obase = ((bb * p.n + i) * p.h_kv + h) * p.top_k;
+    const int64_t obase = ((bb * p.n_q + r) * p.h_kv + h) * p.top_k;
     int32_t* o32 = static_cast<int32_t*>(p.out) + obase;
     int64_t* o64 = static_cast<int64_t*>(p.out) + obase;
     int filled = 0;
@@ -1203,14 +1208,19 @@ extern "C" size_t ssa_select_workspace_bytes(int64_t batch, int64_t n, int h_kv,
   return sel_ws_fixed(rows) + 256 + align_up(static_cast<size_t>(rows) * static_cast<size_t>(k_eff), 256) * 8;
 }
 
-extern "C" int ssa_select(const void* q, const void* k, int dtype, int64_t batch, int64_t n,
-                          int h_q, int h_kv, int d, int64_t q_sb, int64_t q_sn, int64_t q_sh,
-                          int64_t k_sb, int64_t k_sn, int64_t k_sh, const int32_t* q_codes, int a,
-                          const int32_t* offsets, const int32_t* postings, int n_c, int b,
-                          int top_k, int mask_mode, const uint8_t* mask, int64_t mask_sb,
-                          int64_t mask_si, float score_div, int sorted, const int32_t* row_order,
-                          void* out, int out_index_dtype, int32_t* stats, void* workspace,
-                          size_t workspace_bytes, void* stream) {
+extern "C" int ssa_select_block(const void* q, const void* k, int dtype, int64_t batch, int64_t n,
+                                int64_t n_q, int64_t q_pos0, int h_q, int h_kv, int d, int64_t q_sb,
+                                int64_t q_sn, int64_t q_sh, int64_t k_sb, int64_t k_sn, int64_t k_sh,
+                                const int32_t* q_codes, int a, const int32_t* offsets,
+                                const int32_t* postings, int n_c, int b, int top_k, int mask_mode,
+                                const uint8_t* mask, int64_t mask_sb, int64_t mask_si,
+                                float score_div, int sorted, const int32_t* row_order, void* out,
+                                int out_index_dtype, int32_t* stats, void* workspace,
+                                size_t workspace_bytes, void* stream) {
+  if (n_q < 0 || q_pos0 < 0 || q_pos0 + n_q > n)
+    return fail(SSA_ERR_INVALID_ARGUMENT, "select: query rows [%lld, %lld) outside the %lld keys",
+                static_cast<long long>(q_pos0), static_cast<long long>(q_pos0 + n_q),
+                static_cast<long long>(n));
   if (dtype != SSA_DTYPE_F32 && dtype != SSA_DTYPE_BF16)
     return fail(SSA_ERR_UNSUPPORTED, "select: dtype %d not supported (f32, bf16)", dtype);
   if (batch < 0 || n < 0 || h_q <= 0 || h_kv <= 0 || d <= 0 || a <= 0 || b <= 0 || n_c <= 0 ||
@@ -1236,10 +1246,10 @@ extern "C" int ssa_select(const void* q, const void* k, int dtype, int64_t batch
   if ((k_sn % vec) || (k_sh % vec) || (k_sb % vec) || (reinterpret_cast<uintptr_t>(k) % 16) ||
       (q_sn % vec) || (q_sh % vec) || (q_sb % vec) || (reinterpret_cast<uintptr_t>(q) % 16))
     return fail(SSA_ERR_UNSUPPORTED, "select: q and k rows must be 16-byte aligned");
-  if (workspace && workspace_bytes < ssa_select_workspace_bytes(batch, n, h_kv, 0))
+  if (workspace && workspace_bytes < ssa_select_workspace_bytes(batch, n_q, h_kv, 0))
     return fail(SSA_ERR_WORKSPACE, "select: workspace %zu < %zu bytes", workspace_bytes,
-                ssa_select_workspace_bytes(batch, n, h_kv, 0));
-  if (batch == 0 || n == 0) return SSA_OK;
+                ssa_select_workspace_bytes(batch, n_q, h_kv, 0));
+  if (batch == 0 || n == 0 || n_q == 0) return SSA_OK;
   if (!q || !k || !q_codes || !offsets || !postings || !out)
     return fail(SSA_ERR_INVALID_ARGUMENT, "select: null pointer");
   SelParams p{};
@@ -1270,15 +1280,31 @@ extern "C" int ssa_select(const void* q, const void* k, int dtype, int64_t batch
   p.out = out;
   p.out_i64 = (out_index_dtype == SSA_INDEX_I64);
   p.stats = stats;
-  p.rows = batch * h_kv * n;
+  p.n_q = n_q;
+  p.q_pos0 = q_pos0;
+  p.rows = batch * h_kv * n_q;
   p.order = row_order;
   const size_t smem = select_smem(n, p.sortn, p.k_eff);
   if (smem > 160 * 1024)
     return fail(SSA_ERR_UNSUPPORTED, "select: needs %zu bytes of LDS (n=%lld, top_k=%d)", smem,
                 static_cast<long long>(n), top_k);
-  const int64_t rows = batch * h_kv * n;
+  const int64_t rows = batch * h_kv * n_q;
   if (rows >= (int64_t(1) << 31)) return fail(SSA_ERR_UNSUPPORTED, "select: too many rows");
   hipStream_t st = as_stream(stream);
   if (dtype == SSA_DTYPE_BF16) return dispatch_select<uint16_t>(p, rows, smem, workspace, workspace_bytes, st);
   return dispatch_select<float>(p, rows, smem, workspace, workspace_bytes, st);
+}
+
+extern "C" int ssa_select(const void* q, const void* k, int dtype, int64_t batch, int64_t n,
+                          int h_q, int h_kv, int d, int64_t q_sb, int64_t q_sn, int64_t q_sh,
+                          int64_t k_sb, int64_t k_sn, int64_t k_sh, const int32_t* q_codes, int a,
+                          const int32_t* offsets, const int32_t* postings, int n_c, int b,
+                          int top_k, int mask_mode, const uint8_t* mask, int64_t mask_sb,
+                          int64_t mask_si, float score_div, int sorted, const int32_t* row_order,
+                          void* out, int out_index_dtype, int32_t* stats, void* workspace,
+                          size_t workspace_bytes, void* stream) {
+  return ssa_select_block(q, k, dtype, batch, n, n, 0, h_q, h_kv, d, q_sb, q_sn, q_sh, k_sb, k_sn,
+                          k_sh, q_codes, a, offsets, postings, n_c, b, top_k, mask_mode, mask,
+                          mask_sb, mask_si, score_div, sorted, row_order, out, out_index_dtype,
+                          stats, workspace, workspace_bytes, stream);
 }

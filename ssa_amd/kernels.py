@@ -132,8 +132,13 @@ def select(q: torch.Tensor, k: torch.Tensor, q_codes: torch.Tensor, offsets: tor
            mask: Optional[torch.Tensor] = None, score_div: Optional[float] = None,
            index_dtype: torch.dtype = torch.int64,
            with_stats: bool = False, sorted: bool = True, use_workspace: Union[bool, int] = True,
-           row_order: Optional[torch.Tensor] = None):
-    """Stage (c): candidate indices [B, n, h_kv, top_k] (ssa/router.py:151-214).
+           row_order: Optional[torch.Tensor] = None, q_pos0: Optional[int] = None):
+    """Stage (c): candidate indices [B, n_q, h_kv, top_k] (ssa/router.py:151-214).
+
+    ``q`` and ``q_codes`` may hold fewer rows (n_q) than ``k`` has keys (n): a
+    block of queries at key positions ``q_pos0 .. q_pos0 + n_q - 1`` (default:
+    the last n_q positions, as in decoding against a cache).  With n_q = n this
+    is the whole sequence.
 
     ``mask`` (MASK_DENSE) is a bool/uint8 ``[n, n]`` or ``[B, n, n]`` tensor with a
     contiguous last dimension.  ``with_stats`` also returns int32 ``[B, h_kv, n, 2]``
@@ -148,7 +153,10 @@ def select(q: torch.Tensor, k: torch.Tensor, q_codes: torch.Tensor, offsets: tor
     _check_rows(q, "q")
     _check_rows(k, "k")
     _lib.require_device(q, k, q_codes, offsets, postings, mask)
-    B, n, h_q, d = q.shape
+    B, n_q, h_q, d = q.shape
+    n = k.shape[1]
+    if q_pos0 is None:
+        q_pos0 = n - n_q
     h_kv = k.shape[2]
     a = q_codes.shape[-1]
     n_c = offsets.shape[-1] - 1
@@ -169,19 +177,19 @@ def select(q: torch.Tensor, k: torch.Tensor, q_codes: torch.Tensor, offsets: tor
             m_sb, m_si = mask.stride(0), mask.stride(1)
     if row_order is not None:
         _lib.require_device(row_order)
-        if row_order.dtype != torch.int32 or tuple(row_order.shape) != (B, h_kv, n):
-            raise ValueError(f"row_order must be int32 [{B}, {h_kv}, {n}]")
+        if row_order.dtype != torch.int32 or tuple(row_order.shape) != (B, h_kv, n_q):
+            raise ValueError(f"row_order must be int32 [{B}, {h_kv}, {n_q}]")
         row_order = row_order.contiguous()
-    out = torch.empty((B, n, h_kv, top_k), device=q.device, dtype=index_dtype)
-    stats = torch.empty((B, h_kv, n, 2), device=q.device, dtype=torch.int32) if with_stats else None
+    out = torch.empty((B, n_q, h_kv, top_k), device=q.device, dtype=index_dtype)
+    stats = torch.empty((B, h_kv, n_q, 2), device=q.device, dtype=torch.int32) if with_stats else None
     ws_bytes, ws = 0, None
     if use_workspace is True:
-        ws_bytes = int(_lib.load().ssa_select_workspace_bytes(B, n, h_kv, top_k))
+        ws_bytes = int(_lib.load().ssa_select_workspace_bytes(B, n_q, h_kv, top_k))
     elif use_workspace is not False:
         ws_bytes = int(use_workspace)
     if ws_bytes > 0:
         ws = torch.empty(ws_bytes, device=q.device, dtype=torch.uint8)
-    call("ssa_select", ptr(q), ptr(k), _lib.elem_dtype(q), B, n, h_q, h_kv, d,
+    call("ssa_select_block", ptr(q), ptr(k), _lib.elem_dtype(q), B, n, n_q, q_pos0, h_q, h_kv, d,
          q.stride(0), q.stride(1), q.stride(2), k.stride(0), k.stride(1), k.stride(2),
          ptr(q_codes), a, ptr(offsets), ptr(postings), n_c, b, top_k, mask_mode, ptr(mask),
          m_sb, m_si, float(score_div), int(bool(sorted)), ptr(row_order), ptr(out), _lib.index_dtype(out),
@@ -193,29 +201,37 @@ def sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, idx: tor
                      scale_div: Optional[float] = None, causal: bool = False,
                      out: Optional[torch.Tensor] = None,
                      error_flag: Optional[torch.Tensor] = None,
-                     row_order: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """Stage (d): gathered exact attention, [B, n, h_q, d] in q's dtype (ssa/attention.py:12-115).
+                     row_order: Optional[torch.Tensor] = None,
+                     q_pos0: Optional[int] = None) -> torch.Tensor:
+    """Stage (d): gathered exact attention, [B, n_q, h_q, d] in q's dtype (ssa/attention.py:12-115).
 
-    ``row_order`` (int32 [B, h_kv, n], a permutation of 0..n-1 per head) only sets
-    the order in which rows are processed; results are the same."""
+    ``row_order`` (int32 [B, h_kv, n_q], a permutation of 0..n_q-1 per head) only
+    sets the order in which rows are processed; results are the same.  ``q`` and
+    ``idx`` may hold fewer rows (n_q) than ``k``/``v`` have keys: query row r
+    then sits at key position ``q_pos0 + r`` (default n - n_q), which is what
+    ``causal`` compares the indices with."""
     for name, t in (("q", q), ("k", k), ("v", v), ("indices", idx)):
         _check_rows(t, name)
     _lib.require_device(q, k, v, idx)
     if not (q.dtype == k.dtype == v.dtype):
         raise TypeError(f"q, k, v must share a dtype ({q.dtype}, {k.dtype}, {v.dtype})")
-    B, n, h_q, d = q.shape
+    B, n_q, h_q, d = q.shape
+    n = k.shape[1]
+    if q_pos0 is None:
+        q_pos0 = n - n_q
     h_kv = k.shape[2]
     top_k = idx.shape[-1]
     if scale_div is None:
         scale_div = math.sqrt(d)
     if out is None:
-        out = torch.empty((B, n, h_q, d), device=q.device, dtype=q.dtype)
+        out = torch.empty((B, n_q, h_q, d), device=q.device, dtype=q.dtype)
     if row_order is not None:
         _lib.require_device(row_order)
-        if row_order.dtype != torch.int32 or tuple(row_order.shape) != (B, h_kv, n):
-            raise ValueError(f"row_order must be int32 [{B}, {h_kv}, {n}]")
+        if row_order.dtype != torch.int32 or tuple(row_order.shape) != (B, h_kv, n_q):
+            raise ValueError(f"row_order must be int32 [{B}, {h_kv}, {n_q}]")
         row_order = row_order.contiguous()
-    call("ssa_sparse_attention", ptr(q), ptr(k), ptr(v), _lib.elem_dtype(q), B, n, h_q, h_kv, d,
+    call("ssa_sparse_attention_block", ptr(q), ptr(k), ptr(v), _lib.elem_dtype(q), B, n, n_q, q_pos0,
+         h_q, h_kv, d,
          q.stride(0), q.stride(1), q.stride(2), k.stride(0), k.stride(1), k.stride(2),
          v.stride(0), v.stride(1), v.stride(2), ptr(idx), _lib.index_dtype(idx), top_k,
          idx.stride(0), idx.stride(1), idx.stride(2), float(scale_div), int(bool(causal)),

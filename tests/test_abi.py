@@ -57,7 +57,7 @@ def L():
 
 def test_header_parses_every_entry_point():
     decls = _declarations()
-    assert len(decls) == 17
+    assert len(decls) == 19
     assert set(decls) == set(_lib.SIGNATURES)
 
 
@@ -229,3 +229,18 @@ def test_workspace_sizes_grow(L):
     for ws in (f(1, 1024, 8, 4096, 32), g(1, 1024, 8, 4, 4096),
                L.ssa_code_topk_workspace_bytes(1, 8, 1024, 4096)):
         assert ws % 256 == 0, "workspace sub-buffers are 256-byte aligned"
+
+
+def test_block_entry_points_reject_rows_past_the_keys(L):
+    """ssa_select_block / ssa_sparse_attention_block: query rows
+    [q_pos0, q_pos0 + n_q) must lie inside the n keys (checked before any launch)."""
+    null = ctypes.c_void_p(0)
+    st = L.ssa_sparse_attention_block(null, null, null, 0, 1, 32, 4, 30, 4, 2, 64, 0, 256, 64, 0, 128,
+                                      64, 0, 128, 64, null, 0, 8, 0, 16, 8, 8.0, 1, null, null, 0,
+                                      0, 256, 64, null, null)
+    assert st == _lib.SSA_ERR_INVALID_ARGUMENT
+    assert b"outside" in L.ssa_last_error()
+    st = L.ssa_select_block(null, null, 0, 1, 32, 4, -1, 4, 2, 64, 0, 256, 64, 0, 128, 64, null, 8,
+                            null, null, 16, 4, 8, 1, null, 0, 0, 8.0, 0, null, null, 0, null, null, 0,
+                            null)
+    assert st == _lib.SSA_ERR_INVALID_ARGUMENT
