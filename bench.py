@@ -53,6 +53,9 @@ def parse():
                    help="also run one device copy of this size (PMC byte calibration)")
     p.add_argument("--backward", action="store_true",
                    help="also time the stage-(d) backward (dq, dk, dv) on the workload's indices")
+    p.add_argument("--decode", type=int, default=0,
+                   help="also time this many single-token decode steps after a prefill of n minus "
+                        "that many tokens (SSADecodeCache)")
     p.add_argument("--sweep", default="", help="comma list of n for a tokens/s vs n sweep")
     p.add_argument("--sweep-nc", default="scaled", choices=("scaled", "fixed"),
                    help="codebook size in the sweep: scaled with n (constant bucket size; the "
@@ -238,6 +241,28 @@ def time_backward(cfg, q, k, v, inter, reps=3):
             "algorithmic_gb": byt / 1e9, "gbs": byt / (ms / 1000) / 1e9}
 
 
+def time_decode(cfg, q, k, v, router, steps):
+    """Single-token decode steps (ssa_amd.decode.SSADecodeCache) for the last
+    `steps` tokens of the workload after a prefill of the rest; wall time per
+    step on the host (each step launches about a dozen kernels)."""
+    import torch
+
+    from ssa_amd.decode import SSADecodeCache
+
+    n = cfg["n"]
+    cache = SSADecodeCache(router, cfg["B"], n, cfg["d"], dtype=q.dtype)
+    n0 = n - steps
+    cache.step(q[:, :n0], k[:, :n0], v[:, :n0])
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for t in range(n0, n):
+        cache.step(q[:, t:t + 1], k[:, t:t + 1], v[:, t:t + 1])
+    torch.cuda.synchronize()
+    ms = 1000 * (time.perf_counter() - t0) / steps
+    return {"ms_per_token": ms, "tokens_per_s": cfg["B"] / (ms / 1000), "cache_len": n,
+            "steps": steps, "prefill_tokens": n0}
+
+
 def cpu_baseline(cfg, q, k, v, router, inter, budget_s):
     """Times the CPU oracle (oracle/ssa_oracle.c, OpenMP) on sampled rows of the same
     workload and extrapolates each stage to the full forward."""
@@ -417,6 +442,8 @@ def main():
     }
     if args.backward:
         line["backward"] = time_backward(cfg, q, k, v, inter)
+    if args.decode > 0:
+        line["decode"] = time_decode(cfg, q, k, v, router, args.decode)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(cfg, q, k, v, router, inter, args.cpu_seconds)
     if args.sweep:
