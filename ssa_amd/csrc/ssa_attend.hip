@@ -463,10 +463,12 @@ __global__ __launch_bounds__(kAttThreads, (AttMinBlocks<T, D, GMAX>::value)) voi
 //                  and tile.
 // Dropped slots (causal, past top_k, out of range) load zeros, so 0 * inf
 // never reaches the sums.
-// Waves per block and blocks per CU of the matrix-core kernel.  Each wave keeps
+// Waves per block and waves per SIMD of the matrix-core kernel.  Each wave keeps
 // one chunk (16 KB at d = 128) of K and V in flight in its LDS slices, so the
-// bytes in flight per CU are LDS-bound.
-constexpr int kMfWaves = 4;
+// bytes in flight per CU are LDS-bound; the waves share nothing, so one-wave
+// blocks let a CU hold 10 of them (160 KB) and start each as soon as one ends
+// (c3 stage d: 3.90 ms against 4.04 with four-wave blocks, 3.95 with two).
+constexpr int kMfWaves = 1;
 constexpr int kMfMinBlocks = 2;
 
 // Issue one chunk's K and V loads: load r moves chunk rows KPI*r .. KPI*r +
