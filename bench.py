@@ -46,6 +46,7 @@ def parse():
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--config", default="c3", choices=sorted(CONFIGS))
     p.add_argument("--n", type=int, default=None, help="override sequence length")
+    p.add_argument("--num-codebook", type=int, default=None, help="override the codebook size N_c")
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline budget")
@@ -382,6 +383,8 @@ def main():
     cfg = dict(CONFIGS[args.config])
     if args.n:
         cfg["n"] = args.n
+    if args.num_codebook:
+        cfg["n_c"] = args.num_codebook
     if args.copy_probe_gib > 0:
         nb = copy_probe(args.copy_probe_gib)
         print(f"copy probe: {nb} bytes read, {nb} bytes written", file=sys.stderr, flush=True)
@@ -397,7 +400,7 @@ def main():
     t_d = st["d"] / 1000.0
     d_gbs = alg["d_bytes"] / t_d / 1e9
     # Counter-measured traffic applies only to the profiled workload shape.
-    traffic, traffic_src = (measured_traffic(args.config) if args.n is None and args.seed == 0
+    traffic, traffic_src = (measured_traffic(args.config) if args.n is None and args.num_codebook is None and args.seed == 0
                             else (None, None))
     stages = {
         "a": {"ms": st["a"], "gflop": alg["a_flops"] / 1e9,

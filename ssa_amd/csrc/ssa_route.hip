@@ -440,8 +440,7 @@ __host__ __device__ inline size_t code_topk_smem(int d_s, int top) {
 // by insertion after each tile.
 __global__ __launch_bounds__(kTopThreads) void code_topk_kernel(
     const float* __restrict__ xhat, int64_t rows, int h, const float* __restrict__ chat, int n_c,
-    int d_s, float temperature, int top, int32_t* __restrict__ codes,
-    const uint8_t* __restrict__ only_flagged) {
+    int d_s, float temperature, int top, int32_t* __restrict__ codes) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   constexpr int rpad = kTopRows + 4, cpad = kTopCodes + 4;
   float* Xs = reinterpret_cast<float*>(smem_raw);                // [d_s][rpad]
@@ -453,8 +452,6 @@ __global__ __launch_bounds__(kTopThreads) void code_topk_kernel(
   int* bcnt = cnt + kTopRows;                                    // [rows]
 
   const int64_t tiles = (rows + kTopRows - 1) / kTopRows;
-  // Fallback role: only the 64-row groups the MFMA filter could not settle.
-  if (only_flagged && !only_flagged[blockIdx.x]) return;
   const int64_t bh = blockIdx.x / tiles;
   const int64_t r0 = (blockIdx.x % tiles) * kTopRows;
   const int hh = static_cast<int>(bh % h);
@@ -564,8 +561,8 @@ __global__ __launch_bounds__(kTopThreads) void code_topk_kernel(
 // LDS round trips; a lane visits the append code only for the scores that hit.
 // Pass 3 rescores a row's four lists in the canonical fp32 order and keeps the
 // exact top-`top` (score desc, code asc).  Rows with an overflowing list (or
-// non-finite inputs) flag their 64-row group, which code_topk_kernel then
-// recomputes exhaustively.
+// non-finite inputs) are flagged, and code_topk_rows_kernel recomputes them
+// exhaustively, one wave per row.
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float floatx4_t __attribute__((ext_vector_type(4)));
 
@@ -1014,8 +1011,77 @@ __global__ __launch_bounds__(256, Q == 1 ? 4 : 1) void code_topk_mfma_kernel(
       for (int p = 0; p < top; ++p) out[p] = static_cast<int32_t>(key_index(my[p * 64]));
     }
   }
-  const bool any_over = __ballot(row < rows && over) != 0ull;
-  if (lane == 0 && r0 < rows) flags[bh * ((rows + 63) / 64) + r0 / 64] = any_over ? 1 : 0;
+  if (row < rows) flags[bh * rows + row] = over ? 1 : 0;
+}
+
+// Exact top-`top` codes of the rows flagged by the matrix-core filter
+// (flags[bh * rows + row] != 0), one wave per row: lane l scores codes l, l + 64,
+// ... in the canonical fp32 order (one fmaf chain over d_s, then / temperature)
+// and keeps its best TM composite keys in a sorted register list; `top` rounds
+// of a wave-wide maximum then take the row's keys in descending order.  The
+// result is the top-`top` by (score desc, code asc), as code_topk_kernel gives.
+// Each wave scans the flags of 64 consecutive rows per step, so unflagged rows
+// cost one byte read.
+template <int TM>
+__global__ __launch_bounds__(256) void code_topk_rows_kernel(const float* __restrict__ xhat, int64_t total,
+                                                             int64_t rows, int h, const float* __restrict__ chat,
+                                                             int n_c, int d_s, float temperature, int top,
+                                                             int32_t* __restrict__ codes,
+                                                             const uint8_t* __restrict__ flags) {
+  const int lane = threadIdx.x & 63;
+  const int64_t gw = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int64_t nw = static_cast<int64_t>(gridDim.x) * 4;
+  const bool scale = (temperature != 1.0f);
+  for (int64_t base = gw * 64; base < total; base += nw * 64) {
+    const bool f = base + lane < total && flags[base + lane] != 0;
+    for (uint64_t m = __ballot(f); m != 0ull; m &= m - 1ull) {
+      const int64_t grow = base + (__ffsll(static_cast<long long>(m)) - 1);  // bh * rows + row
+      const int hh = static_cast<int>((grow / rows) % h);
+      const float* xr = xhat + grow * d_s;
+      const float* cb = chat + static_cast<int64_t>(hh) * n_c * d_s;
+      float x[32];
+#pragma unroll
+      for (int s = 0; s < 32; ++s) x[s] = (s < d_s) ? xr[s] : 0.0f;
+      uint64_t best[TM];
+#pragma unroll
+      for (int p = 0; p < TM; ++p) best[p] = 0ull;  // below every key
+      for (int c = lane; c < n_c; c += 64) {
+        const float4* cr = reinterpret_cast<const float4*>(cb + static_cast<int64_t>(c) * d_s);
+        float acc = 0.0f;
+#pragma unroll
+        for (int s4 = 0; s4 < 8; ++s4) {
+          if (s4 * 4 < d_s) {
+            const float4 cv = cr[s4];
+            acc = fma_rn(x[s4 * 4 + 0], cv.x, acc);
+            acc = fma_rn(x[s4 * 4 + 1], cv.y, acc);
+            acc = fma_rn(x[s4 * 4 + 2], cv.z, acc);
+            acc = fma_rn(x[s4 * 4 + 3], cv.w, acc);
+          }
+        }
+        if (scale) acc = acc / temperature;
+        const uint64_t key = composite_key(acc, static_cast<uint32_t>(c));
+#pragma unroll
+        for (int p = TM - 1; p > 0; --p) best[p] = key > best[p - 1] ? best[p - 1] : (key > best[p] ? key : best[p]);
+        best[0] = key > best[0] ? key : best[0];
+      }
+      int32_t* out = codes + grow * top;
+      for (int p = 0; p < top; ++p) {
+        uint64_t v = best[0];
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+          const uint32_t lo = static_cast<uint32_t>(__shfl_xor(static_cast<int>(v & 0xFFFFFFFFull), o));
+          const uint32_t hi = static_cast<uint32_t>(__shfl_xor(static_cast<int>(v >> 32), o));
+          const uint64_t w = (static_cast<uint64_t>(hi) << 32) | lo;
+          v = w > v ? w : v;
+        }
+        const bool win = best[0] == v;  // keys are distinct, so one lane holds v
+#pragma unroll
+        for (int q = 0; q < TM - 1; ++q) best[q] = win ? best[q + 1] : best[q];
+        best[TM - 1] = win ? 0ull : best[TM - 1];
+        if (lane == 0) out[p] = static_cast<int32_t>(key_index(v));
+      }
+    }
+  }
 }
 
 int next_pow2(int v) {
@@ -1125,7 +1191,7 @@ struct TopkWorkspace {
 size_t topk_workspace_bytes(int64_t batch, int h, int64_t rows, int n_c) {
   return align_up(sizeof(uint16_t) * static_cast<size_t>(h) * n_c_padded(n_c) * 32, 256) +
          align_up(sizeof(float) * static_cast<size_t>(h), 256) +
-         align_up(static_cast<size_t>(batch * h * ceil_div(rows, 64)), 256);
+         align_up(static_cast<size_t>(batch * h * rows), 256);  // a flag per row
 }
 
 TopkWorkspace carve_topk(void* ws, int h, int n_c) {
@@ -1142,14 +1208,34 @@ TopkWorkspace carve_topk(void* ws, int h, int n_c) {
 bool mfma_path_ok(int top, int d_s, int n_c) { return top <= 32 && d_s <= 32 && d_s % 4 == 0 && n_c <= 65535; }
 
 int launch_exact_topk(const float* xhat, int64_t batch, int h, int64_t rows, const float* chat,
-                      int n_c, int d_s, float temperature, int top, int32_t* codes,
-                      const uint8_t* only_flagged, hipStream_t st) {
+                      int n_c, int d_s, float temperature, int top, int32_t* codes, hipStream_t st) {
   const int64_t grid = batch * h * ceil_div(rows, kTopRows);
   const size_t smem = code_topk_smem(d_s, top);
   if (int s = reserve_lds(reinterpret_cast<const void*>(code_topk_kernel), smem, "code_topk")) return s;
   code_topk_kernel<<<dim3(static_cast<unsigned>(grid)), kTopThreads, smem, st>>>(
-      xhat, rows, h, chat, n_c, d_s, temperature, top, codes, only_flagged);
+      xhat, rows, h, chat, n_c, d_s, temperature, top, codes);
   return check_launch("code_topk_kernel");
+}
+
+template <int TM>
+int launch_rows_tm(const float* xhat, int64_t total, int64_t rows, int h, const float* chat, int n_c,
+                   int d_s, float temperature, int top, int32_t* codes, const uint8_t* flags,
+                   hipStream_t st) {
+  const int64_t grid = std::min<int64_t>(ceil_div(total, 256), 1024);
+  code_topk_rows_kernel<TM><<<dim3(static_cast<unsigned>(grid)), 256, 0, st>>>(
+      xhat, total, rows, h, chat, n_c, d_s, temperature, top, codes, flags);
+  return check_launch("code_topk_rows_kernel");
+}
+
+// The flagged rows of a matrix-core pass (top <= 32, d_s <= 32).
+int launch_flagged_topk(const float* xhat, int64_t batch, int h, int64_t rows, const float* chat,
+                        int n_c, int d_s, float temperature, int top, int32_t* codes,
+                        const uint8_t* flags, hipStream_t st) {
+  const int64_t total = batch * h * rows;
+  if (top <= 4) return launch_rows_tm<4>(xhat, total, rows, h, chat, n_c, d_s, temperature, top, codes, flags, st);
+  if (top <= 8) return launch_rows_tm<8>(xhat, total, rows, h, chat, n_c, d_s, temperature, top, codes, flags, st);
+  if (top <= 16) return launch_rows_tm<16>(xhat, total, rows, h, chat, n_c, d_s, temperature, top, codes, flags, st);
+  return launch_rows_tm<32>(xhat, total, rows, h, chat, n_c, d_s, temperature, top, codes, flags, st);
 }
 
 int launch_codebook_prep(const float* chat, int h, int n_c, int d_s, const TopkWorkspace& w,
@@ -1183,7 +1269,7 @@ int launch_code_topk(const float* xhat, int64_t batch, int h, int64_t rows, cons
                      bool prepped, hipStream_t st) {
   if (batch == 0 || rows == 0) return SSA_OK;
   if (!ws || !mfma_path_ok(top, d_s, n_c))
-    return launch_exact_topk(xhat, batch, h, rows, chat, n_c, d_s, temperature, top, codes, nullptr, st);
+    return launch_exact_topk(xhat, batch, h, rows, chat, n_c, d_s, temperature, top, codes, st);
   const TopkWorkspace w = carve_topk(ws, h, n_c);
   int s;
   if (!prepped && (s = launch_codebook_prep(chat, h, n_c, d_s, w, st))) return s;
@@ -1192,7 +1278,7 @@ int launch_code_topk(const float* xhat, int64_t batch, int h, int64_t rows, cons
   else if (top <= 16) s = launch_mfma_q<4>(xhat, batch, h, rows, chat, n_c, d_s, temperature, top, codes, w, st);
   else s = launch_mfma_q<8>(xhat, batch, h, rows, chat, n_c, d_s, temperature, top, codes, w, st);
   if (s) return s;
-  return launch_exact_topk(xhat, batch, h, rows, chat, n_c, d_s, temperature, top, codes, w.flags, st);
+  return launch_flagged_topk(xhat, batch, h, rows, chat, n_c, d_s, temperature, top, codes, w.flags, st);
 }
 
 int launch_normalize(const float* x, int64_t rows, int d_s, float* out, hipStream_t st) {

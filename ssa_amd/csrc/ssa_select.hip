@@ -469,11 +469,20 @@ __global__ __launch_bounds__(kSelThreads) void select_heavy_kernel(SelParams p, 
 
 // Index-order rows, one wave per row, no block barriers: the row's buckets go
 // through the wave's LDS bitmap; a row with at most k_eff candidates writes its
-// candidates ascending and the filler directly.  A row with more writes its
-// candidate list into the workspace for select_screen_kernel when it fits
-// (w.cap), and is listed for the exact pass otherwise.  One wave per block, so
-// no row waits for a longer one before its LDS is released.
-constexpr int kLightWaves = 1;
+// candidates ascending and the filler directly.  A row whose causal window
+// spans more than kFlatWords bitmap words also keeps a summary level (bit x:
+// bitmap word x was touched by this row): only the summary is cleared, a word is
+// zeroed by the lane whose summary atomicOr set its bit (a wave's LDS
+// operations run in program order, so that store lands before any lane's
+// atomicOr on the word), and the candidates are read back from the touched
+// words only, so a row costs n / 1024 summary words plus its touched words
+// rather than n / 32 words.  Shorter windows clear and scan the flat bitmap,
+// which costs less than the summary's extra atomic per posting.  A row with
+// more than k_eff candidates writes its list into the workspace for
+// select_screen_kernel when it fits (w.cap), and is listed for the exact pass
+// otherwise.  One wave per block, so no row waits for a longer one before its
+// LDS is released.
+constexpr int kFlatWords = 1024;  // windows of up to 32768 keys use the flat bitmap
 
 __device__ __forceinline__ int wave_excl_scan(int v, int lane, int* total) {
   int x = v;
@@ -486,16 +495,64 @@ __device__ __forceinline__ int wave_excl_scan(int v, int lane, int* total) {
   return x - v;
 }
 
-__global__ __launch_bounds__(64 * kLightWaves) void select_light_kernel(SelParams p, int64_t rows, SelWs w) {
+// LDS words per wave: the summary (one bit per bitmap word, padded to 4 words)
+// and the bitmap (one bit per key).
+__host__ __device__ inline int light_summary_words(int64_t n) {
+  return static_cast<int>(((n + 1023) / 1024 + 3) & ~int64_t(3));
+}
+__host__ __device__ inline int light_words(int64_t n) {
+  return light_summary_words(n) + static_cast<int>((n + 31) / 32);
+}
+
+// Writes the row's candidates (the set bits of the touched bitmap words) in
+// ascending order through sink(pos, key) and returns their number.  Lane l
+// takes summary words s0 + l of each chunk of 64: it counts the bits of its
+// touched words, an exclusive scan over the lanes gives its first position,
+// and it writes its keys; lane order is key order within a chunk.
+template <typename Sink>
+__device__ __forceinline__ int light_emit(const uint32_t* sm, const uint32_t* bm, int slive, int lane, Sink&& sink) {
+  int filled = 0;
+  for (int s0 = 0; s0 < slive; s0 += 64) {
+    const int sx = s0 + lane;
+    const uint32_t sbits = (sx < slive) ? sm[sx] : 0u;
+    int cnt = 0;
+    for (uint32_t t = sbits; t != 0u; t &= t - 1u) cnt += __popc(bm[sx * 32 + __ffs(t) - 1]);
+    int total = 0;
+    int pos = filled + wave_excl_scan(cnt, lane, &total);
+    for (uint32_t t = sbits; t != 0u; t &= t - 1u) {
+      const int x = sx * 32 + __ffs(t) - 1;
+      for (uint32_t bits = bm[x]; bits != 0u; bits &= bits - 1u) sink(pos++, x * 32 + __ffs(bits) - 1);
+    }
+    filled += total;
+  }
+  return filled;
+}
+
+// The same from the flat bitmap words [0, live).
+template <typename Sink>
+__device__ __forceinline__ int light_emit_flat(const uint32_t* bm, int live, int lane, Sink&& sink) {
+  int filled = 0;
+  for (int w0 = 0; w0 < live; w0 += 64) {
+    const int x = w0 + lane;
+    uint32_t bits = (x < live) ? bm[x] : 0u;
+    int total = 0;
+    int pos = filled + wave_excl_scan(__popc(bits), lane, &total);
+    for (; bits != 0u; bits &= bits - 1u) sink(pos++, x * 32 + __ffs(bits) - 1);
+    filled += total;
+  }
+  return filled;
+}
+
+__global__ __launch_bounds__(64) void select_light_kernel(SelParams p, int64_t rows, SelWs w) {
   extern __shared__ __align__(16) uint32_t lbits[];
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
-  const int64_t slot = static_cast<int64_t>(blockIdx.x) * kLightWaves + wave;
+  const int64_t slot = blockIdx.x;
   if (slot >= rows) return;
   const int64_t row = row_of_slot(p, slot);
   if (row < 0) return;
+  uint32_t* sm = lbits;                             // summary
+  uint32_t* bm = lbits + light_summary_words(p.n);  // bitmap
   const int words = static_cast<int>((p.n + 31) >> 5);
-  uint32_t* bm = lbits + static_cast<int64_t>(wave) * words;
   const int64_t r = row % p.n_q;
   const int64_t i = p.q_pos0 + r;
   const int64_t bh = row / p.n_q;
@@ -505,7 +562,13 @@ __global__ __launch_bounds__(64 * kLightWaves) void select_light_kernel(SelParam
   const bool causal = p.mask_mode == SSA_MASK_CAUSAL;
   const uint8_t* mrow = (p.mask_mode == SSA_MASK_DENSE) ? p.mask + bb * p.mask_sb + i * p.mask_si : nullptr;
   const int live = causal ? static_cast<int>(i >> 5) + 1 : words;
-  for (int x = lane; x < live; x += 64) bm[x] = 0u;
+  const int slive = (live + 31) >> 5;
+  const bool flat = live <= kFlatWords;
+  if (flat) {
+    for (int x = lane; x < live; x += 64) bm[x] = 0u;
+  } else {
+    for (int x = lane; x < slive; x += 64) sm[x] = 0u;
+  }
 
   int32_t lo = 0, len = 0;
   if (lane < p.a) {
@@ -528,8 +591,13 @@ __global__ __launch_bounds__(64 * kLightWaves) void select_light_kernel(SelParam
         seen += in_window ? 1 : 0;
         if (static_cast<uint32_t>(j) < static_cast<uint32_t>(p.n) && in_window &&
             (mrow == nullptr || mrow[j] != 0)) {
+          const int x = j >> 5;
+          if (!flat) {
+            const uint32_t sb = 1u << (x & 31);
+            if (!(atomicOr(&sm[x >> 5], sb) & sb)) bm[x] = 0u;
+          }
           const uint32_t bit = 1u << (j & 31);
-          if (!(atomicOr(&bm[j >> 5], bit) & bit)) ++fresh;
+          if (!(atomicOr(&bm[x], bit) & bit)) ++fresh;
         }
       }
     }
@@ -563,18 +631,9 @@ __global__ __launch_bounds__(64 * kLightWaves) void select_light_kernel(SelParam
       return;
     }
     int32_t* dst = w.cand + off;
-    int filled = 0;
-    for (int w0 = 0; w0 < live && filled < C; w0 += 64) {
-      const int x = w0 + lane;
-      uint32_t bits = (x < live) ? bm[x] : 0u;
-      int total = 0;
-      int pos = filled + wave_excl_scan(__popc(bits), lane, &total);
-      while (bits != 0u) {
-        dst[pos++] = x * 32 + __ffs(bits) - 1;
-        bits &= bits - 1u;
-      }
-      filled += total;
-    }
+    auto to_list = [&](int pos, int32_t v) { dst[pos] = v; };
+    if (flat) light_emit_flat(bm, live, lane, to_list);
+    else light_emit(sm, bm, slive, lane, to_list);
     if (lane == 0) {
       const int slot = atomicAdd(&sc[0], 1);
       if (slot >= 0 && slot < w.shard_rows) {
@@ -597,23 +656,13 @@ __global__ __launch_bounds__(64 * kLightWaves) void select_light_kernel(SelParam
     else o32[pos] = v;
   };
   // Candidates ascending, then the lowest non-candidates up to k_eff.
-  int filled = 0;
-  for (int w0 = 0; w0 < live && filled < C; w0 += 64) {
-    const int x = w0 + lane;
-    uint32_t bits = (x < live) ? bm[x] : 0u;
-    int total = 0;
-    int pos = filled + wave_excl_scan(__popc(bits), lane, &total);
-    while (bits != 0u) {
-      put(pos++, x * 32 + __ffs(bits) - 1);
-      bits &= bits - 1u;
-    }
-    filled += total;
-  }
+  int filled = flat ? light_emit_flat(bm, live, lane, put) : light_emit(sm, bm, slive, lane, put);
   for (int w0 = 0; filled < p.k_eff; w0 += 64) {
     const int x = w0 + lane;
     uint32_t bits = 0u;
     if (x < words) {
-      bits = ~((x < live) ? bm[x] : 0u);
+      const bool set = x < live && (flat || ((sm[x >> 5] >> (x & 31)) & 1u));
+      bits = ~(set ? bm[x] : 0u);
       if (x == words - 1 && (p.n & 31)) bits &= (1u << (p.n & 31)) - 1u;
     }
     int total = 0;
@@ -1070,10 +1119,10 @@ __global__ void zero_ctr_kernel(int32_t* __restrict__ ctr) {
   for (int x = threadIdx.x; x < static_cast<int>(kSelCtrBytes / 4); x += blockDim.x) ctr[x] = 0;
 }
 
-size_t light_smem(int64_t n) { return sizeof(uint32_t) * kLightWaves * static_cast<size_t>((n + 31) / 32); }
+size_t light_smem(int64_t n) { return sizeof(uint32_t) * static_cast<size_t>(light_words(n)); }
 
 // Rows of the light-pass blocks of one shard (block b -> shard b % kShards).
-int64_t shard_rows_for(int64_t rows) { return ceil_div(ceil_div(rows, kLightWaves), kShards) * kLightWaves; }
+int64_t shard_rows_for(int64_t rows) { return ceil_div(rows, kShards); }
 
 size_t sel_ws_fixed(int64_t rows) {
   return kSelCtrBytes + align_up(sizeof(int32_t) * static_cast<size_t>(rows), 256) +
@@ -1157,8 +1206,7 @@ int launch_select(const SelParams& p, int64_t rows, size_t smem, void* ws, size_
   const SelWs w = carve_sel_ws(ws, ws_bytes, rows, screen);
   zero_ctr_kernel<<<1, 256, 0, st>>>(w.ctr);
   if (int s = check_launch("zero_ctr_kernel")) return s;
-  select_light_kernel<<<dim3(static_cast<unsigned>(ceil_div(rows, kLightWaves))), 64 * kLightWaves,
-                        light_smem(p.n), st>>>(p, rows, w);
+  select_light_kernel<<<dim3(static_cast<unsigned>(rows)), 64, light_smem(p.n), st>>>(p, rows, w);
   if (int s = check_launch("select_light_kernel")) return s;
   if constexpr (kScreenable) {
     if (w.cap > 0) {

@@ -264,3 +264,57 @@ def test_code_topk_screen_overflow_falls_back(dev, orc):
     np.testing.assert_array_equal(got.cpu().numpy()[0], ref)
     assert (ref[0, 0] == np.arange(100, 116)).all()
     assert (ref[0, 250] == np.arange(16)).all()
+
+
+@pytest.mark.parametrize("top,n_c,temperature", [(4, 1024, 1.0), (8, 2000, 0.7), (16, 1024, 1.0),
+                                                 (16, 20000, 1.0), (32, 1500, 0.7)])
+def test_code_topk_flagged_rows_batched(dev, orc, top, n_c, temperature):
+    """Rows the screen cannot settle (exact ties over a block of 300 equal codes in
+    head 1 only) are recomputed one wave per row; every (batch, head, row) lands
+    in its own output row and matches the oracle."""
+    from ssa_amd import kernels
+
+    _say(f"code_topk flagged rows top={top} n_c={n_c} temperature={temperature}")
+    B, h, rows, d_s = 2, 2, 700, 32
+    chat = orc.normalize(f32(randn((h, n_c, d_s), 16)))
+    chat[1, 100:400] = chat[1, 100]
+    xhat = orc.normalize(f32(randn((B, h, rows, d_s), 17)))
+    xhat[:, 1, 50:120] = chat[1, 100]         # tied rows in head 1 of both batches
+    xhat[1, 1, 600] = 0.0                     # every score ties at 0
+    got = kernels.code_topk(torch.from_numpy(xhat).to(dev), torch.from_numpy(chat).to(dev), top,
+                            temperature).cpu().numpy()
+    for bb in range(B):
+        ref = orc.code_topk(xhat[bb], chat, top, temperature)
+        np.testing.assert_array_equal(got[bb], ref)
+    assert (got[:, 1, 50] == np.arange(100, 100 + top)).all()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("mode", ["causal", "none"])
+def test_router_long_rows_bit_exact(dev, orc, dtype, mode):
+    """n = 70000 keys: a row's key bitmap spans more than 64 summary words, so the
+    index-order pass reads its candidates back in two chunks; stats and indices
+    must equal the oracle's."""
+    from ssa_amd import CodebookRouter
+
+    _say(f"router long rows dtype={dtype} mode={mode}")
+    n, h_q, h_kv, d, d_s, n_c, a, b, k = 70000, 2, 1, 64, 16, 2048, 4, 2, 128
+    q, kk, w_qr, w_kr, cb = _route_inputs(n, h_q, h_kv, d, d_s, n_c, 23, dtype, False)
+    r = CodebookRouter(head_dim=d, route_dim=d_s, num_kv_heads=h_kv, num_codebook=n_c,
+                       codes_per_key=b, codes_per_query=a, top_k=k)
+    with torch.no_grad():
+        r.W_qr.weight.copy_(w_qr)
+        r.W_kr.weight.copy_(w_kr)
+        r.codebook.copy_(cb)
+    r = r.to(dev)
+    causal = mode == "causal"
+    res = r.route(q.to(dev), kk.to(dev), causal_mask=True if causal else None, with_stats=True,
+                  sorted=False)
+    (ref, ncand, nraw), _ = orc.router_forward(f32(q), f32(kk), f32(w_qr), f32(w_kr), f32(cb),
+                                               a, b, k, orc.MASK_CAUSAL if causal else orc.MASK_NONE,
+                                               None, with_stats=True, sorted=False)
+    np.testing.assert_array_equal(res.indices[0].cpu().numpy(), ref)
+    st = res.stats[0].cpu().numpy()
+    np.testing.assert_array_equal(st[..., 0].T, ncand)
+    np.testing.assert_array_equal(st[..., 1].T, nraw)
+    assert (ncand > k).any()
