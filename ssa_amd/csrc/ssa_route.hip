@@ -1045,24 +1045,38 @@ __global__ __launch_bounds__(256) void code_topk_rows_kernel(const float* __rest
       uint64_t best[TM];
 #pragma unroll
       for (int p = 0; p < TM; ++p) best[p] = 0ull;  // below every key
-      for (int c = lane; c < n_c; c += 64) {
+      auto insert = [&](uint64_t key) {
+#pragma unroll
+        for (int p = TM - 1; p > 0; --p) best[p] = key > best[p - 1] ? best[p - 1] : (key > best[p] ? key : best[p]);
+        best[0] = key > best[0] ? key : best[0];
+      };
+      auto load = [&](int c, float4 (&cv)[8]) {
         const float4* cr = reinterpret_cast<const float4*>(cb + static_cast<int64_t>(c) * d_s);
+#pragma unroll
+        for (int s4 = 0; s4 < 8; ++s4) cv[s4] = (s4 * 4 < d_s) ? cr[s4] : make_float4(0.f, 0.f, 0.f, 0.f);
+      };
+      auto key_of = [&](int c, const float4 (&cv)[8]) -> uint64_t {
         float acc = 0.0f;
 #pragma unroll
         for (int s4 = 0; s4 < 8; ++s4) {
           if (s4 * 4 < d_s) {
-            const float4 cv = cr[s4];
-            acc = fma_rn(x[s4 * 4 + 0], cv.x, acc);
-            acc = fma_rn(x[s4 * 4 + 1], cv.y, acc);
-            acc = fma_rn(x[s4 * 4 + 2], cv.z, acc);
-            acc = fma_rn(x[s4 * 4 + 3], cv.w, acc);
+            acc = fma_rn(x[s4 * 4 + 0], cv[s4].x, acc);
+            acc = fma_rn(x[s4 * 4 + 1], cv[s4].y, acc);
+            acc = fma_rn(x[s4 * 4 + 2], cv[s4].z, acc);
+            acc = fma_rn(x[s4 * 4 + 3], cv[s4].w, acc);
           }
         }
         if (scale) acc = acc / temperature;
-        const uint64_t key = composite_key(acc, static_cast<uint32_t>(c));
-#pragma unroll
-        for (int p = TM - 1; p > 0; --p) best[p] = key > best[p - 1] ? best[p - 1] : (key > best[p] ? key : best[p]);
-        best[0] = key > best[0] ? key : best[0];
+        return composite_key(acc, static_cast<uint32_t>(c));
+      };
+      // two codes per step, both code rows in flight before either is scored
+      for (int c = lane; c < n_c; c += 128) {
+        const bool two = c + 64 < n_c;
+        float4 cv0[8], cv1[8];
+        load(c, cv0);
+        load(two ? c + 64 : c, cv1);
+        insert(key_of(c, cv0));
+        if (two) insert(key_of(c + 64, cv1));
       }
       int32_t* out = codes + grow * top;
       for (int p = 0; p < top; ++p) {

@@ -483,6 +483,7 @@ __global__ __launch_bounds__(kSelThreads) void select_heavy_kernel(SelParams p, 
 // otherwise.  One wave per block, so no row waits for a longer one before its
 // LDS is released.
 constexpr int kFlatWords = 1024;  // windows of up to 32768 keys use the flat bitmap
+constexpr int kLightBatch = 4;    // buckets whose postings load together
 
 __device__ __forceinline__ int wave_excl_scan(int v, int lane, int* total) {
   int x = v;
@@ -582,24 +583,37 @@ __global__ __launch_bounds__(64) void select_light_kernel(SelParams p, int64_t r
   }
   __builtin_amdgcn_wave_barrier();
   int fresh = 0, seen = 0;  // per lane: new keys, postings inside the window
-  for (int m = 0; m < p.a; ++m) {
-    const int lo_m = __shfl(lo, m), len_m = __shfl(len, m);
-    for (int base = 0; base < len_m; base += 64) {
-      if (base + lane < len_m) {
-        const int32_t j = pp[lo_m + base + lane];
-        const bool in_window = !causal || j <= i;
-        seen += in_window ? 1 : 0;
-        if (static_cast<uint32_t>(j) < static_cast<uint32_t>(p.n) && in_window &&
-            (mrow == nullptr || mrow[j] != 0)) {
-          const int x = j >> 5;
-          if (!flat) {
-            const uint32_t sb = 1u << (x & 31);
-            if (!(atomicOr(&sm[x >> 5], sb) & sb)) bm[x] = 0u;
-          }
-          const uint32_t bit = 1u << (j & 31);
-          if (!(atomicOr(&bm[x], bit) & bit)) ++fresh;
-        }
+  auto add = [&](int32_t j) {
+    const bool in_window = !causal || j <= i;
+    seen += in_window ? 1 : 0;
+    if (static_cast<uint32_t>(j) < static_cast<uint32_t>(p.n) && in_window &&
+        (mrow == nullptr || mrow[j] != 0)) {
+      const int x = j >> 5;
+      if (!flat) {
+        const uint32_t sb = 1u << (x & 31);
+        if (!(atomicOr(&sm[x >> 5], sb) & sb)) bm[x] = 0u;
       }
+      const uint32_t bit = 1u << (j & 31);
+      if (!(atomicOr(&bm[x], bit) & bit)) ++fresh;
+    }
+  };
+  // Buckets kLightBatch at a time: their postings are loaded together, then
+  // marked (the bitmap, the counts and the summary do not depend on the order).
+  for (int m0 = 0; m0 < p.a; m0 += kLightBatch) {
+    int lo_u[kLightBatch], len_u[kLightBatch], most = 0;
+#pragma unroll
+    for (int u = 0; u < kLightBatch; ++u) {
+      lo_u[u] = __shfl(lo, min(m0 + u, 63));
+      len_u[u] = (m0 + u < p.a) ? __shfl(len, min(m0 + u, 63)) : 0;
+      most = max(most, len_u[u]);
+    }
+    for (int base = 0; base < most; base += 64) {
+      int32_t j_u[kLightBatch];
+#pragma unroll
+      for (int u = 0; u < kLightBatch; ++u) j_u[u] = (base + lane < len_u[u]) ? pp[lo_u[u] + base + lane] : -1;
+#pragma unroll
+      for (int u = 0; u < kLightBatch; ++u)
+        if (base + lane < len_u[u]) add(j_u[u]);
     }
   }
   int C = 0, raw = 0;
