@@ -55,53 +55,75 @@ __global__ __launch_bounds__(kHistThreads) void index_hist_kernel(
   for (int c = threadIdx.x; c < n_c; c += kHistThreads) hb[c] = lds_hist[c];
 }
 
+// Entries per chunk of kScanThreads codes: block (chunk, bh), one code per
+// thread summed over the tiles, then a block sum into sums[bh][chunk].
+__global__ __launch_bounds__(kScanThreads) void index_chunk_sum_kernel(const int32_t* __restrict__ hist, int n_c,
+                                                                       int64_t tiles, int chunks,
+                                                                       int32_t* __restrict__ sums) {
+  __shared__ int32_t wsum[kScanThreads / 64];
+  const int chunk = blockIdx.x;
+  const int64_t bh = blockIdx.y;
+  const int c = chunk * kScanThreads + static_cast<int>(threadIdx.x);
+  const int32_t* hb = hist + bh * tiles * static_cast<int64_t>(n_c);
+  int32_t tot = 0;
+  if (c < n_c)
+    for (int64_t t = 0; t < tiles; ++t) tot += hb[t * n_c + c];
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) tot += __shfl_xor(tot, off, 64);
+  if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = tot;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int32_t all = 0;
+    for (int w = 0; w < kScanThreads / 64; ++w) all += wsum[w];
+    sums[bh * chunks + chunk] = all;
+  }
+}
+
 // Bucket base positions, in place: hist[bh][tile][c] (keys of code c in tile)
 // becomes the number of entries before them in (code, tile) order, i.e. where
-// tile `tile` starts writing bucket c; offsets[bh][c] = start of bucket c.  One
-// block per bh, one code per thread per round of kScanThreads codes (coalesced
-// over codes), with a running carry across rounds.
-__global__ __launch_bounds__(kScanThreads) void index_scan_kernel(int32_t* __restrict__ hist,
-                                                                  int n_c, int64_t tiles,
+// tile `tile` starts writing bucket c; offsets[bh][c] = start of bucket c.
+// Block (chunk, bh) takes kScanThreads codes (one per thread, coalesced over
+// codes); its base is the sum of the earlier chunks' entries.
+__global__ __launch_bounds__(kScanThreads) void index_scan_kernel(int32_t* __restrict__ hist, int n_c,
+                                                                  int64_t tiles, int chunks,
+                                                                  const int32_t* __restrict__ sums,
                                                                   int32_t* __restrict__ offsets) {
   __shared__ int32_t wsum[kScanThreads / 64];
-  const int64_t bh = blockIdx.x;
+  const int chunk = blockIdx.x;
+  const int64_t bh = blockIdx.y;
   int32_t* hb = hist + bh * tiles * static_cast<int64_t>(n_c);
   int32_t* ob = offsets + bh * (n_c + 1);
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
   int32_t carry = 0;
-  for (int c0 = 0; c0 < n_c; c0 += kScanThreads) {
-    const int c = c0 + static_cast<int>(threadIdx.x);
-    int32_t tot = 0;
-    if (c < n_c)
-      for (int64_t t = 0; t < tiles; ++t) tot += hb[t * n_c + c];
-    int32_t x = tot;
+  for (int q = 0; q < chunk; ++q) carry += sums[bh * chunks + q];
+  const int c = chunk * kScanThreads + static_cast<int>(threadIdx.x);
+  int32_t tot = 0;
+  if (c < n_c)
+    for (int64_t t = 0; t < tiles; ++t) tot += hb[t * n_c + c];
+  int32_t x = tot;
+  const int lane = threadIdx.x & 63;
 #pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const int32_t y = __shfl_up(x, off, 64);
-      if (lane >= off) x += y;
-    }
-    if (lane == 63) wsum[wave] = x;
-    __syncthreads();
-    int32_t before = carry, round = 0;
-    for (int w = 0; w < kScanThreads / 64; ++w) {
-      const int32_t v = wsum[w];
-      if (w < wave) before += v;
-      round += v;
-    }
-    __syncthreads();  // wsum is rewritten next round
-    if (c < n_c) {
-      int32_t run = before + x - tot;
-      ob[c] = run;
-      for (int64_t t = 0; t < tiles; ++t) {
-        const int32_t v = hb[t * n_c + c];
-        hb[t * n_c + c] = run;
-        run += v;
-      }
-    }
-    carry += round;
+  for (int off = 1; off < 64; off <<= 1) {
+    const int32_t y = __shfl_up(x, off, 64);
+    if (lane >= off) x += y;
   }
-  if (threadIdx.x == 0) ob[n_c] = carry;
+  if (lane == 63) wsum[threadIdx.x >> 6] = x;
+  __syncthreads();
+  int32_t before = carry, all = 0;
+  for (int w = 0; w < kScanThreads / 64; ++w) {
+    const int32_t v = wsum[w];
+    if (w < static_cast<int>(threadIdx.x >> 6)) before += v;
+    all += v;
+  }
+  if (c < n_c) {
+    int32_t run = before + x - tot;
+    ob[c] = run;
+    for (int64_t t = 0; t < tiles; ++t) {
+      const int32_t v = hb[t * n_c + c];
+      hb[t * n_c + c] = run;
+      run += v;
+    }
+  }
+  if (chunk == chunks - 1 && threadIdx.x == 0) ob[n_c] = carry + all;
 }
 
 // One wave per (tile, bh).  Entries are visited in index order e = j*b + r, 64
@@ -152,7 +174,15 @@ __global__ void fill_i32_kernel(int32_t* __restrict__ p, int64_t count, int32_t 
   if (e < count) p[e] = v;
 }
 
-// The three index kernels over entries (j, r < b) of every (batch, head); `hist`
+// Per-tile bucket counts [bh][tiles][n_c], then the per-chunk entry counts
+// [bh][ceil(n_c / kScanThreads)].
+size_t hist_entry_bytes(int64_t bh, int64_t n, int n_c) {
+  const int64_t tiles = ceil_div(n, tile_keys_for(n));
+  return align_up(sizeof(int32_t) * static_cast<size_t>(bh) * n_c * tiles, 256);
+}
+size_t hist_bytes(int64_t bh, int64_t n, int n_c);
+
+// The index kernels over entries (j, r < b) of every (batch, head); `hist`
 // is the workspace, `offsets` receives the bucket starts.
 int run_index(const int32_t* codes, int64_t bh, int64_t n, int b, int cstride, int n_c,
               int32_t* offsets, int32_t* postings, int32_t* hist, hipStream_t st) {
@@ -164,8 +194,13 @@ int run_index(const int32_t* codes, int64_t bh, int64_t n, int b, int cstride, i
                       sizeof(int32_t) * n_c, st>>>(codes, n, b, cstride, n_c, tk, tiles, hist);
   int s = check_launch("index_hist_kernel");
   if (s) return s;
-  index_scan_kernel<<<dim3(static_cast<unsigned>(bh)), kScanThreads, 0, st>>>(hist, n_c, tiles,
-                                                                               offsets);
+  const int chunks = static_cast<int>(ceil_div(n_c, kScanThreads));
+  int32_t* sums = reinterpret_cast<int32_t*>(reinterpret_cast<char*>(hist) + hist_entry_bytes(bh, n, n_c));
+  index_chunk_sum_kernel<<<dim3(static_cast<unsigned>(chunks), static_cast<unsigned>(bh)), kScanThreads, 0, st>>>(
+      hist, n_c, tiles, chunks, sums);
+  if ((s = check_launch("index_chunk_sum_kernel"))) return s;
+  index_scan_kernel<<<dim3(static_cast<unsigned>(chunks), static_cast<unsigned>(bh)), kScanThreads, 0, st>>>(
+      hist, n_c, tiles, chunks, sums, offsets);
   if ((s = check_launch("index_scan_kernel"))) return s;
   index_scatter_kernel<<<dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(bh)), 64,
                          sizeof(int32_t) * n_c, st>>>(codes, n, b, cstride, n_c, code_bits, tk,
@@ -174,8 +209,8 @@ int run_index(const int32_t* codes, int64_t bh, int64_t n, int b, int cstride, i
 }
 
 size_t hist_bytes(int64_t bh, int64_t n, int n_c) {
-  const int64_t tiles = ceil_div(n, tile_keys_for(n));
-  return align_up(sizeof(int32_t) * static_cast<size_t>(bh) * n_c * tiles, 256);
+  return hist_entry_bytes(bh, n, n_c) +
+         align_up(sizeof(int32_t) * static_cast<size_t>(bh) * static_cast<size_t>(ceil_div(n_c, kScanThreads)), 256);
 }
 
 }  // namespace
