@@ -213,6 +213,43 @@ int ssa_sparse_attention_block(
     int causal, const int32_t* row_order, void* out, int out_dtype, int64_t o_sb, int64_t o_sn,
     int64_t o_sh, int32_t* error_flag, void* stream);
 
+/* Key blocks per query block: replaces convert_indices_to_blocks
+ * (ssa/triton_kernel.py:226-294).  idx [batch][n][h_kv][top_k] (strides
+ * idx_sb, idx_sn, idx_sh; int32 or int64 by idx_dtype) -> out
+ * [batch][nb][h_kv][n_k_blocks] (strides o_sb, o_sq, o_sh; SSA_INDEX_I32 or
+ * _I64 by out_dtype), nb = ceil(n / block_size), n_k_blocks <= nb (the
+ * reference takes min(top_k, nb)).  For each query block, the key blocks
+ * (key j -> block j / block_size) its rows reference most often, by count
+ * descending and then block id ascending (the reference leaves the order of
+ * equal counts to torch.topk); rows of the last query block past n count as
+ * top_k references to block 0 each, as in the reference.  block_size: a power
+ * of 2 in [2, 256]; nb <= 8192.  Indices outside [0, n) are skipped and set
+ * *error_flag (nullable) to 1. */
+int ssa_block_indices(const void* idx, int idx_dtype, int64_t batch, int64_t n, int h_kv, int top_k,
+                      int64_t idx_sb, int64_t idx_sn, int64_t idx_sh, int block_size, int n_k_blocks,
+                      void* out, int out_dtype, int64_t o_sb, int64_t o_sq, int64_t o_sh,
+                      int32_t* error_flag, void* stream);
+
+/* Block-sparse exact attention: replaces ssa_triton_attention
+ * (ssa/triton_kernel.py:141-223).  Query row i attends, causally (keys j <=
+ * i), to every key of the n_k_blocks key blocks listed for its query block
+ * i / block_size in blocks [batch][nb][h_kv][n_k_blocks] (strides b_sb, b_sq,
+ * b_sh; int32 or int64 by idx_dtype).  Keys past n in the last block are
+ * skipped; a block id outside [0, nb) sets *error_flag.  The softmax is exact
+ * and normalised (the reference's kernel rescales and normalises its running
+ * sums incorrectly, so its outputs are not a target); scores are q.k /
+ * scale_div (the reference's default scale 1/sqrt(d) is scale_div =
+ * sqrt(d)).  Other arguments as ssa_sparse_attention; it runs the same
+ * kernels with the listed blocks expanded to keys on load. */
+int ssa_block_sparse_attention(const void* q, const void* k, const void* v, int dtype, int64_t batch,
+                               int64_t n, int h_q, int h_kv, int d, int64_t q_sb, int64_t q_sn,
+                               int64_t q_sh, int64_t k_sb, int64_t k_sn, int64_t k_sh, int64_t v_sb,
+                               int64_t v_sn, int64_t v_sh, const void* blocks, int idx_dtype,
+                               int block_size, int n_k_blocks, int64_t b_sb, int64_t b_sq,
+                               int64_t b_sh, float scale_div, void* out, int out_dtype,
+                               int64_t o_sb, int64_t o_sn, int64_t o_sh, int32_t* error_flag,
+                               void* stream);
+
 /* Gradients of ssa_sparse_attention with respect to q, k and v, given the
  * forward output `out` and the output gradient `dout`.  Replaces the autograd
  * backward of sparse_exact_attention (gather -> einsum -> / scale -> softmax ->

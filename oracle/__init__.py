@@ -365,3 +365,76 @@ def np_sparse_attention64(q, k, v, idx, scale=None, causal: bool = False) -> np.
     den = p.sum(-1, keepdims=True)
     p = np.where(den > 0, p / np.where(den > 0, den, 1.0), 0.0)
     return np.einsum("nhgk,nhkd->nhgd", p, vg).reshape(n, h_q, d)
+
+
+# ---------------------------------------------------------------------------
+# Block-granular variant (ssa/triton_kernel.py).  numpy restatements; the
+# product kernels are ssa_block_indices / ssa_block_sparse_attention.
+
+
+def block_indices(indices, block_size: int, n_k_blocks: Optional[int] = None) -> np.ndarray:
+    """Key blocks per query block (ssa/triton_kernel.py:226-294): token indices
+    [n, h, top_k] -> int64 [ceil(n / bs), h, n_k_blocks] (default min(top_k,
+    blocks)).  Key j is in block j // bs (:259); rows past n are zero-padded
+    (:262-268), so each adds top_k references to block 0; a query block's
+    counts come from its bs x top_k entries (:287-288); the n_k_blocks most
+    referenced blocks are kept (:291-292), equal counts by lower block id
+    (torch.topk leaves that order open)."""
+    idx = np.asarray(indices, dtype=np.int64)
+    n, h, k = idx.shape
+    nb = (n + block_size - 1) // block_size
+    nkb = min(k, nb) if n_k_blocks is None else n_k_blocks
+    blk = idx // block_size
+    pad = nb * block_size - n
+    if pad:
+        blk = np.concatenate([blk, np.zeros((pad, h, k), np.int64)], axis=0)
+    blk = blk.reshape(nb, block_size, h, k)
+    out = np.empty((nb, h, nkb), np.int64)
+    ids = np.arange(nb)
+    for bq in range(nb):
+        for hh in range(h):
+            cnt = np.bincount(blk[bq, :, hh, :].ravel(), minlength=nb)
+            out[bq, hh] = np.lexsort((ids, -cnt))[:nkb]
+    return out
+
+
+def brute_block_indices(indices, block_size: int, n_k_blocks: int) -> np.ndarray:
+    """The same ranking from pure-Python counting over (query block, head):
+    an independent check of ``block_indices``."""
+    idx = np.asarray(indices, dtype=np.int64)
+    n, h, k = idx.shape
+    nb = (n + block_size - 1) // block_size
+    out = np.empty((nb, h, n_k_blocks), np.int64)
+    for bq in range(nb):
+        for hh in range(h):
+            counts = {c: 0 for c in range(nb)}
+            for r in range(bq * block_size, (bq + 1) * block_size):
+                for t in range(k):
+                    counts[int(idx[r, hh, t]) // block_size if r < n else 0] += 1
+            ranked = sorted(counts, key=lambda c: (-counts[c], c))
+            out[bq, hh] = ranked[:n_k_blocks]
+    return out
+
+
+def block_sparse_attention64(q, k, v, blocks, block_size: int, scale_div=None) -> np.ndarray:
+    """float64 causal attention of row i over the keys of the blocks listed for
+    block i // bs (ssa/triton_kernel.py:84-130 with an exact, normalised
+    softmax): keys past n are skipped; a row with no key gives zeros."""
+    q, k, v = (np.asarray(x, np.float64) for x in (q, k, v))
+    blocks = np.asarray(blocks, np.int64)
+    n, h_q, d = q.shape
+    h_kv = k.shape[1]
+    g = h_q // h_kv
+    sd = np.sqrt(d) if scale_div is None else scale_div
+    out = np.zeros_like(q)
+    for i in range(n):
+        for hq in range(h_q):
+            hh = hq // g
+            keys = (blocks[i // block_size, hh][:, None] * block_size + np.arange(block_size)[None, :]).ravel()
+            keys = keys[(keys < n) & (keys <= i)]
+            if keys.size == 0:
+                continue
+            s = k[keys, hh] @ q[i, hq] / sd
+            p = np.exp(s - s.max())
+            out[i, hq] = (p / p.sum()) @ v[keys, hh]
+    return out

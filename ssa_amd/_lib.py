@@ -79,6 +79,15 @@ SIGNATURES = {
         [_vp, _vp, _vp, _int, _i64, _i64, _i64, _i64, _int, _int, _int, _i64, _i64, _i64, _i64,
          _i64, _i64, _i64, _i64, _i64, _vp, _int, _int, _i64, _i64, _i64, _flt, _int, _vp, _vp,
          _int, _i64, _i64, _i64, _vp, _vp]),
+    "ssa_block_indices": (
+        _int,
+        [_vp, _int, _i64, _i64, _int, _int, _i64, _i64, _i64, _int, _int, _vp, _int, _i64, _i64,
+         _i64, _vp, _vp]),
+    "ssa_block_sparse_attention": (
+        _int,
+        [_vp, _vp, _vp, _int, _i64, _i64, _int, _int, _int, _i64, _i64, _i64, _i64, _i64, _i64,
+         _i64, _i64, _i64, _vp, _int, _int, _int, _i64, _i64, _i64, _flt, _vp, _int, _i64, _i64,
+         _i64, _vp, _vp]),
     "ssa_sparse_attention_backward": (
         _int,
         [_vp, _vp, _vp, _int, _i64, _i64, _int, _int, _int, _i64, _i64, _i64, _i64, _i64, _i64,

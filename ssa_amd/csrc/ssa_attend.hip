@@ -55,7 +55,31 @@ struct AttParams {
   int64_t rows;
   const int32_t* order;  // nullable [B*h_kv][n_q]: query row processed at each slot
   int64_t n_q, q_pos0;   // query rows (q, idx, out) and the key position of row 0
+  // Block mode (blk_log2 > 0): idx row qr >> blk_log2 holds key-block ids in
+  // [0, nbk); key slot t of a row is key blk[t >> blk_log2] * 2^blk_log2 +
+  // (t & (2^blk_log2 - 1)), and keys at or past n are dropped silently.
+  int blk_log2;
+  int64_t nbk;
 };
+
+// Key of slot `slot` given the index entry loaded for it: -1 = none (block mode:
+// past n), -2 = invalid index (reported through the error flag).
+template <bool BLK>
+__device__ __forceinline__ int att_key(const AttParams& p, int slot, int64_t jv) {
+  if constexpr (!BLK) {
+    if (jv < 0 || jv >= p.n) {
+      if (p.err) p.err[0] = 1;
+      return -2;
+    }
+    return static_cast<int>(jv);
+  }
+  if (jv < 0 || jv >= p.nbk) {
+    if (p.err) p.err[0] = 1;
+    return -2;
+  }
+  const int64_t j = (jv << p.blk_log2) + (slot & ((1 << p.blk_log2) - 1));
+  return j < p.n ? static_cast<int>(j) : -1;
+}
 
 // Row processed by wave slot `lrow` (in (b*h_kv + h)*n_q + slot order): the query
 // row r is the slot itself, or order[lrow] when a processing order is given; it
@@ -262,20 +286,17 @@ __global__ __launch_bounds__(kAttThreads, (AttMinBlocks<T, D, GMAX>::value)) voi
 
   const T* kbase = static_cast<const T*>(p.k) + bb * p.k_sb + static_cast<int64_t>(h) * p.k_sh;
   const T* vbase = static_cast<const T*>(p.v) + bb * p.v_sb + static_cast<int64_t>(h) * p.v_sh + c16 * DQ;
-  const int64_t ibase = bb * p.idx_sb + qr * p.idx_sn + static_cast<int64_t>(h) * p.idx_sh;
+  const int64_t ibase = bb * p.idx_sb + (qr >> p.blk_log2) * p.idx_sn + static_cast<int64_t>(h) * p.idx_sh;
 
   // Index of this lane's slot in chunk ch, range-checked on load: -1 = no slot,
   // -2 = outside [0, n) (reported through the error flag).
   auto load_idx = [&](int ch) -> int {
     const int slot = ch * kChunk + lane;
     if (!row_ok || lane >= kChunk || slot >= p.top_k) return -1;
-    const int64_t j = p.idx_i64 ? static_cast<const int64_t*>(p.idx)[ibase + slot]
-                                : static_cast<int64_t>(static_cast<const int32_t*>(p.idx)[ibase + slot]);
-    if (j < 0 || j >= p.n) {
-      if (p.err) p.err[0] = 1;
-      return -2;
-    }
-    return static_cast<int>(j);
+    const int e = slot >> p.blk_log2;
+    const int64_t jv = p.idx_i64 ? static_cast<const int64_t*>(p.idx)[ibase + e]
+                                 : static_cast<int64_t>(static_cast<const int32_t*>(p.idx)[ibase + e]);
+    return p.blk_log2 ? att_key<true>(p, slot, jv) : att_key<false>(p, slot, jv);
   };
 
   float m_run[4], l_run[4];
@@ -499,7 +520,7 @@ __device__ __forceinline__ void mf_issue(__amdgpu_buffer_rsrc_t krs, __amdgpu_bu
   }
 }
 
-template <int D>
+template <int D, bool BLK>
 __global__ __launch_bounds__(64 * kMfWaves, kMfMinBlocks) void sparse_attention_mfma_kernel(AttParams p) {
   using S = MfShape<D>;
   __shared__ __align__(16) unsigned char kv_lds[kMfWaves][2][kMfChunk * S::ROW];
@@ -526,20 +547,17 @@ __global__ __launch_bounds__(64 * kMfWaves, kMfMinBlocks) void sparse_attention_
 
   const uint16_t* kbase = static_cast<const uint16_t*>(p.k) + bb * p.k_sb + static_cast<int64_t>(h) * p.k_sh;
   const uint16_t* vbase = static_cast<const uint16_t*>(p.v) + bb * p.v_sb + static_cast<int64_t>(h) * p.v_sh;
-  const int64_t ibase = bb * p.idx_sb + qr * p.idx_sn + static_cast<int64_t>(h) * p.idx_sh;
+  const int64_t ibase = bb * p.idx_sb + (BLK ? qr >> p.blk_log2 : qr) * p.idx_sn + static_cast<int64_t>(h) * p.idx_sh;
   unsigned char* kl = kv_lds[wave][0];
   unsigned char* vl = kv_lds[wave][1];
 
   auto load_idx = [&](int ch) -> int {
     const int slot = ch * kMfChunk + lane;
     if (!row_ok || lane >= kMfChunk || slot >= p.top_k) return -1;
-    const int64_t j = p.idx_i64 ? static_cast<const int64_t*>(p.idx)[ibase + slot]
-                                : static_cast<int64_t>(static_cast<const int32_t*>(p.idx)[ibase + slot]);
-    if (j < 0 || j >= p.n) {
-      if (p.err) p.err[0] = 1;
-      return -2;
-    }
-    return static_cast<int>(j);
+    const int e = BLK ? slot >> p.blk_log2 : slot;
+    const int64_t jv = p.idx_i64 ? static_cast<const int64_t*>(p.idx)[ibase + e]
+                                 : static_cast<int64_t>(static_cast<const int32_t*>(p.idx)[ibase + e]);
+    return att_key<BLK>(p, slot, jv);
   };
   // Load r of a chunk: lane l fetches the segment stored in slot l % SEGS of
   // chunk row KPI*r + l / SEGS; the LDS address is the load's base + 16*l.
@@ -724,7 +742,9 @@ int launch_att_d(const AttParams& p, hipStream_t st) {
       return sn >= 0 && 2 * sn < (int64_t(1) << 24) && (p.n - 1) * sn * 2 + 2 * D < (int64_t(1) << 31);
     };
     if (p.g <= 8 && p.d == D && p.n < (int64_t(1) << 24) && fits(p.k_sn) && fits(p.v_sn)) {
-      sparse_attention_mfma_kernel<D><<<dim3(static_cast<unsigned>(ceil_div(p.rows, kMfWaves))), 64 * kMfWaves, 0, st>>>(p);
+      const dim3 grid(static_cast<unsigned>(ceil_div(p.rows, kMfWaves)));
+      if (p.blk_log2 > 0) sparse_attention_mfma_kernel<D, true><<<grid, 64 * kMfWaves, 0, st>>>(p);
+      else sparse_attention_mfma_kernel<D, false><<<grid, 64 * kMfWaves, 0, st>>>(p);
       return check_launch("sparse_attention_mfma_kernel");
     }
   }
@@ -748,13 +768,17 @@ int launch_att(const AttParams& p, int d, hipStream_t st) {
 
 using namespace ssa;
 
-extern "C" int ssa_sparse_attention_block(
-    const void* q, const void* k, const void* v, int dtype, int64_t batch, int64_t n, int64_t n_q,
-    int64_t q_pos0, int h_q, int h_kv, int d, int64_t q_sb, int64_t q_sn, int64_t q_sh, int64_t k_sb,
-    int64_t k_sn, int64_t k_sh, int64_t v_sb, int64_t v_sn, int64_t v_sh, const void* idx,
-    int idx_dtype, int top_k, int64_t idx_sb, int64_t idx_sn, int64_t idx_sh, float scale_div,
-    int causal, const int32_t* row_order, void* out, int out_dtype, int64_t o_sb, int64_t o_sn,
-    int64_t o_sh, int32_t* error_flag, void* stream) {
+namespace ssa {
+namespace {
+// Token indices (blk_log2 = 0, top_k keys per row) or key-block ids
+// (blk_log2 > 0: top_k = blocks per row, nbk blocks in all).
+int attention_entry(const void* q, const void* k, const void* v, int dtype, int64_t batch, int64_t n,
+                    int64_t n_q, int64_t q_pos0, int h_q, int h_kv, int d, int64_t q_sb, int64_t q_sn,
+                    int64_t q_sh, int64_t k_sb, int64_t k_sn, int64_t k_sh, int64_t v_sb, int64_t v_sn,
+                    int64_t v_sh, const void* idx, int idx_dtype, int top_k, int64_t idx_sb, int64_t idx_sn,
+                    int64_t idx_sh, float scale_div, int causal, const int32_t* row_order, void* out,
+                    int out_dtype, int64_t o_sb, int64_t o_sn, int64_t o_sh, int32_t* error_flag,
+                    void* stream, int blk_log2, int64_t nbk) {
   if (n_q < 0 || q_pos0 < 0 || q_pos0 + n_q > n)
     return fail(SSA_ERR_INVALID_ARGUMENT, "sparse_attention: query rows [%lld, %lld) outside the %lld keys",
                 static_cast<long long>(q_pos0), static_cast<long long>(q_pos0 + n_q),
@@ -812,11 +836,50 @@ extern "C" int ssa_sparse_attention_block(
   p.order = row_order;
   p.n_q = n_q;
   p.q_pos0 = q_pos0;
+  p.blk_log2 = blk_log2;
+  p.nbk = nbk;
+  if (blk_log2 > 0) {
+    if ((static_cast<int64_t>(top_k) << blk_log2) >= (int64_t(1) << 31))
+      return fail(SSA_ERR_UNSUPPORTED, "block_sparse_attention: blocks x block_size must be < 2^31");
+    p.top_k = top_k << blk_log2;
+  }
   if (p.rows >= (int64_t(1) << 31))
     return fail(SSA_ERR_UNSUPPORTED, "sparse_attention: too many rows");
   hipStream_t st = as_stream(stream);
   if (dtype == SSA_DTYPE_BF16) return launch_att<uint16_t>(p, d, st);
   return launch_att<float>(p, d, st);
+}
+}  // namespace
+}  // namespace ssa
+
+extern "C" int ssa_sparse_attention_block(
+    const void* q, const void* k, const void* v, int dtype, int64_t batch, int64_t n, int64_t n_q,
+    int64_t q_pos0, int h_q, int h_kv, int d, int64_t q_sb, int64_t q_sn, int64_t q_sh, int64_t k_sb,
+    int64_t k_sn, int64_t k_sh, int64_t v_sb, int64_t v_sn, int64_t v_sh, const void* idx,
+    int idx_dtype, int top_k, int64_t idx_sb, int64_t idx_sn, int64_t idx_sh, float scale_div,
+    int causal, const int32_t* row_order, void* out, int out_dtype, int64_t o_sb, int64_t o_sn,
+    int64_t o_sh, int32_t* error_flag, void* stream) {
+  return attention_entry(q, k, v, dtype, batch, n, n_q, q_pos0, h_q, h_kv, d, q_sb, q_sn, q_sh, k_sb, k_sn,
+                         k_sh, v_sb, v_sn, v_sh, idx, idx_dtype, top_k, idx_sb, idx_sn, idx_sh, scale_div,
+                         causal, row_order, out, out_dtype, o_sb, o_sn, o_sh, error_flag, stream, 0, 0);
+}
+
+extern "C" int ssa_block_sparse_attention(
+    const void* q, const void* k, const void* v, int dtype, int64_t batch, int64_t n, int h_q, int h_kv,
+    int d, int64_t q_sb, int64_t q_sn, int64_t q_sh, int64_t k_sb, int64_t k_sn, int64_t k_sh, int64_t v_sb,
+    int64_t v_sn, int64_t v_sh, const void* blocks, int idx_dtype, int block_size, int n_k_blocks,
+    int64_t b_sb, int64_t b_sq, int64_t b_sh, float scale_div, void* out, int out_dtype, int64_t o_sb,
+    int64_t o_sn, int64_t o_sh, int32_t* error_flag, void* stream) {
+  if (block_size < 2 || block_size > 256 || (block_size & (block_size - 1)) != 0)
+    return fail(SSA_ERR_INVALID_ARGUMENT, "block_sparse_attention: block_size %d (need a power of 2 in [2, 256])",
+                block_size);
+  if (n_k_blocks < 0) return fail(SSA_ERR_INVALID_ARGUMENT, "block_sparse_attention: n_k_blocks < 0");
+  int lg = 0;
+  while ((1 << lg) < block_size) ++lg;
+  const int64_t nbk = (n + block_size - 1) / block_size;
+  return attention_entry(q, k, v, dtype, batch, n, n, 0, h_q, h_kv, d, q_sb, q_sn, q_sh, k_sb, k_sn, k_sh,
+                         v_sb, v_sn, v_sh, blocks, idx_dtype, n_k_blocks, b_sb, b_sq, b_sh, scale_div, 1,
+                         nullptr, out, out_dtype, o_sb, o_sn, o_sh, error_flag, stream, lg, nbk);
 }
 
 extern "C" int ssa_sparse_attention(const void* q, const void* k, const void* v, int dtype,
@@ -829,8 +892,7 @@ extern "C" int ssa_sparse_attention(const void* q, const void* k, const void* v,
                                     void* out, int out_dtype,
                                     int64_t o_sb, int64_t o_sn, int64_t o_sh, int32_t* error_flag,
                                     void* stream) {
-  return ssa_sparse_attention_block(q, k, v, dtype, batch, n, n, 0, h_q, h_kv, d, q_sb, q_sn, q_sh,
-                                    k_sb, k_sn, k_sh, v_sb, v_sn, v_sh, idx, idx_dtype, top_k,
-                                    idx_sb, idx_sn, idx_sh, scale_div, causal, row_order, out,
-                                    out_dtype, o_sb, o_sn, o_sh, error_flag, stream);
+  return attention_entry(q, k, v, dtype, batch, n, n, 0, h_q, h_kv, d, q_sb, q_sn, q_sh, k_sb, k_sn, k_sh,
+                         v_sb, v_sn, v_sh, idx, idx_dtype, top_k, idx_sb, idx_sn, idx_sh, scale_div, causal,
+                         row_order, out, out_dtype, o_sb, o_sn, o_sh, error_flag, stream, 0, 0);
 }

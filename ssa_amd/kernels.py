@@ -240,6 +240,56 @@ def sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, idx: tor
     return out
 
 
+def block_indices(idx: torch.Tensor, block_size: int, n_k_blocks: Optional[int] = None,
+                  error_flag: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Key blocks per query block, int64 [B, ceil(n / block_size), h_kv, n_k_blocks]
+    (ssa/triton_kernel.py:226-294) from token selections ``idx`` [B, n, h_kv, top_k];
+    n_k_blocks defaults to min(top_k, number of blocks).  Ranked by reference
+    count, then lower block id."""
+    _check_rows(idx, "indices")
+    _lib.require_device(idx)
+    B, n, h_kv, top_k = idx.shape
+    nb = (n + block_size - 1) // block_size
+    if n_k_blocks is None:
+        n_k_blocks = min(top_k, nb)
+    out = torch.empty((B, nb, h_kv, n_k_blocks), device=idx.device, dtype=torch.int64)
+    call("ssa_block_indices", ptr(idx), _lib.index_dtype(idx), B, n, h_kv, top_k,
+         idx.stride(0), idx.stride(1), idx.stride(2), int(block_size), int(n_k_blocks), ptr(out),
+         _lib.index_dtype(out), out.stride(0), out.stride(1), out.stride(2), ptr(error_flag),
+         stream_of(idx))
+    return out
+
+
+def block_sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, blocks: torch.Tensor,
+                           block_size: int, scale_div: Optional[float] = None,
+                           out: Optional[torch.Tensor] = None,
+                           error_flag: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Causal exact attention of each query over the key blocks listed for its
+    query block: ``blocks`` [B, ceil(n / block_size), h_kv, n_k_blocks]
+    (ssa/triton_kernel.py:141-223, with an exact normalised softmax)."""
+    for name, t in (("q", q), ("k", k), ("v", v), ("block_indices", blocks)):
+        _check_rows(t, name)
+    _lib.require_device(q, k, v, blocks)
+    if not (q.dtype == k.dtype == v.dtype):
+        raise TypeError(f"q, k, v must share a dtype ({q.dtype}, {k.dtype}, {v.dtype})")
+    B, n, h_q, d = q.shape
+    h_kv = k.shape[2]
+    nb = (n + block_size - 1) // block_size
+    if tuple(blocks.shape[:3]) != (B, nb, h_kv):
+        raise ValueError(f"block_indices must be [{B}, {nb}, {h_kv}, n_k_blocks], got {tuple(blocks.shape)}")
+    if scale_div is None:
+        scale_div = math.sqrt(d)
+    if out is None:
+        out = torch.empty((B, n, h_q, d), device=q.device, dtype=q.dtype)
+    call("ssa_block_sparse_attention", ptr(q), ptr(k), ptr(v), _lib.elem_dtype(q), B, n, h_q, h_kv, d,
+         q.stride(0), q.stride(1), q.stride(2), k.stride(0), k.stride(1), k.stride(2),
+         v.stride(0), v.stride(1), v.stride(2), ptr(blocks), _lib.index_dtype(blocks),
+         int(block_size), blocks.shape[-1], blocks.stride(0), blocks.stride(1), blocks.stride(2),
+         float(scale_div), ptr(out), _lib.elem_dtype(out), out.stride(0), out.stride(1), out.stride(2),
+         ptr(error_flag), stream_of(q))
+    return out
+
+
 def sparse_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, idx: torch.Tensor,
                               out: torch.Tensor, dout: torch.Tensor,
                               scale_div: Optional[float] = None, causal: bool = False,
