@@ -57,6 +57,9 @@ def parse():
     p.add_argument("--decode", type=int, default=0,
                    help="also time this many single-token decode steps after a prefill of n minus "
                         "that many tokens (SSADecodeCache)")
+    p.add_argument("--block-sparse", type=int, default=0,
+                   help="also time the block-granular variant with this many 64-key blocks per "
+                        "query block (block indices from the workload's selections, then attention)")
     p.add_argument("--sweep", default="", help="comma list of n for a tokens/s vs n sweep")
     p.add_argument("--sweep-nc", default="scaled", choices=("scaled", "fixed"),
                    help="codebook size in the sweep: scaled with n (constant bucket size; the "
@@ -240,6 +243,32 @@ def time_backward(cfg, q, k, v, inter, reps=3):
     byt = rows * (3 * kk * d * s + 2 * kk * 4 + g * d * (2 * s + 4) + g * d * 4 + 2 * kk * d * 8)
     return {"ms": ms, "tokens_per_s": B * n / (ms / 1000), "kernel": "sparse_attention_bwd_kernel",
             "algorithmic_gb": byt / 1e9, "gbs": byt / (ms / 1000) / 1e9}
+
+
+def time_blocks(cfg, q, k, v, inter, n_k_blocks, block_size=64, reps=3):
+    """Block-granular variant: ssa_block_indices on the workload's token
+    selections, then ssa_block_sparse_attention; median of `reps` (HIP events)."""
+    import torch
+
+    from ssa_amd import kernels
+
+    qc, kc, off, post, _ = inter
+    idx = kernels.select(q, k, qc, off, post, cfg["b"], cfg["k"], sorted=False, index_dtype=torch.int32)
+    ts = {"indices": [], "attention": []}
+    for _ in range(reps):
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        e[0].record()
+        blocks = kernels.block_indices(idx, block_size, n_k_blocks)
+        e[1].record()
+        kernels.block_sparse_attention(q, k, v, blocks, block_size)
+        e[2].record()
+        torch.cuda.synchronize()
+        ts["indices"].append(e[0].elapsed_time(e[1]))
+        ts["attention"].append(e[1].elapsed_time(e[2]))
+    med = {key: sorted(v)[len(v) // 2] for key, v in ts.items()}
+    return {"block_size": block_size, "n_k_blocks": n_k_blocks, "ms_indices": med["indices"],
+            "ms_attention": med["attention"],
+            "tokens_per_s": cfg["B"] * cfg["n"] / ((med["indices"] + med["attention"]) / 1000.0)}
 
 
 def time_decode(cfg, q, k, v, router, steps):
@@ -447,6 +476,8 @@ def main():
         line["backward"] = time_backward(cfg, q, k, v, inter)
     if args.decode > 0:
         line["decode"] = time_decode(cfg, q, k, v, router, args.decode)
+    if args.block_sparse > 0:
+        line["block_sparse"] = time_blocks(cfg, q, k, v, inter, args.block_sparse)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(cfg, q, k, v, router, inter, args.cpu_seconds)
     if args.sweep:
