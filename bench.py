@@ -5,11 +5,15 @@ codebook top-codes (stage a), inverted index (b), candidate selection (c) and
 gathered-KV attention (d), exactly as CodebookRouter + sparse_exact_attention
 run them.  Workload (default): BASELINE config 3 -- 1 x 32768 tokens, bf16,
 GQA 32/8, d 128, d_s 32, N_c 4096, a 16, b 4, k 512, causal, RoPE theta 1e6 on
-a seeded 64-cluster Gaussian mixture (sigma 0.3), V ~ N(0, 1).
+a seeded 64-cluster Gaussian mixture (sigma 0.3), V ~ N(0, 1).  --config c5 is
+the 128K-token layer; --config c4 times the whole decoder attention block
+(RMSNorm + SSAAttention with its projections) at B 4, n 8192, d_model 4096.
 
 Prints ONE JSON line (rank 0) with the metric, per-stage times, the roofline
-of the dominant kernel (stage d, HIP events on the launch stream) and a
-bounded CPU-oracle baseline.
+of the dominant kernel (stage d: compulsory HBM bytes per launch over its
+HIP-event time on the launch stream, next to the counter-measured traffic and
+the scope table's logical gather rate) and two bounded CPU baselines: the
+reference's dense algorithm restated in torch, and the linear C oracle.
 """
 
 from __future__ import annotations
@@ -29,11 +33,12 @@ if ROOT not in sys.path:
 METRIC = "SSA fwd tokens/s at n=32K,k=512 bf16; % HBM/MFMA roofline per stage"
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
-FP32_PEAK_TFLOPS = 157.3
 
 CONFIGS = {
     "c3": dict(B=1, n=32768, h_q=32, h_kv=8, d=128, d_s=32, n_c=4096, b=4, a=16, k=512,
                clusters=64, sigma=0.3, theta=1e6, dtype="bf16"),
+    "c4": dict(B=4, n=8192, h_q=32, h_kv=8, d=128, d_s=32, n_c=4096, b=4, a=16, k=512,
+               d_model=4096, theta=1e6, dtype="bf16"),
     "c5": dict(B=1, n=131072, h_q=16, h_kv=2, d=128, d_s=32, n_c=8192, b=4, a=32, k=1024,
                clusters=256, sigma=0.3, theta=1e6, dtype="bf16"),
 }
@@ -99,8 +104,79 @@ def make_workload(cfg, seed, device):
     return q, k, v, router
 
 
-def algorithmic(cfg, n, stats_sum=None):
-    """Algorithmic bytes / flops per stage for one forward (B*n*h_kv rows)."""
+def make_block(cfg, seed, device):
+    """Config 4: RMSNorm, then one full SSAAttention forward (q/k/v projections,
+    RoPE as the reference layer applies it (ssa/ssa_layer.py:115-117), routing,
+    attention, o_proj) with the default random init from a fixed seed; hidden
+    states x ~ N(0, 1) of shape [B, n, d_model], bf16."""
+    import torch
+
+    from ssa_amd import SSAAttention
+    from ssa_amd.utils import precompute_rope_freqs
+
+    torch.manual_seed(seed + 1)
+    layer = SSAAttention(hidden_size=cfg["d_model"], num_q_heads=cfg["h_q"],
+                         num_kv_heads=cfg["h_kv"], head_dim=cfg["d"], route_dim=cfg["d_s"],
+                         num_codebook=cfg["n_c"], codes_per_key=cfg["b"],
+                         codes_per_query=cfg["a"], top_k=cfg["k"])
+    norm = torch.nn.RMSNorm(cfg["d_model"], eps=1e-6)
+    layer = layer.to(device, torch.bfloat16).eval()
+    norm = norm.to(device, torch.bfloat16)
+    gen = torch.Generator(device=device).manual_seed(seed)
+    x = torch.randn(cfg["B"], cfg["n"], cfg["d_model"], generator=gen, device=device).to(torch.bfloat16)
+    freqs = precompute_rope_freqs(cfg["d"], cfg["n"], cfg["theta"], device=device)
+    return {"layer": layer, "norm": norm, "x": x, "freqs": freqs}
+
+
+def block_step(blk):
+    """One c4 step: exactly the module calls a user makes."""
+    return blk["layer"](blk["norm"](blk["x"]), freqs=blk["freqs"])
+
+
+def block_stages(blk, reps=5):
+    """Per-phase times of the c4 forward: the same calls SSAAttention.forward
+    makes, with HIP events between them (median of `reps`)."""
+    import torch
+
+    from ssa_amd import kernels
+
+    layer, r = blk["layer"], blk["layer"].router
+    names = ["norm", "projections+rope", "a", "b", "c", "d", "o_proj"]
+    ts = {k_: [] for k_ in names}
+    with torch.no_grad():
+        for _ in range(reps):
+            ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
+            ev[0].record()
+            h = blk["norm"](blk["x"])
+            ev[1].record()
+            q, k, v = layer.project(h, None, blk["freqs"])
+            ev[2].record()
+            qc, kc = kernels.route_codes(q, k, r.W_qr.weight, r.W_kr.weight, r.codebook,
+                                         r.codes_per_query, r.codes_per_key, r.temperature)
+            ev[3].record()
+            off, post = kernels.build_index(kc, r.num_codebook)
+            order = kernels.query_order(qc, r.num_codebook)
+            ev[4].record()
+            idx = kernels.select(q, k, qc, off, post, r.codes_per_key, r.top_k, sorted=False,
+                                 index_dtype=torch.int32, row_order=order)
+            ev[5].record()
+            out = kernels.sparse_attention(q, k, v, idx, None, layer.causal_attention,
+                                           row_order=order)
+            ev[6].record()
+            layer.o_proj(out.reshape(h.shape[0], h.shape[1], -1))
+            ev[7].record()
+            torch.cuda.synchronize()
+            for i, k_ in enumerate(names):
+                ts[k_].append(ev[i].elapsed_time(ev[i + 1]))
+    return {k_: sorted(v_)[len(v_) // 2] for k_, v_ in ts.items()}
+
+
+def algorithmic(cfg, n, stats_sum=None, distinct_kv=None):
+    """Algorithmic bytes / flops per stage for one forward (B*n*h_kv rows).
+
+    stats_sum = (R postings read, C all candidates, C_r candidates of the rows
+    that are rescored, heavy rows) from the select kernels' counters;
+    distinct_kv = number of distinct (batch, kv head, key) rows stage (d) reads."""
     B, h_q, h_kv, d = cfg["B"], cfg["h_q"], cfg["h_kv"], cfg["d"]
     s = 2 if cfg["dtype"] == "bf16" else 4
     g = h_q // h_kv
@@ -108,16 +184,25 @@ def algorithmic(cfg, n, stats_sum=None):
     a, b, k, n_c, d_s = cfg["a"], cfg["b"], cfg["k"], cfg["n_c"], cfg["d_s"]
     out = {}
     out["a_flops"] = 2 * B * n * (h_q + h_kv) * d * d_s + 4 * rows * n_c * d_s
+    out["a_flops_projection"] = 2 * B * n * (h_q + h_kv) * d * d_s
     out["a_bytes"] = B * n * (h_q + h_kv) * d * s + h_kv * n_c * d_s * 4 + rows * (a + b) * 4
     out["b_bytes"] = 3 * rows * b * 4 + h_kv * B * (n_c + 1) * 4
     if stats_sum is not None:
-        # index order: postings, the K rows of the rescored rows' candidates and
-        # their query rows, q_codes and bucket bounds, the output row
-        R, C_r, heavy = stats_sum
+        R, C, C_r, heavy = stats_sum
+        # the scope table's formula: every candidate's K row, each row's q group
+        out["c_bytes_survey"] = R * 4 + C * d * s + rows * (g * d * s + 3 * a * 4 + k * 4)
+        # what the index-order kernels read: postings, the K rows of the rescored
+        # rows' candidates and their q groups, q_codes and bucket bounds, the output
         out["c_bytes"] = R * 4 + C_r * d * s + heavy * g * d * s + rows * (3 * a * 4 + k * 4)
         out["c_flops"] = C_r * 2 * d * g
-    out["d_bytes"] = rows * (k * 4 + 2 * k * d * s + 2 * g * d * s)
+    # the scope table's logical gather: each selected K/V row once per (query, kv head)
+    out["d_bytes_logical"] = rows * (k * 4 + 2 * k * d * s + 2 * g * d * s)
     out["d_flops"] = 4 * rows * g * k * d
+    if distinct_kv is not None:
+        # compulsory: q and the output once, the int32 indices once, every distinct
+        # K/V row once -- what a kernel with a perfect cache moves to and from HBM
+        out["d_bytes_compulsory"] = (2 * B * n * h_q * d * s + rows * k * 4
+                                     + distinct_kv * 2 * d * s)
     return out
 
 
@@ -206,7 +291,14 @@ def stats_sums(q, k, router):
     R = int(st[..., 1].sum())
     heavy = st[..., 0] > router.top_k      # index order rescores only these rows
     C_r = int(st[..., 0][heavy].sum())
-    return R, C, int(heavy.sum()), C_r, st[..., 0].numel(), (qc, kc, off, post, idx)
+    # distinct (batch, kv head, key) rows that stage (d) reads
+    B, n, h_kv, _ = idx.shape
+    base = (torch.arange(B, device=idx.device)[:, None, None, None] * h_kv
+            + torch.arange(h_kv, device=idx.device)[None, None, :, None]) * n
+    seen = torch.zeros(B * h_kv * n, dtype=torch.bool, device=idx.device)
+    seen[(idx + base).reshape(-1)] = True
+    distinct = int(seen.sum())
+    return R, C, int(heavy.sum()), C_r, st[..., 0].numel(), distinct, (qc, kc, off, post, idx)
 
 
 def time_backward(cfg, q, k, v, inter, reps=3):
@@ -293,9 +385,93 @@ def time_decode(cfg, q, k, v, router, steps):
             "steps": steps, "prefill_tokens": n0}
 
 
-def cpu_baseline(cfg, q, k, v, router, inter, budget_s):
-    """Times the CPU oracle (oracle/ssa_oracle.c, OpenMP) on sampled rows of the same
-    workload and extrapolates each stage to the full forward."""
+def _cpu_model():
+    cpu = platform.processor() or platform.machine()
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return cpu
+
+
+def cpu_reference(cfg, q, k, v, router, budget_s, blk=None):
+    """The reference's own dense algorithm (oracle/dense_ref.py: torch on the host
+    cores) on batch element 0.  Its memory grows as rows * n (about 280 GB with
+    every row at n = 32768), so routing runs in full, selection and attention on
+    sampled query rows against all n keys (each sampled row does the full
+    per-row work: all keys scored, masked and ranked), scaled to n rows and to
+    the batch.  With a block (config 4) the q/k/v/o projections of sampled
+    tokens are timed too (fp32 GEMMs) and scaled."""
+    import torch
+
+    from oracle import dense_ref
+
+    threads = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    n, B = cfg["n"], cfg["B"]
+    qf, kf, vf = q[0].float().cpu(), k[0].float().cpu(), v[0].float().cpu()
+    w_qr, w_kr = router.W_qr.weight.float().cpu(), router.W_kr.weight.float().cpu()
+    cb = router.codebook.float().cpu()
+    with torch.no_grad():
+        t0 = time.perf_counter()
+        qc, ka = dense_ref.route_codes(qf, kf, w_qr, w_kr, cb, cfg["a"], cfg["b"])
+        t_a = time.perf_counter() - t0
+        sc = 4
+        while True:
+            rows = torch.linspace(0, n - 1, sc).long()
+            t0 = time.perf_counter()
+            idx = dense_ref.select(qf, kf, qc, ka, cfg["k"], rows, causal=True)
+            t_c1 = time.perf_counter() - t0
+            t0 = time.perf_counter()
+            dense_ref.sparse_attention(qf, kf, vf, idx, rows)
+            t_d1 = time.perf_counter() - t0
+            if t_a + t_c1 + t_d1 > budget_s / 2 or sc >= min(n, 256):
+                break
+            sc = min(n, sc * 2)
+        t_proj = 0.0
+        if blk is not None:
+            layer = blk["layer"]
+            tok = min(512, n)
+            xs = blk["x"][0, :tok].float().cpu()
+            ws = [getattr(layer, m).weight.float().cpu() for m in ("q_proj", "k_proj", "v_proj", "o_proj")]
+            t0 = time.perf_counter()
+            for w in ws:            # every projection's input width is d_model = h_q * d here
+                xs @ w.T
+            t_proj = (time.perf_counter() - t0) * n / tok
+    t_c, t_d = t_c1 * n / sc, t_d1 * n / sc
+    total = t_a + t_c + t_d + t_proj                  # one batch element
+    return {
+        "value": n / total,
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"the reference's dense algorithm (ssa/router.py:102-259, ssa/attention.py:64-113) "
+                   f"restated in torch on the CPU (oracle/dense_ref.py; {threads} threads, "
+                   f"{_cpu_model()}): routing of all {n} tokens in full, dense rescoring + candidate "
+                   f"mask + top-k + attention for {sc} sampled query rows against all {n} keys, scaled "
+                   f"to {n} rows" + (f" and {B} batch elements" if B > 1 else "")
+                   + ("; q/k/v/o projections timed on 512 tokens, scaled" if blk is not None else "")
+                   + f"; all rows at once would need about {dense_bytes(cfg) / 1e9:.0f} GB"),
+        "stage_s": {"a": t_a, "c": t_c, "d": t_d, "projections": t_proj},
+    }
+
+
+def dense_bytes(cfg):
+    """Host memory the reference's dense algorithm needs for one batch element with
+    every row at once: fp32 scores [n, h_kv, g, n], their masked copy and group
+    mean, the candidate mask, the gathered K and V."""
+    n, h_q, h_kv, d, k = cfg["n"], cfg["h_q"], cfg["h_kv"], cfg["d"], cfg["k"]
+    s = 2 if cfg["dtype"] == "bf16" else 4
+    return 4 * n * n * h_q * 2 + 4 * n * n * h_kv + n * n * h_kv + 2 * n * h_kv * k * d * s
+
+
+def cpu_oracle(cfg, q, k, v, router, inter, budget_s):
+    """Times the linear-memory CPU oracle (oracle/ssa_oracle.c, OpenMP) on sampled
+    rows of batch element 0 and extrapolates each stage to the full forward (all
+    batch elements).  Its outputs on the sample are checked equal to the GPU's."""
     import numpy as np
     import torch
 
@@ -347,21 +523,13 @@ def cpu_baseline(cfg, q, k, v, router, inter, budget_s):
     t_c = t_c1 * n / sc
     t_d = t_d1 * n / sc
     total = t_a + t_b + t_c + t_d
-    cpu = platform.processor() or platform.machine()
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    cpu = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
+    cpu = _cpu_model()
     return {
-        "value": cfg["B"] * n / total,
+        "value": n / total,
         "unit": "tokens/s",
         "cores": threads,
         "kind": "port",
-        "sample": (f"CPU oracle (oracle/ssa_oracle.c, OpenMP {threads} threads, {cpu}): stage a on "
+        "sample": (f"linear CPU oracle (oracle/ssa_oracle.c, OpenMP {threads} threads, {cpu}): stage a on "
                    f"{sa} of {n} token rows, stage b in full, stages c+d on {sc} of {n} query "
                    f"positions (all {h_kv} kv heads), each scaled to n; outputs checked equal to "
                    f"the GPU's on the sample"),
@@ -418,34 +586,77 @@ def main():
         nb = copy_probe(args.copy_probe_gib)
         print(f"copy probe: {nb} bytes read, {nb} bytes written", file=sys.stderr, flush=True)
 
-    q, k, v, router = make_workload(cfg, args.seed, dev)
-    torch.cuda.synchronize()
-    print(f"workload ready: {args.config} n={cfg['n']}", file=sys.stderr, flush=True)
-    wall, st = time_gpu(cfg, q, k, v, router, args.steps, args.warmup)
+    is_block = "d_model" in cfg
+    blk = None
+    if is_block:
+        blk = make_block(cfg, args.seed, dev)
+        torch.cuda.synchronize()
+        print(f"block ready: {args.config} B={cfg['B']} n={cfg['n']}", file=sys.stderr, flush=True)
+        with torch.no_grad():
+            for _ in range(args.warmup):
+                block_step(blk)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(args.steps):
+                block_step(blk)
+            torch.cuda.synchronize()
+            wall = time.perf_counter() - t0
+            phases = block_stages(blk)
+            q, k, v = blk["layer"].project(blk["norm"](blk["x"]), None, blk["freqs"])
+        router = blk["layer"].router
+        st = {key: phases[key] for key in "abcd"}
+    else:
+        q, k, v, router = make_workload(cfg, args.seed, dev)
+        torch.cuda.synchronize()
+        print(f"workload ready: {args.config} n={cfg['n']}", file=sys.stderr, flush=True)
+        wall, st = time_gpu(cfg, q, k, v, router, args.steps, args.warmup)
     ms_step = 1000.0 * wall / args.steps
-    R, C, heavy_rows, C_r, nrows, inter = stats_sums(q, k, router)
-    alg = algorithmic(cfg, cfg["n"], (R, C_r, heavy_rows))
+    R, C, heavy_rows, C_r, nrows, distinct, inter = stats_sums(q, k, router)
+    alg = algorithmic(cfg, cfg["n"], (R, C, C_r, heavy_rows), distinct)
     tokens = cfg["B"] * cfg["n"]
-    t_d = st["d"] / 1000.0
-    d_gbs = alg["d_bytes"] / t_d / 1e9
+    t = {key: st[key] / 1000.0 for key in "abcd"}
+    d_comp_gbs = alg["d_bytes_compulsory"] / t["d"] / 1e9
     # Counter-measured traffic applies only to the profiled workload shape.
     traffic, traffic_src = (measured_traffic(args.config) if args.n is None and args.num_codebook is None and args.seed == 0
                             else (None, None))
     stages = {
         "a": {"ms": st["a"], "gflop": alg["a_flops"] / 1e9,
-              "tflops": alg["a_flops"] / (st["a"] / 1000) / 1e12,
-              "frac_mfma_bf16": alg["a_flops"] / (st["a"] / 1000) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
-              "frac_fp32": alg["a_flops"] / (st["a"] / 1000) / 1e12 / FP32_PEAK_TFLOPS},
+              "gflop_fp32_projection": alg["a_flops_projection"] / 1e9,
+              "tflops": alg["a_flops"] / t["a"] / 1e12,
+              "frac_mfma_bf16": alg["a_flops"] / t["a"] / 1e12 / MFMA_BF16_PEAK_TFLOPS},
         "b": {"ms": st["b"], "gb": alg["b_bytes"] / 1e9,
-              "frac_hbm": alg["b_bytes"] / (st["b"] / 1000) / 1e9 / HBM_PEAK_GBS},
-        "c": {"ms": st["c"], "gb": alg["c_bytes"] / 1e9,
-              "frac_hbm": alg["c_bytes"] / (st["c"] / 1000) / 1e9 / HBM_PEAK_GBS,
-              "order": "index (same set as by score)",
+              "frac_hbm": alg["b_bytes"] / t["b"] / 1e9 / HBM_PEAK_GBS},
+        "c": {"ms": st["c"], "order": "index (same set as by score)",
+              "gb_read": alg["c_bytes"] / 1e9,
+              "frac_hbm_read": alg["c_bytes"] / t["c"] / 1e9 / HBM_PEAK_GBS,
+              "gb_scope_formula": alg["c_bytes_survey"] / 1e9,
+              "gbs_scope_formula": alg["c_bytes_survey"] / t["c"] / 1e9,
               "ms_sorted_by_score": time_sorted_select(q, k, router),
               "postings_read": R, "candidates": C, "rows": nrows,
               "rows_rescored": heavy_rows, "candidates_rescored": C_r},
-        "d": {"ms": st["d"], "gb": alg["d_bytes"] / 1e9, "frac_hbm": d_gbs / HBM_PEAK_GBS},
+        "d": {"ms": st["d"], "gb_compulsory": alg["d_bytes_compulsory"] / 1e9,
+              "frac_hbm_compulsory": d_comp_gbs / HBM_PEAK_GBS,
+              "distinct_kv_rows": distinct,
+              "gb_logical_gather": alg["d_bytes_logical"] / 1e9,
+              "gbs_logical_gather": alg["d_bytes_logical"] / t["d"] / 1e9,
+              "tflops": alg["d_flops"] / t["d"] / 1e12},
     }
+    workload = (f"{args.config}: RMSNorm + SSAAttention forward (projections, RoPE, stages a-d, "
+                f"o_proj), causal routing" if is_block else
+                f"{args.config}: SSA forward (stages a-d), causal")
+    if is_block:
+        data = "synthetic: hidden states ~ N(0,1); layer, RMSNorm and router default init from a fixed seed"
+    else:
+        data = ("synthetic: seeded Gaussian-mixture Q/K (%d clusters, sigma %.1f, RoPE theta %g), "
+                "V ~ N(0,1); router default init from a fixed seed" %
+                (cfg["clusters"], cfg["sigma"], cfg["theta"]))
+    config = {"workload": workload, "batch": cfg["B"], "seq_len": cfg["n"], "h_q": cfg["h_q"],
+              "h_kv": cfg["h_kv"], "head_dim": cfg["d"], "route_dim": cfg["d_s"],
+              "num_codebook": cfg["n_c"], "codes_per_query": cfg["a"], "codes_per_key": cfg["b"],
+              "top_k": cfg["k"]}
+    if is_block:
+        config["d_model"] = cfg["d_model"]
+        stages["block_phases_ms"] = phases
     line = {
         "metric": METRIC,
         "value": tokens / (wall / args.steps),
@@ -458,18 +669,19 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": cfg["dtype"],
-        "data": ("synthetic: seeded Gaussian-mixture Q/K (%d clusters, sigma %.1f, RoPE theta %g), "
-                 "V ~ N(0,1); router default init from a fixed seed" %
-                 (cfg["clusters"], cfg["sigma"], cfg["theta"])),
-        "config": {"workload": f"{args.config}: SSA forward (stages a-d), causal",
-                   "batch": cfg["B"], "seq_len": cfg["n"], "h_q": cfg["h_q"], "h_kv": cfg["h_kv"],
-                   "head_dim": cfg["d"], "route_dim": cfg["d_s"], "num_codebook": cfg["n_c"],
-                   "codes_per_query": cfg["a"], "codes_per_key": cfg["b"], "top_k": cfg["k"]},
+        "data": data,
+        "config": config,
         "roofline": {"bound": "hbm", "kernel": "sparse_attention_mfma_kernel (stage d)",
-                     "achieved": d_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": d_gbs / HBM_PEAK_GBS, "traffic": traffic,
+                     "achieved": d_comp_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": d_comp_gbs / HBM_PEAK_GBS, "traffic": traffic,
+                     "traffic_counter": "FETCH_SIZE + WRITE_SIZE (bytes between L2 and the fabric; "
+                                        "the 256 MB Infinity Cache serves part of them)",
                      "traffic_source": traffic_src,
-                     "algorithmic_bytes": alg["d_bytes"]},
+                     "algorithmic_bytes": alg["d_bytes_compulsory"],
+                     "algorithmic_basis": "compulsory: q and output once, int32 indices once, each "
+                                          "distinct K/V row once",
+                     "logical_gather_bytes": alg["d_bytes_logical"],
+                     "logical_gather_gbs": alg["d_bytes_logical"] / t["d"] / 1e9},
         "stages": stages,
     }
     if args.backward:
@@ -479,7 +691,10 @@ def main():
     if args.block_sparse > 0:
         line["block_sparse"] = time_blocks(cfg, q, k, v, inter, args.block_sparse)
     if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline(cfg, q, k, v, router, inter, args.cpu_seconds)
+        print("cpu baseline: reference algorithm", file=sys.stderr, flush=True)
+        line["cpu_baseline"] = cpu_reference(cfg, q, k, v, router, args.cpu_seconds, blk)
+        print("cpu baseline: linear oracle", file=sys.stderr, flush=True)
+        line["cpu_oracle"] = cpu_oracle(cfg, q, k, v, router, inter, args.cpu_seconds)
     if args.sweep:
         sweep = {}
         for n_ in [int(x) for x in args.sweep.split(",")]:
@@ -498,10 +713,10 @@ def main():
         if len(ns) >= 3:  # least-squares t = alpha * n + beta and its R^2
             mn, mt = sum(ns) / len(ns), sum(ts) / len(ts)
             sxx = sum((x - mn) ** 2 for x in ns)
-            alpha = sum((x - mn) * (t - mt) for x, t in zip(ns, ts)) / sxx
+            alpha = sum((x - mn) * (t_ - mt) for x, t_ in zip(ns, ts)) / sxx
             beta = mt - alpha * mn
-            ss_res = sum((t - (alpha * x + beta)) ** 2 for x, t in zip(ns, ts))
-            ss_tot = sum((t - mt) ** 2 for t in ts)
+            ss_res = sum((t_ - (alpha * x + beta)) ** 2 for x, t_ in zip(ns, ts))
+            ss_tot = sum((t_ - mt) ** 2 for t_ in ts)
             sweep["fit"] = {"ms_per_token": alpha, "ms_offset": beta,
                             "r2": 1.0 - ss_res / ss_tot if ss_tot > 0 else 1.0}
         sweep["num_codebook_policy"] = args.sweep_nc

@@ -56,6 +56,34 @@ int ssa_version(void);
 const char* ssa_status_str(int status);
 const char* ssa_last_error(void);
 
+/* rotary-embedding angle rows for ssa_rope */
+#define SSA_ROPE_BY_POSITION 0 /* table row = token position (Hugging Face Qwen2)        */
+#define SSA_ROPE_BY_HEAD 1     /* table row = head index (SSAAttention's apply_rope call) */
+
+/* ---- layer prologue: rotary embedding ----------------------------------- */
+
+/* Rotary embedding of q or k rows: features j < rot rotate in pairs
+ * (j, j + rot/2), out = x * cos + rotate_half(x) * sin, and features j >= rot
+ * pass through.  Replaces apply_rope (ssa/utils.py:7-41) as SSAAttention calls
+ * it on [n, heads, d] per batch element (ssa/ssa_layer.py:115-120: rot = d/2,
+ * angle row = head index, table freqs[:, :d/2]) and Hugging Face's
+ * apply_rotary_pos_emb in the Qwen2 path (training/train_qwen.py:134-135:
+ * rot = d, angle row = position, the model's cos/sin tables).
+ *   x   [batch][n][h][d] strides (x_sb, x_sn, x_sh), type dtype
+ *   cos_table, sin_table  [batch or 1][table_rows][>= rot], row stride t_sr,
+ *       batch stride t_sb (0 = one table for every batch element), type table_dtype
+ *   angle_axis  SSA_ROPE_BY_POSITION (row = token i) or SSA_ROPE_BY_HEAD (row = head)
+ *   inverse != 0 applies the transpose of the rotation (the backward)
+ *   out [batch][n][h][d] strides (o_sb, o_sn, o_sh), type out_dtype; out == x
+ *       (same strides and type) rotates in place and leaves features >= rot alone.
+ * Arithmetic matches torch's ops: bf16 x with bf16 tables rounds every product
+ * and the sum to bf16; otherwise fp32 intermediates, the result rounded once. */
+int ssa_rope(const void* x, int dtype, int64_t batch, int64_t n, int h, int d, int64_t x_sb,
+             int64_t x_sn, int64_t x_sh, const void* cos_table, const void* sin_table,
+             int table_dtype, int64_t t_sb, int64_t t_sr, int64_t table_rows, int rot,
+             int angle_axis, int inverse, void* out, int out_dtype, int64_t o_sb, int64_t o_sn,
+             int64_t o_sh, void* stream);
+
 /* ---- stage (a): routing ------------------------------------------------- */
 
 /* Routing vectors: out[b][h][i] = normalize(mean_{gg<group}(x[b][i][h*group+gg] . w^T)).
@@ -152,6 +180,17 @@ int ssa_query_order(const int32_t* q_codes, int64_t batch, int64_t n, int h_kv, 
  *          written and an entry outside [0, n) is skipped.
  * Limits: top_k <= 4096, g = h_q/h_kv <= 16, d <= 256 (d % 8 == 0), n < 2^31. */
 size_t ssa_select_workspace_bytes(int64_t batch, int64_t n, int h_kv, int top_k);
+
+/* Where ssa_select places its regions inside a workspace of workspace_bytes
+ * (no reference counterpart; for tests and for callers that size or share
+ * workspaces).  layout[10] receives byte offsets of the counter block, the
+ * exact-pass row list, the screened-row entries, the per-row error bounds,
+ * the candidate lists and their approximate scores, then the entries per
+ * shard, the list entries per shard (0 = no screen), the shard count and the
+ * counter block's size.  Nothing is launched or dereferenced. */
+int ssa_select_workspace_layout(int64_t batch, int64_t n, int h_kv, size_t workspace_bytes,
+                                int screen, int64_t* layout);
+
 int ssa_select(const void* q, const void* k, int dtype, int64_t batch, int64_t n, int h_q,
                int h_kv, int d, int64_t q_sb, int64_t q_sn, int64_t q_sh, int64_t k_sb,
                int64_t k_sn, int64_t k_sh, const int32_t* q_codes, int a, const int32_t* offsets,

@@ -113,6 +113,58 @@ def score_div_for(d: int) -> float:
     return float(np.float32(d ** 0.5))
 
 
+def bf16_round(a) -> np.ndarray:
+    """float32 values rounded to the nearest bf16 (ties to even), kept as float32."""
+    a = np.asarray(a, dtype=np.float32)
+    u = a.view(np.uint32).astype(np.uint64)
+    u = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    out = (u & 0xFFFFFFFF).astype(np.uint32).view(np.float32).copy()
+    out[np.isnan(a)] = np.nan
+    return out
+
+
+def rope(x, cos, sin, rot: int, by_head: bool, round_bf16: bool = False,
+         inverse: bool = False) -> np.ndarray:
+    """Rotary embedding in float32 numpy (the arithmetic ssa_rope must match bit for bit).
+
+    Follows apply_rope / _rotate_half (ssa/utils.py:7-48) as SSAAttention calls it
+    on [n, heads, d] (ssa/ssa_layer.py:115-117: rot = d/2, angle row = head, only
+    x[..., :d/2] rotates) and Hugging Face's apply_rotary_pos_emb in the Qwen2
+    path (training/train_qwen.py:134-135: rot = d, angle row = position):
+    y = x * cos + rotate_half(x) * sin over features j < rot, pairs (j, j + rot/2),
+    features >= rot unchanged.  Three rounded float32 ops, no fusion; with
+    ``round_bf16`` (bf16 x and bf16 tables in torch) each op's result rounds to
+    bf16.  ``inverse`` is the transpose of the rotation.
+
+    x: [B, n, h, d]; cos/sin: [rows, w] or [B or 1, rows, w] with w >= rot."""
+    x = np.asarray(x, dtype=np.float32)
+    cos = np.asarray(cos, dtype=np.float32)
+    sin = np.asarray(sin, dtype=np.float32)
+    if cos.ndim == 2:
+        cos, sin = cos[None], sin[None]
+    B, n, h, d = x.shape
+    r = rot // 2
+    rows = h if by_head else n
+    c = cos[:, :rows, :rot]
+    s = sin[:, :rows, :rot]
+    # broadcast the table rows onto [B, n, h, rot]
+    c = c[:, None, :, :] if by_head else c[:, :, None, :]
+    s = s[:, None, :, :] if by_head else s[:, :, None, :]
+    rnd = bf16_round if round_bf16 else (lambda v: v)
+    x1, x2 = x[..., :r], x[..., r:rot]
+    c1, c2, s1, s2 = c[..., :r], c[..., r:], s[..., :r], s[..., r:]
+    if not inverse:
+        y1 = rnd(rnd(x1 * c1) + rnd((-x2) * s1))
+        y2 = rnd(rnd(x2 * c2) + rnd(x1 * s2))
+    else:
+        y1 = rnd(rnd(x1 * c1) + rnd(x2 * s2))
+        y2 = rnd(rnd(x2 * c2) + rnd((-x1) * s1))
+    out = x.copy()
+    out[..., :r] = y1
+    out[..., r:rot] = y2
+    return out
+
+
 # ----------------------------------------------------------------- C layer
 
 def normalize(x) -> np.ndarray:

@@ -31,6 +31,8 @@ INDEX_I64 = 1
 MASK_NONE = 0
 MASK_CAUSAL = 1
 MASK_DENSE = 2
+ROPE_BY_POSITION = 0
+ROPE_BY_HEAD = 1
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -43,6 +45,9 @@ SIGNATURES = {
     "ssa_version": (_int, []),
     "ssa_status_str": (ctypes.c_char_p, [_int]),
     "ssa_last_error": (ctypes.c_char_p, []),
+    "ssa_rope": (
+        _int, [_vp, _int, _i64, _i64, _int, _int, _i64, _i64, _i64, _vp, _vp, _int, _i64, _i64,
+               _i64, _int, _int, _int, _vp, _int, _i64, _i64, _i64, _vp]),
     "ssa_route_vectors": (
         _int, [_vp, _int, _i64, _i64, _int, _int, _int, _i64, _i64, _i64, _vp, _int, _vp, _vp]),
     "ssa_normalize_rows": (_int, [_vp, _i64, _int, _vp, _vp]),
@@ -64,6 +69,7 @@ SIGNATURES = {
          _vp, _int, _vp, _vp, _int, _int, _int, _int, _vp, _i64, _i64, _flt, _int, _vp, _vp,
          _int, _vp, _vp, _sz, _vp]),
     "ssa_select_workspace_bytes": (_sz, [_i64, _i64, _int, _int]),
+    "ssa_select_workspace_layout": (_int, [_i64, _i64, _int, _sz, _int, _vp]),
     "ssa_select_block": (
         _int,
         [_vp, _vp, _int, _i64, _i64, _i64, _i64, _int, _int, _int, _i64, _i64, _i64, _i64, _i64,

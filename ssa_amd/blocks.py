@@ -47,7 +47,22 @@ def block_sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     kb, _ = _batched(k, 3)
     vb, _ = _batched(v, 3)
     bb, _ = _batched(block_indices, 3)
+    out_dtype = qb.dtype
+    if qb.dtype == torch.float16:  # fp16 widens exactly to fp32 (the kernels take f32 / bf16)
+        qb, kb, vb = qb.float(), kb.float(), vb.float()
+    qb, kb, vb = (t if t.stride(-1) == 1 else t.contiguous() for t in (qb, kb, vb))
     d = qb.shape[-1]
     scale_div = (d ** 0.5) if scale is None else 1.0 / scale
     out = kernels.block_sparse_attention(qb, kb, vb, bb, block_size, scale_div)
+    if out.dtype != out_dtype:
+        out = out.to(out_dtype)
     return out[0] if single else out
+
+
+def ssa_triton_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                         block_indices: torch.Tensor, block_size: int = 64,
+                         scale: Optional[float] = None) -> torch.Tensor:
+    """The reference launcher's name and signature (ssa/triton_kernel.py:141-148):
+    the same computation as block_sparse_attention (HIP kernels, no Triton), for
+    callers written against the reference."""
+    return block_sparse_attention(q, k, v, block_indices, block_size, scale)

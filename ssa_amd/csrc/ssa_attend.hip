@@ -109,13 +109,6 @@ __device__ __forceinline__ AttRow att_row(const AttParams& p, int64_t lrow) {
   return r;
 }
 
-__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x007FFFFFu)) return static_cast<uint16_t>((u >> 16) | 0x40u);
-  u += 0x7FFFu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
-}
-
 __device__ __forceinline__ float max16(float x) {
   x = fmaxf(x, __shfl_xor(x, 8, 16));
   x = fmaxf(x, __shfl_xor(x, 4, 16));

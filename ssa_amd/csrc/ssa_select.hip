@@ -1261,6 +1261,31 @@ int dispatch_select(const SelParams& p, int64_t rows, size_t smem, void* ws, siz
 
 using namespace ssa;
 
+extern "C" int ssa_select_workspace_layout(int64_t batch, int64_t n, int h_kv, size_t workspace_bytes,
+                                           int screen, int64_t* layout) {
+  if (batch < 0 || n < 0 || h_kv <= 0 || !layout)
+    return fail(SSA_ERR_INVALID_ARGUMENT, "select layout: bad arguments");
+  const int64_t rows = batch * h_kv * n;
+  const size_t min_bytes = sel_ws_fixed(rows) + 256;  // ssa_select_workspace_bytes(.., 0)
+  if (workspace_bytes < min_bytes)
+    return fail(SSA_ERR_WORKSPACE, "select layout: workspace %zu < %zu bytes", workspace_bytes,
+                min_bytes);
+  char* base = reinterpret_cast<char*>(uintptr_t(1) << 20);  // never dereferenced
+  const SelWs w = carve_sel_ws(base, workspace_bytes, rows, screen != 0);
+  auto off = [&](const void* ptr) { return static_cast<int64_t>(static_cast<const char*>(ptr) - base); };
+  layout[0] = off(w.ctr);
+  layout[1] = off(w.exact);
+  layout[2] = off(w.scr);
+  layout[3] = off(w.emax);
+  layout[4] = off(w.cand);
+  layout[5] = off(w.approx);
+  layout[6] = w.shard_rows;
+  layout[7] = w.cap;
+  layout[8] = kShards;
+  layout[9] = static_cast<int64_t>(kSelCtrBytes);
+  return SSA_OK;
+}
+
 extern "C" size_t ssa_select_workspace_bytes(int64_t batch, int64_t n, int h_kv, int top_k) {
   if (batch < 0 || n < 0 || h_kv <= 0 || top_k < 0) return 0;
   const int64_t rows = batch * h_kv * n;

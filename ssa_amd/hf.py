@@ -21,6 +21,7 @@ import torch
 
 from .attention import dense_attention, sparse_exact_attention
 from .router import CodebookRouter
+from .ssa_layer import rope_rows
 from .utils import build_causal_mask
 
 
@@ -77,17 +78,22 @@ def replace_attention_forward(model=None):
     causal attention, as in the reference.  A key/value cache longer than the
     query block is not supported (the reference's routing needs n_q == n_k too)."""
     from transformers.cache_utils import Cache
-    from transformers.models.qwen2.modeling_qwen2 import Qwen2Attention, apply_rotary_pos_emb
+    from transformers.models.qwen2.modeling_qwen2 import Qwen2Attention
 
     def ssa_forward(self, hidden_states, position_embeddings, attention_mask=None,
                     past_key_values=None, **kwargs):
         input_shape = hidden_states.shape[:-1]
         hidden_shape = (*input_shape, -1, self.head_dim)
-        q = self.q_proj(hidden_states).view(hidden_shape).transpose(1, 2)
-        k = self.k_proj(hidden_states).view(hidden_shape).transpose(1, 2)
-        v = self.v_proj(hidden_states).view(hidden_shape).transpose(1, 2)
         cos, sin = position_embeddings
-        q, k = apply_rotary_pos_emb(q, k, cos, sin)
+        # apply_rotary_pos_emb (training/train_qwen.py:134-135) on the HIP kernel:
+        # positional angles, every feature rotated, the same rounded ops; the
+        # [B, n, h, d] projections are read where they lie and the results are
+        # handed on as [B, h, n, d] views
+        q = rope_rows(self.q_proj(hidden_states).view(hidden_shape), cos, sin, self.head_dim,
+                      by_head=False).transpose(1, 2)
+        k = rope_rows(self.k_proj(hidden_states).view(hidden_shape), cos, sin, self.head_dim,
+                      by_head=False).transpose(1, 2)
+        v = self.v_proj(hidden_states).view(hidden_shape).transpose(1, 2)
         if past_key_values is not None and isinstance(past_key_values, Cache):
             k, v = past_key_values.update(k, v, self.layer_idx)
         if k.shape[-2] != q.shape[-2]:

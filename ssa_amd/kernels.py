@@ -29,6 +29,41 @@ def _f32c(t: torch.Tensor) -> torch.Tensor:
     return t.detach().to(torch.float32).contiguous()
 
 
+def rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, rot: int, by_head: bool,
+         inverse: bool = False, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Rotary embedding of ``x`` [B, n, h, d] (ssa_rope): features j < rot rotate in
+    pairs (j, j + rot/2) as ``x * cos + rotate_half(x) * sin``; the rest pass through.
+
+    ``cos``/``sin`` are ``[rows, >= rot]`` (one table) or ``[B, rows, >= rot]``
+    with a contiguous last dimension; the angle row is the head index
+    (``by_head``, SSAAttention's apply_rope call) or the token position (Hugging
+    Face).  ``inverse`` applies the transpose (the gradient).  ``out`` defaults
+    to a new contiguous tensor of x's dtype; ``out is x`` rotates in place."""
+    _check_rows(x, "x")
+    _lib.require_device(x, cos, sin)
+    B, n, h, d = x.shape
+    if cos.shape != sin.shape or cos.dtype != sin.dtype:
+        raise ValueError("cos and sin tables must have the same shape and dtype")
+    if cos.stride(-1) != 1 or sin.stride(-1) != 1 or cos.stride() != sin.stride():
+        cos, sin = cos.contiguous(), sin.contiguous()
+    if cos.dim() == 2:
+        t_sb, t_sr, rows = 0, cos.stride(0), cos.shape[0]
+    elif cos.dim() == 3 and cos.shape[0] in (1, B):
+        t_sb = cos.stride(0) if cos.shape[0] == B else 0
+        t_sr, rows = cos.stride(1), cos.shape[1]
+    else:
+        raise ValueError(f"rope tables must be [rows, w] or [B, rows, w], got {tuple(cos.shape)}")
+    if cos.shape[-1] < rot:
+        raise ValueError(f"rope tables are {cos.shape[-1]} wide, rot={rot} needs that many")
+    if out is None:
+        out = torch.empty((B, n, h, d), device=x.device, dtype=x.dtype)
+    call("ssa_rope", ptr(x), _lib.elem_dtype(x), B, n, h, d, x.stride(0), x.stride(1), x.stride(2),
+         ptr(cos), ptr(sin), _lib.elem_dtype(cos), t_sb, t_sr, rows, int(rot),
+         _lib.ROPE_BY_HEAD if by_head else _lib.ROPE_BY_POSITION, int(bool(inverse)),
+         ptr(out), _lib.elem_dtype(out), out.stride(0), out.stride(1), out.stride(2), stream_of(x))
+    return out
+
+
 def route_vectors(x: torch.Tensor, w: torch.Tensor, group: int) -> torch.Tensor:
     """normalize(mean_g(x . w^T)) -> float32 [B, heads/group, n, d_s] (ssa/router.py:102-117)."""
     _check_rows(x, "x")

@@ -12,43 +12,72 @@ from typing import Optional
 import torch
 import torch.nn as nn
 
+from . import kernels
 from .attention import dense_attention, sparse_exact_attention
 from .router import CodebookRouter
 from .utils import build_causal_mask
 
 
-def _rope_batched(x: torch.Tensor, ang: torch.Tensor) -> torch.Tensor:
-    """apply_rope (ssa/utils.py:7-41) on x [B, n, h, d] with per-batch angle rows.
+class _Rope(torch.autograd.Function):
+    """ssa_rope with its transpose as the backward (rotation by the negative
+    angle, the same three rounded ops torch's autograd of the op sequence runs)."""
 
-    ``ang`` is ``[rows, rot]`` (shared) or ``[B, rows, rot]``.  As in the
-    reference, the angle index runs over x's second-to-last axis (the heads
-    when x is [n, h, d]) and only the first d/2 features rotate.  The result
-    keeps x's dtype.
-    """
-    h, d = x.shape[-2], x.shape[-1]
-    half = d // 2
+    @staticmethod
+    def forward(ctx, x, cos, sin, rot, by_head):
+        ctx.save_for_backward(cos, sin)
+        ctx.rot, ctx.by_head = rot, by_head
+        return kernels.rope(x, cos, sin, rot, by_head)
+
+    @staticmethod
+    def backward(ctx, grad):
+        cos, sin = ctx.saved_tensors
+        grad = grad if grad.stride(-1) == 1 else grad.contiguous()
+        return kernels.rope(grad, cos, sin, ctx.rot, ctx.by_head, inverse=True), None, None, None, None
+
+
+def rope_rows(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, rot: int,
+              by_head: bool) -> torch.Tensor:
+    """Rotary embedding of x [B, n, h, d] on the HIP kernel (ssa_rope), differentiable
+    in x; the result keeps x's dtype."""
+    if torch.is_grad_enabled() and x.requires_grad:
+        return _Rope.apply(x, cos, sin, rot, by_head)
+    return kernels.rope(x, cos, sin, rot, by_head)
+
+
+def head_rope_tables(freqs: torch.Tensor, n: int, heads: int, head_dim: int,
+                     position_ids: Optional[torch.Tensor] = None):
+    """cos/sin tables of the reference layer's apply_rope call (ssa/ssa_layer.py:
+    106-117 with ssa/utils.py:19-27): per batch element the angle rows are
+    freqs[position_ids[b]] (or freqs[:n]) and, because apply_rope sees an
+    [n, heads, d] tensor, row j is used for head j; only the first head_dim/2
+    features rotate.  Returns ([B or 1, heads, d/2] cos, sin)."""
+    half = head_dim // 2
+    ang = freqs[position_ids] if position_ids is not None else freqs[:n]
+    if ang.shape[-2] < heads:
+        raise ValueError(f"apply_rope indexes the angle table by head: {heads} heads need "
+                         f"{heads} angle rows, the table has {ang.shape[-2]}")
+    if ang.shape[-1] < half:
+        raise ValueError(f"freqs must be at least head_dim/2 = {half} wide, got {ang.shape[-1]}")
+    ang = ang[..., :heads, :half]
+    if ang.dtype not in (torch.float32, torch.bfloat16):
+        ang = ang.float()
     if ang.dim() == 2:
-        ang = ang[:h, :half].unsqueeze(0)
-    else:
-        ang = ang[:, :h, :half]
-    cos = ang.cos().unsqueeze(1)  # [B or 1, 1, h, half]
-    sin = ang.sin().unsqueeze(1)
-    x_rot, x_pass = x[..., :half], x[..., half:]
-    cut = half // 2
-    rot_half = torch.cat([-x_rot[..., cut:], x_rot[..., :cut]], dim=-1)
-    out = torch.cat([x_rot * cos + rot_half * sin, x_pass.to(torch.result_type(x_rot, cos))], dim=-1)
-    return out.to(x.dtype)
+        ang = ang.unsqueeze(0)
+    return ang.cos().contiguous(), ang.sin().contiguous()
 
 
 class SSAAttention(nn.Module):
     """Sub-quadratic Selective Attention layer (ssa/ssa_layer.py:17-66).
 
-    Extension: ``causal_attention`` (default True) makes stage 3 ignore
-    selected indices above the query position.  Every selected candidate is
-    causal already; the flag only concerns the filler indices of rows with
-    fewer than top_k candidates, which the reference attends unmasked
-    (its choice of them is unspecified).  With it, top_k = n reproduces causal
-    dense attention exactly.
+    Extension: ``causal_attention`` (keyword, default False) makes stage 3
+    ignore selected indices above the query position.  Every selected
+    candidate is causal already; the flag only concerns the filler indices of
+    rows with fewer than top_k candidates.  The default attends them unmasked,
+    as the reference does (ssa/ssa_layer.py:129-130 passes the router's indices
+    to sparse_exact_attention, which applies no mask); the filler keys are the
+    lowest non-candidate indices, so rows i < top_k can attend keys past i.
+    With ``causal_attention=True``, top_k = n reproduces causal dense attention
+    exactly.
     """
 
     def __init__(
@@ -63,7 +92,7 @@ class SSAAttention(nn.Module):
         codes_per_query: int = 8,
         top_k: int = 64,
         bias: bool = False,
-        causal_attention: bool = True,
+        causal_attention: bool = False,
     ):
         super().__init__()
         self.hidden_size = hidden_size
@@ -96,9 +125,9 @@ class SSAAttention(nn.Module):
         k = self.k_proj(hidden_states).view(B, n, self.num_kv_heads, self.head_dim)
         v = self.v_proj(hidden_states).view(B, n, self.num_kv_heads, self.head_dim)
         if freqs is not None:
-            ang = freqs[position_ids] if position_ids is not None else freqs[:n]
-            q = _rope_batched(q, ang)
-            k = _rope_batched(k, ang)
+            cos, sin = head_rope_tables(freqs, n, self.num_q_heads, self.head_dim, position_ids)
+            q = rope_rows(q, cos, sin, self.head_dim // 2, by_head=True)
+            k = rope_rows(k, cos, sin, self.head_dim // 2, by_head=True)
         return q, k, v
 
     def forward(

@@ -57,7 +57,7 @@ def L():
 
 def test_header_parses_every_entry_point():
     decls = _declarations()
-    assert len(decls) == 21
+    assert len(decls) == len(_lib.SIGNATURES) >= 22
     assert set(decls) == set(_lib.SIGNATURES)
 
 
@@ -80,6 +80,36 @@ def test_status_strings(L):
 FAKE = ctypes.c_void_p(1 << 20)       # non-null, 16-byte aligned, never dereferenced
 MISALIGNED = ctypes.c_void_p((1 << 20) + 8)
 NULL = None
+
+
+def _rope(L, **kw):
+    a = dict(x=FAKE, dtype=_lib.DTYPE_BF16, batch=1, n=64, h=8, d=128, x_sb=64 * 8 * 128,
+             x_sn=8 * 128, x_sh=128, cos=FAKE, sin=FAKE, table_dtype=_lib.DTYPE_F32, t_sb=0,
+             t_sr=64, table_rows=64, rot=64, angle_axis=_lib.ROPE_BY_HEAD, inverse=0, out=FAKE,
+             out_dtype=_lib.DTYPE_BF16, o_sb=64 * 8 * 128, o_sn=8 * 128, o_sh=128, stream=NULL)
+    a.update(kw)
+    st = L.ssa_rope(*a.values())
+    return st, (L.ssa_last_error() or b"").decode()
+
+
+@pytest.mark.parametrize("kw,status,text", [
+    (dict(dtype=3), _lib.SSA_ERR_UNSUPPORTED, "types"),
+    (dict(rot=63), _lib.SSA_ERR_INVALID_ARGUMENT, "rot"),
+    (dict(rot=130), _lib.SSA_ERR_INVALID_ARGUMENT, "rot"),
+    (dict(angle_axis=2), _lib.SSA_ERR_INVALID_ARGUMENT, "angle_axis"),
+    (dict(table_rows=7), _lib.SSA_ERR_INVALID_ARGUMENT, "rows"),
+    (dict(angle_axis=_lib.ROPE_BY_POSITION, table_rows=63), _lib.SSA_ERR_INVALID_ARGUMENT, "rows"),
+    (dict(cos=NULL), _lib.SSA_ERR_INVALID_ARGUMENT, "null"),
+    (dict(out=FAKE, out_dtype=_lib.DTYPE_F32), _lib.SSA_ERR_INVALID_ARGUMENT, "in place"),
+])
+def test_rope_rejects(L, kw, status, text):
+    st, msg = _rope(L, **kw)
+    assert st == status, msg
+    assert text in msg
+
+
+def test_rope_empty_is_noop(L):
+    assert _rope(L, n=0, x=NULL, out=NULL, cos=NULL, sin=NULL)[0] == _lib.SSA_OK
 
 
 def _select(L, **kw):
@@ -244,3 +274,41 @@ def test_block_entry_points_reject_rows_past_the_keys(L):
                             null, null, 16, 4, 8, 1, null, 0, 0, 8.0, 0, null, null, 0, null, null, 0,
                             null)
     assert st == _lib.SSA_ERR_INVALID_ARGUMENT
+
+
+@pytest.mark.parametrize("batch,n,h_kv,top_k", [
+    (1, 32768, 8, 512), (1, 131072, 2, 1024), (2, 300, 2, 32), (4, 8192, 8, 512), (1, 1, 1, 1),
+    (3, 1000, 3, 4096), (1, 64 * 5 + 1, 1, 7), (2, 70000, 2, 512),
+])
+def test_select_workspace_regions_do_not_overlap(L, batch, n, h_kv, top_k):
+    """The select workspace's regions (carve_sel_ws) are disjoint, in order, as
+    large as the kernels index them, and inside the workspace: the counter
+    block holds 16 + 4 ints per shard, the exact list one int per row, the
+    screened-row entries 3 ints and the error bounds one float per shard slot,
+    the candidate lists and scores cap entries per shard.  Swept over shapes and
+    workspace sizes from the minimum to past the recommended size (a too-small
+    counter block once let a garbage counter drive an out-of-bounds write)."""
+    rows = batch * n * h_kv
+    lo = L.ssa_select_workspace_bytes(batch, n, h_kv, 0)
+    hi = L.ssa_select_workspace_bytes(batch, n, h_kv, top_k)
+    assert hi >= lo > 0
+    for bytes_ in sorted({lo, lo + 255, (lo + hi) // 2, hi, 2 * hi + 77}):
+        for screen in (0, 1):
+            lay = (ctypes.c_int64 * 10)()
+            assert L.ssa_select_workspace_layout(batch, n, h_kv, bytes_, screen, lay) == _lib.SSA_OK
+            ctr, exact, scr, emax, cand, approx, shard_rows, cap, shards, ctr_bytes = list(lay)
+            assert shard_rows * shards >= rows
+            assert 4 * (16 + 4 * shards) <= ctr_bytes
+            ends = [(ctr, ctr + ctr_bytes), (exact, exact + 4 * rows),
+                    (scr, scr + 12 * shards * shard_rows), (emax, emax + 4 * shards * shard_rows),
+                    (cand, cand + 4 * shards * cap), (approx, approx + 4 * shards * cap)]
+            assert ctr == 0
+            for (s0, e0), (s1, _) in zip(ends, ends[1:]):
+                assert s0 <= e0 <= s1, (ends, bytes_)
+            assert ends[-1][1] <= bytes_
+            assert all(o % 256 == 0 for o in (exact, scr, emax, cand, approx))
+            assert cap % 32 == 0 and cap >= 0
+            if not screen or bytes_ == lo:
+                assert cap == 0
+    assert L.ssa_select_workspace_layout(batch, n, h_kv, lo - 1, 1, (ctypes.c_int64 * 10)()) \
+        == _lib.SSA_ERR_WORKSPACE

@@ -14,7 +14,7 @@ import torch.nn.functional as F
 import ssa_amd
 from ssa_amd import _lib, kernels
 from ssa_amd.router import CodebookRouter, mask_mode_for
-from ssa_amd.ssa_layer import SSAAttention, ToyTransformerBlock, _rope_batched
+from ssa_amd.ssa_layer import SSAAttention, ToyTransformerBlock, head_rope_tables
 from ssa_amd.utils import (apply_rope, build_causal_mask, expand_kv_for_gqa, precompute_rope_freqs,
                            validate_indices)
 
@@ -165,17 +165,24 @@ def test_apply_rope_closed_form_and_pair_norm():
     assert torch.equal(y[:, 0], x[:, 0]), "angle row 0 is the identity"
 
 
-def test_rope_batched_matches_per_batch_apply_rope():
+def test_head_rope_tables_give_the_reference_layer_rotation():
+    """The layer's host-side tables (head_rope_tables) plus the rotation the kernel
+    applies (oracle.rope, bit-exact with ssa_rope on the GPU) equal the
+    reference's per-batch apply_rope calls (ssa/ssa_layer.py:106-117), with and
+    without position_ids."""
+    import oracle
+
     B, n, h, d = 3, 7, 4, 16
     x = torch.randn(B, n, h, d)
     freqs = precompute_rope_freqs(d, 32, 1e4)
-    ref = torch.stack([apply_rope(x[b], freqs[:n]) for b in range(B)])
-    torch.testing.assert_close(_rope_batched(x, freqs[:n]), ref, rtol=0, atol=0)
-    pos = torch.randint(0, 32, (B, n))
-    ref = torch.stack([apply_rope(x[b], freqs[pos[b]]) for b in range(B)])
-    torch.testing.assert_close(_rope_batched(x, freqs[pos]), ref, rtol=0, atol=0)
-    xb = x.to(torch.bfloat16)
-    assert _rope_batched(xb, freqs[:n]).dtype == torch.bfloat16
+    for pos in (None, torch.randint(0, 32, (B, n))):
+        cos, sin = head_rope_tables(freqs, n, h, d, pos)
+        got = oracle.rope(x.numpy(), cos.numpy(), sin.numpy(), d // 2, by_head=True)
+        fb = [freqs[:n] if pos is None else freqs[pos[b]] for b in range(B)]
+        ref = torch.stack([apply_rope(x[b], fb[b]) for b in range(B)])
+        np.testing.assert_array_equal(got, ref.numpy())
+    with pytest.raises(ValueError, match="angle rows"):
+        head_rope_tables(freqs[:3], 3, h, d)
 
 
 def test_expand_kv_for_gqa():

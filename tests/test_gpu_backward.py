@@ -123,22 +123,29 @@ def test_autograd_through_sparse_exact_attention(dev, orc, dtype):
     _close(vd.grad.float().cpu().numpy(), rv[0], tol, "v.grad")
 
 
-def test_layer_gradient_flow_matches_reference_formula(dev):
+@pytest.mark.parametrize("causal_attention,rope", [(False, False), (False, True), (True, True)])
+def test_layer_gradient_flow_matches_reference_formula(dev, causal_attention, rope):
     """tests/test_integration.py:32-49 of the reference (gradients reach q/k/v/o_proj
     and the input), and the gradients equal those of the reference's op sequence
-    run under float64 autograd on the CPU with the layer's own indices."""
-    from ssa_amd import SSAAttention
+    (apply_rope on [n, h, d], gather, einsum, / scale, softmax, einsum) run under
+    float64 autograd on the CPU with the layer's own indices.  With rope the
+    layer's HIP RoPE kernel and its transpose are on the gradient path."""
+    from ssa_amd import SSAAttention, precompute_rope_freqs
+    from ssa_amd.utils import apply_rope
 
+    print(f"layer gradients causal_attention={causal_attention} rope={rope}", flush=True)
     torch.manual_seed(0)
-    layer = SSAAttention(hidden_size=256, num_q_heads=4, num_kv_heads=1, head_dim=64, route_dim=16,
-                         num_codebook=128, codes_per_key=4, codes_per_query=8, top_k=16)
+    kw = dict(hidden_size=256, num_q_heads=4, num_kv_heads=1, head_dim=64, route_dim=16,
+              num_codebook=128, codes_per_key=4, codes_per_query=8, top_k=16,
+              causal_attention=causal_attention)
+    layer = SSAAttention(**kw)
     x = torch.randn(2, 32, 256)
-    ref_layer = SSAAttention(hidden_size=256, num_q_heads=4, num_kv_heads=1, head_dim=64, route_dim=16,
-                             num_codebook=128, codes_per_key=4, codes_per_query=8, top_k=16)
+    ref_layer = SSAAttention(**kw)
     ref_layer.load_state_dict(layer.state_dict())
     layer = layer.to(dev)
+    freqs = precompute_rope_freqs(64, 32, 1e4) if rope else None
     xd = x.to(dev).requires_grad_()
-    out = layer(xd)
+    out = layer(xd, freqs=freqs.to(dev) if rope else None)
     out.sum().backward()
     for name in ("q_proj", "k_proj", "v_proj", "o_proj"):
         gr = getattr(layer, name).weight.grad
@@ -147,20 +154,27 @@ def test_layer_gradient_flow_matches_reference_formula(dev):
 
     # reference op sequence in float64 on the CPU, same indices as the layer routed
     with torch.no_grad():
-        q, k, _ = layer.project(x.to(dev))
+        q, k, _ = layer.project(x.to(dev), freqs=freqs.to(dev) if rope else None)
         idx = torch.stack([layer.router(q[b], k[b], causal_mask=True) for b in range(2)]).cpu()
     ref_layer = ref_layer.double()
     xr = x.double().requires_grad_()
-    q, k, v = ref_layer.project(xr)
-    B, n, h_q, d = q.shape
+    B, n = 2, 32
+    h_q, d = 4, 64
+    q = ref_layer.q_proj(xr).view(B, n, h_q, d)
+    k = ref_layer.k_proj(xr).view(B, n, 1, d)
+    v = ref_layer.v_proj(xr).view(B, n, 1, d)
     heads = torch.arange(1)[None, :, None]
     outs = []
     for b in range(B):
-        kg, vg = k[b][idx[b], heads], v[b][idx[b], heads]
-        lg = torch.einsum("nhgd,nhkd->nhgk", q[b].view(n, 1, h_q, d), kg) / d ** 0.5
-        # the layer's default causal_attention=True drops selected keys past the query
-        fut = idx[b][:, :, None, :] > torch.arange(n)[:, None, None, None]
-        p = torch.softmax(lg.masked_fill(fut, float("-inf")), dim=-1)
+        qb, kb = q[b], k[b]
+        if rope:  # ssa/ssa_layer.py:115-117: apply_rope on [n, heads, d]
+            qb, kb = apply_rope(qb, freqs.double()), apply_rope(kb, freqs.double())
+        kg, vg = kb[idx[b], heads], v[b][idx[b], heads]
+        lg = torch.einsum("nhgd,nhkd->nhgk", qb.reshape(n, 1, h_q, d), kg) / d ** 0.5
+        if causal_attention:  # drops selected keys past the query
+            fut = idx[b][:, :, None, :] > torch.arange(n)[:, None, None, None]
+            lg = lg.masked_fill(fut, float("-inf"))
+        p = torch.softmax(lg, dim=-1)
         outs.append(torch.einsum("nhgk,nhkd->nhgd", p, vg).reshape(n, h_q * d))
     ref_out = ref_layer.o_proj(torch.stack(outs))
     ref_out.sum().backward()

@@ -99,3 +99,24 @@ def test_router_blocks_pipeline_all_blocks_is_dense(dev, orc):
     got = block_sparse_attention(q.to(dev), k.to(dev), v.to(dev), blocks, bs).cpu().numpy()
     ref = orc.dense_attention(f32(q), f32(k), f32(v), causal=True)
     np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-5)
+
+
+def test_ssa_triton_attention_name_and_fp16(dev, orc):
+    """The reference launcher's name and signature (ssa/triton_kernel.py:141-148)
+    with fp16 inputs (the reference kernel's type), widened exactly to fp32: the
+    output equals the fp32 call rounded to fp16, and the float64 restatement
+    within 1e-3."""
+    from ssa_amd.blocks import block_sparse_attention, ssa_triton_attention
+
+    n, h_q, h_kv, d, bs, nkb = 300, 4, 2, 64, 64, 3
+    q, k, v = (randn((n, h, d), s).to(torch.float16) for h, s in ((h_q, 81), (h_kv, 82), (h_kv, 83)))
+    nb = (n + bs - 1) // bs
+    g = torch.Generator().manual_seed(84)
+    blocks = torch.randint(0, nb, (nb, h_kv, nkb), generator=g)
+    got = ssa_triton_attention(q.to(dev), k.to(dev), v.to(dev), blocks.to(dev), bs)
+    assert got.dtype == torch.float16
+    ref32 = block_sparse_attention(q.float().to(dev), k.float().to(dev), v.float().to(dev),
+                                   blocks.to(dev), bs)
+    assert torch.equal(got, ref32.to(torch.float16))
+    ref = orc.block_sparse_attention64(f32(q), f32(k), f32(v), blocks.numpy(), bs)
+    np.testing.assert_allclose(got.float().cpu().numpy(), ref, rtol=1e-3, atol=1e-3)

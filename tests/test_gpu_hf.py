@@ -1,12 +1,13 @@
 """GPU checks of the Qwen2 adapter (ssa_amd.hf) on a small random-init Qwen2.
 
-The patched forward (strided [B, n, h, d] views, batch folded) must give the
-same logits as the reference's own structure (training/train_qwen.py:122-170:
-per batch element, [n, h, d] contiguous copies, router call with an explicit
-tril mask, sparse_exact_attention), both built from this package's drop-in
-functions; with routing disabled it must match transformers' own attention.
-Gradients flow through the patched forward.  Tolerance 1e-4 of max|logits|
-(fp32; the two structures sum the same keys in different orders).
+The patched forward (the HIP RoPE kernel, strided [B, n, h, d] views, batch
+folded) must give the same logits as the reference's own structure
+(training/train_qwen.py:122-170: transformers' RoPE, per batch element
+[n, h, d] contiguous copies, router call with the causal mask, attention) run
+with the CPU oracle as router and attention; the router's indices must equal
+the oracle's bit for bit on the way.  With routing disabled the adapter must
+match transformers' own attention.  Gradients flow through the patched
+forward.  Tolerance 1e-4 of max|logits| (fp32 against the float64 oracle).
 """
 
 from __future__ import annotations
@@ -30,11 +31,15 @@ def _model(dev):
 
 
 def _reference_structure_forward():
-    """training/train_qwen.py:122-170 restated with this package's drop-in calls."""
+    """training/train_qwen.py:122-170 restated with the CPU oracle in place of the
+    router and the attention: transformers' own RoPE, per batch element
+    [n, h, d] copies, routing with the causal mask (oracle.router_forward, whose
+    indices the module's router must reproduce bit for bit), then the float64
+    oracle attention with no mask, as the reference's stage 3."""
+    import numpy as np
     from transformers.models.qwen2.modeling_qwen2 import apply_rotary_pos_emb
 
-    from ssa_amd import sparse_exact_attention
-    from ssa_amd.utils import build_causal_mask
+    import oracle
 
     def fwd(self, hidden_states, position_embeddings, attention_mask=None, past_key_values=None,
             **kwargs):
@@ -45,15 +50,21 @@ def _reference_structure_forward():
         v = self.v_proj(hidden_states).view(hidden_shape).transpose(1, 2)
         cos, sin = position_embeddings
         q, k = apply_rotary_pos_emb(q, k, cos, sin)
+        r = self.ssa_router
         outs = []
         for b in range(input_shape[0]):
             q_b = q[b].transpose(0, 1).contiguous()
             k_b = k[b].transpose(0, 1).contiguous()
             v_b = v[b].transpose(0, 1).contiguous()
-            mask = build_causal_mask(k_b.shape[0], device=hidden_states.device)
-            idx = self.ssa_router(q_b, k_b, causal_mask=mask, hard=True)
-            outs.append(sparse_exact_attention(q_b, k_b, v_b, idx).transpose(0, 1).contiguous())
-        out = torch.stack(outs).transpose(1, 2).contiguous().reshape(*input_shape, -1)
+            idx, _ = oracle.router_forward(oracle.to_f32(q_b), oracle.to_f32(k_b),
+                                           oracle.to_f32(r.W_qr.weight), oracle.to_f32(r.W_kr.weight),
+                                           oracle.to_f32(r.codebook), r.codes_per_query,
+                                           r.codes_per_key, r.top_k, oracle.MASK_CAUSAL)
+            got = r(q_b, k_b, causal_mask=True).cpu().numpy()
+            np.testing.assert_array_equal(got, idx)
+            att = oracle.sparse_attention(oracle.to_f32(q_b), oracle.to_f32(k_b), oracle.to_f32(v_b), idx)
+            outs.append(torch.from_numpy(att).to(hidden_states.device, torch.float32))
+        out = torch.stack(outs).reshape(*input_shape, -1).to(hidden_states.dtype)
         return self.o_proj(out), None
 
     return fwd

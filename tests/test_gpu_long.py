@@ -1,8 +1,10 @@
-"""Full-size parity at the headline workload (n=32768, bf16, GQA 32/8, d 128,
-d_s 32, N_c 4096, a 16, b 4, k 512, causal, clustered inputs).
+"""Full-size parity at the long-context workloads: config 3 (n=32768, bf16,
+GQA 32/8, d 128, d_s 32, N_c 4096, a 16, b 4, k 512, 64-cluster inputs) and
+config 5 (n=131072, GQA 16/2, N_c 8192, a 32, k 1024, 256-cluster inputs),
+both causal.
 
-The oracle is too slow for every row at this size, so each stage is checked on
-sampled rows against the oracle fed with the previous stage's (already
+The oracle is too slow for every row at these sizes, so each stage is checked
+on sampled rows against the oracle fed with the previous stage's (already
 verified) GPU output, and the whole output is checked through size-independent
 properties.  Sampled rows always include the rows with the most candidates,
 which exercise the streaming top-k with several rescoring batches.
@@ -17,13 +19,13 @@ import bench
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture(scope="module")
-def c3(dev):
+@pytest.fixture(scope="module", params=["c3", "c5"])
+def lc(dev, request):
     from ssa_amd import kernels
     from ssa_amd.router import query_order
 
-    print("config3: generating workload", flush=True)
-    cfg = dict(bench.CONFIGS["c3"])
+    print(f"{request.param}: generating workload", flush=True)
+    cfg = dict(bench.CONFIGS[request.param])
     q, k, v, router = bench.make_workload(cfg, 0, dev)
     qc, kc = kernels.route_codes(q, k, router.W_qr.weight, router.W_kr.weight, router.codebook,
                                  cfg["a"], cfg["b"])
@@ -41,35 +43,35 @@ def c3(dev):
     out_ord = torch.empty_like(out)
     kernels.sparse_attention(q, k, v, idx_u, None, True, out=out_ord, row_order=order)
     torch.cuda.synchronize()
-    print("config3: GPU pipeline done", flush=True)
+    print(f"{request.param}: GPU pipeline done", flush=True)
     return dict(cfg=cfg, q=q, k=k, v=v, router=router, qc=qc, kc=kc, off=off, post=post,
                 idx_s=idx_s, idx_u=idx_u, idx_s2=idx_s2, idx_u2=idx_u2, idx_ub=idx_ub, st_u=st_u,
                 st_ub=st_ub, stats=st, out=out,
                 order=order, out_ord=out_ord)
 
 
-def test_c3_row_order_changes_nothing(c3):
+def test_long_row_order_changes_nothing(lc):
     """Processing rows grouped by code gives bit-identical outputs; the order is
     a permutation of the positions of every (batch, kv head)."""
-    order = c3["order"][0].to(torch.int64)
-    n = c3["cfg"]["n"]
+    order = lc["order"][0].to(torch.int64)
+    n = lc["cfg"]["n"]
     assert torch.equal(order.sort(-1).values, torch.arange(n, device=order.device).expand_as(order))
-    first = c3["qc"][0][:, :, 0].gather(1, order)        # best code along the order
+    first = lc["qc"][0][:, :, 0].gather(1, order)        # best code along the order
     assert bool((first[:, 1:] >= first[:, :-1]).all()), "order groups rows by ascending code"
-    assert torch.equal(c3["out"], c3["out_ord"])
+    assert torch.equal(lc["out"], lc["out_ord"])
 
 
-def test_c3_select_light_heavy_equals_block_path(c3):
+def test_long_select_light_heavy_equals_block_path(lc):
     """Index order through the wave-per-row pass plus the listed heavy rows gives
     the same indices and stats as one block per row."""
-    assert torch.equal(c3["idx_u"], c3["idx_ub"])
-    assert torch.equal(c3["st_u"], c3["st_ub"])
-    assert torch.equal(c3["st_u"], c3["stats"])  # sorted order counts the same
+    assert torch.equal(lc["idx_u"], lc["idx_ub"])
+    assert torch.equal(lc["st_u"], lc["st_ub"])
+    assert torch.equal(lc["st_u"], lc["stats"])  # sorted order counts the same
 
 
-def test_c3_select_deterministic(c3):
-    assert torch.equal(c3["idx_u"], c3["idx_u2"]), "unsorted selection differs between runs"
-    assert torch.equal(c3["idx_s"], c3["idx_s2"]), "sorted selection differs between runs"
+def test_long_select_deterministic(lc):
+    assert torch.equal(lc["idx_u"], lc["idx_u2"]), "unsorted selection differs between runs"
+    assert torch.equal(lc["idx_s"], lc["idx_s2"]), "sorted selection differs between runs"
 
 
 def _sample_rows(n, extra, seed=0, count=48):
@@ -78,54 +80,54 @@ def _sample_rows(n, extra, seed=0, count=48):
     return np.array(sorted(rows), dtype=np.int64)
 
 
-def test_c3_stage_a_codes(c3, orc):
-    cfg, r = c3["cfg"], c3["router"]
+def test_long_stage_a_codes(lc, orc):
+    cfg, r = lc["cfg"], lc["router"]
     n, g = cfg["n"], cfg["h_q"] // cfg["h_kv"]
     rows = _sample_rows(n, [], seed=1, count=256)
-    qf, kf = orc.to_f32(c3["q"][0][rows]), orc.to_f32(c3["k"][0][rows])
+    qf, kf = orc.to_f32(lc["q"][0][rows]), orc.to_f32(lc["k"][0][rows])
     chat = orc.normalize(orc.to_f32(r.codebook))
     qcs = orc.code_topk(orc.route_vectors(qf, orc.to_f32(r.W_qr.weight), g), chat, cfg["a"])
     kcs = orc.code_topk(orc.route_vectors(kf, orc.to_f32(r.W_kr.weight), 1), chat, cfg["b"])
-    np.testing.assert_array_equal(c3["qc"][0][:, rows].cpu().numpy(), qcs)
-    np.testing.assert_array_equal(c3["kc"][0][:, rows].cpu().numpy(), kcs)
+    np.testing.assert_array_equal(lc["qc"][0][:, rows].cpu().numpy(), qcs)
+    np.testing.assert_array_equal(lc["kc"][0][:, rows].cpu().numpy(), kcs)
 
 
-def test_c3_stage_b_index(c3, orc):
-    off, post = orc.build_index(c3["kc"][0].cpu().numpy(), c3["cfg"]["n_c"])
-    np.testing.assert_array_equal(c3["off"][0].cpu().numpy(), off)
-    np.testing.assert_array_equal(c3["post"][0].cpu().numpy(), post)
+def test_long_stage_b_index(lc, orc):
+    off, post = orc.build_index(lc["kc"][0].cpu().numpy(), lc["cfg"]["n_c"])
+    np.testing.assert_array_equal(lc["off"][0].cpu().numpy(), off)
+    np.testing.assert_array_equal(lc["post"][0].cpu().numpy(), post)
 
 
 @pytest.mark.parametrize("sorted_", [True, False])
-def test_c3_stage_c_rows_vs_oracle(c3, orc, sorted_):
-    cfg = c3["cfg"]
+def test_long_stage_c_rows_vs_oracle(lc, orc, sorted_):
+    cfg = lc["cfg"]
     n = cfg["n"]
-    cand = c3["stats"][0, :, :, 0].cpu().numpy()           # [h, n]
+    cand = lc["stats"][0, :, :, 0].cpu().numpy()           # [h, n]
     heavy = np.argsort(-cand.max(0))[:16].tolist()          # rows with the most candidates
     rows = _sample_rows(n, heavy, seed=2)
-    idx = (c3["idx_s"] if sorted_ else c3["idx_u"])[0].cpu().numpy()
-    ref, ncand, nraw = orc.select(orc.to_f32(c3["q"][0]), orc.to_f32(c3["k"][0]),
-                                  c3["qc"][0].cpu().numpy(), c3["off"][0].cpu().numpy(),
-                                  c3["post"][0].cpu().numpy(), cfg["b"], cfg["k"],
+    idx = (lc["idx_s"] if sorted_ else lc["idx_u"])[0].cpu().numpy()
+    ref, ncand, nraw = orc.select(orc.to_f32(lc["q"][0]), orc.to_f32(lc["k"][0]),
+                                  lc["qc"][0].cpu().numpy(), lc["off"][0].cpu().numpy(),
+                                  lc["post"][0].cpu().numpy(), cfg["b"], cfg["k"],
                                   orc.MASK_CAUSAL, rows=rows, with_stats=True, sorted=sorted_)
-    assert cand.max() > 2 * 512, "workload should contain rows needing several rescoring batches"
+    assert cand.max() > 2 * cfg["k"], "workload should contain rows needing several rescoring batches"
     for t, i in enumerate(rows):
         np.testing.assert_array_equal(idx[i], ref[t], err_msg=f"row {i} (sorted={sorted_})")
-    st = c3["stats"][0].cpu().numpy()
+    st = lc["stats"][0].cpu().numpy()
     np.testing.assert_array_equal(st[:, rows, 0].T, ncand)
     np.testing.assert_array_equal(st[:, rows, 1].T, nraw)
 
 
-def test_c3_stage_c_properties(c3):
+def test_long_stage_c_properties(lc):
     """Whole-output invariants: same set in both orders, candidates causal and
     distinct, filler ascending, bounds."""
-    cfg = c3["cfg"]
+    cfg = lc["cfg"]
     n, k = cfg["n"], cfg["k"]
-    idx_s = c3["idx_s"][0]
-    idx_u = c3["idx_u"][0]
+    idx_s = lc["idx_s"][0]
+    idx_u = lc["idx_u"][0]
     assert int(idx_s.min()) >= 0 and int(idx_s.max()) < n
     assert torch.equal(idx_s.sort(-1).values, idx_u.sort(-1).values)
-    ncand = c3["stats"][0, :, :, 0].T.to(torch.int64)           # [n, h]
+    ncand = lc["stats"][0, :, :, 0].T.to(torch.int64)           # [n, h]
     sel = torch.minimum(ncand, torch.tensor(k))
     pos = torch.arange(k, device=idx_s.device)
     is_cand = pos[None, None, :] < sel[..., None]
@@ -139,11 +141,11 @@ def test_c3_stage_c_properties(c3):
     assert bool((d[valid] > 0).all()), "filler must ascend"
 
 
-def test_c3_stage_d_rows_vs_oracle(c3, orc):
-    n = c3["cfg"]["n"]
+def test_long_stage_d_rows_vs_oracle(lc, orc):
+    n = lc["cfg"]["n"]
     rows = _sample_rows(n, [], seed=3, count=64)
-    idx = c3["idx_u"][0].cpu().numpy()[rows]
-    ref = orc.sparse_attention(orc.to_f32(c3["q"][0]), orc.to_f32(c3["k"][0]),
-                               orc.to_f32(c3["v"][0]), idx, causal=True, rows=rows)
-    got = c3["out"][0].cpu().numpy()[rows]
+    idx = lc["idx_u"][0].cpu().numpy()[rows]
+    ref = orc.sparse_attention(orc.to_f32(lc["q"][0]), orc.to_f32(lc["k"][0]),
+                               orc.to_f32(lc["v"][0]), idx, causal=True, rows=rows)
+    got = lc["out"][0].cpu().numpy()[rows]
     np.testing.assert_allclose(got, ref, rtol=1e-3, atol=1e-3)
