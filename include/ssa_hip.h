@@ -215,6 +215,28 @@ int ssa_select_block(const void* q, const void* k, int dtype, int64_t batch, int
                      int sorted, const int32_t* row_order, void* out, int out_index_dtype,
                      int32_t* stats, void* workspace, size_t workspace_bytes, void* stream);
 
+/* ssa_select_block without a workspace argument: no counterpart in the
+ * reference; for callers that cannot allocate (code under HIP graph capture,
+ * serving loops, harnesses that forbid hipMalloc).  The workspace is a static
+ * device array of ssa_select_noalloc_scratch_bytes() bytes (64 MiB) that the
+ * library holds on every device it runs on until the process ends; the call
+ * allocates nothing and uses min(that, ssa_select_workspace_bytes(batch, n_q,
+ * h_kv, top_k)) of it (rows whose candidate lists do not fit take the exact
+ * pass, with identical results).  Shapes whose minimum workspace
+ * (ssa_select_workspace_bytes(batch, n_q, h_kv, 0), about 20 bytes per
+ * (batch, query row, kv head)) exceeds the array are rejected with
+ * SSA_ERR_WORKSPACE.  Every call on one device shares the array: calls that
+ * overlap on one device (other streams, other threads) race. */
+size_t ssa_select_noalloc_scratch_bytes(void);
+int ssa_select_block_noalloc(const void* q, const void* k, int dtype, int64_t batch, int64_t n,
+                             int64_t n_q, int64_t q_pos0, int h_q, int h_kv, int d, int64_t q_sb,
+                             int64_t q_sn, int64_t q_sh, int64_t k_sb, int64_t k_sn, int64_t k_sh,
+                             const int32_t* q_codes, int a, const int32_t* offsets,
+                             const int32_t* postings, int n_c, int b, int top_k, int mask_mode,
+                             const uint8_t* mask, int64_t mask_sb, int64_t mask_si,
+                             float score_div, int sorted, const int32_t* row_order, void* out,
+                             int out_index_dtype, int32_t* stats, void* stream);
+
 /* ---- stage (d): gathered exact attention -------------------------------- */
 
 /* out[b][i][hq] = softmax_m(q[b][i][hq] . k[b][idx[b][i][h][m]][h] / scale_div) . v[...]

@@ -75,6 +75,12 @@ SIGNATURES = {
         [_vp, _vp, _int, _i64, _i64, _i64, _i64, _int, _int, _int, _i64, _i64, _i64, _i64, _i64,
          _i64, _vp, _int, _vp, _vp, _int, _int, _int, _int, _vp, _i64, _i64, _flt, _int, _vp, _vp,
          _int, _vp, _vp, _sz, _vp]),
+    "ssa_select_noalloc_scratch_bytes": (_sz, []),
+    "ssa_select_block_noalloc": (
+        _int,
+        [_vp, _vp, _int, _i64, _i64, _i64, _i64, _int, _int, _int, _i64, _i64, _i64, _i64, _i64,
+         _i64, _vp, _int, _vp, _vp, _int, _int, _int, _int, _vp, _i64, _i64, _flt, _int, _vp, _vp,
+         _int, _vp, _vp]),
     "ssa_sparse_attention": (
         _int,
         [_vp, _vp, _vp, _int, _i64, _i64, _int, _int, _int, _i64, _i64, _i64, _i64, _i64, _i64,

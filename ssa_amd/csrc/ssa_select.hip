@@ -19,6 +19,8 @@
 //              filler.  Rows with at most k candidates need no scores at all in
 //              this order (their set is every candidate), so only rows with
 //              more than k candidates are rescored.
+#include <mutex>
+
 #include "ssa_common.h"
 #include "ssa_rows.h"
 
@@ -1380,6 +1382,87 @@ extern "C" int ssa_select_block(const void* q, const void* k, int dtype, int64_t
   hipStream_t st = as_stream(stream);
   if (dtype == SSA_DTYPE_BF16) return dispatch_select<uint16_t>(p, rows, smem, workspace, workspace_bytes, st);
   return dispatch_select<float>(p, rows, smem, workspace, workspace_bytes, st);
+}
+
+// ---------------------------------------------------------------- no-alloc variant
+//
+// ssa_select_block_noalloc runs ssa_select_block with its workspace in the
+// file-scope array below instead of caller memory, for callers that cannot
+// allocate (code under HIP graph capture, serving loops).  The array is a
+// host-side symbol: kernels get its device address, looked up once per device
+// with hipGetSymbolAddress and cached; every call on one device shares it, so
+// calls that overlap on one device race.  Only the counter block must start at
+// zero, and the select path clears it with a kernel on every call.
+
+constexpr size_t kSelScratchBytes = size_t(64) << 20;
+static __device__ __align__(256) unsigned char scratch[kSelScratchBytes];
+
+namespace ssa {
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device (nullptr on failure, with
+// the status in *st).
+void* scratch_address(int* st) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    *st = fail(SSA_ERR_HIP, "select (no alloc): cannot query the current device");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+      *st = fail(SSA_ERR_HIP, "select (no alloc): hipGetSymbolAddress: %s", hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  *st = SSA_OK;
+  return g_scratch_ptr[dev];
+}
+
+}  // namespace
+}  // namespace ssa
+
+extern "C" size_t ssa_select_noalloc_scratch_bytes(void) { return kSelScratchBytes; }
+
+extern "C" int ssa_select_block_noalloc(const void* q, const void* k, int dtype, int64_t batch,
+                                        int64_t n, int64_t n_q, int64_t q_pos0, int h_q, int h_kv,
+                                        int d, int64_t q_sb, int64_t q_sn, int64_t q_sh,
+                                        int64_t k_sb, int64_t k_sn, int64_t k_sh,
+                                        const int32_t* q_codes, int a, const int32_t* offsets,
+                                        const int32_t* postings, int n_c, int b, int top_k,
+                                        int mask_mode, const uint8_t* mask, int64_t mask_sb,
+                                        int64_t mask_si, float score_div, int sorted,
+                                        const int32_t* row_order, void* out, int out_index_dtype,
+                                        int32_t* stats, void* stream) {
+  if (batch < 0 || n_q < 0 || h_kv <= 0 || top_k < 0)
+    return fail(SSA_ERR_INVALID_ARGUMENT, "select (no alloc): bad shape");
+  const size_t need = ssa_select_workspace_bytes(batch, n_q, h_kv, 0);
+  if (need > kSelScratchBytes)
+    return fail(SSA_ERR_WORKSPACE,
+                "select (no alloc): %lld query rows x %d kv heads need %zu bytes of scratch, more "
+                "than its %zu bytes; use ssa_select_block with a workspace",
+                static_cast<long long>(batch * n_q), h_kv, need, kSelScratchBytes);
+  size_t bytes = ssa_select_workspace_bytes(batch, n_q, h_kv, top_k);
+  if (bytes > kSelScratchBytes) bytes = kSelScratchBytes;
+  if (batch == 0 || n == 0 || n_q == 0)  // nothing to launch: the scratch is not needed
+    return ssa_select_block(q, k, dtype, batch, n, n_q, q_pos0, h_q, h_kv, d, q_sb, q_sn, q_sh,
+                            k_sb, k_sn, k_sh, q_codes, a, offsets, postings, n_c, b, top_k,
+                            mask_mode, mask, mask_sb, mask_si, score_div, sorted, row_order, out,
+                            out_index_dtype, stats, nullptr, 0, stream);
+  int st = SSA_OK;
+  void* ws = ssa::scratch_address(&st);
+  if (!ws) return st;
+  return ssa_select_block(q, k, dtype, batch, n, n_q, q_pos0, h_q, h_kv, d, q_sb, q_sn, q_sh, k_sb,
+                          k_sn, k_sh, q_codes, a, offsets, postings, n_c, b, top_k, mask_mode, mask,
+                          mask_sb, mask_si, score_div, sorted, row_order, out, out_index_dtype,
+                          stats, ws, bytes, stream);
 }
 
 extern "C" int ssa_select(const void* q, const void* k, int dtype, int64_t batch, int64_t n,
