@@ -513,16 +513,15 @@ __device__ __forceinline__ void mf_issue(__amdgpu_buffer_rsrc_t krs, __amdgpu_bu
   }
 }
 
+// One (batch, kv head, query) row on one wave, with the wave's LDS slices kl
+// and vl (kMfChunk rows of K and of V each).
 template <int D, bool BLK>
-__global__ __launch_bounds__(64 * kMfWaves, kMfMinBlocks) void sparse_attention_mfma_kernel(AttParams p) {
+__device__ __forceinline__ void attend_row_mfma(const AttParams& p, const AttRow& ar, unsigned char* kl,
+                                                unsigned char* vl) {
   using S = MfShape<D>;
-  __shared__ __align__(16) unsigned char kv_lds[kMfWaves][2][kMfChunk * S::ROW];
-
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int q4 = lane >> 4;
   const int c16 = lane & 15;
-  const AttRow ar = att_row(p, static_cast<int64_t>(blockIdx.x) * kMfWaves + wave);
   const bool row_ok = ar.ok;
   const int64_t i = ar.i;  // key position (causal cut)
   const int64_t qr = ar.r;  // query row (q, idx, out)
@@ -541,8 +540,6 @@ __global__ __launch_bounds__(64 * kMfWaves, kMfMinBlocks) void sparse_attention_
   const uint16_t* kbase = static_cast<const uint16_t*>(p.k) + bb * p.k_sb + static_cast<int64_t>(h) * p.k_sh;
   const uint16_t* vbase = static_cast<const uint16_t*>(p.v) + bb * p.v_sb + static_cast<int64_t>(h) * p.v_sh;
   const int64_t ibase = bb * p.idx_sb + (BLK ? qr >> p.blk_log2 : qr) * p.idx_sn + static_cast<int64_t>(h) * p.idx_sh;
-  unsigned char* kl = kv_lds[wave][0];
-  unsigned char* vl = kv_lds[wave][1];
 
   auto load_idx = [&](int ch) -> int {
     const int slot = ch * kMfChunk + lane;
@@ -724,6 +721,15 @@ __global__ __launch_bounds__(64 * kMfWaves, kMfMinBlocks) void sparse_attention_
       *reinterpret_cast<float4*>(dst + 16 * t) =
           make_float4(oacc[t][0] * inv, oacc[t][1] * inv, oacc[t][2] * inv, oacc[t][3] * inv);
   }
+}
+
+template <int D, bool BLK>
+__global__ __launch_bounds__(64 * kMfWaves, kMfMinBlocks) void sparse_attention_mfma_kernel(AttParams p) {
+  using S = MfShape<D>;
+  __shared__ __align__(16) unsigned char kv_lds[kMfWaves][2][kMfChunk * S::ROW];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const AttRow ar = att_row(p, static_cast<int64_t>(blockIdx.x) * kMfWaves + wave);
+  attend_row_mfma<D, BLK>(p, ar, kv_lds[wave][0], kv_lds[wave][1]);
 }
 
 template <typename T, int D>

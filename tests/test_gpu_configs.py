@@ -180,7 +180,7 @@ def c4(dev):
         att32 = torch.empty(q.shape, device=dev, dtype=torch.float32)
         from ssa_amd import kernels
         kernels.sparse_attention(q, k, v, res.indices, None, False, out=att32, row_order=res.order)
-        att_bf16 = kernels.sparse_attention(q, k, v, res.indices, None, False)
+        att_bf16 = kernels.sparse_attention(q, k, v, res.indices, None, False, row_order=res.order)
         again = layer.o_proj(att_bf16.reshape(B, n, -1))
     torch.cuda.synchronize()
     return dict(layer=layer, freqs=blk["freqs"], out=out, q=q, k=k, v=v, q_lin=q_lin, k_lin=k_lin,
@@ -189,7 +189,7 @@ def c4(dev):
 
 def test_c4_output_is_o_proj_of_the_attention(c4):
     """The layer's output is o_proj of the bf16 attention output (same kernels,
-    same inputs, run again outside the layer)."""
+    same inputs and processing order, run again outside the layer)."""
     assert torch.equal(c4["out"], c4["again"])
 
 
