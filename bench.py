@@ -62,6 +62,9 @@ def parse():
     p.add_argument("--decode", type=int, default=0,
                    help="also time this many single-token decode steps after a prefill of n minus "
                         "that many tokens (SSADecodeCache)")
+    p.add_argument("--decode-lens", default="",
+                   help="with --decode: also time the steps at these cache lengths (c3 head "
+                        "shapes; codebook fixed at the config's N_c and scaled with n)")
     p.add_argument("--block-sparse", type=int, default=0,
                    help="also time the block-granular variant with this many 64-key blocks per "
                         "query block (block indices from the workload's selections, then attention)")
@@ -363,26 +366,34 @@ def time_blocks(cfg, q, k, v, inter, n_k_blocks, block_size=64, reps=3):
             "tokens_per_s": cfg["B"] * cfg["n"] / ((med["indices"] + med["attention"]) / 1000.0)}
 
 
-def time_decode(cfg, q, k, v, router, steps):
-    """Single-token decode steps (ssa_amd.decode.SSADecodeCache) for the last
-    `steps` tokens of the workload after a prefill of the rest; wall time per
-    step on the host (each step launches about a dozen kernels)."""
+def time_decode(cfg, q, k, v, router, steps, tail_tokens=512):
+    """Single-token decode steps (ssa_amd.decode.SSADecodeCache: one native call
+    per step, a tail index over the newest keys, the main index rebuilt every
+    tail_tokens keys) for the last `steps` tokens of the workload after a
+    prefill of the rest; host wall time per step, including the rebuilds that
+    fall inside the timed steps, and HIP-event time of the steps."""
     import torch
 
     from ssa_amd.decode import SSADecodeCache
 
     n = cfg["n"]
-    cache = SSADecodeCache(router, cfg["B"], n, cfg["d"], dtype=q.dtype)
+    cache = SSADecodeCache(router, cfg["B"], n, cfg["d"], dtype=q.dtype, tail_tokens=tail_tokens)
     n0 = n - steps
     cache.step(q[:, :n0], k[:, :n0], v[:, :n0])
     torch.cuda.synchronize()
+    rebuilds0 = cache.rebuilds
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
+    e0.record()
     for t in range(n0, n):
         cache.step(q[:, t:t + 1], k[:, t:t + 1], v[:, t:t + 1])
+    e1.record()
     torch.cuda.synchronize()
     ms = 1000 * (time.perf_counter() - t0) / steps
-    return {"ms_per_token": ms, "tokens_per_s": cfg["B"] / (ms / 1000), "cache_len": n,
-            "steps": steps, "prefill_tokens": n0}
+    return {"ms_per_token": ms, "gpu_ms_per_token": e0.elapsed_time(e1) / steps,
+            "tokens_per_s": cfg["B"] / (ms / 1000), "cache_len": n, "steps": steps,
+            "prefill_tokens": n0, "tail_tokens": tail_tokens,
+            "rebuilds_in_timed_steps": cache.rebuilds - rebuilds0}
 
 
 def _cpu_model():
@@ -688,6 +699,20 @@ def main():
         line["backward"] = time_backward(cfg, q, k, v, inter)
     if args.decode > 0:
         line["decode"] = time_decode(cfg, q, k, v, router, args.decode)
+        if args.decode_lens:
+            by_len = {}
+            for n_ in [int(x) for x in args.decode_lens.split(",")]:
+                for policy in ("fixed", "scaled"):
+                    c2 = dict(cfg, n=n_)
+                    if policy == "scaled":
+                        c2["n_c"] = max(16, cfg["n_c"] * n_ // cfg["n"])
+                    q2, k2, v2, r2 = make_workload(c2, args.seed, dev)
+                    by_len[f"{n_}_{policy}"] = dict(time_decode(c2, q2, k2, v2, r2, args.decode),
+                                                    num_codebook=c2["n_c"])
+                    print(f"decode n={n_} N_c={c2['n_c']}: "
+                          f"{by_len[f'{n_}_{policy}']['ms_per_token']:.3f} ms", file=sys.stderr, flush=True)
+                    del q2, k2, v2, r2
+            line["decode_by_cache_len"] = by_len
     if args.block_sparse > 0:
         line["block_sparse"] = time_blocks(cfg, q, k, v, inter, args.block_sparse)
     if not args.no_cpu_baseline:

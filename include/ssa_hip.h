@@ -237,6 +237,50 @@ int ssa_select_block_noalloc(const void* q, const void* k, int dtype, int64_t ba
                              float score_div, int sorted, const int32_t* row_order, void* out,
                              int out_index_dtype, int32_t* stats, void* stream);
 
+/* ---- incremental decoding ----------------------------------------------- */
+
+/* One decoding step for m new tokens against a key/value cache: no reference
+ * counterpart (the reference runs whole sequences; ssa_design.md:225-234
+ * describes decode-time routing against the cached keys' inverted index,
+ * "maintained incrementally, avoiding re-scanning the full KV cache").
+ * The caller owns the cache state:
+ *   k_cache, v_cache [batch][max_len][h_kv][d] (strides kc_*, vc_*), holding
+ *       n0 tokens; the step writes the new rows at n0 .. n0 + m - 1;
+ *   k_codes int32 [batch][h_kv][max_len][b]: the keys' codes (written likewise);
+ *   offsets/postings: an ssa_build_index index over keys 0 .. n_base - 1
+ *       ([batch][h_kv][n_c + 1], [batch][h_kv][n_base * b]; n_base <= n0);
+ *   tail_offsets int32 [batch][h_kv][n_c + 1], tail_postings int32
+ *       [batch][h_kv][tail_cap]: rebuilt by the step over keys n_base ..
+ *       n0 + m - 1 ((n0 + m - n_base) * b <= tail_cap, else SSA_ERR_WORKSPACE:
+ *       rebuild the main index over every cached key and start a new tail);
+ *   prep: the codebook prepared by ssa_decode_prepare (normalized rows, their
+ *       bf16 copy and largest norm; prepare again when the codebook changes).
+ * q [batch][m][h_q][d], k, v [batch][m][h_kv][d] (strided) are the new tokens.
+ * The step routes them (top-a query and top-b key codes), selects each new
+ * query's top_k keys among all cached keys from both indices (causal, index
+ * order, the same selection as ssa_select_block over the whole cache) into
+ * indices (nullable int32 [batch][m][h_kv][top_k]) and attends them
+ * (ssa_sparse_attention_block; causal != 0 drops selected keys past the
+ * query) into out [batch][m][h_q][d] (strides o_*, type out_dtype).  Limits
+ * as the stages', plus a <= 32, d_s <= 32, n_c <= 16384, rows of 16 bytes. */
+size_t ssa_decode_prepare_bytes(int h_kv, int n_c, int d_s);
+int ssa_decode_prepare(const float* codebook, int h_kv, int n_c, int d_s, void* prep,
+                       size_t prep_bytes, void* stream);
+size_t ssa_decode_workspace_bytes(int64_t batch, int64_t m, int h_kv, int d_s, int n_c, int a,
+                                  int b, int top_k);
+int ssa_decode_step(const void* q, const void* k, const void* v, int dtype, int64_t batch, int64_t m,
+                    int h_q, int h_kv, int d, int64_t q_sb, int64_t q_sn, int64_t q_sh, int64_t k_sb,
+                    int64_t k_sn, int64_t k_sh, int64_t v_sb, int64_t v_sn, int64_t v_sh,
+                    void* k_cache, void* v_cache, int64_t max_len, int64_t kc_sb, int64_t kc_sn,
+                    int64_t kc_sh, int64_t vc_sb, int64_t vc_sn, int64_t vc_sh, int64_t n0,
+                    const float* w_qr, const float* w_kr, const void* prep, int d_s, int n_c, int a,
+                    int b, float temperature, int32_t* k_codes, const int32_t* offsets,
+                    const int32_t* postings, int64_t n_base, int32_t* tail_offsets,
+                    int32_t* tail_postings, int64_t tail_cap, int top_k, float score_div,
+                    float scale_div, int causal, int32_t* indices, void* out, int out_dtype,
+                    int64_t o_sb, int64_t o_sn, int64_t o_sh, void* workspace,
+                    size_t workspace_bytes, void* stream);
+
 /* ---- stage (d): gathered exact attention -------------------------------- */
 
 /* out[b][i][hq] = softmax_m(q[b][i][hq] . k[b][idx[b][i][h][m]][h] / scale_div) . v[...]

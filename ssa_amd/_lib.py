@@ -81,6 +81,15 @@ SIGNATURES = {
         [_vp, _vp, _int, _i64, _i64, _i64, _i64, _int, _int, _int, _i64, _i64, _i64, _i64, _i64,
          _i64, _vp, _int, _vp, _vp, _int, _int, _int, _int, _vp, _i64, _i64, _flt, _int, _vp, _vp,
          _int, _vp, _vp]),
+    "ssa_decode_prepare_bytes": (_sz, [_int, _int, _int]),
+    "ssa_decode_prepare": (_int, [_vp, _int, _int, _int, _vp, _sz, _vp]),
+    "ssa_decode_workspace_bytes": (_sz, [_i64, _i64, _int, _int, _int, _int, _int, _int]),
+    "ssa_decode_step": (
+        _int,
+        [_vp, _vp, _vp, _int, _i64, _i64, _int, _int, _int, _i64, _i64, _i64, _i64, _i64, _i64,
+         _i64, _i64, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp,
+         _vp, _int, _int, _int, _int, _flt, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _int, _flt,
+         _flt, _int, _vp, _vp, _int, _i64, _i64, _i64, _vp, _sz, _vp]),
     "ssa_sparse_attention": (
         _int,
         [_vp, _vp, _vp, _int, _i64, _i64, _int, _int, _int, _i64, _i64, _i64, _i64, _i64, _i64,

@@ -13,6 +13,7 @@
 // `scale_div` is the reference's `scale` (a divisor).  Duplicated indices count
 // twice, as in the reference.
 #include "ssa_common.h"
+#include "ssa_internal.h"
 #include "ssa_rows.h"
 
 namespace ssa {
@@ -514,10 +515,12 @@ __device__ __forceinline__ void mf_issue(__amdgpu_buffer_rsrc_t krs, __amdgpu_bu
 }
 
 // One (batch, kv head, query) row on one wave, with the wave's LDS slices kl
-// and vl (kMfChunk rows of K and of V each).
-template <int D, bool BLK>
+// and vl (kMfChunk rows of K and of V each).  NSPLIT > 1: the wave takes only
+// chunks c0, c0 + NSPLIT, ... and leaves its unnormalised state in `part`
+// (O [8][D], the running max [8] and sum [8] per head) for a combine step.
+template <int D, bool BLK, int NSPLIT = 1>
 __device__ __forceinline__ void attend_row_mfma(const AttParams& p, const AttRow& ar, unsigned char* kl,
-                                                unsigned char* vl) {
+                                                unsigned char* vl, int c0 = 0, float* part = nullptr) {
   using S = MfShape<D>;
   const int lane = threadIdx.x & 63;
   const int q4 = lane >> 4;
@@ -592,16 +595,19 @@ __device__ __forceinline__ void attend_row_mfma(const AttParams& p, const AttRow
   for (int t = 0; t < S::NT; ++t) oacc[t] = floatx4_t{0.f, 0.f, 0.f, 0.f};
 
   const int nchunks = (p.top_k + kMfChunk - 1) / kMfChunk;
+  // this wave's chunks: c0, c0 + NSPLIT, ... (all of them when NSPLIT = 1)
+  const int nmine = (nchunks > c0) ? (nchunks - c0 + NSPLIT - 1) / NSPLIT : 0;
+  auto chunk_of = [&](int u) { return c0 + u * NSPLIT; };
   uint64_t okbits = 0;
   int j_next = -1;
-  if (nchunks > 0) {
-    const int j0 = load_idx(0);
+  if (nmine > 0) {
+    const int j0 = load_idx(chunk_of(0));
     const bool ok0 = chunk_ok(j0);
     okbits = __ballot(ok0);
     issue(ok0 ? j0 : -1, static_cast<uint32_t>(okbits) == 0xFFFFFFFFu);
-    if (nchunks > 1) j_next = load_idx(1);
+    if (nmine > 1) j_next = load_idx(chunk_of(1));
   }
-  for (int ch = 0; ch < nchunks; ++ch) {
+  for (int u = 0; u < nmine; ++u) {
     // This chunk's rows are in LDS once its loads have completed.
     __builtin_amdgcn_s_waitcnt(kWaitVm0);
     bf16x8_t kf[2][S::KB];
@@ -623,11 +629,11 @@ __device__ __forceinline__ void attend_row_mfma(const AttParams& p, const AttRow
     // The slices are free once the reads have returned: start the next chunk.
     __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
     const uint64_t okb = okbits;
-    if (ch + 1 < nchunks) {
+    if (u + 1 < nmine) {
       const bool okn = chunk_ok(j_next);
       okbits = __ballot(okn);
       issue(okn ? j_next : -1, static_cast<uint32_t>(okbits) == 0xFFFFFFFFu);
-      if (ch + 2 < nchunks) j_next = load_idx(ch + 2);
+      if (u + 2 < nmine) j_next = load_idx(chunk_of(u + 2));
     }
 
     // Scores of eight keys of head c16 (keys 16t + 4*q4 + e).
@@ -702,6 +708,18 @@ __device__ __forceinline__ void attend_row_mfma(const AttParams& p, const AttRow
   for (int t = 0; t < S::NT; ++t)
 #pragma unroll
     for (int e = 0; e < 4; ++e) oacc[t][e] += dpp_from_plus8(oacc[t][e]);
+  if constexpr (NSPLIT > 1) {
+    if (!row_ok || !hi_row) return;
+    float* po = part + c16 * D + 4 * q4;
+#pragma unroll
+    for (int t = 0; t < S::NT; ++t)
+      *reinterpret_cast<float4*>(po + 16 * t) = make_float4(oacc[t][0], oacc[t][1], oacc[t][2], oacc[t][3]);
+    if (q4 == 0) {
+      part[8 * D + c16] = m_run;
+      part[8 * D + 8 + c16] = lt;
+    }
+    return;
+  }
   if (!row_ok || !hi_row) return;
   const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
   const int64_t ob = bb * p.o_sb + qr * p.o_sn + static_cast<int64_t>(h * p.g + c16) * p.o_sh + 4 * q4;
@@ -732,6 +750,50 @@ __global__ __launch_bounds__(64 * kMfWaves, kMfMinBlocks) void sparse_attention_
   attend_row_mfma<D, BLK>(p, ar, kv_lds[wave][0], kv_lds[wave][1]);
 }
 
+// Few rows (decoding): one block of kSplitWaves waves per row, wave w taking
+// chunks w, w + kSplitWaves, ...; the waves' partial states (per head: running
+// max m_w, sum l_w, unnormalised O_w) combine as O = sum_w 2^(m_w - M) O_w /
+// sum_w 2^(m_w - M) l_w with M = max_w m_w.  A row otherwise runs its chunks
+// one after another on one wave, which leaves the GPU idle when a call has a
+// few rows.
+constexpr int kSplitWaves = 4;
+constexpr int64_t kSplitRowsMax = 512;
+
+template <int D>
+__global__ __launch_bounds__(64 * kSplitWaves) void sparse_attention_split_kernel(AttParams p) {
+  using S = MfShape<D>;
+  __shared__ __align__(16) unsigned char kv_lds[kSplitWaves][2][kMfChunk * S::ROW];
+  __shared__ __align__(16) float part[kSplitWaves][8 * D + 16];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const AttRow ar = att_row(p, blockIdx.x);
+  attend_row_mfma<D, false, kSplitWaves>(p, ar, kv_lds[wave][0], kv_lds[wave][1], wave, part[wave]);
+  __syncthreads();
+  if (!ar.ok) return;
+  const int h = static_cast<int>(ar.bh % p.h_kv);
+  const int64_t bb = ar.bh / p.h_kv;
+  for (int e = threadIdx.x; e < p.g * D; e += 64 * kSplitWaves) {
+    const int hh = e / D, dim = e - hh * D;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kSplitWaves; ++w) M = fmaxf(M, part[w][8 * D + hh]);
+    float L = 0.0f, O = 0.0f;
+    if (M != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < kSplitWaves; ++w) {
+        const float mw = part[w][8 * D + hh];
+        if (mw == -INFINITY) continue;  // no valid key in this wave's chunks
+        const float a = __builtin_amdgcn_exp2f(mw - M);
+        L += a * part[w][8 * D + 8 + hh];
+        O += a * part[w][hh * D + dim];
+      }
+    }
+    const float val = L > 0.0f ? O / L : 0.0f;
+    const int64_t ob = bb * p.o_sb + ar.r * p.o_sn + static_cast<int64_t>(h * p.g + hh) * p.o_sh + dim;
+    if (p.out_bf16) static_cast<uint16_t*>(p.out)[ob] = f32_to_bf16_rne(val);
+    else static_cast<float*>(p.out)[ob] = val;
+  }
+}
+
 template <typename T, int D>
 int launch_att_d(const AttParams& p, hipStream_t st) {
   const int64_t blocks = ceil_div(p.rows, kAttWaves);
@@ -741,6 +803,10 @@ int launch_att_d(const AttParams& p, hipStream_t st) {
       return sn >= 0 && 2 * sn < (int64_t(1) << 24) && (p.n - 1) * sn * 2 + 2 * D < (int64_t(1) << 31);
     };
     if (p.g <= 8 && p.d == D && p.n < (int64_t(1) << 24) && fits(p.k_sn) && fits(p.v_sn)) {
+      if (p.blk_log2 == 0 && p.rows <= kSplitRowsMax && p.top_k >= 2 * kSplitWaves * kMfChunk) {
+        sparse_attention_split_kernel<D><<<dim3(static_cast<unsigned>(p.rows)), 64 * kSplitWaves, 0, st>>>(p);
+        return check_launch("sparse_attention_split_kernel");
+      }
       const dim3 grid(static_cast<unsigned>(ceil_div(p.rows, kMfWaves)));
       if (p.blk_log2 > 0) sparse_attention_mfma_kernel<D, true><<<grid, 64 * kMfWaves, 0, st>>>(p);
       else sparse_attention_mfma_kernel<D, false><<<grid, 64 * kMfWaves, 0, st>>>(p);
@@ -768,7 +834,6 @@ int launch_att(const AttParams& p, int d, hipStream_t st) {
 using namespace ssa;
 
 namespace ssa {
-namespace {
 // Token indices (blk_log2 = 0, top_k keys per row) or key-block ids
 // (blk_log2 > 0: top_k = blocks per row, nbk blocks in all).
 int attention_entry(const void* q, const void* k, const void* v, int dtype, int64_t batch, int64_t n,
@@ -848,7 +913,6 @@ int attention_entry(const void* q, const void* k, const void* v, int dtype, int6
   if (dtype == SSA_DTYPE_BF16) return launch_att<uint16_t>(p, d, st);
   return launch_att<float>(p, d, st);
 }
-}  // namespace
 }  // namespace ssa
 
 extern "C" int ssa_sparse_attention_block(

@@ -54,6 +54,27 @@ __device__ __forceinline__ uint32_t key_index(uint64_t key) {
 // fp32 fused multiply-add, single rounding (v_fma_f32).
 __device__ __forceinline__ float fma_rn(float a, float b, float c) { return __builtin_fmaf(a, b, c); }
 
+// Block-strided loop over elements [0, count) (thread `tid` of NT takes tid,
+// tid + NT, ...) that issues U independent loads before it uses any of them.
+// A loop whose body loads one element and then uses it waits out a whole
+// memory round trip per iteration; in the small grids of decoding those
+// round trips are most of a kernel's time.  Whole batches load without
+// bounds tests (a guarded load sits in a branch of its own, behind a wait
+// for the loads before it); only the last, partial batch tests each element.
+template <int U, int NT, typename Load, typename Use>
+__device__ __forceinline__ void strided_batches(int64_t count, int tid, Load load, Use use) {
+  using V = decltype(load(int64_t(0)));
+  int64_t e0 = 0;
+  for (; e0 + static_cast<int64_t>(U) * NT <= count; e0 += static_cast<int64_t>(U) * NT) {
+    V v[U];
+#pragma unroll
+    for (int j = 0; j < U; ++j) v[j] = load(e0 + static_cast<int64_t>(j) * NT + tid);
+#pragma unroll
+    for (int j = 0; j < U; ++j) use(e0 + static_cast<int64_t>(j) * NT + tid, v[j]);
+  }
+  for (int64_t e = e0 + tid; e < count; e += NT) use(e, load(e));
+}
+
 // ------------------------------------------------------------------ host
 
 // Records a human-readable detail for the last failing call on this thread.

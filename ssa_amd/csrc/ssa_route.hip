@@ -3,7 +3,10 @@
 // Replaces ssa/router.py:102-141 (projection, GQA mean, F.normalize, codebook
 // einsum / temperature, topk).  All arithmetic is exact-order fp32 so that the
 // selected codes are bit-identical with the CPU oracle.
+#include <algorithm>
+
 #include "ssa_common.h"
+#include "ssa_internal.h"
 
 namespace ssa {
 namespace {
@@ -1098,6 +1101,90 @@ __global__ __launch_bounds__(256) void code_topk_rows_kernel(const float* __rest
   }
 }
 
+// Few rows (decoding): one block per (batch, output head, row).  W [d_s][d]
+// (rows padded to d + 1 floats: no bank conflicts) and the group's x rows are
+// staged in LDS; wave w runs the chains of heads w, w + 4, ..., lane s the
+// chain of coordinate s (t ascending), so the group's heads run in parallel;
+// wave 0 then adds the heads in order, divides by group and runs the norm
+// chain over s on the broadcast coordinates.  Same arithmetic as the
+// row-parallel kernels above, which stay in charge of calls with many rows.
+constexpr int64_t kLaneRowsMax = 256;
+
+__host__ __device__ inline size_t route_few_smem(int group, int d, int d_s) {
+  return sizeof(float) * (static_cast<size_t>(d_s) * (d + 1) + static_cast<size_t>(group) * d +
+                          static_cast<size_t>(group) * 64);
+}
+
+// One routing task of route_vectors_few_kernel (blockIdx.y picks the task, so
+// the queries and the keys of a decoding step route in one launch).
+struct FewRoute {
+  const void* x;
+  int64_t n, sb, sn, sh, rows;  // rows = batch * (h_in / group) * n
+  int h_in, group, d, d_s;
+  const float* w;
+  float* out;
+};
+
+template <typename T>
+__global__ __launch_bounds__(256) void route_vectors_few_kernel(FewRoute t0, FewRoute t1) {
+  extern __shared__ __align__(16) float few_lds[];
+  const FewRoute& a = blockIdx.y ? t1 : t0;
+  const int64_t row = blockIdx.x;  // (b * h_out + h) * n + i
+  if (row >= a.rows) return;
+  const int d = a.d, d_s = a.d_s, group = a.group;
+  float* wl = few_lds;                                              // [d_s][d + 1]
+  float* xl = wl + static_cast<size_t>(d_s) * (d + 1);              // [group][d]
+  float* part = xl + static_cast<size_t>(group) * d;                // [group][64]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int h_out = a.h_in / group;
+  const int64_t i = row % a.n;
+  const int64_t bh = row / a.n;
+  const int h = static_cast<int>(bh % h_out);
+  const int64_t b = bh / h_out;
+  const T* x = static_cast<const T*>(a.x);
+  strided_batches<16, 256>(
+      static_cast<int64_t>(d_s) * d, tid, [&](int64_t e) { return a.w[e]; },
+      [&](int64_t e, float v) { wl[(e / d) * (d + 1) + e % d] = v; });
+  const T* xrow = x + b * a.sb + i * a.sn + static_cast<int64_t>(h * group) * a.sh;
+  strided_batches<4, 256>(
+      static_cast<int64_t>(group) * d, tid,
+      [&](int64_t e) { return ld(xrow + (e / d) * a.sh + e % d); }, [&](int64_t e, float v) { xl[e] = v; });
+  __syncthreads();
+  if (lane < d_s) {
+    const float* wr = wl + static_cast<size_t>(lane) * (d + 1);
+    for (int gg = wave; gg < group; gg += 4) {
+      const float* xr = xl + static_cast<size_t>(gg) * d;
+      float acc = 0.0f;
+      for (int t = 0; t < d; ++t) acc = fma_rn(xr[t], wr[t], acc);
+      part[gg * 64 + lane] = acc;
+    }
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  float sum = 0.0f;
+  if (lane < d_s) {
+    sum = part[lane];
+    for (int gg = 1; gg < group; ++gg) sum = sum + part[gg * 64 + lane];
+  }
+  const float v = sum / static_cast<float>(group);
+  float nrm = 0.0f;
+  for (int s2 = 0; s2 < d_s; ++s2) {
+    const float vs = __shfl(v, s2);
+    nrm = fma_rn(vs, vs, nrm);
+  }
+  const float den = fmaxf(sqrtf(nrm), 1e-12f);
+  if (lane < d_s) a.out[row * d_s + lane] = v / den;
+}
+
+int launch_route_few(const FewRoute& t0, const FewRoute& t1, int dtype, hipStream_t st) {
+  const size_t smem = std::max(route_few_smem(t0.group, t0.d, t0.d_s),
+                               t1.rows > 0 ? route_few_smem(t1.group, t1.d, t1.d_s) : size_t(0));
+  const dim3 grid(static_cast<unsigned>(std::max(t0.rows, t1.rows)), t1.rows > 0 ? 2u : 1u);
+  if (dtype == SSA_DTYPE_BF16) route_vectors_few_kernel<uint16_t><<<grid, 256, smem, st>>>(t0, t1);
+  else route_vectors_few_kernel<float><<<grid, 256, smem, st>>>(t0, t1);
+  return check_launch("route_vectors_few_kernel");
+}
+
 int next_pow2(int v) {
   int p = 1;
   while (p < v) p <<= 1;
@@ -1137,6 +1224,12 @@ int launch_route_vectors(const void* x, int dtype, int64_t batch, int64_t n, int
   const int64_t pe = 16 / esz;
   const bool piece8 = (d % 8 == 0) && (sb % pe == 0) && (sn % pe == 0) && (sh % pe == 0) &&
                       (reinterpret_cast<uintptr_t>(x) % 16 == 0);
+  const int64_t total = batch * (h_in / group) * n;
+  if (d_s <= 64 && total <= kLaneRowsMax && route_few_smem(group, d, d_s) <= 64 * 1024) {
+    const FewRoute t0{x, n, sb, sn, sh, total, h_in, group, d, d_s, w, out};
+    FewRoute none{};
+    return launch_route_few(t0, none, dtype, st);
+  }
   if (d_s == 32 && piece8 && group > 1) {
     const int64_t grid = batch * (h_in / group) * ceil_div(n, kRsRows);
     if (dtype == SSA_DTYPE_BF16)
@@ -1196,6 +1289,366 @@ int check_code_topk(int64_t batch, int h, int64_t rows, int n_c, int d_s, float 
 
 // Workspace of the matrix-core path: bf16 codebook, per-head max norm, and a
 // fallback flag per 64-row group.
+// Exact top-`top` codes of a handful of rows (decoding): one block of 1024
+// threads per row (blockIdx.y picks one of two tasks, so the queries' and
+// keys' codes come from one launch).  Thread t scores codes t, t + 1024, ...
+// in the canonical fp32 order and keeps its best TM composite keys; each wave
+// then takes its top `top` by `top` rounds of a wave-wide maximum, and wave 0
+// merges the waves' lists the same way: the row's keys in descending order
+// (score desc, code asc), as code_topk_kernel orders them.
+constexpr int kFewThreads = 1024;
+constexpr int kFewWaves = kFewThreads / 64;
+
+struct FewTopk {
+  const float* xhat;  // [total][d_s]
+  int64_t rows, total;  // rows per (batch, head); total = batch * h * rows
+  int top;
+  int32_t* codes;     // [total][top]
+};
+
+template <int TM>
+__device__ __forceinline__ void keep_top(uint64_t (&best)[TM], uint64_t key) {
+#pragma unroll
+  for (int p = TM - 1; p > 0; --p) best[p] = key > best[p - 1] ? best[p - 1] : (key > best[p] ? key : best[p]);
+  best[0] = key > best[0] ? key : best[0];
+}
+
+// Pops the wave's largest head entry: returns it (in every lane) and removes
+// it from the lane that holds it (keys are distinct).
+template <int TM>
+__device__ __forceinline__ uint64_t wave_pop_max(uint64_t (&best)[TM]) {
+  uint64_t v = best[0];
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const uint32_t lo = static_cast<uint32_t>(__shfl_xor(static_cast<int>(v & 0xFFFFFFFFull), o));
+    const uint32_t hi = static_cast<uint32_t>(__shfl_xor(static_cast<int>(v >> 32), o));
+    const uint64_t w = (static_cast<uint64_t>(hi) << 32) | lo;
+    v = w > v ? w : v;
+  }
+  const bool win = best[0] == v;
+#pragma unroll
+  for (int q = 0; q < TM - 1; ++q) best[q] = win ? best[q + 1] : best[q];
+  best[TM - 1] = win ? 0ull : best[TM - 1];
+  return v;
+}
+
+template <int TM>
+__global__ __launch_bounds__(kFewThreads) void code_topk_few_kernel(FewTopk t0, FewTopk t1, int h,
+                                                                    const float* __restrict__ chat, int n_c,
+                                                                    int d_s, float temperature) {
+  __shared__ uint64_t s_top[kFewWaves][TM];
+  const FewTopk& a = blockIdx.y ? t1 : t0;
+  const int64_t grow = blockIdx.x;  // bh * rows + row
+  if (grow >= a.total) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int top = a.top;
+  const int hh = static_cast<int>((grow / a.rows) % h);
+  const float* xr = a.xhat + grow * d_s;
+  const float* cb = chat + static_cast<int64_t>(hh) * n_c * d_s;
+  const bool scale = (temperature != 1.0f);
+  float x[32];
+#pragma unroll
+  for (int s = 0; s < 32; ++s) x[s] = (s < d_s) ? xr[s] : 0.0f;
+  uint64_t best[TM];
+#pragma unroll
+  for (int p = 0; p < TM; ++p) best[p] = 0ull;  // below every key
+  for (int c = tid; c < n_c; c += kFewThreads) {
+    const float4* cr = reinterpret_cast<const float4*>(cb + static_cast<int64_t>(c) * d_s);
+    float4 cv[8];
+#pragma unroll
+    for (int s4 = 0; s4 < 8; ++s4) cv[s4] = (s4 * 4 < d_s) ? cr[s4] : make_float4(0.f, 0.f, 0.f, 0.f);
+    float acc = 0.0f;
+#pragma unroll
+    for (int s4 = 0; s4 < 8; ++s4) {
+      if (s4 * 4 < d_s) {
+        acc = fma_rn(x[s4 * 4 + 0], cv[s4].x, acc);
+        acc = fma_rn(x[s4 * 4 + 1], cv[s4].y, acc);
+        acc = fma_rn(x[s4 * 4 + 2], cv[s4].z, acc);
+        acc = fma_rn(x[s4 * 4 + 3], cv[s4].w, acc);
+      }
+    }
+    if (scale) acc = acc / temperature;
+    keep_top<TM>(best, composite_key(acc, static_cast<uint32_t>(c)));
+  }
+  // each wave's top `top`, then wave 0 merges the waves' lists
+  for (int p = 0; p < TM; ++p) {
+    const uint64_t v = (p < top) ? wave_pop_max<TM>(best) : 0ull;
+    if (lane == 0) s_top[wave][p] = v;
+  }
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll
+  for (int p = 0; p < TM; ++p) best[p] = 0ull;
+  for (int e = lane; e < kFewWaves * TM; e += 64) keep_top<TM>(best, s_top[e / TM][e % TM]);
+  int32_t* out = a.codes + grow * top;
+  for (int p = 0; p < top; ++p) {
+    const uint64_t v = wave_pop_max<TM>(best);
+    if (lane == 0) out[p] = static_cast<int32_t>(key_index(v));
+  }
+}
+
+int launch_topk_few(const FewTopk& t0, const FewTopk& t1, int h, const float* chat, int n_c, int d_s,
+                    float temperature, hipStream_t st) {
+  const int top = std::max(t0.top, t1.total > 0 ? t1.top : 0);
+  const dim3 grid(static_cast<unsigned>(std::max(t0.total, t1.total)), t1.total > 0 ? 2u : 1u);
+  if (top <= 4) code_topk_few_kernel<4><<<grid, kFewThreads, 0, st>>>(t0, t1, h, chat, n_c, d_s, temperature);
+  else if (top <= 8) code_topk_few_kernel<8><<<grid, kFewThreads, 0, st>>>(t0, t1, h, chat, n_c, d_s, temperature);
+  else if (top <= 16) code_topk_few_kernel<16><<<grid, kFewThreads, 0, st>>>(t0, t1, h, chat, n_c, d_s, temperature);
+  else code_topk_few_kernel<32><<<grid, kFewThreads, 0, st>>>(t0, t1, h, chat, n_c, d_s, temperature);
+  return check_launch("code_topk_few_kernel");
+}
+
+// Decoding's few rows, in two launches that spread the codebook over the chip
+// (one block reading a head's whole codebook is bound by the requests a
+// single CU keeps in flight).
+//   1. code_scores_few_kernel: block (head, 256-code chunk) loads its codes
+//      once and writes score_key(score) of each code for every row of that
+//      head in both tasks: scores [row][n_c], canonical fp32 order.
+//   2. code_select_few_kernel: one block per row holds the row's n_c keys
+//      in registers.  The top-th largest of the threads' maxima bounds the
+//      row's top-th key from below; the keys at or above it (about `top`)
+//      are ranked exactly against each other.  When too many keys pass
+//      (the best keys crowd into few threads) a radix select over the score
+//      bits finds the threshold instead (8-bit digits, most significant
+//      first; ties on the score at the threshold go to the lowest codes,
+//      counted in code order by a block scan).  The row's `top` codes are
+//      written in descending key order (score desc, code asc).
+struct FewScore {
+  const float* xhat;    // [total][d_s]
+  int64_t rows, total;  // rows per (batch, head); total = batch * h * rows
+  int top;
+  uint32_t* scores;     // [total][n_c]
+  int32_t* codes;       // [total][top]
+};
+
+constexpr int kScoreChunk = 256;
+constexpr int kFewSelThreads = 256;
+constexpr int kFewSelMaxCodes = 16384;  // n_c keys of 4 bytes in 64 KB of LDS
+
+__global__ __launch_bounds__(kScoreChunk) void code_scores_few_kernel(FewScore t0, FewScore t1, int h,
+                                                                      const float* __restrict__ chat,
+                                                                      int n_c, int d_s, float temperature) {
+  const int hh = blockIdx.x;
+  const int c = blockIdx.y * kScoreChunk + threadIdx.x;
+  if (c >= n_c) return;
+  const float4* cr = reinterpret_cast<const float4*>(chat + (static_cast<int64_t>(hh) * n_c + c) * d_s);
+  float4 cv[8];
+#pragma unroll
+  for (int s4 = 0; s4 < 8; ++s4) cv[s4] = (s4 * 4 < d_s) ? cr[s4] : make_float4(0.f, 0.f, 0.f, 0.f);
+  const bool scale = (temperature != 1.0f);
+  for (int task = 0; task < 2; ++task) {
+    const FewScore& a = task ? t1 : t0;
+    if (a.total == 0) continue;
+    const int64_t nb = a.total / (a.rows * h);
+    for (int64_t b = 0; b < nb; ++b) {
+      for (int64_t i = 0; i < a.rows; ++i) {
+        const int64_t grow = (b * h + hh) * a.rows + i;
+        const float* x = a.xhat + grow * d_s;
+        float acc = 0.0f;
+#pragma unroll
+        for (int s4 = 0; s4 < 8; ++s4) {
+          if (s4 * 4 < d_s) {
+            acc = fma_rn(x[s4 * 4 + 0], cv[s4].x, acc);
+            acc = fma_rn(x[s4 * 4 + 1], cv[s4].y, acc);
+            acc = fma_rn(x[s4 * 4 + 2], cv[s4].z, acc);
+            acc = fma_rn(x[s4 * 4 + 3], cv[s4].w, acc);
+          }
+        }
+        if (scale) acc = acc / temperature;
+        a.scores[grow * n_c + c] = score_key(acc);
+      }
+    }
+  }
+}
+
+constexpr int kFewCandMax = 256;
+
+template <int KPT>  // keys per thread: n_c <= KPT * kFewSelThreads
+__global__ __launch_bounds__(kFewSelThreads) void code_select_few_kernel(FewScore t0, FewScore t1, int n_c) {
+  extern __shared__ __align__(16) uint32_t few_keys[];  // [n_c] (for the radix select)
+  __shared__ uint64_t s_max[kFewSelThreads];
+  __shared__ uint64_t s_cand[kFewCandMax];
+  __shared__ uint64_t s_thr;
+  __shared__ uint32_t hist[256];
+  __shared__ uint32_t s_wsum[kFewSelThreads / 64];
+  __shared__ uint32_t s_lo[kFewSelThreads / 64], s_hi[kFewSelThreads / 64];
+  __shared__ uint32_t s_prefix, s_need, s_cnt, s_nsel;
+  const FewScore& a = blockIdx.y ? t1 : t0;
+  const int64_t grow = blockIdx.x;
+  if (grow >= a.total) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int top = a.top;
+  const uint32_t* src = a.scores + grow * n_c;
+  int32_t* out = a.codes + grow * top;
+  // thread t holds codes t, t + 256, ... (loads clamped in bounds, all issued at once)
+  uint32_t u[KPT];
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) u[j] = src[min(tid + j * kFewSelThreads, n_c - 1)];
+  const auto key_of = [](uint32_t v, int c) {
+    return (static_cast<uint64_t>(v) << 32) | static_cast<uint64_t>(0xFFFFFFFFu - static_cast<uint32_t>(c));
+  };
+  uint64_t best = 0ull;
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) {
+    const int c = tid + j * kFewSelThreads;
+    if (c < n_c) {
+      few_keys[c] = u[j];
+      const uint64_t k = key_of(u[j], c);
+      best = k > best ? k : best;
+    }
+  }
+  s_max[tid] = best;
+  if (tid == 0) s_cnt = 0u;
+  __syncthreads();
+  // The top-th largest of the threads' maxima, T, has `top` keys at or above
+  // it, so the row's top-th largest key is >= T: the keys >= T are the
+  // candidates (about `top` of them unless the best keys crowd into a few
+  // threads).  At least `top` threads hold keys (n_c >= top), so exactly one
+  // thread's maximum has rank top - 1.
+  int r = 0;
+#pragma unroll 16
+  for (int i = 0; i < kFewSelThreads; ++i) r += (s_max[i] > best) ? 1 : 0;
+  if (best != 0ull && r == top - 1) s_thr = best;
+  __syncthreads();
+  const uint64_t thr = s_thr;
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) {
+    const int c = tid + j * kFewSelThreads;
+    const uint64_t k = key_of(u[j], c);
+    if (c < n_c && k >= thr) {
+      const uint32_t slot = atomicAdd(&s_cnt, 1u);
+      if (slot < kFewCandMax) s_cand[slot] = k;
+    }
+  }
+  __syncthreads();
+  const uint32_t cnt = s_cnt;
+  if (cnt <= kFewCandMax) {
+    if (tid < static_cast<int>(cnt)) {
+      const uint64_t k = s_cand[tid];
+      int rk = 0;
+      for (uint32_t j = 0; j < cnt; ++j) rk += (s_cand[j] > k) ? 1 : 0;
+      if (rk < top) out[rk] = static_cast<int32_t>(key_index(k));
+    }
+    return;
+  }
+
+  // Too many candidates: radix select of the top-th largest score key over
+  // the row in LDS.  The bits every key shares are known from the row's
+  // minimum and maximum; the digits start below them.
+  uint32_t lo = 0xFFFFFFFFu, hi = 0u;
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) {
+    if (tid + j * kFewSelThreads < n_c) {
+      lo = min(lo, u[j]);
+      hi = max(hi, u[j]);
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    lo = min(lo, static_cast<uint32_t>(__shfl_xor(static_cast<int>(lo), o)));
+    hi = max(hi, static_cast<uint32_t>(__shfl_xor(static_cast<int>(hi), o)));
+  }
+  if (lane == 0) {
+    s_lo[wave] = lo;
+    s_hi[wave] = hi;
+  }
+  if (tid == 0) s_nsel = 0u;
+  __syncthreads();
+#pragma unroll
+  for (int w = 0; w < kFewSelThreads / 64; ++w) {
+    lo = min(lo, s_lo[w]);
+    hi = max(hi, s_hi[w]);
+  }
+  int rem = (lo == hi) ? 0 : 32 - __clz(lo ^ hi);
+  uint32_t mask = (rem == 32) ? 0u : ~((1u << rem) - 1u);
+  uint32_t prefix = hi & mask, need = static_cast<uint32_t>(top);
+  while (rem > 0) {
+    const int shift = rem > 8 ? rem - 8 : 0;
+    hist[tid] = 0u;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+      if (tid + j * kFewSelThreads < n_c && (u[j] & mask) == prefix)
+        atomicAdd(&hist[(u[j] >> shift) & 255u], 1u);
+    }
+    __syncthreads();
+    if (wave == 0) {
+      // lane l holds digits 255 - 4l .. 252 - 4l (descending)
+      uint32_t hv[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) hv[j] = hist[255 - 4 * lane - j];
+      const uint32_t sum = hv[0] + hv[1] + hv[2] + hv[3];
+      uint32_t incl = sum;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t y = __shfl_up(incl, o);
+        if (lane >= o) incl += y;
+      }
+      const uint32_t excl = incl - sum;
+      if (excl < need && incl >= need) {
+        uint32_t cum = excl, left = 0u;
+        int digit = -1;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if (digit < 0 && cum + hv[j] >= need) {
+            digit = 255 - 4 * lane - j;
+            left = need - cum;
+          }
+          cum += hv[j];
+        }
+        s_prefix = prefix | (static_cast<uint32_t>(digit) << shift);
+        s_need = left;
+      }
+    }
+    __syncthreads();
+    prefix = s_prefix;
+    need = s_need;
+    mask |= ((1u << (rem - shift)) - 1u) << shift;
+    rem = shift;
+  }
+  // keys above the threshold, and the `need` lowest codes tied on it
+  // (counted in code order: thread t scans codes [t * per, (t + 1) * per))
+  const int per = (n_c + kFewSelThreads - 1) / kFewSelThreads;
+  const int c0 = tid * per, c1 = min(n_c, c0 + per);
+  uint32_t ties = 0u;
+  for (int c = c0; c < c1; ++c) ties += (few_keys[c] == prefix) ? 1u : 0u;
+  uint32_t incl = ties;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t y = __shfl_up(incl, o);
+    if (lane >= o) incl += y;
+  }
+  if (lane == 63) s_wsum[wave] = incl;
+  __syncthreads();
+  uint32_t rank = incl - ties;
+  for (int w = 0; w < wave; ++w) rank += s_wsum[w];
+  for (int c = c0; c < c1; ++c) {
+    const uint32_t v = few_keys[c];
+    bool take = v > prefix;
+    if (v == prefix) take = (rank++ < need);
+    if (take) s_cand[atomicAdd(&s_nsel, 1u)] = key_of(v, c);  // exactly `top` keys
+  }
+  __syncthreads();
+  if (tid >= top) return;
+  const uint64_t k = s_cand[tid];
+  int rk = 0;
+  for (int j = 0; j < top; ++j) rk += (s_cand[j] > k) ? 1 : 0;
+  out[rk] = static_cast<int32_t>(key_index(k));
+}
+
+int launch_topk_few_split(const FewScore& t0, const FewScore& t1, int h, const float* chat, int n_c, int d_s,
+                          float temperature, hipStream_t st) {
+  const dim3 g1(static_cast<unsigned>(h), static_cast<unsigned>(ceil_div(n_c, kScoreChunk)));
+  code_scores_few_kernel<<<g1, kScoreChunk, 0, st>>>(t0, t1, h, chat, n_c, d_s, temperature);
+  if (int s = check_launch("code_scores_few_kernel")) return s;
+  const dim3 g2(static_cast<unsigned>(std::max(t0.total, t1.total)), t1.total > 0 ? 2u : 1u);
+  const size_t smem = sizeof(uint32_t) * static_cast<size_t>(n_c);
+  if (n_c <= 4 * kFewSelThreads) code_select_few_kernel<4><<<g2, kFewSelThreads, smem, st>>>(t0, t1, n_c);
+  else if (n_c <= 16 * kFewSelThreads) code_select_few_kernel<16><<<g2, kFewSelThreads, smem, st>>>(t0, t1, n_c);
+  else code_select_few_kernel<64><<<g2, kFewSelThreads, smem, st>>>(t0, t1, n_c);
+  return check_launch("code_select_few_kernel");
+}
+
 struct TopkWorkspace {
   uint16_t* cbf;
   uint32_t* cmax_bits;
@@ -1218,6 +1671,8 @@ TopkWorkspace carve_topk(void* ws, int h, int n_c) {
   w.flags = reinterpret_cast<uint8_t*>(p);
   return w;
 }
+
+constexpr int64_t kFewTopkRows = 64;
 
 bool mfma_path_ok(int top, int d_s, int n_c) { return top <= 32 && d_s <= 32 && d_s % 4 == 0 && n_c <= 65535; }
 
@@ -1278,6 +1733,26 @@ int launch_mfma_q(const float* xhat, int64_t batch, int h, int64_t rows, const f
 // Top codes per row.  With a workspace (and top <= 32, d_s <= 32) the matrix-core
 // filter runs and the exact kernel recomputes only flagged groups; otherwise the
 // exact kernel handles every row.  `prepped` = the bf16 codebook is already in w.
+int launch_code_topk_w(const float* xhat, int64_t batch, int h, int64_t rows, const float* chat,
+                       int n_c, int d_s, float temperature, int top, int32_t* codes,
+                       const TopkWorkspace& w, hipStream_t st) {
+  // A handful of rows (decoding): every row exhaustively, one wave each.  The
+  // matrix-core screen streams the whole codebook through one block per 256
+  // rows, so for a few rows it runs one long dependent chain per head.
+  if (batch * h * rows <= kFewTopkRows) {
+    const FewTopk t0{xhat, rows, batch * h * rows, top, codes};
+    FewTopk none{};
+    return launch_topk_few(t0, none, h, chat, n_c, d_s, temperature, st);
+  }
+  int s;
+  if (top <= 4) s = launch_mfma_q<1>(xhat, batch, h, rows, chat, n_c, d_s, temperature, top, codes, w, st);
+  else if (top <= 8) s = launch_mfma_q<2>(xhat, batch, h, rows, chat, n_c, d_s, temperature, top, codes, w, st);
+  else if (top <= 16) s = launch_mfma_q<4>(xhat, batch, h, rows, chat, n_c, d_s, temperature, top, codes, w, st);
+  else s = launch_mfma_q<8>(xhat, batch, h, rows, chat, n_c, d_s, temperature, top, codes, w, st);
+  if (s) return s;
+  return launch_flagged_topk(xhat, batch, h, rows, chat, n_c, d_s, temperature, top, codes, w.flags, st);
+}
+
 int launch_code_topk(const float* xhat, int64_t batch, int h, int64_t rows, const float* chat,
                      int n_c, int d_s, float temperature, int top, int32_t* codes, void* ws,
                      bool prepped, hipStream_t st) {
@@ -1287,12 +1762,7 @@ int launch_code_topk(const float* xhat, int64_t batch, int h, int64_t rows, cons
   const TopkWorkspace w = carve_topk(ws, h, n_c);
   int s;
   if (!prepped && (s = launch_codebook_prep(chat, h, n_c, d_s, w, st))) return s;
-  if (top <= 4) s = launch_mfma_q<1>(xhat, batch, h, rows, chat, n_c, d_s, temperature, top, codes, w, st);
-  else if (top <= 8) s = launch_mfma_q<2>(xhat, batch, h, rows, chat, n_c, d_s, temperature, top, codes, w, st);
-  else if (top <= 16) s = launch_mfma_q<4>(xhat, batch, h, rows, chat, n_c, d_s, temperature, top, codes, w, st);
-  else s = launch_mfma_q<8>(xhat, batch, h, rows, chat, n_c, d_s, temperature, top, codes, w, st);
-  if (s) return s;
-  return launch_flagged_topk(xhat, batch, h, rows, chat, n_c, d_s, temperature, top, codes, w.flags, st);
+  return launch_code_topk_w(xhat, batch, h, rows, chat, n_c, d_s, temperature, top, codes, w, st);
 }
 
 int launch_normalize(const float* x, int64_t rows, int d_s, float* out, hipStream_t st) {
@@ -1303,6 +1773,96 @@ int launch_normalize(const float* x, int64_t rows, int d_s, float* out, hipStrea
 }
 
 }  // namespace
+
+// ---- routing of a few new rows against a codebook prepared once (decoding)
+
+size_t decode_prep_bytes(int h_kv, int n_c, int d_s) {
+  return align_up(sizeof(float) * static_cast<size_t>(h_kv) * n_c * d_s, 256) +
+         align_up(sizeof(uint16_t) * static_cast<size_t>(h_kv) * n_c_padded(n_c) * 32, 256) +
+         align_up(sizeof(float) * static_cast<size_t>(h_kv), 256);
+}
+
+namespace {
+struct DecodePrep {
+  float* chat;
+  TopkWorkspace w;
+};
+DecodePrep carve_prep(const void* prep, int h_kv, int n_c, int d_s) {
+  char* c = static_cast<char*>(const_cast<void*>(prep));
+  DecodePrep d{};
+  d.chat = reinterpret_cast<float*>(c);
+  c += align_up(sizeof(float) * static_cast<size_t>(h_kv) * n_c * d_s, 256);
+  d.w.cbf = reinterpret_cast<uint16_t*>(c);
+  c += align_up(sizeof(uint16_t) * static_cast<size_t>(h_kv) * n_c_padded(n_c) * 32, 256);
+  d.w.cmax_bits = reinterpret_cast<uint32_t*>(c);
+  d.w.flags = nullptr;
+  return d;
+}
+}  // namespace
+
+int decode_prep(const float* codebook, int h_kv, int n_c, int d_s, void* prep, hipStream_t st) {
+  const DecodePrep d = carve_prep(prep, h_kv, n_c, d_s);
+  if (int s = launch_normalize(codebook, static_cast<int64_t>(h_kv) * n_c, d_s, d.chat, st)) return s;
+  return launch_codebook_prep(d.chat, h_kv, n_c, d_s, d.w, st);
+}
+
+size_t route_prepped_ws_bytes(int64_t batch, int64_t n, int h_kv, int d_s, int n_c) {
+  const size_t rows = static_cast<size_t>(batch * h_kv * n);
+  size_t bytes = 2 * align_up(sizeof(float) * rows * d_s, 256) + align_up(rows, 256);
+  if (static_cast<int64_t>(rows) <= kFewTopkRows) bytes += 2 * align_up(sizeof(uint32_t) * rows * n_c, 256);
+  return bytes;
+}
+
+int route_codes_prepped(const void* q, const void* k, int dtype, int64_t batch, int64_t n, int h_q,
+                        int h_kv, int d, int64_t q_sb, int64_t q_sn, int64_t q_sh, int64_t k_sb,
+                        int64_t k_sn, int64_t k_sh, const float* w_qr, const float* w_kr,
+                        const void* prep, int d_s, int n_c, int a, int b, float temperature,
+                        int32_t* q_codes, int32_t* k_codes, void* ws, hipStream_t st) {
+  const int g = h_q / h_kv;
+  int s = check_route_vectors(dtype, batch, n, h_q, g, d, d_s);
+  if (!s) s = check_route_vectors(dtype, batch, n, h_kv, 1, d, d_s);
+  if (!s) s = check_code_topk(batch, h_kv, n, n_c, d_s, temperature, a);
+  if (!s) s = check_code_topk(batch, h_kv, n, n_c, d_s, temperature, b);
+  if (s) return s;
+  if (batch * n == 0) return SSA_OK;
+  const size_t vec = align_up(sizeof(float) * static_cast<size_t>(batch * h_kv * n * d_s), 256);
+  float* qhat = static_cast<float*>(ws);
+  float* khat = reinterpret_cast<float*>(static_cast<char*>(ws) + vec);
+  DecodePrep dp = carve_prep(prep, h_kv, n_c, d_s);
+  dp.w.flags = reinterpret_cast<uint8_t*>(static_cast<char*>(ws) + 2 * vec);
+  const int64_t rows = batch * h_kv * n;
+  if (rows <= kFewTopkRows && mfma_path_ok(a, d_s, n_c) && mfma_path_ok(b, d_s, n_c) &&
+      route_few_smem(g, d, d_s) <= 64 * 1024) {
+    // a decoding step's few rows: queries and keys in one launch per stage
+    const FewRoute rq{q, n, q_sb, q_sn, q_sh, rows, h_q, g, d, d_s, w_qr, qhat};
+    const FewRoute rk{k, n, k_sb, k_sn, k_sh, rows, h_kv, 1, d, d_s, w_kr, khat};
+    if ((s = launch_route_few(rq, rk, dtype, st))) return s;
+    if (n_c <= kFewSelMaxCodes) {
+      char* sc = static_cast<char*>(ws) + 2 * vec + align_up(static_cast<size_t>(rows), 256);
+      const size_t sc_bytes = align_up(sizeof(uint32_t) * static_cast<size_t>(rows * n_c), 256);
+      const FewScore sq{qhat, n, rows, a, reinterpret_cast<uint32_t*>(sc), q_codes};
+      const FewScore sk{khat, n, rows, b, reinterpret_cast<uint32_t*>(sc + sc_bytes), k_codes};
+      return launch_topk_few_split(sq, sk, h_kv, dp.chat, n_c, d_s, temperature, st);
+    }
+    const FewTopk tq{qhat, n, rows, a, q_codes};
+    const FewTopk tk{khat, n, rows, b, k_codes};
+    return launch_topk_few(tq, tk, h_kv, dp.chat, n_c, d_s, temperature, st);
+  }
+  if ((s = launch_route_vectors(q, dtype, batch, n, h_q, g, d, q_sb, q_sn, q_sh, w_qr, d_s, qhat, st))) return s;
+  if ((s = launch_route_vectors(k, dtype, batch, n, h_kv, 1, d, k_sb, k_sn, k_sh, w_kr, d_s, khat, st))) return s;
+  for (int pass = 0; pass < 2; ++pass) {
+    const float* x = pass ? khat : qhat;
+    const int top = pass ? b : a;
+    int32_t* codes = pass ? k_codes : q_codes;
+    if (mfma_path_ok(top, d_s, n_c))
+      s = launch_code_topk_w(x, batch, h_kv, n, dp.chat, n_c, d_s, temperature, top, codes, dp.w, st);
+    else
+      s = launch_exact_topk(x, batch, h_kv, n, dp.chat, n_c, d_s, temperature, top, codes, st);
+    if (s) return s;
+  }
+  return SSA_OK;
+}
+
 }  // namespace ssa
 
 using namespace ssa;

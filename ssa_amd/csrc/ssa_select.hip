@@ -22,6 +22,7 @@
 #include <mutex>
 
 #include "ssa_common.h"
+#include "ssa_internal.h"
 #include "ssa_rows.h"
 
 namespace ssa {
@@ -56,6 +57,19 @@ struct SelParams {
   int64_t n_q, q_pos0;   // query rows (q, q_codes, out, stats) and the position of row 0
   int64_t rows;          // batch * h_kv * n_q
   const int32_t* order;  // nullable [rows]: slot t of head bh runs query row order[bh * n_q + t]
+  // Postings per (batch, kv head) of the index: n * b for an index over every
+  // key; fewer when a tail index holds the newest keys (incremental decoding).
+  int64_t post_bh;
+  // Optional second (tail) index over the keys appended since the main index
+  // was built: offsets [bh][n_c + 1], postings [bh][tail_bh] holding key -
+  // tail_key0.  A row's candidates are the union over both indices' buckets of
+  // its codes; nseg = a without a tail, 2a with one (segment s >= a: tail
+  // bucket of code s - a).
+  const int32_t* tail_offsets;
+  const int32_t* tail_postings;
+  int64_t tail_bh;
+  int32_t tail_key0;
+  int nseg;
 };
 
 // Row ((b * h_kv + h) * n_q + r) processed in slot t of the launch
@@ -231,7 +245,8 @@ __device__ __forceinline__ void select_row(const SelParams& p, const T* __restri
   const int64_t bb = bh / p.h_kv;
   const T* q0 = qg + bb * p.q_sb + r * p.q_sn + static_cast<int64_t>(h * p.g) * p.q_sh;
   const T* kbase = static_cast<const T*>(p.k) + bb * p.k_sb + static_cast<int64_t>(h) * p.k_sh;
-  const int32_t* pp = p.postings + bh * p.n * p.b;
+  const int32_t* pp = p.postings + bh * p.post_bh;
+  const int32_t* tp = p.tail_postings ? p.tail_postings + bh * p.tail_bh : nullptr;
   const uint8_t* mrow =
       (p.mask_mode == SSA_MASK_DENSE) ? p.mask + bb * p.mask_sb + i * p.mask_si : nullptr;
 
@@ -244,11 +259,12 @@ __device__ __forceinline__ void select_row(const SelParams& p, const T* __restri
   // start positions in the concatenated list.
   if (tid < 64) {
     int32_t lo = 0, len = 0;
-    if (tid < p.a) {
-      const int32_t c = p.q_codes[(bh * p.n_q + r) * p.a + tid];
+    if (tid < p.nseg) {
+      const bool tl = tid >= p.a;
+      const int32_t c = p.q_codes[(bh * p.n_q + r) * p.a + (tl ? tid - p.a : tid)];
       if (static_cast<uint32_t>(c) < static_cast<uint32_t>(p.n_c)) {
-        const int32_t* off = p.offsets + bh * (p.n_c + 1);
-        const int32_t total = static_cast<int32_t>(p.n * p.b);
+        const int32_t* off = (tl ? p.tail_offsets : p.offsets) + bh * (p.n_c + 1);
+        const int32_t total = static_cast<int32_t>(tl ? p.tail_bh : p.post_bh);
         lo = min(max(off[c], 0), total);
         len = min(max(off[c + 1], lo), total) - lo;
       }
@@ -259,7 +275,7 @@ __device__ __forceinline__ void select_row(const SelParams& p, const T* __restri
       const int32_t y = __shfl_up(x, o, 64);
       if (tid >= o) x += y;
     }
-    if (tid < p.a) {
+    if (tid < p.nseg) {
       seg_lo[tid] = lo;
       seg_start[tid + 1] = x;
     }
@@ -273,7 +289,7 @@ __device__ __forceinline__ void select_row(const SelParams& p, const T* __restri
     }
   }
   __syncthreads();
-  const int R = seg_start[p.a];
+  const int R = seg_start[p.nseg];
   const bool causal = p.mask_mode == SSA_MASK_CAUSAL;
 
   // Union of the row's postings into the bitmap.  With `collect`, new keys also
@@ -285,13 +301,14 @@ __device__ __forceinline__ void select_row(const SelParams& p, const T* __restri
       const int pidx = base + tid;
       bool in_window = false;
       if (pidx < R) {
-        int lo_m = 0, hi_m = p.a;
+        int lo_m = 0, hi_m = p.nseg;
         while (hi_m - lo_m > 1) {
           const int mid = (lo_m + hi_m) >> 1;
           if (seg_start[mid] <= pidx) lo_m = mid;
           else hi_m = mid;
         }
-        const int32_t j = pp[seg_lo[lo_m] + (pidx - seg_start[lo_m])];
+        const int32_t e = seg_lo[lo_m] + (pidx - seg_start[lo_m]);
+        const int32_t j = lo_m < p.a ? pp[e] : tp[e] + p.tail_key0;
         in_window = !causal || j <= i;
         const bool allowed = (static_cast<uint32_t>(j) < static_cast<uint32_t>(p.n)) && in_window &&
                              ((mrow == nullptr) || (mrow[j] != 0));
@@ -561,7 +578,8 @@ __global__ __launch_bounds__(64) void select_light_kernel(SelParams p, int64_t r
   const int64_t bh = row / p.n_q;
   const int h = static_cast<int>(bh % p.h_kv);
   const int64_t bb = bh / p.h_kv;
-  const int32_t* pp = p.postings + bh * p.n * p.b;
+  const int32_t* pp = p.postings + bh * p.post_bh;
+  const int32_t* tp = p.tail_postings ? p.tail_postings + bh * p.tail_bh : nullptr;
   const bool causal = p.mask_mode == SSA_MASK_CAUSAL;
   const uint8_t* mrow = (p.mask_mode == SSA_MASK_DENSE) ? p.mask + bb * p.mask_sb + i * p.mask_si : nullptr;
   const int live = causal ? static_cast<int>(i >> 5) + 1 : words;
@@ -574,11 +592,12 @@ __global__ __launch_bounds__(64) void select_light_kernel(SelParams p, int64_t r
   }
 
   int32_t lo = 0, len = 0;
-  if (lane < p.a) {
-    const int32_t c = p.q_codes[(bh * p.n_q + r) * p.a + lane];
+  if (lane < p.nseg) {
+    const bool tl = lane >= p.a;
+    const int32_t c = p.q_codes[(bh * p.n_q + r) * p.a + (tl ? lane - p.a : lane)];
     if (static_cast<uint32_t>(c) < static_cast<uint32_t>(p.n_c)) {
-      const int32_t* off = p.offsets + bh * (p.n_c + 1);
-      const int32_t total = static_cast<int32_t>(p.n * p.b);
+      const int32_t* off = (tl ? p.tail_offsets : p.offsets) + bh * (p.n_c + 1);
+      const int32_t total = static_cast<int32_t>(tl ? p.tail_bh : p.post_bh);
       lo = min(max(off[c], 0), total);
       len = min(max(off[c + 1], lo), total) - lo;
     }
@@ -601,18 +620,21 @@ __global__ __launch_bounds__(64) void select_light_kernel(SelParams p, int64_t r
   };
   // Buckets kLightBatch at a time: their postings are loaded together, then
   // marked (the bitmap, the counts and the summary do not depend on the order).
-  for (int m0 = 0; m0 < p.a; m0 += kLightBatch) {
+  for (int m0 = 0; m0 < p.nseg; m0 += kLightBatch) {
     int lo_u[kLightBatch], len_u[kLightBatch], most = 0;
 #pragma unroll
     for (int u = 0; u < kLightBatch; ++u) {
       lo_u[u] = __shfl(lo, min(m0 + u, 63));
-      len_u[u] = (m0 + u < p.a) ? __shfl(len, min(m0 + u, 63)) : 0;
+      len_u[u] = (m0 + u < p.nseg) ? __shfl(len, min(m0 + u, 63)) : 0;
       most = max(most, len_u[u]);
     }
     for (int base = 0; base < most; base += 64) {
       int32_t j_u[kLightBatch];
 #pragma unroll
-      for (int u = 0; u < kLightBatch; ++u) j_u[u] = (base + lane < len_u[u]) ? pp[lo_u[u] + base + lane] : -1;
+      for (int u = 0; u < kLightBatch; ++u)
+        j_u[u] = (base + lane < len_u[u]) ? (m0 + u < p.a ? pp[lo_u[u] + base + lane]
+                                                          : tp[lo_u[u] + base + lane] + p.tail_key0)
+                                          : -1;
 #pragma unroll
       for (int u = 0; u < kLightBatch; ++u)
         if (base + lane < len_u[u]) add(j_u[u]);
@@ -1297,15 +1319,19 @@ extern "C" size_t ssa_select_workspace_bytes(int64_t batch, int64_t n, int h_kv,
   return sel_ws_fixed(rows) + 256 + align_up(static_cast<size_t>(rows) * static_cast<size_t>(k_eff), 256) * 8;
 }
 
-extern "C" int ssa_select_block(const void* q, const void* k, int dtype, int64_t batch, int64_t n,
-                                int64_t n_q, int64_t q_pos0, int h_q, int h_kv, int d, int64_t q_sb,
-                                int64_t q_sn, int64_t q_sh, int64_t k_sb, int64_t k_sn, int64_t k_sh,
-                                const int32_t* q_codes, int a, const int32_t* offsets,
-                                const int32_t* postings, int n_c, int b, int top_k, int mask_mode,
-                                const uint8_t* mask, int64_t mask_sb, int64_t mask_si,
-                                float score_div, int sorted, const int32_t* row_order, void* out,
-                                int out_index_dtype, int32_t* stats, void* workspace,
-                                size_t workspace_bytes, void* stream) {
+namespace ssa {
+// ssa_select_block, optionally with a tail index (tail_offsets non-null): the
+// main index covers post_bh / b keys per (batch, kv head) and the tail index
+// the keys from tail_key0 on (see SelParams).
+int select_entry(const void* q, const void* k, int dtype, int64_t batch, int64_t n, int64_t n_q,
+                 int64_t q_pos0, int h_q, int h_kv, int d, int64_t q_sb, int64_t q_sn, int64_t q_sh,
+                 int64_t k_sb, int64_t k_sn, int64_t k_sh, const int32_t* q_codes, int a,
+                 const int32_t* offsets, const int32_t* postings, int n_c, int b, int top_k,
+                 int mask_mode, const uint8_t* mask, int64_t mask_sb, int64_t mask_si,
+                 float score_div, int sorted, const int32_t* row_order, void* out,
+                 int out_index_dtype, int32_t* stats, void* workspace, size_t workspace_bytes,
+                 void* stream, int64_t post_bh, const int32_t* tail_offsets,
+                 const int32_t* tail_postings, int64_t tail_bh, int64_t tail_key0) {
   if (n_q < 0 || q_pos0 < 0 || q_pos0 + n_q > n)
     return fail(SSA_ERR_INVALID_ARGUMENT, "select: query rows [%lld, %lld) outside the %lld keys",
                 static_cast<long long>(q_pos0), static_cast<long long>(q_pos0 + n_q),
@@ -1373,6 +1399,20 @@ extern "C" int ssa_select_block(const void* q, const void* k, int dtype, int64_t
   p.q_pos0 = q_pos0;
   p.rows = batch * h_kv * n_q;
   p.order = row_order;
+  p.post_bh = post_bh;
+  p.nseg = a;
+  if (tail_offsets) {
+    if (2 * a > kMaxA)
+      return fail(SSA_ERR_UNSUPPORTED, "select: a tail index needs codes_per_query <= %d", kMaxA / 2);
+    if (!tail_postings || tail_bh < 0 || tail_key0 < 0 || tail_key0 > n || post_bh < 0 ||
+        tail_bh >= (int64_t(1) << 31) || post_bh >= (int64_t(1) << 31))
+      return fail(SSA_ERR_INVALID_ARGUMENT, "select: bad tail index");
+    p.tail_offsets = tail_offsets;
+    p.tail_postings = tail_postings;
+    p.tail_bh = tail_bh;
+    p.tail_key0 = static_cast<int32_t>(tail_key0);
+    p.nseg = 2 * a;
+  }
   const size_t smem = select_smem(n, p.sortn, p.k_eff);
   if (smem > 160 * 1024)
     return fail(SSA_ERR_UNSUPPORTED, "select: needs %zu bytes of LDS (n=%lld, top_k=%d)", smem,
@@ -1383,6 +1423,7 @@ extern "C" int ssa_select_block(const void* q, const void* k, int dtype, int64_t
   if (dtype == SSA_DTYPE_BF16) return dispatch_select<uint16_t>(p, rows, smem, workspace, workspace_bytes, st);
   return dispatch_select<float>(p, rows, smem, workspace, workspace_bytes, st);
 }
+}  // namespace ssa
 
 // ---------------------------------------------------------------- no-alloc variant
 //
@@ -1463,6 +1504,21 @@ extern "C" int ssa_select_block_noalloc(const void* q, const void* k, int dtype,
                           k_sn, k_sh, q_codes, a, offsets, postings, n_c, b, top_k, mask_mode, mask,
                           mask_sb, mask_si, score_div, sorted, row_order, out, out_index_dtype,
                           stats, ws, bytes, stream);
+}
+
+extern "C" int ssa_select_block(const void* q, const void* k, int dtype, int64_t batch, int64_t n,
+                                int64_t n_q, int64_t q_pos0, int h_q, int h_kv, int d, int64_t q_sb,
+                                int64_t q_sn, int64_t q_sh, int64_t k_sb, int64_t k_sn, int64_t k_sh,
+                                const int32_t* q_codes, int a, const int32_t* offsets,
+                                const int32_t* postings, int n_c, int b, int top_k, int mask_mode,
+                                const uint8_t* mask, int64_t mask_sb, int64_t mask_si,
+                                float score_div, int sorted, const int32_t* row_order, void* out,
+                                int out_index_dtype, int32_t* stats, void* workspace,
+                                size_t workspace_bytes, void* stream) {
+  return ssa::select_entry(q, k, dtype, batch, n, n_q, q_pos0, h_q, h_kv, d, q_sb, q_sn, q_sh, k_sb,
+                           k_sn, k_sh, q_codes, a, offsets, postings, n_c, b, top_k, mask_mode, mask,
+                           mask_sb, mask_si, score_div, sorted, row_order, out, out_index_dtype,
+                           stats, workspace, workspace_bytes, stream, n * b, nullptr, nullptr, 0, 0);
 }
 
 extern "C" int ssa_select(const void* q, const void* k, int dtype, int64_t batch, int64_t n,

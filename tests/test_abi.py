@@ -312,3 +312,38 @@ def test_select_workspace_regions_do_not_overlap(L, batch, n, h_kv, top_k):
                 assert cap == 0
     assert L.ssa_select_workspace_layout(batch, n, h_kv, lo - 1, 1, (ctypes.c_int64 * 10)()) \
         == _lib.SSA_ERR_WORKSPACE
+
+
+def _decode(L, **kw):
+    a = dict(q=FAKE, k=FAKE, v=FAKE, dtype=_lib.DTYPE_BF16, batch=1, m=1, h_q=32, h_kv=8, d=128,
+             q_sb=4096, q_sn=4096, q_sh=128, k_sb=1024, k_sn=1024, k_sh=128, v_sb=1024, v_sn=1024,
+             v_sh=128, k_cache=FAKE, v_cache=FAKE, max_len=1024, kc_sb=1024 * 1024, kc_sn=1024,
+             kc_sh=128, vc_sb=1024 * 1024, vc_sn=1024, vc_sh=128, n0=100, w_qr=FAKE, w_kr=FAKE,
+             prep=FAKE, d_s=32, n_c=4096, a=16, b=4, temperature=1.0, k_codes=FAKE, offsets=FAKE,
+             postings=FAKE, n_base=90, tail_offsets=FAKE, tail_postings=FAKE, tail_cap=2048,
+             top_k=512, score_div=11.3137, scale_div=11.3137, causal=1, indices=NULL, out=FAKE,
+             out_dtype=_lib.DTYPE_BF16, o_sb=4096, o_sn=4096, o_sh=128, workspace=FAKE,
+             workspace_bytes=1 << 30, stream=NULL)
+    a.update(kw)
+    st = L.ssa_decode_step(*a.values())
+    return st, (L.ssa_last_error() or b"").decode()
+
+
+@pytest.mark.parametrize("kw,status,text", [
+    (dict(dtype=5), _lib.SSA_ERR_UNSUPPORTED, "dtype"),
+    (dict(n0=1024), _lib.SSA_ERR_INVALID_ARGUMENT, "exceed"),
+    (dict(n_base=101), _lib.SSA_ERR_INVALID_ARGUMENT, "main index"),
+    (dict(n_base=0, tail_cap=100), _lib.SSA_ERR_WORKSPACE, "tail"),
+    (dict(workspace_bytes=16), _lib.SSA_ERR_WORKSPACE, "workspace"),
+    (dict(n_c=20000), _lib.SSA_ERR_UNSUPPORTED, "16384"),
+    (dict(k_sn=1028), _lib.SSA_ERR_UNSUPPORTED, "aligned"),
+    (dict(h_q=30), _lib.SSA_ERR_INVALID_ARGUMENT, "shape"),
+])
+def test_decode_step_rejects(L, kw, status, text):
+    st, msg = _decode(L, **kw)
+    assert st == status, msg
+    assert text in msg
+
+
+def test_decode_empty_step_is_noop(L):
+    assert _decode(L, m=0, q=NULL, k=NULL, v=NULL)[0] == _lib.SSA_OK

@@ -2,10 +2,12 @@
 entry points ssa_select_block / ssa_sparse_attention_block).
 
 A step that leaves n tokens in the cache must equal the last rows of the
-whole-sequence forward over those n tokens (same keys, codes and index; the
-filler of a row with fewer than k candidates comes from the same n keys):
-selected index sets bit for bit, attention outputs bit for bit (same kernels
-on the same inputs).
+whole-sequence forward over those n tokens (same keys, codes and candidate
+sets -- a single-token step reads them from the main index over the keys up to
+its last rebuild plus the tail index over the keys appended since; the filler
+of a row with fewer than k candidates comes from the same n keys): selected
+index sets bit for bit, attention outputs bit for bit (same kernels on the
+same inputs).
 The prefix forward is itself pinned to the oracle by the other GPU tests; here
 one step is also checked against the oracle directly.
 """
@@ -21,15 +23,18 @@ from tests.helpers import clustered_qk, f32
 pytestmark = pytest.mark.gpu
 
 
-def _setup(dev, n, h_q, h_kv, d, n_c, top_k, dtype, seed):
+def _setup(dev, n, h_q, h_kv, d, n_c, top_k, dtype, seed, batch=1):
     from ssa_amd import CodebookRouter
 
-    q, k = clustered_qk(n, h_q, h_kv, d, 16, 0.3, seed, dtype)
-    v = torch.randn(n, h_kv, d, generator=torch.Generator().manual_seed(seed + 1)).to(dtype)
+    qs, ks, vs = [], [], []
+    for bb in range(batch):
+        q, k = clustered_qk(n, h_q, h_kv, d, 16, 0.3, seed + 10 * bb, dtype)
+        v = torch.randn(n, h_kv, d, generator=torch.Generator().manual_seed(seed + 10 * bb + 1)).to(dtype)
+        qs.append(q), ks.append(k), vs.append(v)
     torch.manual_seed(seed + 2)
     router = CodebookRouter(head_dim=d, route_dim=32, num_kv_heads=h_kv, num_codebook=n_c,
                             codes_per_key=4, codes_per_query=8, top_k=top_k).to(dev)
-    return q[None].to(dev), k[None].to(dev), v[None].to(dev), router
+    return (torch.stack(qs).to(dev), torch.stack(ks).to(dev), torch.stack(vs).to(dev), router)
 
 
 def _prefix_forward(router, q, k, v, n):
@@ -47,20 +52,28 @@ def _prefix_forward(router, q, k, v, n):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_decode_steps_match_prefix_forward(dev, dtype):
+@pytest.mark.parametrize("tail_tokens,batch", [(512, 1), (6, 1), (6, 2)])
+def test_decode_steps_match_prefix_forward(dev, dtype, tail_tokens, batch):
+    """A prefill chunk, then single tokens and small chunks: each step's indices
+    and outputs equal the last rows of the whole-sequence forward.  With
+    tail_tokens = 6 the main index is rebuilt inside the single-token steps
+    (the tail outgrows it) as well as by the chunks."""
     from ssa_amd.decode import SSADecodeCache
 
+    print(f"decode dtype={dtype} tail_tokens={tail_tokens} batch={batch}", flush=True)
     n, h_q, h_kv, d = 160, 8, 2, 128
-    q, k, v, router = _setup(dev, n, h_q, h_kv, d, 64, 24, dtype, seed=3)
-    cache = SSADecodeCache(router, 1, 256, d, dtype=dtype)
+    q, k, v, router = _setup(dev, n, h_q, h_kv, d, 64, 24, dtype, seed=3, batch=batch)
+    cache = SSADecodeCache(router, batch, 256, d, dtype=dtype, tail_tokens=tail_tokens)
     pos = 0
-    for m in (96, 1, 1, 3, 1, 7, 1):  # a prefill chunk, then single tokens and small chunks
+    for m in (96, 1, 1, 3, 1, 1, 1, 7, 1, 1):
         out, idx = cache.step(q[:, pos:pos + m], k[:, pos:pos + m], v[:, pos:pos + m], return_indices=True)
         ref_idx, ref_out = _prefix_forward(router, q, k, v, pos + m)
         assert torch.equal(idx, ref_idx[:, pos:]), f"indices differ in the step at {pos}"
         assert torch.equal(out, ref_out[:, pos:]), f"outputs differ in the step at {pos}"
         pos += m
     assert cache.len == pos
+    if tail_tokens == 6:
+        assert cache.rebuilds == 3  # the two chunks and one single step (the tail passed 6 keys)
 
 
 def test_decode_step_matches_oracle(dev, orc):
@@ -87,3 +100,37 @@ def test_block_rejects_rows_past_the_keys(dev):
     idx = torch.zeros(1, 4, 2, 8, dtype=torch.int32, device=dev)
     with pytest.raises(Exception, match="outside"):
         kernels.sparse_attention(q[:, :4], k, v, idx, None, True, q_pos0=30)
+
+
+@pytest.mark.parametrize("n_c,a,periodic", [(1000, 32, False), (4096, 8, False), (4096, 32, True),
+                                             (16384, 16, False)])
+def test_decode_codebook_sizes_and_ties(dev, n_c, a, periodic):
+    """Single-token steps route their rows with the decoding top-k (scores per
+    256-code chunk, then a per-row select): codebooks that are not a multiple
+    of the chunk, a temperature, the largest code count, zero queries and
+    keys, whose scores all tie (the lowest codes win), and a codebook whose
+    rows repeat every 256 codes (each thread of the select then holds many
+    equal best keys, which sends it to its radix select) give the indices and
+    outputs of the whole-sequence forward."""
+    from ssa_amd import CodebookRouter
+    from ssa_amd.decode import SSADecodeCache
+
+    print(f"decode n_c={n_c} a={a} periodic={periodic}", flush=True)
+    n, h_q, h_kv, d, batch = 120, 8, 2, 128, 2
+    q, k, v, _ = _setup(dev, n, h_q, h_kv, d, 64, 24, torch.bfloat16, seed=5, batch=batch)
+    q[0, 110] = 0
+    k[1, 112] = 0
+    q[1, 115], k[1, 115] = 0, 0
+    torch.manual_seed(11)
+    router = CodebookRouter(head_dim=d, route_dim=32, num_kv_heads=h_kv, num_codebook=n_c,
+                            codes_per_key=4, codes_per_query=a, top_k=24, temperature=0.7).to(dev)
+    if periodic:
+        with torch.no_grad():
+            router.codebook.copy_(router.codebook[:, :256].repeat(1, n_c // 256, 1))
+    cache = SSADecodeCache(router, batch, 128, d, dtype=torch.bfloat16, tail_tokens=16)
+    cache.step(q[:, :100], k[:, :100], v[:, :100])
+    for pos in range(100, n):
+        out, idx = cache.step(q[:, pos:pos + 1], k[:, pos:pos + 1], v[:, pos:pos + 1], return_indices=True)
+        ref_idx, ref_out = _prefix_forward(router, q, k, v, pos + 1)
+        assert torch.equal(idx, ref_idx[:, pos:]), f"indices differ at {pos}"
+        assert torch.equal(out, ref_out[:, pos:]), f"outputs differ at {pos}"

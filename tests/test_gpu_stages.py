@@ -33,6 +33,40 @@ def test_route_vectors_bit_exact(dev, orc, dtype, h_in, group, d, d_s):
         np.testing.assert_array_equal(got[b], ref)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("n,batch,h_in,group,d,d_s", [
+    (1, 1, 32, 4, 128, 32),     # a decoding step: the one-wave-per-row kernel
+    (3, 2, 6, 3, 64, 16),
+    (17, 1, 8, 1, 128, 48),
+    (500, 2, 4, 2, 64, 48),     # route_dim > 32: the general LDS-tiled kernel
+    (300, 1, 2, 1, 128, 64),
+])
+def test_route_vectors_small_and_wide_bit_exact(dev, orc, dtype, n, batch, h_in, group, d, d_s):
+    """Few rows (the lane-per-coordinate kernel of decoding steps) and route
+    dims above 32 (the general kernel) against the oracle's chains."""
+    from ssa_amd import kernels
+
+    _say(f"route_vectors small/wide n={n} B={batch} h_in={h_in} g={group} d={d} d_s={d_s}")
+    x = randn((batch, n, h_in, d), 5, dtype)
+    w = torch.nn.init.uniform_(torch.empty(d_s, d), -0.2, 0.2)
+    got = kernels.route_vectors(x.to(dev), w.to(dev), group).cpu().numpy()
+    for b in range(batch):
+        np.testing.assert_array_equal(got[b], orc.route_vectors(f32(x[b]), f32(w), group))
+
+
+@pytest.mark.parametrize("top,n_c,d_s,rows,h", [(16, 4096, 32, 1, 8), (4, 4096, 32, 3, 2),
+                                                (32, 8192, 32, 2, 2), (8, 300, 16, 5, 3)])
+def test_code_topk_few_rows_bit_exact(dev, orc, top, n_c, d_s, rows, h):
+    """A handful of rows (decoding) take the exhaustive one-wave-per-row kernel."""
+    from ssa_amd import kernels
+
+    _say(f"code_topk few rows top={top} n_c={n_c} rows={rows} h={h}")
+    xhat = torch.from_numpy(orc.normalize(f32(randn((1, h, rows, d_s), 6))))
+    chat = torch.from_numpy(orc.normalize(f32(randn((h, n_c, d_s), 7))))
+    got = kernels.code_topk(xhat.to(dev), chat.to(dev), top).cpu().numpy()
+    np.testing.assert_array_equal(got[0], orc.code_topk(xhat[0].numpy(), chat.numpy(), top))
+
+
 def test_normalize_rows_bit_exact(dev, orc):
     from ssa_amd import kernels
 
@@ -202,6 +236,39 @@ def test_sparse_attention_vs_oracle(dev, orc, dtype, d, g, tol, causal):
     for b in range(B):
         ref = orc.sparse_attention(f32(q[b]), f32(k[b]), f32(v[b]), idx[b].numpy(), causal=causal)
         np.testing.assert_allclose(got[b], ref, rtol=tol, atol=tol)
+
+
+@pytest.mark.parametrize("top_k,causal,g", [(512, True, 4), (2048, False, 8), (256, True, 2)])
+def test_sparse_attention_few_rows_split(dev, orc, top_k, causal, g):
+    """Calls of at most 512 rows (decoding steps) split each row's chunks over
+    four waves and combine their states: against the oracle (bf16 inputs, fp32
+    output, 1e-3) and against the same rows of a large call (one wave per row)
+    within 1e-5; with duplicated and out-of-range slots."""
+    from ssa_amd import kernels
+
+    _say(f"attention few rows split top_k={top_k} causal={causal} g={g}")
+    n, h_kv, d, m = 3000, 2, 128, 3
+    q = randn((1, n, h_kv * g, d), 121, torch.bfloat16).to(dev)
+    k = randn((1, n, h_kv, d), 122, torch.bfloat16).to(dev)
+    v = randn((1, n, h_kv, d), 123, torch.bfloat16).to(dev)
+    gi = torch.Generator().manual_seed(124)
+    idx = torch.randint(0, n, (1, n, h_kv, top_k), generator=gi)
+    idx[0, -2, 0, 7] = idx[0, -2, 0, 3]                # a duplicate counts twice
+    idx = idx.to(torch.int32).to(dev)
+    rows = slice(n - m, n)
+    few = torch.empty((1, m, h_kv * g, d), device=dev, dtype=torch.float32)
+    kernels.sparse_attention(q[:, rows], k, v, idx[:, rows], None, causal, out=few, q_pos0=n - m)
+    big = torch.empty((1, n, h_kv * g, d), device=dev, dtype=torch.float32)
+    kernels.sparse_attention(q, k, v, idx, None, causal, out=big)
+    torch.testing.assert_close(few, big[:, rows], rtol=1e-5, atol=1e-5)
+    ref = orc.sparse_attention(f32(q[0]), f32(k[0]), f32(v[0]), idx[0].cpu().numpy()[rows],
+                               causal=causal, rows=np.arange(n - m, n))
+    np.testing.assert_allclose(few[0].cpu().numpy(), ref, rtol=1e-3, atol=1e-3)
+    flag = torch.zeros(1, device=dev, dtype=torch.int32)
+    bad = idx[:, rows].clone()
+    bad[0, 0, 1, 5] = n + 3
+    kernels.sparse_attention(q[:, rows], k, v, bad, None, causal, out=few, q_pos0=n - m, error_flag=flag)
+    assert int(flag.item()) == 1
 
 
 def test_sparse_attention_k_equals_n_is_causal_dense(dev, orc):
