@@ -160,11 +160,12 @@ def block_stages(blk, reps=5):
             off, post = kernels.build_index(kc, r.num_codebook)
             order = kernels.query_order(qc, r.num_codebook)
             ev[4].record()
+            pfx = torch.empty(order.shape, device=q.device, dtype=torch.int32)
             idx = kernels.select(q, k, qc, off, post, r.codes_per_key, r.top_k, sorted=False,
-                                 index_dtype=torch.int32, row_order=order)
+                                 index_dtype=torch.int32, row_order=order, row_prefix=pfx)
             ev[5].record()
             out = kernels.sparse_attention(q, k, v, idx, None, layer.causal_attention,
-                                           row_order=order)
+                                           row_order=order, row_prefix=pfx)
             ev[6].record()
             layer.o_proj(out.reshape(h.shape[0], h.shape[1], -1))
             ev[7].record()
@@ -227,12 +228,15 @@ def run_step(q, k, v, router, events=None):
     # Same calls as SSAAttention: stage (d) does not depend on the order of the
     # selected keys, so the router lists them by index (same set as sorted),
     # the indices pass to stage (d) as int32, and stages (c) and (d) process the
-    # rows of each head grouped by best code (results do not depend on the order).
+    # rows of each head grouped by best code (results do not depend on the order);
+    # the selection also names each row's key prefix [0, X) (its lowest-key
+    # filler), which stage (d) attends in blocks of neighbouring rows.
+    pfx = torch.empty(order.shape, device=q.device, dtype=torch.int32)
     idx = kernels.select(q, k, qc, off, post, router.codes_per_key, router.top_k, sorted=False,
-                         index_dtype=torch.int32, row_order=order)
+                         index_dtype=torch.int32, row_order=order, row_prefix=pfx)
     if events:
         events[3].record()
-    out = kernels.sparse_attention(q, k, v, idx, None, True, row_order=order)
+    out = kernels.sparse_attention(q, k, v, idx, None, True, row_order=order, row_prefix=pfx)
     if events:
         events[4].record()
     return out
@@ -579,8 +583,8 @@ def copy_probe(gib):
 def main():
     args = parse()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 (sharding design is "
-                                   "described in DESIGN.md, not built)"}))
+        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 (the sharded path "
+                                   "is designed, not built)"}))
         sys.exit(2)
     import torch
 

@@ -164,6 +164,11 @@ int ssa_query_order(const int32_t* q_codes, int64_t batch, int64_t n, int h_kv, 
  *   mask   (SSA_MASK_DENSE only) uint8 [batch][n][n], strides (mask_sb, mask_si); mask_sb may be 0
  *   stats  (nullable) int32 [batch][h_kv][n][2] = (candidates, postings read
  *          inside the mask window: j <= i when causal, all otherwise)
+ *   row_prefix (nullable) int32 [batch][h_kv][n]: X per row such that the
+ *          row's indices hold each key of [0, X) exactly once -- the last
+ *          filler key + 1 for a row with filler, 0 otherwise (and 0 with k > n
+ *          padding).  ssa_sparse_attention takes it to attend those keys in a
+ *          dense pass.  No reference counterpart.
  *   workspace (nullable): with it, index order runs one wave per row; a row
  *          with more than k candidates leaves its candidate list in the
  *          workspace, which bf16 inputs with d = 64 or 128 then screen on the
@@ -197,7 +202,7 @@ int ssa_select(const void* q, const void* k, int dtype, int64_t batch, int64_t n
                const int32_t* postings, int n_c, int b, int top_k, int mask_mode,
                const uint8_t* mask, int64_t mask_sb, int64_t mask_si, float score_div, int sorted,
                const int32_t* row_order, void* out, int out_index_dtype, int32_t* stats,
-               void* workspace, size_t workspace_bytes, void* stream);
+               int32_t* row_prefix, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ssa_select for a block of n_q query rows at key positions q_pos0 .. q_pos0 +
  * n_q - 1 against all n keys (0 <= q_pos0, q_pos0 + n_q <= n): q, q_codes,
@@ -213,7 +218,8 @@ int ssa_select_block(const void* q, const void* k, int dtype, int64_t batch, int
                      const int32_t* postings, int n_c, int b, int top_k, int mask_mode,
                      const uint8_t* mask, int64_t mask_sb, int64_t mask_si, float score_div,
                      int sorted, const int32_t* row_order, void* out, int out_index_dtype,
-                     int32_t* stats, void* workspace, size_t workspace_bytes, void* stream);
+                     int32_t* stats, int32_t* row_prefix, void* workspace, size_t workspace_bytes,
+                     void* stream);
 
 /* ssa_select_block without a workspace argument: no counterpart in the
  * reference; for callers that cannot allocate (code under HIP graph capture,
@@ -235,7 +241,7 @@ int ssa_select_block_noalloc(const void* q, const void* k, int dtype, int64_t ba
                              const int32_t* postings, int n_c, int b, int top_k, int mask_mode,
                              const uint8_t* mask, int64_t mask_sb, int64_t mask_si,
                              float score_div, int sorted, const int32_t* row_order, void* out,
-                             int out_index_dtype, int32_t* stats, void* stream);
+                             int out_index_dtype, int32_t* stats, int32_t* row_prefix, void* stream);
 
 /* ---- incremental decoding ----------------------------------------------- */
 
@@ -295,15 +301,30 @@ int ssa_decode_step(const void* q, const void* k, const void* v, int dtype, int6
  *   written, and an entry outside [0, n) is skipped and sets *error_flag.
  *   idx [batch][n][h_kv][top_k] strides (idx_sb, idx_sn, idx_sh)
  *   out [batch][n][h_q][d] strides (o_sb, o_sn, o_sh), type out_dtype
+ * workspace (nullable) of ssa_sparse_attention_workspace_bytes(...) bytes: with
+ *   it, the keys [0, X) that a row's indices hold exactly once (the lowest-key
+ *   filler of a row with few candidates) are attended by a pass that streams
+ *   them once per block of neighbouring rows, and the row pass skips them.
+ *   The result is the same attention (a different summation order).
+ * row_prefix (nullable) int32 [batch][h_kv][n]: X per row as ssa_select
+ *   writes it (the caller vouches that the row's indices hold [0, X) once);
+ *   without it the dense pass finds X from the indices (a bitmap per row).
  * Limits: d a multiple of 8 in [8, 256], g <= 16. */
 int ssa_sparse_attention(const void* q, const void* k, const void* v, int dtype, int64_t batch,
                          int64_t n, int h_q, int h_kv, int d, int64_t q_sb, int64_t q_sn,
                          int64_t q_sh, int64_t k_sb, int64_t k_sn, int64_t k_sh, int64_t v_sb,
                          int64_t v_sn, int64_t v_sh, const void* idx, int idx_dtype, int top_k,
                          int64_t idx_sb, int64_t idx_sn, int64_t idx_sh, float scale_div,
-                         int causal, const int32_t* row_order, void* out, int out_dtype,
-                         int64_t o_sb, int64_t o_sn,
-                         int64_t o_sh, int32_t* error_flag, void* stream);
+                         int causal, const int32_t* row_order, const int32_t* row_prefix,
+                         void* out, int out_dtype, int64_t o_sb, int64_t o_sn,
+                         int64_t o_sh, int32_t* error_flag, void* workspace,
+                         size_t workspace_bytes, void* stream);
+
+/* Bytes of ssa_sparse_attention's optional workspace for n_q query rows; 0
+ * where the dense-prefix pass does not run (fp32 inputs, d other than 64 or
+ * 128, g > 8, top_k < 64).  No reference counterpart. */
+size_t ssa_sparse_attention_workspace_bytes(int dtype, int64_t batch, int64_t n_q, int h_q, int h_kv,
+                                            int d, int top_k);
 
 /* ssa_sparse_attention for a block of n_q query rows at key positions q_pos0
  * .. q_pos0 + n_q - 1 (0 <= q_pos0, q_pos0 + n_q <= n): q, idx, out and
@@ -315,8 +336,9 @@ int ssa_sparse_attention_block(
     int64_t q_pos0, int h_q, int h_kv, int d, int64_t q_sb, int64_t q_sn, int64_t q_sh, int64_t k_sb,
     int64_t k_sn, int64_t k_sh, int64_t v_sb, int64_t v_sn, int64_t v_sh, const void* idx,
     int idx_dtype, int top_k, int64_t idx_sb, int64_t idx_sn, int64_t idx_sh, float scale_div,
-    int causal, const int32_t* row_order, void* out, int out_dtype, int64_t o_sb, int64_t o_sn,
-    int64_t o_sh, int32_t* error_flag, void* stream);
+    int causal, const int32_t* row_order, const int32_t* row_prefix, void* out, int out_dtype,
+    int64_t o_sb, int64_t o_sn, int64_t o_sh, int32_t* error_flag, void* workspace,
+    size_t workspace_bytes, void* stream);
 
 /* Key blocks per query block: replaces convert_indices_to_blocks
  * (ssa/triton_kernel.py:226-294).  idx [batch][n][h_kv][top_k] (strides

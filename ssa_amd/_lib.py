@@ -67,20 +67,20 @@ SIGNATURES = {
         _int,
         [_vp, _vp, _int, _i64, _i64, _int, _int, _int, _i64, _i64, _i64, _i64, _i64, _i64,
          _vp, _int, _vp, _vp, _int, _int, _int, _int, _vp, _i64, _i64, _flt, _int, _vp, _vp,
-         _int, _vp, _vp, _sz, _vp]),
+         _int, _vp, _vp, _vp, _sz, _vp]),
     "ssa_select_workspace_bytes": (_sz, [_i64, _i64, _int, _int]),
     "ssa_select_workspace_layout": (_int, [_i64, _i64, _int, _sz, _int, _vp]),
     "ssa_select_block": (
         _int,
         [_vp, _vp, _int, _i64, _i64, _i64, _i64, _int, _int, _int, _i64, _i64, _i64, _i64, _i64,
          _i64, _vp, _int, _vp, _vp, _int, _int, _int, _int, _vp, _i64, _i64, _flt, _int, _vp, _vp,
-         _int, _vp, _vp, _sz, _vp]),
+         _int, _vp, _vp, _vp, _sz, _vp]),
     "ssa_select_noalloc_scratch_bytes": (_sz, []),
     "ssa_select_block_noalloc": (
         _int,
         [_vp, _vp, _int, _i64, _i64, _i64, _i64, _int, _int, _int, _i64, _i64, _i64, _i64, _i64,
          _i64, _vp, _int, _vp, _vp, _int, _int, _int, _int, _vp, _i64, _i64, _flt, _int, _vp, _vp,
-         _int, _vp, _vp]),
+         _int, _vp, _vp, _vp]),
     "ssa_decode_prepare_bytes": (_sz, [_int, _int, _int]),
     "ssa_decode_prepare": (_int, [_vp, _int, _int, _int, _vp, _sz, _vp]),
     "ssa_decode_workspace_bytes": (_sz, [_i64, _i64, _int, _int, _int, _int, _int, _int]),
@@ -93,13 +93,14 @@ SIGNATURES = {
     "ssa_sparse_attention": (
         _int,
         [_vp, _vp, _vp, _int, _i64, _i64, _int, _int, _int, _i64, _i64, _i64, _i64, _i64, _i64,
-         _i64, _i64, _i64, _vp, _int, _int, _i64, _i64, _i64, _flt, _int, _vp, _vp, _int, _i64,
-         _i64, _i64, _vp, _vp]),
+         _i64, _i64, _i64, _vp, _int, _int, _i64, _i64, _i64, _flt, _int, _vp, _vp, _vp, _int,
+         _i64, _i64, _i64, _vp, _vp, _sz, _vp]),
+    "ssa_sparse_attention_workspace_bytes": (_sz, [_int, _i64, _i64, _int, _int, _int, _int]),
     "ssa_sparse_attention_block": (
         _int,
         [_vp, _vp, _vp, _int, _i64, _i64, _i64, _i64, _int, _int, _int, _i64, _i64, _i64, _i64,
          _i64, _i64, _i64, _i64, _i64, _vp, _int, _int, _i64, _i64, _i64, _flt, _int, _vp, _vp,
-         _int, _i64, _i64, _i64, _vp, _vp]),
+         _vp, _int, _i64, _i64, _i64, _vp, _vp, _sz, _vp]),
     "ssa_block_indices": (
         _int,
         [_vp, _int, _i64, _i64, _int, _int, _i64, _i64, _i64, _int, _int, _vp, _int, _i64, _i64,

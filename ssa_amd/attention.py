@@ -21,12 +21,12 @@ class _SparseAttention(torch.autograd.Function):
     (ssa/attention.py:64-113); the indices get none, as in the reference."""
 
     @staticmethod
-    def forward(ctx, q, k, v, indices, scale, causal, row_order, flag):
+    def forward(ctx, q, k, v, indices, scale, causal, row_order, flag, row_prefix):
         # The backward's D = dO . o uses an fp32 copy of the output: a bf16 one
         # would carry its 2^-9 rounding into every gradient.
         out32 = torch.empty(q.shape, device=q.device, dtype=torch.float32)
         kernels.sparse_attention(q, k, v, indices, scale, causal, out=out32, error_flag=flag,
-                                 row_order=row_order)
+                                 row_order=row_order, row_prefix=row_prefix)
         ctx.scale, ctx.causal = scale, causal
         ctx.has_order = row_order is not None
         saved = [q, k, v, indices, out32] + ([row_order] if row_order is not None else [])
@@ -41,7 +41,7 @@ class _SparseAttention(torch.autograd.Function):
             dout = dout.contiguous()
         dq, dk, dv = kernels.sparse_attention_backward(q, k, v, indices, out, dout, ctx.scale,
                                                        ctx.causal, row_order=order)
-        return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), None, None, None, None, None
+        return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), None, None, None, None, None, None
 
 
 def sparse_exact_attention(
@@ -54,6 +54,7 @@ def sparse_exact_attention(
     causal: bool = False,
     check_indices: bool = True,
     row_order: Optional[torch.Tensor] = None,
+    row_prefix: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """softmax(q . K[indices]^T / scale) . V[indices] per (query, KV head).
 
@@ -68,7 +69,11 @@ def sparse_exact_attention(
     gather does -- out-of-range slots are never read either way.
     ``row_order`` (int32 [B, h_kv, n], e.g. ``CodebookRouter.route(...,
     with_order=True).order``) sets the order rows are processed in, for cache
-    locality; it does not change the result.
+    locality; it does not change the result.  ``row_prefix`` (int32 [B, h_kv, n],
+    ``route(..., with_prefix=True).prefix``) names the key prefix [0, X) each
+    row's indices hold once; bf16 inputs with d 64 or 128 attend it in a dense
+    pass (also found from the indices without it; same result up to summation
+    order).
 
     Differentiable in q, k and v (HIP backward kernel); not in ``indices``.
     """
@@ -90,11 +95,14 @@ def sparse_exact_attention(
     flag = torch.zeros(1, device=q.device, dtype=torch.int32) if check_indices else None
     if row_order is not None and unbatched and row_order.dim() == 2:
         row_order = row_order.unsqueeze(0)
+    if row_prefix is not None and unbatched and row_prefix.dim() == 2:
+        row_prefix = row_prefix.unsqueeze(0)
     if torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad):
-        out = _SparseAttention.apply(q, k, v, indices, float(scale), bool(causal), row_order, flag)
+        out = _SparseAttention.apply(q, k, v, indices, float(scale), bool(causal), row_order, flag,
+                                     row_prefix)
     else:
         out = kernels.sparse_attention(q, k, v, indices, float(scale), causal, error_flag=flag,
-                                       row_order=row_order)
+                                       row_order=row_order, row_prefix=row_prefix)
     if flag is not None and int(flag.item()) != 0:
         raise IndexError(f"sparse_exact_attention: an index is outside [0, {seq_len})")
     if out.dtype != out_dtype:

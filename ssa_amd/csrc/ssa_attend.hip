@@ -61,6 +61,14 @@ struct AttParams {
   // (t & (2^blk_log2 - 1)), and keys at or past n are dropped silently.
   int blk_log2;
   int64_t nbk;
+  // Dense key prefix (nullable): pfx_x [B*h_kv][n_q] = X, the length of the
+  // key prefix [0, X) that a row's indices hold exactly once, and pfx_part the
+  // prefix's unnormalised attention state per (row, head): [B*h_kv*n_q][g][D + 4]
+  // = O (D floats), running max, sum.  prefix_attention_kernel writes both; the
+  // row kernel then drops the row's indices below X and starts from that state.
+  int32_t* pfx_x;
+  float* pfx_part;
+  int pfx_given;  // pfx_x came from the selection (row_prefix): the prefix kernel only reads it
 };
 
 // Key of slot `slot` given the index entry loaded for it: -1 = none (block mode:
@@ -578,7 +586,9 @@ __device__ __forceinline__ void attend_row_mfma(const AttParams& p, const AttRow
       else mf_issue<D, false, false>(krs, vrs, kl, vl, jsafe, lrow, ksn2, vsn2, seg16);
     }
   };
-  auto chunk_ok = [&](int j) { return j >= 0 && !(p.causal && j > i); };
+  // keys below the row's dense prefix were attended by prefix_attention_kernel
+  const int xpre = (NSPLIT == 1 && !BLK && p.pfx_x && row_ok) ? p.pfx_x[bh * p.n_q + qr] : 0;
+  auto chunk_ok = [&](int j) { return j >= xpre && !(p.causal && j > i); };
 
   // Fragment addresses (fixed per lane): K tile t, block kb; V^T tile t (rows
   // 4*q4 + c16/4, +16 for the second half of the chunk).
@@ -593,6 +603,17 @@ __device__ __forceinline__ void attend_row_mfma(const AttParams& p, const AttRow
   floatx4_t oacc[S::NT];
 #pragma unroll
   for (int t = 0; t < S::NT; ++t) oacc[t] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+  if (xpre > 0 && hi_row) {
+    // column c16 < g (head c16's P_hi) carries the prefix state; P_lo columns start at 0
+    const float* pp = p.pfx_part + ((bh * p.n_q + qr) * p.g + c16) * (D + 4);
+#pragma unroll
+    for (int t = 0; t < S::NT; ++t) {
+      const float4 o4 = *reinterpret_cast<const float4*>(pp + 16 * t + 4 * q4);
+      oacc[t] = floatx4_t{o4.x, o4.y, o4.z, o4.w};
+    }
+    m_run = pp[D];
+    l_run = (q4 == 0) ? pp[D + 1] : 0.0f;
+  }
 
   const int nchunks = (p.top_k + kMfChunk - 1) / kMfChunk;
   // this wave's chunks: c0, c0 + NSPLIT, ... (all of them when NSPLIT = 1)
@@ -604,10 +625,21 @@ __device__ __forceinline__ void attend_row_mfma(const AttParams& p, const AttRow
     const int j0 = load_idx(chunk_of(0));
     const bool ok0 = chunk_ok(j0);
     okbits = __ballot(ok0);
-    issue(ok0 ? j0 : -1, static_cast<uint32_t>(okbits) == 0xFFFFFFFFu);
+    if (okbits) issue(ok0 ? j0 : -1, static_cast<uint32_t>(okbits) == 0xFFFFFFFFu);
     if (nmine > 1) j_next = load_idx(chunk_of(1));
   }
   for (int u = 0; u < nmine; ++u) {
+    // A chunk with no key to attend (all below the prefix, past the causal cut
+    // or past top_k) loads nothing and leaves the state as it is.
+    if (okbits == 0) {
+      if (u + 1 < nmine) {
+        const bool okn = chunk_ok(j_next);
+        okbits = __ballot(okn);
+        if (okbits) issue(okn ? j_next : -1, static_cast<uint32_t>(okbits) == 0xFFFFFFFFu);
+        if (u + 2 < nmine) j_next = load_idx(chunk_of(u + 2));
+      }
+      continue;
+    }
     // This chunk's rows are in LDS once its loads have completed.
     __builtin_amdgcn_s_waitcnt(kWaitVm0);
     bf16x8_t kf[2][S::KB];
@@ -629,10 +661,11 @@ __device__ __forceinline__ void attend_row_mfma(const AttParams& p, const AttRow
     // The slices are free once the reads have returned: start the next chunk.
     __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
     const uint64_t okb = okbits;
+    okbits = 0;
     if (u + 1 < nmine) {
       const bool okn = chunk_ok(j_next);
       okbits = __ballot(okn);
-      issue(okn ? j_next : -1, static_cast<uint32_t>(okbits) == 0xFFFFFFFFu);
+      if (okbits) issue(okn ? j_next : -1, static_cast<uint32_t>(okbits) == 0xFFFFFFFFu);
       if (u + 2 < nmine) j_next = load_idx(chunk_of(u + 2));
     }
 
@@ -746,8 +779,265 @@ __global__ __launch_bounds__(64 * kMfWaves, kMfMinBlocks) void sparse_attention_
   using S = MfShape<D>;
   __shared__ __align__(16) unsigned char kv_lds[kMfWaves][2][kMfChunk * S::ROW];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const AttRow ar = att_row(p, static_cast<int64_t>(blockIdx.x) * kMfWaves + wave);
+  const int64_t blk = xcd_block(blockIdx.x, xcd_per(ceil_div(p.rows, kMfWaves)));
+  const AttRow ar = att_row(p, blk * kMfWaves + wave);
   attend_row_mfma<D, BLK>(p, ar, kv_lds[wave][0], kv_lds[wave][1]);
+}
+
+// ---- dense key prefix of many rows ------------------------------------------
+//
+// A row with fewer candidates than top_k fills its list with the lowest keys
+// it does not hold already, so its indices cover a prefix [0, X) of the keys
+// (at the headline shape 54% of all selected slots lie in such prefixes, and
+// neighbouring rows have similar X).  Gathering those keys row by row moves the
+// same few hundred K/V rows once per row through each CU; here one block takes
+// kPfxQv query vectors (R = kPfxQv / g consecutive rows of one (batch, kv
+// head), all their heads) and streams the keys [0, max X) through LDS once for
+// all of them:
+//   1. X per row: from the selection (ssa_select's row_prefix), or else from
+//      the indices: those below min(top_k, kPfxXMax, n) set bits of an LDS
+//      bitmap, X is the first clear bit, lowered to the smallest index that
+//      occurs twice (duplicates count twice in the reference, so a prefix must
+//      hold each key once); X then goes to pfx_x.
+//   2. Chunks of 32 consecutive keys, three LDS buffers: every wave loads its
+//      share of chunk u + 2 while the block computes chunk u (one barrier per
+//      chunk).  Each wave scores its two 16-query tiles (S^T = K.Q^T on the
+//      matrix cores, queries as the 16 columns), masks keys at or past the
+//      query row's X (and past its position when causal), runs the online
+//      softmax in the exp2 domain and accumulates O^T += V^T (P_hi + P_lo) as
+//      two MFMAs (P split into bf16 hi and lo as in the row kernel).
+//   3. The unnormalised state (O, running max, sum) of each query goes to
+//      pfx_part; the row kernel starts from it and skips indices below X.
+constexpr int kPfxWaves = 4;
+constexpr int kPfxQv = 32 * kPfxWaves;  // query vectors per block: two 16-column tiles per wave
+constexpr int kPfxXMax = 1024;          // longest prefix looked for in the indices
+constexpr int kPfxBufs = 3;
+
+template <int D>
+__global__ __launch_bounds__(64 * kPfxWaves, 2) void prefix_attention_kernel(AttParams p) {
+  using S = MfShape<D>;
+  constexpr int kLoadsPerWave = S::NLD / kPfxWaves;  // of K and of V, per chunk
+  static_assert(S::NLD % kPfxWaves == 0, "chunk loads split evenly over the waves");
+  __shared__ __align__(16) unsigned char kv[kPfxBufs][2][kMfChunk * S::ROW];  // [buffer][K, V]
+  __shared__ uint32_t bits[kPfxQv][kPfxXMax / 32];
+  __shared__ int s_dup[kPfxQv];
+  __shared__ int s_x[kPfxQv];
+  __shared__ int s_xmax;
+  const int g = p.g;
+  const int R = kPfxQv / g;  // rows per block
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int q4 = lane >> 4, c16 = lane & 15;
+  const int64_t tiles = ceil_div(p.n_q, R);
+  const int64_t nblk = (p.rows / p.n_q) * tiles;
+  const int64_t blk = xcd_block(blockIdx.x, xcd_per(nblk));
+  if (blk >= nblk) return;
+  const int64_t bh = blk / tiles;
+  const int64_t r0 = (blk - bh * tiles) * R;
+  const int h = static_cast<int>(bh % p.h_kv);
+  const int64_t bb = bh / p.h_kv;
+  const int nr = static_cast<int>(min(static_cast<int64_t>(R), p.n_q - r0));
+
+  // 1. X of each row
+  if (tid == 0) s_xmax = 0;
+  if (p.pfx_given) {
+    const int xcap = static_cast<int>(min(static_cast<int64_t>(p.top_k), p.n));
+    if (tid < R) s_x[tid] = (tid < nr) ? min(max(p.pfx_x[bh * p.n_q + r0 + tid], 0), xcap) : 0;
+    __syncthreads();
+  } else {
+    const int xb = static_cast<int>(min(static_cast<int64_t>(min(p.top_k, kPfxXMax)), p.n));
+    const int words = (xb + 31) >> 5;
+    for (int e = tid; e < R * (kPfxXMax / 32); e += 64 * kPfxWaves)
+      bits[e / (kPfxXMax / 32)][e % (kPfxXMax / 32)] = 0u;
+    if (tid < kPfxQv) s_dup[tid] = 0x7FFFFFFF;
+    __syncthreads();
+    const int top_k = p.top_k;
+    const int64_t ib0 = bb * p.idx_sb + r0 * p.idx_sn + static_cast<int64_t>(h) * p.idx_sh;
+    strided_batches<8, 64 * kPfxWaves>(
+        static_cast<int64_t>(nr) * top_k, tid,
+        [&](int64_t e) -> int64_t {
+          const int64_t r = e / top_k;
+          const int64_t a = ib0 + r * p.idx_sn + (e - r * top_k);
+          return p.idx_i64 ? static_cast<const int64_t*>(p.idx)[a]
+                           : static_cast<int64_t>(static_cast<const int32_t*>(p.idx)[a]);
+        },
+        [&](int64_t e, int64_t j) {
+          if (j >= 0 && j < xb) {
+            const int r = static_cast<int>(e / top_k);
+            const uint32_t bit = 1u << (j & 31);
+            const uint32_t old = atomicOr(&bits[r][j >> 5], bit);
+            if (old & bit) atomicMin(&s_dup[r], static_cast<int>(j));
+          }
+        });
+    __syncthreads();
+    if (tid < R) {
+      int x = 0;
+      if (tid < nr) {
+        x = 32 * words;
+        for (int w = 0; w < words; ++w) {
+          const uint32_t v = bits[tid][w];
+          if (v != 0xFFFFFFFFu) {
+            x = 32 * w + __ffs(~v) - 1;
+            break;
+          }
+        }
+        x = min(min(x, xb), s_dup[tid]);
+        p.pfx_x[bh * p.n_q + r0 + tid] = x;
+      }
+      s_x[tid] = x;
+    }
+  }
+  if (tid < R) atomicMax(&s_xmax, s_x[tid]);
+  __syncthreads();
+  const int xmax = s_xmax;
+  if (xmax == 0) return;
+
+  // 2. the prefix keys, 32 at a time, for the block's query vectors
+  bf16x8_t qf[2][S::KB];
+  int xr[2], ilim[2];
+  bool qok[2];
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    const int qv = 32 * wave + 16 * qt + c16;
+    const int r = qv / g, hh = qv - r * g;
+    qok[qt] = qv < R * g && r < nr;
+    xr[qt] = qok[qt] ? s_x[r] : 0;
+    ilim[qt] = p.causal ? static_cast<int>(min(p.q_pos0 + r0 + r, static_cast<int64_t>(0x7FFFFFFF)))
+                        : 0x7FFFFFFF;
+    const uint16_t* qh = static_cast<const uint16_t*>(p.q) + bb * p.q_sb + (r0 + (qok[qt] ? r : 0)) * p.q_sn +
+                         static_cast<int64_t>(h * g + (qok[qt] ? hh : 0)) * p.q_sh;
+#pragma unroll
+    for (int kb = 0; kb < S::KB; ++kb)
+      qf[qt][kb] = qok[qt] ? *reinterpret_cast<const bf16x8_t*>(qh + kb * 32 + q4 * 8) : bf16x8_t{};
+  }
+  const uint16_t* kbase = static_cast<const uint16_t*>(p.k) + bb * p.k_sb + static_cast<int64_t>(h) * p.k_sh;
+  const uint16_t* vbase = static_cast<const uint16_t*>(p.v) + bb * p.v_sb + static_cast<int64_t>(h) * p.v_sh;
+  const int kbytes = static_cast<int>((p.n - 1) * p.k_sn * 2 + 2 * D);
+  const int vbytes = static_cast<int>((p.n - 1) * p.v_sn * 2 + 2 * D);
+  const __amdgpu_buffer_rsrc_t krs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(kbase), 0, kbytes, kBufferWord3);
+  const __amdgpu_buffer_rsrc_t vrs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(vbase), 0, vbytes, kBufferWord3);
+  uint32_t seg16[S::SWZ_PERIOD];
+  row_seg16<D>(lane, seg16);
+  const uint32_t ksn2 = 2u * static_cast<uint32_t>(p.k_sn), vsn2 = 2u * static_cast<uint32_t>(p.v_sn);
+  // This wave's share of chunk ch: loads r = wave * kLoadsPerWave + t of K
+  // and of V (load r moves chunk rows KPI*r .. KPI*r + KPI - 1).
+  auto issue = [&](int ch) {
+    unsigned char* kl = kv[ch % kPfxBufs][0];
+    unsigned char* vl = kv[ch % kPfxBufs][1];
+#pragma unroll
+    for (int t = 0; t < kLoadsPerWave; ++t) {
+      const int r = wave * kLoadsPerWave + t;
+      const int j = ch * kMfChunk + S::KPI * r + lane / S::SEGS;
+      const uint32_t sg = seg16[r % S::SWZ_PERIOD];
+      const uint32_t ko = j < xmax ? __umul24(static_cast<uint32_t>(j), ksn2) + sg : kOobOffset;
+      const uint32_t vo = j < xmax ? __umul24(static_cast<uint32_t>(j), vsn2) + sg : kOobOffset;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_void_ptr)(kl + r * 1024), 16, static_cast<int>(ko), 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_void_ptr)(vl + r * 1024), 16, static_cast<int>(vo), 0, 0, 0);
+    }
+  };
+
+  float m_run[2] = {-INFINITY, -INFINITY};
+  float l_run[2] = {0.0f, 0.0f};
+  floatx4_t oacc[2][S::NT];
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+    for (int t = 0; t < S::NT; ++t) oacc[qt][t] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+  const int kswz = mf_swz<D>(c16);
+  const int nch = (xmax + kMfChunk - 1) / kMfChunk;
+  issue(0);
+  if (nch > 1) issue(1);
+  for (int u = 0; u < nch; ++u) {
+    // this wave's share of chunk u has landed (chunk u + 1's may still fly)
+    if (u + 1 < nch) __builtin_amdgcn_s_waitcnt(kWaitVmBase | (2 * kLoadsPerWave));
+    else __builtin_amdgcn_s_waitcnt(kWaitVm0);
+    // every share of chunk u is in LDS, and every wave is done with chunk u - 1
+    __syncthreads();
+    if (u + 2 < nch) issue(u + 2);
+    const unsigned char* kl = kv[u % kPfxBufs][0];
+    const unsigned char* vl = kv[u % kPfxBufs][1];
+    bf16x8_t kf[2][S::KB];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int kb = 0; kb < S::KB; ++kb)
+        kf[t][kb] = *(lds_bf16x8_ptr)(kl + (16 * t + c16) * S::ROW + (((kb * 4 + q4) ^ kswz) << 4));
+    bf16x8_t vt[S::NT];
+#pragma unroll
+    for (int t = 0; t < S::NT; ++t) vt[t] = rows_transposed<D>(vl, t, q4, c16);
+    const int jbase = u * kMfChunk + 4 * q4;
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+      float sc[8];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        floatx4_t sv = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kb = 0; kb < S::KB; ++kb) sv = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[t][kb], qf[qt][kb], sv, 0, 0, 0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int j = jbase + 16 * t + e;
+          sc[4 * t + e] = (j < xr[qt] && j <= ilim[qt]) ? sv[e] * p.qk_scale_log2 : -INFINITY;
+        }
+      }
+      float mx = sc[0];
+#pragma unroll
+      for (int x = 1; x < 8; ++x) mx = fmaxf(mx, sc[x]);
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float mnew = fmaxf(m_run[qt], mx);
+      const float mref = (mnew == -INFINITY) ? 0.0f : mnew;
+      const float alpha = __builtin_amdgcn_exp2f(m_run[qt] - mref);
+      m_run[qt] = mnew;
+      float pr[8];
+      float ps = 0.0f;
+#pragma unroll
+      for (int x = 0; x < 8; ++x) {
+        pr[x] = __builtin_amdgcn_exp2f(sc[x] - mref);
+        ps += pr[x];
+      }
+      l_run[qt] = l_run[qt] * alpha + ps;
+      uint32_t ph[4], pl[4];
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        ph[w] = pack_bf16x2(pr[2 * w], pr[2 * w + 1]);
+        pl[w] = pack_bf16x2(pr[2 * w] - __uint_as_float(ph[w] << 16),
+                            pr[2 * w + 1] - __uint_as_float(ph[w] & 0xFFFF0000u));
+      }
+      const bf16x8_t phv = __builtin_bit_cast(bf16x8_t, make_uint4(ph[0], ph[1], ph[2], ph[3]));
+      const bf16x8_t plv = __builtin_bit_cast(bf16x8_t, make_uint4(pl[0], pl[1], pl[2], pl[3]));
+      if (__ballot(alpha != 1.0f)) {
+#pragma unroll
+        for (int t = 0; t < S::NT; ++t) oacc[qt][t] *= alpha;
+      }
+#pragma unroll
+      for (int t = 0; t < S::NT; ++t) {
+        oacc[qt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vt[t], phv, oacc[qt][t], 0, 0, 0);
+        oacc[qt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vt[t], plv, oacc[qt][t], 0, 0, 0);
+      }
+    }
+  }
+
+  // 3. the state of each query with a prefix
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    float lt = l_run[qt] + __shfl_xor(l_run[qt], 16);
+    lt += __shfl_xor(lt, 32);
+    if (!qok[qt] || xr[qt] == 0) continue;
+    const int qv = 32 * wave + 16 * qt + c16;
+    const int r = qv / g, hh = qv - r * g;
+    float* pp = p.pfx_part + ((bh * p.n_q + r0 + r) * g + hh) * (D + 4);
+#pragma unroll
+    for (int t = 0; t < S::NT; ++t)
+      *reinterpret_cast<float4*>(pp + 16 * t + 4 * q4) =
+          make_float4(oacc[qt][t][0], oacc[qt][t][1], oacc[qt][t][2], oacc[qt][t][3]);
+    if (q4 == 0) {
+      pp[D] = m_run[qt];
+      pp[D + 1] = lt;
+    }
+  }
 }
 
 // Few rows (decoding): one block of kSplitWaves waves per row, wave w taking
@@ -804,12 +1094,23 @@ int launch_att_d(const AttParams& p, hipStream_t st) {
     };
     if (p.g <= 8 && p.d == D && p.n < (int64_t(1) << 24) && fits(p.k_sn) && fits(p.v_sn)) {
       if (p.blk_log2 == 0 && p.rows <= kSplitRowsMax && p.top_k >= 2 * kSplitWaves * kMfChunk) {
-        sparse_attention_split_kernel<D><<<dim3(static_cast<unsigned>(p.rows)), 64 * kSplitWaves, 0, st>>>(p);
+        AttParams ps = p;
+        ps.pfx_x = nullptr;
+        sparse_attention_split_kernel<D><<<dim3(static_cast<unsigned>(p.rows)), 64 * kSplitWaves, 0, st>>>(ps);
         return check_launch("sparse_attention_split_kernel");
       }
-      const dim3 grid(static_cast<unsigned>(ceil_div(p.rows, kMfWaves)));
-      if (p.blk_log2 > 0) sparse_attention_mfma_kernel<D, true><<<grid, 64 * kMfWaves, 0, st>>>(p);
-      else sparse_attention_mfma_kernel<D, false><<<grid, 64 * kMfWaves, 0, st>>>(p);
+      AttParams pr = p;
+      if (p.blk_log2 == 0 && p.pfx_x) {
+        const int64_t rows_per = kPfxQv / p.g;
+        const int64_t pblocks = (p.rows / p.n_q) * ceil_div(p.n_q, rows_per);
+        prefix_attention_kernel<D><<<dim3(static_cast<unsigned>(kXcds * xcd_per(pblocks))), 64 * kPfxWaves, 0, st>>>(p);
+        if (int s = check_launch("prefix_attention_kernel")) return s;
+      } else {
+        pr.pfx_x = nullptr;
+      }
+      const dim3 grid(static_cast<unsigned>(kXcds * xcd_per(ceil_div(p.rows, kMfWaves))));
+      if (p.blk_log2 > 0) sparse_attention_mfma_kernel<D, true><<<grid, 64 * kMfWaves, 0, st>>>(pr);
+      else sparse_attention_mfma_kernel<D, false><<<grid, 64 * kMfWaves, 0, st>>>(pr);
       return check_launch("sparse_attention_mfma_kernel");
     }
   }
@@ -834,6 +1135,18 @@ int launch_att(const AttParams& p, int d, hipStream_t st) {
 using namespace ssa;
 
 namespace ssa {
+// Workspace of the dense-prefix path: X per row, then the prefix state per
+// (row, head).  Zero where the path does not run (fp32, head dims other than
+// 64 and 128, groups over 8, fewer than 64 keys per row, block mode).
+size_t attention_ws_bytes(int dtype, int64_t batch, int64_t n_q, int h_q, int h_kv, int d, int top_k) {
+  if (dtype != SSA_DTYPE_BF16 || (d != 64 && d != 128) || h_kv <= 0 || h_q % h_kv != 0 || h_q / h_kv > 8 ||
+      top_k < 2 * kMfChunk || batch <= 0 || n_q <= 0)
+    return 0;
+  const size_t rows = static_cast<size_t>(batch * h_kv * n_q);
+  return align_up(sizeof(int32_t) * rows, 256) +
+         sizeof(float) * rows * static_cast<size_t>(h_q / h_kv) * static_cast<size_t>(d + 4);
+}
+
 // Token indices (blk_log2 = 0, top_k keys per row) or key-block ids
 // (blk_log2 > 0: top_k = blocks per row, nbk blocks in all).
 int attention_entry(const void* q, const void* k, const void* v, int dtype, int64_t batch, int64_t n,
@@ -842,7 +1155,8 @@ int attention_entry(const void* q, const void* k, const void* v, int dtype, int6
                     int64_t v_sh, const void* idx, int idx_dtype, int top_k, int64_t idx_sb, int64_t idx_sn,
                     int64_t idx_sh, float scale_div, int causal, const int32_t* row_order, void* out,
                     int out_dtype, int64_t o_sb, int64_t o_sn, int64_t o_sh, int32_t* error_flag,
-                    void* stream, int blk_log2, int64_t nbk) {
+                    void* stream, int blk_log2, int64_t nbk, void* workspace, size_t workspace_bytes,
+                    const int32_t* row_prefix) {
   if (n_q < 0 || q_pos0 < 0 || q_pos0 + n_q > n)
     return fail(SSA_ERR_INVALID_ARGUMENT, "sparse_attention: query rows [%lld, %lld) outside the %lld keys",
                 static_cast<long long>(q_pos0), static_cast<long long>(q_pos0 + n_q),
@@ -909,6 +1223,17 @@ int attention_entry(const void* q, const void* k, const void* v, int dtype, int6
   }
   if (p.rows >= (int64_t(1) << 31))
     return fail(SSA_ERR_UNSUPPORTED, "sparse_attention: too many rows");
+  if (workspace) {
+    const size_t need = attention_ws_bytes(dtype, batch, n_q, h_q, h_kv, d, blk_log2 > 0 ? 0 : top_k);
+    if (workspace_bytes < need)
+      return fail(SSA_ERR_WORKSPACE, "sparse_attention: workspace %zu < %zu bytes", workspace_bytes, need);
+    if (need > 0) {
+      p.pfx_x = row_prefix ? const_cast<int32_t*>(row_prefix) : static_cast<int32_t*>(workspace);
+      p.pfx_given = row_prefix ? 1 : 0;
+      p.pfx_part = reinterpret_cast<float*>(static_cast<char*>(workspace) +
+                                            align_up(sizeof(int32_t) * static_cast<size_t>(p.rows), 256));
+    }
+  }
   hipStream_t st = as_stream(stream);
   if (dtype == SSA_DTYPE_BF16) return launch_att<uint16_t>(p, d, st);
   return launch_att<float>(p, d, st);
@@ -920,11 +1245,18 @@ extern "C" int ssa_sparse_attention_block(
     int64_t q_pos0, int h_q, int h_kv, int d, int64_t q_sb, int64_t q_sn, int64_t q_sh, int64_t k_sb,
     int64_t k_sn, int64_t k_sh, int64_t v_sb, int64_t v_sn, int64_t v_sh, const void* idx,
     int idx_dtype, int top_k, int64_t idx_sb, int64_t idx_sn, int64_t idx_sh, float scale_div,
-    int causal, const int32_t* row_order, void* out, int out_dtype, int64_t o_sb, int64_t o_sn,
-    int64_t o_sh, int32_t* error_flag, void* stream) {
+    int causal, const int32_t* row_order, const int32_t* row_prefix, void* out, int out_dtype,
+    int64_t o_sb, int64_t o_sn, int64_t o_sh, int32_t* error_flag, void* workspace, size_t workspace_bytes,
+    void* stream) {
   return attention_entry(q, k, v, dtype, batch, n, n_q, q_pos0, h_q, h_kv, d, q_sb, q_sn, q_sh, k_sb, k_sn,
                          k_sh, v_sb, v_sn, v_sh, idx, idx_dtype, top_k, idx_sb, idx_sn, idx_sh, scale_div,
-                         causal, row_order, out, out_dtype, o_sb, o_sn, o_sh, error_flag, stream, 0, 0);
+                         causal, row_order, out, out_dtype, o_sb, o_sn, o_sh, error_flag, stream, 0, 0,
+                         workspace, workspace_bytes, row_prefix);
+}
+
+extern "C" size_t ssa_sparse_attention_workspace_bytes(int dtype, int64_t batch, int64_t n_q, int h_q,
+                                                       int h_kv, int d, int top_k) {
+  return attention_ws_bytes(dtype, batch, n_q, h_q, h_kv, d, top_k);
 }
 
 extern "C" int ssa_block_sparse_attention(
@@ -942,7 +1274,7 @@ extern "C" int ssa_block_sparse_attention(
   const int64_t nbk = (n + block_size - 1) / block_size;
   return attention_entry(q, k, v, dtype, batch, n, n, 0, h_q, h_kv, d, q_sb, q_sn, q_sh, k_sb, k_sn, k_sh,
                          v_sb, v_sn, v_sh, blocks, idx_dtype, n_k_blocks, b_sb, b_sq, b_sh, scale_div, 1,
-                         nullptr, out, out_dtype, o_sb, o_sn, o_sh, error_flag, stream, lg, nbk);
+                         nullptr, out, out_dtype, o_sb, o_sn, o_sh, error_flag, stream, lg, nbk, nullptr, 0);
 }
 
 extern "C" int ssa_sparse_attention(const void* q, const void* k, const void* v, int dtype,
@@ -952,10 +1284,11 @@ extern "C" int ssa_sparse_attention(const void* q, const void* k, const void* v,
                                     int64_t v_sh, const void* idx, int idx_dtype, int top_k,
                                     int64_t idx_sb, int64_t idx_sn, int64_t idx_sh,
                                     float scale_div, int causal, const int32_t* row_order,
-                                    void* out, int out_dtype,
+                                    const int32_t* row_prefix, void* out, int out_dtype,
                                     int64_t o_sb, int64_t o_sn, int64_t o_sh, int32_t* error_flag,
-                                    void* stream) {
+                                    void* workspace, size_t workspace_bytes, void* stream) {
   return attention_entry(q, k, v, dtype, batch, n, n, 0, h_q, h_kv, d, q_sb, q_sn, q_sh, k_sb, k_sn, k_sh,
                          v_sb, v_sn, v_sh, idx, idx_dtype, top_k, idx_sb, idx_sn, idx_sh, scale_div, causal,
-                         row_order, out, out_dtype, o_sb, o_sn, o_sh, error_flag, stream, 0, 0);
+                         row_order, out, out_dtype, o_sb, o_sn, o_sh, error_flag, stream, 0, 0, workspace,
+                         workspace_bytes, row_prefix);
 }

@@ -54,6 +54,16 @@ __device__ __forceinline__ uint32_t key_index(uint64_t key) {
 // fp32 fused multiply-add, single rounding (v_fma_f32).
 __device__ __forceinline__ float fma_rn(float a, float b, float c) { return __builtin_fmaf(a, b, c); }
 
+// The GPU hands workgroups to its 8 XCDs (each with its own L2) round-robin:
+// workgroup w runs on XCD w mod 8.  xcd_block maps the launched workgroup w of
+// a grid of 8 * per workgroups to the logical block (w mod 8) * per + w / 8, so
+// that XCD x runs the contiguous logical blocks [x * per, (x + 1) * per) and
+// its L2 holds their shared data (the rows of one KV head, say) instead of a
+// slice of everything.  Logical blocks at or past the real count are idle.
+constexpr int kXcds = 8;
+__host__ __device__ inline int64_t xcd_per(int64_t nblocks) { return (nblocks + kXcds - 1) / kXcds; }
+__device__ __forceinline__ int64_t xcd_block(int64_t w, int64_t per) { return (w % kXcds) * per + w / kXcds; }
+
 // Block-strided loop over elements [0, count) (thread `tid` of NT takes tid,
 // tid + NT, ...) that issues U independent loads before it uses any of them.
 // A loop whose body loads one element and then uses it waits out a whole

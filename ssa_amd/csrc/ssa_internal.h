@@ -31,15 +31,19 @@ int select_entry(const void* q, const void* k, int dtype, int64_t batch, int64_t
                  float score_div, int sorted, const int32_t* row_order, void* out,
                  int out_index_dtype, int32_t* stats, void* workspace, size_t workspace_bytes,
                  void* stream, int64_t post_bh, const int32_t* tail_offsets,
-                 const int32_t* tail_postings, int64_t tail_bh, int64_t tail_key0);
+                 const int32_t* tail_postings, int64_t tail_bh, int64_t tail_key0,
+                 int32_t* row_prefix = nullptr);
 
-// ssa_sparse_attention_block (blk_log2 = 0) or the block-granular variant.
+// ssa_sparse_attention_block (blk_log2 = 0) or the block-granular variant;
+// a workspace of attention_ws_bytes(...) bytes enables the dense-prefix path.
+size_t attention_ws_bytes(int dtype, int64_t batch, int64_t n_q, int h_q, int h_kv, int d, int top_k);
 int attention_entry(const void* q, const void* k, const void* v, int dtype, int64_t batch, int64_t n,
                     int64_t n_q, int64_t q_pos0, int h_q, int h_kv, int d, int64_t q_sb, int64_t q_sn,
                     int64_t q_sh, int64_t k_sb, int64_t k_sn, int64_t k_sh, int64_t v_sb, int64_t v_sn,
                     int64_t v_sh, const void* idx, int idx_dtype, int top_k, int64_t idx_sb, int64_t idx_sn,
                     int64_t idx_sh, float scale_div, int causal, const int32_t* row_order, void* out,
                     int out_dtype, int64_t o_sb, int64_t o_sn, int64_t o_sh, int32_t* error_flag,
-                    void* stream, int blk_log2, int64_t nbk);
+                    void* stream, int blk_log2, int64_t nbk, void* workspace = nullptr,
+                    size_t workspace_bytes = 0, const int32_t* row_prefix = nullptr);
 
 }  // namespace ssa

@@ -54,6 +54,10 @@ struct SelParams {
   void* out;
   int out_i64;
   int32_t* stats;
+  // Nullable [rows]: X per row, the key prefix [0, X) that the row's indices
+  // hold exactly once (its lowest-key filler and the candidates below it);
+  // 0 for a row without filler.  Stage (d) attends such prefixes densely.
+  int32_t* prefix;
   int64_t n_q, q_pos0;   // query rows (q, q_codes, out, stats) and the position of row 0
   int64_t rows;          // batch * h_kv * n_q
   const int32_t* order;  // nullable [rows]: slot t of head bh runs query row order[bh * n_q + t]
@@ -424,6 +428,10 @@ __device__ __forceinline__ void select_row(const SelParams& p, const T* __restri
     p.stats[(bh * p.n_q + r) * 2 + 0] = s_cand;
     p.stats[(bh * p.n_q + r) * 2 + 1] = s_R;
   }
+  // the filler stage[nsel .. k_eff) is the lowest keys the row does not hold:
+  // every key up to its last one is in the row once (see select_light_kernel)
+  if (p.prefix && tid == 0)
+    p.prefix[row] = (nsel < p.k_eff && p.k_eff == p.top_k) ? stage[p.k_eff - 1] + 1 : 0;
 }
 
 template <typename T, int GMAX, int D>
@@ -650,6 +658,7 @@ __global__ __launch_bounds__(64) void select_light_kernel(SelParams p, int64_t r
   __builtin_amdgcn_wave_barrier();
 
   if (C > p.k_eff) {
+    if (p.prefix && lane == 0) p.prefix[row] = 0;
     const int shard = static_cast<int>(blockIdx.x % kShards);
     int32_t* sc = w.ctr + 16 + 4 * shard;
     int64_t off = -1;
@@ -695,6 +704,11 @@ __global__ __launch_bounds__(64) void select_light_kernel(SelParams p, int64_t r
   };
   // Candidates ascending, then the lowest non-candidates up to k_eff.
   int filled = flat ? light_emit_flat(bm, live, lane, put) : light_emit(sm, bm, slive, lane, put);
+  // The filler is the k_eff - C lowest keys the row does not hold, so every key
+  // up to the last one is in the row, once: X = last filler key + 1 (0 without
+  // filler, and 0 when index-0 padding repeats a key).
+  const bool want_x = p.prefix != nullptr && p.k_eff == p.top_k;
+  if (p.prefix && lane == 0 && (filled >= p.k_eff || !want_x)) p.prefix[row] = 0;
   for (int w0 = 0; filled < p.k_eff; w0 += 64) {
     const int x = w0 + lane;
     uint32_t bits = 0u;
@@ -706,7 +720,9 @@ __global__ __launch_bounds__(64) void select_light_kernel(SelParams p, int64_t r
     int total = 0;
     int pos = filled + wave_excl_scan(__popc(bits), lane, &total);
     while (bits != 0u && pos < p.k_eff) {
-      put(pos++, x * 32 + __ffs(bits) - 1);
+      const int key = x * 32 + __ffs(bits) - 1;
+      if (want_x && pos == p.k_eff - 1) p.prefix[row] = key + 1;
+      put(pos++, key);
       bits &= bits - 1u;
     }
     filled += total;
@@ -1331,7 +1347,8 @@ int select_entry(const void* q, const void* k, int dtype, int64_t batch, int64_t
                  float score_div, int sorted, const int32_t* row_order, void* out,
                  int out_index_dtype, int32_t* stats, void* workspace, size_t workspace_bytes,
                  void* stream, int64_t post_bh, const int32_t* tail_offsets,
-                 const int32_t* tail_postings, int64_t tail_bh, int64_t tail_key0) {
+                 const int32_t* tail_postings, int64_t tail_bh, int64_t tail_key0,
+                 int32_t* row_prefix) {
   if (n_q < 0 || q_pos0 < 0 || q_pos0 + n_q > n)
     return fail(SSA_ERR_INVALID_ARGUMENT, "select: query rows [%lld, %lld) outside the %lld keys",
                 static_cast<long long>(q_pos0), static_cast<long long>(q_pos0 + n_q),
@@ -1395,6 +1412,7 @@ int select_entry(const void* q, const void* k, int dtype, int64_t batch, int64_t
   p.out = out;
   p.out_i64 = (out_index_dtype == SSA_INDEX_I64);
   p.stats = stats;
+  p.prefix = row_prefix;
   p.n_q = n_q;
   p.q_pos0 = q_pos0;
   p.rows = batch * h_kv * n_q;
@@ -1481,7 +1499,7 @@ extern "C" int ssa_select_block_noalloc(const void* q, const void* k, int dtype,
                                         int mask_mode, const uint8_t* mask, int64_t mask_sb,
                                         int64_t mask_si, float score_div, int sorted,
                                         const int32_t* row_order, void* out, int out_index_dtype,
-                                        int32_t* stats, void* stream) {
+                                        int32_t* stats, int32_t* row_prefix, void* stream) {
   if (batch < 0 || n_q < 0 || h_kv <= 0 || top_k < 0)
     return fail(SSA_ERR_INVALID_ARGUMENT, "select (no alloc): bad shape");
   const size_t need = ssa_select_workspace_bytes(batch, n_q, h_kv, 0);
@@ -1496,14 +1514,14 @@ extern "C" int ssa_select_block_noalloc(const void* q, const void* k, int dtype,
     return ssa_select_block(q, k, dtype, batch, n, n_q, q_pos0, h_q, h_kv, d, q_sb, q_sn, q_sh,
                             k_sb, k_sn, k_sh, q_codes, a, offsets, postings, n_c, b, top_k,
                             mask_mode, mask, mask_sb, mask_si, score_div, sorted, row_order, out,
-                            out_index_dtype, stats, nullptr, 0, stream);
+                            out_index_dtype, stats, row_prefix, nullptr, 0, stream);
   int st = SSA_OK;
   void* ws = ssa::scratch_address(&st);
   if (!ws) return st;
   return ssa_select_block(q, k, dtype, batch, n, n_q, q_pos0, h_q, h_kv, d, q_sb, q_sn, q_sh, k_sb,
                           k_sn, k_sh, q_codes, a, offsets, postings, n_c, b, top_k, mask_mode, mask,
                           mask_sb, mask_si, score_div, sorted, row_order, out, out_index_dtype,
-                          stats, ws, bytes, stream);
+                          stats, row_prefix, ws, bytes, stream);
 }
 
 extern "C" int ssa_select_block(const void* q, const void* k, int dtype, int64_t batch, int64_t n,
@@ -1513,12 +1531,13 @@ extern "C" int ssa_select_block(const void* q, const void* k, int dtype, int64_t
                                 const int32_t* postings, int n_c, int b, int top_k, int mask_mode,
                                 const uint8_t* mask, int64_t mask_sb, int64_t mask_si,
                                 float score_div, int sorted, const int32_t* row_order, void* out,
-                                int out_index_dtype, int32_t* stats, void* workspace,
-                                size_t workspace_bytes, void* stream) {
+                                int out_index_dtype, int32_t* stats, int32_t* row_prefix,
+                                void* workspace, size_t workspace_bytes, void* stream) {
   return ssa::select_entry(q, k, dtype, batch, n, n_q, q_pos0, h_q, h_kv, d, q_sb, q_sn, q_sh, k_sb,
                            k_sn, k_sh, q_codes, a, offsets, postings, n_c, b, top_k, mask_mode, mask,
                            mask_sb, mask_si, score_div, sorted, row_order, out, out_index_dtype,
-                           stats, workspace, workspace_bytes, stream, n * b, nullptr, nullptr, 0, 0);
+                           stats, workspace, workspace_bytes, stream, n * b, nullptr, nullptr, 0, 0,
+                           row_prefix);
 }
 
 extern "C" int ssa_select(const void* q, const void* k, int dtype, int64_t batch, int64_t n,
@@ -1527,10 +1546,10 @@ extern "C" int ssa_select(const void* q, const void* k, int dtype, int64_t batch
                           const int32_t* offsets, const int32_t* postings, int n_c, int b,
                           int top_k, int mask_mode, const uint8_t* mask, int64_t mask_sb,
                           int64_t mask_si, float score_div, int sorted, const int32_t* row_order,
-                          void* out, int out_index_dtype, int32_t* stats, void* workspace,
-                          size_t workspace_bytes, void* stream) {
+                          void* out, int out_index_dtype, int32_t* stats, int32_t* row_prefix,
+                          void* workspace, size_t workspace_bytes, void* stream) {
   return ssa_select_block(q, k, dtype, batch, n, n, 0, h_q, h_kv, d, q_sb, q_sn, q_sh, k_sb, k_sn,
                           k_sh, q_codes, a, offsets, postings, n_c, b, top_k, mask_mode, mask,
                           mask_sb, mask_si, score_div, sorted, row_order, out, out_index_dtype,
-                          stats, workspace, workspace_bytes, stream);
+                          stats, row_prefix, workspace, workspace_bytes, stream);
 }

@@ -66,9 +66,9 @@ def ssa_attention_bnhd(query: torch.Tensor, key: torch.Tensor, value: torch.Tens
     selected keys.  Returns ``[B, n, h_q, d]`` (contiguous).  Differentiable in
     query, key and value."""
     res = router.route(query, key, causal_mask=True, hard=True, sorted=False,
-                       index_dtype=torch.int32, with_order=True)
+                       index_dtype=torch.int32, with_order=True, with_prefix=True)
     return sparse_exact_attention(query, key, value, res.indices, causal=causal_attention,
-                                  check_indices=False, row_order=res.order)
+                                  check_indices=False, row_order=res.order, row_prefix=res.prefix)
 
 
 def replace_attention_forward(model=None):

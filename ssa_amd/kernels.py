@@ -167,7 +167,8 @@ def select(q: torch.Tensor, k: torch.Tensor, q_codes: torch.Tensor, offsets: tor
            mask: Optional[torch.Tensor] = None, score_div: Optional[float] = None,
            index_dtype: torch.dtype = torch.int64,
            with_stats: bool = False, sorted: bool = True, use_workspace: Union[bool, int] = True,
-           row_order: Optional[torch.Tensor] = None, q_pos0: Optional[int] = None):
+           row_order: Optional[torch.Tensor] = None, q_pos0: Optional[int] = None,
+           row_prefix: Optional[torch.Tensor] = None):
     """Stage (c): candidate indices [B, n_q, h_kv, top_k] (ssa/router.py:151-214).
 
     ``q`` and ``q_codes`` may hold fewer rows (n_q) than ``k`` has keys (n): a
@@ -184,6 +185,9 @@ def select(q: torch.Tensor, k: torch.Tensor, q_codes: torch.Tensor, offsets: tor
     recommended ``ssa_select_workspace_bytes(B, n, h_kv, top_k)`` (same results).
     ``row_order`` (int32 [B, h_kv, n], a permutation of 0..n-1 per head, e.g.
     ``query_order``) only sets the order in which rows are processed.
+    ``row_prefix`` (int32 [B, h_kv, n_q], written): X per row, the key prefix
+    [0, X) its indices hold exactly once (the lowest-key filler), for
+    ``sparse_attention``'s dense-prefix pass.
     """
     _check_rows(q, "q")
     _check_rows(k, "k")
@@ -215,6 +219,11 @@ def select(q: torch.Tensor, k: torch.Tensor, q_codes: torch.Tensor, offsets: tor
         if row_order.dtype != torch.int32 or tuple(row_order.shape) != (B, h_kv, n_q):
             raise ValueError(f"row_order must be int32 [{B}, {h_kv}, {n_q}]")
         row_order = row_order.contiguous()
+    if row_prefix is not None:
+        _lib.require_device(row_prefix)
+        if (row_prefix.dtype != torch.int32 or tuple(row_prefix.shape) != (B, h_kv, n_q)
+                or not row_prefix.is_contiguous()):
+            raise ValueError(f"row_prefix must be a contiguous int32 [{B}, {h_kv}, {n_q}] tensor")
     out = torch.empty((B, n_q, h_kv, top_k), device=q.device, dtype=index_dtype)
     stats = torch.empty((B, h_kv, n_q, 2), device=q.device, dtype=torch.int32) if with_stats else None
     ws_bytes, ws = 0, None
@@ -228,7 +237,7 @@ def select(q: torch.Tensor, k: torch.Tensor, q_codes: torch.Tensor, offsets: tor
          q.stride(0), q.stride(1), q.stride(2), k.stride(0), k.stride(1), k.stride(2),
          ptr(q_codes), a, ptr(offsets), ptr(postings), n_c, b, top_k, mask_mode, ptr(mask),
          m_sb, m_si, float(score_div), int(bool(sorted)), ptr(row_order), ptr(out), _lib.index_dtype(out),
-         ptr(stats), ptr(ws), ws_bytes, stream_of(q))
+         ptr(stats), ptr(row_prefix), ptr(ws), ws_bytes, stream_of(q))
     return (out, stats) if with_stats else out
 
 
@@ -237,14 +246,19 @@ def sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, idx: tor
                      out: Optional[torch.Tensor] = None,
                      error_flag: Optional[torch.Tensor] = None,
                      row_order: Optional[torch.Tensor] = None,
-                     q_pos0: Optional[int] = None) -> torch.Tensor:
+                     q_pos0: Optional[int] = None, dense_prefix: bool = True,
+                     row_prefix: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Stage (d): gathered exact attention, [B, n_q, h_q, d] in q's dtype (ssa/attention.py:12-115).
 
     ``row_order`` (int32 [B, h_kv, n_q], a permutation of 0..n_q-1 per head) only
     sets the order in which rows are processed; results are the same.  ``q`` and
     ``idx`` may hold fewer rows (n_q) than ``k``/``v`` have keys: query row r
     then sits at key position ``q_pos0 + r`` (default n - n_q), which is what
-    ``causal`` compares the indices with."""
+    ``causal`` compares the indices with.  ``dense_prefix`` (bf16, d 64 or 128):
+    the keys [0, X) a row's indices hold exactly once are attended in blocks of
+    neighbouring rows that load them once (a workspace of the library's size);
+    ``row_prefix`` (int32 [B, h_kv, n_q], from ``select``) gives X per row, which
+    the pass otherwise finds from the indices."""
     for name, t in (("q", q), ("k", k), ("v", v), ("indices", idx)):
         _check_rows(t, name)
     _lib.require_device(q, k, v, idx)
@@ -265,13 +279,23 @@ def sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, idx: tor
         if row_order.dtype != torch.int32 or tuple(row_order.shape) != (B, h_kv, n_q):
             raise ValueError(f"row_order must be int32 [{B}, {h_kv}, {n_q}]")
         row_order = row_order.contiguous()
+    ws_bytes = 0
+    if dense_prefix:
+        ws_bytes = int(_lib.load().ssa_sparse_attention_workspace_bytes(
+            _lib.elem_dtype(q), B, n_q, h_q, h_kv, d, top_k))
+    ws = torch.empty(ws_bytes, device=q.device, dtype=torch.uint8) if ws_bytes else None
+    if row_prefix is not None:
+        _lib.require_device(row_prefix)
+        if (row_prefix.dtype != torch.int32 or tuple(row_prefix.shape) != (B, h_kv, n_q)
+                or not row_prefix.is_contiguous()):
+            raise ValueError(f"row_prefix must be a contiguous int32 [{B}, {h_kv}, {n_q}] tensor")
     call("ssa_sparse_attention_block", ptr(q), ptr(k), ptr(v), _lib.elem_dtype(q), B, n, n_q, q_pos0,
          h_q, h_kv, d,
          q.stride(0), q.stride(1), q.stride(2), k.stride(0), k.stride(1), k.stride(2),
          v.stride(0), v.stride(1), v.stride(2), ptr(idx), _lib.index_dtype(idx), top_k,
          idx.stride(0), idx.stride(1), idx.stride(2), float(scale_div), int(bool(causal)),
-         ptr(row_order), ptr(out), _lib.elem_dtype(out), out.stride(0), out.stride(1), out.stride(2),
-         ptr(error_flag), stream_of(q))
+         ptr(row_order), ptr(row_prefix), ptr(out), _lib.elem_dtype(out), out.stride(0), out.stride(1),
+         out.stride(2), ptr(error_flag), ptr(ws), ws_bytes, stream_of(q))
     return out
 
 

@@ -120,14 +120,17 @@ class CodebookRouter(nn.Module):
 
     def route(self, q_full: torch.Tensor, k_full: torch.Tensor, causal_mask: MaskArg = None,
               hard: bool = True, with_stats: bool = False, index_dtype=torch.int64,
-              sorted: bool = True, with_order: bool = False):
+              sorted: bool = True, with_order: bool = False, with_prefix: bool = False):
         """Run stages (a)-(c) and keep the intermediates (a RouteResult).
 
         ``with_order`` also returns ``order`` (int32 [B, h_kv, n]): per head, the
         query positions grouped by their best code (ascending within a code).
         Selection already runs its rows in this order, and attention can too:
         rows that share buckets and candidate keys then run together.  It
-        changes no result."""
+        changes no result.  ``with_prefix`` also returns ``prefix`` (int32
+        [B, h_kv, n]): X per row, the keys [0, X) its indices hold once (the
+        lowest-key filler), which ``sparse_exact_attention(row_prefix=...)``
+        attends in a dense pass."""
         if not hard:
             raise NotImplementedError(
                 "hard=False (Gumbel-softmax assignment) is not supported: the reference's one-hot "
@@ -152,12 +155,15 @@ class CodebookRouter(nn.Module):
         if mask is not None:
             mask = mask.to(q.device)
         order = query_order(q_codes, self.num_codebook) if with_order else None
+        prefix = (torch.empty(q.shape[0], self.num_kv_heads, n, device=q.device, dtype=torch.int32)
+                  if with_prefix else None)
         res = kernels.select(q, k, q_codes, offsets, postings, self.codes_per_key, self.top_k,
                              mode, mask, index_dtype=index_dtype, with_stats=with_stats,
-                             sorted=sorted, row_order=order)
+                             sorted=sorted, row_order=order, row_prefix=prefix)
         idx, stats = res if with_stats else (res, None)
         out = RouteResult(q_codes, k_codes, offsets, postings, idx, stats)
         out.order = order
+        out.prefix = prefix
         out.indices_view = idx[0] if unbatched else idx
         return out
 
@@ -186,11 +192,11 @@ class RouteResult:
     offsets int32 [B, h_kv, N_c + 1], postings int32 [B, h_kv, n * b],
     indices [B, n, h_kv, top_k], stats int32 [B, h_kv, n, 2] or None
     (unique candidates, postings read), order int32 [B, h_kv, n] or None (see
-    query_order); indices_view is the reference-shaped view returned by
-    forward()."""
+    query_order), prefix int32 [B, h_kv, n] or None (X per row, see route);
+    indices_view is the reference-shaped view returned by forward()."""
 
     __slots__ = ("q_codes", "k_codes", "offsets", "postings", "indices", "stats", "order",
-                 "indices_view")
+                 "prefix", "indices_view")
 
     def __init__(self, q_codes, k_codes, offsets, postings, indices, stats):
         self.q_codes = q_codes
@@ -200,4 +206,5 @@ class RouteResult:
         self.indices = indices
         self.stats = stats
         self.order = None
+        self.prefix = None
         self.indices_view = indices

@@ -156,9 +156,10 @@ class SSAAttention(nn.Module):
             # of each head are attended grouped by best code, so rows sharing
             # candidate keys run together (no result depends on that order).
             res = self.router.route(q, k, causal_mask=True, hard=True, sorted=False,
-                                    index_dtype=torch.int32, with_order=True)
+                                    index_dtype=torch.int32, with_order=True, with_prefix=True)
             out = sparse_exact_attention(q, k, v, res.indices, causal=self.causal_attention,
-                                         check_indices=False, row_order=res.order)
+                                         check_indices=False, row_order=res.order,
+                                         row_prefix=res.prefix)
         return self.o_proj(out.reshape(B, n, -1).to(hidden_states.dtype))
 
 

@@ -117,7 +117,8 @@ def _select(L, **kw):
              q_sb=1024 * 32 * 128, q_sn=32 * 128, q_sh=128, k_sb=1024 * 8 * 128, k_sn=8 * 128,
              k_sh=128, q_codes=FAKE, a=16, offsets=FAKE, postings=FAKE, n_c=4096, b=4, top_k=512,
              mask_mode=_lib.MASK_CAUSAL, mask=NULL, mask_sb=0, mask_si=0, score_div=11.3137,
-             sorted=0, row_order=NULL, out=FAKE, out_index_dtype=_lib.INDEX_I64, stats=NULL, workspace=NULL,
+             sorted=0, row_order=NULL, out=FAKE, out_index_dtype=_lib.INDEX_I64, stats=NULL,
+             row_prefix=NULL, workspace=NULL,
              workspace_bytes=0, stream=NULL)
     a.update(kw)
     st = L.ssa_select(*a.values())
@@ -171,9 +172,10 @@ def _attention(L, **kw):
              d=128, q_sb=1024 * 32 * 128, q_sn=32 * 128, q_sh=128, k_sb=1024 * 8 * 128,
              k_sn=8 * 128, k_sh=128, v_sb=1024 * 8 * 128, v_sn=8 * 128, v_sh=128, idx=FAKE,
              idx_dtype=_lib.INDEX_I64, top_k=512, idx_sb=1024 * 8 * 512, idx_sn=8 * 512,
-             idx_sh=512, scale_div=11.3137, causal=1, row_order=NULL, out=FAKE,
+             idx_sh=512, scale_div=11.3137, causal=1, row_order=NULL, row_prefix=NULL, out=FAKE,
              out_dtype=_lib.DTYPE_BF16,
-             o_sb=1024 * 32 * 128, o_sn=32 * 128, o_sh=128, error_flag=NULL, stream=NULL)
+             o_sb=1024 * 32 * 128, o_sn=32 * 128, o_sh=128, error_flag=NULL, workspace=NULL,
+             workspace_bytes=0, stream=NULL)
     a.update(kw)
     st = L.ssa_sparse_attention(*a.values())
     return st, (L.ssa_last_error() or b"").decode()
@@ -196,6 +198,20 @@ def test_attention_rejects(L, kw, status, text):
     st, msg = _attention(L, **kw)
     assert st == status, msg
     assert text in msg
+
+
+def test_attention_workspace_bytes(L):
+    """The dense-prefix workspace: X per row (256-byte aligned), then the state
+    of each (row, head), d + 4 floats; none where the pass does not run."""
+    rows, g = 1 * 8 * 1024, 4
+    need = L.ssa_sparse_attention_workspace_bytes(_lib.DTYPE_BF16, 1, 1024, 32, 8, 128, 512)
+    assert need == rows * 4 + rows * g * (128 + 4) * 4
+    assert L.ssa_sparse_attention_workspace_bytes(_lib.DTYPE_F32, 1, 1024, 32, 8, 128, 512) == 0
+    assert L.ssa_sparse_attention_workspace_bytes(_lib.DTYPE_BF16, 1, 1024, 32, 8, 96, 512) == 0
+    assert L.ssa_sparse_attention_workspace_bytes(_lib.DTYPE_BF16, 1, 1024, 32, 2, 128, 512) == 0
+    assert L.ssa_sparse_attention_workspace_bytes(_lib.DTYPE_BF16, 1, 1024, 32, 8, 128, 32) == 0
+    st, msg = _attention(L, workspace=FAKE, workspace_bytes=need - 1)
+    assert st == _lib.SSA_ERR_WORKSPACE and "workspace" in msg
 
 
 def test_index_rejects(L):
@@ -266,13 +282,13 @@ def test_block_entry_points_reject_rows_past_the_keys(L):
     [q_pos0, q_pos0 + n_q) must lie inside the n keys (checked before any launch)."""
     null = ctypes.c_void_p(0)
     st = L.ssa_sparse_attention_block(null, null, null, 0, 1, 32, 4, 30, 4, 2, 64, 0, 256, 64, 0, 128,
-                                      64, 0, 128, 64, null, 0, 8, 0, 16, 8, 8.0, 1, null, null, 0,
-                                      0, 256, 64, null, null)
+                                      64, 0, 128, 64, null, 0, 8, 0, 16, 8, 8.0, 1, null, null, null,
+                                      0, 0, 256, 64, null, null, 0, null)
     assert st == _lib.SSA_ERR_INVALID_ARGUMENT
     assert b"outside" in L.ssa_last_error()
     st = L.ssa_select_block(null, null, 0, 1, 32, 4, -1, 4, 2, 64, 0, 256, 64, 0, 128, 64, null, 8,
-                            null, null, 16, 4, 8, 1, null, 0, 0, 8.0, 0, null, null, 0, null, null, 0,
-                            null)
+                            null, null, 16, 4, 8, 1, null, 0, 0, 8.0, 0, null, null, 0, null, null, null,
+                            0, null)
     assert st == _lib.SSA_ERR_INVALID_ARGUMENT
 
 

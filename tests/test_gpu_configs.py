@@ -176,11 +176,13 @@ def c4(dev):
         q_lin = layer.q_proj(h).view(B, n, layer.num_q_heads, layer.head_dim)
         k_lin = layer.k_proj(h).view(B, n, layer.num_kv_heads, layer.head_dim)
         res = layer.router.route(q, k, causal_mask=True, sorted=False, index_dtype=torch.int32,
-                                 with_order=True)
+                                 with_order=True, with_prefix=True)
         att32 = torch.empty(q.shape, device=dev, dtype=torch.float32)
         from ssa_amd import kernels
-        kernels.sparse_attention(q, k, v, res.indices, None, False, out=att32, row_order=res.order)
-        att_bf16 = kernels.sparse_attention(q, k, v, res.indices, None, False, row_order=res.order)
+        kernels.sparse_attention(q, k, v, res.indices, None, False, out=att32, row_order=res.order,
+                                 row_prefix=res.prefix)
+        att_bf16 = kernels.sparse_attention(q, k, v, res.indices, None, False, row_order=res.order,
+                                            row_prefix=res.prefix)
         again = layer.o_proj(att_bf16.reshape(B, n, -1))
     torch.cuda.synchronize()
     return dict(layer=layer, freqs=blk["freqs"], out=out, q=q, k=k, v=v, q_lin=q_lin, k_lin=k_lin,

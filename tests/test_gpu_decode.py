@@ -47,7 +47,8 @@ def _prefix_forward(router, q, k, v, n):
     off, post = kernels.build_index(kc, router.num_codebook)
     idx = kernels.select(qp, kp, qc, off, post, router.codes_per_key, router.top_k, sorted=False,
                          index_dtype=torch.int32)
-    out = kernels.sparse_attention(qp, kp, vp, idx, None, True)
+    # the row path alone (the dense-prefix pass sums the same terms in another order)
+    out = kernels.sparse_attention(qp, kp, vp, idx, None, True, dense_prefix=False)
     return idx, out
 
 

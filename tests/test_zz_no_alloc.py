@@ -36,17 +36,18 @@ def _call(L, name, q, k, qc, off, post, b, top_k, sorted_, ws=None):
     n_c = off.shape[-1] - 1
     out = torch.full((B, n, h_kv, top_k), -7, device=q.device, dtype=torch.int32)
     stats = torch.full((B, h_kv, n, 2), -7, device=q.device, dtype=torch.int32)
+    prefix = torch.full((B, h_kv, n), -7, device=q.device, dtype=torch.int32)
     args = [_lib.ptr(q), _lib.ptr(k), _lib.DTYPE_BF16, B, n, n, 0, h_q, h_kv, d,
             q.stride(0), q.stride(1), q.stride(2), k.stride(0), k.stride(1), k.stride(2),
             _lib.ptr(qc), a, _lib.ptr(off), _lib.ptr(post), n_c, b, top_k, _lib.MASK_CAUSAL, None,
             0, 0, float(d ** 0.5), int(sorted_), None, _lib.ptr(out), _lib.INDEX_I32,
-            _lib.ptr(stats)]
+            _lib.ptr(stats), _lib.ptr(prefix)]
     if ws is not None:
         args += [_lib.ptr(ws), ws.numel()]
     args.append(_lib.stream_of(q))
     st = getattr(L, name)(*args)
     assert st == _lib.SSA_OK, (L.ssa_last_error() or b"").decode()
-    return out, stats
+    return out, stats, prefix
 
 
 @pytest.mark.parametrize("sorted_", [False, True])
@@ -63,11 +64,13 @@ def test_noalloc_select_equals_workspace_select_twice(dev, sorted_):
         b = c["b"]
         nbytes = L.ssa_select_workspace_bytes(1, c["n"], c["h_kv"], top_k)
         ws = torch.empty(nbytes, device=dev, dtype=torch.uint8)
-        ref, ref_st = _call(L, "ssa_select_block", q, k, qc, off, post, b, top_k, sorted_, ws)
-        got, got_st = _call(L, "ssa_select_block_noalloc", q, k, qc, off, post, b, top_k, sorted_)
+        ref, ref_st, ref_x = _call(L, "ssa_select_block", q, k, qc, off, post, b, top_k, sorted_, ws)
+        got, got_st, got_x = _call(L, "ssa_select_block_noalloc", q, k, qc, off, post, b, top_k,
+                                   sorted_)
         torch.cuda.synchronize()
         assert torch.equal(got, ref)
         assert torch.equal(got_st, ref_st)
+        assert torch.equal(got_x, ref_x)
         if not sorted_:
             assert int((ref_st[..., 0] > top_k).sum()) > 0, "the case should list heavy rows"
 
@@ -83,6 +86,6 @@ def test_noalloc_select_rejects_oversized_shape(dev):
     fake = ctypes.c_void_p(1 << 20)
     st = L.ssa_select_block_noalloc(fake, fake, _lib.DTYPE_BF16, 1, n, n, 0, 8, 2, 128, 0, 0, 0, 0,
                                     0, 0, fake, 16, fake, fake, 4096, 4, 512, _lib.MASK_CAUSAL,
-                                    None, 0, 0, 11.3, 0, None, fake, _lib.INDEX_I32, None, None)
+                                    None, 0, 0, 11.3, 0, None, fake, _lib.INDEX_I32, None, None, None)
     assert st == _lib.SSA_ERR_WORKSPACE
     assert "scratch" in (L.ssa_last_error() or b"").decode()
