@@ -188,11 +188,13 @@ size_t ssa_select_workspace_bytes(int64_t batch, int64_t n, int h_kv, int top_k)
 
 /* Where ssa_select places its regions inside a workspace of workspace_bytes
  * (no reference counterpart; for tests and for callers that size or share
- * workspaces).  layout[10] receives byte offsets of the counter block, the
+ * workspaces).  layout[11] receives byte offsets of the counter block, the
  * exact-pass row list, the screened-row entries, the per-row error bounds,
  * the candidate lists and their approximate scores, then the entries per
- * shard, the list entries per shard (0 = no screen), the shard count and the
- * counter block's size.  Nothing is launched or dereferenced. */
+ * shard, the list entries per shard (0 = no screen), the shard count, the
+ * counter block's size and the offset of the per-row candidate counts (one
+ * int32 per row, between the error bounds and the lists).  Nothing is
+ * launched or dereferenced. */
 int ssa_select_workspace_layout(int64_t batch, int64_t n, int h_kv, size_t workspace_bytes,
                                 int screen, int64_t* layout);
 

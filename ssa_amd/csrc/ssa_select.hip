@@ -58,6 +58,10 @@ struct SelParams {
   // hold exactly once (its lowest-key filler and the candidates below it);
   // 0 for a row without filler.  Stage (d) attends such prefixes densely.
   int32_t* prefix;
+  // Nullable [rows] (workspace): candidates per row, written by the light pass
+  // when the score order is wanted (select_sort_kernel reorders the index-order
+  // rows afterwards).
+  int32_t* cnt;
   int64_t n_q, q_pos0;   // query rows (q, q_codes, out, stats) and the position of row 0
   int64_t rows;          // batch * h_kv * n_q
   const int32_t* order;  // nullable [rows]: slot t of head bh runs query row order[bh * n_q + t]
@@ -434,6 +438,73 @@ __device__ __forceinline__ void select_row(const SelParams& p, const T* __restri
     p.prefix[row] = (nsel < p.k_eff && p.k_eff == p.top_k) ? stage[p.k_eff - 1] + 1 : 0;
 }
 
+// Score order through the index-order passes: a row's first m = min(C, k_eff)
+// slots hold its selected keys ascending; select_sort_kernel (one wave per
+// row) rescores them in the canonical order (rescore_row, lane l taking keys
+// l, l + 64, ...), sorts the composite keys (score desc, index asc -- unique,
+// so the order is total) with a bitonic network in the wave's LDS and writes
+// them back; the filler after them keeps its ascending order, as in
+// select_kernel.
+constexpr int kSortMax = 1024;  // m at most this (k_eff larger: select_kernel)
+
+template <typename T, int GMAX, int D>
+__global__ __launch_bounds__(64) void select_sort_kernel(SelParams p, const T* __restrict__ qg) {
+  __shared__ uint64_t keys[kSortMax];
+  const int lane = threadIdx.x;
+  const int64_t row = row_of_slot(p, blockIdx.x);
+  if (row < 0) return;
+  const int m = min(p.cnt[row], p.k_eff);
+  if (m <= 1) return;
+  const int64_t r = row % p.n_q;
+  const int64_t bh = row / p.n_q;
+  const int h = static_cast<int>(bh % p.h_kv);
+  const int64_t bb = bh / p.h_kv;
+  const T* q0 = qg + bb * p.q_sb + r * p.q_sn + static_cast<int64_t>(h * p.g) * p.q_sh;
+  const T* kbase = static_cast<const T*>(p.k) + bb * p.k_sb + static_cast<int64_t>(h) * p.k_sh;
+  const int64_t obase = ((bb * p.n_q + r) * p.h_kv + h) * p.top_k;
+  int32_t* o32 = static_cast<int32_t*>(p.out) + obase;
+  int64_t* o64 = static_cast<int64_t*>(p.out) + obase;
+  int np = 2;
+  while (np < m) np <<= 1;
+  for (int e = lane; e < np; e += 64) {
+    uint64_t key = 0ull;  // below every real key: padding sorts last
+    if (e < m) {
+      const int32_t j = p.out_i64 ? static_cast<int32_t>(o64[e]) : o32[e];
+      float acc[GMAX];
+      rescore_row<T, GMAX, D>(kbase + static_cast<int64_t>(j) * p.k_sn, q0, p.q_sh, p.g, p.d, acc);
+      float sc = acc[0] / p.score_div;
+#pragma unroll
+      for (int gg = 1; gg < GMAX; ++gg)
+        if (gg < p.g) sc = sc + acc[gg] / p.score_div;
+      sc = sc / static_cast<float>(p.g);
+      key = composite_key(sc, static_cast<uint32_t>(j));
+    }
+    keys[e] = key;
+  }
+  __syncthreads();
+  // bitonic network over np keys by the one wave, descending overall
+  for (int size = 2; size <= np; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int t = lane; t < (np >> 1); t += 64) {
+        const int i = 2 * stride * (t / stride) + (t % stride);
+        const int jx = i + stride;
+        const uint64_t a = keys[i], b = keys[jx];
+        const bool desc = (i & size) == 0;
+        if (desc ? (a < b) : (a > b)) {
+          keys[i] = b;
+          keys[jx] = a;
+        }
+      }
+      __syncthreads();
+    }
+  }
+  for (int e = lane; e < m; e += 64) {
+    const int32_t j = static_cast<int32_t>(key_index(keys[e]));
+    if (p.out_i64) o64[e] = j;
+    else o32[e] = j;
+  }
+}
+
 template <typename T, int GMAX, int D>
 __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams p, const T* __restrict__ qg) {
   const int64_t row = row_of_slot(p, blockIdx.x);
@@ -448,6 +519,8 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams p, const 
 //          ctr + 16 + 4 s: [0] screened rows, [2..3] int64 list entries used
 //   exact  int32 [rows]: rows for select_heavy_kernel
 //   scr    int32 [kShards][shard_rows][3]: (row, list offset, candidates)
+//   emax   float [kShards][shard_rows]: the screen's error bound per entry
+//   cnt    int32 [rows]: candidates per row (score order: for the sort pass)
 //   cand   int32 [kShards][cap]: screened rows' candidates, ascending
 //   approx float [kShards][cap]: their approximate scores
 constexpr int kShards = 64;
@@ -462,6 +535,7 @@ struct SelWs {
   int32_t* cand;
   float* approx;
   float* emax;         // [kShards][shard_rows]: the screen's error bound per row (inf: exact pass)
+  int32_t* cnt;        // [rows]
   int64_t shard_rows;  // scr entries per shard
   int64_t cap;         // list entries per shard (0: no screen)
 };
@@ -655,6 +729,7 @@ __global__ __launch_bounds__(64) void select_light_kernel(SelParams p, int64_t r
     p.stats[(bh * p.n_q + r) * 2 + 0] = C;
     p.stats[(bh * p.n_q + r) * 2 + 1] = raw;
   }
+  if (p.cnt && lane == 0) p.cnt[row] = C;
   __builtin_amdgcn_wave_barrier();
 
   if (C > p.k_eff) {
@@ -1179,7 +1254,7 @@ size_t light_smem(int64_t n) { return sizeof(uint32_t) * static_cast<size_t>(lig
 int64_t shard_rows_for(int64_t rows) { return ceil_div(rows, kShards); }
 
 size_t sel_ws_fixed(int64_t rows) {
-  return kSelCtrBytes + align_up(sizeof(int32_t) * static_cast<size_t>(rows), 256) +
+  return kSelCtrBytes + 2 * align_up(sizeof(int32_t) * static_cast<size_t>(rows), 256) +
          align_up(3 * sizeof(int32_t) * static_cast<size_t>(kShards * shard_rows_for(rows)), 256) +
          align_up(sizeof(float) * static_cast<size_t>(kShards * shard_rows_for(rows)), 256);
 }
@@ -1196,6 +1271,8 @@ SelWs carve_sel_ws(void* ws, size_t bytes, int64_t rows, bool screen) {
   c += align_up(3 * sizeof(int32_t) * static_cast<size_t>(kShards * w.shard_rows), 256);
   w.emax = reinterpret_cast<float*>(c);
   c += align_up(sizeof(float) * static_cast<size_t>(kShards * w.shard_rows), 256);
+  w.cnt = reinterpret_cast<int32_t*>(c);
+  c += align_up(sizeof(int32_t) * static_cast<size_t>(rows), 256);
   const size_t fixed = sel_ws_fixed(rows);
   // per shard: cap candidates and cap scores
   int64_t cap = (screen && bytes > fixed + 256) ? static_cast<int64_t>((bytes - fixed - 256) / (8 * kShards)) : 0;
@@ -1249,34 +1326,42 @@ int launch_select(const SelParams& p, int64_t rows, size_t smem, void* ws, size_
   auto kern = select_kernel<T, GMAX, D>;
   if (int s = reserve_lds(reinterpret_cast<const void*>(kern), smem, "select")) return s;
   const T* qg = static_cast<const T*>(p.q);
-  if (ws == nullptr || p.sorted || light_smem(p.n) > 64 * 1024) {
-    kern<<<dim3(static_cast<unsigned>(rows)), kSelThreads, smem, st>>>(p, qg);
-    return check_launch("select_kernel");
-  }
   constexpr bool kScreenable = sizeof(T) == 2 && (D == 64 || D == 128);
   // 32-bit buffer offsets of the screen's K gathers
   const bool screen = kScreenable && p.n < (int64_t(1) << 24) && 2 * p.k_sn < (int64_t(1) << 24) &&
                       (p.n - 1) * p.k_sn * 2 + 2 * p.d < (int64_t(1) << 31);
+  if (ws == nullptr || (p.sorted && p.k_eff > kSortMax) || light_smem(p.n) > 64 * 1024) {
+    kern<<<dim3(static_cast<unsigned>(rows)), kSelThreads, smem, st>>>(p, qg);
+    return check_launch("select_kernel");
+  }
   const SelWs w = carve_sel_ws(ws, ws_bytes, rows, screen);
+  // score order: the index-order passes, then the sort pass over their rows
+  const bool sort_after = p.sorted != 0;
+  SelParams pi = p;
+  pi.sorted = 0;
+  pi.cnt = sort_after ? w.cnt : nullptr;
   zero_ctr_kernel<<<1, 256, 0, st>>>(w.ctr);
   if (int s = check_launch("zero_ctr_kernel")) return s;
-  select_light_kernel<<<dim3(static_cast<unsigned>(rows)), 64, light_smem(p.n), st>>>(p, rows, w);
+  select_light_kernel<<<dim3(static_cast<unsigned>(rows)), 64, light_smem(p.n), st>>>(pi, rows, w);
   if (int s = check_launch("select_light_kernel")) return s;
   if constexpr (kScreenable) {
     if (w.cap > 0) {
       constexpr int DS = (D == 64) ? 64 : 128;
       select_screen_kernel<DS, GMAX><<<dim3(static_cast<unsigned>(shard_grid<DS, GMAX, 0>())), 64 * kScrWaves, 0,
-                                      st>>>(p, w);
+                                      st>>>(pi, w);
       if (int s = check_launch("select_screen_kernel")) return s;
       select_pick_kernel<DS, GMAX><<<dim3(static_cast<unsigned>(shard_grid<DS, GMAX, 1>())), 64 * kScrWaves, 0,
-                                    st>>>(p, w);
+                                    st>>>(pi, w);
       if (int s = check_launch("select_pick_kernel")) return s;
     }
   }
   auto hk = select_heavy_kernel<T, GMAX, D>;
   if (int s = reserve_lds(reinterpret_cast<const void*>(hk), smem, "select")) return s;
-  hk<<<dim3(static_cast<unsigned>(persistent_grid(rows, 8))), kSelThreads, smem, st>>>(p, qg, w);
-  return check_launch("select_heavy_kernel");
+  hk<<<dim3(static_cast<unsigned>(persistent_grid(rows, 8))), kSelThreads, smem, st>>>(pi, qg, w);
+  if (int s = check_launch("select_heavy_kernel")) return s;
+  if (!sort_after) return SSA_OK;
+  select_sort_kernel<T, GMAX, D><<<dim3(static_cast<unsigned>(rows)), 64, 0, st>>>(pi, qg);
+  return check_launch("select_sort_kernel");
 }
 
 template <typename T, int GMAX>
@@ -1323,6 +1408,7 @@ extern "C" int ssa_select_workspace_layout(int64_t batch, int64_t n, int h_kv, s
   layout[7] = w.cap;
   layout[8] = kShards;
   layout[9] = static_cast<int64_t>(kSelCtrBytes);
+  layout[10] = off(w.cnt);
   return SSA_OK;
 }
 

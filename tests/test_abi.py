@@ -301,7 +301,8 @@ def test_select_workspace_regions_do_not_overlap(L, batch, n, h_kv, top_k):
     large as the kernels index them, and inside the workspace: the counter
     block holds 16 + 4 ints per shard, the exact list one int per row, the
     screened-row entries 3 ints and the error bounds one float per shard slot,
-    the candidate lists and scores cap entries per shard.  Swept over shapes and
+    the candidate counts one int per row, the candidate lists and scores cap
+    entries per shard.  Swept over shapes and
     workspace sizes from the minimum to past the recommended size (a too-small
     counter block once let a garbage counter drive an out-of-bounds write)."""
     rows = batch * n * h_kv
@@ -310,23 +311,24 @@ def test_select_workspace_regions_do_not_overlap(L, batch, n, h_kv, top_k):
     assert hi >= lo > 0
     for bytes_ in sorted({lo, lo + 255, (lo + hi) // 2, hi, 2 * hi + 77}):
         for screen in (0, 1):
-            lay = (ctypes.c_int64 * 10)()
+            lay = (ctypes.c_int64 * 11)()
             assert L.ssa_select_workspace_layout(batch, n, h_kv, bytes_, screen, lay) == _lib.SSA_OK
-            ctr, exact, scr, emax, cand, approx, shard_rows, cap, shards, ctr_bytes = list(lay)
+            ctr, exact, scr, emax, cand, approx, shard_rows, cap, shards, ctr_bytes, cnt = list(lay)
             assert shard_rows * shards >= rows
             assert 4 * (16 + 4 * shards) <= ctr_bytes
             ends = [(ctr, ctr + ctr_bytes), (exact, exact + 4 * rows),
                     (scr, scr + 12 * shards * shard_rows), (emax, emax + 4 * shards * shard_rows),
-                    (cand, cand + 4 * shards * cap), (approx, approx + 4 * shards * cap)]
+                    (cnt, cnt + 4 * rows), (cand, cand + 4 * shards * cap),
+                    (approx, approx + 4 * shards * cap)]
             assert ctr == 0
             for (s0, e0), (s1, _) in zip(ends, ends[1:]):
                 assert s0 <= e0 <= s1, (ends, bytes_)
             assert ends[-1][1] <= bytes_
-            assert all(o % 256 == 0 for o in (exact, scr, emax, cand, approx))
+            assert all(o % 256 == 0 for o in (exact, scr, emax, cnt, cand, approx))
             assert cap % 32 == 0 and cap >= 0
             if not screen or bytes_ == lo:
                 assert cap == 0
-    assert L.ssa_select_workspace_layout(batch, n, h_kv, lo - 1, 1, (ctypes.c_int64 * 10)()) \
+    assert L.ssa_select_workspace_layout(batch, n, h_kv, lo - 1, 1, (ctypes.c_int64 * 11)()) \
         == _lib.SSA_ERR_WORKSPACE
 
 
