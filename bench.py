@@ -291,8 +291,10 @@ def stats_sums(q, k, router):
     qc, kc = kernels.route_codes(q, k, router.W_qr.weight, router.W_kr.weight, router.codebook,
                                  router.codes_per_query, router.codes_per_key, router.temperature)
     off, post = kernels.build_index(kc, router.num_codebook)
+    pfx = torch.empty(qc.shape[:3], device=q.device, dtype=torch.int32)
     idx, st = kernels.select(q, k, qc, off, post, router.codes_per_key, router.top_k,
-                             with_stats=True, sorted=False)
+                             with_stats=True, sorted=False, row_prefix=pfx)
+    prefix_slots = int(pfx.to(torch.int64).sum())
     st = st.to(torch.int64)
     C = int(st[..., 0].sum())
     R = int(st[..., 1].sum())
@@ -305,7 +307,8 @@ def stats_sums(q, k, router):
     seen = torch.zeros(B * h_kv * n, dtype=torch.bool, device=idx.device)
     seen[(idx + base).reshape(-1)] = True
     distinct = int(seen.sum())
-    return R, C, int(heavy.sum()), C_r, st[..., 0].numel(), distinct, (qc, kc, off, post, idx)
+    return (R, C, int(heavy.sum()), C_r, st[..., 0].numel(), distinct, (qc, kc, off, post, idx),
+            prefix_slots)
 
 
 def time_backward(cfg, q, k, v, inter, reps=3):
@@ -552,10 +555,11 @@ def cpu_oracle(cfg, q, k, v, router, inter, budget_s):
     }
 
 
-def measured_traffic(workload, kernel="sparse_attention_mfma_kernel"):
-    """HBM bytes per launch of `kernel` at `workload`, from the committed rocprofv3
-    FETCH_SIZE / WRITE_SIZE summary (profiles/<kernel>_<workload>_traffic.md, line
-    ``traffic_bytes <kernel> <workload> <bytes>``); None when no such profile exists."""
+def measured_traffic(workload, kernel="stage_d"):
+    """Bytes between L2 and the fabric per stage-(d) call (its two kernels) at
+    `workload`, from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
+    (profiles/sparse_attention_<workload>_traffic.md, line ``traffic_bytes
+    stage_d <workload> <bytes>``); None when no such profile exists."""
     path = os.path.join(ROOT, "profiles", f"sparse_attention_{workload}_traffic.md")
     try:
         with open(path) as f:
@@ -626,7 +630,7 @@ def main():
         print(f"workload ready: {args.config} n={cfg['n']}", file=sys.stderr, flush=True)
         wall, st = time_gpu(cfg, q, k, v, router, args.steps, args.warmup)
     ms_step = 1000.0 * wall / args.steps
-    R, C, heavy_rows, C_r, nrows, distinct, inter = stats_sums(q, k, router)
+    R, C, heavy_rows, C_r, nrows, distinct, inter, prefix_slots = stats_sums(q, k, router)
     alg = algorithmic(cfg, cfg["n"], (R, C, C_r, heavy_rows), distinct)
     tokens = cfg["B"] * cfg["n"]
     t = {key: st[key] / 1000.0 for key in "abcd"}
@@ -652,6 +656,7 @@ def main():
         "d": {"ms": st["d"], "gb_compulsory": alg["d_bytes_compulsory"] / 1e9,
               "frac_hbm_compulsory": d_comp_gbs / HBM_PEAK_GBS,
               "distinct_kv_rows": distinct,
+              "slots": nrows * cfg["k"], "slots_in_dense_prefixes": prefix_slots,
               "gb_logical_gather": alg["d_bytes_logical"] / 1e9,
               "gbs_logical_gather": alg["d_bytes_logical"] / t["d"] / 1e9,
               "tflops": alg["d_flops"] / t["d"] / 1e12},
@@ -686,7 +691,8 @@ def main():
         "dtype": cfg["dtype"],
         "data": data,
         "config": config,
-        "roofline": {"bound": "hbm", "kernel": "sparse_attention_mfma_kernel (stage d)",
+        "roofline": {"bound": "hbm",
+                     "kernel": "stage d: prefix_attention_kernel + sparse_attention_mfma_kernel",
                      "achieved": d_comp_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": d_comp_gbs / HBM_PEAK_GBS, "traffic": traffic,
                      "traffic_counter": "FETCH_SIZE + WRITE_SIZE (bytes between L2 and the fabric; "
