@@ -321,17 +321,19 @@ def time_backward(cfg, q, k, v, inter, reps=3):
 
     qc, kc, off, post, _ = inter
     order = kernels.query_order(qc, cfg["n_c"])
+    pfx = torch.empty(order.shape, device=q.device, dtype=torch.int32)
     idx = kernels.select(q, k, qc, off, post, cfg["b"], cfg["k"], sorted=False,
-                         index_dtype=torch.int32, row_order=order)
+                         index_dtype=torch.int32, row_order=order, row_prefix=pfx)
     out32 = torch.empty(q.shape, device=q.device, dtype=torch.float32)
-    kernels.sparse_attention(q, k, v, idx, None, True, out=out32, row_order=order)
+    kernels.sparse_attention(q, k, v, idx, None, True, out=out32, row_order=order, row_prefix=pfx)
     gen = torch.Generator(device=q.device).manual_seed(7)
     dout = torch.randn(q.shape, generator=gen, device=q.device).to(q.dtype)
     ts = []
     for _ in range(reps):
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
-        kernels.sparse_attention_backward(q, k, v, idx, out32, dout, None, True, row_order=order)
+        kernels.sparse_attention_backward(q, k, v, idx, out32, dout, None, True, row_order=order,
+                                          row_prefix=pfx)
         e1.record()
         torch.cuda.synchronize()
         ts.append(e0.elapsed_time(e1))

@@ -400,7 +400,18 @@ int ssa_sparse_attention_backward(
     int top_k, int64_t idx_sb, int64_t idx_sn, int64_t idx_sh, float scale_div, int causal,
     const int32_t* row_order, const void* out, int out_dtype, int64_t o_sb, int64_t o_sn,
     int64_t o_sh, const void* dout, int dout_dtype, int64_t do_sb, int64_t do_sn, int64_t do_sh,
-    float* dq, float* dk, float* dv, int32_t* error_flag, void* stream);
+    float* dq, float* dk, float* dv, int32_t* error_flag, const int32_t* row_prefix, void* workspace,
+    size_t workspace_bytes, void* stream);
+
+/* Bytes of ssa_sparse_attention_backward's optional workspace (4 floats per
+ * (row, query head)); 0 where the dense-prefix pass does not run (fp32 q/k/v
+ * or dO, d other than 64 or 128, g > 8).  With row_prefix (X per row, as
+ * ssa_select writes it) and this workspace, the keys [0, X) of each row are
+ * differentiated by blocks of 8 neighbouring rows, whose dK/dV sums meet in
+ * LDS before one fp32 atomic per (key, dim) and block.  No reference
+ * counterpart. */
+size_t ssa_sparse_attention_backward_workspace_bytes(int dtype, int dout_dtype, int64_t batch, int64_t n,
+                                                     int h_q, int h_kv, int d);
 
 #ifdef __cplusplus
 }

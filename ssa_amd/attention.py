@@ -29,18 +29,21 @@ class _SparseAttention(torch.autograd.Function):
                                  row_order=row_order, row_prefix=row_prefix)
         ctx.scale, ctx.causal = scale, causal
         ctx.has_order = row_order is not None
-        saved = [q, k, v, indices, out32] + ([row_order] if row_order is not None else [])
+        ctx.has_prefix = row_prefix is not None
+        saved = ([q, k, v, indices, out32] + ([row_order] if row_order is not None else [])
+                 + ([row_prefix] if row_prefix is not None else []))
         ctx.save_for_backward(*saved)
         return out32 if q.dtype == torch.float32 else out32.to(q.dtype)
 
     @staticmethod
     def backward(ctx, dout):
         q, k, v, indices, out, *rest = ctx.saved_tensors
-        order = rest[0] if ctx.has_order else None
+        order = rest.pop(0) if ctx.has_order else None
+        prefix = rest.pop(0) if ctx.has_prefix else None
         if dout.stride(-1) != 1:
             dout = dout.contiguous()
         dq, dk, dv = kernels.sparse_attention_backward(q, k, v, indices, out, dout, ctx.scale,
-                                                       ctx.causal, row_order=order)
+                                                       ctx.causal, row_order=order, row_prefix=prefix)
         return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), None, None, None, None, None, None
 
 

@@ -49,6 +49,13 @@ struct BwdParams {
   int32_t* err;
   int64_t rows;
   const int32_t* order;  // nullable [B*h_kv][n]
+  // Dense key prefixes (nullable; matrix-core path): X per row [B*h_kv][n] as
+  // the selection writes it, and per (row, head) the softmax reference, the
+  // reciprocal sum and D = dO . o that the row kernel found ([rows][g][4]).
+  // The row kernel then skips indices below X; prefix_attention_bwd_kernel
+  // handles them for blocks of neighbouring rows.
+  const int32_t* pfx;
+  float* pstats;
 };
 
 __device__ __forceinline__ float ld_any(const void* p, int64_t off, int is_bf16) {
@@ -368,6 +375,16 @@ __global__ __launch_bounds__(64 * kBwMfWaves, 2) void sparse_attention_bwd_mfma_
   l_tot += __shfl_xor(l_tot, 32);
   const float inv_l = (l_tot > 0.0f && col_ok) ? 1.0f / l_tot : 0.0f;  // 0: no slot, or an unused column
   const float mref = (m_run == -INFINITY) ? 0.0f : m_run;
+  // the prefix keys [0, X) go to prefix_attention_bwd_kernel, which needs the
+  // row's softmax reference, 1/sum and D
+  const int xpre = p.pfx ? p.pfx[bh * p.n + i] : 0;
+  if (p.pfx && q4 == 0 && col_ok) {
+    float* ps = p.pstats + ((bh * p.n + i) * g + c16) * 4;
+    ps[0] = mref;
+    ps[1] = inv_l;
+    ps[2] = dcol;
+  }
+  auto chunk_ok2 = [&](int j) { return j >= xpre && chunk_ok(j); };
 
   // ---- pass 2
   const bool hi_row = c16 < g;
@@ -403,10 +420,10 @@ __global__ __launch_bounds__(64 * kBwMfWaves, 2) void sparse_attention_bwd_mfma_
     return *reinterpret_cast<const bf16x8_t*>(&hd_lds[wave][which][16 * dt + c16][0]);
   };
   int jc = nchunks > 0 ? load_idx(0) : -1;
-  uint64_t okn = __ballot(chunk_ok(jc));
+  uint64_t okn = __ballot(chunk_ok2(jc));
   if (nchunks > 0) {
-    row_issue<D>(krs, kl, chunk_ok(jc) ? jc : -1, lane, ksn2, seg16);
-    row_issue<D>(vrs, vl, chunk_ok(jc) ? jc : -1, lane, vsn2, seg16);
+    row_issue<D>(krs, kl, chunk_ok2(jc) ? jc : -1, lane, ksn2, seg16);
+    row_issue<D>(vrs, vl, chunk_ok2(jc) ? jc : -1, lane, vsn2, seg16);
   }
   int jn = nchunks > 1 ? load_idx(1) : -1;
   for (int ch = 0; ch < nchunks; ++ch) {
@@ -420,9 +437,9 @@ __global__ __launch_bounds__(64 * kBwMfWaves, 2) void sparse_attention_bwd_mfma_
     const uint64_t okb = okn;
     const int jcur = jc;
     if (ch + 1 < nchunks) {
-      okn = __ballot(chunk_ok(jn));
-      row_issue<D>(krs, kl, chunk_ok(jn) ? jn : -1, lane, ksn2, seg16);
-      row_issue<D>(vrs, vl, chunk_ok(jn) ? jn : -1, lane, vsn2, seg16);
+      okn = __ballot(chunk_ok2(jn));
+      row_issue<D>(krs, kl, chunk_ok2(jn) ? jn : -1, lane, ksn2, seg16);
+      row_issue<D>(vrs, vl, chunk_ok2(jn) ? jn : -1, lane, vsn2, seg16);
       jc = jn;
       jn = ch + 2 < nchunks ? load_idx(ch + 2) : -1;
     }
@@ -500,6 +517,237 @@ __global__ __launch_bounds__(64 * kBwMfWaves, 2) void sparse_attention_bwd_mfma_
                     dqacc[t][3] * p.inv_scale);
 }
 
+// ---------------------------------------------------------------------------
+// Dense key prefixes (after the matrix-core row kernel, which skipped them):
+// one block per kPbWaves neighbouring rows of one (batch, kv head), wave w
+// taking row r0 + w.  The keys [0, max X) stream through LDS in 32-key chunks
+// (loads shared by the block); per chunk each wave forms its row's p and ds
+// with the row kernel's MFMA layout and the stats the row kernel left
+// (softmax reference, 1/sum, D), masked to keys below its X (and its position
+// when causal), and adds dQ^T += K^T dS^T in registers.  P and dS of all the
+// block's query vectors then meet in LDS as [key][query vector], and
+// dV = P^T dO, dK = dS^T Q come from MFMAs that sum over the block's query
+// vectors (A = P^T or dS^T split into bf16 hi and lo, B = dO or Q as
+// [dim][query vector] in LDS): one fp32 atomic per (key, dim) and block instead
+// of one per row.
+constexpr int kPbWaves = 8;
+
+template <int D>
+__global__ __launch_bounds__(64 * kPbWaves, 1) void prefix_attention_bwd_kernel(BwdParams p) {
+  using S = MfShape<D>;
+  constexpr int KB = S::KB, NT = S::NT;
+  constexpr int QV = 8 * kPbWaves;      // query vectors per block at most (g <= 8)
+  constexpr int LPW = (S::NLD + kPbWaves - 1) / kPbWaves;  // chunk loads per wave and tensor
+  __shared__ __align__(16) unsigned char kv[2][2][kMfChunk * S::ROW];  // [buffer][K, V]
+  __shared__ __align__(16) float pall[2][kMfChunk][QV];                // P, dS as [key][qv]
+  __shared__ __align__(16) uint16_t qall[2][D][QV];                    // Q, dO as [dim][qv] (bf16)
+  __shared__ int s_xmax;
+
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int q4 = lane >> 4, c16 = lane & 15;
+  const int g = p.g;
+  const int64_t tiles = ceil_div(p.n, kPbWaves);
+  const int64_t nblk = (p.rows / p.n) * tiles;
+  const int64_t blk = xcd_block(blockIdx.x, xcd_per(nblk));
+  if (blk >= nblk) return;
+  const int64_t bh = blk / tiles;
+  const int64_t i = (blk - bh * tiles) * kPbWaves + wave;  // this wave's row
+  const bool row_ok = i < p.n;
+  const int h = static_cast<int>(bh % p.h_kv);
+  const int64_t bb = bh / p.h_kv;
+  const bool col_ok = c16 < g;
+  const int xcap = static_cast<int>(min(static_cast<int64_t>(p.top_k), p.n));
+  const int xrow = row_ok ? min(max(p.pfx[bh * p.n + i], 0), xcap) : 0;
+
+  // the block's Q and dO as [dim][qv], zero for unused query vectors (whose P
+  // and dS columns stay zero too: the reductions run over whole 32-column blocks)
+  for (int e = tid; e < 2 * D * QV; e += 64 * kPbWaves) reinterpret_cast<uint16_t*>(qall)[e] = 0;
+  for (int e = tid; e < 2 * kMfChunk * QV; e += 64 * kPbWaves) reinterpret_cast<float*>(pall)[e] = 0.0f;
+  if (tid == 0) s_xmax = 0;
+  __syncthreads();
+  if (lane == 0) atomicMax(&s_xmax, xrow);
+  const int hq = h * g + (col_ok ? c16 : 0);
+  const uint16_t* qh = static_cast<const uint16_t*>(p.q) + bb * p.q_sb + (row_ok ? i : 0) * p.q_sn +
+                       static_cast<int64_t>(hq) * p.q_sh;
+  const uint16_t* dh = static_cast<const uint16_t*>(p.dout) + bb * p.do_sb + (row_ok ? i : 0) * p.do_sn +
+                       static_cast<int64_t>(hq) * p.do_sh;
+  bf16x8_t qf[KB], df[KB];
+  const bool have = row_ok && col_ok && xrow > 0;
+#pragma unroll
+  for (int kb = 0; kb < KB; ++kb) {
+    qf[kb] = have ? *reinterpret_cast<const bf16x8_t*>(qh + kb * 32 + q4 * 8) : bf16x8_t{};
+    df[kb] = have ? *reinterpret_cast<const bf16x8_t*>(dh + kb * 32 + q4 * 8) : bf16x8_t{};
+    if (have) {
+      const uint4 qu = __builtin_bit_cast(uint4, qf[kb]), du = __builtin_bit_cast(uint4, df[kb]);
+      const uint32_t qw[4] = {qu.x, qu.y, qu.z, qu.w}, dw[4] = {du.x, du.y, du.z, du.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int dim = kb * 32 + q4 * 8 + e;
+        qall[0][dim][wave * g + c16] = static_cast<uint16_t>((e & 1) ? (qw[e >> 1] >> 16) : (qw[e >> 1] & 0xFFFFu));
+        qall[1][dim][wave * g + c16] = static_cast<uint16_t>((e & 1) ? (dw[e >> 1] >> 16) : (dw[e >> 1] & 0xFFFFu));
+      }
+    }
+  }
+  float mref = 0.0f, inv_l = 0.0f, dcol = 0.0f;
+  if (have) {
+    const float* ps = p.pstats + ((bh * p.n + i) * g + c16) * 4;
+    mref = ps[0];
+    inv_l = ps[1];
+    dcol = ps[2];
+  }
+  __syncthreads();
+  const int xmax = s_xmax;
+  if (xmax == 0) return;
+
+  const uint16_t* kbase = static_cast<const uint16_t*>(p.k) + bb * p.k_sb + static_cast<int64_t>(h) * p.k_sh;
+  const uint16_t* vbase = static_cast<const uint16_t*>(p.v) + bb * p.v_sb + static_cast<int64_t>(h) * p.v_sh;
+  const uint32_t ksn2 = 2u * static_cast<uint32_t>(p.k_sn), vsn2 = 2u * static_cast<uint32_t>(p.v_sn);
+  const int kbytes = static_cast<int>((p.n - 1) * p.k_sn * 2 + 2 * D);
+  const int vbytes = static_cast<int>((p.n - 1) * p.v_sn * 2 + 2 * D);
+  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(kbase), 0, kbytes, kBufferWord3);
+  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(vbase), 0, vbytes, kBufferWord3);
+  uint32_t seg16[S::SWZ_PERIOD];
+  row_seg16<D>(lane, seg16);
+  const int kswz = mf_swz<D>(c16);
+  // this wave's loads of chunk ch: loads r = wave + kPbWaves * t (< NLD) of K and V
+  auto issue = [&](int ch) {
+#pragma unroll
+    for (int t = 0; t < LPW; ++t) {
+      const int r = wave + kPbWaves * t;
+      if (r < S::NLD) {
+        const int j = ch * kMfChunk + S::KPI * r + lane / S::SEGS;
+        const uint32_t sg = seg16[r % S::SWZ_PERIOD];
+        const uint32_t ko = j < xmax ? __umul24(static_cast<uint32_t>(j), ksn2) + sg : kOobOffset;
+        const uint32_t vo = j < xmax ? __umul24(static_cast<uint32_t>(j), vsn2) + sg : kOobOffset;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_void_ptr)(kv[ch & 1][0] + r * 1024), 16, static_cast<int>(ko), 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_void_ptr)(kv[ch & 1][1] + r * 1024), 16, static_cast<int>(vo), 0, 0, 0);
+      }
+    }
+  };
+  const int ilim = p.causal ? static_cast<int>(min(i, static_cast<int64_t>(0x7FFFFFFF))) : 0x7FFFFFFF;
+  const bool hi_row = c16 < g;
+  const bool lo_row = c16 >= 8 && c16 < 8 + g;
+  floatx4_t dqacc[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) dqacc[t] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+  float* dkb = p.dk + (bb * p.n * p.h_kv + h) * p.d;
+  float* dvb = p.dv + (bb * p.n * p.h_kv + h) * p.d;
+  const int64_t krow = static_cast<int64_t>(p.h_kv) * p.d;
+  const int nqv = kPbWaves * g;
+  const int kblocks = (nqv + 31) / 32;
+  const int nch = (xmax + kMfChunk - 1) / kMfChunk;
+  issue(0);
+  for (int u = 0; u < nch; ++u) {
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);
+    // chunk u is in LDS for every wave; every wave is done with chunk u - 1 and pall
+    __syncthreads();
+    if (u + 1 < nch) issue(u + 1);
+    const unsigned char* kl = kv[u & 1][0];
+    const unsigned char* vl = kv[u & 1][1];
+    bf16x8_t kf[2][KB], vf[2][KB], kt[NT];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        kf[t][kb] = *(lds_bf16x8_ptr)(kl + (16 * t + c16) * S::ROW + (((kb * 4 + q4) ^ kswz) << 4));
+        vf[t][kb] = *(lds_bf16x8_ptr)(vl + (16 * t + c16) * S::ROW + (((kb * 4 + q4) ^ kswz) << 4));
+      }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) kt[t] = rows_transposed<D>(kl, t, q4, c16);
+    float pr[8], ds[8];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      floatx4_t sv = {0.f, 0.f, 0.f, 0.f}, dv = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        sv = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[t][kb], qf[kb], sv, 0, 0, 0);
+        dv = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[t][kb], df[kb], dv, 0, 0, 0);
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int x = 4 * t + e;
+        const int j = u * kMfChunk + 16 * t + 4 * q4 + e;
+        const bool ok = have && j < xrow && j <= ilim;
+        pr[x] = ok ? exp2f(sv[e] * p.qk_scale_log2 - mref) * inv_l : 0.0f;
+        ds[x] = pr[x] * (dv[e] - dcol);
+      }
+    }
+    // dQ^T += K^T dS^T (B: rows c16 < g dS_hi of head c16, rows 8 + r dS_lo of head r)
+    uint32_t db[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const uint32_t hi = pack_bf16x2(ds[2 * w], ds[2 * w + 1]);
+      const uint32_t lo = pack_bf16x2(ds[2 * w] - __uint_as_float(hi << 16), ds[2 * w + 1] - __uint_as_float(hi & 0xFFFF0000u));
+      const uint32_t lo_in = dpp_from_minus8(lo);
+      db[w] = hi_row ? hi : (lo_row ? lo_in : 0u);
+    }
+    const bf16x8_t dsb = __builtin_bit_cast(bf16x8_t, make_uint4(db[0], db[1], db[2], db[3]));
+#pragma unroll
+    for (int t = 0; t < NT; ++t) dqacc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kt[t], dsb, dqacc[t], 0, 0, 0);
+    // P and dS of this row's heads into [key][qv]
+    if (col_ok) {
+#pragma unroll
+      for (int x = 0; x < 8; ++x) {
+        const int key = 16 * (x >> 2) + 4 * q4 + (x & 3);
+        pall[0][key][wave * g + c16] = pr[x];
+        pall[1][key][wave * g + c16] = ds[x];
+      }
+    }
+    __syncthreads();
+    // dV = P^T dO (pass 0) and dK = dS^T Q (pass 1), summed over the block's
+    // query vectors: item (pass, dt) by wave item % kPbWaves
+    for (int item = wave; item < 2 * NT; item += kPbWaves) {
+      const int pass = item / NT, dt = item - pass * NT;
+      const int which = pass == 0 ? 1 : 0;  // B: dO for dV, Q for dK
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        floatx4_t c = {0.f, 0.f, 0.f, 0.f};
+        for (int kq = 0; kq < kblocks; ++kq) {
+          const float* src = &pall[pass][16 * t + c16][32 * kq + 8 * q4];
+          const float4 a = *reinterpret_cast<const float4*>(src);
+          const float4 b = *reinterpret_cast<const float4*>(src + 4);
+          const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+          uint32_t hw[4], lw[4];
+#pragma unroll
+          for (int x = 0; x < 4; ++x) {
+            hw[x] = pack_bf16x2(v[2 * x], v[2 * x + 1]);
+            lw[x] = pack_bf16x2(v[2 * x] - __uint_as_float(hw[x] << 16), v[2 * x + 1] - __uint_as_float(hw[x] & 0xFFFF0000u));
+          }
+          const bf16x8_t ah = __builtin_bit_cast(bf16x8_t, make_uint4(hw[0], hw[1], hw[2], hw[3]));
+          const bf16x8_t al = __builtin_bit_cast(bf16x8_t, make_uint4(lw[0], lw[1], lw[2], lw[3]));
+          const bf16x8_t bop = *reinterpret_cast<const bf16x8_t*>(&qall[which][16 * dt + c16][32 * kq + 8 * q4]);
+          c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bop, c, 0, 0, 0);
+          c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bop, c, 0, 0, 0);
+        }
+        float* dst = pass == 0 ? dvb : dkb;
+        const float mul = pass == 0 ? 1.0f : p.inv_scale;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int j = u * kMfChunk + 16 * t + 4 * q4 + e;
+          if (j < xmax) unsafeAtomicAdd(dst + j * krow + 16 * dt + c16, c[e] * mul);
+        }
+      }
+    }
+  }
+  // dQ of the prefix: hi row + lo row, / scale, added to the row kernel's part
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) dqacc[t][e] += dpp_from_plus8(dqacc[t][e]);
+  if (!have || !hi_row) return;
+  float* dqb = p.dq + ((bb * p.n + i) * p.h_q + h * g + c16) * p.d + 4 * q4;
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    float4 cur = *reinterpret_cast<float4*>(dqb + 16 * t);
+    cur.x += dqacc[t][0] * p.inv_scale;
+    cur.y += dqacc[t][1] * p.inv_scale;
+    cur.z += dqacc[t][2] * p.inv_scale;
+    cur.w += dqacc[t][3] * p.inv_scale;
+    *reinterpret_cast<float4*>(dqb + 16 * t) = cur;
+  }
+}
+
 template <typename T, int GMAX>
 int launch_bwd_g(const BwdParams& p, hipStream_t st) {
   const dim3 grid(static_cast<unsigned>(ceil_div(p.rows, kBwdWaves)));
@@ -536,7 +784,14 @@ int launch_bwd(const BwdParams& p, hipStream_t st) {
         sparse_attention_bwd_mfma_kernel<64><<<grid, 64 * kBwMfWaves, 0, st>>>(p);
       else
         sparse_attention_bwd_mfma_kernel<128><<<grid, 64 * kBwMfWaves, 0, st>>>(p);
-      return check_launch("sparse_attention_bwd_mfma_kernel");
+      if (int s = check_launch("sparse_attention_bwd_mfma_kernel")) return s;
+      if (!p.pfx) return SSA_OK;
+      const dim3 pgrid(static_cast<unsigned>(kXcds * xcd_per((p.rows / p.n) * ceil_div(p.n, kPbWaves))));
+      if (p.d == 64)
+        prefix_attention_bwd_kernel<64><<<pgrid, 64 * kPbWaves, 0, st>>>(p);
+      else
+        prefix_attention_bwd_kernel<128><<<pgrid, 64 * kPbWaves, 0, st>>>(p);
+      return check_launch("prefix_attention_bwd_kernel");
     }
   }
   if (p.g <= 4) return launch_bwd_g<T, 4>(p, st);
@@ -549,6 +804,23 @@ int launch_bwd(const BwdParams& p, hipStream_t st) {
 
 using namespace ssa;
 
+namespace ssa {
+namespace {
+// Per (row, head) softmax stats for the dense-prefix pass: 4 floats.
+size_t bwd_ws_bytes(int dtype, int dout_dtype, int64_t batch, int64_t n, int h_q, int h_kv, int d) {
+  if (dtype != SSA_DTYPE_BF16 || dout_dtype != SSA_DTYPE_BF16 || (d != 64 && d != 128) || h_kv <= 0 ||
+      h_q % h_kv != 0 || h_q / h_kv > 8 || batch <= 0 || n <= 0)
+    return 0;
+  return sizeof(float) * 4 * static_cast<size_t>(batch * n * h_q);
+}
+}  // namespace
+}  // namespace ssa
+
+extern "C" size_t ssa_sparse_attention_backward_workspace_bytes(int dtype, int dout_dtype, int64_t batch,
+                                                                int64_t n, int h_q, int h_kv, int d) {
+  return bwd_ws_bytes(dtype, dout_dtype, batch, n, h_q, h_kv, d);
+}
+
 extern "C" int ssa_sparse_attention_backward(
     const void* q, const void* k, const void* v, int dtype, int64_t batch, int64_t n, int h_q,
     int h_kv, int d, int64_t q_sb, int64_t q_sn, int64_t q_sh, int64_t k_sb, int64_t k_sn,
@@ -556,7 +828,8 @@ extern "C" int ssa_sparse_attention_backward(
     int top_k, int64_t idx_sb, int64_t idx_sn, int64_t idx_sh, float scale_div, int causal,
     const int32_t* row_order, const void* out, int out_dtype, int64_t o_sb, int64_t o_sn,
     int64_t o_sh, const void* dout, int dout_dtype, int64_t do_sb, int64_t do_sn, int64_t do_sh,
-    float* dq, float* dk, float* dv, int32_t* error_flag, void* stream) {
+    float* dq, float* dk, float* dv, int32_t* error_flag, const int32_t* row_prefix, void* workspace,
+    size_t workspace_bytes, void* stream) {
   if (dtype != SSA_DTYPE_F32 && dtype != SSA_DTYPE_BF16)
     return fail(SSA_ERR_UNSUPPORTED, "sparse_attention_backward: dtype %d not supported (f32, bf16)", dtype);
   if ((out_dtype != SSA_DTYPE_F32 && out_dtype != SSA_DTYPE_BF16) ||
@@ -598,6 +871,15 @@ extern "C" int ssa_sparse_attention_backward(
   p.order = row_order;
   if (p.rows >= (int64_t(1) << 31))
     return fail(SSA_ERR_UNSUPPORTED, "sparse_attention_backward: too many rows");
+  if (row_prefix && workspace) {
+    const size_t need = bwd_ws_bytes(dtype, dout_dtype, batch, n, h_q, h_kv, d);
+    if (workspace_bytes < need)
+      return fail(SSA_ERR_WORKSPACE, "sparse_attention_backward: workspace %zu < %zu bytes", workspace_bytes, need);
+    if (need > 0 && dtype == SSA_DTYPE_BF16 && bwd_mfma_ok(p, q, dout)) {
+      p.pfx = row_prefix;
+      p.pstats = static_cast<float*>(workspace);
+    }
+  }
   hipStream_t st = as_stream(stream);
   // dk and dv accumulate; dq rows are written whole by the row that owns them
   const int64_t kv_elems = batch * n * h_kv * d;

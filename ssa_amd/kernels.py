@@ -353,7 +353,8 @@ def sparse_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                               out: torch.Tensor, dout: torch.Tensor,
                               scale_div: Optional[float] = None, causal: bool = False,
                               error_flag: Optional[torch.Tensor] = None,
-                              row_order: Optional[torch.Tensor] = None
+                              row_order: Optional[torch.Tensor] = None,
+                              row_prefix: Optional[torch.Tensor] = None
                               ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """Gradients of stage (d) w.r.t. q, k, v (fp32, shapes of q, k, v), given the
     forward output ``out`` and its gradient ``dout`` (the autograd backward of
@@ -378,11 +379,21 @@ def sparse_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         if row_order.dtype != torch.int32 or tuple(row_order.shape) != (B, h_kv, n):
             raise ValueError(f"row_order must be int32 [{B}, {h_kv}, {n}]")
         row_order = row_order.contiguous()
+    ws_bytes, ws = 0, None
+    if row_prefix is not None:
+        _lib.require_device(row_prefix)
+        if (row_prefix.dtype != torch.int32 or tuple(row_prefix.shape) != (B, h_kv, n)
+                or not row_prefix.is_contiguous()):
+            raise ValueError(f"row_prefix must be a contiguous int32 [{B}, {h_kv}, {n}] tensor")
+        ws_bytes = int(_lib.load().ssa_sparse_attention_backward_workspace_bytes(
+            _lib.elem_dtype(q), _lib.elem_dtype(dout), B, n, h_q, h_kv, d))
+        ws = torch.empty(ws_bytes, device=q.device, dtype=torch.uint8) if ws_bytes else None
     call("ssa_sparse_attention_backward", ptr(q), ptr(k), ptr(v), _lib.elem_dtype(q), B, n, h_q,
          h_kv, d, q.stride(0), q.stride(1), q.stride(2), k.stride(0), k.stride(1), k.stride(2),
          v.stride(0), v.stride(1), v.stride(2), ptr(idx), _lib.index_dtype(idx), top_k,
          idx.stride(0), idx.stride(1), idx.stride(2), float(scale_div), int(bool(causal)),
          ptr(row_order), ptr(out), _lib.elem_dtype(out), out.stride(0), out.stride(1),
          out.stride(2), ptr(dout), _lib.elem_dtype(dout), dout.stride(0), dout.stride(1),
-         dout.stride(2), ptr(dq), ptr(dk), ptr(dv), ptr(error_flag), stream_of(q))
+         dout.stride(2), ptr(dq), ptr(dk), ptr(dv), ptr(error_flag), ptr(row_prefix), ptr(ws),
+         ws_bytes, stream_of(q))
     return dq, dk, dv

@@ -129,3 +129,50 @@ def test_select_row_prefix(dev, sorted_, use_ws):
     out_i = torch.empty_like(out_p)
     kernels.sparse_attention(q, k, v, idx, None, True, out=out_i)  # X found from the indices
     torch.testing.assert_close(out_i, out_r, rtol=1e-5, atol=1e-5)
+
+
+def _first_free(idx_row, cap):
+    """X of one index row: the first key in [0, cap) it does not hold, lowered
+    to the smallest key it holds twice (as the dense pass finds it)."""
+    vals, counts = np.unique(idx_row, return_counts=True)
+    x = 0
+    held = set(vals.tolist())
+    while x < cap and x in held:
+        x += 1
+    dups = vals[counts > 1]
+    return int(min(x, dups.min())) if dups.size else x
+
+
+@pytest.mark.parametrize("d,g,causal,n", [(128, 4, True, 700), (64, 8, False, 500), (128, 3, True, 333)])
+def test_backward_dense_prefix(dev, orc, d, g, causal, n):
+    """Gradients with the dense-prefix pass (row_prefix given: the row kernel
+    skips [0, X), blocks of 8 rows take it) equal the row path's and the
+    float64 oracle's (max|err| <= 2e-5 max|ref| per tensor, fp32 forward
+    output)."""
+    from ssa_amd import kernels
+
+    print(f"backward dense prefix d={d} g={g} causal={causal} n={n}", flush=True)
+    h_kv, top_k = 2, 128
+    q = randn((1, n, h_kv * g, d), 401, torch.bfloat16)
+    k = randn((1, n, h_kv, d), 402, torch.bfloat16)
+    v = randn((1, n, h_kv, d), 403, torch.bfloat16)
+    dout = randn((1, n, h_kv * g, d), 404, torch.float32).to(torch.bfloat16)
+    idx, _ = _prefix_rows(n, h_kv, top_k, 405)
+    idx[0, 40, 0, :] = torch.cat([torch.arange(top_k - 1), torch.tensor([5])])  # a duplicate in a prefix
+    xs = np.array([[_first_free(idx[0, i, h].numpy(), top_k) for i in range(n)] for h in range(h_kv)],
+                  dtype=np.int32)
+    assert (xs > 0).mean() > 0.3
+    pfx = torch.from_numpy(xs).unsqueeze(0).contiguous().to(dev)
+    qd, kd, vd, idd, dod = q.to(dev), k.to(dev), v.to(dev), idx.to(torch.int32).to(dev), dout.to(dev)
+    out32 = torch.empty(qd.shape, device=dev, dtype=torch.float32)
+    kernels.sparse_attention(qd, kd, vd, idd, None, causal, out=out32, row_prefix=pfx)
+    got = kernels.sparse_attention_backward(qd, kd, vd, idd, out32, dod, None, causal, row_prefix=pfx)
+    ref_row = kernels.sparse_attention_backward(qd, kd, vd, idd, out32, dod, None, causal)
+    rq, rk, rv = [np.stack([o]) for o in orc.sparse_attention_backward(
+        f32(q[0]), f32(k[0]), f32(v[0]), idx[0].numpy(), dout[0].double().numpy(), causal=causal)]
+    for name, a, b, r in zip(("dq", "dk", "dv"), got, ref_row, (rq, rk, rv)):
+        scale = float(np.abs(r).max())
+        err_o = float((a.cpu().double() - torch.from_numpy(r)).abs().max())
+        err_r = float((a - b).abs().max())
+        assert err_o <= 2e-5 * scale, f"{name} vs oracle: {err_o:.3e} > 2e-5 * {scale:.3e}"
+        assert err_r <= 2e-5 * scale, f"{name} vs row path: {err_r:.3e} > 2e-5 * {scale:.3e}"
