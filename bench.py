@@ -345,7 +345,7 @@ def time_backward(cfg, q, k, v, inter, reps=3):
     # per row: K gathered twice (two passes) and V once, indices twice, q/dO
     # (input type) and o (fp32) read, dq written, dk and dv read-modify-written
     byt = rows * (3 * kk * d * s + 2 * kk * 4 + g * d * (2 * s + 4) + g * d * 4 + 2 * kk * d * 8)
-    return {"ms": ms, "tokens_per_s": B * n / (ms / 1000), "kernel": "sparse_attention_bwd_kernel",
+    return {"ms": ms, "tokens_per_s": B * n / (ms / 1000), "kernel": "sparse_attention_bwd_mfma_kernel + prefix_attention_bwd_kernel",
             "algorithmic_gb": byt / 1e9, "gbs": byt / (ms / 1000) / 1e9}
 
 
