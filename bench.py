@@ -312,9 +312,11 @@ def stats_sums(q, k, router):
 
 
 def time_backward(cfg, q, k, v, inter, reps=3):
-    """Stage (d) backward (ssa_sparse_attention_backward) on the forward's indices
-    and query order, with an fp32 forward output and a seeded bf16 output
-    gradient; median of `reps` launches (HIP events on the launch stream)."""
+    """Stage (d) backward on the forward's indices and query order, with an fp32
+    forward output and a seeded bf16 output gradient, as SSAAttention trains:
+    ssa_sparse_attention_backward_routed (candidate keys by codebook bucket)
+    and, for comparison, the plain ssa_sparse_attention_backward; median of
+    `reps` launches each (HIP events on the launch stream)."""
     import torch
 
     from ssa_amd import kernels
@@ -328,16 +330,22 @@ def time_backward(cfg, q, k, v, inter, reps=3):
     kernels.sparse_attention(q, k, v, idx, None, True, out=out32, row_order=order, row_prefix=pfx)
     gen = torch.Generator(device=q.device).manual_seed(7)
     dout = torch.randn(q.shape, generator=gen, device=q.device).to(q.dtype)
-    ts = []
-    for _ in range(reps):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        kernels.sparse_attention_backward(q, k, v, idx, out32, dout, None, True, row_order=order,
-                                          row_prefix=pfx)
-        e1.record()
-        torch.cuda.synchronize()
-        ts.append(e0.elapsed_time(e1))
-    ms = sorted(ts)[len(ts) // 2]
+    routing = kernels.Routing(qc, kc, off, post, True)
+
+    def median_ms(rt):
+        ts = []
+        for _ in range(reps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            kernels.sparse_attention_backward(q, k, v, idx, out32, dout, None, True, row_order=order,
+                                              row_prefix=pfx, routing=rt)
+            e1.record()
+            torch.cuda.synchronize()
+            ts.append(e0.elapsed_time(e1))
+        return sorted(ts)[len(ts) // 2]
+
+    ms = median_ms(routing)
+    ms_plain = median_ms(None)
     B, n, h_q, h_kv, d, kk = cfg["B"], cfg["n"], cfg["h_q"], cfg["h_kv"], cfg["d"], cfg["k"]
     s = 2 if cfg["dtype"] == "bf16" else 4
     rows = B * n * h_kv
@@ -345,7 +353,9 @@ def time_backward(cfg, q, k, v, inter, reps=3):
     # per row: K gathered twice (two passes) and V once, indices twice, q/dO
     # (input type) and o (fp32) read, dq written, dk and dv read-modify-written
     byt = rows * (3 * kk * d * s + 2 * kk * 4 + g * d * (2 * s + 4) + g * d * 4 + 2 * kk * d * 8)
-    return {"ms": ms, "tokens_per_s": B * n / (ms / 1000), "kernel": "sparse_attention_bwd_mfma_kernel + prefix_attention_bwd_kernel",
+    return {"ms": ms, "tokens_per_s": B * n / (ms / 1000),
+            "kernel": "sparse_attention_bwd_mfma_kernel + prefix_attention_bwd_kernel + bucket_attention_bwd_kernel",
+            "ms_without_buckets": ms_plain,
             "algorithmic_gb": byt / 1e9, "gbs": byt / (ms / 1000) / 1e9}
 
 

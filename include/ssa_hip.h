@@ -413,6 +413,44 @@ int ssa_sparse_attention_backward(
 size_t ssa_sparse_attention_backward_workspace_bytes(int dtype, int dout_dtype, int64_t batch, int64_t n,
                                                      int h_q, int h_kv, int d);
 
+/* ssa_sparse_attention_backward for indices that ssa_select produced (index
+ * or score order, n >= top_k) from q_codes [batch][h_kv][n][a] and k_codes
+ * [batch][h_kv][n][b] (ssa_route_codes), offsets / postings of
+ * ssa_build_index, its row_prefix (required) and its causal routing flag
+ * (router_causal: the mask was causal, else none).  Same results as
+ * ssa_sparse_attention_backward (which pairs the indices hold is read from the
+ * codes, row_prefix and the indices, never from scores).  dk and dv of the
+ * candidate slots come from one pass per codebook
+ * bucket: the rows holding a code and the keys holding it form a dense tile
+ * (a pair sharing several codes counts in its smallest one), differentiated on
+ * the matrix cores with one fp32 atomic per (key, dim) and 32-key chunk of a
+ * bucket instead of one per selecting row.  Rows without filler (at least
+ * top_k candidates) look their keys up in a bitmap of n bits each; the
+ * workspace holds ssa_sparse_attention_backward_routed_workspace_bytes(...)
+ * bytes, and rows past its bitmap capacity keep per-row atomics.  Shapes the
+ * bucket pass does not take (fp32, d other than 64 / 128, g > 8, a > 32,
+ * b > 8, N_c > 16384) run ssa_sparse_attention_backward's path.  No reference
+ * counterpart (the reference's backward is autograd, ssa/attention.py:64-113). */
+int ssa_sparse_attention_backward_routed(
+    const void* q, const void* k, const void* v, int dtype, int64_t batch, int64_t n, int h_q,
+    int h_kv, int d, int64_t q_sb, int64_t q_sn, int64_t q_sh, int64_t k_sb, int64_t k_sn,
+    int64_t k_sh, int64_t v_sb, int64_t v_sn, int64_t v_sh, const void* idx, int idx_dtype,
+    int top_k, int64_t idx_sb, int64_t idx_sn, int64_t idx_sh, float scale_div, int causal,
+    const int32_t* row_order, const void* out, int out_dtype, int64_t o_sb, int64_t o_sn,
+    int64_t o_sh, const void* dout, int dout_dtype, int64_t do_sb, int64_t do_sn, int64_t do_sh,
+    float* dq, float* dk, float* dv, int32_t* error_flag, const int32_t* row_prefix,
+    const int32_t* q_codes, int a, const int32_t* k_codes, int b, const int32_t* offsets,
+    const int32_t* postings, int n_c, int router_causal, void* workspace, size_t workspace_bytes,
+    void* stream);
+
+/* Bytes of ssa_sparse_attention_backward_routed's workspace with key bitmaps
+ * for bitmap_rows rows without filler (negative: half of the batch x kv head
+ * x n rows); ssa_sparse_attention_backward_workspace_bytes(...) where the
+ * bucket pass does not run.  No reference counterpart. */
+size_t ssa_sparse_attention_backward_routed_workspace_bytes(int dtype, int dout_dtype, int64_t batch,
+                                                            int64_t n, int h_q, int h_kv, int d, int a, int b,
+                                                            int n_c, int64_t bitmap_rows);
+
 #ifdef __cplusplus
 }
 #endif

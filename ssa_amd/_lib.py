@@ -116,6 +116,14 @@ SIGNATURES = {
          _i64, _i64, _i64, _vp, _int, _int, _i64, _i64, _i64, _flt, _int, _vp, _vp, _int, _i64,
          _i64, _i64, _vp, _int, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "ssa_sparse_attention_backward_workspace_bytes": (_sz, [_int, _int, _i64, _i64, _int, _int, _int]),
+    "ssa_sparse_attention_backward_routed": (
+        _int,
+        [_vp, _vp, _vp, _int, _i64, _i64, _int, _int, _int, _i64, _i64, _i64, _i64, _i64, _i64,
+         _i64, _i64, _i64, _vp, _int, _int, _i64, _i64, _i64, _flt, _int, _vp, _vp, _int, _i64,
+         _i64, _i64, _vp, _int, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp,
+         _vp, _int, _vp, _int, _vp, _vp, _int, _int, _vp, _sz, _vp]),
+    "ssa_sparse_attention_backward_routed_workspace_bytes": (
+        _sz, [_int, _int, _i64, _i64, _int, _int, _int, _int, _int, _int, _i64]),
 }
 
 _lib = None

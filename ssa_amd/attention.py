@@ -21,7 +21,7 @@ class _SparseAttention(torch.autograd.Function):
     (ssa/attention.py:64-113); the indices get none, as in the reference."""
 
     @staticmethod
-    def forward(ctx, q, k, v, indices, scale, causal, row_order, flag, row_prefix):
+    def forward(ctx, q, k, v, indices, scale, causal, row_order, flag, row_prefix, routing):
         # The backward's D = dO . o uses an fp32 copy of the output: a bf16 one
         # would carry its 2^-9 rounding into every gradient.
         out32 = torch.empty(q.shape, device=q.device, dtype=torch.float32)
@@ -30,8 +30,10 @@ class _SparseAttention(torch.autograd.Function):
         ctx.scale, ctx.causal = scale, causal
         ctx.has_order = row_order is not None
         ctx.has_prefix = row_prefix is not None
+        ctx.routing_causal = None if routing is None else bool(routing.causal)
         saved = ([q, k, v, indices, out32] + ([row_order] if row_order is not None else [])
-                 + ([row_prefix] if row_prefix is not None else []))
+                 + ([row_prefix] if row_prefix is not None else [])
+                 + (list(routing[:4]) if routing is not None else []))
         ctx.save_for_backward(*saved)
         return out32 if q.dtype == torch.float32 else out32.to(q.dtype)
 
@@ -40,11 +42,13 @@ class _SparseAttention(torch.autograd.Function):
         q, k, v, indices, out, *rest = ctx.saved_tensors
         order = rest.pop(0) if ctx.has_order else None
         prefix = rest.pop(0) if ctx.has_prefix else None
+        routing = kernels.Routing(*rest[:4], ctx.routing_causal) if ctx.routing_causal is not None else None
         if dout.stride(-1) != 1:
             dout = dout.contiguous()
         dq, dk, dv = kernels.sparse_attention_backward(q, k, v, indices, out, dout, ctx.scale,
-                                                       ctx.causal, row_order=order, row_prefix=prefix)
-        return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), None, None, None, None, None, None
+                                                       ctx.causal, row_order=order, row_prefix=prefix,
+                                                       routing=routing)
+        return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), None, None, None, None, None, None, None
 
 
 def sparse_exact_attention(
@@ -58,6 +62,7 @@ def sparse_exact_attention(
     check_indices: bool = True,
     row_order: Optional[torch.Tensor] = None,
     row_prefix: Optional[torch.Tensor] = None,
+    routing: Optional[kernels.Routing] = None,
 ) -> torch.Tensor:
     """softmax(q . K[indices]^T / scale) . V[indices] per (query, KV head).
 
@@ -76,7 +81,9 @@ def sparse_exact_attention(
     ``route(..., with_prefix=True).prefix``) names the key prefix [0, X) each
     row's indices hold once; bf16 inputs with d 64 or 128 attend it in a dense
     pass (also found from the indices without it; same result up to summation
-    order).
+    order).  ``routing`` (``route(...).routing()``, with ``row_prefix``) is the
+    selection the indices came from: the backward then differentiates the
+    candidate keys by codebook bucket (same gradients, far fewer atomics).
 
     Differentiable in q, k and v (HIP backward kernel); not in ``indices``.
     """
@@ -102,7 +109,7 @@ def sparse_exact_attention(
         row_prefix = row_prefix.unsqueeze(0)
     if torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad):
         out = _SparseAttention.apply(q, k, v, indices, float(scale), bool(causal), row_order, flag,
-                                     row_prefix)
+                                     row_prefix, routing)
     else:
         out = kernels.sparse_attention(q, k, v, indices, float(scale), causal, error_flag=flag,
                                        row_order=row_order, row_prefix=row_prefix)

@@ -19,6 +19,7 @@
 // g-head sums for dk[idx_t] and dv[idx_t] with fp32 atomics (many rows select
 // the same key).  All arithmetic is fp32; dq, dk and dv are fp32 buffers.
 #include "ssa_common.h"
+#include "ssa_internal.h"
 #include "ssa_rows.h"
 
 namespace ssa {
@@ -56,6 +57,10 @@ struct BwdParams {
   // handles them for blocks of neighbouring rows.
   const int32_t* pfx;
   float* pstats;
+  // Bucket mode (nullable [rows], with pfx): the candidate slots' dk and dv
+  // come from bucket_attention_bwd_kernel, so the row kernel adds them only
+  // for rows marked -1 here (rows without filler that got no key bitmap).
+  const int32_t* rowmap;
 };
 
 __device__ __forceinline__ float ld_any(const void* p, int64_t off, int is_bf16) {
@@ -385,6 +390,7 @@ __global__ __launch_bounds__(64 * kBwMfWaves, 2) void sparse_attention_bwd_mfma_
     ps[2] = dcol;
   }
   auto chunk_ok2 = [&](int j) { return j >= xpre && chunk_ok(j); };
+  const bool row_dkdv = !p.rowmap || p.rowmap[bh * p.n + i] == -1;
 
   // ---- pass 2
   const bool hi_row = c16 < g;
@@ -473,6 +479,7 @@ __global__ __launch_bounds__(64 * kBwMfWaves, 2) void sparse_attention_bwd_mfma_
     for (int t = 0; t < NT; ++t) dqacc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kt[t], dsb, dqacc[t], 0, 0, 0);
 
     // dV and dK tiles; P then dS pass through tr as [key][head]
+    if (!row_dkdv) continue;
 #pragma unroll
     for (int pass = 0; pass < 2; ++pass) {
       const float* src = pass == 0 ? pr : ds;
@@ -748,6 +755,534 @@ __global__ __launch_bounds__(64 * kPbWaves, 1) void prefix_attention_bwd_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Bucket mode: dk and dv of the candidate slots, by codebook bucket.
+//
+// A row's candidates are the keys that share one of its a query codes (inside
+// the routing window), so the (query row, candidate key) pairs of one kv head
+// are the union over buckets c of R_c x K_c: R_c the rows holding code c (an
+// index of q_codes built like stage (b)'s) and K_c the keys holding it (stage
+// (b)'s index).  A pair sharing several codes counts in the bucket of the
+// smallest shared code.  The pairs a row selected, at or above its dense
+// prefix X, are
+//   * for a row with filler (X > 0): every candidate at or above X;
+//   * for a row without filler (X = 0: at least top_k candidates): the ones
+//     its indices hold, read from a per-row key bitmap (bucket_rowmap_kernel);
+//     rows past the bitmap capacity keep the row kernel's atomics.
+// One block per (bucket, 32-key chunk) "item": K and V of the chunk stay in
+// LDS while the bucket's rows stream through in chunks of 16 query vectors
+// (row, head), staged one chunk ahead.  Wave w takes keys 16 (w & 1) ... + 15
+// and dims (w >> 1) D/2 ... + D/2 - 1: S = Q K^T and dP = dO V^T on the matrix
+// cores (A = the query vectors' Q / dO rows, B = the chunk's K / V rows),
+// p = exp2(s - m) / l and ds = p (dP - D) from the row kernel's stats, and
+// dV^T += dO^T P, dK^T += Q^T dS in registers (B = P or dS split into bf16 hi
+// and lo, k = 8 q4 + e <-> query vector 4 q4 + (e & 3); A = dO^T or Q^T from
+// transposing LDS reads of the staged rows, the same four query vectors
+// twice).  One fp32 atomic per (key, dim) and item at the end.  Every LDS read
+// of a chunk precedes the next chunk's LDS-bound loads, so no read waits for
+// them.
+constexpr int kBkKeys = 32;    // keys per item
+constexpr int kBkQv = 16;      // query vectors per row chunk
+constexpr int kBkMaxA = 32;    // query codes per row (bucket mode)
+constexpr int kBkMaxB = 8;     // key codes per key (bucket mode)
+constexpr int kBkHash = 512;   // LDS hash of the item's codes below c (at most 32 x 7)
+constexpr int kBkThreads = 256;
+
+struct BucketParams {
+  const int32_t* kpost;   // [bh][n * b] key index postings
+  const int32_t* kcodes;  // [bh][n][b]
+  const int4* desc;       // [bh][max_items] (bucket_desc_kernel)
+  const int2* meta;       // [bh][n * a]: (row position, w) per query posting, w as bucket_meta_kernel
+  const int32_t* qcodes;  // [bh][n][a]
+  const uint32_t* bits;   // [capacity][words]: key bitmaps of rows without filler
+  int64_t words, max_items;
+  int a, b, gp_log2, router_causal;
+};
+
+// items[bh][c] = sum over c' < c of ceil(|K_c'| / kBkKeys); one block per bh.
+__global__ __launch_bounds__(1024) void bucket_items_kernel(const int32_t* __restrict__ koff, int n_c,
+                                                            int32_t* __restrict__ items) {
+  __shared__ int32_t wsum[16];
+  __shared__ int32_t carry;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int32_t* o = koff + static_cast<int64_t>(blockIdx.x) * (n_c + 1);
+  int32_t* it = items + static_cast<int64_t>(blockIdx.x) * (n_c + 1);
+  if (tid == 0) carry = 0;
+  __syncthreads();
+  for (int base = 0; base < n_c; base += 1024) {
+    const int c = base + tid;
+    const int cnt = c < n_c ? (o[c + 1] - o[c] + kBkKeys - 1) / kBkKeys : 0;
+    int x = cnt;
+#pragma unroll
+    for (int s = 1; s < 64; s <<= 1) {
+      const int y = __shfl_up(x, s);
+      if (lane >= s) x += y;
+    }
+    if (lane == 63) wsum[wave] = x;
+    __syncthreads();
+    if (tid == 0) {
+      int run = carry;
+      for (int w = 0; w < 16; ++w) {
+        const int t = wsum[w];
+        wsum[w] = run;
+        run += t;
+      }
+      carry = run;
+    }
+    __syncthreads();
+    if (c < n_c) it[c] = wsum[wave] + x - cnt;
+    __syncthreads();
+  }
+  if (tid == 0) it[n_c] = carry;
+}
+
+// Per item slot of (bh, max_items): int4 (c | nk << 16, k0, rs, r1) -- the
+// bucket, its postings k0 .. k0 + nk - 1, and its rows rs .. r1 - 1 in the
+// query index (rows below the chunk's lowest key dropped when a mask is
+// causal) -- or c = -1 past the bh's items.
+__global__ void bucket_desc_kernel(const int32_t* __restrict__ koff, const int32_t* __restrict__ kpost,
+                                   const int32_t* __restrict__ qoff, const int32_t* __restrict__ qpost,
+                                   const int32_t* __restrict__ items, int n_c, int64_t n, int a, int b,
+                                   int64_t max_items, int causal_any, int4* __restrict__ desc) {
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t bh = blockIdx.y;
+  if (item >= max_items) return;
+  const int64_t ob = bh * (n_c + 1);
+  const int32_t* it = items + ob;
+  int4 out = make_int4(-1, 0, 0, 0);
+  if (item < it[n_c]) {
+    int lo = 0, hi = n_c;  // it[lo] <= item < it[hi]
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (it[mid] <= item) lo = mid;
+      else hi = mid;
+    }
+    const int k0 = koff[ob + lo] + static_cast<int>(item - it[lo]) * kBkKeys;
+    const int nk = min(kBkKeys, koff[ob + lo + 1] - k0);
+    int rs = qoff[ob + lo];
+    const int r1 = qoff[ob + lo + 1];
+    if (causal_any) {
+      const int kmin = kpost[bh * n * b + k0];
+      const int32_t* qp = qpost + bh * n * a;
+      int h2 = r1;
+      while (rs < h2) {
+        const int mid = (rs + h2) >> 1;
+        if (qp[mid] < kmin) rs = mid + 1;
+        else h2 = mid;
+      }
+    }
+    out = make_int4(lo | (nk << 16), k0, rs, r1);
+  }
+  desc[bh * max_items + item] = out;
+}
+
+// Rows without filler (X <= 0) get a slot of `bits` holding the keys of their
+// indices; rowmap = slot, -1 past the capacity (the row kernel keeps those
+// rows' dk and dv), -2 for rows with filler.  One wave per 64 rows, one
+// counter atomic per wave.
+__global__ __launch_bounds__(256) void bucket_rowmap_kernel(BwdParams p, int32_t* __restrict__ ctr,
+                                                            int32_t* __restrict__ rowmap,
+                                                            uint32_t* __restrict__ bits, int64_t cap,
+                                                            int64_t words) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t r0 = (static_cast<int64_t>(blockIdx.x) * 4 + wave) * 64;
+  if (r0 >= p.rows) return;
+  const int64_t r = r0 + lane;
+  const bool in = r < p.rows;
+  const bool need = in && p.pfx[r] <= 0;
+  const uint64_t bal = __ballot(need);
+  int base = 0;
+  if (lane == 0 && bal) base = atomicAdd(ctr, static_cast<int>(__popcll(bal)));
+  base = __shfl(base, 0);
+  const int id = base + static_cast<int>(__builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(bal >> 32),
+                                                                   __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bal), 0u)));
+  if (in) rowmap[r] = need ? (id < cap ? id : -1) : -2;
+  for (uint64_t todo = bal; todo; todo &= todo - 1) {
+    const int rid = __shfl(id, __builtin_ctzll(todo));
+    if (rid >= cap) break;  // ids ascend with the lane
+    uint32_t* bm = bits + static_cast<int64_t>(rid) * words;
+    for (int64_t w = lane; w < words; w += 64) bm[w] = 0u;
+  }
+  __threadfence();  // the cleared words reach memory before the ORs below
+  for (uint64_t todo = bal; todo; todo &= todo - 1) {
+    const int l = __builtin_ctzll(todo);
+    const int rid = __shfl(id, l);
+    if (rid >= cap) break;
+    uint32_t* bm = bits + static_cast<int64_t>(rid) * words;
+    const int64_t rr = r0 + l;
+    const int64_t bh = rr / p.n, i = rr - bh * p.n;
+    const int h = static_cast<int>(bh % p.h_kv);
+    const int64_t bb = bh / p.h_kv;
+    const unsigned char* ib = static_cast<const unsigned char*>(p.idx) +
+                              (bb * p.idx_sb + i * p.idx_sn + h * p.idx_sh) * (p.idx_i64 ? 8 : 4);
+    for (int s = lane; s < p.top_k; s += 64) {
+      const int64_t j = p.idx_i64 ? reinterpret_cast<const int64_t*>(ib)[s]
+                                  : static_cast<int64_t>(reinterpret_cast<const int32_t*>(ib)[s]);
+      if (j >= 0 && j < p.n) atomicOr(bm + (j >> 5), 1u << (j & 31));
+    }
+  }
+}
+
+// meta[e] = (row position i, w) per query posting e: w = X for a row with
+// filler, -2 - bitmap slot for a row without, -1 for a row the row kernel keeps.
+__global__ void bucket_meta_kernel(const int32_t* __restrict__ qpost, int64_t per_bh, int64_t total, int64_t n,
+                                   const int32_t* __restrict__ pfx, const int32_t* __restrict__ rowmap,
+                                   int2* __restrict__ meta) {
+  const int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (e >= total) return;
+  const int i = qpost[e];
+  const int64_t r = (e / per_bh) * n + i;
+  const int x = pfx[r];
+  int w = x;
+  if (x <= 0) {
+    const int id = rowmap[r];
+    w = id >= 0 ? -2 - id : -1;
+  }
+  meta[e] = make_int2(i, w);
+}
+
+// 4 bf16 of the staged rows 4 q4 + e (e = 0..3) at column 16 dt + c16 (the
+// first half of rows_transposed: a 16-row buffer).
+template <int D>
+__device__ __forceinline__ uint2 rows_transposed16(const unsigned char* l, int dt, int q4, int c16) {
+  const int vkey = 4 * q4 + (c16 >> 2);
+  const int off = vkey * MfShape<D>::ROW + (((2 * dt + ((c16 & 3) >> 1)) ^ mf_swz<D>(vkey)) << 4) + (c16 & 1) * 8;
+  return __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_ptr)(l + off)));
+}
+
+__device__ __forceinline__ int bk_hash(int code) {
+  return static_cast<int>((static_cast<uint32_t>(code) * 2654435761u) >> 23) & (kBkHash - 1);
+}
+
+template <int D>
+__global__ __launch_bounds__(kBkThreads, 2) void bucket_attention_bwd_kernel(BwdParams p, BucketParams bp) {
+  using S = MfShape<D>;
+  constexpr int KB = S::KB;
+  constexpr int DT = D / 32;             // 16-dim tiles per wave (half of the dims)
+  constexpr int QLD = kBkQv / S::KPI;    // wave-wide loads per staged tensor
+  __shared__ __align__(16) unsigned char kvs[2][kBkKeys * S::ROW];     // K, V of the item's keys
+  __shared__ __align__(16) unsigned char qds[2][2][kBkQv * S::ROW];    // [buffer][Q, dO] query vectors
+  __shared__ __align__(16) float s_st[2][kBkQv][4];                    // softmax reference, 1/sum, D
+  __shared__ int2 s_meta[2][kBkQv];                                    // (i, w) per row of a chunk
+  __shared__ uint32_t s_bw[2][kBkQv][kBkKeys];                         // bitmap word per (row, key)
+  __shared__ uint32_t s_dup[2][kBkQv];   // keys sharing a code below c with the row
+  __shared__ uint32_t s_mask[kBkQv];     // pairs counted here, per row
+  __shared__ int32_t s_j[kBkKeys];
+  __shared__ int32_t s_kc[kBkKeys][kBkMaxB];
+  __shared__ int32_t s_hk[kBkHash];      // codes below c of the item's keys ...
+  __shared__ uint32_t s_hm[kBkHash];     // ... and the keys holding each
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int q4 = lane >> 4, c16 = lane & 15;
+  const int64_t bh = blockIdx.y;
+  const int4 ds = bp.desc[bh * bp.max_items + blockIdx.x];
+  if (ds.x < 0) return;
+  const int c = ds.x & 0xFFFF, nk = ds.x >> 16, k0 = ds.y, rs = ds.z, r1 = ds.w;
+  const int g = p.g, gpl = bp.gp_log2, rpc = kBkQv >> gpl;
+  const int nrc = (r1 - rs + rpc - 1) / rpc;
+  if (nrc <= 0) return;
+  const int32_t* kp = bp.kpost + bh * p.n * bp.b;
+  const int2* meta = bp.meta + bh * p.n * bp.a;
+  const int h = static_cast<int>(bh % p.h_kv);
+  const int64_t bb = bh / p.h_kv;
+
+  if (tid < kBkKeys) {
+    const int j = tid < nk ? kp[k0 + tid] : -1;
+    s_j[tid] = j;
+    const int32_t* kcj = bp.kcodes + (bh * p.n + (j >= 0 ? j : 0)) * bp.b;
+    int cv[kBkMaxB];
+#pragma unroll
+    for (int x = 0; x < kBkMaxB; ++x) cv[x] = kcj[x < bp.b ? x : 0];  // all loads in flight together
+#pragma unroll
+    for (int x = 0; x < kBkMaxB; ++x) s_kc[tid][x] = (j >= 0 && x < bp.b) ? cv[x] : 0x7FFFFFFF;
+  }
+  for (int e = tid; e < kBkHash; e += kBkThreads) {
+    s_hk[e] = -1;
+    s_hm[e] = 0u;
+  }
+  if (tid < kBkQv) s_dup[0][tid] = 0u;
+  // K and V of the chunk (32-bit buffer offsets, zeros past the chunk)
+  const uint16_t* kbase = static_cast<const uint16_t*>(p.k) + bb * p.k_sb + static_cast<int64_t>(h) * p.k_sh;
+  const uint16_t* vbase = static_cast<const uint16_t*>(p.v) + bb * p.v_sb + static_cast<int64_t>(h) * p.v_sh;
+  const uint32_t ksn2 = 2u * static_cast<uint32_t>(p.k_sn), vsn2 = 2u * static_cast<uint32_t>(p.v_sn);
+  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(kbase), 0, static_cast<int>((p.n - 1) * p.k_sn * 2 + 2 * D), kBufferWord3);
+  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(vbase), 0, static_cast<int>((p.n - 1) * p.v_sn * 2 + 2 * D), kBufferWord3);
+  uint32_t seg16[S::SWZ_PERIOD];
+  row_seg16<D>(lane, seg16);
+  constexpr int KVL = (S::NLD + kBkThreads / 64 - 1) / (kBkThreads / 64);  // K/V loads per wave
+  int jl[KVL];
+#pragma unroll
+  for (int x = 0; x < KVL; ++x) {
+    const int slot = S::KPI * (wave + x * (kBkThreads / 64)) + lane / S::SEGS;
+    jl[x] = (wave + x * (kBkThreads / 64) < S::NLD && slot < nk) ? kp[k0 + slot] : -1;
+  }
+#pragma unroll
+  for (int x = 0; x < KVL; ++x) {
+    const int r = wave + x * (kBkThreads / 64);
+    if (r >= S::NLD) break;
+    const int j = jl[x];
+    const uint32_t sg = seg16[r % S::SWZ_PERIOD];
+    const uint32_t ko = j >= 0 ? __umul24(static_cast<uint32_t>(j), ksn2) + sg : kOobOffset;
+    const uint32_t vo = j >= 0 ? __umul24(static_cast<uint32_t>(j), vsn2) + sg : kOobOffset;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_void_ptr)(kvs[0] + r * 1024), 16, static_cast<int>(ko), 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_void_ptr)(kvs[1] + r * 1024), 16, static_cast<int>(vo), 0, 0, 0);
+  }
+  // Q and dO of the head group (offsets checked below 2^31 on the host)
+  const uint16_t* qbase = static_cast<const uint16_t*>(p.q) + bb * p.q_sb + static_cast<int64_t>(h * g) * p.q_sh;
+  const uint16_t* dbase = static_cast<const uint16_t*>(p.dout) + bb * p.do_sb + static_cast<int64_t>(h * g) * p.do_sh;
+  const __amdgpu_buffer_rsrc_t qrs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(qbase), 0, static_cast<int>(((p.n - 1) * p.q_sn + (g - 1) * p.q_sh) * 2 + 2 * D), kBufferWord3);
+  const __amdgpu_buffer_rsrc_t drs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(dbase), 0, static_cast<int>(((p.n - 1) * p.do_sn + (g - 1) * p.do_sh) * 2 + 2 * D), kBufferWord3);
+  const int gmask = (1 << gpl) - 1;
+
+  // the query vectors of chunk rows s_meta[bf] into qds[bf]
+  auto stage_rows = [&](int bf) {
+    if (wave < QLD) {
+      const int qv = S::KPI * wave + lane / S::SEGS;
+      const int rho = qv >> gpl, hh = qv & gmask;
+      const int i = s_meta[bf][rho].x;
+      const bool ok = rho < rpc && i >= 0 && hh < g;
+      const uint32_t sg = seg16[wave % S::SWZ_PERIOD];
+      const uint32_t qo = ok ? static_cast<uint32_t>((i * p.q_sn + hh * p.q_sh) * 2) + sg : kOobOffset;
+      const uint32_t dof = ok ? static_cast<uint32_t>((i * p.do_sn + hh * p.do_sh) * 2) + sg : kOobOffset;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(qrs, (lds_void_ptr)(qds[bf][0] + wave * 1024), 16, static_cast<int>(qo), 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(drs, (lds_void_ptr)(qds[bf][1] + wave * 1024), 16, static_cast<int>(dof), 0, 0, 0);
+    }
+  };
+  // stats, query codes and bitmap words of chunk rows s_meta[bf], into registers
+  float4 st_r = make_float4(0.f, 0.f, 0.f, 0.f);
+  int qc_r[2] = {-1, -1};
+  int qrho[2] = {kBkQv, kBkQv};
+  uint32_t bw_r[2] = {0u, 0u};
+  auto load_rows = [&](int bf) {
+    if (tid < kBkQv) {
+      const int rho = tid >> gpl, hh = tid & gmask;
+      const int i = s_meta[bf][rho].x;
+      st_r = (rho < rpc && i >= 0 && hh < g)
+                 ? *reinterpret_cast<const float4*>(p.pstats + ((bh * p.n + i) * g + hh) * 4)
+                 : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int x = 0; x < 2; ++x) {
+      const int e = tid + kBkThreads * x;
+      const int rho = e / bp.a, aa = e - rho * bp.a;
+      qc_r[x] = -1;
+      qrho[x] = kBkQv;
+      if (rho < rpc) {
+        const int i = s_meta[bf][rho].x;
+        if (i >= 0) {
+          qc_r[x] = bp.qcodes[(bh * p.n + i) * bp.a + aa];
+          qrho[x] = rho;
+        }
+      }
+      const int rk = e >> 5, kappa = e & 31;
+      bw_r[x] = 0u;
+      if (rk < rpc) {
+        const int w = s_meta[bf][rk].y;
+        const int j = s_j[kappa];
+        if (w <= -2 && j >= 0) bw_r[x] = bp.bits[static_cast<int64_t>(-2 - w) * bp.words + (j >> 5)];
+      }
+    }
+  };
+  // ... into LDS; a row code below c names the item's keys that share it
+  auto store_rows = [&](int bf) {
+    if (tid < kBkQv) *reinterpret_cast<float4*>(&s_st[bf][tid][0]) = st_r;
+#pragma unroll
+    for (int x = 0; x < 2; ++x) {
+      const int e = tid + kBkThreads * x;
+      const int rk = e >> 5;
+      if (rk < rpc) s_bw[bf][rk][e & 31] = bw_r[x];
+      const int code = qc_r[x];
+      if (qrho[x] < kBkQv && code >= 0 && code < c) {
+        int slot = bk_hash(code);
+        uint32_t m = 0u;
+        for (int probe = 0; probe < kBkHash; ++probe) {
+          const int k2 = s_hk[slot];
+          if (k2 == code) {
+            m = s_hm[slot];
+            break;
+          }
+          if (k2 == -1) break;
+          slot = (slot + 1) & (kBkHash - 1);
+        }
+        if (m) atomicOr(&s_dup[bf][qrho[x]], m);
+      }
+    }
+  };
+  // which (row, key) pairs of chunk bf this item counts -> s_mask
+  auto make_mask = [&](int bf) {
+#pragma unroll
+    for (int x = 0; x < 2; ++x) {
+      if (x == 1 && rpc * kBkKeys <= kBkThreads) break;
+      const int pr = tid + kBkThreads * x;
+      const int rho = pr >> 5, kappa = pr & 31;
+      bool ok = false;
+      if (rho < rpc) {
+        const int2 m = s_meta[bf][rho];
+        const int j = s_j[kappa];
+        if (m.x >= 0 && j >= 0 && m.y != -1 && !(p.causal && j > m.x) && !((s_dup[bf][rho] >> kappa) & 1u)) {
+          if (m.y > 0) ok = j >= m.y && !(bp.router_causal && j > m.x);
+          else ok = ((s_bw[bf][rho][kappa] >> (j & 31)) & 1u) != 0;
+        }
+      }
+      const uint64_t bal = __ballot(ok);
+      const int rb = 2 * wave + 8 * x;
+      if (lane == 0) {
+        if (rb < rpc) s_mask[rb] = static_cast<uint32_t>(bal);
+        if (rb + 1 < rpc) s_mask[rb + 1] = static_cast<uint32_t>(bal >> 32);
+      }
+    }
+  };
+
+  int2 m_next = make_int2(-1, -1);
+  if (tid < kBkQv) {
+    const int e0 = rs + tid, e1 = rs + rpc + tid;
+    s_meta[0][tid] = (tid < rpc && e0 < r1) ? meta[e0] : make_int2(-1, -1);
+    m_next = (tid < rpc && e1 < r1) ? meta[e1] : make_int2(-1, -1);
+  }
+  __syncthreads();
+  // the item's codes below c -> keys holding them
+  {
+    const int kappa = tid >> 3, y = tid & 7;
+    const int code = s_kc[kappa][y];
+    if (code < c) {
+      int slot = bk_hash(code);
+      for (int probe = 0; probe < kBkHash; ++probe) {
+        const int prev = atomicCAS(&s_hk[slot], -1, code);
+        if (prev == -1 || prev == code) {
+          atomicOr(&s_hm[slot], 1u << kappa);
+          break;
+        }
+        slot = (slot + 1) & (kBkHash - 1);
+      }
+    }
+  }
+  load_rows(0);
+  stage_rows(0);
+  __syncthreads();  // the hash is complete
+  store_rows(0);
+  if (tid < kBkQv) s_meta[1][tid] = m_next;
+  __builtin_amdgcn_s_waitcnt(kWaitVm0);
+  __syncthreads();
+
+  const int t = wave & 1, dh = wave >> 1;
+  const bool keys_here = 16 * t < nk;
+  const int kswz = mf_swz<D>(16 * t + c16);
+  bf16x8_t kf[KB], vf[KB];
+#pragma unroll
+  for (int kb = 0; kb < KB; ++kb) {
+    kf[kb] = *(lds_bf16x8_ptr)(kvs[0] + (16 * t + c16) * S::ROW + (((kb * 4 + q4) ^ kswz) << 4));
+    vf[kb] = *(lds_bf16x8_ptr)(kvs[1] + (16 * t + c16) * S::ROW + (((kb * 4 + q4) ^ kswz) << 4));
+  }
+  const int qswz = mf_swz<D>(c16);
+  floatx4_t accv[DT], acck[DT];
+#pragma unroll
+  for (int dd = 0; dd < DT; ++dd) {
+    accv[dd] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+    acck[dd] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+  }
+  const uint32_t keybit = 1u << (16 * t + c16);
+
+  for (int u = 0; u < nrc; ++u) {
+    const int bf = u & 1, nb = bf ^ 1;
+    make_mask(bf);
+    if (tid < kBkQv) s_dup[nb][tid] = 0u;
+    __syncthreads();  // s_mask of chunk u
+    // every LDS read of chunk u, before chunk u + 1's LDS-bound loads
+    uint32_t hm = 0;
+    for (int rho = 0; rho < rpc; ++rho) hm |= s_mask[rho];
+    const bool act = keys_here && ((hm >> (16 * t)) & 0xFFFFu) != 0;
+    bf16x8_t qa[KB], da[KB];
+    uint2 ad[DT], aq[DT];
+    float4 stv[4];
+    bool okv[4];
+    if (act) {
+      const unsigned char* ql = qds[bf][0];
+      const unsigned char* dl = qds[bf][1];
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        qa[kb] = *(lds_bf16x8_ptr)(ql + c16 * S::ROW + (((kb * 4 + q4) ^ qswz) << 4));
+        da[kb] = *(lds_bf16x8_ptr)(dl + c16 * S::ROW + (((kb * 4 + q4) ^ qswz) << 4));
+      }
+#pragma unroll
+      for (int dd = 0; dd < DT; ++dd) {
+        ad[dd] = rows_transposed16<D>(dl, DT * dh + dd, q4, c16);
+        aq[dd] = rows_transposed16<D>(ql, DT * dh + dd, q4, c16);
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int qv = 4 * q4 + e;
+        stv[e] = *reinterpret_cast<const float4*>(&s_st[bf][qv][0]);
+        okv[e] = (qv & gmask) < g && (s_mask[qv >> gpl] & keybit) != 0;
+      }
+    }
+    if (u + 1 < nrc) load_rows(nb);
+    if (u + 2 < nrc && tid < kBkQv) {
+      const int e2 = rs + (u + 2) * rpc + tid;
+      m_next = (tid < rpc && e2 < r1) ? meta[e2] : make_int2(-1, -1);
+    }
+    if (u + 1 < nrc) stage_rows(nb);
+    if (act) {
+      floatx4_t sv = {0.f, 0.f, 0.f, 0.f}, dv = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        sv = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[kb], kf[kb], sv, 0, 0, 0);
+        dv = __builtin_amdgcn_mfma_f32_16x16x32_bf16(da[kb], vf[kb], dv, 0, 0, 0);
+      }
+      // lane (q4, c16): query vectors 4 q4 + e against key 16 t + c16
+      float pv[4], dsv[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        pv[e] = okv[e] ? exp2f(sv[e] * p.qk_scale_log2 - stv[e].x) * stv[e].y : 0.0f;
+        dsv[e] = pv[e] * (dv[e] - stv[e].z);
+      }
+      uint32_t bpw[4], bdw[4];
+#pragma unroll
+      for (int w = 0; w < 2; ++w) {
+        const uint32_t ph = pack_bf16x2(pv[2 * w], pv[2 * w + 1]);
+        const uint32_t qh = pack_bf16x2(dsv[2 * w], dsv[2 * w + 1]);
+        bpw[w] = ph;
+        bpw[2 + w] = pack_bf16x2(pv[2 * w] - __uint_as_float(ph << 16), pv[2 * w + 1] - __uint_as_float(ph & 0xFFFF0000u));
+        bdw[w] = qh;
+        bdw[2 + w] = pack_bf16x2(dsv[2 * w] - __uint_as_float(qh << 16), dsv[2 * w + 1] - __uint_as_float(qh & 0xFFFF0000u));
+      }
+      const bf16x8_t bpv = __builtin_bit_cast(bf16x8_t, make_uint4(bpw[0], bpw[1], bpw[2], bpw[3]));
+      const bf16x8_t bds = __builtin_bit_cast(bf16x8_t, make_uint4(bdw[0], bdw[1], bdw[2], bdw[3]));
+#pragma unroll
+      for (int dd = 0; dd < DT; ++dd) {
+        accv[dd] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            __builtin_bit_cast(bf16x8_t, make_uint4(ad[dd].x, ad[dd].y, ad[dd].x, ad[dd].y)), bpv, accv[dd], 0, 0, 0);
+        acck[dd] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            __builtin_bit_cast(bf16x8_t, make_uint4(aq[dd].x, aq[dd].y, aq[dd].x, aq[dd].y)), bds, acck[dd], 0, 0, 0);
+      }
+    }
+    if (u + 1 < nrc) store_rows(nb);
+    if (u + 2 < nrc && tid < kBkQv) s_meta[bf][tid] = m_next;
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);
+    __syncthreads();  // chunk u + 1 staged; every wave is done with chunk u
+  }
+
+  // dV^T, dK^T tiles: lane (q4, c16) holds dims 16 dt + 4 q4 + e of key 16 t + c16
+  if (!keys_here) return;
+  const int j = s_j[16 * t + c16];
+  if (j < 0) return;
+  float* dvr = p.dv + ((bb * p.n + j) * p.h_kv + h) * p.d;
+  float* dkr = p.dk + ((bb * p.n + j) * p.h_kv + h) * p.d;
+#pragma unroll
+  for (int dd = 0; dd < DT; ++dd) {
+    const int dim0 = 16 * (DT * dh + dd) + 4 * q4;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      unsafeAtomicAdd(dvr + dim0 + e, accv[dd][e]);
+      unsafeAtomicAdd(dkr + dim0 + e, acck[dd][e] * p.inv_scale);
+    }
+  }
+}
+
 template <typename T, int GMAX>
 int launch_bwd_g(const BwdParams& p, hipStream_t st) {
   const dim3 grid(static_cast<unsigned>(ceil_div(p.rows, kBwdWaves)));
@@ -813,23 +1348,74 @@ size_t bwd_ws_bytes(int dtype, int dout_dtype, int64_t batch, int64_t n, int h_q
     return 0;
   return sizeof(float) * 4 * static_cast<size_t>(batch * n * h_q);
 }
-}  // namespace
-}  // namespace ssa
 
-extern "C" size_t ssa_sparse_attention_backward_workspace_bytes(int dtype, int dout_dtype, int64_t batch,
-                                                                int64_t n, int h_q, int h_kv, int d) {
-  return bwd_ws_bytes(dtype, dout_dtype, batch, n, h_q, h_kv, d);
+// Bucket-mode workspace after the stats: query index (offsets, postings and
+// its build scratch), item starts, a counter, rowmap, posting meta, then the
+// key bitmaps (words per row each).
+struct BucketWs {
+  int32_t* qoff;
+  int32_t* qpost;
+  void* hist;
+  int32_t* items;
+  int4* desc;
+  int32_t* ctr;
+  int32_t* rowmap;
+  int2* meta;
+  uint32_t* bits;
+  int64_t cap;  // bitmaps that fit
+};
+
+// Items (bucket, 32-key chunk) per bh at most: sum over c of ceil(|K_c| / 32).
+int64_t bucket_max_items(int64_t n, int b, int n_c) { return ceil_div(n * b, kBkKeys) + n_c; }
+
+size_t bucket_fixed_bytes(int64_t batch, int64_t n, int h_kv, int a, int b, int n_c) {
+  const int64_t bh = batch * h_kv;
+  return align_up(sizeof(int32_t) * static_cast<size_t>(bh * (n_c + 1)), 256) +
+         align_up(sizeof(int32_t) * static_cast<size_t>(bh * n * a), 256) +
+         align_up(index_ws_bytes(bh, n, n_c), 256) +
+         align_up(sizeof(int32_t) * static_cast<size_t>(bh * (n_c + 1)), 256) +
+         align_up(sizeof(int4) * static_cast<size_t>(bh * bucket_max_items(n, b, n_c)), 256) + 256 +
+         align_up(sizeof(int32_t) * static_cast<size_t>(bh * n), 256) +
+         align_up(sizeof(int2) * static_cast<size_t>(bh * n * a), 256);
 }
 
-extern "C" int ssa_sparse_attention_backward(
-    const void* q, const void* k, const void* v, int dtype, int64_t batch, int64_t n, int h_q,
-    int h_kv, int d, int64_t q_sb, int64_t q_sn, int64_t q_sh, int64_t k_sb, int64_t k_sn,
-    int64_t k_sh, int64_t v_sb, int64_t v_sn, int64_t v_sh, const void* idx, int idx_dtype,
-    int top_k, int64_t idx_sb, int64_t idx_sn, int64_t idx_sh, float scale_div, int causal,
-    const int32_t* row_order, const void* out, int out_dtype, int64_t o_sb, int64_t o_sn,
-    int64_t o_sh, const void* dout, int dout_dtype, int64_t do_sb, int64_t do_sn, int64_t do_sh,
-    float* dq, float* dk, float* dv, int32_t* error_flag, const int32_t* row_prefix, void* workspace,
-    size_t workspace_bytes, void* stream) {
+int64_t bucket_words(int64_t n) { return ceil_div(n, 32); }
+
+BucketWs carve_bucket_ws(void* base, size_t bytes, int64_t batch, int64_t n, int h_kv, int a, int b, int n_c) {
+  const int64_t bh = batch * h_kv;
+  char* c = static_cast<char*>(base);
+  BucketWs w{};
+  auto take = [&](size_t sz) {
+    char* r = c;
+    c += align_up(sz, 256);
+    return r;
+  };
+  w.qoff = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * static_cast<size_t>(bh * (n_c + 1))));
+  w.qpost = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * static_cast<size_t>(bh * n * a)));
+  w.hist = take(index_ws_bytes(bh, n, n_c));
+  w.items = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * static_cast<size_t>(bh * (n_c + 1))));
+  w.desc = reinterpret_cast<int4*>(take(sizeof(int4) * static_cast<size_t>(bh * bucket_max_items(n, b, n_c))));
+  w.ctr = reinterpret_cast<int32_t*>(take(256));
+  w.rowmap = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * static_cast<size_t>(bh * n)));
+  w.meta = reinterpret_cast<int2*>(take(sizeof(int2) * static_cast<size_t>(bh * n * a)));
+  w.bits = reinterpret_cast<uint32_t*>(c);
+  const size_t used = static_cast<size_t>(c - static_cast<char*>(base));
+  const size_t row_bytes = sizeof(uint32_t) * static_cast<size_t>(bucket_words(n));
+  w.cap = bytes > used ? static_cast<int64_t>((bytes - used) / row_bytes) : 0;
+  if (w.cap > bh * n) w.cap = bh * n;
+  return w;
+}
+
+// Checks and fills the parameters shared by both backward entry points.
+// Returns SSA_OK with `empty` set when there is nothing to compute.
+int bwd_setup(const void* q, const void* k, const void* v, int dtype, int64_t batch, int64_t n, int h_q,
+              int h_kv, int d, int64_t q_sb, int64_t q_sn, int64_t q_sh, int64_t k_sb, int64_t k_sn,
+              int64_t k_sh, int64_t v_sb, int64_t v_sn, int64_t v_sh, const void* idx, int idx_dtype,
+              int top_k, int64_t idx_sb, int64_t idx_sn, int64_t idx_sh, float scale_div, int causal,
+              const int32_t* row_order, const void* out, int out_dtype, int64_t o_sb, int64_t o_sn,
+              int64_t o_sh, const void* dout, int dout_dtype, int64_t do_sb, int64_t do_sn, int64_t do_sh,
+              float* dq, float* dk, float* dv, int32_t* error_flag, BwdParams& p, bool& empty) {
+  empty = false;
   if (dtype != SSA_DTYPE_F32 && dtype != SSA_DTYPE_BF16)
     return fail(SSA_ERR_UNSUPPORTED, "sparse_attention_backward: dtype %d not supported (f32, bf16)", dtype);
   if ((out_dtype != SSA_DTYPE_F32 && out_dtype != SSA_DTYPE_BF16) ||
@@ -847,10 +1433,13 @@ extern "C" int ssa_sparse_attention_backward(
     return fail(SSA_ERR_UNSUPPORTED, "sparse_attention_backward: head_dim %d (need 1..256)", d);
   if (!(scale_div > 0.0f) && !(scale_div < 0.0f))
     return fail(SSA_ERR_INVALID_ARGUMENT, "sparse_attention_backward: scale must be non-zero");
-  if (batch == 0 || n == 0) return SSA_OK;
+  if (batch == 0 || n == 0) {
+    empty = true;
+    return SSA_OK;
+  }
   if (!q || !k || !v || !out || !dout || !dq || !dk || !dv || (top_k > 0 && !idx))
     return fail(SSA_ERR_INVALID_ARGUMENT, "sparse_attention_backward: null pointer");
-  BwdParams p{};
+  p = BwdParams{};
   p.q = q; p.k = k; p.v = v; p.o = out; p.dout = dout;
   p.n = n; p.h_q = h_q; p.h_kv = h_kv; p.g = h_q / h_kv; p.d = d;
   p.q_sb = q_sb; p.q_sn = q_sn; p.q_sh = q_sh;
@@ -871,21 +1460,158 @@ extern "C" int ssa_sparse_attention_backward(
   p.order = row_order;
   if (p.rows >= (int64_t(1) << 31))
     return fail(SSA_ERR_UNSUPPORTED, "sparse_attention_backward: too many rows");
+  return SSA_OK;
+}
+
+// dk and dv accumulate; dq rows are written whole by the row that owns them.
+int zero_dkdv(const BwdParams& p, int64_t batch, hipStream_t st) {
+  const int64_t kv_elems = batch * p.n * p.h_kv * p.d;
+  zero_f32_kernel<<<dim3(static_cast<unsigned>(ceil_div(kv_elems, 256))), 256, 0, st>>>(p.dk, kv_elems);
+  zero_f32_kernel<<<dim3(static_cast<unsigned>(ceil_div(kv_elems, 256))), 256, 0, st>>>(p.dv, kv_elems);
+  return check_launch("zero_f32_kernel");
+}
+
+// The plain path (row kernel, then the dense-prefix pass when p.pfx is set).
+int run_bwd(BwdParams& p, int dtype, int64_t batch, const int32_t* row_prefix, void* workspace,
+            size_t workspace_bytes, int dout_dtype, hipStream_t st) {
   if (row_prefix && workspace) {
-    const size_t need = bwd_ws_bytes(dtype, dout_dtype, batch, n, h_q, h_kv, d);
+    const size_t need = bwd_ws_bytes(dtype, dout_dtype, batch, p.n, p.h_q, p.h_kv, p.d);
     if (workspace_bytes < need)
       return fail(SSA_ERR_WORKSPACE, "sparse_attention_backward: workspace %zu < %zu bytes", workspace_bytes, need);
-    if (need > 0 && dtype == SSA_DTYPE_BF16 && bwd_mfma_ok(p, q, dout)) {
+    if (need > 0 && dtype == SSA_DTYPE_BF16 && bwd_mfma_ok(p, p.q, p.dout)) {
       p.pfx = row_prefix;
       p.pstats = static_cast<float*>(workspace);
     }
   }
-  hipStream_t st = as_stream(stream);
-  // dk and dv accumulate; dq rows are written whole by the row that owns them
-  const int64_t kv_elems = batch * n * h_kv * d;
-  zero_f32_kernel<<<dim3(static_cast<unsigned>(ceil_div(kv_elems, 256))), 256, 0, st>>>(dk, kv_elems);
-  zero_f32_kernel<<<dim3(static_cast<unsigned>(ceil_div(kv_elems, 256))), 256, 0, st>>>(dv, kv_elems);
-  if (int s = check_launch("zero_f32_kernel")) return s;
+  if (int s = zero_dkdv(p, batch, st)) return s;
   if (dtype == SSA_DTYPE_BF16) return launch_bwd<uint16_t>(p, st);
   return launch_bwd<float>(p, st);
+}
+
+// Shapes the bucket path takes (else the routed entry runs the plain path).
+bool bucket_ok(const BwdParams& p, int dtype, int dout_dtype, int a, int b, int n_c) {
+  if (dtype != SSA_DTYPE_BF16 || dout_dtype != SSA_DTYPE_BF16 || !bwd_mfma_ok(p, p.q, p.dout)) return false;
+  if (a < 1 || a > kBkMaxA || b < 1 || b > kBkMaxB || n_c < 1 || n_c > 16384) return false;
+  if (p.n < p.top_k || p.top_k < 1) return false;  // rows padded past n hold key 0 repeatedly
+  const auto fits = [&](int64_t sn, int64_t sh) {
+    return sn >= 0 && sh >= 0 && ((p.n - 1) * sn + (p.g - 1) * sh) * 2 + 2 * p.d < (int64_t(1) << 31);
+  };
+  return fits(p.q_sn, p.q_sh) && fits(p.do_sn, p.do_sh) && p.n * a < (int64_t(1) << 31);
+}
+}  // namespace
+}  // namespace ssa
+
+extern "C" size_t ssa_sparse_attention_backward_workspace_bytes(int dtype, int dout_dtype, int64_t batch,
+                                                                int64_t n, int h_q, int h_kv, int d) {
+  return bwd_ws_bytes(dtype, dout_dtype, batch, n, h_q, h_kv, d);
+}
+
+extern "C" int ssa_sparse_attention_backward(
+    const void* q, const void* k, const void* v, int dtype, int64_t batch, int64_t n, int h_q,
+    int h_kv, int d, int64_t q_sb, int64_t q_sn, int64_t q_sh, int64_t k_sb, int64_t k_sn,
+    int64_t k_sh, int64_t v_sb, int64_t v_sn, int64_t v_sh, const void* idx, int idx_dtype,
+    int top_k, int64_t idx_sb, int64_t idx_sn, int64_t idx_sh, float scale_div, int causal,
+    const int32_t* row_order, const void* out, int out_dtype, int64_t o_sb, int64_t o_sn,
+    int64_t o_sh, const void* dout, int dout_dtype, int64_t do_sb, int64_t do_sn, int64_t do_sh,
+    float* dq, float* dk, float* dv, int32_t* error_flag, const int32_t* row_prefix, void* workspace,
+    size_t workspace_bytes, void* stream) {
+  BwdParams p;
+  bool empty = false;
+  if (int s = bwd_setup(q, k, v, dtype, batch, n, h_q, h_kv, d, q_sb, q_sn, q_sh, k_sb, k_sn, k_sh, v_sb, v_sn,
+                        v_sh, idx, idx_dtype, top_k, idx_sb, idx_sn, idx_sh, scale_div, causal, row_order, out,
+                        out_dtype, o_sb, o_sn, o_sh, dout, dout_dtype, do_sb, do_sn, do_sh, dq, dk, dv,
+                        error_flag, p, empty))
+    return s;
+  if (empty) return SSA_OK;
+  return run_bwd(p, dtype, batch, row_prefix, workspace, workspace_bytes, dout_dtype, as_stream(stream));
+}
+
+extern "C" size_t ssa_sparse_attention_backward_routed_workspace_bytes(int dtype, int dout_dtype, int64_t batch,
+                                                                       int64_t n, int h_q, int h_kv, int d,
+                                                                       int a, int b, int n_c, int64_t bitmap_rows) {
+  const size_t stats = bwd_ws_bytes(dtype, dout_dtype, batch, n, h_q, h_kv, d);
+  if (stats == 0 || a < 1 || a > kBkMaxA || b < 1 || b > kBkMaxB || n_c < 1 || n_c > 16384) return stats;
+  const int64_t rows = batch * h_kv * n;
+  const int64_t cap = bitmap_rows < 0 ? (rows + 1) / 2 : (bitmap_rows < rows ? bitmap_rows : rows);
+  return align_up(stats, 256) + bucket_fixed_bytes(batch, n, h_kv, a, b, n_c) +
+         sizeof(uint32_t) * static_cast<size_t>(bucket_words(n)) * static_cast<size_t>(cap);
+}
+
+extern "C" int ssa_sparse_attention_backward_routed(
+    const void* q, const void* k, const void* v, int dtype, int64_t batch, int64_t n, int h_q,
+    int h_kv, int d, int64_t q_sb, int64_t q_sn, int64_t q_sh, int64_t k_sb, int64_t k_sn,
+    int64_t k_sh, int64_t v_sb, int64_t v_sn, int64_t v_sh, const void* idx, int idx_dtype,
+    int top_k, int64_t idx_sb, int64_t idx_sn, int64_t idx_sh, float scale_div, int causal,
+    const int32_t* row_order, const void* out, int out_dtype, int64_t o_sb, int64_t o_sn,
+    int64_t o_sh, const void* dout, int dout_dtype, int64_t do_sb, int64_t do_sn, int64_t do_sh,
+    float* dq, float* dk, float* dv, int32_t* error_flag, const int32_t* row_prefix,
+    const int32_t* q_codes, int a, const int32_t* k_codes, int b, const int32_t* offsets,
+    const int32_t* postings, int n_c, int router_causal, void* workspace, size_t workspace_bytes,
+    void* stream) {
+  BwdParams p;
+  bool empty = false;
+  if (int s = bwd_setup(q, k, v, dtype, batch, n, h_q, h_kv, d, q_sb, q_sn, q_sh, k_sb, k_sn, k_sh, v_sb, v_sn,
+                        v_sh, idx, idx_dtype, top_k, idx_sb, idx_sn, idx_sh, scale_div, causal, row_order, out,
+                        out_dtype, o_sb, o_sn, o_sh, dout, dout_dtype, do_sb, do_sn, do_sh, dq, dk, dv,
+                        error_flag, p, empty))
+    return s;
+  if (empty) return SSA_OK;
+  if (!row_prefix || !q_codes || !k_codes || !offsets || !postings)
+    return fail(SSA_ERR_INVALID_ARGUMENT, "sparse_attention_backward_routed: null routing pointer");
+  hipStream_t st = as_stream(stream);
+  if (!bucket_ok(p, dtype, dout_dtype, a, b, n_c))
+    return run_bwd(p, dtype, batch, row_prefix, workspace, workspace_bytes, dout_dtype, st);
+  const size_t stats = align_up(bwd_ws_bytes(dtype, dout_dtype, batch, n, h_q, h_kv, d), 256);
+  const size_t need = stats + bucket_fixed_bytes(batch, n, h_kv, a, b, n_c);
+  if (!workspace || workspace_bytes < need)
+    return fail(SSA_ERR_WORKSPACE, "sparse_attention_backward_routed: workspace %zu < %zu bytes",
+                workspace ? workspace_bytes : size_t(0), need);
+  const int64_t bhn = batch * h_kv;
+  BucketWs w = carve_bucket_ws(static_cast<char*>(workspace) + stats, workspace_bytes - stats, batch, n, h_kv, a, b, n_c);
+  p.pfx = row_prefix;
+  p.pstats = static_cast<float*>(workspace);
+  p.rowmap = w.rowmap;
+  if (int s = zero_dkdv(p, batch, st)) return s;
+  zero_f32_kernel<<<1, 64, 0, st>>>(reinterpret_cast<float*>(w.ctr), 64);
+  // stats of a row that row_order never lists stay zero (1/sum = 0: no pair of it counts)
+  const int64_t nstats = 4 * p.rows * p.g;
+  zero_f32_kernel<<<dim3(static_cast<unsigned>(ceil_div(nstats, 256))), 256, 0, st>>>(p.pstats, nstats);
+  if (int s = check_launch("zero_f32_kernel")) return s;
+  if (int s = build_index_into(q_codes, bhn, n, a, n_c, w.qoff, w.qpost, w.hist, st)) return s;
+  bucket_items_kernel<<<dim3(static_cast<unsigned>(bhn)), 1024, 0, st>>>(offsets, n_c, w.items);
+  if (int s = check_launch("bucket_items_kernel")) return s;
+  const int64_t max_items = bucket_max_items(n, b, n_c);
+  bucket_desc_kernel<<<dim3(static_cast<unsigned>(ceil_div(max_items, 256)), static_cast<unsigned>(bhn)), 256, 0, st>>>(
+      offsets, postings, w.qoff, w.qpost, w.items, n_c, n, a, b, max_items, (causal || router_causal) ? 1 : 0, w.desc);
+  if (int s = check_launch("bucket_desc_kernel")) return s;
+  const int64_t words = bucket_words(n);
+  bucket_rowmap_kernel<<<dim3(static_cast<unsigned>(ceil_div(p.rows, 256))), 256, 0, st>>>(p, w.ctr, w.rowmap, w.bits,
+                                                                                             w.cap, words);
+  if (int s = check_launch("bucket_rowmap_kernel")) return s;
+  const int64_t entries = bhn * n * a;
+  bucket_meta_kernel<<<dim3(static_cast<unsigned>(ceil_div(entries, 256))), 256, 0, st>>>(
+      w.qpost, n * a, entries, n, row_prefix, w.rowmap, w.meta);
+  if (int s = check_launch("bucket_meta_kernel")) return s;
+  if (int s = launch_bwd<uint16_t>(p, st)) return s;  // row kernel (dq, stats, fallback rows) + prefix pass
+  BucketParams bp{};
+  bp.kpost = postings;
+  bp.kcodes = k_codes;
+  bp.desc = w.desc;
+  bp.meta = w.meta;
+  bp.qcodes = q_codes;
+  bp.bits = w.bits;
+  bp.words = words;
+  bp.max_items = max_items;
+  bp.a = a;
+  bp.b = b;
+  int gpl = 0;
+  while ((1 << gpl) < p.g) ++gpl;
+  bp.gp_log2 = gpl;
+  bp.router_causal = router_causal ? 1 : 0;
+  const dim3 grid(static_cast<unsigned>(max_items), static_cast<unsigned>(bhn));
+  if (d == 64)
+    bucket_attention_bwd_kernel<64><<<grid, kBkThreads, 0, st>>>(p, bp);
+  else
+    bucket_attention_bwd_kernel<128><<<grid, kBkThreads, 0, st>>>(p, bp);
+  return check_launch("bucket_attention_bwd_kernel");
 }

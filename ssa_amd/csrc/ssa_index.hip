@@ -14,6 +14,7 @@
 //                      share a code rank themselves by ballot (lowest lane =
 //                      lowest key first) and advance an LDS cursor per code.
 #include "ssa_common.h"
+#include "ssa_internal.h"
 
 namespace ssa {
 namespace {
@@ -214,6 +215,15 @@ size_t hist_bytes(int64_t bh, int64_t n, int n_c) {
 }
 
 }  // namespace
+
+// Library-internal: the index of codes [bh][n][b] into offsets [bh][n_c + 1]
+// and postings [bh][n * b], with index_ws_bytes(bh, n, n_c) bytes of `ws`.
+size_t index_ws_bytes(int64_t bh, int64_t n, int n_c) { return hist_bytes(bh, n, n_c); }
+int build_index_into(const int32_t* codes, int64_t bh, int64_t n, int b, int n_c, int32_t* offsets,
+                     int32_t* postings, void* ws, hipStream_t st) {
+  return run_index(codes, bh, n, b, b, n_c, offsets, postings, static_cast<int32_t*>(ws), st);
+}
+
 }  // namespace ssa
 
 using namespace ssa;

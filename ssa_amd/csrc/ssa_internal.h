@@ -20,6 +20,12 @@ int route_codes_prepped(const void* q, const void* k, int dtype, int64_t batch, 
                         const void* prep, int d_s, int n_c, int a, int b, float temperature,
                         int32_t* q_codes, int32_t* k_codes, void* ws, hipStream_t st);
 
+// The inverted index of codes [bh][n][b] (offsets [bh][n_c + 1], postings
+// [bh][n * b], as ssa_build_index) with index_ws_bytes(bh, n, n_c) bytes of ws.
+size_t index_ws_bytes(int64_t bh, int64_t n, int n_c);
+int build_index_into(const int32_t* codes, int64_t bh, int64_t n, int b, int n_c, int32_t* offsets,
+                     int32_t* postings, void* ws, hipStream_t st);
+
 // ssa_select_block with a main index of post_bh postings per (batch, kv head)
 // and an optional tail index (tail_offsets non-null) over the keys from
 // tail_key0 on, whose postings hold key - tail_key0.

@@ -68,7 +68,8 @@ def ssa_attention_bnhd(query: torch.Tensor, key: torch.Tensor, value: torch.Tens
     res = router.route(query, key, causal_mask=True, hard=True, sorted=False,
                        index_dtype=torch.int32, with_order=True, with_prefix=True)
     return sparse_exact_attention(query, key, value, res.indices, causal=causal_attention,
-                                  check_indices=False, row_order=res.order, row_prefix=res.prefix)
+                                  check_indices=False, row_order=res.order, row_prefix=res.prefix,
+                                  routing=res.routing())
 
 
 def replace_attention_forward(model=None):

@@ -10,7 +10,7 @@ every call is enqueued on the current stream without synchronising.
 from __future__ import annotations
 
 import math
-from typing import Optional, Tuple, Union
+from typing import NamedTuple, Optional, Tuple, Union
 
 import torch
 
@@ -349,16 +349,33 @@ def block_sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, bl
     return out
 
 
+class Routing(NamedTuple):
+    """What one selection was made from, for the bucket-mode backward: the
+    stage (a) codes, the stage (b) key index and whether the selection's mask
+    was causal (else none; an explicit mask has no bucket mode)."""
+    q_codes: torch.Tensor   # int32 [B, h_kv, n, a]
+    k_codes: torch.Tensor   # int32 [B, h_kv, n, b]
+    offsets: torch.Tensor   # int32 [B, h_kv, N_c + 1]
+    postings: torch.Tensor  # int32 [B, h_kv, n * b]
+    causal: bool
+
+
 def sparse_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, idx: torch.Tensor,
                               out: torch.Tensor, dout: torch.Tensor,
                               scale_div: Optional[float] = None, causal: bool = False,
                               error_flag: Optional[torch.Tensor] = None,
                               row_order: Optional[torch.Tensor] = None,
-                              row_prefix: Optional[torch.Tensor] = None
+                              row_prefix: Optional[torch.Tensor] = None,
+                              routing: Optional[Routing] = None, bitmap_rows: int = -1
                               ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """Gradients of stage (d) w.r.t. q, k, v (fp32, shapes of q, k, v), given the
     forward output ``out`` and its gradient ``dout`` (the autograd backward of
-    ssa/attention.py:64-113)."""
+    ssa/attention.py:64-113).
+
+    With ``row_prefix`` and ``routing`` (the selection that produced ``idx``,
+    n >= top_k) the candidate slots' dk and dv come from the bucket pass
+    (ssa_sparse_attention_backward_routed); ``bitmap_rows`` sizes its key
+    bitmaps for rows without filler (-1: half the rows).  Same results."""
     for name, t in (("q", q), ("k", k), ("v", v), ("indices", idx), ("out", out), ("dout", dout)):
         _check_rows(t, name)
     _lib.require_device(q, k, v, idx, out, dout)
@@ -385,15 +402,37 @@ def sparse_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         if (row_prefix.dtype != torch.int32 or tuple(row_prefix.shape) != (B, h_kv, n)
                 or not row_prefix.is_contiguous()):
             raise ValueError(f"row_prefix must be a contiguous int32 [{B}, {h_kv}, {n}] tensor")
-        ws_bytes = int(_lib.load().ssa_sparse_attention_backward_workspace_bytes(
-            _lib.elem_dtype(q), _lib.elem_dtype(dout), B, n, h_q, h_kv, d))
+        if routing is None:
+            ws_bytes = int(_lib.load().ssa_sparse_attention_backward_workspace_bytes(
+                _lib.elem_dtype(q), _lib.elem_dtype(dout), B, n, h_q, h_kv, d))
+    common = (ptr(q), ptr(k), ptr(v), _lib.elem_dtype(q), B, n, h_q,
+              h_kv, d, q.stride(0), q.stride(1), q.stride(2), k.stride(0), k.stride(1), k.stride(2),
+              v.stride(0), v.stride(1), v.stride(2), ptr(idx), _lib.index_dtype(idx), top_k,
+              idx.stride(0), idx.stride(1), idx.stride(2), float(scale_div), int(bool(causal)),
+              ptr(row_order), ptr(out), _lib.elem_dtype(out), out.stride(0), out.stride(1),
+              out.stride(2), ptr(dout), _lib.elem_dtype(dout), dout.stride(0), dout.stride(1),
+              dout.stride(2), ptr(dq), ptr(dk), ptr(dv), ptr(error_flag), ptr(row_prefix))
+    if row_prefix is not None and routing is not None:
+        qc, kc, off, post = (_contig_i32(t, name) for t, name in (
+            (routing.q_codes, "q_codes"), (routing.k_codes, "k_codes"), (routing.offsets, "offsets"),
+            (routing.postings, "postings")))
+        _lib.require_device(qc, kc, off, post)
+        a, b, n_c = qc.shape[-1], kc.shape[-1], off.shape[-1] - 1
+        if (tuple(qc.shape[:3]) != (B, h_kv, n) or tuple(kc.shape[:3]) != (B, h_kv, n)
+                or tuple(off.shape[:2]) != (B, h_kv) or tuple(post.shape) != (B, h_kv, n * b)):
+            raise ValueError("routing tensors do not match q, k (see kernels.Routing)")
+        ws_bytes = int(_lib.load().ssa_sparse_attention_backward_routed_workspace_bytes(
+            _lib.elem_dtype(q), _lib.elem_dtype(dout), B, n, h_q, h_kv, d, a, b, n_c, int(bitmap_rows)))
         ws = torch.empty(ws_bytes, device=q.device, dtype=torch.uint8) if ws_bytes else None
-    call("ssa_sparse_attention_backward", ptr(q), ptr(k), ptr(v), _lib.elem_dtype(q), B, n, h_q,
-         h_kv, d, q.stride(0), q.stride(1), q.stride(2), k.stride(0), k.stride(1), k.stride(2),
-         v.stride(0), v.stride(1), v.stride(2), ptr(idx), _lib.index_dtype(idx), top_k,
-         idx.stride(0), idx.stride(1), idx.stride(2), float(scale_div), int(bool(causal)),
-         ptr(row_order), ptr(out), _lib.elem_dtype(out), out.stride(0), out.stride(1),
-         out.stride(2), ptr(dout), _lib.elem_dtype(dout), dout.stride(0), dout.stride(1),
-         dout.stride(2), ptr(dq), ptr(dk), ptr(dv), ptr(error_flag), ptr(row_prefix), ptr(ws),
-         ws_bytes, stream_of(q))
+        call("ssa_sparse_attention_backward_routed", *common, ptr(qc), a, ptr(kc), b, ptr(off), ptr(post),
+             n_c, int(bool(routing.causal)), ptr(ws), ws_bytes, stream_of(q))
+        return dq, dk, dv
+    ws = torch.empty(ws_bytes, device=q.device, dtype=torch.uint8) if ws_bytes else None
+    call("ssa_sparse_attention_backward", *common, ptr(ws), ws_bytes, stream_of(q))
     return dq, dk, dv
+
+
+def _contig_i32(t: torch.Tensor, name: str) -> torch.Tensor:
+    if t.dtype != torch.int32:
+        raise TypeError(f"{name} must be int32")
+    return t if t.is_contiguous() else t.contiguous()

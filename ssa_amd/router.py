@@ -164,6 +164,7 @@ class CodebookRouter(nn.Module):
         out = RouteResult(q_codes, k_codes, offsets, postings, idx, stats)
         out.order = order
         out.prefix = prefix
+        out.mask_mode = mode
         out.indices_view = idx[0] if unbatched else idx
         return out
 
@@ -196,7 +197,7 @@ class RouteResult:
     indices_view is the reference-shaped view returned by forward()."""
 
     __slots__ = ("q_codes", "k_codes", "offsets", "postings", "indices", "stats", "order",
-                 "prefix", "indices_view")
+                 "prefix", "indices_view", "mask_mode")
 
     def __init__(self, q_codes, k_codes, offsets, postings, indices, stats):
         self.q_codes = q_codes
@@ -208,3 +209,12 @@ class RouteResult:
         self.order = None
         self.prefix = None
         self.indices_view = indices
+        self.mask_mode = None
+
+    def routing(self):
+        """kernels.Routing for the bucket-mode backward of attention over these
+        indices, or None (an explicit mask, or an unknown one)."""
+        if self.mask_mode not in (_lib.MASK_NONE, _lib.MASK_CAUSAL):
+            return None
+        return kernels.Routing(self.q_codes, self.k_codes, self.offsets, self.postings,
+                               self.mask_mode == _lib.MASK_CAUSAL)

@@ -159,7 +159,7 @@ class SSAAttention(nn.Module):
                                     index_dtype=torch.int32, with_order=True, with_prefix=True)
             out = sparse_exact_attention(q, k, v, res.indices, causal=self.causal_attention,
                                          check_indices=False, row_order=res.order,
-                                         row_prefix=res.prefix)
+                                         row_prefix=res.prefix, routing=res.routing())
         return self.o_proj(out.reshape(B, n, -1).to(hidden_states.dtype))
 
 
