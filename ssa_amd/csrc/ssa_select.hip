@@ -442,10 +442,69 @@ __device__ __forceinline__ void select_row(const SelParams& p, const T* __restri
 // slots hold its selected keys ascending; select_sort_kernel (one wave per
 // row) rescores them in the canonical order (rescore_row, lane l taking keys
 // l, l + 64, ...), sorts the composite keys (score desc, index asc -- unique,
-// so the order is total) with a bitonic network in the wave's LDS and writes
+// so the order is total) with the register bitonic network below and writes
 // them back; the filler after them keeps its ascending order, as in
 // select_kernel.
 constexpr int kSortMax = 1024;  // m at most this (k_eff larger: select_kernel)
+
+// Bitonic network of one wave over 64 E keys in registers (lane l holds keys
+// l E + r): exchanges between the slots of one lane run in registers, between
+// lanes through DPP (lane ^ 1, ^ 2), ds_swizzle (^ 4, ^ 8, ^ 16) or
+// ds_bpermute (^ 32).
+__device__ __forceinline__ uint32_t lane_xor(uint32_t v, int lx) {
+  switch (lx) {
+    case 1: return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0xB1, 0xF, 0xF, false));
+    case 2: return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x4E, 0xF, 0xF, false));
+    case 4: return static_cast<uint32_t>(__builtin_amdgcn_ds_swizzle(static_cast<int>(v), 0x101F));
+    case 8: return static_cast<uint32_t>(__builtin_amdgcn_ds_swizzle(static_cast<int>(v), 0x201F));
+    case 16: return static_cast<uint32_t>(__builtin_amdgcn_ds_swizzle(static_cast<int>(v), 0x401F));
+    default: return static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), lx));
+  }
+}
+
+// Descending bitonic sort of the wave's 64 E keys, key l E + r in x[r] of lane l.
+template <int E>
+__device__ __forceinline__ void wave_sort_desc(uint64_t (&x)[E], int lane) {
+#pragma unroll
+  for (int size = 2; size <= 64 * E; size <<= 1) {
+#pragma unroll
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      if (stride >= E) {  // partner: the same slot of lane ^ (stride / E)
+#pragma unroll
+        for (int r = 0; r < E; ++r) {
+          const uint32_t lo = lane_xor(static_cast<uint32_t>(x[r]), stride / E);
+          const uint32_t hi = lane_xor(static_cast<uint32_t>(x[r] >> 32), stride / E);
+          const uint64_t y = (static_cast<uint64_t>(hi) << 32) | lo;
+          const int e = lane * E + r;
+          const bool keep_max = ((e & stride) == 0) == ((e & size) == 0);
+          x[r] = keep_max ? (x[r] > y ? x[r] : y) : (x[r] < y ? x[r] : y);
+        }
+      } else {  // partner: slot r ^ stride of this lane
+#pragma unroll
+        for (int r = 0; r < E; ++r) {
+          if (r & stride) continue;
+          const int r2 = r | stride;
+          const bool desc = ((lane * E + r) & size) == 0;
+          const uint64_t a = x[r], b = x[r2];
+          const bool sw = desc ? (a < b) : (a > b);
+          x[r] = sw ? b : a;
+          x[r2] = sw ? a : b;
+        }
+      }
+    }
+  }
+}
+
+template <int E>
+__device__ __forceinline__ void sort_slots_desc(uint64_t* keys, int lane) {
+  uint64_t x[E];
+#pragma unroll
+  for (int r = 0; r < E; ++r) x[r] = keys[lane * E + r];
+  wave_sort_desc<E>(x, lane);
+#pragma unroll
+  for (int r = 0; r < E; ++r) keys[lane * E + r] = x[r];
+}
+
 
 template <typename T, int GMAX, int D>
 __global__ __launch_bounds__(64) void select_sort_kernel(SelParams p, const T* __restrict__ qg) {
@@ -464,7 +523,7 @@ __global__ __launch_bounds__(64) void select_sort_kernel(SelParams p, const T* _
   const int64_t obase = ((bb * p.n_q + r) * p.h_kv + h) * p.top_k;
   int32_t* o32 = static_cast<int32_t*>(p.out) + obase;
   int64_t* o64 = static_cast<int64_t*>(p.out) + obase;
-  int np = 2;
+  int np = 64;
   while (np < m) np <<= 1;
   for (int e = lane; e < np; e += 64) {
     uint64_t key = 0ull;  // below every real key: padding sorts last
@@ -482,22 +541,15 @@ __global__ __launch_bounds__(64) void select_sort_kernel(SelParams p, const T* _
     keys[e] = key;
   }
   __syncthreads();
-  // bitonic network over np keys by the one wave, descending overall
-  for (int size = 2; size <= np; size <<= 1) {
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      for (int t = lane; t < (np >> 1); t += 64) {
-        const int i = 2 * stride * (t / stride) + (t % stride);
-        const int jx = i + stride;
-        const uint64_t a = keys[i], b = keys[jx];
-        const bool desc = (i & size) == 0;
-        if (desc ? (a < b) : (a > b)) {
-          keys[i] = b;
-          keys[jx] = a;
-        }
-      }
-      __syncthreads();
-    }
+  // descending over np keys (np / 64 per lane, in registers)
+  switch (np >> 6) {
+    case 1: sort_slots_desc<1>(keys, lane); break;
+    case 2: sort_slots_desc<2>(keys, lane); break;
+    case 4: sort_slots_desc<4>(keys, lane); break;
+    case 8: sort_slots_desc<8>(keys, lane); break;
+    default: sort_slots_desc<16>(keys, lane); break;
   }
+  __syncthreads();
   for (int e = lane; e < m; e += 64) {
     const int32_t j = static_cast<int32_t>(key_index(keys[e]));
     if (p.out_i64) o64[e] = j;

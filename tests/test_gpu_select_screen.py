@@ -181,3 +181,33 @@ def test_select_row_order(dev, orc, sorted_, ws):
     keep[skipped] = False
     assert torch.equal(got[0], ref[0]) and torch.equal(got[1, :, 1], ref[1, :, 1])
     assert torch.equal(got[1, keep, 0], ref[1, keep, 0])
+
+
+@pytest.mark.parametrize("d,g,top_k,n,i64", [
+    (128, 4, 512, 1500, False),
+    (64, 8, 1024, 2600, True),
+    (128, 1, 100, 900, True),
+    (64, 2, 40, 700, False),
+])
+def test_select_score_order_sort_pass(dev, orc, d, g, top_k, n, i64):
+    """Score order through the workspace (index-order passes, then the per-row
+    rescore-and-sort pass: key rows in registers, a register bitonic network)
+    equals the one-block-per-row kernel bit for bit: rows of 1 to top_k
+    selected keys (every slot count per lane, 64 to 1024 sorted slots), exact
+    score ties (repeated keys), int32 and int64 indices."""
+    _say(f"select score order d={d} g={g} top_k={top_k} n={n} i64={i64}")
+    from ssa_amd import _lib, kernels
+
+    rng = np.random.default_rng(31)
+    k_from = np.arange(n)
+    dup = rng.choice(n, n // 5, replace=False)
+    k_from[dup] = rng.integers(0, n, n // 5)  # a fifth of the keys repeat another key
+    c = _case(orc, dev, 1, n, 2, g, d, 32, 6, 3, 37 + g, k_from=k_from)
+    args = (c["q"], c["k"], c["qc"], c["off"], c["post"], c["b"], top_k, _lib.MASK_CAUSAL)
+    dt = torch.int64 if i64 else torch.int32
+    ref, st_ref = kernels.select(*args, sorted=True, with_stats=True, use_workspace=False, index_dtype=dt)
+    got, st = kernels.select(*args, sorted=True, with_stats=True, use_workspace=True, index_dtype=dt)
+    assert torch.equal(st, st_ref)
+    C = st[..., 0]
+    assert int(C.min()) <= 1 and int((C >= top_k).sum()) > 0, "short and full rows"
+    assert torch.equal(got, ref)
