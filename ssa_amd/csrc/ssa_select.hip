@@ -227,6 +227,46 @@ __device__ __forceinline__ void rescore_row(const T* kr, const T* q0, int64_t q_
   }
 }
 
+// rescore_row for two key rows at once (the same chains, interleaved): both
+// rows' loads are in flight together and each query operand serves both.
+template <typename T, int GMAX, int D>
+__device__ __forceinline__ void rescore_rows2(const T* kr0, const T* kr1, const T* q0, int64_t q_sh, int g, int d,
+                                              float (&acc0)[GMAX], float (&acc1)[GMAX]) {
+#pragma unroll
+  for (int gg = 0; gg < GMAX; ++gg) {
+    acc0[gg] = 0.0f;
+    acc1[gg] = 0.0f;
+  }
+  constexpr int G = kRescoreLoads;
+  const int dd = (D > 0) ? D : d;
+#pragma unroll 1
+  for (int t0 = 0; t0 < dd; t0 += 8 * G) {
+    float kv0[G][8], kv1[G][8];
+#pragma unroll
+    for (int u = 0; u < G; ++u)
+      if (D > 0 || t0 + 8 * u < dd) {
+        load8(kr0 + t0 + 8 * u, kv0[u]);
+        load8(kr1 + t0 + 8 * u, kv1[u]);
+      }
+#pragma unroll
+    for (int gg = 0; gg < GMAX; ++gg) {
+      if (gg >= g) continue;
+      const T* qgp = q0 + static_cast<int64_t>(gg) * q_sh + t0;
+#pragma unroll
+      for (int u = 0; u < G; ++u) {
+        if (D == 0 && t0 + 8 * u >= dd) continue;
+        float qv[8];
+        load8(qgp + 8 * u, qv);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          acc0[gg] = fma_rn(qv[e], kv0[u][e], acc0[gg]);
+          acc1[gg] = fma_rn(qv[e], kv1[u][e], acc1[gg]);
+        }
+      }
+    }
+  }
+}
+
 // One row ((b * h_kv + h) * n + i) by the whole block.  `heavy`: the row is
 // known to have more than k_eff candidates (index order only), so the counting
 // pass is skipped.
@@ -525,20 +565,29 @@ __global__ __launch_bounds__(64) void select_sort_kernel(SelParams p, const T* _
   int64_t* o64 = static_cast<int64_t*>(p.out) + obase;
   int np = 64;
   while (np < m) np <<= 1;
-  for (int e = lane; e < np; e += 64) {
-    uint64_t key = 0ull;  // below every real key: padding sorts last
-    if (e < m) {
-      const int32_t j = p.out_i64 ? static_cast<int32_t>(o64[e]) : o32[e];
-      float acc[GMAX];
-      rescore_row<T, GMAX, D>(kbase + static_cast<int64_t>(j) * p.k_sn, q0, p.q_sh, p.g, p.d, acc);
-      float sc = acc[0] / p.score_div;
+  auto score_of = [&](const float (&acc)[GMAX]) {
+    float sc = acc[0] / p.score_div;
 #pragma unroll
-      for (int gg = 1; gg < GMAX; ++gg)
-        if (gg < p.g) sc = sc + acc[gg] / p.score_div;
-      sc = sc / static_cast<float>(p.g);
-      key = composite_key(sc, static_cast<uint32_t>(j));
+    for (int gg = 1; gg < GMAX; ++gg)
+      if (gg < p.g) sc = sc + acc[gg] / p.score_div;
+    return sc / static_cast<float>(p.g);
+  };
+  // slots e and e + 64 together; padding (0) sorts below every real key
+  for (int e = lane; e < np; e += 128) {
+    const int e2 = e + 64;
+    const int32_t j0 = e < m ? (p.out_i64 ? static_cast<int32_t>(o64[e]) : o32[e]) : -1;
+    const int32_t j1 = e2 < m ? (p.out_i64 ? static_cast<int32_t>(o64[e2]) : o32[e2]) : -1;
+    if (j0 >= 0) {
+      float acc0[GMAX], acc1[GMAX];
+      rescore_rows2<T, GMAX, D>(kbase + static_cast<int64_t>(j0) * p.k_sn,
+                                kbase + static_cast<int64_t>(j1 >= 0 ? j1 : j0) * p.k_sn, q0, p.q_sh, p.g, p.d,
+                                acc0, acc1);
+      keys[e] = composite_key(score_of(acc0), static_cast<uint32_t>(j0));
+      if (e2 < np) keys[e2] = j1 >= 0 ? composite_key(score_of(acc1), static_cast<uint32_t>(j1)) : 0ull;
+    } else {
+      keys[e] = 0ull;
+      if (e2 < np) keys[e2] = 0ull;
     }
-    keys[e] = key;
   }
   __syncthreads();
   // descending over np keys (np / 64 per lane, in registers)
