@@ -311,6 +311,12 @@ int ssa_decode_step(const void* q, const void* k, const void* v, int dtype, int6
  * row_prefix (nullable) int32 [batch][h_kv][n]: X per row as ssa_select
  *   writes it (the caller vouches that the row's indices hold [0, X) once);
  *   without it the dense pass finds X from the indices (a bitmap per row).
+ * row_stats (nullable) fp32 [batch][h_kv][n][g][2]: the bf16 matrix-core path
+ *   (d 64 / 128, g <= 8) writes each (row, query head)'s softmax reference
+ *   (the running maximum of q.k / scale_div in log2 units, 0 for a row with
+ *   no slot) and 1 / sum there; other paths leave it as it was.  Given to the
+ *   backward, it saves that kernel's first pass over the slots (fill it with
+ *   NaN first: rows still NaN are recomputed).  No reference counterpart.
  * Limits: d a multiple of 8 in [8, 256], g <= 16. */
 int ssa_sparse_attention(const void* q, const void* k, const void* v, int dtype, int64_t batch,
                          int64_t n, int h_q, int h_kv, int d, int64_t q_sb, int64_t q_sn,
@@ -319,7 +325,7 @@ int ssa_sparse_attention(const void* q, const void* k, const void* v, int dtype,
                          int64_t idx_sb, int64_t idx_sn, int64_t idx_sh, float scale_div,
                          int causal, const int32_t* row_order, const int32_t* row_prefix,
                          void* out, int out_dtype, int64_t o_sb, int64_t o_sn,
-                         int64_t o_sh, int32_t* error_flag, void* workspace,
+                         int64_t o_sh, int32_t* error_flag, float* row_stats, void* workspace,
                          size_t workspace_bytes, void* stream);
 
 /* Bytes of ssa_sparse_attention's optional workspace for n_q query rows; 0
@@ -339,7 +345,7 @@ int ssa_sparse_attention_block(
     int64_t k_sn, int64_t k_sh, int64_t v_sb, int64_t v_sn, int64_t v_sh, const void* idx,
     int idx_dtype, int top_k, int64_t idx_sb, int64_t idx_sn, int64_t idx_sh, float scale_div,
     int causal, const int32_t* row_order, const int32_t* row_prefix, void* out, int out_dtype,
-    int64_t o_sb, int64_t o_sn, int64_t o_sh, int32_t* error_flag, void* workspace,
+    int64_t o_sb, int64_t o_sn, int64_t o_sh, int32_t* error_flag, float* row_stats, void* workspace,
     size_t workspace_bytes, void* stream);
 
 /* Key blocks per query block: replaces convert_indices_to_blocks
@@ -391,7 +397,10 @@ int ssa_block_sparse_attention(const void* q, const void* k, const void* v, int 
  *   dq fp32 [batch][n][h_q][d] contiguous: each processed row writes its own
  *      (a row never listed in row_order is not written);
  *   dk, dv fp32 [batch][n][h_kv][d] contiguous: zeroed, then accumulated.
- * Arithmetic is fp32 (softmax recomputed from q and k).
+ * Arithmetic is fp32 (softmax recomputed from q and k).  row_stats
+ * (nullable): the forward's per-row softmax stats (ssa_sparse_attention's
+ * row_stats); the matrix-core path then skips its first pass for every row
+ * whose entry is not NaN.
  * Limits: d in [1, 256], g <= 16. */
 int ssa_sparse_attention_backward(
     const void* q, const void* k, const void* v, int dtype, int64_t batch, int64_t n, int h_q,
@@ -400,8 +409,8 @@ int ssa_sparse_attention_backward(
     int top_k, int64_t idx_sb, int64_t idx_sn, int64_t idx_sh, float scale_div, int causal,
     const int32_t* row_order, const void* out, int out_dtype, int64_t o_sb, int64_t o_sn,
     int64_t o_sh, const void* dout, int dout_dtype, int64_t do_sb, int64_t do_sn, int64_t do_sh,
-    float* dq, float* dk, float* dv, int32_t* error_flag, const int32_t* row_prefix, void* workspace,
-    size_t workspace_bytes, void* stream);
+    float* dq, float* dk, float* dv, int32_t* error_flag, const int32_t* row_prefix,
+    const float* row_stats, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Bytes of ssa_sparse_attention_backward's optional workspace (4 floats per
  * (row, query head)); 0 where the dense-prefix pass does not run (fp32 q/k/v
@@ -439,7 +448,8 @@ int ssa_sparse_attention_backward_routed(
     const int32_t* row_order, const void* out, int out_dtype, int64_t o_sb, int64_t o_sn,
     int64_t o_sh, const void* dout, int dout_dtype, int64_t do_sb, int64_t do_sn, int64_t do_sh,
     float* dq, float* dk, float* dv, int32_t* error_flag, const int32_t* row_prefix,
-    const int32_t* q_codes, int a, const int32_t* k_codes, int b, const int32_t* offsets,
+    const float* row_stats, const int32_t* q_codes, int a, const int32_t* k_codes, int b,
+    const int32_t* offsets,
     const int32_t* postings, int n_c, int router_causal, void* workspace, size_t workspace_bytes,
     void* stream);
 

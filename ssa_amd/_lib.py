@@ -94,13 +94,13 @@ SIGNATURES = {
         _int,
         [_vp, _vp, _vp, _int, _i64, _i64, _int, _int, _int, _i64, _i64, _i64, _i64, _i64, _i64,
          _i64, _i64, _i64, _vp, _int, _int, _i64, _i64, _i64, _flt, _int, _vp, _vp, _vp, _int,
-         _i64, _i64, _i64, _vp, _vp, _sz, _vp]),
+         _i64, _i64, _i64, _vp, _vp, _vp, _sz, _vp]),
     "ssa_sparse_attention_workspace_bytes": (_sz, [_int, _i64, _i64, _int, _int, _int, _int]),
     "ssa_sparse_attention_block": (
         _int,
         [_vp, _vp, _vp, _int, _i64, _i64, _i64, _i64, _int, _int, _int, _i64, _i64, _i64, _i64,
          _i64, _i64, _i64, _i64, _i64, _vp, _int, _int, _i64, _i64, _i64, _flt, _int, _vp, _vp,
-         _vp, _int, _i64, _i64, _i64, _vp, _vp, _sz, _vp]),
+         _vp, _int, _i64, _i64, _i64, _vp, _vp, _vp, _sz, _vp]),
     "ssa_block_indices": (
         _int,
         [_vp, _int, _i64, _i64, _int, _int, _i64, _i64, _i64, _int, _int, _vp, _int, _i64, _i64,
@@ -114,13 +114,13 @@ SIGNATURES = {
         _int,
         [_vp, _vp, _vp, _int, _i64, _i64, _int, _int, _int, _i64, _i64, _i64, _i64, _i64, _i64,
          _i64, _i64, _i64, _vp, _int, _int, _i64, _i64, _i64, _flt, _int, _vp, _vp, _int, _i64,
-         _i64, _i64, _vp, _int, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+         _i64, _i64, _vp, _int, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "ssa_sparse_attention_backward_workspace_bytes": (_sz, [_int, _int, _i64, _i64, _int, _int, _int]),
     "ssa_sparse_attention_backward_routed": (
         _int,
         [_vp, _vp, _vp, _int, _i64, _i64, _int, _int, _int, _i64, _i64, _i64, _i64, _i64, _i64,
          _i64, _i64, _i64, _vp, _int, _int, _i64, _i64, _i64, _flt, _int, _vp, _vp, _int, _i64,
-         _i64, _i64, _vp, _int, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp,
+         _i64, _i64, _vp, _int, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp,
          _vp, _int, _vp, _int, _vp, _vp, _int, _int, _vp, _sz, _vp]),
     "ssa_sparse_attention_backward_routed_workspace_bytes": (
         _sz, [_int, _int, _i64, _i64, _int, _int, _int, _int, _int, _int, _i64]),

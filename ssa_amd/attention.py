@@ -25,14 +25,18 @@ class _SparseAttention(torch.autograd.Function):
         # The backward's D = dO . o uses an fp32 copy of the output: a bf16 one
         # would carry its 2^-9 rounding into every gradient.
         out32 = torch.empty(q.shape, device=q.device, dtype=torch.float32)
+        # the forward's softmax stats spare the backward its first pass (bf16 path)
+        stats = kernels.row_stats_buffer(q, k.shape[2]) if q.dtype == torch.bfloat16 else None
         kernels.sparse_attention(q, k, v, indices, scale, causal, out=out32, error_flag=flag,
-                                 row_order=row_order, row_prefix=row_prefix)
+                                 row_order=row_order, row_prefix=row_prefix, row_stats=stats)
         ctx.scale, ctx.causal = scale, causal
         ctx.has_order = row_order is not None
         ctx.has_prefix = row_prefix is not None
+        ctx.has_stats = stats is not None
         ctx.routing_causal = None if routing is None else bool(routing.causal)
         saved = ([q, k, v, indices, out32] + ([row_order] if row_order is not None else [])
                  + ([row_prefix] if row_prefix is not None else [])
+                 + ([stats] if stats is not None else [])
                  + (list(routing[:4]) if routing is not None else []))
         ctx.save_for_backward(*saved)
         return out32 if q.dtype == torch.float32 else out32.to(q.dtype)
@@ -42,12 +46,13 @@ class _SparseAttention(torch.autograd.Function):
         q, k, v, indices, out, *rest = ctx.saved_tensors
         order = rest.pop(0) if ctx.has_order else None
         prefix = rest.pop(0) if ctx.has_prefix else None
+        stats = rest.pop(0) if ctx.has_stats else None
         routing = kernels.Routing(*rest[:4], ctx.routing_causal) if ctx.routing_causal is not None else None
         if dout.stride(-1) != 1:
             dout = dout.contiguous()
         dq, dk, dv = kernels.sparse_attention_backward(q, k, v, indices, out, dout, ctx.scale,
                                                        ctx.causal, row_order=order, row_prefix=prefix,
-                                                       routing=routing)
+                                                       routing=routing, row_stats=stats)
         return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), None, None, None, None, None, None, None
 
 

@@ -69,6 +69,10 @@ struct AttParams {
   int32_t* pfx_x;
   float* pfx_part;
   int pfx_given;  // pfx_x came from the selection (row_prefix): the prefix kernel only reads it
+  // Nullable [B*h_kv*n_q][g][2]: the matrix-core row kernel leaves each (row,
+  // head)'s softmax reference (running max, log2 units) and 1 / sum here, for
+  // the backward; other paths write nothing.
+  float* stats;
 };
 
 // Key of slot `slot` given the index entry loaded for it: -1 = none (block mode:
@@ -755,6 +759,11 @@ __device__ __forceinline__ void attend_row_mfma(const AttParams& p, const AttRow
   }
   if (!row_ok || !hi_row) return;
   const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+  if (p.stats && q4 == 0) {
+    float* sp = p.stats + ((bh * p.n_q + qr) * p.g + c16) * 2;
+    sp[0] = (m_run == -INFINITY) ? 0.0f : m_run;
+    sp[1] = inv;
+  }
   const int64_t ob = bb * p.o_sb + qr * p.o_sn + static_cast<int64_t>(h * p.g + c16) * p.o_sh + 4 * q4;
   if (p.out_bf16) {
     uint16_t* dst = static_cast<uint16_t*>(p.out) + ob;
@@ -1156,7 +1165,7 @@ int attention_entry(const void* q, const void* k, const void* v, int dtype, int6
                     int64_t idx_sh, float scale_div, int causal, const int32_t* row_order, void* out,
                     int out_dtype, int64_t o_sb, int64_t o_sn, int64_t o_sh, int32_t* error_flag,
                     void* stream, int blk_log2, int64_t nbk, void* workspace, size_t workspace_bytes,
-                    const int32_t* row_prefix) {
+                    const int32_t* row_prefix, float* row_stats) {
   if (n_q < 0 || q_pos0 < 0 || q_pos0 + n_q > n)
     return fail(SSA_ERR_INVALID_ARGUMENT, "sparse_attention: query rows [%lld, %lld) outside the %lld keys",
                 static_cast<long long>(q_pos0), static_cast<long long>(q_pos0 + n_q),
@@ -1234,6 +1243,7 @@ int attention_entry(const void* q, const void* k, const void* v, int dtype, int6
                                             align_up(sizeof(int32_t) * static_cast<size_t>(p.rows), 256));
     }
   }
+  if (blk_log2 == 0) p.stats = row_stats;
   hipStream_t st = as_stream(stream);
   if (dtype == SSA_DTYPE_BF16) return launch_att<uint16_t>(p, d, st);
   return launch_att<float>(p, d, st);
@@ -1246,12 +1256,12 @@ extern "C" int ssa_sparse_attention_block(
     int64_t k_sn, int64_t k_sh, int64_t v_sb, int64_t v_sn, int64_t v_sh, const void* idx,
     int idx_dtype, int top_k, int64_t idx_sb, int64_t idx_sn, int64_t idx_sh, float scale_div,
     int causal, const int32_t* row_order, const int32_t* row_prefix, void* out, int out_dtype,
-    int64_t o_sb, int64_t o_sn, int64_t o_sh, int32_t* error_flag, void* workspace, size_t workspace_bytes,
-    void* stream) {
+    int64_t o_sb, int64_t o_sn, int64_t o_sh, int32_t* error_flag, float* row_stats, void* workspace,
+    size_t workspace_bytes, void* stream) {
   return attention_entry(q, k, v, dtype, batch, n, n_q, q_pos0, h_q, h_kv, d, q_sb, q_sn, q_sh, k_sb, k_sn,
                          k_sh, v_sb, v_sn, v_sh, idx, idx_dtype, top_k, idx_sb, idx_sn, idx_sh, scale_div,
                          causal, row_order, out, out_dtype, o_sb, o_sn, o_sh, error_flag, stream, 0, 0,
-                         workspace, workspace_bytes, row_prefix);
+                         workspace, workspace_bytes, row_prefix, row_stats);
 }
 
 extern "C" size_t ssa_sparse_attention_workspace_bytes(int dtype, int64_t batch, int64_t n_q, int h_q,
@@ -1286,9 +1296,9 @@ extern "C" int ssa_sparse_attention(const void* q, const void* k, const void* v,
                                     float scale_div, int causal, const int32_t* row_order,
                                     const int32_t* row_prefix, void* out, int out_dtype,
                                     int64_t o_sb, int64_t o_sn, int64_t o_sh, int32_t* error_flag,
-                                    void* workspace, size_t workspace_bytes, void* stream) {
+                                    float* row_stats, void* workspace, size_t workspace_bytes, void* stream) {
   return attention_entry(q, k, v, dtype, batch, n, n, 0, h_q, h_kv, d, q_sb, q_sn, q_sh, k_sb, k_sn, k_sh,
                          v_sb, v_sn, v_sh, idx, idx_dtype, top_k, idx_sb, idx_sn, idx_sh, scale_div, causal,
                          row_order, out, out_dtype, o_sb, o_sn, o_sh, error_flag, stream, 0, 0, workspace,
-                         workspace_bytes, row_prefix);
+                         workspace_bytes, row_prefix, row_stats);
 }

@@ -61,6 +61,9 @@ struct BwdParams {
   // come from bucket_attention_bwd_kernel, so the row kernel adds them only
   // for rows marked -1 here (rows without filler that got no key bitmap).
   const int32_t* rowmap;
+  // Nullable [rows][g][2]: the forward's softmax reference and 1 / sum per
+  // (row, head); a row whose entry is not NaN skips the row kernel's pass 1.
+  const float* stats_in;
 };
 
 __device__ __forceinline__ float ld_any(const void* p, int64_t off, int is_bf16) {
@@ -335,9 +338,12 @@ __global__ __launch_bounds__(64 * kBwMfWaves, 2) void sparse_attention_bwd_mfma_
   auto valid = [&](uint64_t okb, int x) { return ((okb >> (4 * q4 + 16 * (x >> 2) + (x & 3))) & 1ull) != 0; };
   const int nchunks = (p.top_k + kMfChunk - 1) / kMfChunk;
 
-  // ---- pass 1: running max (log2 domain) and sum per head over the row's slots
+  // ---- pass 1: running max (log2 domain) and sum per head over the row's
+  // slots, unless the forward left them (a NaN entry: it did not)
   float m_run = -INFINITY, l_run = 0.0f;
-  {
+  const float* fst = p.stats_in ? p.stats_in + (bh * p.n + i) * g * 2 : nullptr;
+  const bool have_st = fst != nullptr && !__builtin_isnan(fst[0]);
+  if (!have_st) {
     int jn = nchunks > 0 ? load_idx(0) : -1;
     uint64_t okn = __ballot(chunk_ok(jn));
     if (nchunks > 0) row_issue<D>(krs, kl, chunk_ok(jn) ? jn : -1, lane, ksn2, seg16);
@@ -378,8 +384,12 @@ __global__ __launch_bounds__(64 * kBwMfWaves, 2) void sparse_attention_bwd_mfma_
   }
   float l_tot = l_run + __shfl_xor(l_run, 16);
   l_tot += __shfl_xor(l_tot, 32);
-  const float inv_l = (l_tot > 0.0f && col_ok) ? 1.0f / l_tot : 0.0f;  // 0: no slot, or an unused column
-  const float mref = (m_run == -INFINITY) ? 0.0f : m_run;
+  float inv_l = (l_tot > 0.0f && col_ok) ? 1.0f / l_tot : 0.0f;  // 0: no slot, or an unused column
+  float mref = (m_run == -INFINITY) ? 0.0f : m_run;
+  if (have_st) {
+    mref = col_ok ? fst[2 * c16] : 0.0f;
+    inv_l = col_ok ? fst[2 * c16 + 1] : 0.0f;
+  }
   // the prefix keys [0, X) go to prefix_attention_bwd_kernel, which needs the
   // row's softmax reference, 1/sum and D
   const int xpre = p.pfx ? p.pfx[bh * p.n + i] : 0;
@@ -1172,12 +1182,9 @@ __global__ __launch_bounds__(kBkThreads, 2) void bucket_attention_bwd_kernel(Bwd
   const int t = wave & 1, dh = wave >> 1;
   const bool keys_here = 16 * t < nk;
   const int kswz = mf_swz<D>(16 * t + c16);
-  bf16x8_t kf[KB], vf[KB];
-#pragma unroll
-  for (int kb = 0; kb < KB; ++kb) {
-    kf[kb] = *(lds_bf16x8_ptr)(kvs[0] + (16 * t + c16) * S::ROW + (((kb * 4 + q4) ^ kswz) << 4));
-    vf[kb] = *(lds_bf16x8_ptr)(kvs[1] + (16 * t + c16) * S::ROW + (((kb * 4 + q4) ^ kswz) << 4));
-  }
+  // K / V fragments of the wave's keys, read from kvs at each use (not held in registers)
+  const unsigned char* krow = kvs[0] + (16 * t + c16) * S::ROW;
+  const unsigned char* vrow = kvs[1] + (16 * t + c16) * S::ROW;
   const int qswz = mf_swz<D>(c16);
   floatx4_t accv[DT], acck[DT];
 #pragma unroll
@@ -1230,8 +1237,10 @@ __global__ __launch_bounds__(kBkThreads, 2) void bucket_attention_bwd_kernel(Bwd
       floatx4_t sv = {0.f, 0.f, 0.f, 0.f}, dv = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
-        sv = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[kb], kf[kb], sv, 0, 0, 0);
-        dv = __builtin_amdgcn_mfma_f32_16x16x32_bf16(da[kb], vf[kb], dv, 0, 0, 0);
+        const bf16x8_t kf = *(lds_bf16x8_ptr)(krow + (((kb * 4 + q4) ^ kswz) << 4));
+        const bf16x8_t vf = *(lds_bf16x8_ptr)(vrow + (((kb * 4 + q4) ^ kswz) << 4));
+        sv = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[kb], kf, sv, 0, 0, 0);
+        dv = __builtin_amdgcn_mfma_f32_16x16x32_bf16(da[kb], vf, dv, 0, 0, 0);
       }
       // lane (q4, c16): query vectors 4 q4 + e against key 16 t + c16
       float pv[4], dsv[4];
@@ -1513,8 +1522,8 @@ extern "C" int ssa_sparse_attention_backward(
     int top_k, int64_t idx_sb, int64_t idx_sn, int64_t idx_sh, float scale_div, int causal,
     const int32_t* row_order, const void* out, int out_dtype, int64_t o_sb, int64_t o_sn,
     int64_t o_sh, const void* dout, int dout_dtype, int64_t do_sb, int64_t do_sn, int64_t do_sh,
-    float* dq, float* dk, float* dv, int32_t* error_flag, const int32_t* row_prefix, void* workspace,
-    size_t workspace_bytes, void* stream) {
+    float* dq, float* dk, float* dv, int32_t* error_flag, const int32_t* row_prefix,
+    const float* row_stats, void* workspace, size_t workspace_bytes, void* stream) {
   BwdParams p;
   bool empty = false;
   if (int s = bwd_setup(q, k, v, dtype, batch, n, h_q, h_kv, d, q_sb, q_sn, q_sh, k_sb, k_sn, k_sh, v_sb, v_sn,
@@ -1523,6 +1532,7 @@ extern "C" int ssa_sparse_attention_backward(
                         error_flag, p, empty))
     return s;
   if (empty) return SSA_OK;
+  p.stats_in = row_stats;
   return run_bwd(p, dtype, batch, row_prefix, workspace, workspace_bytes, dout_dtype, as_stream(stream));
 }
 
@@ -1545,9 +1555,9 @@ extern "C" int ssa_sparse_attention_backward_routed(
     const int32_t* row_order, const void* out, int out_dtype, int64_t o_sb, int64_t o_sn,
     int64_t o_sh, const void* dout, int dout_dtype, int64_t do_sb, int64_t do_sn, int64_t do_sh,
     float* dq, float* dk, float* dv, int32_t* error_flag, const int32_t* row_prefix,
-    const int32_t* q_codes, int a, const int32_t* k_codes, int b, const int32_t* offsets,
-    const int32_t* postings, int n_c, int router_causal, void* workspace, size_t workspace_bytes,
-    void* stream) {
+    const float* row_stats, const int32_t* q_codes, int a, const int32_t* k_codes, int b,
+    const int32_t* offsets, const int32_t* postings, int n_c, int router_causal, void* workspace,
+    size_t workspace_bytes, void* stream) {
   BwdParams p;
   bool empty = false;
   if (int s = bwd_setup(q, k, v, dtype, batch, n, h_q, h_kv, d, q_sb, q_sn, q_sh, k_sb, k_sn, k_sh, v_sb, v_sn,
@@ -1556,6 +1566,7 @@ extern "C" int ssa_sparse_attention_backward_routed(
                         error_flag, p, empty))
     return s;
   if (empty) return SSA_OK;
+  p.stats_in = row_stats;
   if (!row_prefix || !q_codes || !k_codes || !offsets || !postings)
     return fail(SSA_ERR_INVALID_ARGUMENT, "sparse_attention_backward_routed: null routing pointer");
   hipStream_t st = as_stream(stream);

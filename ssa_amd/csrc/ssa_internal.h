@@ -50,6 +50,7 @@ int attention_entry(const void* q, const void* k, const void* v, int dtype, int6
                     int64_t idx_sh, float scale_div, int causal, const int32_t* row_order, void* out,
                     int out_dtype, int64_t o_sb, int64_t o_sn, int64_t o_sh, int32_t* error_flag,
                     void* stream, int blk_log2, int64_t nbk, void* workspace = nullptr,
-                    size_t workspace_bytes = 0, const int32_t* row_prefix = nullptr);
+                    size_t workspace_bytes = 0, const int32_t* row_prefix = nullptr,
+                    float* row_stats = nullptr);
 
 }  // namespace ssa

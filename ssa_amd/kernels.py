@@ -247,7 +247,8 @@ def sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, idx: tor
                      error_flag: Optional[torch.Tensor] = None,
                      row_order: Optional[torch.Tensor] = None,
                      q_pos0: Optional[int] = None, dense_prefix: bool = True,
-                     row_prefix: Optional[torch.Tensor] = None) -> torch.Tensor:
+                     row_prefix: Optional[torch.Tensor] = None,
+                     row_stats: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Stage (d): gathered exact attention, [B, n_q, h_q, d] in q's dtype (ssa/attention.py:12-115).
 
     ``row_order`` (int32 [B, h_kv, n_q], a permutation of 0..n_q-1 per head) only
@@ -289,14 +290,33 @@ def sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, idx: tor
         if (row_prefix.dtype != torch.int32 or tuple(row_prefix.shape) != (B, h_kv, n_q)
                 or not row_prefix.is_contiguous()):
             raise ValueError(f"row_prefix must be a contiguous int32 [{B}, {h_kv}, {n_q}] tensor")
+    _check_stats(row_stats, B, h_kv, n_q, h_q)
     call("ssa_sparse_attention_block", ptr(q), ptr(k), ptr(v), _lib.elem_dtype(q), B, n, n_q, q_pos0,
          h_q, h_kv, d,
          q.stride(0), q.stride(1), q.stride(2), k.stride(0), k.stride(1), k.stride(2),
          v.stride(0), v.stride(1), v.stride(2), ptr(idx), _lib.index_dtype(idx), top_k,
          idx.stride(0), idx.stride(1), idx.stride(2), float(scale_div), int(bool(causal)),
          ptr(row_order), ptr(row_prefix), ptr(out), _lib.elem_dtype(out), out.stride(0), out.stride(1),
-         out.stride(2), ptr(error_flag), ptr(ws), ws_bytes, stream_of(q))
+         out.stride(2), ptr(error_flag), ptr(row_stats), ptr(ws), ws_bytes, stream_of(q))
     return out
+
+
+def _check_stats(row_stats, B, h_kv, n, h_q):
+    if row_stats is None:
+        return
+    _lib.require_device(row_stats)
+    if (row_stats.dtype != torch.float32 or tuple(row_stats.shape) != (B, h_kv, n, h_q // h_kv, 2)
+            or not row_stats.is_contiguous()):
+        raise ValueError(f"row_stats must be a contiguous fp32 [{B}, {h_kv}, {n}, {h_q // h_kv}, 2] tensor")
+
+
+def row_stats_buffer(q: torch.Tensor, h_kv: int) -> torch.Tensor:
+    """NaN-filled fp32 [B, h_kv, n, g, 2] for sparse_attention(row_stats=...):
+    the matrix-core forward writes each (row, head)'s softmax reference and
+    1 / sum, which sparse_attention_backward(row_stats=...) then reuses; entries
+    left NaN (other paths) are recomputed by the backward."""
+    B, n, h_q = q.shape[0], q.shape[1], q.shape[2]
+    return torch.full((B, h_kv, n, h_q // h_kv, 2), float("nan"), device=q.device, dtype=torch.float32)
 
 
 def block_indices(idx: torch.Tensor, block_size: int, n_k_blocks: Optional[int] = None,
@@ -366,7 +386,8 @@ def sparse_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                               error_flag: Optional[torch.Tensor] = None,
                               row_order: Optional[torch.Tensor] = None,
                               row_prefix: Optional[torch.Tensor] = None,
-                              routing: Optional[Routing] = None, bitmap_rows: int = -1
+                              routing: Optional[Routing] = None, bitmap_rows: int = -1,
+                              row_stats: Optional[torch.Tensor] = None
                               ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """Gradients of stage (d) w.r.t. q, k, v (fp32, shapes of q, k, v), given the
     forward output ``out`` and its gradient ``dout`` (the autograd backward of
@@ -375,7 +396,9 @@ def sparse_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     With ``row_prefix`` and ``routing`` (the selection that produced ``idx``,
     n >= top_k) the candidate slots' dk and dv come from the bucket pass
     (ssa_sparse_attention_backward_routed); ``bitmap_rows`` sizes its key
-    bitmaps for rows without filler (-1: half the rows).  Same results."""
+    bitmaps for rows without filler (-1: half the rows).  ``row_stats``
+    (``row_stats_buffer`` filled by the forward) saves the row kernel's first
+    pass for the rows it covers.  Same results."""
     for name, t in (("q", q), ("k", k), ("v", v), ("indices", idx), ("out", out), ("dout", dout)):
         _check_rows(t, name)
     _lib.require_device(q, k, v, idx, out, dout)
@@ -405,13 +428,14 @@ def sparse_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         if routing is None:
             ws_bytes = int(_lib.load().ssa_sparse_attention_backward_workspace_bytes(
                 _lib.elem_dtype(q), _lib.elem_dtype(dout), B, n, h_q, h_kv, d))
+    _check_stats(row_stats, B, h_kv, n, h_q)
     common = (ptr(q), ptr(k), ptr(v), _lib.elem_dtype(q), B, n, h_q,
               h_kv, d, q.stride(0), q.stride(1), q.stride(2), k.stride(0), k.stride(1), k.stride(2),
               v.stride(0), v.stride(1), v.stride(2), ptr(idx), _lib.index_dtype(idx), top_k,
               idx.stride(0), idx.stride(1), idx.stride(2), float(scale_div), int(bool(causal)),
               ptr(row_order), ptr(out), _lib.elem_dtype(out), out.stride(0), out.stride(1),
               out.stride(2), ptr(dout), _lib.elem_dtype(dout), dout.stride(0), dout.stride(1),
-              dout.stride(2), ptr(dq), ptr(dk), ptr(dv), ptr(error_flag), ptr(row_prefix))
+              dout.stride(2), ptr(dq), ptr(dk), ptr(dv), ptr(error_flag), ptr(row_prefix), ptr(row_stats))
     if row_prefix is not None and routing is not None:
         qc, kc, off, post = (_contig_i32(t, name) for t, name in (
             (routing.q_codes, "q_codes"), (routing.k_codes, "k_codes"), (routing.offsets, "offsets"),

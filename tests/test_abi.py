@@ -174,8 +174,8 @@ def _attention(L, **kw):
              idx_dtype=_lib.INDEX_I64, top_k=512, idx_sb=1024 * 8 * 512, idx_sn=8 * 512,
              idx_sh=512, scale_div=11.3137, causal=1, row_order=NULL, row_prefix=NULL, out=FAKE,
              out_dtype=_lib.DTYPE_BF16,
-             o_sb=1024 * 32 * 128, o_sn=32 * 128, o_sh=128, error_flag=NULL, workspace=NULL,
-             workspace_bytes=0, stream=NULL)
+             o_sb=1024 * 32 * 128, o_sn=32 * 128, o_sh=128, error_flag=NULL, row_stats=NULL,
+             workspace=NULL, workspace_bytes=0, stream=NULL)
     a.update(kw)
     st = L.ssa_sparse_attention(*a.values())
     return st, (L.ssa_last_error() or b"").decode()
@@ -283,7 +283,7 @@ def test_block_entry_points_reject_rows_past_the_keys(L):
     null = ctypes.c_void_p(0)
     st = L.ssa_sparse_attention_block(null, null, null, 0, 1, 32, 4, 30, 4, 2, 64, 0, 256, 64, 0, 128,
                                       64, 0, 128, 64, null, 0, 8, 0, 16, 8, 8.0, 1, null, null, null,
-                                      0, 0, 256, 64, null, null, 0, null)
+                                      0, 0, 256, 64, null, null, null, 0, null)
     assert st == _lib.SSA_ERR_INVALID_ARGUMENT
     assert b"outside" in L.ssa_last_error()
     st = L.ssa_select_block(null, null, 0, 1, 32, 4, -1, 4, 2, 64, 0, 256, 64, 0, 128, 64, null, 8,

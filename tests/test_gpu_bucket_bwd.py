@@ -130,3 +130,47 @@ def test_sparse_exact_attention_routing_autograd(dev):
     for name, got, ref in zip(("dq", "dk", "dv"), grads[0], grads[1]):
         # bf16 gradients: the two fp32 sums round to bf16 independently
         _close(name, got, ref, rel=1e-2)
+
+
+@pytest.mark.parametrize("causal,routed", [(True, True), (False, False), (True, False)])
+def test_backward_with_forward_row_stats(dev, causal, routed):
+    """The forward's row stats (softmax reference in log2 units and 1 / sum per
+    row and head) match a float64 recomputation from the selected slots; the
+    backward given them (its first pass skipped, NaN rows recomputed) equals the
+    backward without them."""
+    from ssa_amd import kernels
+
+    print(f"row stats causal={causal} routed={routed}", flush=True)
+    n, h_q, h_kv, d, n_c, a, b, top_k = 1200, 8, 2, 128, 128, 8, 4, 96
+    q, k, v, idx, st, pfx, routing = _pipeline(dev, 1, n, h_q, h_kv, d, n_c, a, b, top_k, True, False,
+                                               torch.int32, 750)
+    stats = kernels.row_stats_buffer(q, h_kv)
+    out32 = torch.empty(q.shape, device=dev, dtype=torch.float32)
+    kernels.sparse_attention(q, k, v, idx, None, causal, out=out32, row_prefix=pfx, row_stats=stats)
+    assert not bool(torch.isnan(stats).any()), "the matrix-core forward writes every row"
+    # float64 recomputation on sampled rows
+    g = h_q // h_kv
+    rows = torch.tensor([0, 1, 5, 97, 400, 777, n - 1])
+    scale_log2 = 1.4426950408889634 / (d ** 0.5)
+    qd, kd, idc = q[0].double().cpu(), k[0].double().cpu(), idx[0].cpu().long()
+    for i in rows.tolist():
+        for h in range(h_kv):
+            keys = idc[i, h]
+            if causal:
+                keys = keys[keys <= i]
+            s = (qd[i, h * g:(h + 1) * g] @ kd[keys, h].T) * scale_log2  # [g, slots]
+            m = s.max(-1).values
+            inv = 1.0 / torch.exp2(s - m[:, None]).sum(-1)
+            got = stats[0, h, i].double().cpu()
+            torch.testing.assert_close(got[:, 0], m, rtol=1e-5, atol=1e-5)
+            torch.testing.assert_close(got[:, 1], inv, rtol=1e-5, atol=1e-9)
+    dout = randn(tuple(q.shape), 751, torch.float32).to(torch.bfloat16).to(dev)
+    kw = dict(row_prefix=pfx, routing=routing if routed else None)
+    ref = kernels.sparse_attention_backward(q, k, v, idx, out32, dout, None, causal, **kw)
+    got = kernels.sparse_attention_backward(q, k, v, idx, out32, dout, None, causal, row_stats=stats, **kw)
+    for name, x, y in zip(("dq", "dk", "dv"), got, ref):
+        _close(name + " with stats", x, y)
+    stats[0, 1, 300:700] = float("nan")  # these rows take the first pass again
+    got2 = kernels.sparse_attention_backward(q, k, v, idx, out32, dout, None, causal, row_stats=stats, **kw)
+    for name, x, y in zip(("dq", "dk", "dv"), got2, ref):
+        _close(name + " with NaN rows", x, y)
