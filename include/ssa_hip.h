@@ -458,8 +458,8 @@ int ssa_sparse_attention_backward_routed(
  * x n rows); ssa_sparse_attention_backward_workspace_bytes(...) where the
  * bucket pass does not run.  No reference counterpart. */
 size_t ssa_sparse_attention_backward_routed_workspace_bytes(int dtype, int dout_dtype, int64_t batch,
-                                                            int64_t n, int h_q, int h_kv, int d, int a, int b,
-                                                            int n_c, int64_t bitmap_rows);
+                                                            int64_t n, int h_q, int h_kv, int d, int top_k,
+                                                            int a, int b, int n_c, int64_t bitmap_rows);
 
 #ifdef __cplusplus
 }

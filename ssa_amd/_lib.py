@@ -123,7 +123,7 @@ SIGNATURES = {
          _i64, _i64, _vp, _int, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp,
          _vp, _int, _vp, _int, _vp, _vp, _int, _int, _vp, _sz, _vp]),
     "ssa_sparse_attention_backward_routed_workspace_bytes": (
-        _sz, [_int, _int, _i64, _i64, _int, _int, _int, _int, _int, _int, _i64]),
+        _sz, [_int, _int, _i64, _i64, _int, _int, _int, _int, _int, _int, _int, _i64]),
 }
 
 _lib = None

@@ -64,6 +64,9 @@ struct BwdParams {
   // Nullable [rows][g][2]: the forward's softmax reference and 1 / sum per
   // (row, head); a row whose entry is not NaN skips the row kernel's pass 1.
   const float* stats_in;
+  // prefix_attention_bwd_kernel adds dq only (the prefix keys' dk and dv come
+  // from bucket_attention_bwd_kernel's prefix mode)
+  int pfx_dq_only;
 };
 
 __device__ __forceinline__ float ld_any(const void* p, int64_t off, int is_bf16) {
@@ -702,6 +705,7 @@ __global__ __launch_bounds__(64 * kPbWaves, 1) void prefix_attention_bwd_kernel(
     const bf16x8_t dsb = __builtin_bit_cast(bf16x8_t, make_uint4(db[0], db[1], db[2], db[3]));
 #pragma unroll
     for (int t = 0; t < NT; ++t) dqacc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kt[t], dsb, dqacc[t], 0, 0, 0);
+    if (p.pfx_dq_only) continue;
     // P and dS of this row's heads into [key][qv]
     if (col_ok) {
 #pragma unroll
@@ -951,6 +955,83 @@ __global__ void bucket_meta_kernel(const int32_t* __restrict__ qpost, int64_t pe
   meta[e] = make_int2(i, w);
 }
 
+// Prefix mode: the keys [0, X) of the rows with filler.  Rows are indexed by
+// X (a counting sort of clamp(X, 0, top_k)), so the rows whose prefix reaches
+// past key 32 kc are one suffix of that index; an item is 32 consecutive keys
+// and up to kBkPfxRows of those rows.
+constexpr int kBkPfxRows = 256;
+
+__global__ void bucket_xcodes_kernel(const int32_t* __restrict__ pfx, int64_t rows, int top_k,
+                                     int32_t* __restrict__ xc) {
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (r < rows) xc[r] = min(max(pfx[r], 0), top_k);
+}
+
+// pitems[bh][kc] = sum over kc' < kc of ceil(R_kc' / kBkPfxRows), R_kc the rows
+// with X > 32 kc (xoff: [bh][top_k + 2]); kchunks key chunks; one block per bh.
+__global__ __launch_bounds__(1024) void prefix_items_kernel(const int32_t* __restrict__ xoff, int top_k,
+                                                            int kchunks, int32_t* __restrict__ pitems) {
+  __shared__ int32_t wsum[16];
+  __shared__ int32_t carry;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int32_t* o = xoff + static_cast<int64_t>(blockIdx.x) * (top_k + 2);
+  int32_t* it = pitems + static_cast<int64_t>(blockIdx.x) * (kchunks + 1);
+  if (tid == 0) carry = 0;
+  __syncthreads();
+  for (int base = 0; base < kchunks; base += 1024) {
+    const int kc = base + tid;
+    const int rk = kc < kchunks ? o[top_k + 1] - o[min(kBkKeys * kc + 1, top_k + 1)] : 0;
+    const int cnt = (rk + kBkPfxRows - 1) / kBkPfxRows;
+    int x = cnt;
+#pragma unroll
+    for (int s = 1; s < 64; s <<= 1) {
+      const int y = __shfl_up(x, s);
+      if (lane >= s) x += y;
+    }
+    if (lane == 63) wsum[wave] = x;
+    __syncthreads();
+    if (tid == 0) {
+      int run = carry;
+      for (int w = 0; w < 16; ++w) {
+        const int t = wsum[w];
+        wsum[w] = run;
+        run += t;
+      }
+      carry = run;
+    }
+    __syncthreads();
+    if (kc < kchunks) it[kc] = wsum[wave] + x - cnt;
+    __syncthreads();
+  }
+  if (tid == 0) it[kchunks] = carry;
+}
+
+// Per prefix item slot: int4 (nk << 16, k0, rs, r1) -- keys k0 .. k0 + nk - 1
+// and rows rs .. r1 - 1 of the X index -- or -1 past the bh's items.
+__global__ void prefix_desc_kernel(const int32_t* __restrict__ xoff, const int32_t* __restrict__ pitems,
+                                   int top_k, int kchunks, int kmax, int64_t max_items, int4* __restrict__ desc) {
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t bh = blockIdx.y;
+  if (item >= max_items) return;
+  const int32_t* it = pitems + bh * (kchunks + 1);
+  const int32_t* o = xoff + bh * (top_k + 2);
+  int4 out = make_int4(-1, 0, 0, 0);
+  if (item < it[kchunks]) {
+    int lo = 0, hi = kchunks;  // it[lo] <= item < it[hi]
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (it[mid] <= item) lo = mid;
+      else hi = mid;
+    }
+    const int k0 = kBkKeys * lo;
+    const int nk = min(kBkKeys, kmax - k0);
+    const int rs = o[min(k0 + 1, top_k + 1)] + static_cast<int>(item - it[lo]) * kBkPfxRows;
+    const int r1 = min(rs + kBkPfxRows, o[top_k + 1]);
+    out = make_int4(nk << 16, k0, rs, r1);
+  }
+  desc[bh * max_items + item] = out;
+}
+
 // 4 bf16 of the staged rows 4 q4 + e (e = 0..3) at column 16 dt + c16 (the
 // first half of rows_transposed: a 16-row buffer).
 template <int D>
@@ -964,7 +1045,7 @@ __device__ __forceinline__ int bk_hash(int code) {
   return static_cast<int>((static_cast<uint32_t>(code) * 2654435761u) >> 23) & (kBkHash - 1);
 }
 
-template <int D>
+template <int D, bool PFX>
 __global__ __launch_bounds__(kBkThreads, 2) void bucket_attention_bwd_kernel(BwdParams p, BucketParams bp) {
   using S = MfShape<D>;
   constexpr int KB = S::KB;
@@ -992,20 +1073,24 @@ __global__ __launch_bounds__(kBkThreads, 2) void bucket_attention_bwd_kernel(Bwd
   const int g = p.g, gpl = bp.gp_log2, rpc = kBkQv >> gpl;
   const int nrc = (r1 - rs + rpc - 1) / rpc;
   if (nrc <= 0) return;
-  const int32_t* kp = bp.kpost + bh * p.n * bp.b;
+  const int32_t* kp = PFX ? nullptr : bp.kpost + bh * p.n * bp.b;
   const int2* meta = bp.meta + bh * p.n * bp.a;
+  // key of item slot t (< nk): the bucket's posting, or prefix key k0 + t
+  auto key_at = [&](int t) -> int { return PFX ? k0 + t : kp[k0 + t]; };
   const int h = static_cast<int>(bh % p.h_kv);
   const int64_t bb = bh / p.h_kv;
 
   if (tid < kBkKeys) {
-    const int j = tid < nk ? kp[k0 + tid] : -1;
+    const int j = tid < nk ? key_at(tid) : -1;
     s_j[tid] = j;
-    const int32_t* kcj = bp.kcodes + (bh * p.n + (j >= 0 ? j : 0)) * bp.b;
-    int cv[kBkMaxB];
+    if constexpr (!PFX) {
+      const int32_t* kcj = bp.kcodes + (bh * p.n + (j >= 0 ? j : 0)) * bp.b;
+      int cv[kBkMaxB];
 #pragma unroll
-    for (int x = 0; x < kBkMaxB; ++x) cv[x] = kcj[x < bp.b ? x : 0];  // all loads in flight together
+      for (int x = 0; x < kBkMaxB; ++x) cv[x] = kcj[x < bp.b ? x : 0];  // all loads in flight together
 #pragma unroll
-    for (int x = 0; x < kBkMaxB; ++x) s_kc[tid][x] = (j >= 0 && x < bp.b) ? cv[x] : 0x7FFFFFFF;
+      for (int x = 0; x < kBkMaxB; ++x) s_kc[tid][x] = (j >= 0 && x < bp.b) ? cv[x] : 0x7FFFFFFF;
+    }
   }
   for (int e = tid; e < kBkHash; e += kBkThreads) {
     s_hk[e] = -1;
@@ -1027,7 +1112,7 @@ __global__ __launch_bounds__(kBkThreads, 2) void bucket_attention_bwd_kernel(Bwd
 #pragma unroll
   for (int x = 0; x < KVL; ++x) {
     const int slot = S::KPI * (wave + x * (kBkThreads / 64)) + lane / S::SEGS;
-    jl[x] = (wave + x * (kBkThreads / 64) < S::NLD && slot < nk) ? kp[k0 + slot] : -1;
+    jl[x] = (wave + x * (kBkThreads / 64) < S::NLD && slot < nk) ? key_at(slot) : -1;
   }
 #pragma unroll
   for (int x = 0; x < KVL; ++x) {
@@ -1076,6 +1161,7 @@ __global__ __launch_bounds__(kBkThreads, 2) void bucket_attention_bwd_kernel(Bwd
                  ? *reinterpret_cast<const float4*>(p.pstats + ((bh * p.n + i) * g + hh) * 4)
                  : make_float4(0.f, 0.f, 0.f, 0.f);
     }
+    if constexpr (PFX) return;
 #pragma unroll
     for (int x = 0; x < 2; ++x) {
       const int e = tid + kBkThreads * x;
@@ -1101,6 +1187,7 @@ __global__ __launch_bounds__(kBkThreads, 2) void bucket_attention_bwd_kernel(Bwd
   // ... into LDS; a row code below c names the item's keys that share it
   auto store_rows = [&](int bf) {
     if (tid < kBkQv) *reinterpret_cast<float4*>(&s_st[bf][tid][0]) = st_r;
+    if constexpr (PFX) return;
 #pragma unroll
     for (int x = 0; x < 2; ++x) {
       const int e = tid + kBkThreads * x;
@@ -1134,7 +1221,10 @@ __global__ __launch_bounds__(kBkThreads, 2) void bucket_attention_bwd_kernel(Bwd
       if (rho < rpc) {
         const int2 m = s_meta[bf][rho];
         const int j = s_j[kappa];
-        if (m.x >= 0 && j >= 0 && m.y != -1 && !(p.causal && j > m.x) && !((s_dup[bf][rho] >> kappa) & 1u)) {
+        if constexpr (PFX) {
+          ok = m.x >= 0 && j >= 0 && j < m.y && !(p.causal && j > m.x);  // the row's prefix [0, X)
+        } else if (m.x >= 0 && j >= 0 && m.y != -1 && !(p.causal && j > m.x) &&
+                   !((s_dup[bf][rho] >> kappa) & 1u)) {
           if (m.y > 0) ok = j >= m.y && !(bp.router_causal && j > m.x);
           else ok = ((s_bw[bf][rho][kappa] >> (j & 31)) & 1u) != 0;
         }
@@ -1156,7 +1246,7 @@ __global__ __launch_bounds__(kBkThreads, 2) void bucket_attention_bwd_kernel(Bwd
   }
   __syncthreads();
   // the item's codes below c -> keys holding them
-  {
+  if constexpr (!PFX) {
     const int kappa = tid >> 3, y = tid & 7;
     const int code = s_kc[kappa][y];
     if (code < c) {
@@ -1370,27 +1460,48 @@ struct BucketWs {
   int32_t* ctr;
   int32_t* rowmap;
   int2* meta;
+  // prefix mode: X per row (clamped), its index, item starts and descriptors,
+  // posting meta (row, X)
+  int32_t* xcodes;
+  int32_t* xoff;
+  int32_t* xpost;
+  int32_t* pitems;
+  int4* pdesc;
+  int2* pmeta;
   uint32_t* bits;
   int64_t cap;  // bitmaps that fit
 };
 
 // Items (bucket, 32-key chunk) per bh at most: sum over c of ceil(|K_c| / 32).
 int64_t bucket_max_items(int64_t n, int b, int n_c) { return ceil_div(n * b, kBkKeys) + n_c; }
+// Prefix mode (X index of top_k + 1 codes): key chunks and items per bh at most.
+bool prefix_mode_ok(int top_k) { return top_k + 1 <= 16384; }
+int prefix_kchunks(int64_t n, int top_k) { return static_cast<int>(ceil_div(min(static_cast<int64_t>(top_k), n), kBkKeys)); }
+int64_t prefix_max_items(int64_t n, int top_k) { return prefix_kchunks(n, top_k) * (ceil_div(n, kBkPfxRows) + 1); }
 
-size_t bucket_fixed_bytes(int64_t batch, int64_t n, int h_kv, int a, int b, int n_c) {
+size_t bucket_fixed_bytes(int64_t batch, int64_t n, int h_kv, int a, int b, int n_c, int top_k) {
   const int64_t bh = batch * h_kv;
+  const int xn = prefix_mode_ok(top_k) ? top_k + 1 : 1;
+  const size_t hist = index_ws_bytes(bh, n, n_c) > index_ws_bytes(bh, n, xn) ? index_ws_bytes(bh, n, n_c)
+                                                                              : index_ws_bytes(bh, n, xn);
   return align_up(sizeof(int32_t) * static_cast<size_t>(bh * (n_c + 1)), 256) +
-         align_up(sizeof(int32_t) * static_cast<size_t>(bh * n * a), 256) +
-         align_up(index_ws_bytes(bh, n, n_c), 256) +
+         align_up(sizeof(int32_t) * static_cast<size_t>(bh * n * a), 256) + align_up(hist, 256) +
          align_up(sizeof(int32_t) * static_cast<size_t>(bh * (n_c + 1)), 256) +
          align_up(sizeof(int4) * static_cast<size_t>(bh * bucket_max_items(n, b, n_c)), 256) + 256 +
          align_up(sizeof(int32_t) * static_cast<size_t>(bh * n), 256) +
-         align_up(sizeof(int2) * static_cast<size_t>(bh * n * a), 256);
+         align_up(sizeof(int2) * static_cast<size_t>(bh * n * a), 256) +
+         align_up(sizeof(int32_t) * static_cast<size_t>(bh * n), 256) +
+         align_up(sizeof(int32_t) * static_cast<size_t>(bh * (xn + 1)), 256) +
+         align_up(sizeof(int32_t) * static_cast<size_t>(bh * n), 256) +
+         align_up(sizeof(int32_t) * static_cast<size_t>(bh * (prefix_kchunks(n, top_k) + 1)), 256) +
+         align_up(sizeof(int4) * static_cast<size_t>(bh * prefix_max_items(n, top_k)), 256) +
+         align_up(sizeof(int2) * static_cast<size_t>(bh * n), 256);
 }
 
 int64_t bucket_words(int64_t n) { return ceil_div(n, 32); }
 
-BucketWs carve_bucket_ws(void* base, size_t bytes, int64_t batch, int64_t n, int h_kv, int a, int b, int n_c) {
+BucketWs carve_bucket_ws(void* base, size_t bytes, int64_t batch, int64_t n, int h_kv, int a, int b, int n_c,
+                         int top_k) {
   const int64_t bh = batch * h_kv;
   char* c = static_cast<char*>(base);
   BucketWs w{};
@@ -1401,12 +1512,20 @@ BucketWs carve_bucket_ws(void* base, size_t bytes, int64_t batch, int64_t n, int
   };
   w.qoff = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * static_cast<size_t>(bh * (n_c + 1))));
   w.qpost = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * static_cast<size_t>(bh * n * a)));
-  w.hist = take(index_ws_bytes(bh, n, n_c));
+  const int xn = prefix_mode_ok(top_k) ? top_k + 1 : 1;
+  w.hist = take(index_ws_bytes(bh, n, n_c) > index_ws_bytes(bh, n, xn) ? index_ws_bytes(bh, n, n_c)
+                                                                       : index_ws_bytes(bh, n, xn));
   w.items = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * static_cast<size_t>(bh * (n_c + 1))));
   w.desc = reinterpret_cast<int4*>(take(sizeof(int4) * static_cast<size_t>(bh * bucket_max_items(n, b, n_c))));
   w.ctr = reinterpret_cast<int32_t*>(take(256));
   w.rowmap = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * static_cast<size_t>(bh * n)));
   w.meta = reinterpret_cast<int2*>(take(sizeof(int2) * static_cast<size_t>(bh * n * a)));
+  w.xcodes = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * static_cast<size_t>(bh * n)));
+  w.xoff = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * static_cast<size_t>(bh * (xn + 1))));
+  w.xpost = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * static_cast<size_t>(bh * n)));
+  w.pitems = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * static_cast<size_t>(bh * (prefix_kchunks(n, top_k) + 1))));
+  w.pdesc = reinterpret_cast<int4*>(take(sizeof(int4) * static_cast<size_t>(bh * prefix_max_items(n, top_k))));
+  w.pmeta = reinterpret_cast<int2*>(take(sizeof(int2) * static_cast<size_t>(bh * n)));
   w.bits = reinterpret_cast<uint32_t*>(c);
   const size_t used = static_cast<size_t>(c - static_cast<char*>(base));
   const size_t row_bytes = sizeof(uint32_t) * static_cast<size_t>(bucket_words(n));
@@ -1538,12 +1657,14 @@ extern "C" int ssa_sparse_attention_backward(
 
 extern "C" size_t ssa_sparse_attention_backward_routed_workspace_bytes(int dtype, int dout_dtype, int64_t batch,
                                                                        int64_t n, int h_q, int h_kv, int d,
-                                                                       int a, int b, int n_c, int64_t bitmap_rows) {
+                                                                       int top_k, int a, int b, int n_c,
+                                                                       int64_t bitmap_rows) {
   const size_t stats = bwd_ws_bytes(dtype, dout_dtype, batch, n, h_q, h_kv, d);
   if (stats == 0 || a < 1 || a > kBkMaxA || b < 1 || b > kBkMaxB || n_c < 1 || n_c > 16384) return stats;
   const int64_t rows = batch * h_kv * n;
   const int64_t cap = bitmap_rows < 0 ? (rows + 1) / 2 : (bitmap_rows < rows ? bitmap_rows : rows);
-  return align_up(stats, 256) + bucket_fixed_bytes(batch, n, h_kv, a, b, n_c) +
+  if (top_k < 1) return stats;
+  return align_up(stats, 256) + bucket_fixed_bytes(batch, n, h_kv, a, b, n_c, top_k) +
          sizeof(uint32_t) * static_cast<size_t>(bucket_words(n)) * static_cast<size_t>(cap);
 }
 
@@ -1573,12 +1694,13 @@ extern "C" int ssa_sparse_attention_backward_routed(
   if (!bucket_ok(p, dtype, dout_dtype, a, b, n_c))
     return run_bwd(p, dtype, batch, row_prefix, workspace, workspace_bytes, dout_dtype, st);
   const size_t stats = align_up(bwd_ws_bytes(dtype, dout_dtype, batch, n, h_q, h_kv, d), 256);
-  const size_t need = stats + bucket_fixed_bytes(batch, n, h_kv, a, b, n_c);
+  const size_t need = stats + bucket_fixed_bytes(batch, n, h_kv, a, b, n_c, top_k);
   if (!workspace || workspace_bytes < need)
     return fail(SSA_ERR_WORKSPACE, "sparse_attention_backward_routed: workspace %zu < %zu bytes",
                 workspace ? workspace_bytes : size_t(0), need);
   const int64_t bhn = batch * h_kv;
-  BucketWs w = carve_bucket_ws(static_cast<char*>(workspace) + stats, workspace_bytes - stats, batch, n, h_kv, a, b, n_c);
+  BucketWs w = carve_bucket_ws(static_cast<char*>(workspace) + stats, workspace_bytes - stats, batch, n, h_kv, a, b,
+                               n_c, top_k);
   p.pfx = row_prefix;
   p.pstats = static_cast<float*>(workspace);
   p.rowmap = w.rowmap;
@@ -1603,6 +1725,25 @@ extern "C" int ssa_sparse_attention_backward_routed(
   bucket_meta_kernel<<<dim3(static_cast<unsigned>(ceil_div(entries, 256))), 256, 0, st>>>(
       w.qpost, n * a, entries, n, row_prefix, w.rowmap, w.meta);
   if (int s = check_launch("bucket_meta_kernel")) return s;
+  // prefix mode: the X index, its items and meta; the prefix pass then adds dq only
+  const bool pfx_mode = prefix_mode_ok(top_k);
+  const int kchunks = prefix_kchunks(n, top_k);
+  const int64_t pmax = prefix_max_items(n, top_k);
+  if (pfx_mode && kchunks > 0) {
+    bucket_xcodes_kernel<<<dim3(static_cast<unsigned>(ceil_div(p.rows, 256))), 256, 0, st>>>(row_prefix, p.rows, top_k,
+                                                                                             w.xcodes);
+    if (int s = check_launch("bucket_xcodes_kernel")) return s;
+    if (int s = build_index_into(w.xcodes, bhn, n, 1, top_k + 1, w.xoff, w.xpost, w.hist, st)) return s;
+    prefix_items_kernel<<<dim3(static_cast<unsigned>(bhn)), 1024, 0, st>>>(w.xoff, top_k, kchunks, w.pitems);
+    if (int s = check_launch("prefix_items_kernel")) return s;
+    prefix_desc_kernel<<<dim3(static_cast<unsigned>(ceil_div(pmax, 256)), static_cast<unsigned>(bhn)), 256, 0, st>>>(
+        w.xoff, w.pitems, top_k, kchunks, static_cast<int>(min(static_cast<int64_t>(top_k), n)), pmax, w.pdesc);
+    if (int s = check_launch("prefix_desc_kernel")) return s;
+    bucket_meta_kernel<<<dim3(static_cast<unsigned>(ceil_div(p.rows, 256))), 256, 0, st>>>(
+        w.xpost, n, p.rows, n, row_prefix, w.rowmap, w.pmeta);
+    if (int s = check_launch("bucket_meta_kernel")) return s;
+    p.pfx_dq_only = 1;
+  }
   if (int s = launch_bwd<uint16_t>(p, st)) return s;  // row kernel (dq, stats, fallback rows) + prefix pass
   BucketParams bp{};
   bp.kpost = postings;
@@ -1621,8 +1762,20 @@ extern "C" int ssa_sparse_attention_backward_routed(
   bp.router_causal = router_causal ? 1 : 0;
   const dim3 grid(static_cast<unsigned>(max_items), static_cast<unsigned>(bhn));
   if (d == 64)
-    bucket_attention_bwd_kernel<64><<<grid, kBkThreads, 0, st>>>(p, bp);
+    bucket_attention_bwd_kernel<64, false><<<grid, kBkThreads, 0, st>>>(p, bp);
   else
-    bucket_attention_bwd_kernel<128><<<grid, kBkThreads, 0, st>>>(p, bp);
+    bucket_attention_bwd_kernel<128, false><<<grid, kBkThreads, 0, st>>>(p, bp);
+  if (int s = check_launch("bucket_attention_bwd_kernel")) return s;
+  if (!p.pfx_dq_only) return SSA_OK;
+  BucketParams pp = bp;  // the prefix keys: X index rows, consecutive keys
+  pp.desc = w.pdesc;
+  pp.meta = w.pmeta;
+  pp.a = 1;
+  pp.max_items = pmax;
+  const dim3 pgrid(static_cast<unsigned>(pmax), static_cast<unsigned>(bhn));
+  if (d == 64)
+    bucket_attention_bwd_kernel<64, true><<<pgrid, kBkThreads, 0, st>>>(p, pp);
+  else
+    bucket_attention_bwd_kernel<128, true><<<pgrid, kBkThreads, 0, st>>>(p, pp);
   return check_launch("bucket_attention_bwd_kernel");
 }

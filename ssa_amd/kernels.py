@@ -446,7 +446,7 @@ def sparse_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                 or tuple(off.shape[:2]) != (B, h_kv) or tuple(post.shape) != (B, h_kv, n * b)):
             raise ValueError("routing tensors do not match q, k (see kernels.Routing)")
         ws_bytes = int(_lib.load().ssa_sparse_attention_backward_routed_workspace_bytes(
-            _lib.elem_dtype(q), _lib.elem_dtype(dout), B, n, h_q, h_kv, d, a, b, n_c, int(bitmap_rows)))
+            _lib.elem_dtype(q), _lib.elem_dtype(dout), B, n, h_q, h_kv, d, top_k, a, b, n_c, int(bitmap_rows)))
         ws = torch.empty(ws_bytes, device=q.device, dtype=torch.uint8) if ws_bytes else None
         call("ssa_sparse_attention_backward_routed", *common, ptr(qc), a, ptr(kc), b, ptr(off), ptr(post),
              n_c, int(bool(routing.causal)), ptr(ws), ws_bytes, stream_of(q))
