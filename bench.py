@@ -314,9 +314,10 @@ def stats_sums(q, k, router):
 def time_backward(cfg, q, k, v, inter, reps=3):
     """Stage (d) backward on the forward's indices and query order, with an fp32
     forward output and a seeded bf16 output gradient, as SSAAttention trains:
-    ssa_sparse_attention_backward_routed (candidate keys by codebook bucket)
-    and, for comparison, the plain ssa_sparse_attention_backward; median of
-    `reps` launches each (HIP events on the launch stream)."""
+    ssa_sparse_attention_backward_routed (candidate and prefix keys by codebook
+    bucket / prefix tile) with the forward's row stats, and, for comparison,
+    the plain ssa_sparse_attention_backward without either; median of `reps`
+    launches each (HIP events on the launch stream)."""
     import torch
 
     from ssa_amd import kernels
@@ -327,35 +328,37 @@ def time_backward(cfg, q, k, v, inter, reps=3):
     idx = kernels.select(q, k, qc, off, post, cfg["b"], cfg["k"], sorted=False,
                          index_dtype=torch.int32, row_order=order, row_prefix=pfx)
     out32 = torch.empty(q.shape, device=q.device, dtype=torch.float32)
-    kernels.sparse_attention(q, k, v, idx, None, True, out=out32, row_order=order, row_prefix=pfx)
+    stats = kernels.row_stats_buffer(q, cfg["h_kv"])  # the forward's softmax stats, as in training
+    kernels.sparse_attention(q, k, v, idx, None, True, out=out32, row_order=order, row_prefix=pfx,
+                             row_stats=stats)
     gen = torch.Generator(device=q.device).manual_seed(7)
     dout = torch.randn(q.shape, generator=gen, device=q.device).to(q.dtype)
     routing = kernels.Routing(qc, kc, off, post, True)
 
-    def median_ms(rt):
+    def median_ms(rt, st):
         ts = []
         for _ in range(reps):
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record()
             kernels.sparse_attention_backward(q, k, v, idx, out32, dout, None, True, row_order=order,
-                                              row_prefix=pfx, routing=rt)
+                                              row_prefix=pfx, routing=rt, row_stats=st)
             e1.record()
             torch.cuda.synchronize()
             ts.append(e0.elapsed_time(e1))
         return sorted(ts)[len(ts) // 2]
 
-    ms = median_ms(routing)
-    ms_plain = median_ms(None)
+    ms = median_ms(routing, stats)
+    ms_plain = median_ms(None, None)
     B, n, h_q, h_kv, d, kk = cfg["B"], cfg["n"], cfg["h_q"], cfg["h_kv"], cfg["d"], cfg["k"]
     s = 2 if cfg["dtype"] == "bf16" else 4
     rows = B * n * h_kv
     g = h_q // h_kv
-    # per row: K gathered twice (two passes) and V once, indices twice, q/dO
-    # (input type) and o (fp32) read, dq written, dk and dv read-modify-written
-    byt = rows * (3 * kk * d * s + 2 * kk * 4 + g * d * (2 * s + 4) + g * d * 4 + 2 * kk * d * 8)
+    # per row: K and V of each slot once, its indices, q / dO (input type) and
+    # o (fp32) read, dq written; dk and dv written once per key
+    byt = rows * (2 * kk * d * s + kk * 4 + g * d * (2 * s + 4) + g * d * 4) + B * n * h_kv * d * 8
     return {"ms": ms, "tokens_per_s": B * n / (ms / 1000),
             "kernel": "sparse_attention_bwd_mfma_kernel + prefix_attention_bwd_kernel + bucket_attention_bwd_kernel",
-            "ms_without_buckets": ms_plain,
+            "ms_plain_without_buckets_or_stats": ms_plain,
             "algorithmic_gb": byt / 1e9, "gbs": byt / (ms / 1000) / 1e9}
 
 
