@@ -1365,20 +1365,31 @@ __global__ __launch_bounds__(kBkThreads, 2) void bucket_attention_bwd_kernel(Bwd
     __syncthreads();  // chunk u + 1 staged; every wave is done with chunk u
   }
 
-  // dV^T, dK^T tiles: lane (q4, c16) holds dims 16 dt + 4 q4 + e of key 16 t + c16
+  // dV^T, dK^T tiles: lane (q4, c16) holds dims 16 dt + 4 q4 + e of key 16 t + c16.
+  // They pass through LDS (the row buffers are free now) as [key][dim] so that
+  // each atomic instruction adds D/2 consecutive floats of one key row.
   if (!keys_here) return;
-  const int j = s_j[16 * t + c16];
-  if (j < 0) return;
-  float* dvr = p.dv + ((bb * p.n + j) * p.h_kv + h) * p.d;
-  float* dkr = p.dk + ((bb * p.n + j) * p.h_kv + h) * p.d;
+  constexpr int HD = D / 2;
+  float* tw = reinterpret_cast<float*>(&qds[0][0][0]) + wave * 16 * HD;
+  const int64_t grow = static_cast<int64_t>(p.h_kv) * p.d;  // floats between consecutive keys of dk / dv
+  const int64_t kbase0 = (bb * p.n * p.h_kv + h) * p.d + dh * HD;
 #pragma unroll
-  for (int dd = 0; dd < DT; ++dd) {
-    const int dim0 = 16 * (DT * dh + dd) + 4 * q4;
+  for (int pass = 0; pass < 2; ++pass) {
+    const float mul = pass == 0 ? 1.0f : p.inv_scale;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      unsafeAtomicAdd(dvr + dim0 + e, accv[dd][e]);
-      unsafeAtomicAdd(dkr + dim0 + e, acck[dd][e] * p.inv_scale);
+    for (int dd = 0; dd < DT; ++dd)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        tw[c16 * HD + 16 * dd + 4 * q4 + e] = (pass == 0 ? accv[dd][e] : acck[dd][e]) * mul;
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+    __builtin_amdgcn_wave_barrier();
+    float* dst = (pass == 0 ? p.dv : p.dk) + kbase0;
+    for (int kk = 0; kk < 16; ++kk) {
+      const int j = s_j[16 * t + kk];
+      if (j >= 0 && lane < HD) unsafeAtomicAdd(dst + j * grow + lane, tw[kk * HD + lane]);
     }
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+    __builtin_amdgcn_wave_barrier();  // tw is rewritten by the next pass
   }
 }
 
