@@ -247,13 +247,16 @@ __global__ __launch_bounds__(64 * kBwdWaves) void sparse_attention_bwd_kernel(Bw
 // exact in bf16.
 constexpr int kBwMfWaves = 2;
 
-template <int D>
+// DKDV = false: dq only, for the rows whose dk and dv the bucket kernel adds
+// (rowmap != -1); DKDV = true: every row, or in bucket mode only rowmap == -1.
+template <int D, bool DKDV>
 __global__ __launch_bounds__(64 * kBwMfWaves, 2) void sparse_attention_bwd_mfma_kernel(BwdParams p) {
   using S = MfShape<D>;
   constexpr int KB = S::KB, NT = S::NT;
+  constexpr int TW = DKDV ? kBwMfWaves : 1;  // the dk / dv staging exists only in the DKDV build
   __shared__ __align__(16) unsigned char kv_lds[kBwMfWaves][2][kMfChunk * S::ROW];
-  __shared__ __align__(16) float tr_lds[kBwMfWaves][kMfChunk][16];      // P or dS as [key][head]
-  __shared__ __align__(16) uint16_t hd_lds[kBwMfWaves][2][D][8];        // Q, dO as [dim][head] (bf16)
+  __shared__ __align__(16) float tr_lds[TW][kMfChunk][16];      // P or dS as [key][head]
+  __shared__ __align__(16) uint16_t hd_lds[TW][2][D][8];        // Q, dO as [dim][head] (bf16)
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -270,6 +273,7 @@ __global__ __launch_bounds__(64 * kBwMfWaves, 2) void sparse_attention_bwd_mfma_
     }
     i = oi;
   }
+  if (p.rowmap && DKDV != (p.rowmap[bh * p.n + i] == -1)) return;  // the other build takes this row
   const int h = static_cast<int>(bh % p.h_kv);
   const int64_t bb = bh / p.h_kv;
   const int g = p.g;
@@ -293,9 +297,9 @@ __global__ __launch_bounds__(64 * kBwMfWaves, 2) void sparse_attention_bwd_mfma_
       const uint16_t qv = static_cast<uint16_t>((e & 1) ? (qw[e >> 1] >> 16) : (qw[e >> 1] & 0xFFFFu));
       const uint16_t dv = static_cast<uint16_t>((e & 1) ? (dw[e >> 1] >> 16) : (dw[e >> 1] & 0xFFFFu));
       if (col_ok) dpart = fma_rn(bf16_bits_to_f32(dv), ld_any(p.o, bb * p.o_sb + i * p.o_sn + static_cast<int64_t>(hq) * p.o_sh + dim, p.o_bf16), dpart);
-      if (c16 < 8) {  // head slots 0..7 of the [dim][head] copies (zero past g)
-        hd_lds[wave][0][dim][c16] = col_ok ? qv : static_cast<uint16_t>(0);
-        hd_lds[wave][1][dim][c16] = col_ok ? dv : static_cast<uint16_t>(0);
+      if (DKDV && c16 < 8) {  // head slots 0..7 of the [dim][head] copies (zero past g)
+        hd_lds[DKDV ? wave : 0][0][dim][c16] = col_ok ? qv : static_cast<uint16_t>(0);
+        hd_lds[DKDV ? wave : 0][1][dim][c16] = col_ok ? dv : static_cast<uint16_t>(0);
       }
     }
   }
@@ -414,7 +418,7 @@ __global__ __launch_bounds__(64 * kBwMfWaves, 2) void sparse_attention_bwd_mfma_
   float* dkb = p.dk + (bb * p.n * p.h_kv + h) * p.d;
   float* dvb = p.dv + (bb * p.n * p.h_kv + h) * p.d;
   const int64_t krow = static_cast<int64_t>(p.h_kv) * p.d;
-  float* tr = &tr_lds[wave][0][0];
+  float* tr = &tr_lds[DKDV ? wave : 0][0][0];
   // A operand over heads from the [key][head] copy: k = 0..7 bf16 hi of heads
   // 0..7 (lanes q4 = 0), 8..15 their lo (q4 = 1), 16..31 zero
   auto heads_operand = [&](int t) -> bf16x8_t {
@@ -436,7 +440,7 @@ __global__ __launch_bounds__(64 * kBwMfWaves, 2) void sparse_attention_bwd_mfma_
   // head row), zero for q4 >= 2; column c16 = dim 16 dt + c16
   auto head_rows = [&](int which, int dt) -> bf16x8_t {
     if (q4 >= 2) return bf16x8_t{};
-    return *reinterpret_cast<const bf16x8_t*>(&hd_lds[wave][which][16 * dt + c16][0]);
+    return *reinterpret_cast<const bf16x8_t*>(&hd_lds[DKDV ? wave : 0][which][16 * dt + c16][0]);
   };
   int jc = nchunks > 0 ? load_idx(0) : -1;
   uint64_t okn = __ballot(chunk_ok2(jc));
@@ -492,7 +496,7 @@ __global__ __launch_bounds__(64 * kBwMfWaves, 2) void sparse_attention_bwd_mfma_
     for (int t = 0; t < NT; ++t) dqacc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kt[t], dsb, dqacc[t], 0, 0, 0);
 
     // dV and dK tiles; P then dS pass through tr as [key][head]
-    if (!row_dkdv) continue;
+    if (!DKDV || !row_dkdv) continue;
 #pragma unroll
     for (int pass = 0; pass < 2; ++pass) {
       const float* src = pass == 0 ? pr : ds;
@@ -1425,10 +1429,17 @@ int launch_bwd(const BwdParams& p, hipStream_t st) {
   if constexpr (sizeof(T) == 2) {
     if (bwd_mfma_ok(p, p.q, p.dout)) {
       const dim3 grid(static_cast<unsigned>(ceil_div(p.rows, kBwMfWaves)));
+      if (p.rowmap) {  // bucket mode: dq only for most rows, the full kernel for rowmap == -1
+        if (p.d == 64)
+          sparse_attention_bwd_mfma_kernel<64, false><<<grid, 64 * kBwMfWaves, 0, st>>>(p);
+        else
+          sparse_attention_bwd_mfma_kernel<128, false><<<grid, 64 * kBwMfWaves, 0, st>>>(p);
+        if (int s = check_launch("sparse_attention_bwd_mfma_kernel")) return s;
+      }
       if (p.d == 64)
-        sparse_attention_bwd_mfma_kernel<64><<<grid, 64 * kBwMfWaves, 0, st>>>(p);
+        sparse_attention_bwd_mfma_kernel<64, true><<<grid, 64 * kBwMfWaves, 0, st>>>(p);
       else
-        sparse_attention_bwd_mfma_kernel<128><<<grid, 64 * kBwMfWaves, 0, st>>>(p);
+        sparse_attention_bwd_mfma_kernel<128, true><<<grid, 64 * kBwMfWaves, 0, st>>>(p);
       if (int s = check_launch("sparse_attention_bwd_mfma_kernel")) return s;
       if (!p.pfx) return SSA_OK;
       const dim3 pgrid(static_cast<unsigned>(kXcds * xcd_per((p.rows / p.n) * ceil_div(p.n, kPbWaves))));
