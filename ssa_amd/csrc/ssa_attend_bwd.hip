@@ -556,27 +556,30 @@ __global__ __launch_bounds__(64 * kBwMfWaves, 2) void sparse_attention_bwd_mfma_
 // of one per row.
 constexpr int kPbWaves = 8;
 
-template <int D>
-__global__ __launch_bounds__(64 * kPbWaves, 1) void prefix_attention_bwd_kernel(BwdParams p) {
+// DQ: dq only (the bucket kernel's prefix mode adds dk and dv): 4 rows per
+// block and no [key][query vector] staging, for 3 blocks per CU.
+template <int D, bool DQ>
+__global__ __launch_bounds__(64 * (DQ ? 4 : kPbWaves), 1) void prefix_attention_bwd_kernel(BwdParams p) {
   using S = MfShape<D>;
   constexpr int KB = S::KB, NT = S::NT;
-  constexpr int QV = 8 * kPbWaves;      // query vectors per block at most (g <= 8)
-  constexpr int LPW = (S::NLD + kPbWaves - 1) / kPbWaves;  // chunk loads per wave and tensor
+  constexpr int W = DQ ? 4 : kPbWaves;  // rows (waves) per block
+  constexpr int QV = DQ ? 1 : 8 * W;    // query vectors per block at most (g <= 8)
+  constexpr int LPW = (S::NLD + W - 1) / W;  // chunk loads per wave and tensor
   __shared__ __align__(16) unsigned char kv[2][2][kMfChunk * S::ROW];  // [buffer][K, V]
   __shared__ __align__(16) float pall[2][kMfChunk][QV];                // P, dS as [key][qv]
-  __shared__ __align__(16) uint16_t qall[2][D][QV];                    // Q, dO as [dim][qv] (bf16)
+  __shared__ __align__(16) uint16_t qall[2][DQ ? 1 : D][QV];           // Q, dO as [dim][qv] (bf16)
   __shared__ int s_xmax;
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int tid = threadIdx.x, lane = tid & 63;
   const int q4 = lane >> 4, c16 = lane & 15;
   const int g = p.g;
-  const int64_t tiles = ceil_div(p.n, kPbWaves);
+  const int64_t tiles = ceil_div(p.n, W);
   const int64_t nblk = (p.rows / p.n) * tiles;
   const int64_t blk = xcd_block(blockIdx.x, xcd_per(nblk));
   if (blk >= nblk) return;
   const int64_t bh = blk / tiles;
-  const int64_t i = (blk - bh * tiles) * kPbWaves + wave;  // this wave's row
+  const int64_t i = (blk - bh * tiles) * W + wave;  // this wave's row
   const bool row_ok = i < p.n;
   const int h = static_cast<int>(bh % p.h_kv);
   const int64_t bb = bh / p.h_kv;
@@ -586,8 +589,10 @@ __global__ __launch_bounds__(64 * kPbWaves, 1) void prefix_attention_bwd_kernel(
 
   // the block's Q and dO as [dim][qv], zero for unused query vectors (whose P
   // and dS columns stay zero too: the reductions run over whole 32-column blocks)
-  for (int e = tid; e < 2 * D * QV; e += 64 * kPbWaves) reinterpret_cast<uint16_t*>(qall)[e] = 0;
-  for (int e = tid; e < 2 * kMfChunk * QV; e += 64 * kPbWaves) reinterpret_cast<float*>(pall)[e] = 0.0f;
+  if (!DQ) {
+    for (int e = tid; e < 2 * D * QV; e += 64 * W) reinterpret_cast<uint16_t*>(qall)[e] = 0;
+    for (int e = tid; e < 2 * kMfChunk * QV; e += 64 * W) reinterpret_cast<float*>(pall)[e] = 0.0f;
+  }
   if (tid == 0) s_xmax = 0;
   __syncthreads();
   if (lane == 0) atomicMax(&s_xmax, xrow);
@@ -606,10 +611,12 @@ __global__ __launch_bounds__(64 * kPbWaves, 1) void prefix_attention_bwd_kernel(
       const uint4 qu = __builtin_bit_cast(uint4, qf[kb]), du = __builtin_bit_cast(uint4, df[kb]);
       const uint32_t qw[4] = {qu.x, qu.y, qu.z, qu.w}, dw[4] = {du.x, du.y, du.z, du.w};
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
+      for (int e = 0; e < 8 && !DQ; ++e) {
         const int dim = kb * 32 + q4 * 8 + e;
-        qall[0][dim][wave * g + c16] = static_cast<uint16_t>((e & 1) ? (qw[e >> 1] >> 16) : (qw[e >> 1] & 0xFFFFu));
-        qall[1][dim][wave * g + c16] = static_cast<uint16_t>((e & 1) ? (dw[e >> 1] >> 16) : (dw[e >> 1] & 0xFFFFu));
+        qall[0][DQ ? 0 : dim][DQ ? 0 : wave * g + c16] =
+            static_cast<uint16_t>((e & 1) ? (qw[e >> 1] >> 16) : (qw[e >> 1] & 0xFFFFu));
+        qall[1][DQ ? 0 : dim][DQ ? 0 : wave * g + c16] =
+            static_cast<uint16_t>((e & 1) ? (dw[e >> 1] >> 16) : (dw[e >> 1] & 0xFFFFu));
       }
     }
   }
@@ -634,11 +641,11 @@ __global__ __launch_bounds__(64 * kPbWaves, 1) void prefix_attention_bwd_kernel(
   uint32_t seg16[S::SWZ_PERIOD];
   row_seg16<D>(lane, seg16);
   const int kswz = mf_swz<D>(c16);
-  // this wave's loads of chunk ch: loads r = wave + kPbWaves * t (< NLD) of K and V
+  // this wave's loads of chunk ch: loads r = wave + W * t (< NLD) of K and V
   auto issue = [&](int ch) {
 #pragma unroll
     for (int t = 0; t < LPW; ++t) {
-      const int r = wave + kPbWaves * t;
+      const int r = wave + W * t;
       if (r < S::NLD) {
         const int j = ch * kMfChunk + S::KPI * r + lane / S::SEGS;
         const uint32_t sg = seg16[r % S::SWZ_PERIOD];
@@ -658,7 +665,7 @@ __global__ __launch_bounds__(64 * kPbWaves, 1) void prefix_attention_bwd_kernel(
   float* dkb = p.dk + (bb * p.n * p.h_kv + h) * p.d;
   float* dvb = p.dv + (bb * p.n * p.h_kv + h) * p.d;
   const int64_t krow = static_cast<int64_t>(p.h_kv) * p.d;
-  const int nqv = kPbWaves * g;
+  const int nqv = W * g;
   const int kblocks = (nqv + 31) / 32;
   const int nch = (xmax + kMfChunk - 1) / kMfChunk;
   issue(0);
@@ -709,27 +716,27 @@ __global__ __launch_bounds__(64 * kPbWaves, 1) void prefix_attention_bwd_kernel(
     const bf16x8_t dsb = __builtin_bit_cast(bf16x8_t, make_uint4(db[0], db[1], db[2], db[3]));
 #pragma unroll
     for (int t = 0; t < NT; ++t) dqacc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kt[t], dsb, dqacc[t], 0, 0, 0);
-    if (p.pfx_dq_only) continue;
+    if (DQ) continue;
     // P and dS of this row's heads into [key][qv]
     if (col_ok) {
 #pragma unroll
       for (int x = 0; x < 8; ++x) {
         const int key = 16 * (x >> 2) + 4 * q4 + (x & 3);
-        pall[0][key][wave * g + c16] = pr[x];
-        pall[1][key][wave * g + c16] = ds[x];
+        pall[0][key][DQ ? 0 : wave * g + c16] = pr[x];
+        pall[1][key][DQ ? 0 : wave * g + c16] = ds[x];
       }
     }
     __syncthreads();
     // dV = P^T dO (pass 0) and dK = dS^T Q (pass 1), summed over the block's
-    // query vectors: item (pass, dt) by wave item % kPbWaves
-    for (int item = wave; item < 2 * NT; item += kPbWaves) {
+    // query vectors: item (pass, dt) by wave item % W
+    for (int item = wave; item < 2 * NT; item += W) {
       const int pass = item / NT, dt = item - pass * NT;
       const int which = pass == 0 ? 1 : 0;  // B: dO for dV, Q for dK
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         floatx4_t c = {0.f, 0.f, 0.f, 0.f};
         for (int kq = 0; kq < kblocks; ++kq) {
-          const float* src = &pall[pass][16 * t + c16][32 * kq + 8 * q4];
+          const float* src = &pall[pass][16 * t + c16][DQ ? 0 : 32 * kq + 8 * q4];
           const float4 a = *reinterpret_cast<const float4*>(src);
           const float4 b = *reinterpret_cast<const float4*>(src + 4);
           const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
@@ -741,7 +748,8 @@ __global__ __launch_bounds__(64 * kPbWaves, 1) void prefix_attention_bwd_kernel(
           }
           const bf16x8_t ah = __builtin_bit_cast(bf16x8_t, make_uint4(hw[0], hw[1], hw[2], hw[3]));
           const bf16x8_t al = __builtin_bit_cast(bf16x8_t, make_uint4(lw[0], lw[1], lw[2], lw[3]));
-          const bf16x8_t bop = *reinterpret_cast<const bf16x8_t*>(&qall[which][16 * dt + c16][32 * kq + 8 * q4]);
+          const bf16x8_t bop =
+              *reinterpret_cast<const bf16x8_t*>(&qall[which][DQ ? 0 : 16 * dt + c16][DQ ? 0 : 32 * kq + 8 * q4]);
           c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bop, c, 0, 0, 0);
           c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bop, c, 0, 0, 0);
         }
@@ -1442,11 +1450,18 @@ int launch_bwd(const BwdParams& p, hipStream_t st) {
         sparse_attention_bwd_mfma_kernel<128, true><<<grid, 64 * kBwMfWaves, 0, st>>>(p);
       if (int s = check_launch("sparse_attention_bwd_mfma_kernel")) return s;
       if (!p.pfx) return SSA_OK;
-      const dim3 pgrid(static_cast<unsigned>(kXcds * xcd_per((p.rows / p.n) * ceil_div(p.n, kPbWaves))));
-      if (p.d == 64)
-        prefix_attention_bwd_kernel<64><<<pgrid, 64 * kPbWaves, 0, st>>>(p);
-      else
-        prefix_attention_bwd_kernel<128><<<pgrid, 64 * kPbWaves, 0, st>>>(p);
+      const int w = p.pfx_dq_only ? 4 : kPbWaves;
+      const dim3 pgrid(static_cast<unsigned>(kXcds * xcd_per((p.rows / p.n) * ceil_div(p.n, w))));
+      if (p.pfx_dq_only) {
+        if (p.d == 64)
+          prefix_attention_bwd_kernel<64, true><<<pgrid, 64 * w, 0, st>>>(p);
+        else
+          prefix_attention_bwd_kernel<128, true><<<pgrid, 64 * w, 0, st>>>(p);
+      } else if (p.d == 64) {
+        prefix_attention_bwd_kernel<64, false><<<pgrid, 64 * w, 0, st>>>(p);
+      } else {
+        prefix_attention_bwd_kernel<128, false><<<pgrid, 64 * w, 0, st>>>(p);
+      }
       return check_launch("prefix_attention_bwd_kernel");
     }
   }
