@@ -495,8 +495,11 @@ __global__ __launch_bounds__(kAttThreads, (AttMinBlocks<T, D, GMAX>::value)) voi
 // bytes in flight per CU are LDS-bound; the waves share nothing, so one-wave
 // blocks let a CU hold 10 of them (160 KB) and start each as soon as one ends
 // (c3 stage d: 3.90 ms against 4.04 with four-wave blocks, 3.95 with two).
+// At least 3 waves per SIMD (at most 168 VGPRs at d = 128, no spills) so the
+// LDS, not the register file, sets the 10 waves per CU (c3 stage d 3.45 ->
+// 3.29 ms against 2 waves per SIMD at 176 VGPRs).
 constexpr int kMfWaves = 1;
-constexpr int kMfMinBlocks = 2;
+constexpr int kMfMinWavesPerEu = 3;
 
 // Issue one chunk's K and V loads: load r moves chunk rows KPI*r .. KPI*r +
 // KPI - 1 into LDS at base + r KB, lane l fetching the segment of row KPI*r +
@@ -784,7 +787,8 @@ __device__ __forceinline__ void attend_row_mfma(const AttParams& p, const AttRow
 }
 
 template <int D, bool BLK>
-__global__ __launch_bounds__(64 * kMfWaves, kMfMinBlocks) void sparse_attention_mfma_kernel(AttParams p) {
+__global__ __launch_bounds__(64 * kMfWaves) __attribute__((amdgpu_waves_per_eu(kMfMinWavesPerEu, 8))) void
+sparse_attention_mfma_kernel(AttParams p) {
   using S = MfShape<D>;
   __shared__ __align__(16) unsigned char kv_lds[kMfWaves][2][kMfChunk * S::ROW];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
