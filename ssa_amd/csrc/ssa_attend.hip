@@ -559,14 +559,16 @@ __device__ __forceinline__ void attend_row_mfma(const AttParams& p, const AttRow
   const uint16_t* vbase = static_cast<const uint16_t*>(p.v) + bb * p.v_sb + static_cast<int64_t>(h) * p.v_sh;
   const int64_t ibase = bb * p.idx_sb + (BLK ? qr >> p.blk_log2 : qr) * p.idx_sn + static_cast<int64_t>(h) * p.idx_sh;
 
-  auto load_idx = [&](int ch) -> int {
-    const int slot = ch * kMfChunk + lane;
-    if (!row_ok || lane >= kMfChunk || slot >= p.top_k) return -1;
+  // Key of slot l of chunk ch (-1 past top_k, l >= kMfChunk or on a dropped row).
+  auto load_idx_at = [&](int ch, int l) -> int {
+    const int slot = ch * kMfChunk + l;
+    if (!row_ok || l >= kMfChunk || slot >= p.top_k) return -1;
     const int e = BLK ? slot >> p.blk_log2 : slot;
     const int64_t jv = p.idx_i64 ? static_cast<const int64_t*>(p.idx)[ibase + e]
                                  : static_cast<int64_t>(static_cast<const int32_t*>(p.idx)[ibase + e]);
     return att_key<BLK>(p, slot, jv);
   };
+  auto load_idx = [&](int ch) { return load_idx_at(ch, lane); };
   // Load r of a chunk: lane l fetches the segment stored in slot l % SEGS of
   // chunk row KPI*r + l / SEGS; the LDS address is the load's base + 16*l.
   // Loads go through buffer descriptors of this head's K and V rows with 32-bit
@@ -626,24 +628,84 @@ __device__ __forceinline__ void attend_row_mfma(const AttParams& p, const AttRow
   // this wave's chunks: c0, c0 + NSPLIT, ... (all of them when NSPLIT = 1)
   const int nmine = (nchunks > c0) ? (nchunks - c0 + NSPLIT - 1) / NSPLIT : 0;
   auto chunk_of = [&](int u) { return c0 + u * NSPLIT; };
+  // Live chunks: bit u of `live` is set when my chunk u holds a key to attend
+  // (a chunk wholly below the prefix, past the causal cut or past top_k loads
+  // nothing and leaves the state as it is).  The indices of the first 64 chunks
+  // are loaded up front, all at once, two chunks per load (lanes 32..63 take the
+  // odd one), so the loop below goes from live chunk to live chunk: a row whose
+  // filler and prefix empty half its chunks would otherwise wait out one index
+  // load per empty chunk with nothing else in flight.  Chunks from 64 on count
+  // as live and are checked when reached.
+  constexpr int kBatch = 8;  // chunk pairs per batch of loads
+  const int nmask = nmine < 64 ? nmine : 64;
+  uint64_t live = 0;
+  int jv[kBatch];
+#pragma unroll
+  for (int e = 0; e < kBatch; ++e) {
+    const int u = 2 * e + (lane >> 5);
+    jv[e] = u < nmask ? load_idx_at(chunk_of(u), lane & 31) : -1;
+  }
+#pragma unroll
+  for (int e = 0; e < kBatch; ++e) {
+    const uint64_t b = __ballot(chunk_ok(jv[e]));
+    live |= (static_cast<uint64_t>(static_cast<uint32_t>(b) != 0u) << (2 * e)) |
+            (static_cast<uint64_t>((b >> 32) != 0u) << (2 * e + 1));
+  }
+  for (int v0 = kBatch; 2 * v0 < nmask; v0 += kBatch) {
+    int jw[kBatch];
+#pragma unroll
+    for (int e = 0; e < kBatch; ++e) {
+      const int u = 2 * (v0 + e) + (lane >> 5);
+      jw[e] = u < nmask ? load_idx_at(chunk_of(u), lane & 31) : -1;
+    }
+#pragma unroll
+    for (int e = 0; e < kBatch; ++e) {
+      const uint64_t b = __ballot(chunk_ok(jw[e]));
+      live |= (static_cast<uint64_t>(static_cast<uint32_t>(b) != 0u) << (2 * (v0 + e))) |
+              (static_cast<uint64_t>((b >> 32) != 0u) << (2 * (v0 + e) + 1));
+    }
+  }
+  // first chunk after u to process, nmine when none is left
+  auto next_live = [&](int u) -> int {
+    const int v = u + 1;
+    if (v >= 64) return v < nmine ? v : nmine;
+    const uint64_t m = live & (~0ull << v);
+    if (m) return __builtin_ctzll(m);
+    return nmine > 64 ? 64 : nmine;
+  };
+  // indices of my chunk u (lanes < 32; -1 elsewhere), from the first batch's
+  // registers when it holds them (the first two live chunks; the loop reloads
+  // the later ones, which the loads above left in the caches)
+  auto chunk_idx = [&](int u) -> int {
+    if (u >= 2 * kBatch) return load_idx(chunk_of(u));
+    int x = jv[0];
+#pragma unroll
+    for (int e = 1; e < kBatch; ++e) x = (u >> 1) == e ? jv[e] : x;
+    const int y = __shfl_xor(x, 32);
+    return lane < kMfChunk ? ((u & 1) ? y : x) : -1;
+  };
+  int u = next_live(-1);
+  int un = nmine;  // the chunk whose indices j_next holds
   uint64_t okbits = 0;
   int j_next = -1;
-  if (nmine > 0) {
-    const int j0 = load_idx(chunk_of(0));
+  if (u < nmine) {
+    const int j0 = chunk_idx(u);
     const bool ok0 = chunk_ok(j0);
     okbits = __ballot(ok0);
     if (okbits) issue(ok0 ? j0 : -1, static_cast<uint32_t>(okbits) == 0xFFFFFFFFu);
-    if (nmine > 1) j_next = load_idx(chunk_of(1));
+    un = next_live(u);
+    if (un < nmine) j_next = chunk_idx(un);
   }
-  for (int u = 0; u < nmine; ++u) {
-    // A chunk with no key to attend (all below the prefix, past the causal cut
-    // or past top_k) loads nothing and leaves the state as it is.
+  while (u < nmine) {
+    // (only a chunk from 64 on can turn out empty here)
     if (okbits == 0) {
-      if (u + 1 < nmine) {
+      u = un;
+      if (u < nmine) {
         const bool okn = chunk_ok(j_next);
         okbits = __ballot(okn);
         if (okbits) issue(okn ? j_next : -1, static_cast<uint32_t>(okbits) == 0xFFFFFFFFu);
-        if (u + 2 < nmine) j_next = load_idx(chunk_of(u + 2));
+        un = next_live(u);
+        if (un < nmine) j_next = load_idx(chunk_of(un));
       }
       continue;
     }
@@ -669,11 +731,13 @@ __device__ __forceinline__ void attend_row_mfma(const AttParams& p, const AttRow
     __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
     const uint64_t okb = okbits;
     okbits = 0;
-    if (u + 1 < nmine) {
+    u = un;
+    if (u < nmine) {
       const bool okn = chunk_ok(j_next);
       okbits = __ballot(okn);
       if (okbits) issue(okn ? j_next : -1, static_cast<uint32_t>(okbits) == 0xFFFFFFFFu);
-      if (u + 2 < nmine) j_next = load_idx(chunk_of(u + 2));
+      un = next_live(u);
+      if (un < nmine) j_next = load_idx(chunk_of(un));
     }
 
     // Scores of eight keys of head c16 (keys 16t + 4*q4 + e).
