@@ -628,63 +628,10 @@ __device__ __forceinline__ void attend_row_mfma(const AttParams& p, const AttRow
   // this wave's chunks: c0, c0 + NSPLIT, ... (all of them when NSPLIT = 1)
   const int nmine = (nchunks > c0) ? (nchunks - c0 + NSPLIT - 1) / NSPLIT : 0;
   auto chunk_of = [&](int u) { return c0 + u * NSPLIT; };
-  // Live chunks: bit u of `live` is set when my chunk u holds a key to attend
-  // (a chunk wholly below the prefix, past the causal cut or past top_k loads
-  // nothing and leaves the state as it is).  The indices of the first 64 chunks
-  // are loaded up front, all at once, two chunks per load (lanes 32..63 take the
-  // odd one), so the loop below goes from live chunk to live chunk: a row whose
-  // filler and prefix empty half its chunks would otherwise wait out one index
-  // load per empty chunk with nothing else in flight.  Chunks from 64 on count
-  // as live and are checked when reached.
-  constexpr int kBatch = 8;  // chunk pairs per batch of loads
-  const int nmask = nmine < 64 ? nmine : 64;
-  uint64_t live = 0;
-  int jv[kBatch];
-#pragma unroll
-  for (int e = 0; e < kBatch; ++e) {
-    const int u = 2 * e + (lane >> 5);
-    jv[e] = u < nmask ? load_idx_at(chunk_of(u), lane & 31) : -1;
-  }
-#pragma unroll
-  for (int e = 0; e < kBatch; ++e) {
-    const uint64_t b = __ballot(chunk_ok(jv[e]));
-    live |= (static_cast<uint64_t>(static_cast<uint32_t>(b) != 0u) << (2 * e)) |
-            (static_cast<uint64_t>((b >> 32) != 0u) << (2 * e + 1));
-  }
-  for (int v0 = kBatch; 2 * v0 < nmask; v0 += kBatch) {
-    int jw[kBatch];
-#pragma unroll
-    for (int e = 0; e < kBatch; ++e) {
-      const int u = 2 * (v0 + e) + (lane >> 5);
-      jw[e] = u < nmask ? load_idx_at(chunk_of(u), lane & 31) : -1;
-    }
-#pragma unroll
-    for (int e = 0; e < kBatch; ++e) {
-      const uint64_t b = __ballot(chunk_ok(jw[e]));
-      live |= (static_cast<uint64_t>(static_cast<uint32_t>(b) != 0u) << (2 * (v0 + e))) |
-              (static_cast<uint64_t>((b >> 32) != 0u) << (2 * (v0 + e) + 1));
-    }
-  }
-  // first chunk after u to process, nmine when none is left
-  auto next_live = [&](int u) -> int {
-    const int v = u + 1;
-    if (v >= 64) return v < nmine ? v : nmine;
-    const uint64_t m = live & (~0ull << v);
-    if (m) return __builtin_ctzll(m);
-    return nmine > 64 ? 64 : nmine;
-  };
-  // indices of my chunk u (lanes < 32; -1 elsewhere), from the first batch's
-  // registers when it holds them (the first two live chunks; the loop reloads
-  // the later ones, which the loads above left in the caches)
-  auto chunk_idx = [&](int u) -> int {
-    if (u >= 2 * kBatch) return load_idx(chunk_of(u));
-    int x = jv[0];
-#pragma unroll
-    for (int e = 1; e < kBatch; ++e) x = (u >> 1) == e ? jv[e] : x;
-    const int y = __shfl_xor(x, 32);
-    return lane < kMfChunk ? ((u & 1) ? y : x) : -1;
-  };
-  int u = next_live(-1);
+  LiveChunks lc;
+  lc.build(nmine, lane, [&](int u, int l) { return load_idx_at(chunk_of(u), l); }, chunk_ok);
+  auto chunk_idx = [&](int u) { return lc.get(u, lane, [&](int v) { return load_idx(chunk_of(v)); }); };
+  int u = lc.next(-1);
   int un = nmine;  // the chunk whose indices j_next holds
   uint64_t okbits = 0;
   int j_next = -1;
@@ -693,7 +640,7 @@ __device__ __forceinline__ void attend_row_mfma(const AttParams& p, const AttRow
     const bool ok0 = chunk_ok(j0);
     okbits = __ballot(ok0);
     if (okbits) issue(ok0 ? j0 : -1, static_cast<uint32_t>(okbits) == 0xFFFFFFFFu);
-    un = next_live(u);
+    un = lc.next(u);
     if (un < nmine) j_next = chunk_idx(un);
   }
   while (u < nmine) {
@@ -704,7 +651,7 @@ __device__ __forceinline__ void attend_row_mfma(const AttParams& p, const AttRow
         const bool okn = chunk_ok(j_next);
         okbits = __ballot(okn);
         if (okbits) issue(okn ? j_next : -1, static_cast<uint32_t>(okbits) == 0xFFFFFFFFu);
-        un = next_live(u);
+        un = lc.next(u);
         if (un < nmine) j_next = load_idx(chunk_of(un));
       }
       continue;
@@ -736,7 +683,7 @@ __device__ __forceinline__ void attend_row_mfma(const AttParams& p, const AttRow
       const bool okn = chunk_ok(j_next);
       okbits = __ballot(okn);
       if (okbits) issue(okn ? j_next : -1, static_cast<uint32_t>(okbits) == 0xFFFFFFFFu);
-      un = next_live(u);
+      un = lc.next(u);
       if (un < nmine) j_next = load_idx(chunk_of(un));
     }
 

@@ -322,9 +322,9 @@ __global__ __launch_bounds__(64 * kBwMfWaves, 2) void sparse_attention_bwd_mfma_
   row_seg16<D>(lane, seg16);
   const int kswz = mf_swz<D>(c16);
   // key of chunk slot `lane` (lanes < 32), -1 past top_k, -2 out of range (flagged)
-  auto load_idx = [&](int ch) -> int {
-    const int slot = ch * kMfChunk + lane;
-    if (lane >= kMfChunk || slot >= p.top_k) return -1;
+  auto load_idx_at = [&](int ch, int l) -> int {
+    const int slot = ch * kMfChunk + l;
+    if (l >= kMfChunk || slot >= p.top_k) return -1;
     const int64_t j = p.idx_i64 ? reinterpret_cast<const int64_t*>(ib)[slot]
                                 : static_cast<int64_t>(reinterpret_cast<const int32_t*>(ib)[slot]);
     if (j < 0 || j >= p.n) {
@@ -333,6 +333,7 @@ __global__ __launch_bounds__(64 * kBwMfWaves, 2) void sparse_attention_bwd_mfma_
     }
     return static_cast<int>(j);
   };
+  auto load_idx = [&](int ch) { return load_idx_at(ch, lane); };
   auto chunk_ok = [&](int j) { return j >= 0 && !(p.causal && j > i); };
   auto read_k = [&](const unsigned char* l, bf16x8_t (&f)[2][KB]) {
 #pragma unroll
@@ -442,14 +443,23 @@ __global__ __launch_bounds__(64 * kBwMfWaves, 2) void sparse_attention_bwd_mfma_
     if (q4 >= 2) return bf16x8_t{};
     return *reinterpret_cast<const bf16x8_t*>(&hd_lds[DKDV ? wave : 0][which][16 * dt + c16][0]);
   };
-  int jc = nchunks > 0 ? load_idx(0) : -1;
-  uint64_t okn = __ballot(chunk_ok2(jc));
-  if (nchunks > 0) {
+  // only the chunks with a slot to differentiate (a chunk without one adds
+  // nothing to dQ, dK or dV)
+  LiveChunks lc;
+  lc.build(nchunks, lane, load_idx_at, chunk_ok2);
+  int u = lc.next(-1);
+  int un = nchunks;  // the chunk whose indices jn holds
+  int jc = -1, jn = -1;
+  uint64_t okn = 0;
+  if (u < nchunks) {
+    jc = lc.get(u, lane, load_idx);
+    okn = __ballot(chunk_ok2(jc));
     row_issue<D>(krs, kl, chunk_ok2(jc) ? jc : -1, lane, ksn2, seg16);
     row_issue<D>(vrs, vl, chunk_ok2(jc) ? jc : -1, lane, vsn2, seg16);
+    un = lc.next(u);
+    if (un < nchunks) jn = lc.get(un, lane, load_idx);
   }
-  int jn = nchunks > 1 ? load_idx(1) : -1;
-  for (int ch = 0; ch < nchunks; ++ch) {
+  while (u < nchunks) {
     __builtin_amdgcn_s_waitcnt(kWaitVm0);
     bf16x8_t kf[2][KB], vf[2][KB], kt[NT];
     read_k(kl, kf);
@@ -459,12 +469,14 @@ __global__ __launch_bounds__(64 * kBwMfWaves, 2) void sparse_attention_bwd_mfma_
     __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
     const uint64_t okb = okn;
     const int jcur = jc;
-    if (ch + 1 < nchunks) {
+    u = un;
+    if (u < nchunks) {
       okn = __ballot(chunk_ok2(jn));
       row_issue<D>(krs, kl, chunk_ok2(jn) ? jn : -1, lane, ksn2, seg16);
       row_issue<D>(vrs, vl, chunk_ok2(jn) ? jn : -1, lane, vsn2, seg16);
       jc = jn;
-      jn = ch + 2 < nchunks ? load_idx(ch + 2) : -1;
+      un = lc.next(u);
+      jn = un < nchunks ? load_idx(un) : -1;
     }
     float pr[8], ds[8];
 #pragma unroll

@@ -117,5 +117,69 @@ constexpr int kWaitVm0 = 0x0F70;
 constexpr int kWaitVmBase = 0x0F70;
 constexpr int kWaitLgkm0 = 0xC07F;
 
+// Which chunks (kMfChunk index slots each) of a row hold a key to attend.  A
+// row gathers its chunks one after the other, each chunk's loads flying while
+// the one before computes; a chunk with nothing to attend (below a dense
+// prefix, past the causal cut, filler) would still cost one index load's
+// latency with nothing else in flight.  build() loads the indices of the first
+// 64 chunks all at once, two chunks per load (lanes 32..63 take the odd one),
+// and sets bit u of `live` when a slot of chunk u passes ok(); chunks from 64
+// on count as live.  The first 16 chunks' indices stay in registers for get().
+struct LiveChunks {
+  static constexpr int kPairs = 8;  // chunk pairs per batch of loads
+  uint64_t live;
+  int n;  // chunks of the row
+  int first[kPairs];
+
+  // load_at(u, l): key of slot l of chunk u (negative when none);
+  // ok(key): the slot is attended
+  template <class LoadAt, class Ok>
+  __device__ __forceinline__ void build(int nch, int lane, LoadAt load_at, Ok ok) {
+    n = nch;
+    live = 0;
+    const int nmask = nch < 64 ? nch : 64;
+#pragma unroll
+    for (int e = 0; e < kPairs; ++e) {
+      const int u = 2 * e + (lane >> 5);
+      first[e] = u < nmask ? load_at(u, lane & 31) : -1;
+    }
+#pragma unroll
+    for (int e = 0; e < kPairs; ++e) add(e, __ballot(ok(first[e])));
+    for (int v0 = kPairs; 2 * v0 < nmask; v0 += kPairs) {
+      int jw[kPairs];
+#pragma unroll
+      for (int e = 0; e < kPairs; ++e) {
+        const int u = 2 * (v0 + e) + (lane >> 5);
+        jw[e] = u < nmask ? load_at(u, lane & 31) : -1;
+      }
+#pragma unroll
+      for (int e = 0; e < kPairs; ++e) add(v0 + e, __ballot(ok(jw[e])));
+    }
+  }
+  __device__ __forceinline__ void add(int pair, uint64_t b) {
+    live |= (static_cast<uint64_t>(static_cast<uint32_t>(b) != 0u) << (2 * pair)) |
+            (static_cast<uint64_t>((b >> 32) != 0u) << (2 * pair + 1));
+  }
+  // the first chunk after u to process, n when none is left
+  __device__ __forceinline__ int next(int u) const {
+    const int v = u + 1;
+    if (v >= 64) return v < n ? v : n;
+    const uint64_t m = live & (~0ull << v);
+    if (m) return __builtin_ctzll(m);
+    return n > 64 ? 64 : n;
+  }
+  // indices of chunk u in lanes < kMfChunk (-1 in the others): from the
+  // registers for the first 16 chunks, else load(u) (the caches hold them)
+  template <class Load>
+  __device__ __forceinline__ int get(int u, int lane, Load load) const {
+    if (u >= 2 * kPairs) return load(u);
+    int x = first[0];
+#pragma unroll
+    for (int e = 1; e < kPairs; ++e) x = (u >> 1) == e ? first[e] : x;
+    const int y = __shfl_xor(x, 32);
+    return lane < kMfChunk ? ((u & 1) ? y : x) : -1;
+  }
+};
+
 }  // namespace
 }  // namespace ssa
