@@ -559,16 +559,27 @@ __device__ __forceinline__ void attend_row_mfma(const AttParams& p, const AttRow
   const uint16_t* vbase = static_cast<const uint16_t*>(p.v) + bb * p.v_sb + static_cast<int64_t>(h) * p.v_sh;
   const int64_t ibase = bb * p.idx_sb + (BLK ? qr >> p.blk_log2 : qr) * p.idx_sn + static_cast<int64_t>(h) * p.idx_sh;
 
-  // Key of slot l of chunk ch (-1 past top_k, l >= kMfChunk or on a dropped row).
-  auto load_idx_at = [&](int ch, int l) -> int {
-    const int slot = ch * kMfChunk + l;
-    if (!row_ok || l >= kMfChunk || slot >= p.top_k) return -1;
-    const int e = BLK ? slot >> p.blk_log2 : slot;
-    const int64_t jv = p.idx_i64 ? static_cast<const int64_t*>(p.idx)[ibase + e]
-                                 : static_cast<int64_t>(static_cast<const int32_t*>(p.idx)[ibase + e]);
-    return att_key<BLK>(p, slot, jv);
+  // Index entry of slot l of chunk ch as loaded (int32 entries in the low
+  // word, slot 0's entry where slot_at drops the slot), and its key (-1 past top_k,
+  // l >= kMfChunk or on a dropped row).  Loading and checking apart keeps the
+  // check's wait away from the load: a batch of index loads goes out before
+  // the first check, and the next chunk's indices fly with its K/V gathers.
+  // (two dword loads with no branch on the index type: the low word, and the
+  // high word or, for int32 entries, the same word again)
+  auto slot_at = [&](int ch, int l) { return row_ok && l < kMfChunk && ch * kMfChunk + l < p.top_k; };
+  const int ewords = p.idx_i64 ? 2 : 1;
+  const uint32_t* iwords = static_cast<const uint32_t*>(p.idx) + ibase * ewords;
+  auto raw_at = [&](int ch, int l) -> uint64_t {
+    const int slot = slot_at(ch, l) ? ch * kMfChunk + l : 0;
+    const uint32_t* w = iwords + (BLK ? slot >> p.blk_log2 : slot) * ewords;
+    return (static_cast<uint64_t>(w[ewords - 1]) << 32) | w[0];
   };
-  auto load_idx = [&](int ch) { return load_idx_at(ch, lane); };
+  auto key_at = [&](int ch, int l, uint64_t raw) -> int {
+    const int64_t jv = p.idx_i64 ? static_cast<int64_t>(raw)
+                                 : static_cast<int64_t>(static_cast<int32_t>(static_cast<uint32_t>(raw)));
+    return slot_at(ch, l) ? att_key<BLK>(p, ch * kMfChunk + l, jv) : -1;
+  };
+  auto load_idx = [&](int ch) { return key_at(ch, lane, raw_at(ch, lane)); };
   // Load r of a chunk: lane l fetches the segment stored in slot l % SEGS of
   // chunk row KPI*r + l / SEGS; the LDS address is the load's base + 16*l.
   // Loads go through buffer descriptors of this head's K and V rows with 32-bit
@@ -629,31 +640,41 @@ __device__ __forceinline__ void attend_row_mfma(const AttParams& p, const AttRow
   const int nmine = (nchunks > c0) ? (nchunks - c0 + NSPLIT - 1) / NSPLIT : 0;
   auto chunk_of = [&](int u) { return c0 + u * NSPLIT; };
   LiveChunks lc;
-  lc.build(nmine, lane, [&](int u, int l) { return load_idx_at(chunk_of(u), l); }, chunk_ok);
-  auto chunk_idx = [&](int u) { return lc.get(u, lane, [&](int v) { return load_idx(chunk_of(v)); }); };
+  lc.build(nmine, lane, [&](int u, int l) { return raw_at(chunk_of(u), l); },
+           [&](int u, int l, uint64_t jv) { return key_at(chunk_of(u), l, jv); }, chunk_ok);
+  // The next live chunk's index entries (jn_raw, for chunk un) are loaded
+  // while the current chunk's gathers fly and checked only after the wait
+  // that the gathers need anyway.
   int u = lc.next(-1);
-  int un = nmine;  // the chunk whose indices j_next holds
+  int un = nmine;
   uint64_t okbits = 0;
-  int j_next = -1;
+  uint64_t jn_raw = 0;
   if (u < nmine) {
-    const int j0 = chunk_idx(u);
+    const int j0 = lc.get(u, lane, [&](int v) { return load_idx(chunk_of(v)); });
     const bool ok0 = chunk_ok(j0);
     okbits = __ballot(ok0);
     if (okbits) issue(ok0 ? j0 : -1, static_cast<uint32_t>(okbits) == 0xFFFFFFFFu);
     un = lc.next(u);
-    if (un < nmine) j_next = chunk_idx(un);
+    if (un < nmine) jn_raw = raw_at(chunk_of(un), lane);
   }
+  // u = un: issue chunk u from jn_raw and prefetch the indices of the live
+  // chunk after it
+  auto advance = [&]() {
+    u = un;
+    if (u < nmine) {
+      const int jn = key_at(chunk_of(u), lane, jn_raw);
+      const bool okn = chunk_ok(jn);
+      okbits = __ballot(okn);
+      if (okbits) issue(okn ? jn : -1, static_cast<uint32_t>(okbits) == 0xFFFFFFFFu);
+      un = lc.next(u);
+      if (un < nmine) jn_raw = raw_at(chunk_of(un), lane);
+    }
+  };
   while (u < nmine) {
     // (only a chunk from 64 on can turn out empty here)
     if (okbits == 0) {
-      u = un;
-      if (u < nmine) {
-        const bool okn = chunk_ok(j_next);
-        okbits = __ballot(okn);
-        if (okbits) issue(okn ? j_next : -1, static_cast<uint32_t>(okbits) == 0xFFFFFFFFu);
-        un = lc.next(u);
-        if (un < nmine) j_next = load_idx(chunk_of(un));
-      }
+      __builtin_amdgcn_s_waitcnt(kWaitVm0);
+      advance();
       continue;
     }
     // This chunk's rows are in LDS once its loads have completed.
@@ -678,14 +699,7 @@ __device__ __forceinline__ void attend_row_mfma(const AttParams& p, const AttRow
     __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
     const uint64_t okb = okbits;
     okbits = 0;
-    u = un;
-    if (u < nmine) {
-      const bool okn = chunk_ok(j_next);
-      okbits = __ballot(okn);
-      if (okbits) issue(okn ? j_next : -1, static_cast<uint32_t>(okbits) == 0xFFFFFFFFu);
-      un = lc.next(u);
-      if (un < nmine) j_next = load_idx(chunk_of(un));
-    }
+    advance();
 
     // Scores of eight keys of head c16 (keys 16t + 4*q4 + e).
     float sc[8];
@@ -701,7 +715,9 @@ __device__ __forceinline__ void attend_row_mfma(const AttParams& p, const AttRow
       for (int e = 0; e < 4; ++e) sc[4 * t + e] = s[e] * p.qk_scale_log2;
     }
     if (!full) {
-      const uint32_t mine = static_cast<uint32_t>(okb >> (4 * q4));  // bit 16t + e: key 16t + 4*q4 + e
+      // bit 16t + e: key 16t + 4*q4 + e ((lane >> 2) & 12 = 4*q4, recomputed here
+      // rather than kept live across the loop)
+      const uint32_t mine = static_cast<uint32_t>(okb) >> ((lane >> 2) & 12);
 #pragma unroll
       for (int t = 0; t < 2; ++t)
 #pragma unroll

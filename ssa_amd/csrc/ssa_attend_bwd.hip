@@ -284,6 +284,37 @@ __global__ __launch_bounds__(64 * kBwMfWaves, 2) void sparse_attention_bwd_mfma_
   const uint16_t* qh = static_cast<const uint16_t*>(p.q) + bb * p.q_sb + i * p.q_sn + static_cast<int64_t>(hq) * p.q_sh;
   const uint16_t* dh = static_cast<const uint16_t*>(p.dout) + bb * p.do_sb + i * p.do_sn + static_cast<int64_t>(hq) * p.do_sh;
   bf16x8_t qf[KB], df[KB];
+  // o of head hq at the same dims, in 16-byte loads that all go out before
+  // the first use (one branch on o's type around all of them)
+  float ov[KB][8];
+  {
+    const int64_t oo = bb * p.o_sb + i * p.o_sn + static_cast<int64_t>(hq) * p.o_sh + q4 * 8;
+    if (p.o_bf16) {
+      const uint16_t* ob = static_cast<const uint16_t*>(p.o) + oo;
+      uint4 w[KB];
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) w[kb] = col_ok ? *reinterpret_cast<const uint4*>(ob + kb * 32) : make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        const uint32_t ww[4] = {w[kb].x, w[kb].y, w[kb].z, w[kb].w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ov[kb][e] = __uint_as_float((e & 1) ? (ww[e >> 1] & 0xFFFF0000u) : (ww[e >> 1] << 16));
+      }
+    } else {
+      const float* of = static_cast<const float*>(p.o) + oo;
+      float4 w[KB][2];
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int x = 0; x < 2; ++x)
+          w[kb][x] = col_ok ? *reinterpret_cast<const float4*>(of + kb * 32 + 4 * x) : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        ov[kb][0] = w[kb][0].x, ov[kb][1] = w[kb][0].y, ov[kb][2] = w[kb][0].z, ov[kb][3] = w[kb][0].w;
+        ov[kb][4] = w[kb][1].x, ov[kb][5] = w[kb][1].y, ov[kb][6] = w[kb][1].z, ov[kb][7] = w[kb][1].w;
+      }
+    }
+  }
   float dpart = 0.0f;  // this lane's share of D = dO . o for head c16
 #pragma unroll
   for (int kb = 0; kb < KB; ++kb) {
@@ -296,7 +327,7 @@ __global__ __launch_bounds__(64 * kBwMfWaves, 2) void sparse_attention_bwd_mfma_
       const int dim = kb * 32 + q4 * 8 + e;
       const uint16_t qv = static_cast<uint16_t>((e & 1) ? (qw[e >> 1] >> 16) : (qw[e >> 1] & 0xFFFFu));
       const uint16_t dv = static_cast<uint16_t>((e & 1) ? (dw[e >> 1] >> 16) : (dw[e >> 1] & 0xFFFFu));
-      if (col_ok) dpart = fma_rn(bf16_bits_to_f32(dv), ld_any(p.o, bb * p.o_sb + i * p.o_sn + static_cast<int64_t>(hq) * p.o_sh + dim, p.o_bf16), dpart);
+      if (col_ok) dpart = fma_rn(bf16_bits_to_f32(dv), ov[kb][e], dpart);
       if (DKDV && c16 < 8) {  // head slots 0..7 of the [dim][head] copies (zero past g)
         hd_lds[DKDV ? wave : 0][0][dim][c16] = col_ok ? qv : static_cast<uint16_t>(0);
         hd_lds[DKDV ? wave : 0][1][dim][c16] = col_ok ? dv : static_cast<uint16_t>(0);
@@ -322,18 +353,27 @@ __global__ __launch_bounds__(64 * kBwMfWaves, 2) void sparse_attention_bwd_mfma_
   row_seg16<D>(lane, seg16);
   const int kswz = mf_swz<D>(c16);
   // key of chunk slot `lane` (lanes < 32), -1 past top_k, -2 out of range (flagged)
-  auto load_idx_at = [&](int ch, int l) -> int {
-    const int slot = ch * kMfChunk + l;
-    if (l >= kMfChunk || slot >= p.top_k) return -1;
-    const int64_t j = p.idx_i64 ? reinterpret_cast<const int64_t*>(ib)[slot]
-                                : static_cast<int64_t>(reinterpret_cast<const int32_t*>(ib)[slot]);
+  // (loading and checking apart: a batch of loads goes out before a check waits)
+  // (two dword loads with no branch on the index type: the low word, and the
+  // high word or, for int32 entries, the same word again)
+  auto slot_at = [&](int ch, int l) { return l < kMfChunk && ch * kMfChunk + l < p.top_k; };
+  const int ewords = p.idx_i64 ? 2 : 1;
+  auto raw_at = [&](int ch, int l) -> uint64_t {
+    const int slot = slot_at(ch, l) ? ch * kMfChunk + l : 0;
+    const uint32_t* w = reinterpret_cast<const uint32_t*>(ib) + slot * ewords;
+    return (static_cast<uint64_t>(w[ewords - 1]) << 32) | w[0];
+  };
+  auto key_at = [&](int ch, int l, uint64_t raw) -> int {
+    if (!slot_at(ch, l)) return -1;
+    const int64_t j = p.idx_i64 ? static_cast<int64_t>(raw)
+                                : static_cast<int64_t>(static_cast<int32_t>(static_cast<uint32_t>(raw)));
     if (j < 0 || j >= p.n) {
       if (p.err) p.err[0] = 1;
       return -2;
     }
     return static_cast<int>(j);
   };
-  auto load_idx = [&](int ch) { return load_idx_at(ch, lane); };
+  auto load_idx = [&](int ch) { return key_at(ch, lane, raw_at(ch, lane)); };
   auto chunk_ok = [&](int j) { return j >= 0 && !(p.causal && j > i); };
   auto read_k = [&](const unsigned char* l, bf16x8_t (&f)[2][KB]) {
 #pragma unroll
@@ -352,10 +392,10 @@ __global__ __launch_bounds__(64 * kBwMfWaves, 2) void sparse_attention_bwd_mfma_
   const float* fst = p.stats_in ? p.stats_in + (bh * p.n + i) * g * 2 : nullptr;
   const bool have_st = fst != nullptr && !__builtin_isnan(fst[0]);
   if (!have_st) {
-    int jn = nchunks > 0 ? load_idx(0) : -1;
-    uint64_t okn = __ballot(chunk_ok(jn));
-    if (nchunks > 0) row_issue<D>(krs, kl, chunk_ok(jn) ? jn : -1, lane, ksn2, seg16);
-    jn = nchunks > 1 ? load_idx(1) : -1;
+    const int j0 = nchunks > 0 ? load_idx(0) : -1;
+    uint64_t okn = __ballot(chunk_ok(j0));
+    if (nchunks > 0) row_issue<D>(krs, kl, chunk_ok(j0) ? j0 : -1, lane, ksn2, seg16);
+    uint64_t jn_raw = nchunks > 1 ? raw_at(1, lane) : 0;  // checked after the next wait
     for (int ch = 0; ch < nchunks; ++ch) {
       __builtin_amdgcn_s_waitcnt(kWaitVm0);
       bf16x8_t kf[2][KB];
@@ -363,9 +403,10 @@ __global__ __launch_bounds__(64 * kBwMfWaves, 2) void sparse_attention_bwd_mfma_
       __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
       const uint64_t okb = okn;
       if (ch + 1 < nchunks) {
+        const int jn = key_at(ch + 1, lane, jn_raw);
         okn = __ballot(chunk_ok(jn));
         row_issue<D>(krs, kl, chunk_ok(jn) ? jn : -1, lane, ksn2, seg16);
-        jn = ch + 2 < nchunks ? load_idx(ch + 2) : -1;
+        if (ch + 2 < nchunks) jn_raw = raw_at(ch + 2, lane);
       }
       float sc[8];
 #pragma unroll
@@ -445,11 +486,14 @@ __global__ __launch_bounds__(64 * kBwMfWaves, 2) void sparse_attention_bwd_mfma_
   };
   // only the chunks with a slot to differentiate (a chunk without one adds
   // nothing to dQ, dK or dV)
+  // The next live chunk's index entries (jn_raw, for chunk un) fly with the
+  // current chunk's gathers and are checked after the wait those need anyway.
   LiveChunks lc;
-  lc.build(nchunks, lane, load_idx_at, chunk_ok2);
+  lc.build(nchunks, lane, raw_at, key_at, chunk_ok2);
   int u = lc.next(-1);
-  int un = nchunks;  // the chunk whose indices jn holds
-  int jc = -1, jn = -1;
+  int un = nchunks;
+  int jc = -1;
+  uint64_t jn_raw = 0;
   uint64_t okn = 0;
   if (u < nchunks) {
     jc = lc.get(u, lane, load_idx);
@@ -457,7 +501,7 @@ __global__ __launch_bounds__(64 * kBwMfWaves, 2) void sparse_attention_bwd_mfma_
     row_issue<D>(krs, kl, chunk_ok2(jc) ? jc : -1, lane, ksn2, seg16);
     row_issue<D>(vrs, vl, chunk_ok2(jc) ? jc : -1, lane, vsn2, seg16);
     un = lc.next(u);
-    if (un < nchunks) jn = lc.get(un, lane, load_idx);
+    if (un < nchunks) jn_raw = raw_at(un, lane);
   }
   while (u < nchunks) {
     __builtin_amdgcn_s_waitcnt(kWaitVm0);
@@ -471,12 +515,13 @@ __global__ __launch_bounds__(64 * kBwMfWaves, 2) void sparse_attention_bwd_mfma_
     const int jcur = jc;
     u = un;
     if (u < nchunks) {
+      const int jn = key_at(u, lane, jn_raw);
       okn = __ballot(chunk_ok2(jn));
       row_issue<D>(krs, kl, chunk_ok2(jn) ? jn : -1, lane, ksn2, seg16);
       row_issue<D>(vrs, vl, chunk_ok2(jn) ? jn : -1, lane, vsn2, seg16);
       jc = jn;
       un = lc.next(u);
-      jn = un < nchunks ? load_idx(un) : -1;
+      if (un < nchunks) jn_raw = raw_at(un, lane);
     }
     float pr[8], ds[8];
 #pragma unroll
@@ -1431,15 +1476,18 @@ int launch_bwd_g(const BwdParams& p, hipStream_t st) {
 }
 
 // The matrix-core kernel: bf16 inputs and output gradient, d = 64 or 128,
-// g <= 8, q and dO rows 16-byte aligned, and K/V rows addressable by 32-bit
-// buffer offsets (rows below 2^31 bytes, n and byte strides below 2^24).
+// g <= 8, q, dO and o rows 16-byte aligned (strides in multiples of 8
+// elements), and K/V rows addressable by 32-bit buffer offsets (rows below
+// 2^31 bytes, n and byte strides below 2^24).
 bool bwd_mfma_ok(const BwdParams& p, const void* q, const void* dout) {
   const auto fits = [&](int64_t sn) {
     return sn >= 0 && 2 * sn < (int64_t(1) << 24) && (p.n - 1) * sn * 2 + 2 * p.d < (int64_t(1) << 31);
   };
   const bool aligned = (p.q_sb % 8 == 0) && (p.q_sn % 8 == 0) && (p.q_sh % 8 == 0) &&
                        (p.do_sb % 8 == 0) && (p.do_sn % 8 == 0) && (p.do_sh % 8 == 0) &&
-                       (reinterpret_cast<uintptr_t>(q) % 16 == 0) && (reinterpret_cast<uintptr_t>(dout) % 16 == 0);
+                       (p.o_sb % 8 == 0) && (p.o_sn % 8 == 0) && (p.o_sh % 8 == 0) &&
+                       (reinterpret_cast<uintptr_t>(q) % 16 == 0) && (reinterpret_cast<uintptr_t>(dout) % 16 == 0) &&
+                       (reinterpret_cast<uintptr_t>(p.o) % 16 == 0);
   return p.do_bf16 && (p.d == 64 || p.d == 128) && p.g <= 8 && aligned && p.n < (int64_t(1) << 24) &&
          fits(p.k_sn) && fits(p.v_sn);
 }

@@ -131,29 +131,39 @@ struct LiveChunks {
   int n;  // chunks of the row
   int first[kPairs];
 
-  // load_at(u, l): key of slot l of chunk u (negative when none);
+  // raw(u, l): index entry of slot l of chunk u, as loaded (any value where
+  // key() drops the slot); key(u, l, entry): its key, negative when none
+  // (checks and flags happen here, after all loads of a batch are out);
   // ok(key): the slot is attended
-  template <class LoadAt, class Ok>
-  __device__ __forceinline__ void build(int nch, int lane, LoadAt load_at, Ok ok) {
+  template <class Raw, class Key, class Ok>
+  __device__ __forceinline__ void build(int nch, int lane, Raw raw, Key key, Ok ok) {
     n = nch;
     live = 0;
     const int nmask = nch < 64 ? nch : 64;
+    uint64_t rv[kPairs];
 #pragma unroll
     for (int e = 0; e < kPairs; ++e) {
       const int u = 2 * e + (lane >> 5);
-      first[e] = u < nmask ? load_at(u, lane & 31) : -1;
+      rv[e] = u < nmask ? raw(u, lane & 31) : 0;
+    }
+#pragma unroll
+    for (int e = 0; e < kPairs; ++e) {
+      const int u = 2 * e + (lane >> 5);
+      first[e] = u < nmask ? key(u, lane & 31, rv[e]) : -1;
     }
 #pragma unroll
     for (int e = 0; e < kPairs; ++e) add(e, __ballot(ok(first[e])));
     for (int v0 = kPairs; 2 * v0 < nmask; v0 += kPairs) {
-      int jw[kPairs];
 #pragma unroll
       for (int e = 0; e < kPairs; ++e) {
         const int u = 2 * (v0 + e) + (lane >> 5);
-        jw[e] = u < nmask ? load_at(u, lane & 31) : -1;
+        rv[e] = u < nmask ? raw(u, lane & 31) : 0;
       }
 #pragma unroll
-      for (int e = 0; e < kPairs; ++e) add(v0 + e, __ballot(ok(jw[e])));
+      for (int e = 0; e < kPairs; ++e) {
+        const int u = 2 * (v0 + e) + (lane >> 5);
+        add(v0 + e, __ballot(ok(u < nmask ? key(u, lane & 31, rv[e]) : -1)));
+      }
     }
   }
   __device__ __forceinline__ void add(int pair, uint64_t b) {
