@@ -803,6 +803,13 @@ __global__ __launch_bounds__(64) void select_light_kernel(SelParams p, int64_t r
   };
   // Buckets kLightBatch at a time: their postings are loaded together, then
   // marked (the bitmap, the counts and the summary do not depend on the order).
+  // Buffer descriptors of this (batch, kv head)'s postings (the host keeps
+  // them below 2^31 entries); no tail index: an empty range.
+  const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<int32_t*>(pp), 0, static_cast<int>(min(p.post_bh * 4, int64_t(0x7FFFFFFF))), kBufferWord3);
+  const __amdgpu_buffer_rsrc_t trs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<int32_t*>(tp ? tp : pp), 0, tp ? static_cast<int>(min(p.tail_bh * 4, int64_t(0x7FFFFFFF))) : 0,
+      kBufferWord3);
   for (int m0 = 0; m0 < p.nseg; m0 += kLightBatch) {
     int lo_u[kLightBatch], len_u[kLightBatch], most = 0;
 #pragma unroll
@@ -812,15 +819,18 @@ __global__ __launch_bounds__(64) void select_light_kernel(SelParams p, int64_t r
       most = max(most, len_u[u]);
     }
     for (int base = 0; base < most; base += 64) {
+      // Every lane loads, with no branch (past a bucket's end it reloads the
+      // bucket's last posting; an empty bucket reads out of the buffer's range,
+      // which loads 0), so all kLightBatch loads are out before the first add.
       int32_t j_u[kLightBatch];
 #pragma unroll
-      for (int u = 0; u < kLightBatch; ++u)
-        j_u[u] = (base + lane < len_u[u]) ? (m0 + u < p.a ? pp[lo_u[u] + base + lane]
-                                                          : tp[lo_u[u] + base + lane] + p.tail_key0)
-                                          : -1;
+      for (int u = 0; u < kLightBatch; ++u) {
+        const int e = lo_u[u] + min(base + lane, len_u[u] - 1);
+        j_u[u] = __builtin_amdgcn_raw_buffer_load_b32(m0 + u < p.a ? prs : trs, e * 4, 0, 0);
+      }
 #pragma unroll
       for (int u = 0; u < kLightBatch; ++u)
-        if (base + lane < len_u[u]) add(j_u[u]);
+        if (base + lane < len_u[u]) add(m0 + u < p.a ? j_u[u] : j_u[u] + p.tail_key0);
     }
   }
   int C = 0, raw = 0;
@@ -1151,16 +1161,25 @@ __global__ __launch_bounds__(64 * kScrWaves) void select_pick_kernel(SelParams p
     const int64_t bb = bh / p.h_kv;
     const int R = (C + 63) / 64;  // positions lane + 64 r, r < R
 
-    // The row's scores into LDS (coalesced), with their range.
+    // The row's scores into LDS (coalesced), with their range: eight loads at
+    // a time, all out before the first is used (positions past C reload score
+    // C - 1, C >= 1 for a listed row).
     float amin = INFINITY, amax = -INFINITY;
-#pragma unroll 8
-    for (int r = 0; r < R; ++r) {
-      const int pos = lane + 64 * r;
-      const float a = (pos < C) ? w.approx[off + pos] : -INFINITY;
-      av[pos] = a;
-      if (pos < C) {
-        amin = fminf(amin, a);
-        amax = fmaxf(amax, a);
+    for (int r0 = 0; r0 < R; r0 += 8) {
+      float a8[8];
+#pragma unroll
+      for (int t = 0; t < 8; ++t) a8[t] = w.approx[off + min(lane + 64 * (r0 + t), C - 1)];
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const int pos = lane + 64 * (r0 + t);
+        if (r0 + t < R) {
+          const float a = (pos < C) ? a8[t] : -INFINITY;
+          av[pos] = a;
+          if (pos < C) {
+            amin = fminf(amin, a);
+            amax = fmaxf(amax, a);
+          }
+        }
       }
     }
 #pragma unroll
