@@ -614,9 +614,11 @@ __global__ __launch_bounds__(64 * kBwMfWaves, 2) void sparse_attention_bwd_mfma_
 constexpr int kPbWaves = 8;
 
 // DQ: dq only (the bucket kernel's prefix mode adds dk and dv): 4 rows per
-// block and no [key][query vector] staging, for 3 blocks per CU.
+// block and no [key][query vector] staging, for 4 blocks per CU (at most 128
+// registers at d = 128, a few of them in scratch).
 template <int D, bool DQ>
-__global__ __launch_bounds__(64 * (DQ ? 4 : kPbWaves), 1) void prefix_attention_bwd_kernel(BwdParams p) {
+__global__ __launch_bounds__(64 * (DQ ? 4 : kPbWaves)) __attribute__((amdgpu_waves_per_eu(DQ ? 4 : 1, 8))) void
+prefix_attention_bwd_kernel(BwdParams p) {
   using S = MfShape<D>;
   constexpr int KB = S::KB, NT = S::NT;
   constexpr int W = DQ ? 4 : kPbWaves;  // rows (waves) per block

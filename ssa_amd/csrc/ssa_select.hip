@@ -982,7 +982,10 @@ __device__ __forceinline__ ScrEntry scr_entry(const SelParams& p, const SelWs& w
 }
 
 template <int D, int GMAX>
-__global__ __launch_bounds__(64 * kScrWaves) void select_screen_kernel(SelParams p, SelWs w) {
+// (4 waves per SIMD: at most 128 registers, which the d = 128 build meets
+// without spilling)
+__global__ __launch_bounds__(64 * kScrWaves) __attribute__((amdgpu_waves_per_eu(4, 8))) void
+select_screen_kernel(SelParams p, SelWs w) {
   using S = MfShape<D>;
   __shared__ __align__(16) unsigned char kst[kScrWaves][kMfChunk * S::ROW];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
