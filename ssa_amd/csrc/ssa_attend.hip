@@ -495,11 +495,11 @@ __global__ __launch_bounds__(kAttThreads, (AttMinBlocks<T, D, GMAX>::value)) voi
 // bytes in flight per CU are LDS-bound; the waves share nothing, so one-wave
 // blocks let a CU hold 10 of them (160 KB) and start each as soon as one ends
 // (c3 stage d: 3.90 ms against 4.04 with four-wave blocks, 3.95 with two).
-// At least 3 waves per SIMD (at most 168 VGPRs at d = 128, no spills) so the
-// LDS, not the register file, sets the 10 waves per CU (c3 stage d 3.45 ->
-// 3.29 ms against 2 waves per SIMD at 176 VGPRs).
+// At least 2 waves per SIMD.  Forcing 3 (168 VGPRs at d = 128, so that the
+// LDS's 10 waves per CU are the limit) helped only while the loop stalled on
+// its index loads; with those fixed it costs 0.5 ms at c5 and gains nothing at c3.
 constexpr int kMfWaves = 1;
-constexpr int kMfMinWavesPerEu = 3;
+constexpr int kMfMinWavesPerEu = 2;
 
 // Issue one chunk's K and V loads: load r moves chunk rows KPI*r .. KPI*r +
 // KPI - 1 into LDS at base + r KB, lane l fetching the segment of row KPI*r +
@@ -640,8 +640,11 @@ __device__ __forceinline__ void attend_row_mfma(const AttParams& p, const AttRow
   const int nmine = (nchunks > c0) ? (nchunks - c0 + NSPLIT - 1) / NSPLIT : 0;
   auto chunk_of = [&](int u) { return c0 + u * NSPLIT; };
   LiveChunks lc;
-  lc.build(nmine, lane, [&](int u, int l) { return raw_at(chunk_of(u), l); },
-           [&](int u, int l, uint64_t jv) { return key_at(chunk_of(u), l, jv); }, chunk_ok);
+  if (xpre > 0)
+    lc.build(nmine, lane, [&](int u, int l) { return raw_at(chunk_of(u), l); },
+             [&](int u, int l, uint64_t jv) { return key_at(chunk_of(u), l, jv); }, chunk_ok);
+  else
+    lc.all_live(nmine);
   // The next live chunk's index entries (jn_raw, for chunk un) are loaded
   // while the current chunk's gathers fly and checked only after the wait
   // that the gathers need anyway.
@@ -671,7 +674,7 @@ __device__ __forceinline__ void attend_row_mfma(const AttParams& p, const AttRow
     }
   };
   while (u < nmine) {
-    // (only a chunk from 64 on can turn out empty here)
+    // (only a chunk past the mask can turn out empty here)
     if (okbits == 0) {
       __builtin_amdgcn_s_waitcnt(kWaitVm0);
       advance();

@@ -489,7 +489,8 @@ __global__ __launch_bounds__(64 * kBwMfWaves, 2) void sparse_attention_bwd_mfma_
   // The next live chunk's index entries (jn_raw, for chunk un) fly with the
   // current chunk's gathers and are checked after the wait those need anyway.
   LiveChunks lc;
-  lc.build(nchunks, lane, raw_at, key_at, chunk_ok2);
+  if (xpre > 0) lc.build(nchunks, lane, raw_at, key_at, chunk_ok2);
+  else lc.all_live(nchunks);
   int u = lc.next(-1);
   int un = nchunks;
   int jc = -1;

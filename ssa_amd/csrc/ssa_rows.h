@@ -122,13 +122,16 @@ constexpr int kWaitLgkm0 = 0xC07F;
 // the one before computes; a chunk with nothing to attend (below a dense
 // prefix, past the causal cut, filler) would still cost one index load's
 // latency with nothing else in flight.  build() loads the indices of the first
-// 64 chunks all at once, two chunks per load (lanes 32..63 take the odd one),
-// and sets bit u of `live` when a slot of chunk u passes ok(); chunks from 64
-// on count as live.  The first 16 chunks' indices stay in registers for get().
+// 16 chunks all at once, two chunks per load (lanes 32..63 take the odd one),
+// and sets bit u of `live` when a slot of chunk u passes ok(); chunks from 16
+// on count as live (a second batch would put a second load latency in front of
+// every row, which rows without filler, the common case at top_k 1024, never
+// repay).  The 16 chunks' indices stay in registers for get().
 struct LiveChunks {
   static constexpr int kPairs = 8;  // chunk pairs per batch of loads
   uint64_t live;
-  int n;  // chunks of the row
+  int n;   // chunks of the row
+  int nm;  // chunks the mask covers
   int first[kPairs];
 
   // raw(u, l): index entry of slot l of chunk u, as loaded (any value where
@@ -138,51 +141,46 @@ struct LiveChunks {
   template <class Raw, class Key, class Ok>
   __device__ __forceinline__ void build(int nch, int lane, Raw raw, Key key, Ok ok) {
     n = nch;
+    nm = nch < 2 * kPairs ? nch : 2 * kPairs;
     live = 0;
-    const int nmask = nch < 64 ? nch : 64;
     uint64_t rv[kPairs];
 #pragma unroll
     for (int e = 0; e < kPairs; ++e) {
       const int u = 2 * e + (lane >> 5);
-      rv[e] = u < nmask ? raw(u, lane & 31) : 0;
+      rv[e] = u < nm ? raw(u, lane & 31) : 0;
     }
 #pragma unroll
     for (int e = 0; e < kPairs; ++e) {
       const int u = 2 * e + (lane >> 5);
-      first[e] = u < nmask ? key(u, lane & 31, rv[e]) : -1;
+      first[e] = u < nm ? key(u, lane & 31, rv[e]) : -1;
     }
 #pragma unroll
-    for (int e = 0; e < kPairs; ++e) add(e, __ballot(ok(first[e])));
-    for (int v0 = kPairs; 2 * v0 < nmask; v0 += kPairs) {
-#pragma unroll
-      for (int e = 0; e < kPairs; ++e) {
-        const int u = 2 * (v0 + e) + (lane >> 5);
-        rv[e] = u < nmask ? raw(u, lane & 31) : 0;
-      }
-#pragma unroll
-      for (int e = 0; e < kPairs; ++e) {
-        const int u = 2 * (v0 + e) + (lane >> 5);
-        add(v0 + e, __ballot(ok(u < nmask ? key(u, lane & 31, rv[e]) : -1)));
-      }
+    for (int e = 0; e < kPairs; ++e) {
+      const uint64_t b = __ballot(ok(first[e]));
+      live |= (static_cast<uint64_t>(static_cast<uint32_t>(b) != 0u) << (2 * e)) |
+              (static_cast<uint64_t>((b >> 32) != 0u) << (2 * e + 1));
     }
   }
-  __device__ __forceinline__ void add(int pair, uint64_t b) {
-    live |= (static_cast<uint64_t>(static_cast<uint32_t>(b) != 0u) << (2 * pair)) |
-            (static_cast<uint64_t>((b >> 32) != 0u) << (2 * pair + 1));
+  // no mask: every chunk counts as live (rows without a dense prefix, whose
+  // chunks all hold selected keys)
+  __device__ __forceinline__ void all_live(int nch) {
+    n = nch;
+    nm = 0;
+    live = 0;
   }
   // the first chunk after u to process, n when none is left
   __device__ __forceinline__ int next(int u) const {
     const int v = u + 1;
-    if (v >= 64) return v < n ? v : n;
+    if (v >= nm) return v < n ? v : n;
     const uint64_t m = live & (~0ull << v);
     if (m) return __builtin_ctzll(m);
-    return n > 64 ? 64 : n;
+    return nm < n ? nm : n;
   }
   // indices of chunk u in lanes < kMfChunk (-1 in the others): from the
-  // registers for the first 16 chunks, else load(u) (the caches hold them)
+  // registers for the chunks the mask covers, else load(u)
   template <class Load>
   __device__ __forceinline__ int get(int u, int lane, Load load) const {
-    if (u >= 2 * kPairs) return load(u);
+    if (u >= nm) return load(u);
     int x = first[0];
 #pragma unroll
     for (int e = 1; e < kPairs; ++e) x = (u >> 1) == e ? first[e] : x;
