@@ -1194,8 +1194,10 @@ bucket_attention_bwd_kernel(BwdParams p, BucketParams bp) {
       const_cast<uint16_t*>(kbase), 0, static_cast<int>((p.n - 1) * p.k_sn * 2 + 2 * D), kBufferWord3);
   const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(vbase), 0, static_cast<int>((p.n - 1) * p.v_sn * 2 + 2 * D), kBufferWord3);
-  uint32_t seg16[S::SWZ_PERIOD];
-  row_seg16<D>(lane, seg16);
+  // this lane's segment offset in every load the wave issues: loads r = wave
+  // + 4x (prologue) and r = wave (rows) share r mod SWZ_PERIOD (2 or 4)
+  const uint32_t sgw = static_cast<uint32_t>(
+      ((lane % S::SEGS) ^ mf_swz<D>(S::KPI * (wave % S::SWZ_PERIOD) + lane / S::SEGS)) << 4);
   constexpr int KVL = (S::NLD + kBkThreads / 64 - 1) / (kBkThreads / 64);  // K/V loads per wave
   int jl[KVL];
 #pragma unroll
@@ -1208,7 +1210,7 @@ bucket_attention_bwd_kernel(BwdParams p, BucketParams bp) {
     const int r = wave + x * (kBkThreads / 64);
     if (r >= S::NLD) break;
     const int j = jl[x];
-    const uint32_t sg = seg16[r % S::SWZ_PERIOD];
+    const uint32_t sg = sgw;
     const uint32_t ko = j >= 0 ? __umul24(static_cast<uint32_t>(j), ksn2) + sg : kOobOffset;
     const uint32_t vo = j >= 0 ? __umul24(static_cast<uint32_t>(j), vsn2) + sg : kOobOffset;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_void_ptr)(kvs[0] + r * 1024), 16, static_cast<int>(ko), 0, 0, 0);
@@ -1230,7 +1232,7 @@ bucket_attention_bwd_kernel(BwdParams p, BucketParams bp) {
       const int rho = qv >> gpl, hh = qv & gmask;
       const int i = s_meta[bf][rho].x;
       const bool ok = rho < rpc && i >= 0 && hh < g;
-      const uint32_t sg = seg16[wave % S::SWZ_PERIOD];
+      const uint32_t sg = sgw;
       const uint32_t qo = ok ? static_cast<uint32_t>((i * p.q_sn + hh * p.q_sh) * 2) + sg : kOobOffset;
       const uint32_t dof = ok ? static_cast<uint32_t>((i * p.do_sn + hh * p.do_sh) * 2) + sg : kOobOffset;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(qrs, (lds_void_ptr)(qds[bf][0] + wave * 1024), 16, static_cast<int>(qo), 0, 0, 0);
@@ -1240,11 +1242,15 @@ bucket_attention_bwd_kernel(BwdParams p, BucketParams bp) {
   // stats, query codes and bitmap words of chunk rows s_meta[bf], into registers
   float4 st_r = make_float4(0.f, 0.f, 0.f, 0.f);
   int qc_r[2] = {-1, -1};
-  int qrho[2] = {kBkQv, kBkQv};
   uint32_t bw_r[2] = {0u, 0u};
   auto load_rows = [&](int bf) {
-    if (tid < kBkQv) {
-      const int rho = tid >> gpl, hh = tid & gmask;
+    // (the candidate build makes the thread index opaque per call: its per-lane
+    // address terms are recomputed here instead of hoisted out of the row loop
+    // and spilled)
+    int tidv = tid;
+    if constexpr (!PFX) asm volatile("" : "+v"(tidv));
+    if (tidv < kBkQv) {
+      const int rho = tidv >> gpl, hh = tidv & gmask;
       const int i = s_meta[bf][rho].x;
       st_r = (rho < rpc && i >= 0 && hh < g)
                  ? *reinterpret_cast<const float4*>(p.pstats + ((bh * p.n + i) * g + hh) * 4)
@@ -1253,15 +1259,13 @@ bucket_attention_bwd_kernel(BwdParams p, BucketParams bp) {
     if constexpr (PFX) return;
 #pragma unroll
     for (int x = 0; x < 2; ++x) {
-      const int e = tid + kBkThreads * x;
+      const int e = tidv + kBkThreads * x;
       const int rho = e / bp.a, aa = e - rho * bp.a;
       qc_r[x] = -1;
-      qrho[x] = kBkQv;
       if (rho < rpc) {
         const int i = s_meta[bf][rho].x;
         if (i >= 0) {
           qc_r[x] = bp.qcodes[(bh * p.n + i) * bp.a + aa];
-          qrho[x] = rho;
         }
       }
       const int rk = e >> 5, kappa = e & 31;
@@ -1277,13 +1281,15 @@ bucket_attention_bwd_kernel(BwdParams p, BucketParams bp) {
   auto store_rows = [&](int bf) {
     if (tid < kBkQv) *reinterpret_cast<float4*>(&s_st[bf][tid][0]) = st_r;
     if constexpr (PFX) return;
+    int tidv = tid;  // (opaque, as in load_rows)
+    asm volatile("" : "+v"(tidv));
 #pragma unroll
     for (int x = 0; x < 2; ++x) {
-      const int e = tid + kBkThreads * x;
+      const int e = tidv + kBkThreads * x;
       const int rk = e >> 5;
       if (rk < rpc) s_bw[bf][rk][e & 31] = bw_r[x];
       const int code = qc_r[x];
-      if (qrho[x] < kBkQv && code >= 0 && code < c) {
+      if (code >= 0 && code < c) {  // (code -1: no such row)
         int slot = bk_hash(code);
         uint32_t m = 0u;
         for (int probe = 0; probe < kBkHash; ++probe) {
@@ -1295,16 +1301,18 @@ bucket_attention_bwd_kernel(BwdParams p, BucketParams bp) {
           if (k2 == -1) break;
           slot = (slot + 1) & (kBkHash - 1);
         }
-        if (m) atomicOr(&s_dup[bf][qrho[x]], m);
+        if (m) atomicOr(&s_dup[bf][e / bp.a], m);
       }
     }
   };
   // which (row, key) pairs of chunk bf this item counts -> s_mask
   auto make_mask = [&](int bf) {
+    int tidv = tid;  // (opaque in the candidate build, as in load_rows)
+    if constexpr (!PFX) asm volatile("" : "+v"(tidv));
 #pragma unroll
     for (int x = 0; x < 2; ++x) {
       if (x == 1 && rpc * kBkKeys <= kBkThreads) break;
-      const int pr = tid + kBkThreads * x;
+      const int pr = tidv + kBkThreads * x;
       const int rho = pr >> 5, kappa = pr & 31;
       bool ok = false;
       if (rho < rpc) {
@@ -1384,7 +1392,7 @@ bucket_attention_bwd_kernel(BwdParams p, BucketParams bp) {
     const bool act = keys_here && ((hm >> (16 * t)) & 0xFFFFu) != 0;
     bf16x8_t qa[KB], da[KB];
     uint2 ad[DT], aq[DT];
-    float4 stv[4];
+    float3 stv[4];  // softmax reference, 1/sum, D (the stats' fourth float is unused)
     bool okv[4];
     if (act) {
       const unsigned char* ql = qds[bf][0];
@@ -1402,7 +1410,7 @@ bucket_attention_bwd_kernel(BwdParams p, BucketParams bp) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int qv = 4 * q4 + e;
-        stv[e] = *reinterpret_cast<const float4*>(&s_st[bf][qv][0]);
+        stv[e] = make_float3(s_st[bf][qv][0], s_st[bf][qv][1], s_st[bf][qv][2]);
         okv[e] = (qv & gmask) < g && (s_mask[qv >> gpl] & keybit) != 0;
       }
     }
