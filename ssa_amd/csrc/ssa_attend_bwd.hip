@@ -614,7 +614,13 @@ __global__ __launch_bounds__(64 * kBwMfWaves, 2) void sparse_attention_bwd_mfma_
 // of one per row.
 constexpr int kPbWaves = 8;
 
-// DQ: dq only (the bucket kernel's prefix mode adds dk and dv): 4 rows per
+// Rows per wave: the dq-only build packs 8 / g rows into a wave's 8 query
+// vector columns (column c: row c / g, head c % g; the low parts of dS then
+// fill columns 8 .. 15), so the block's K/V chunks and each MFMA serve 8 / g
+// rows instead of one; the full build keeps one row per wave.
+__host__ __device__ inline int pb_rows_per_wave(int g, bool dq) { return dq && g < 8 ? 8 / g : 1; }
+
+// DQ: dq only (the bucket kernel's prefix mode adds dk and dv): 4 waves per
 // block and no [key][query vector] staging, for 4 blocks per CU (at most 128
 // registers at d = 128, a few of them in scratch).
 template <int D, bool DQ>
@@ -634,18 +640,21 @@ prefix_attention_bwd_kernel(BwdParams p) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int q4 = lane >> 4, c16 = lane & 15;
   const int g = p.g;
-  const int64_t tiles = ceil_div(p.n, W);
+  const int rpw = pb_rows_per_wave(g, DQ);  // rows per wave
+  const int qvw = rpw * g;                  // query vector columns per wave (<= 8)
+  const int64_t tiles = ceil_div(p.n, static_cast<int64_t>(W) * rpw);
   const int64_t nblk = (p.rows / p.n) * tiles;
   const int64_t blk = xcd_block(blockIdx.x, xcd_per(nblk));
   if (blk >= nblk) return;
   const int64_t bh = blk / tiles;
-  const int64_t i = (blk - bh * tiles) * W + wave;  // this wave's row
+  const bool col_ok = c16 < qvw;
+  const int rr = col_ok ? c16 / g : 0, hh = col_ok ? c16 - rr * g : 0;  // this column's row in the wave, head
+  const int64_t i = ((blk - bh * tiles) * W + wave) * rpw + rr;  // this column's row
   const bool row_ok = i < p.n;
   const int h = static_cast<int>(bh % p.h_kv);
   const int64_t bb = bh / p.h_kv;
-  const bool col_ok = c16 < g;
   const int xcap = static_cast<int>(min(static_cast<int64_t>(p.top_k), p.n));
-  const int xrow = row_ok ? min(max(p.pfx[bh * p.n + i], 0), xcap) : 0;
+  const int xrow = (row_ok && col_ok) ? min(max(p.pfx[bh * p.n + i], 0), xcap) : 0;
 
   // the block's Q and dO as [dim][qv], zero for unused query vectors (whose P
   // and dS columns stay zero too: the reductions run over whole 32-column blocks)
@@ -655,8 +664,13 @@ prefix_attention_bwd_kernel(BwdParams p) {
   }
   if (tid == 0) s_xmax = 0;
   __syncthreads();
-  if (lane == 0) atomicMax(&s_xmax, xrow);
-  const int hq = h * g + (col_ok ? c16 : 0);
+  {
+    int xm = xrow;  // the wave's largest X (lanes 0..15 cover its columns)
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) xm = max(xm, __shfl_xor(xm, o));
+    if (lane == 0) atomicMax(&s_xmax, xm);
+  }
+  const int hq = h * g + hh;
   const uint16_t* qh = static_cast<const uint16_t*>(p.q) + bb * p.q_sb + (row_ok ? i : 0) * p.q_sn +
                        static_cast<int64_t>(hq) * p.q_sh;
   const uint16_t* dh = static_cast<const uint16_t*>(p.dout) + bb * p.do_sb + (row_ok ? i : 0) * p.do_sn +
@@ -682,7 +696,7 @@ prefix_attention_bwd_kernel(BwdParams p) {
   }
   float mref = 0.0f, inv_l = 0.0f, dcol = 0.0f;
   if (have) {
-    const float* ps = p.pstats + ((bh * p.n + i) * g + c16) * 4;
+    const float* ps = p.pstats + ((bh * p.n + i) * g + hh) * 4;
     mref = ps[0];
     inv_l = ps[1];
     dcol = ps[2];
@@ -717,8 +731,8 @@ prefix_attention_bwd_kernel(BwdParams p) {
     }
   };
   const int ilim = p.causal ? static_cast<int>(min(i, static_cast<int64_t>(0x7FFFFFFF))) : 0x7FFFFFFF;
-  const bool hi_row = c16 < g;
-  const bool lo_row = c16 >= 8 && c16 < 8 + g;
+  const bool hi_row = c16 < qvw;
+  const bool lo_row = c16 >= 8 && c16 < 8 + qvw;
   floatx4_t dqacc[NT];
 #pragma unroll
   for (int t = 0; t < NT; ++t) dqacc[t] = floatx4_t{0.f, 0.f, 0.f, 0.f};
@@ -829,7 +843,7 @@ prefix_attention_bwd_kernel(BwdParams p) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) dqacc[t][e] += dpp_from_plus8(dqacc[t][e]);
   if (!have || !hi_row) return;
-  float* dqb = p.dq + ((bb * p.n + i) * p.h_q + h * g + c16) * p.d + 4 * q4;
+  float* dqb = p.dq + ((bb * p.n + i) * p.h_q + h * g + hh) * p.d + 4 * q4;
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     float4 cur = *reinterpret_cast<float4*>(dqb + 16 * t);
@@ -1539,7 +1553,8 @@ int launch_bwd(const BwdParams& p, hipStream_t st) {
       if (int s = check_launch("sparse_attention_bwd_mfma_kernel")) return s;
       if (!p.pfx) return SSA_OK;
       const int w = p.pfx_dq_only ? 4 : kPbWaves;
-      const dim3 pgrid(static_cast<unsigned>(kXcds * xcd_per((p.rows / p.n) * ceil_div(p.n, w))));
+      const int64_t brows = static_cast<int64_t>(w) * pb_rows_per_wave(p.g, p.pfx_dq_only != 0);  // rows per block
+      const dim3 pgrid(static_cast<unsigned>(kXcds * xcd_per((p.rows / p.n) * ceil_div(p.n, brows))));
       if (p.pfx_dq_only) {
         if (p.d == 64)
           prefix_attention_bwd_kernel<64, true><<<pgrid, 64 * w, 0, st>>>(p);
