@@ -698,11 +698,13 @@ __device__ __forceinline__ void merge_top_desc(float (&v)[N], const float (&w)[N
 
 // Top <= 4 fits 128 VGPRs and 36 KB of LDS: 4 blocks per CU, so the grid of a
 // config-3 head set (1024 blocks) runs in one round.
+// One block's 256 rows (block index blk of the grid batch * h * ceil(rows /
+// 256)); the kernels below run it for their own blocks.
 template <int Q>
-__global__ __launch_bounds__(256, Q == 1 ? 4 : 1) void code_topk_mfma_kernel(
+__device__ __forceinline__ void code_topk_mfma_block(
     const float* __restrict__ xhat, int64_t rows, int h, const float* __restrict__ chat,
     const uint16_t* __restrict__ cbf, const uint32_t* __restrict__ cmax_bits, int n_c, int d_s,
-    float temperature, int top, int32_t* __restrict__ codes, uint8_t* __restrict__ flags) {
+    float temperature, int top, int32_t* __restrict__ codes, uint8_t* __restrict__ flags, int64_t blk) {
   constexpr int M = mf_segments(Q);  // segment maxima per lane and row
   constexpr int G = M > 8 ? M / 8 : 1;  // 8-tile groups per pass-1 step
   constexpr int CAP = mf_cap(Q);
@@ -716,8 +718,8 @@ __global__ __launch_bounds__(256, Q == 1 ? 4 : 1) void code_topk_mfma_kernel(
   const int q4 = lane >> 4, c16 = lane & 15;
   const int n_c_pad = n_c_padded(n_c);
   const int64_t tiles = (rows + kMfRows - 1) / kMfRows;
-  const int64_t bh = blockIdx.x / tiles;
-  const int64_t r0 = (blockIdx.x % tiles) * kMfRows + wave * 64;
+  const int64_t bh = blk / tiles;
+  const int64_t r0 = (blk % tiles) * kMfRows + wave * 64;
   const int hh = static_cast<int>(bh % h);
   const float* xb = xhat + bh * rows * d_s;
   const uint16_t* cbh = cbf + static_cast<int64_t>(hh) * n_c_pad * 32;
@@ -1015,6 +1017,33 @@ __global__ __launch_bounds__(256, Q == 1 ? 4 : 1) void code_topk_mfma_kernel(
     }
   }
   if (row < rows) flags[bh * rows + row] = over ? 1 : 0;
+}
+
+template <int Q>
+__global__ __launch_bounds__(256, Q == 1 ? 4 : 1) void code_topk_mfma_kernel(
+    const float* __restrict__ xhat, int64_t rows, int h, const float* __restrict__ chat,
+    const uint16_t* __restrict__ cbf, const uint32_t* __restrict__ cmax_bits, int n_c, int d_s,
+    float temperature, int top, int32_t* __restrict__ codes, uint8_t* __restrict__ flags) {
+  code_topk_mfma_block<Q>(xhat, rows, h, chat, cbf, cmax_bits, n_c, d_s, temperature, top, codes, flags,
+                          blockIdx.x);
+}
+
+// The query screen (blocks [0, grid_a)) and the key screen (the rest) in one
+// launch: the query screen's grid fills 4/3 of the blocks a CU holds at once,
+// and the key screen's blocks then run in what its last round leaves idle.
+template <int QA, int QB>
+__global__ __launch_bounds__(256, 1) void code_topk_mfma_pair_kernel(
+    const float* __restrict__ xa, const float* __restrict__ xb, int64_t rows, int h,
+    const float* __restrict__ chat, const uint16_t* __restrict__ cbf, const uint32_t* __restrict__ cmax_bits,
+    int n_c, int d_s, float temperature, int top_a, int top_b, int32_t* __restrict__ codes_a,
+    int32_t* __restrict__ codes_b, uint8_t* __restrict__ flags_a, uint8_t* __restrict__ flags_b,
+    int64_t grid_a) {
+  const int64_t blk = blockIdx.x;
+  if (blk < grid_a)
+    code_topk_mfma_block<QA>(xa, rows, h, chat, cbf, cmax_bits, n_c, d_s, temperature, top_a, codes_a, flags_a, blk);
+  else
+    code_topk_mfma_block<QB>(xb, rows, h, chat, cbf, cmax_bits, n_c, d_s, temperature, top_b, codes_b, flags_b,
+                             blk - grid_a);
 }
 
 // Exact top-`top` codes of the rows flagged by the matrix-core filter
@@ -1730,6 +1759,23 @@ int launch_mfma_q(const float* xhat, int64_t batch, int h, int64_t rows, const f
   return check_launch("code_topk_mfma_kernel");
 }
 
+// The query (top_a) and key (top_b) screens of one routing call in one launch
+// (code_topk_mfma_pair_kernel); each keeps its own flag bytes for the
+// exhaustive pass.
+template <int QA, int QB>
+int launch_mfma_pair(const float* xa, const float* xb, int64_t batch, int h, int64_t rows, const float* chat,
+                     int n_c, int d_s, float temperature, int top_a, int top_b, int32_t* codes_a, int32_t* codes_b,
+                     const TopkWorkspace& w, uint8_t* flags_b, hipStream_t st) {
+  auto kern = code_topk_mfma_pair_kernel<QA, QB>;
+  const size_t smem = std::max(code_topk_mfma_smem(top_a), code_topk_mfma_smem(top_b));
+  if (int s = reserve_lds(reinterpret_cast<const void*>(kern), smem, "code_topk_mfma_pair")) return s;
+  const int64_t grid_a = batch * h * ceil_div(rows, kMfRows);
+  kern<<<dim3(static_cast<unsigned>(2 * grid_a)), 256, smem, st>>>(xa, xb, rows, h, chat, w.cbf, w.cmax_bits, n_c,
+                                                                   d_s, temperature, top_a, top_b, codes_a, codes_b,
+                                                                   w.flags, flags_b, grid_a);
+  return check_launch("code_topk_mfma_pair_kernel");
+}
+
 // Top codes per row.  With a workspace (and top <= 32, d_s <= 32) the matrix-core
 // filter runs and the exact kernel recomputes only flagged groups; otherwise the
 // exact kernel handles every row.  `prepped` = the bf16 codebook is already in w.
@@ -1910,7 +1956,9 @@ extern "C" size_t ssa_route_workspace_bytes(int64_t batch, int64_t n, int h_kv, 
   if (batch < 0 || n < 0 || h_kv <= 0 || n_c <= 0 || d_s <= 0) return 0;
   const size_t vec = align_up(sizeof(float) * static_cast<size_t>(batch * h_kv * n * d_s), 256);
   const size_t cb = align_up(sizeof(float) * static_cast<size_t>(h_kv) * n_c * d_s, 256);
-  return 2 * vec + cb + topk_workspace_bytes(batch, h_kv, n, n_c);
+  // (+ the key screen's flag bytes when both screens run in one launch)
+  return 2 * vec + cb + topk_workspace_bytes(batch, h_kv, n, n_c) +
+         align_up(static_cast<size_t>(batch * h_kv * n), 256);
 }
 
 extern "C" int ssa_route_codes(const void* q, const void* k, int dtype, int64_t batch, int64_t n,
@@ -1945,6 +1993,20 @@ extern "C" int ssa_route_codes(const void* q, const void* k, int dtype, int64_t 
   if ((st = launch_route_vectors(k, dtype, batch, n, h_kv, 1, d, k_sb, k_sn, k_sh, w_kr, d_s, khat, s)))
     return st;
   if ((st = launch_normalize(codebook, static_cast<int64_t>(h_kv) * n_c, d_s, chat, s))) return st;
+  // top 16 for the queries and top 4 for the keys (config 3's a and b): both
+  // screens in one launch, the keys' flag bytes after the workspace's others
+  if (mf_q(a) == 4 && mf_q(b) == 1 && mfma_path_ok(a, d_s, n_c) && mfma_path_ok(b, d_s, n_c) &&
+      batch * h_kv * n > kFewTopkRows) {
+    const TopkWorkspace w = carve_topk(tws, h_kv, n_c);
+    uint8_t* flags_b = static_cast<uint8_t*>(tws) + topk_workspace_bytes(batch, h_kv, n, n_c);
+    if ((st = launch_codebook_prep(chat, h_kv, n_c, d_s, w, s))) return st;
+    if ((st = launch_mfma_pair<4, 1>(qhat, khat, batch, h_kv, n, chat, n_c, d_s, temperature, a, b, q_codes, k_codes,
+                                     w, flags_b, s)))
+      return st;
+    if ((st = launch_flagged_topk(qhat, batch, h_kv, n, chat, n_c, d_s, temperature, a, q_codes, w.flags, s)))
+      return st;
+    return launch_flagged_topk(khat, batch, h_kv, n, chat, n_c, d_s, temperature, b, k_codes, flags_b, s);
+  }
   if ((st = launch_code_topk(qhat, batch, h_kv, n, chat, n_c, d_s, temperature, a, q_codes, tws,
                              false, s)))
     return st;
