@@ -235,11 +235,12 @@ __device__ __forceinline__ Piece8 load8(const float* p) {
   return Piece8{{a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w}};
 }
 
-template <typename T>
+template <typename T, int DC>
 __global__ __launch_bounds__(kRrThreads) void route_vectors_row_kernel(
-    const T* __restrict__ x, int64_t n, int h_in, int group, int d, int64_t sb, int64_t sn,
+    const T* __restrict__ x, int64_t n, int h_in, int group, int d_rt, int64_t sb, int64_t sn,
     int64_t sh, const float* __restrict__ w, float* __restrict__ out) {
   constexpr int d_s = 32;
+  const int d = DC > 0 ? DC : d_rt;
   const int h_out = h_in / group;
   const int64_t tiles = (n + kRrThreads - 1) / kRrThreads;
   const int64_t bh = blockIdx.x / tiles;
@@ -254,27 +255,37 @@ __global__ __launch_bounds__(kRrThreads) void route_vectors_row_kernel(
   float sum[32], acc[32];
 #pragma unroll
   for (int s = 0; s < 32; ++s) sum[s] = acc[s] = 0.0f;
+  // With d fixed at compile time, 8 pieces per unrolled step: every W
+  // operand of the step is an immediate offset from one base, so the scalar
+  // loads of several pieces go out together (one piece per step waits on its
+  // W loads every dozen fmas).
+  constexpr int UNR = DC > 0 && DC % 64 == 0 ? 8 : 1;
   Piece8 cur = load8(xb);
-  for (int c = 0; c < total; ++c) {
-    const int gg = c / pieces;
-    const int t0 = (c - gg * pieces) * 8;
-    const int cn = c + 1 < total ? c + 1 : c;
-    const int ggn = cn / pieces;
-    const Piece8 nxt = load8(xb + static_cast<int64_t>(ggn) * sh + (cn - ggn * pieces) * 8);
+#pragma unroll 1
+  for (int c0 = 0; c0 < total; c0 += UNR) {
 #pragma unroll
-    for (int s = 0; s < d_s; ++s) {
-      const float* ws = w + static_cast<int64_t>(s) * d + t0;
+    for (int u = 0; u < UNR; ++u) {
+      const int c = c0 + u;
+      const int gg = c / pieces;
+      const int t0 = (c - gg * pieces) * 8;
+      const int cn = c + 1 < total ? c + 1 : c;
+      const int ggn = cn / pieces;
+      const Piece8 nxt = load8(xb + static_cast<int64_t>(ggn) * sh + (cn - ggn * pieces) * 8);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc[s] = fma_rn(cur.v[e], ws[e], acc[s]);
-    }
-    if (t0 + 8 == d) {  // head gg complete: fold its chain into the group sum
+      for (int s = 0; s < d_s; ++s) {
+        const float* ws = w + static_cast<int64_t>(s) * d + t0;
 #pragma unroll
-      for (int s = 0; s < 32; ++s) {
-        sum[s] = (gg == 0) ? acc[s] : sum[s] + acc[s];
-        acc[s] = 0.0f;
+        for (int e = 0; e < 8; ++e) acc[s] = fma_rn(cur.v[e], ws[e], acc[s]);
       }
+      if (t0 + 8 == d) {  // head gg complete: fold its chain into the group sum
+#pragma unroll
+        for (int s = 0; s < 32; ++s) {
+          sum[s] = (gg == 0) ? acc[s] : sum[s] + acc[s];
+          acc[s] = 0.0f;
+        }
+      }
+      cur = nxt;
     }
-    cur = nxt;
   }
   float nrm = 0.0f;
 #pragma unroll
@@ -333,11 +344,12 @@ __device__ __forceinline__ Piece8 line_piece(const Line128& l, int pi) {
   return r;
 }
 
-template <typename T>
+template <typename T, int DC>
 __global__ __launch_bounds__(256) void route_vectors_split_kernel(
-    const T* __restrict__ x, int64_t n, int h_in, int group, int d, int64_t sb, int64_t sn,
+    const T* __restrict__ x, int64_t n, int h_in, int group, int d_rt, int64_t sb, int64_t sn,
     int64_t sh, const float* __restrict__ w, float* __restrict__ out) {
   constexpr int d_s = 32;
+  const int d = DC > 0 ? DC : d_rt;
   __shared__ float part[4][kRsRows][d_s + 1];  // per-wave head chains, padded rows
   __shared__ float mean[kRsRows][d_s + 1];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -1262,20 +1274,28 @@ int launch_route_vectors(const void* x, int dtype, int64_t batch, int64_t n, int
   if (d_s == 32 && piece8 && group > 1) {
     const int64_t grid = batch * (h_in / group) * ceil_div(n, kRsRows);
     if (dtype == SSA_DTYPE_BF16)
-      route_vectors_split_kernel<uint16_t><<<dim3(static_cast<unsigned>(grid)), 256, 0, st>>>(
-          static_cast<const uint16_t*>(x), n, h_in, group, d, sb, sn, sh, w, out);
+      if (d == 128)
+        route_vectors_split_kernel<uint16_t, 128><<<dim3(static_cast<unsigned>(grid)), 256, 0, st>>>(
+            static_cast<const uint16_t*>(x), n, h_in, group, d, sb, sn, sh, w, out);
+      else
+        route_vectors_split_kernel<uint16_t, 0><<<dim3(static_cast<unsigned>(grid)), 256, 0, st>>>(
+            static_cast<const uint16_t*>(x), n, h_in, group, d, sb, sn, sh, w, out);
     else
-      route_vectors_split_kernel<float><<<dim3(static_cast<unsigned>(grid)), 256, 0, st>>>(
+      route_vectors_split_kernel<float, 0><<<dim3(static_cast<unsigned>(grid)), 256, 0, st>>>(
           static_cast<const float*>(x), n, h_in, group, d, sb, sn, sh, w, out);
     return check_launch("route_vectors_split_kernel");
   }
   if (d_s == 32 && piece8) {
     const int64_t grid = batch * (h_in / group) * ceil_div(n, kRrThreads);
     if (dtype == SSA_DTYPE_BF16)
-      route_vectors_row_kernel<uint16_t><<<dim3(static_cast<unsigned>(grid)), kRrThreads, 0, st>>>(
-          static_cast<const uint16_t*>(x), n, h_in, group, d, sb, sn, sh, w, out);
+      if (d == 128)
+        route_vectors_row_kernel<uint16_t, 128><<<dim3(static_cast<unsigned>(grid)), kRrThreads, 0, st>>>(
+            static_cast<const uint16_t*>(x), n, h_in, group, d, sb, sn, sh, w, out);
+      else
+        route_vectors_row_kernel<uint16_t, 0><<<dim3(static_cast<unsigned>(grid)), kRrThreads, 0, st>>>(
+            static_cast<const uint16_t*>(x), n, h_in, group, d, sb, sn, sh, w, out);
     else
-      route_vectors_row_kernel<float><<<dim3(static_cast<unsigned>(grid)), kRrThreads, 0, st>>>(
+      route_vectors_row_kernel<float, 0><<<dim3(static_cast<unsigned>(grid)), kRrThreads, 0, st>>>(
           static_cast<const float*>(x), n, h_in, group, d, sb, sn, sh, w, out);
     return check_launch("route_vectors_row_kernel");
   }
