@@ -21,6 +21,7 @@ namespace {
 
 constexpr int kHistThreads = 256;
 constexpr int kScanThreads = 1024;
+constexpr int kScatterBatch = 16;  // rounds of 64 entries whose codes are loaded together
 
 int64_t tile_keys_for(int64_t n) {
   int64_t tk = ceil_div(n, 64);
@@ -30,9 +31,14 @@ int64_t tile_keys_for(int64_t n) {
 
 // Entry e = j*b + r of a head is code r of key j, stored at j*cstride + r
 // (cstride = b for k_codes; the query order reads q_codes[...][0] with b = 1,
-// cstride = a).
+// cstride = a).  Entries of a head number below 2^31 (run_index checks), so the
+// division is 32-bit: no branches between a load's address and its use.
+__device__ __forceinline__ uint32_t key_of(int64_t e, int b) {
+  return static_cast<uint32_t>(e) / static_cast<uint32_t>(b);
+}
 __device__ __forceinline__ int64_t code_at(int64_t e, int b, int cstride) {
-  return (cstride == b) ? e : (e / b) * cstride + e % b;
+  const uint32_t j = key_of(e, b);
+  return static_cast<int64_t>(j) * cstride + (static_cast<uint32_t>(e) - j * static_cast<uint32_t>(b));
 }
 
 __global__ __launch_bounds__(kHistThreads) void index_hist_kernel(
@@ -147,26 +153,40 @@ __global__ __launch_bounds__(64) void index_scatter_kernel(
   const int32_t* kc = k_codes + bh * n * cstride;
   int32_t* post = postings + bh * n * b;
   const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  for (int64_t r0 = e0; r0 < e1; r0 += 64) {
-    const int64_t e = r0 + lane;
-    int32_t c = -1;
-    if (e < e1) c = kc[code_at(e, b, cstride)];
-    const bool ok = static_cast<uint32_t>(c) < static_cast<uint32_t>(n_c);
-    uint64_t peers = __ballot(ok);
-    for (int bit = 0; bit < code_bits; ++bit) {
-      const bool set = ((c >> bit) & 1) != 0;
-      const uint64_t m = __ballot(set);
-      peers &= set ? m : ~m;
+  // The codes of kScatterBatch rounds are loaded before any is ranked, so a
+  // wave waits for memory once per batch instead of once per round.  Indices
+  // past the tile are clamped to its last entry and the code replaced after
+  // the load (a guarded load is waited for where it is issued).
+  for (int64_t b0 = e0; b0 < e1; b0 += 64 * kScatterBatch) {
+    int32_t cb[kScatterBatch];
+#pragma unroll
+    for (int u = 0; u < kScatterBatch; ++u) {
+      const int64_t e = b0 + 64 * u + lane;
+      cb[u] = kc[code_at(e < e1 ? e : e1 - 1, b, cstride)];
     }
-    int32_t pos = 0;
-    if (ok) {
-      const int rank = __popcll(peers & below);
-      pos = cursor[c] + rank;
-      post[pos] = static_cast<int32_t>(e / b);
+#pragma unroll
+    for (int u = 0; u < kScatterBatch; ++u) {
+      const int64_t r0 = b0 + 64 * u;
+      if (r0 >= e1) break;  // uniform
+      const int64_t e = r0 + lane;
+      const int32_t c = e < e1 ? cb[u] : -1;
+      const bool ok = static_cast<uint32_t>(c) < static_cast<uint32_t>(n_c);
+      uint64_t peers = __ballot(ok);
+      for (int bit = 0; bit < code_bits; ++bit) {
+        const bool set = ((c >> bit) & 1) != 0;
+        const uint64_t m = __ballot(set);
+        peers &= set ? m : ~m;
+      }
+      int32_t pos = 0;
+      if (ok) {
+        const int rank = __popcll(peers & below);
+        pos = cursor[c] + rank;
+        post[pos] = static_cast<int32_t>(key_of(e, b));
+      }
+      __builtin_amdgcn_wave_barrier();
+      if (ok && (peers & below) == 0ull) cursor[c] += __popcll(peers);
+      __builtin_amdgcn_wave_barrier();
     }
-    __builtin_amdgcn_wave_barrier();
-    if (ok && (peers & below) == 0ull) cursor[c] += __popcll(peers);
-    __builtin_amdgcn_wave_barrier();
   }
 }
 
@@ -187,6 +207,9 @@ size_t hist_bytes(int64_t bh, int64_t n, int n_c);
 // is the workspace, `offsets` receives the bucket starts.
 int run_index(const int32_t* codes, int64_t bh, int64_t n, int b, int cstride, int n_c,
               int32_t* offsets, int32_t* postings, int32_t* hist, hipStream_t st) {
+  if (n * b >= (int64_t(1) << 31))
+    return fail(SSA_ERR_UNSUPPORTED, "index: n * b = %lld entries per head exceed int32 positions",
+                static_cast<long long>(n * b));
   const int64_t tk = tile_keys_for(n);
   const int64_t tiles = ceil_div(n, tk);
   int code_bits = 0;
