@@ -918,8 +918,8 @@ __global__ __launch_bounds__(64) void select_light_kernel(SelParams p, int64_t r
 
 // ---- rows with more than k candidates: matrix-core screen (bf16) -----------
 //
-// One wave per listed row.  Approximate scores A_j = (k_j . q_s) / score_div /
-// g with q_s = sum_g q_g split as q_s = hi + lo in bf16 (|q_s - hi - lo| <=
+// One wave per listed row.  Approximate scores A_j = (k_j . q_s) * r, r the
+// fp32 reciprocal of score_div * g, with q_s = sum_g q_g split as q_s = hi + lo in bf16 (|q_s - hi - lo| <=
 // 2^-18 |q_s|): K rows are gathered whole into LDS (row_issue) and one 16x16x32
 // MFMA per 32 dims scores 16 keys against the columns (hi, lo); a second one
 // against |K| and the column up(sum_g |q_g|) (rounded up to bf16) gives P_j >=
@@ -927,9 +927,11 @@ __global__ __launch_bounds__(64) void select_light_kernel(SelParams p, int64_t r
 //
 // Bound.  With u = 2^-24, the canonical fp32 score E_j (g fmaf chains of d
 // terms, / score_div, summed, / g) is within (d + g + 3) u P/sd/g of the real
-// value, and A_j within (4.04 d + 64 + g + 8) u P/sd/g (MFMA sums of exact
+// value, and A_j within (4.04 d + 64 + g + 9) u P/sd/g (MFMA sums of exact
 // products with per-add error <= 2u, the dropped 2^-18 remainder, the fp32
-// head sum of q_s).  So |A_j - E_j| <= e_j = (6 d + 2 g + 100) u * 1.02 *
+// head sum of q_s, and 3u for the scaling by r: sd * g, its reciprocal and the
+// product each round once; one multiply instead of two correctly rounded
+// divisions, which cost about ten instructions each for every lane).  So |A_j - E_j| <= e_j = (6 d + 2 g + 100) u * 1.02 *
 // P_j (1 + 4 d u) / sd / g + 1e-30, and e = max_j e_j.
 //
 // Selection (select_pick_kernel).  T = the k-th largest A lies in a band
@@ -1004,6 +1006,7 @@ select_screen_kernel(SelParams p, SelWs w) {
   const float gf = static_cast<float>(p.g);
   const float ce = (6.0f * D + 2.0f * static_cast<float>(p.g) + 100.0f) * 5.9604645e-8f * 1.02f *
                    (1.0f + 4.0f * D * 5.9604645e-8f);
+  const float rsg = 1.0f / (p.score_div * gf);
   for (int e = gw / kShards; e < listed; e += per) {
     const ScrEntry x = scr_entry(p, w, shard, e);
     if (!x.ok) continue;  // the pick pass sends the row to the exact pass
@@ -1104,8 +1107,8 @@ select_screen_kernel(SelParams p, SelWs w) {
           const float slo = dpp_from_plus1(sv[e4]);  // column 1 (lo) of the same keys
           const int pos = ch * kMfChunk + 16 * t + 4 * q4 + e4;
           if (c16 == 0 && pos < C) {
-            const float a = ((sv[e4] + slo) / p.score_div) / gf;
-            const float ej = ce * pv[e4] / p.score_div / gf + 1e-30f;
+            const float a = (sv[e4] + slo) * rsg;
+            const float ej = ce * pv[e4] * rsg + 1e-30f;
             w.approx[off + pos] = a;
             emax = fmaxf(emax, ej);
             bad = bad || !(fabsf(a) <= 3.0e38f) || !(ej <= 3.0e38f);
