@@ -283,6 +283,40 @@ def time_sorted_select(q, k, router, reps=5):
     return sorted(ts)[len(ts) // 2]
 
 
+def time_spread_attention(q, k, v, idx_like, reps=5):
+    """Stage (d) on an index set with no filler: every (batch, row, kv head)
+    attends k distinct keys spread over the whole sequence (a seeded random
+    start and odd stride modulo n, distinct because n is a power of two),
+    unmasked, so no slot is a filler key that neighbouring rows share.  Median
+    ms of `reps` calls (HIP events on the launch stream); None when n is not a
+    power of two."""
+    import torch
+
+    from ssa_amd import kernels
+
+    B, n, h_kv, kk = idx_like.shape
+    if n & (n - 1) or kk > n:
+        return None
+    gen = torch.Generator(device=idx_like.device).manual_seed(7)
+    shape = (B, n, h_kv, 1)
+    start = torch.randint(0, n, shape, device=idx_like.device, generator=gen, dtype=torch.int64)
+    stride = torch.randint(0, max(n // 2, 1), shape, device=idx_like.device, generator=gen,
+                           dtype=torch.int64) * 2 + 1
+    j = torch.arange(kk, device=idx_like.device, dtype=torch.int64)
+    idx = ((start + j * stride) % n).to(idx_like.dtype)
+    del start, stride
+    out = kernels.sparse_attention(q, k, v, idx, None, False)
+    ts = []
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        kernels.sparse_attention(q, k, v, idx, None, False, out=out)
+        e1.record()
+        torch.cuda.synchronize()
+        ts.append(e0.elapsed_time(e1))
+    return sorted(ts)[len(ts) // 2]
+
+
 def stats_sums(q, k, router):
     import torch
 
@@ -676,6 +710,12 @@ def main():
               "gbs_logical_gather": alg["d_bytes_logical"] / t["d"] / 1e9,
               "tflops": alg["d_flops"] / t["d"] / 1e12},
     }
+    spread_ms = time_spread_attention(q, k, v, inter[4])
+    if spread_ms is not None:
+        stages["d"]["spread_keys"] = {
+            "ms": spread_ms,
+            "index_set": "k distinct keys per row spread over the sequence (no filler, unmasked)",
+            "gbs_logical_gather": alg["d_bytes_logical"] / (spread_ms / 1000.0) / 1e9}
     workload = (f"{args.config}: RMSNorm + SSAAttention forward (projections, RoPE, stages a-d, "
                 f"o_proj), causal routing" if is_block else
                 f"{args.config}: SSA forward (stages a-d), causal")
