@@ -68,10 +68,14 @@ def parse():
     p.add_argument("--block-sparse", type=int, default=0,
                    help="also time the block-granular variant with this many 64-key blocks per "
                         "query block (block indices from the workload's selections, then attention)")
-    p.add_argument("--sweep", default="", help="comma list of n for a tokens/s vs n sweep")
-    p.add_argument("--sweep-nc", default="scaled", choices=("scaled", "fixed"),
+    p.add_argument("--sweep", default=None,
+                   help="comma list of n for a tokens/s vs n sweep at the config's head shapes "
+                        "(default for c3: 4K..128K, both codebook policies); '' for none")
+    p.add_argument("--sweep-nc", default="both", choices=("scaled", "fixed", "both"),
                    help="codebook size in the sweep: scaled with n (constant bucket size; the "
-                        "config's N_c at its own n) or fixed at the config's N_c")
+                        "config's N_c at its own n), fixed at the config's N_c, or both")
+    p.add_argument("--no-extras", action="store_true",
+                   help="skip the default n-sweep and the c5 stage times (profiling runs)")
     return p.parse_args()
 
 
@@ -452,6 +456,55 @@ def time_decode(cfg, q, k, v, router, steps, tail_tokens=512):
             "rebuilds_in_timed_steps": cache.rebuilds - rebuilds0}
 
 
+DEFAULT_SWEEP = (4096, 8192, 16384, 32768, 65536, 131072)
+
+
+def run_sweep(cfg, ns, policy, seed, dev, steps):
+    """tokens/s of the full forward at each n (the config's head shapes), the
+    codebook scaled with n (N_c = cfg N_c * n / cfg n, constant expected bucket
+    size) or fixed; least-squares t = alpha * n + beta and its R^2 (the
+    reference's linearity check, benchmark/profile_scaling.py:39-54)."""
+    points = {}
+    for n_ in ns:
+        c2 = dict(cfg, n=n_)
+        if policy == "scaled":
+            c2["n_c"] = max(16, cfg["n_c"] * n_ // cfg["n"])
+        q2, k2, v2, r2 = make_workload(c2, seed, dev)
+        w2, s2 = time_gpu(c2, q2, k2, v2, r2, steps, 2)
+        ms2 = 1000 * w2 / steps
+        points[n_] = {"ms": ms2, "tokens_per_s": c2["B"] * n_ / (ms2 / 1000), "num_codebook": c2["n_c"],
+                      "stages_ms": s2}
+        print(f"sweep ({policy} N_c) n={n_}: {ms2:.3f} ms", file=sys.stderr, flush=True)
+        del q2, k2, v2, r2
+    out = {"num_codebook_policy": (f"scaled: N_c = {cfg['n_c']} * n / {cfg['n']}" if policy == "scaled"
+                                   else f"fixed: N_c = {cfg['n_c']}"),
+           "points": points}
+    xs = sorted(points)
+    ts = [points[x]["ms"] for x in xs]
+    if len(xs) >= 3:
+        mn, mt = sum(xs) / len(xs), sum(ts) / len(ts)
+        sxx = sum((x - mn) ** 2 for x in xs)
+        alpha = sum((x - mn) * (t_ - mt) for x, t_ in zip(xs, ts)) / sxx
+        beta = mt - alpha * mn
+        ss_res = sum((t_ - (alpha * x + beta)) ** 2 for x, t_ in zip(xs, ts))
+        ss_tot = sum((t_ - mt) ** 2 for t_ in ts)
+        out["fit"] = {"ms_per_token": alpha, "ms_offset": beta,
+                      "r2": 1.0 - ss_res / ss_tot if ss_tot > 0 else 1.0}
+    return out
+
+
+def run_c5(seed, dev, steps, warmup):
+    """Config 5 (n = 131072, GQA 16/2, N_c 8192, a 32, k 1024): whole-forward
+    ms and tokens/s and per-stage ms (HIP events on the launch stream)."""
+    cfg = dict(CONFIGS["c5"])
+    q, k, v, router = make_workload(cfg, seed, dev)
+    wall, st = time_gpu(cfg, q, k, v, router, steps, warmup)
+    ms = 1000 * wall / steps
+    print(f"c5: {ms:.3f} ms", file=sys.stderr, flush=True)
+    return {"workload": "c5: SSA forward (stages a-d), causal, n=131072, GQA 16/2, N_c 8192, a 32, k 1024",
+            "ms": ms, "tokens_per_s": cfg["B"] * cfg["n"] / (ms / 1000), "stages_ms": st, "steps": steps}
+
+
 def _cpu_model():
     cpu = platform.processor() or platform.machine()
     try:
@@ -462,6 +515,13 @@ def _cpu_model():
     except OSError:
         pass
     return cpu
+
+
+def cpu_share():
+    """Threads for the CPU baselines: the job's share of the host (16 per GPU on
+    the GPU boxes, which set OMP_NUM_THREADS to it), at most the CPUs present."""
+    share = int(os.environ.get("OMP_NUM_THREADS", "16") or 16)
+    return max(1, min(share, os.cpu_count() or 1))
 
 
 def cpu_reference(cfg, q, k, v, router, budget_s, blk=None):
@@ -476,7 +536,7 @@ def cpu_reference(cfg, q, k, v, router, budget_s, blk=None):
 
     from oracle import dense_ref
 
-    threads = min(16, os.cpu_count() or 1)
+    threads = cpu_share()
     torch.set_num_threads(threads)
     n, B = cfg["n"], cfg["B"]
     qf, kf, vf = q[0].float().cpu(), k[0].float().cpu(), v[0].float().cpu()
@@ -514,10 +574,11 @@ def cpu_reference(cfg, q, k, v, router, budget_s, blk=None):
         "value": n / total,
         "unit": "tokens/s",
         "cores": threads,
+        "host_cpus": os.cpu_count(),
         "kind": "port",
         "sample": (f"the reference's dense algorithm (ssa/router.py:102-259, ssa/attention.py:64-113) "
-                   f"restated in torch on the CPU (oracle/dense_ref.py; {threads} threads, "
-                   f"{_cpu_model()}): routing of all {n} tokens in full, dense rescoring + candidate "
+                   f"restated in torch on the CPU (oracle/dense_ref.py; {threads} threads, the job's "
+                   f"share of {os.cpu_count()} host CPUs, {_cpu_model()}): routing of all {n} tokens in full, dense rescoring + candidate "
                    f"mask + top-k + attention for {sc} sampled query rows against all {n} keys, scaled "
                    f"to {n} rows" + (f" and {B} batch elements" if B > 1 else "")
                    + ("; q/k/v/o projections timed on 512 tokens, scaled" if blk is not None else "")
@@ -544,7 +605,7 @@ def cpu_oracle(cfg, q, k, v, router, inter, budget_s):
 
     import oracle
 
-    threads = min(16, os.cpu_count() or 1)
+    threads = cpu_share()
     oracle.set_threads(threads)
     n, h_q, h_kv, d = cfg["n"], cfg["h_q"], cfg["h_kv"], cfg["d"]
     g = h_q // h_kv
@@ -595,8 +656,10 @@ def cpu_oracle(cfg, q, k, v, router, inter, budget_s):
         "value": n / total,
         "unit": "tokens/s",
         "cores": threads,
+        "host_cpus": os.cpu_count(),
         "kind": "port",
-        "sample": (f"linear CPU oracle (oracle/ssa_oracle.c, OpenMP {threads} threads, {cpu}): stage a on "
+        "sample": (f"linear CPU oracle (oracle/ssa_oracle.c, OpenMP {threads} threads of {os.cpu_count()} "
+                   f"host CPUs, {cpu}): stage a on "
                    f"{sa} of {n} token rows, stage b in full, stages c+d on {sc} of {n} query "
                    f"positions (all {h_kv} kv heads), each scaled to n; outputs checked equal to "
                    f"the GPU's on the sample"),
@@ -785,32 +848,17 @@ def main():
         line["cpu_baseline"] = cpu_reference(cfg, q, k, v, router, args.cpu_seconds, blk)
         print("cpu baseline: linear oracle", file=sys.stderr, flush=True)
         line["cpu_oracle"] = cpu_oracle(cfg, q, k, v, router, inter, args.cpu_seconds)
-    if args.sweep:
-        sweep = {}
-        for n_ in [int(x) for x in args.sweep.split(",")]:
-            c2 = dict(cfg, n=n_)
-            if args.sweep_nc == "scaled":
-                c2["n_c"] = max(16, cfg["n_c"] * n_ // cfg["n"])
-            q2, k2, v2, r2 = make_workload(c2, args.seed, dev)
-            w2, s2 = time_gpu(c2, q2, k2, v2, r2, max(3, args.steps // 2), 1)
-            ms2 = 1000 * w2 / max(3, args.steps // 2)
-            sweep[n_] = {"ms": ms2, "tokens_per_s": c2["B"] * n_ / (ms2 / 1000), "num_codebook": c2["n_c"],
-                         "stages_ms": s2}
-            print(f"sweep n={n_}: {sweep[n_]['ms']:.3f} ms", file=sys.stderr, flush=True)
-            del q2, k2, v2, r2
-        ns = sorted(sweep)
-        ts = [sweep[x]["ms"] for x in ns]
-        if len(ns) >= 3:  # least-squares t = alpha * n + beta and its R^2
-            mn, mt = sum(ns) / len(ns), sum(ts) / len(ts)
-            sxx = sum((x - mn) ** 2 for x in ns)
-            alpha = sum((x - mn) * (t_ - mt) for x, t_ in zip(ns, ts)) / sxx
-            beta = mt - alpha * mn
-            ss_res = sum((t_ - (alpha * x + beta)) ** 2 for x, t_ in zip(ns, ts))
-            ss_tot = sum((t_ - mt) ** 2 for t_ in ts)
-            sweep["fit"] = {"ms_per_token": alpha, "ms_offset": beta,
-                            "r2": 1.0 - ss_res / ss_tot if ss_tot > 0 else 1.0}
-        sweep["num_codebook_policy"] = args.sweep_nc
-        line["sweep"] = sweep
+    sweep_ns = args.sweep
+    if sweep_ns is None:
+        default_shape = args.config == "c3" and args.n is None and args.num_codebook is None
+        sweep_ns = ",".join(str(x) for x in DEFAULT_SWEEP) if default_shape and not args.no_extras else ""
+    if sweep_ns:
+        ns = [int(x) for x in sweep_ns.split(",")]
+        policies = ("scaled", "fixed") if args.sweep_nc == "both" else (args.sweep_nc,)
+        steps = max(3, args.steps // 4)
+        line["sweep"] = {pol: run_sweep(cfg, ns, pol, args.seed, dev, steps) for pol in policies}
+    if args.config == "c3" and not args.no_extras and args.n is None and args.num_codebook is None:
+        line["c5"] = run_c5(args.seed, dev, max(3, args.steps // 4), 2)
     print(json.dumps(line), flush=True)
 
 

@@ -56,6 +56,15 @@ class _SparseAttention(torch.autograd.Function):
         return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), None, None, None, None, None, None, None
 
 
+def flat_gather_view(t: torch.Tensor) -> torch.Tensor:
+    """The ``[.., n, h_kv, d]`` view whose element ``[j, h]`` is row ``j + h*n`` of
+    ``t.reshape(n*h_kv, d)``: the rows ssa/attention.py:76-96 gathers for index j
+    of KV head h (it flattens K to [n*h_kv, d] and offsets head h's indices by
+    h*n).  No copy for a contiguous ``t``; differentiable (a view)."""
+    *lead, n, h_kv, d = t.shape
+    return t.reshape(*lead, n * h_kv, d).view(*lead, h_kv, n, d).transpose(-3, -2)
+
+
 def sparse_exact_attention(
     q: torch.Tensor,
     k: torch.Tensor,
@@ -68,6 +77,7 @@ def sparse_exact_attention(
     row_order: Optional[torch.Tensor] = None,
     row_prefix: Optional[torch.Tensor] = None,
     routing: Optional[kernels.Routing] = None,
+    reference_flat_gather: bool = False,
 ) -> torch.Tensor:
     """softmax(q . K[indices]^T / scale) . V[indices] per (query, KV head).
 
@@ -89,12 +99,19 @@ def sparse_exact_attention(
     order).  ``routing`` (``route(...).routing()``, with ``row_prefix``) is the
     selection the indices came from: the backward then differentiates the
     candidate keys by codebook bucket (same gradients, far fewer atomics).
+    ``reference_flat_gather=True`` reproduces what ssa/attention.py:76-96
+    computes rather than its docstring's ``K[indices[i, h], h]``: index j of KV
+    head h reads row ``j + h*n`` of K and V flattened to ``[n*h_kv, d]``
+    (``flat_gather_view``; the same rows when h_kv = 1).  The kernels read
+    that layout through strides, with no copy.
 
     Differentiable in q, k and v (HIP backward kernel); not in ``indices``.
     """
     unbatched = q.dim() == 3
     if unbatched:
         q, k, v, indices = q.unsqueeze(0), k.unsqueeze(0), v.unsqueeze(0), indices.unsqueeze(0)
+    if reference_flat_gather:
+        k, v = flat_gather_view(k), flat_gather_view(v)
     seq_len, num_q_heads, head_dim = q.shape[1], q.shape[2], q.shape[3]
     num_kv_heads = k.shape[2]
     assert num_q_heads % num_kv_heads == 0

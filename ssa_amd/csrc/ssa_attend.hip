@@ -614,8 +614,12 @@ __device__ __forceinline__ void attend_row_mfma(const AttParams& p, const AttRow
       else mf_issue<D, false, false>(krs, vrs, kl, vl, jsafe, lrow, ksn2, vsn2, seg16);
     }
   };
-  // keys below the row's dense prefix were attended by prefix_attention_kernel
-  const int xpre = (NSPLIT == 1 && !BLK && p.pfx_x && row_ok) ? p.pfx_x[bh * p.n_q + qr] : 0;
+  // keys below the row's dense prefix were attended by prefix_attention_kernel,
+  // which clamps a caller's X to [0, min(top_k, n)] the same way
+  const int xpre = (NSPLIT == 1 && !BLK && p.pfx_x && row_ok)
+                       ? min(max(p.pfx_x[bh * p.n_q + qr], 0),
+                             static_cast<int>(min(static_cast<int64_t>(p.top_k), p.n)))
+                       : 0;
   auto chunk_ok = [&](int j) { return j >= xpre && !(p.causal && j > i); };
 
   // Fragment addresses (fixed per lane): K tile t, block kb; V^T tile t (rows

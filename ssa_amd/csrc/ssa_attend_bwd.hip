@@ -441,7 +441,9 @@ __global__ __launch_bounds__(64 * kBwMfWaves, 2) void sparse_attention_bwd_mfma_
   }
   // the prefix keys [0, X) go to prefix_attention_bwd_kernel, which needs the
   // row's softmax reference, 1/sum and D
-  const int xpre = p.pfx ? p.pfx[bh * p.n + i] : 0;
+  const int xpre = p.pfx ? min(max(p.pfx[bh * p.n + i], 0),
+                               static_cast<int>(min(static_cast<int64_t>(p.top_k), p.n)))
+                         : 0;
   if (p.pfx && q4 == 0 && col_ok) {
     float* ps = p.pstats + ((bh * p.n + i) * g + c16) * 4;
     ps[0] = mref;

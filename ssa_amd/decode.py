@@ -17,8 +17,8 @@ the full KV cache on each step"; its code only runs whole sequences.  Here:
   over the whole cache and selects and attends its rows in one batch.
 
 Row t of a step equals row t of the whole-sequence forward over the same
-prefix: the same keys, codes and candidate sets, indices bit for bit, and
-outputs from the same attention code.
+prefix with the same ``causal_attention`` setting: the same keys, codes and
+candidate sets, indices bit for bit, and outputs from the same attention code.
 """
 
 from __future__ import annotations
@@ -96,14 +96,17 @@ class SSADecodeCache:
 
     @torch.no_grad()
     def step(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
-             causal_attention: bool = True, return_indices: bool = False):
+             causal_attention: bool = False, return_indices: bool = False):
         """Attend the m new tokens' queries ``q [B, m, h_q, d]`` over the cache
         after appending their keys and values ``k, v [B, m, h_kv, d]``.
 
         Returns ``[B, m, h_q, d]`` (and the int32 ``[B, m, h_kv, top_k]``
         selections, keys ascending, with ``return_indices``).  With
         ``causal_attention`` selected keys past a query's position are dropped
-        in the attention."""
+        in the attention; the default (False) attends every selected index, as
+        SSAAttention's default does.  A step's rows equal the whole-sequence
+        forward's rows when both use the same setting (only rows below top_k,
+        whose filler can hold later keys, depend on it)."""
         r = self.router
         B, m = q.shape[0], q.shape[1]
         n0, n = self.len, self.len + m

@@ -172,15 +172,17 @@ def test_head_rope_tables_give_the_reference_layer_rotation():
     without position_ids."""
     import oracle
 
-    B, n, h, d = 3, 7, 4, 16
-    x = torch.randn(B, n, h, d)
+    B, h, d = 3, 4, 16
     freqs = precompute_rope_freqs(d, 32, 1e4)
-    for pos in (None, torch.randint(0, 32, (B, n))):
-        cos, sin = head_rope_tables(freqs, n, h, d, pos)
-        got = oracle.rope(x.numpy(), cos.numpy(), sin.numpy(), d // 2, by_head=True)
-        fb = [freqs[:n] if pos is None else freqs[pos[b]] for b in range(B)]
-        ref = torch.stack([apply_rope(x[b], fb[b]) for b in range(B)])
-        np.testing.assert_array_equal(got, ref.numpy())
+    # n = 1: the reference's one angle row broadcasts over the heads
+    for n in (7, 1):
+        x = torch.randn(B, n, h, d)
+        for pos in (None, torch.randint(0, 32, (B, n))):
+            cos, sin = head_rope_tables(freqs, n, h, d, pos)
+            got = oracle.rope(x.numpy(), cos.numpy(), sin.numpy(), d // 2, by_head=True)
+            fb = [freqs[:n] if pos is None else freqs[pos[b]] for b in range(B)]
+            ref = torch.stack([apply_rope(x[b], fb[b]) for b in range(B)])
+            np.testing.assert_array_equal(got, ref.numpy())
     with pytest.raises(ValueError, match="angle rows"):
         head_rope_tables(freqs[:3], 3, h, d)
 
@@ -249,3 +251,63 @@ def test_dense_layer_path_on_cpu():
     # batch independence (tests/test_integration.py:87-100)
     y0 = blk(x[:1], use_dense=True)
     torch.testing.assert_close(y[:1], y0, atol=1e-6, rtol=0)
+
+
+def _reference_aux_loss(layer, x):
+    """ssa/ssa_layer.py:140-257 step by step (dense n x n teacher and student for
+    every row, then the sampled rows), on the layer's own parameters."""
+    B, n, _ = x.shape
+    hq, hkv, d = layer.num_q_heads, layer.num_kv_heads, layer.head_dim
+    g, r = hq // hkv, layer.router
+    q = layer.q_proj(x).view(B, n, hq, d)
+    k = layer.k_proj(x).view(B, n, hkv, d)
+    k_exp = k.unsqueeze(3).expand(-1, -1, -1, g, -1).reshape(B, n, hq, d)
+    sample = torch.randperm(n)[:min(n, 64)]
+    mask = build_causal_mask(n)
+    total = 0.0
+    for b in range(B):
+        t = torch.einsum("shd,thd->sht", q[b], k_exp[b]) / d ** 0.5
+        tw = F.softmax(t.masked_fill(~mask.unsqueeze(1), float("-inf")), dim=-1)
+        qr = r.W_qr(q[b]).reshape(n, hkv, g, r.route_dim).mean(dim=2)
+        kr = r.W_kr(k[b])
+        cb = F.normalize(r.codebook, dim=-1)
+        qsc = torch.einsum("shd,hcd->shc", F.normalize(qr, dim=-1), cb)
+        ksc = torch.einsum("shd,hcd->shc", F.normalize(kr, dim=-1), cb)
+        st = torch.einsum("shc,thc->sht", qsc, ksc).masked_fill(~mask.unsqueeze(1), float("-inf"))
+        sw = F.softmax(st.unsqueeze(2).expand(-1, -1, g, -1).reshape(n, hq, n), dim=-1)
+        total = total + F.kl_div(torch.log(sw[sample] + 1e-10), tw[sample], reduction="batchmean",
+                                 log_target=False)
+    return total / B
+
+
+@pytest.mark.parametrize("n", [40, 150])
+def test_auxiliary_loss_matches_the_reference_algorithm(n):
+    """compute_auxiliary_loss (sampled rows only) equals the reference's dense
+    algorithm on the same parameters and the same randperm draw, value and
+    gradients; n = 150 > 64 samples a subset of the rows."""
+    torch.manual_seed(3)
+    layer = SSAAttention(hidden_size=64, num_q_heads=4, num_kv_heads=2, head_dim=16, route_dim=8,
+                         num_codebook=32, codes_per_key=2, codes_per_query=4, top_k=8)
+    x = torch.randn(2, n, 64)
+    torch.manual_seed(11)
+    got = layer.compute_auxiliary_loss(x)
+    g_got = torch.autograd.grad(got, [layer.router.W_qr.weight, layer.router.codebook, layer.q_proj.weight])
+    torch.manual_seed(11)
+    ref = _reference_aux_loss(layer, x)
+    g_ref = torch.autograd.grad(ref, [layer.router.W_qr.weight, layer.router.codebook, layer.q_proj.weight])
+    assert got.dim() == 0 and float(got) > 0
+    torch.testing.assert_close(got, ref, rtol=1e-5, atol=1e-6)
+    for a, b in zip(g_got, g_ref):
+        # the q_proj gradient is NaN in both: the teacher's masked weights are
+        # exactly 0, and kl_div's derivative in its target is target / target
+        torch.testing.assert_close(a, b, rtol=1e-4, atol=1e-6, equal_nan=True)
+    assert bool(torch.isnan(g_ref[2]).any()) and bool(torch.isfinite(g_got[0]).all())
+    # _get_routing_logits keeps the reference's full [n, h_kv, n] form
+    q = layer.q_proj(x[0]).view(n, 4, 16)
+    k = layer.k_proj(x[0]).view(n, 2, 16)
+    full = layer._get_routing_logits(q, k, build_causal_mask(n))
+    rows = torch.tensor([0, 5, n - 1])
+    part = layer._get_routing_logits(q, k, build_causal_mask(n)[rows], rows=rows)
+    assert full.shape == (n, 2, n)
+    torch.testing.assert_close(part, full[rows], rtol=1e-6, atol=1e-6)
+    assert bool(torch.isinf(full[0, :, 1:]).all()), "causal: future keys masked"

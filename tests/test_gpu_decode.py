@@ -37,7 +37,7 @@ def _setup(dev, n, h_q, h_kv, d, n_c, top_k, dtype, seed, batch=1):
     return (torch.stack(qs).to(dev), torch.stack(ks).to(dev), torch.stack(vs).to(dev), router)
 
 
-def _prefix_forward(router, q, k, v, n):
+def _prefix_forward(router, q, k, v, n, causal=True):
     """Whole-sequence forward over tokens 0..n-1."""
     from ssa_amd import kernels
 
@@ -48,8 +48,30 @@ def _prefix_forward(router, q, k, v, n):
     idx = kernels.select(qp, kp, qc, off, post, router.codes_per_key, router.top_k, sorted=False,
                          index_dtype=torch.int32)
     # the row path alone (the dense-prefix pass sums the same terms in another order)
-    out = kernels.sparse_attention(qp, kp, vp, idx, None, True, dense_prefix=False)
+    out = kernels.sparse_attention(qp, kp, vp, idx, None, causal, dense_prefix=False)
     return idx, out
+
+
+def test_decode_default_attends_every_selected_index(dev):
+    """The step's default (causal_attention=False, as SSAAttention's) attends
+    every selected index, as the whole-sequence forward without the mask does.
+    Steps of 4 tokens with rows below top_k: an earlier row of a step can hold
+    filler keys of the step's later tokens, so the setting matters there."""
+    from ssa_amd.decode import SSADecodeCache
+
+    n, h_q, h_kv, d, m = 40, 8, 2, 64, 4
+    q, k, v, router = _setup(dev, n, h_q, h_kv, d, 32, 24, torch.bfloat16, seed=4)
+    cache = SSADecodeCache(router, 1, 64, d, dtype=torch.bfloat16, tail_tokens=16)
+    cache.step(q[:, :8], k[:, :8], v[:, :8])
+    later = False
+    for pos in range(8, 24, m):
+        out, idx = cache.step(q[:, pos:pos + m], k[:, pos:pos + m], v[:, pos:pos + m], return_indices=True)
+        ref_idx, ref_out = _prefix_forward(router, q, k, v, pos + m, causal=False)
+        assert torch.equal(idx, ref_idx[:, pos:]), f"indices differ in the step at {pos}"
+        assert torch.equal(out, ref_out[:, pos:]), f"outputs differ in the step at {pos}"
+        rowpos = torch.arange(pos, pos + m, device=idx.device)[None, :, None, None]
+        later = later or bool((idx.to(torch.int64) > rowpos).any())
+    assert later, "some row should hold a filler key past its position"
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
@@ -67,7 +89,8 @@ def test_decode_steps_match_prefix_forward(dev, dtype, tail_tokens, batch):
     cache = SSADecodeCache(router, batch, 256, d, dtype=dtype, tail_tokens=tail_tokens)
     pos = 0
     for m in (96, 1, 1, 3, 1, 1, 1, 7, 1, 1):
-        out, idx = cache.step(q[:, pos:pos + m], k[:, pos:pos + m], v[:, pos:pos + m], return_indices=True)
+        out, idx = cache.step(q[:, pos:pos + m], k[:, pos:pos + m], v[:, pos:pos + m],
+                              causal_attention=True, return_indices=True)
         ref_idx, ref_out = _prefix_forward(router, q, k, v, pos + m)
         assert torch.equal(idx, ref_idx[:, pos:]), f"indices differ in the step at {pos}"
         assert torch.equal(out, ref_out[:, pos:]), f"outputs differ in the step at {pos}"
@@ -84,7 +107,7 @@ def test_decode_step_matches_oracle(dev, orc):
     q, k, v, router = _setup(dev, n, h_q, h_kv, d, 32, 16, torch.float32, seed=8)
     cache = SSADecodeCache(router, 1, n, d, dtype=torch.float32)
     cache.step(q[:, :199], k[:, :199], v[:, :199])
-    out, idx = cache.step(q[:, 199:], k[:, 199:], v[:, 199:], return_indices=True)
+    out, idx = cache.step(q[:, 199:], k[:, 199:], v[:, 199:], causal_attention=True, return_indices=True)
     qf, kf, vf = f32(q[0]), f32(k[0]), f32(v[0])
     ref_idx, _ = orc.router_forward(qf, kf, f32(router.W_qr.weight), f32(router.W_kr.weight),
                                     f32(router.codebook), 8, 4, 16, orc.MASK_CAUSAL)
@@ -131,7 +154,8 @@ def test_decode_codebook_sizes_and_ties(dev, n_c, a, periodic):
     cache = SSADecodeCache(router, batch, 128, d, dtype=torch.bfloat16, tail_tokens=16)
     cache.step(q[:, :100], k[:, :100], v[:, :100])
     for pos in range(100, n):
-        out, idx = cache.step(q[:, pos:pos + 1], k[:, pos:pos + 1], v[:, pos:pos + 1], return_indices=True)
+        out, idx = cache.step(q[:, pos:pos + 1], k[:, pos:pos + 1], v[:, pos:pos + 1],
+                              causal_attention=True, return_indices=True)
         ref_idx, ref_out = _prefix_forward(router, q, k, v, pos + 1)
         assert torch.equal(idx, ref_idx[:, pos:]), f"indices differ at {pos}"
         assert torch.equal(out, ref_out[:, pos:]), f"outputs differ at {pos}"

@@ -42,12 +42,21 @@ def lc(dev, request):
     order = query_order(qc, cfg["n_c"])
     out_ord = torch.empty_like(out)
     kernels.sparse_attention(q, k, v, idx_u, None, True, out=out_ord, row_order=order)
+    # the headline call, as bench.py times it and SSAAttention makes it: int32
+    # indices, the query order, the selection's dense prefix, bf16 output; and
+    # its fp32 twin
+    pfx = torch.empty(order.shape, device=dev, dtype=torch.int32)
+    idx_h = kernels.select(q, k, qc, off, post, cfg["b"], cfg["k"], sorted=False,
+                           index_dtype=torch.int32, row_order=order, row_prefix=pfx)
+    out_h = kernels.sparse_attention(q, k, v, idx_h, None, True, row_order=order, row_prefix=pfx)
+    out_h32 = torch.empty_like(out)
+    kernels.sparse_attention(q, k, v, idx_h, None, True, out=out_h32, row_order=order, row_prefix=pfx)
     torch.cuda.synchronize()
     print(f"{request.param}: GPU pipeline done", flush=True)
     return dict(cfg=cfg, q=q, k=k, v=v, router=router, qc=qc, kc=kc, off=off, post=post,
                 idx_s=idx_s, idx_u=idx_u, idx_s2=idx_s2, idx_u2=idx_u2, idx_ub=idx_ub, st_u=st_u,
                 st_ub=st_ub, stats=st, out=out,
-                order=order, out_ord=out_ord)
+                order=order, out_ord=out_ord, pfx=pfx, idx_h=idx_h, out_h=out_h, out_h32=out_h32)
 
 
 def test_long_row_order_changes_nothing(lc):
@@ -149,3 +158,85 @@ def test_long_stage_d_rows_vs_oracle(lc, orc):
                                orc.to_f32(lc["v"][0]), idx, causal=True, rows=rows)
     got = lc["out"][0].cpu().numpy()[rows]
     np.testing.assert_allclose(got, ref, rtol=1e-3, atol=1e-3)
+
+
+def test_long_headline_call_selection(lc):
+    """The headline selection (int32, query order, prefix written) lists the
+    index-order selection's indices, and each row's X names a key prefix
+    [0, X) that its indices hold exactly once."""
+    assert lc["idx_h"].dtype == torch.int32
+    assert torch.equal(lc["idx_h"].to(torch.int64), lc["idx_u"])
+    k = lc["cfg"]["k"]
+    pfx = lc["pfx"][0].to(torch.int64)                       # [h, n]
+    assert int(pfx.min()) >= 0 and int(pfx.max()) <= k
+    assert int((pfx > 0).sum()) > 0, "clustered rows with filler have a dense prefix"
+    n = lc["cfg"]["n"]
+    rows = torch.from_numpy(_sample_rows(n, [], seed=4, count=512)).to(pfx.device)
+    idx = lc["idx_u"][0][rows]                                 # [r, h, k]
+    x = pfx[:, rows].T                                         # [r, h]
+    in_pfx = idx < x[..., None]
+    assert torch.equal(in_pfx.sum(-1), x), "each key of [0, X) appears exactly once"
+
+
+def test_long_headline_call_outputs(lc, orc):
+    """Stage (d) as timed: the bf16 output is the fp32 twin rounded once; the
+    twin equals the no-prefix path within 1e-5 (the dense-prefix pass sums the
+    same terms in another order) and the float64 oracle on sampled rows within
+    1e-3."""
+    out_h, out_h32, out = lc["out_h"], lc["out_h32"], lc["out"]
+    assert out_h.dtype == torch.bfloat16
+    diff = (out_h.float() - out_h32).abs()
+    assert bool((diff <= out_h32.abs() * 2.0 ** -8 + 1e-30).all()), "bf16 output is the fp32 result rounded"
+    torch.testing.assert_close(out_h32, out, rtol=1e-5, atol=1e-5)
+    n = lc["cfg"]["n"]
+    rows = _sample_rows(n, [], seed=5, count=64)
+    idx = lc["idx_u"][0].cpu().numpy()[rows]
+    ref = orc.sparse_attention(orc.to_f32(lc["q"][0]), orc.to_f32(lc["k"][0]),
+                               orc.to_f32(lc["v"][0]), idx, causal=True, rows=rows)
+    np.testing.assert_allclose(out_h32[0].cpu().numpy()[rows], ref, rtol=1e-3, atol=1e-3)
+
+
+def test_long_routed_backward(lc):
+    """The backward as training runs it (bench.py's call: bucket mode with the
+    forward's row stats, query order and dense prefix) equals the plain
+    backward within 2e-5 of max|ref| per tensor, and its dq equals the float64
+    oracle on sampled rows at or above top_k (whose filler keys all precede
+    them, so the causal mask drops nothing there)."""
+    from ssa_amd import kernels
+
+    cfg = lc["cfg"]
+    q, k, v, order, pfx, idx = lc["q"], lc["k"], lc["v"], lc["order"], lc["pfx"], lc["idx_h"]
+    print(f"{cfg['n']}: routed backward", flush=True)
+    stats = kernels.row_stats_buffer(q, cfg["h_kv"])
+    out32 = torch.empty(q.shape, device=q.device, dtype=torch.float32)
+    kernels.sparse_attention(q, k, v, idx, None, True, out=out32, row_order=order, row_prefix=pfx,
+                             row_stats=stats)
+    gen = torch.Generator(device=q.device).manual_seed(7)
+    dout = torch.randn(q.shape, generator=gen, device=q.device).to(q.dtype)
+    routing = kernels.Routing(lc["qc"], lc["kc"], lc["off"], lc["post"], True)
+    routed = kernels.sparse_attention_backward(q, k, v, idx, out32, dout, None, True, row_order=order,
+                                               row_prefix=pfx, routing=routing, row_stats=stats)
+    plain = kernels.sparse_attention_backward(q, k, v, idx, out32, dout, None, True)
+    torch.cuda.synchronize()
+    for name, got, ref in zip(("dq", "dk", "dv"), routed, plain):
+        scale = float(ref.abs().max())
+        err = float((got - ref).abs().max())
+        assert err <= 2e-5 * scale, f"{name}: {err:.3e} > 2e-5 * {scale:.3e}"
+    del plain
+    # dq of sampled rows by float64 autograd through the reference's gather /
+    # softmax / weighted sum (ssa/attention.py:64-113) on the CPU
+    n, kk, h_kv, d = cfg["n"], cfg["k"], cfg["h_kv"], cfg["d"]
+    g = cfg["h_q"] // h_kv
+    rows = torch.from_numpy(_sample_rows(n - kk, [], seed=6, count=24) + kk)
+    ids = idx[0].cpu().long()[rows]                                   # [r, h_kv, kk]
+    qs = q[0].cpu().double()[rows].requires_grad_(True)               # [r, h_q, d]
+    kd, vd = k[0].cpu().double(), v[0].cpu().double()
+    hh = torch.arange(h_kv)[None, :, None]
+    kg, vg = kd[ids, hh], vd[ids, hh]                                 # [r, h_kv, kk, d]
+    logit = torch.matmul(qs.view(-1, h_kv, g, d), kg.transpose(-1, -2)) / d ** 0.5
+    o = torch.matmul(torch.softmax(logit, -1), vg).reshape(-1, cfg["h_q"], d)
+    (o * dout[0].cpu().double()[rows]).sum().backward()
+    ref = qs.grad
+    got = routed[0][0].cpu().double()[rows]
+    err = float((got - ref).abs().max())
+    assert err <= 2e-5 * float(ref.abs().max()), f"dq vs float64 autograd: {err:.3e}"

@@ -198,6 +198,48 @@ def test_sparse_attention_vs_numpy64(causal):
     np.testing.assert_allclose(got, ref, rtol=1e-12, atol=1e-12)
 
 
+def _reference_flat_gather64(q, k, v, idx, scale):
+    """ssa/attention.py:64-113 as its code runs it, in float64: K and V flattened
+    to [n*h_kv, d], index j of KV head h offset by h*n, then the grouped
+    logits, softmax and weighted sum."""
+    q, k, v = (torch.from_numpy(np.asarray(t, np.float64)) for t in (q, k, v))
+    n, h_q, d = q.shape
+    h_kv, kk = k.shape[1], idx.shape[-1]
+    flat = torch.from_numpy(idx).reshape(-1)
+    offs = (torch.arange(h_kv) * n)[None, :, None].expand(n, h_kv, kk).reshape(-1)
+    kg = k.reshape(n * h_kv, d)[flat + offs].reshape(n, h_kv, kk, d)
+    vg = v.reshape(n * h_kv, d)[flat + offs].reshape(n, h_kv, kk, d)
+    qg = q.reshape(n, h_kv, h_q // h_kv, d)
+    w = torch.softmax(torch.einsum("nhgd,nhkd->nhgk", qg, kg) / scale, dim=-1)
+    return torch.einsum("nhgk,nhkd->nhgd", w, vg).reshape(n, h_q, d).numpy()
+
+
+def test_flat_gather_view_is_the_reference_code_gather():
+    """flat_gather_view(t)[j, h] is row j + h*n of t flattened to [n*h_kv, d], so
+    the oracle fed with that layout computes what ssa/attention.py:76-113's code
+    does (not its docstring's K[j, h]); h_kv = 1 leaves the rows unchanged."""
+    from ssa_amd.attention import flat_gather_view
+
+    n, h_q, h_kv, d, kk = 37, 6, 3, 8, 9
+    t = torch.randn(2, n, h_kv, d, dtype=torch.float64)
+    view = flat_gather_view(t)
+    assert view.shape == t.shape and view.data_ptr() == t.data_ptr()   # a view, no copy
+    flat = t.reshape(2, n * h_kv, d)
+    for j in range(n):
+        for h in range(h_kv):
+            assert torch.equal(view[:, j, h], flat[:, j + h * n])
+    one = torch.randn(n, 1, d)
+    assert torch.equal(flat_gather_view(one), one)
+    q, k, v = (f32(randn(s, 90 + i)) for i, s in enumerate(((n, h_q, d), (n, h_kv, d), (n, h_kv, d))))
+    idx = np.random.default_rng(3).integers(0, n, size=(n, h_kv, kk)).astype(np.int64)
+    ref = _reference_flat_gather64(q, k, v, idx, d ** 0.5)
+    kf = np.ascontiguousarray(flat_gather_view(torch.from_numpy(k)).numpy())
+    vf = np.ascontiguousarray(flat_gather_view(torch.from_numpy(v)).numpy())
+    np.testing.assert_allclose(oracle.sparse_attention(q, kf, vf, idx), ref, rtol=1e-12, atol=1e-12)
+    # the docstring semantics differ from the code's whenever h_kv > 1
+    assert np.abs(oracle.sparse_attention(q, k, v, idx) - ref).max() > 1e-3
+
+
 def test_attention_k_equals_n_matches_torch_sdpa():
     """Library cross-check: k = n sparse (causal) == dense == torch SDPA (float64)."""
     n, h_q, h_kv, d = 64, 8, 2, 32
