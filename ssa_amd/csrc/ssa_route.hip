@@ -606,7 +606,8 @@ __host__ __device__ constexpr int mf_cap(int q) { return q <= 1 ? 16 : q <= 2 ? 
 // LDS: one region used first for the segment maxima ([4 waves][4M][64] fp32),
 // then for the pass-3 lists ([4][top][64] u64, top > 16 only: smaller tops keep
 // them in registers) followed by the pass-2 candidates ([4 waves][4 row
-// tiles][mf_cap][64 lanes] u16); the list counts ([4][4][64] int) come after it.
+// tiles][mf_cap][64 lanes] u16).  The list counts stay in registers and reach
+// pass 3 by cross-lane shuffles.
 __host__ __device__ constexpr size_t mf_list_bytes(int top) {
   return mf_q(top) >= 8 ? static_cast<size_t>(4) * top * 64 * sizeof(uint64_t) : 0;
 }
@@ -617,9 +618,7 @@ __host__ __device__ inline size_t code_topk_mfma_region(int top) {
   return lists + cand > segs ? lists + cand : segs;
 }
 
-__host__ __device__ inline size_t code_topk_mfma_smem(int top) {
-  return code_topk_mfma_region(top) + sizeof(int) * 4 * 4 * 64;
-}
+__host__ __device__ inline size_t code_topk_mfma_smem(int top) { return code_topk_mfma_region(top); }
 
 // bf16 copy of the codebook, zero-padded to [h][n_c_pad][32], and the largest
 // row norm per head accumulated by atomicMax on the (non-negative) float bits
@@ -718,13 +717,11 @@ __device__ __forceinline__ void code_topk_mfma_block(
     const uint16_t* __restrict__ cbf, const uint32_t* __restrict__ cmax_bits, int n_c, int d_s,
     float temperature, int top, int32_t* __restrict__ codes, uint8_t* __restrict__ flags, int64_t blk) {
   constexpr int M = mf_segments(Q);  // segment maxima per lane and row
-  constexpr int G = M > 8 ? M / 8 : 1;  // 8-tile groups per pass-1 step
   constexpr int CAP = mf_cap(Q);
   extern __shared__ __align__(16) unsigned char smem_raw[];
   const size_t list_bytes = mf_list_bytes(top);
   uint64_t* lists = reinterpret_cast<uint64_t*>(smem_raw);               // [4][top][64] (pass 3, Q = 8)
   uint16_t* cand = reinterpret_cast<uint16_t*>(smem_raw + list_bytes);   // [4][4][CAP][64] (pass 2)
-  int* qcnt = reinterpret_cast<int*>(smem_raw + code_topk_mfma_region(top));  // [4][4][64]
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int q4 = lane >> 4, c16 = lane & 15;
@@ -736,26 +733,42 @@ __device__ __forceinline__ void code_topk_mfma_block(
   const float* xb = xhat + bh * rows * d_s;
   const uint16_t* cbh = cbf + static_cast<int64_t>(hh) * n_c_pad * 32;
 
+  // Rows load as float4s (d_s is a multiple of 4, so a row starts 16-byte
+  // aligned and a float4 lies wholly below d_s or wholly above it); all of a
+  // lane's loads are issued before the first use.
+  auto row4 = [&](int64_t row, int s4) -> float4 {
+    return (row < rows && 4 * s4 < d_s) ? *reinterpret_cast<const float4*>(xb + row * d_s + 4 * s4)
+                                        : make_float4(0.f, 0.f, 0.f, 0.f);
+  };
+  float4 xl[4][2];
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) xl[nt][j] = row4(r0 + nt * 16 + c16, 2 * q4 + j);
+  float4 xe[8];
+#pragma unroll
+  for (int s4 = 0; s4 < 8; ++s4) xe[s4] = row4(r0 + lane, s4);
   bf16x8_t bfrag[4];
 #pragma unroll
   for (int nt = 0; nt < 4; ++nt) {
-    const int64_t row = r0 + nt * 16 + c16;
+    const float f[8] = {xl[nt][0].x, xl[nt][0].y, xl[nt][0].z, xl[nt][0].w,
+                        xl[nt][1].x, xl[nt][1].y, xl[nt][1].z, xl[nt][1].w};
     uint16_t tmp[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int dim = q4 * 8 + e;
-      tmp[e] = bf16_rne((row < rows && dim < d_s) ? xb[row * d_s + dim] : 0.0f);
-    }
+    for (int e = 0; e < 8; ++e) tmp[e] = bf16_rne(f[e]);
     bfrag[nt] = __builtin_bit_cast(bf16x8_t, tmp);
   }
   float eps_l = 0.0f;
-  {
-    const int64_t row = r0 + lane;
-    if (row < rows) {
-      float nrm2 = 0.0f;
-      for (int s = 0; s < d_s; ++s) nrm2 = fma_rn(xb[row * d_s + s], xb[row * d_s + s], nrm2);
-      eps_l = kMfEps * sqrtf(nrm2) * __uint_as_float(cmax_bits[hh]) * 1.0001f;
+  if (r0 + lane < rows) {
+    float nrm2 = 0.0f;
+#pragma unroll
+    for (int s4 = 0; s4 < 8; ++s4) {  // entries past d_s are zero
+      nrm2 = fma_rn(xe[s4].x, xe[s4].x, nrm2);
+      nrm2 = fma_rn(xe[s4].y, xe[s4].y, nrm2);
+      nrm2 = fma_rn(xe[s4].z, xe[s4].z, nrm2);
+      nrm2 = fma_rn(xe[s4].w, xe[s4].w, nrm2);
     }
+    eps_l = kMfEps * sqrtf(nrm2) * __uint_as_float(cmax_bits[hh]) * 1.0001f;
   }
   const bool bad_l = !(eps_l <= 3.0e38f);
 
@@ -767,76 +780,65 @@ __device__ __forceinline__ void code_topk_mfma_block(
 
   // ---- pass 1: segment maxima.  Codebook fragments come straight from the
   // (L2-resident) bf16 codebook: lane (q4, c16) reads 16 bytes of code
-  // tile*16 + c16.  Eight tiles per group, each feeding four independent MFMAs
-  // (one per 16-row tile); a step of G groups covers 8G tiles and tile j of the
-  // step updates segment j % M.  The remaining full 8-tile groups and the last
-  // (at most 8) tiles use segments 0..7; only the last tile can hold codes past
-  // n_c and is masked.  Any tile-to-segment map keeps the segments of one lane
-  // disjoint, which is all the bound needs.
+  // tile*16 + c16.  Each tile feeds four independent MFMAs (one per 16-row
+  // tile); tile t of the codebook updates segment t % M, so one lane's segments
+  // stay disjoint, which is all the bound needs.  Tiles go in groups of GT, the
+  // next group's fragments loading while the current group's MFMAs run (the
+  // prefetch start is clamped to the last full group, so every load is in
+  // range).  Only the last tile can hold codes past n_c and is masked.
+  constexpr int GT = 4;                      // tiles per load group
+  constexpr int STEP = M > GT ? M : GT;      // tiles per unrolled step (segment period)
   const int ntile_full = n_c / 16;
   const int ntile = n_c_pad / 16;
   auto frag = [&](int tile) -> bf16x8_t {
     return *reinterpret_cast<const bf16x8_t*>(cbh + (static_cast<int64_t>(tile) * 16 + c16) * 32 + q4 * 8);
   };
-  // The next 8-tile group's fragments load while the current group's MFMAs run;
-  // the prefetch start is clamped to the last full group, so every load is in
-  // range (the extra one near the end re-reads a group already used).  Q = 8
-  // (128 segment maxima in registers) loads each group just before use.
-  constexpr bool PF = Q < 8;
-  auto load8 = [&](bf16x8_t (&a)[8], int t) {
+  const int lastg = ntile_full - GT;  // first tile of the last full group (used when >= 0)
+  auto loadg = [&](bf16x8_t (&a)[GT], int t) {
 #pragma unroll
-    for (int u = 0; u < 8; ++u) a[u] = frag(t + u);
+    for (int u = 0; u < GT; ++u) a[u] = frag(t + u);
   };
-  auto group8 = [&](const bf16x8_t (&a)[8], int seg0) {
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      floatx4_t sc[4];
-#pragma unroll
-      for (int nt = 0; nt < 4; ++nt)
-        sc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[u], bfrag[nt], floatx4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-#pragma unroll
-      for (int nt = 0; nt < 4; ++nt)
-        smax[nt][(seg0 + u) % M] =
-            vmax(vmax(vmax(sc[nt][0], sc[nt][1]), sc[nt][2]), vmax(sc[nt][3], smax[nt][(seg0 + u) % M]));
-    }
-  };
-  const int last8 = ntile_full - 8;  // first tile of the last full group (used when >= 0)
   {
     int t = 0;
-    bf16x8_t a[8];
-    if (PF && ntile_full >= 8) load8(a, 0);
-    auto step = [&](int tg, int seg0) {  // group at tile tg; `a` holds it when PF
-      if constexpr (PF) {
-        bf16x8_t an[8];
-        load8(an, min(tg + 8, last8));
-        group8(a, seg0);
+    bf16x8_t a[GT];
+    if (ntile_full >= GT) loadg(a, 0);
+    for (; t + STEP <= ntile_full; t += STEP) {
 #pragma unroll
-        for (int u = 0; u < 8; ++u) a[u] = an[u];
-      } else {
-        load8(a, tg);
-        group8(a, seg0);
-      }
-    };
-    for (; t + 8 * G <= ntile_full; t += 8 * G) {
+      for (int gi = 0; gi < STEP / GT; ++gi) {
+        bf16x8_t an[GT];
+        loadg(an, min(t + GT * (gi + 1), lastg));
 #pragma unroll
-      for (int gi = 0; gi < G; ++gi) step(t + 8 * gi, 8 * gi);
-    }
-    if (G > 1)
-      for (; t + 8 <= ntile_full; t += 8) step(t, 0);
+        for (int u = 0; u < GT; ++u) {
+          floatx4_t sc[4];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      if (t + u < ntile) {
-        const bf16x8_t af = frag(t + u);
-        const int cbase = (t + u) * 16 + q4 * 4;
+          for (int nt = 0; nt < 4; ++nt)
+            sc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[u], bfrag[nt], floatx4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 #pragma unroll
-        for (int nt = 0; nt < 4; ++nt) {
-          const floatx4_t sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bfrag[nt], floatx4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-          float m = -INFINITY;
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (cbase + e < n_c) m = vmax(m, sc[e]);
-          smax[nt][u % M] = vmax(smax[nt][u % M], m);
+          for (int nt = 0; nt < 4; ++nt) {
+            float& m = smax[nt][(gi * GT + u) % M];
+            m = vmax(vmax(vmax(sc[nt][0], sc[nt][1]), sc[nt][2]), vmax(sc[nt][3], m));
+          }
         }
+#pragma unroll
+        for (int u = 0; u < GT; ++u) a[u] = an[u];
+      }
+    }
+    // the remaining tiles (fewer than STEP), the last one masked past n_c;
+    // tile t still updates segment t % M
+    for (; t < ntile; ++t) {
+      const bf16x8_t af = frag(t);
+      const int cbase = t * 16 + q4 * 4;
+      const int seg = t % M;
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) {
+        const floatx4_t sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bfrag[nt], floatx4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        float m = -INFINITY;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (cbase + e < n_c) m = vmax(m, sc[e]);
+#pragma unroll
+        for (int u = 0; u < M; ++u)
+          if (u == seg) smax[nt][u] = vmax(smax[nt][u], m);
       }
     }
   }
@@ -872,66 +874,99 @@ __device__ __forceinline__ void code_topk_mfma_block(
     for (int i = 1; i < C; ++i)
       if (i == top - 1) lb = v[i];
     thr_l = lb - 2.0f * eps_l;
-    if (r0 + lane >= rows) thr_l = INFINITY;  // padding rows collect nothing
+    // padding rows and rows with a non-finite bound collect nothing (the
+    // latter are flagged for the exhaustive kernel)
+    if (r0 + lane >= rows || bad_l || !(thr_l == thr_l)) thr_l = INFINITY;
   }
   __syncthreads();  // pass 2 writes candidates over other waves' maxima
-  float thr[4];
-#pragma unroll
-  for (int nt = 0; nt < 4; ++nt) thr[nt] = __shfl(thr_l, nt * 16 + c16);
 
   // ---- pass 2: collect codes whose approximate score reaches the threshold.
-  // Lane (q4, c16) owns the list of row nt*16 + c16 and code quarter q4 of row
-  // tile nt; qc[nt] counts its hits (past CAP the last slot is overwritten and
-  // the count flags the row).  Each score's append is skipped by a uniform
-  // branch unless some lane hits with that score.
+  // The MFMA starts from C = -thr of each lane's row, so it yields D = score -
+  // thr (the bound below covers the extra rounding), and a score hits exactly
+  // when D's sign bit is clear.  Each score costs one v_alignbit that shifts
+  // that sign bit into the lane's word for its row tile: after a group of 8
+  // tiles, bit 31 - (4u + e) of hits[nt] belongs to code (t0 + u) * 16 +
+  // 4 q4 + e.  The set bits of the inverted words are then appended to the
+  // lane's list of (row nt*16 + c16, code quarter q4) -- a few iterations per
+  // group, instead of a compare and branch per score.  Past CAP entries the
+  // last slot is overwritten and the count flags the row.
+  floatx4_t cneg[4];
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) {
+    const float t = -__shfl(thr_l, nt * 16 + c16);
+    cneg[nt] = floatx4_t{t, t, t, t};
+  }
   uint16_t* cl = cand + static_cast<size_t>(wave) * 4 * CAP * 64 + lane;  // list nt: cl[(nt*CAP + pos)*64]
   int qc[4] = {0, 0, 0, 0};
-  auto collect = [&](const floatx4_t& sc, int nt, int cbase, bool partial) {
+  uint32_t bits[4];
+  auto shift_in = [&](const floatx4_t& d, int nt) {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const bool hit = sc[e] >= thr[nt] && (!partial || cbase + e < n_c);
-      if (__builtin_expect(hit, 0)) {
-        cl[(nt * CAP + min(qc[nt], CAP - 1)) * 64] = static_cast<uint16_t>(cbase + e);
-        ++qc[nt];
+    for (int e = 0; e < 4; ++e) bits[nt] = __builtin_amdgcn_alignbit(bits[nt], __float_as_uint(d[e]), 31);
+  };
+  auto append = [&](int t0, bool partial) {
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+      uint32_t hm = ~bits[nt];
+      while (hm) {
+        const int b = __builtin_ctz(hm);
+        hm &= hm - 1u;
+        const int v = 31 - b;  // 4u + e
+        const int code = t0 * 16 + ((v >> 2) << 4) + 4 * q4 + (v & 3);
+        if (!partial || code < n_c) {
+          cl[(nt * CAP + min(qc[nt], CAP - 1)) * 64] = static_cast<uint16_t>(code);
+          ++qc[nt];
+        }
       }
     }
   };
   {
-    // full 8-tile groups (prefetched as in pass 1), then the remaining tiles,
-    // including the one that can hold codes past n_c, with the code check
     int t = 0;
-    bf16x8_t a[8], an[8];
-    if (PF && ntile_full >= 8) load8(a, 0);
+    bf16x8_t a[GT];
+    if (ntile_full >= GT) loadg(a, 0);
     for (; t + 8 <= ntile_full; t += 8) {
-      if constexpr (PF)
-        load8(an, min(t + 8, last8));
-      else
-        load8(a, t);
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        floatx4_t sc[4];
+      for (int nt = 0; nt < 4; ++nt) bits[nt] = 0u;
 #pragma unroll
-        for (int nt = 0; nt < 4; ++nt)
-          sc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[u], bfrag[nt], floatx4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+      for (int gi = 0; gi < 8 / GT; ++gi) {
+        bf16x8_t an[GT];
+        loadg(an, min(t + GT * (gi + 1), lastg));
 #pragma unroll
-        for (int nt = 0; nt < 4; ++nt) collect(sc[nt], nt, (t + u) * 16 + q4 * 4, false);
+        for (int u = 0; u < GT; ++u) {
+          floatx4_t sc[4];
+#pragma unroll
+          for (int nt = 0; nt < 4; ++nt) sc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[u], bfrag[nt], cneg[nt], 0, 0, 0);
+#pragma unroll
+          for (int nt = 0; nt < 4; ++nt) shift_in(sc[nt], nt);
+        }
+#pragma unroll
+        for (int u = 0; u < GT; ++u) a[u] = an[u];
       }
-      if constexpr (PF) {
-#pragma unroll
-        for (int u = 0; u < 8; ++u) a[u] = an[u];
-      }
+      // every shift of the group happens here, before the append loops: left
+      // to itself the compiler sinks them past the first loop and keeps the
+      // group's 32 MFMA results live across it
+      asm volatile("" : "+v"(bits[0]), "+v"(bits[1]), "+v"(bits[2]), "+v"(bits[3]));
+      append(t, false);
     }
-    for (; t < ntile; ++t) {
-      const bf16x8_t af = frag(t);
+    if (t < ntile) {
+      // the last, partial group: tiles past ntile shift in misses
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt)
-        collect(__builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bfrag[nt], floatx4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0),
-                nt, t * 16 + q4 * 4, true);
+      for (int nt = 0; nt < 4; ++nt) bits[nt] = 0u;
+      for (int u = 0; u < 8; ++u) {
+        if (t + u < ntile) {
+          const bf16x8_t af = frag(t + u);
+#pragma unroll
+          for (int nt = 0; nt < 4; ++nt)
+            shift_in(__builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bfrag[nt], cneg[nt], 0, 0, 0), nt);
+        } else {
+#pragma unroll
+          for (int nt = 0; nt < 4; ++nt) bits[nt] = (bits[nt] << 4) | 0xFu;
+        }
+      }
+      asm volatile("" : "+v"(bits[0]), "+v"(bits[1]), "+v"(bits[2]), "+v"(bits[3]));
+      append(t, true);
     }
   }
-#pragma unroll
-  for (int nt = 0; nt < 4; ++nt) qcnt[(wave * 4 + nt) * 64 + lane] = qc[nt];
-  __syncthreads();
+  __syncthreads();  // every wave's lists are complete
 
   // ---- pass 3: exact rescoring of the collected codes (one lane per row).
   // Row `lane` is row tile lane / 16, column lane % 16; its four quarter lists
@@ -942,7 +977,14 @@ __device__ __forceinline__ void code_topk_mfma_block(
   bool list_over = false;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
-    qn[q] = qcnt[(wave * 4 + rt) * 64 + q * 16 + rc];
+    // lane q*16 + rc holds the counts of quarter q for the four row tiles
+    int c = 0;
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+      const int v = __shfl(qc[nt], q * 16 + rc);
+      c = (rt == nt) ? v : c;
+    }
+    qn[q] = c;
     list_over = list_over || qn[q] > CAP;
     m += qn[q];
   }
@@ -979,7 +1021,8 @@ __device__ __forceinline__ void code_topk_mfma_block(
       if (scale) acc = acc / temperature;
       return composite_key(acc, static_cast<uint32_t>(c));
     };
-    // The next candidate's code row loads while the current one is scored.
+    // One code row in flight per lane (a second buffer would hold 32 more
+    // VGPRs for the whole kernel; the other resident waves cover the latency).
     int c = code_at(0);
     float4 cv[8];
     code_row(c, cv);
@@ -992,13 +1035,8 @@ __device__ __forceinline__ void code_topk_mfma_block(
 #pragma unroll
       for (int p = 0; p < TM; ++p) best[p] = 0ull;  // below every key
       for (int i = 0; i < m; ++i) {
-        const int cn = code_at(min(i + 1, m - 1));
-        float4 cvn[8];
-        code_row(cn, cvn);
+        if (i > 0) { c = code_at(i); code_row(c, cv); }
         const uint64_t key = exact_key(c, cv);
-        c = cn;
-#pragma unroll
-        for (int s4 = 0; s4 < 8; ++s4) cv[s4] = cvn[s4];
 #pragma unroll
         for (int p = TM - 1; p > 0; --p) best[p] = key > best[p - 1] ? best[p - 1] : (key > best[p] ? key : best[p]);
         best[0] = key > best[0] ? key : best[0];
@@ -1050,12 +1088,20 @@ __global__ __launch_bounds__(256, 1) void code_topk_mfma_pair_kernel(
     int n_c, int d_s, float temperature, int top_a, int top_b, int32_t* __restrict__ codes_a,
     int32_t* __restrict__ codes_b, uint8_t* __restrict__ flags_a, uint8_t* __restrict__ flags_b,
     int64_t grid_a) {
-  const int64_t blk = blockIdx.x;
-  if (blk < grid_a)
-    code_topk_mfma_block<QA>(xa, rows, h, chat, cbf, cmax_bits, n_c, d_s, temperature, top_a, codes_a, flags_a, blk);
+  // Logical block L: (batch, kv head) L / (2T), then that head's T query blocks
+  // and T key blocks (T row tiles per head).  xcd_block gives XCD x the
+  // contiguous range [x per, (x + 1) per), so one XCD's L2 holds the bf16 and
+  // fp32 codebooks of about one head instead of a slice of every head's.
+  const int64_t tiles = (rows + kMfRows - 1) / kMfRows;
+  const int64_t lb = xcd_block(blockIdx.x, xcd_per(2 * grid_a));
+  if (lb >= 2 * grid_a) return;
+  const int64_t bh = lb / (2 * tiles), i = lb - bh * 2 * tiles;
+  if (i < tiles)
+    code_topk_mfma_block<QA>(xa, rows, h, chat, cbf, cmax_bits, n_c, d_s, temperature, top_a, codes_a, flags_a,
+                             bh * tiles + i);
   else
     code_topk_mfma_block<QB>(xb, rows, h, chat, cbf, cmax_bits, n_c, d_s, temperature, top_b, codes_b, flags_b,
-                             blk - grid_a);
+                             bh * tiles + i - tiles);
 }
 
 // Exact top-`top` codes of the rows flagged by the matrix-core filter
@@ -1790,7 +1836,8 @@ int launch_mfma_pair(const float* xa, const float* xb, int64_t batch, int h, int
   const size_t smem = std::max(code_topk_mfma_smem(top_a), code_topk_mfma_smem(top_b));
   if (int s = reserve_lds(reinterpret_cast<const void*>(kern), smem, "code_topk_mfma_pair")) return s;
   const int64_t grid_a = batch * h * ceil_div(rows, kMfRows);
-  kern<<<dim3(static_cast<unsigned>(2 * grid_a)), 256, smem, st>>>(xa, xb, rows, h, chat, w.cbf, w.cmax_bits, n_c,
+  const int64_t grid = kXcds * xcd_per(2 * grid_a);  // whole rounds of the 8 XCDs; extras return at once
+  kern<<<dim3(static_cast<unsigned>(grid)), 256, smem, st>>>(xa, xb, rows, h, chat, w.cbf, w.cmax_bits, n_c,
                                                                    d_s, temperature, top_a, top_b, codes_a, codes_b,
                                                                    w.flags, flags_b, grid_a);
   return check_launch("code_topk_mfma_pair_kernel");
