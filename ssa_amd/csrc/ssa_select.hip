@@ -895,23 +895,31 @@ __global__ __launch_bounds__(64) void select_light_kernel(SelParams p, int64_t r
   // filler, and 0 when index-0 padding repeats a key).
   const bool want_x = p.prefix != nullptr && p.k_eff == p.top_k;
   if (p.prefix && lane == 0 && (filled >= p.k_eff || !want_x)) p.prefix[row] = 0;
-  for (int w0 = 0; filled < p.k_eff; w0 += 64) {
-    const int x = w0 + lane;
-    uint32_t bits = 0u;
+  // One key per lane: 64 consecutive keys (two bitmap words) per step, lane l
+  // taking key w0*32 + l; a key the row does not hold goes to position
+  // `filled` + the number of such keys on lower lanes (one mask count).  The
+  // filler lies in the keys below k_eff + C <= 2 k_eff, so at most 2 k_eff / 64
+  // + 1 steps run, each a few instructions with no per-bit loop, and the
+  // stores of a step are contiguous.
+  for (int w0 = 0; filled < p.k_eff; w0 += 2) {
+    const int x = w0 + (lane >> 5);
+    uint32_t nb = 0u;  // keys of word x the row does not hold (and that exist)
     if (x < words) {
       const bool set = x < live && (flat || ((sm[x >> 5] >> (x & 31)) & 1u));
-      bits = ~(set ? bm[x] : 0u);
-      if (x == words - 1 && (p.n & 31)) bits &= (1u << (p.n & 31)) - 1u;
+      nb = ~(set ? bm[x] : 0u);
+      if (x == words - 1 && (p.n & 31)) nb &= (1u << (p.n & 31)) - 1u;
     }
-    int total = 0;
-    int pos = filled + wave_excl_scan(__popc(bits), lane, &total);
-    while (bits != 0u && pos < p.k_eff) {
-      const int key = x * 32 + __ffs(bits) - 1;
+    const bool mine = (nb >> (lane & 31)) & 1u;
+    const uint64_t bal = __ballot(mine);
+    const int pos = filled + static_cast<int>(__builtin_amdgcn_mbcnt_hi(
+                                 static_cast<uint32_t>(bal >> 32),
+                                 __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bal), 0u)));
+    if (mine && pos < p.k_eff) {
+      const int key = x * 32 + (lane & 31);
       if (want_x && pos == p.k_eff - 1) p.prefix[row] = key + 1;
-      put(pos++, key);
-      bits &= bits - 1u;
+      put(pos, key);
     }
-    filled += total;
+    filled += __popcll(bal);
   }
   for (int x = p.k_eff + lane; x < p.top_k; x += 64) put(x, 0);
 }
