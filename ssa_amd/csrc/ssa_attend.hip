@@ -503,9 +503,9 @@ __global__ __launch_bounds__(kAttThreads, (AttMinBlocks<T, D, GMAX>::value)) voi
 // bytes in flight per CU are LDS-bound; the waves share nothing, so one-wave
 // blocks let a CU hold 10 of them (160 KB) and start each as soon as one ends
 // (c3 stage d: 3.90 ms against 4.04 with four-wave blocks, 3.95 with two).
-// At least 2 waves per SIMD.  Forcing 3 (168 VGPRs at d = 128, so that the
-// LDS's 10 waves per CU are the limit) helped only while the loop stalled on
-// its index loads; with those fixed it costs 0.5 ms at c5 and gains nothing at c3.
+// At least 2 waves per SIMD.  The d = 128 build needs 167 VGPRs (3 waves per
+// SIMD), so the LDS's 10 waves per CU are the limit; forcing that bound while
+// the build needed more cost 0.5 ms at c5 (spills) and gained nothing at c3.
 constexpr int kMfWaves = 1;
 constexpr int kMfMinWavesPerEu = 2;
 
@@ -659,7 +659,12 @@ __device__ __forceinline__ void attend_row_mfma(const AttParams& p, const AttRow
     lc.all_live(nmine);
   // The next live chunk's index entries (jn_raw, for chunk un) are loaded
   // while the current chunk's gathers fly and checked only after the wait
-  // that the gathers need anyway.
+  // that the gathers need anyway.  Every chunk issues its loads, also one
+  // whose slots all turn out dropped (only a chunk past the causal cut can):
+  // those load zeros, its scores are masked to -inf and it adds nothing, and
+  // the loop keeps a single path, so the accumulators stay in place across
+  // iterations (a separate skip path made the compiler copy all 32 of them
+  // twice per chunk).
   int u = lc.next(-1);
   int un = nmine;
   uint64_t okbits = 0;
@@ -668,7 +673,7 @@ __device__ __forceinline__ void attend_row_mfma(const AttParams& p, const AttRow
     const int j0 = lc.get(u, lane, [&](int v) { return load_idx(chunk_of(v)); });
     const bool ok0 = chunk_ok(j0);
     okbits = __ballot(ok0);
-    if (okbits) issue(ok0 ? j0 : -1, static_cast<uint32_t>(okbits) == 0xFFFFFFFFu);
+    issue(ok0 ? j0 : -1, static_cast<uint32_t>(okbits) == 0xFFFFFFFFu);
     un = lc.next(u);
     if (un < nmine) jn_raw = raw_at(chunk_of(un), lane);
   }
@@ -680,19 +685,13 @@ __device__ __forceinline__ void attend_row_mfma(const AttParams& p, const AttRow
       const int jn = key_at(chunk_of(u), lane, jn_raw);
       const bool okn = chunk_ok(jn);
       okbits = __ballot(okn);
-      if (okbits) issue(okn ? jn : -1, static_cast<uint32_t>(okbits) == 0xFFFFFFFFu);
+      issue(okn ? jn : -1, static_cast<uint32_t>(okbits) == 0xFFFFFFFFu);
       if (NSPLIT == 1 && p.gather_wait) __builtin_amdgcn_s_waitcnt(kWaitVm0);  // (not the few-row split kernel)
       un = lc.next(u);
       if (un < nmine) jn_raw = raw_at(chunk_of(un), lane);
     }
   };
   while (u < nmine) {
-    // (only a chunk past the mask can turn out empty here)
-    if (okbits == 0) {
-      __builtin_amdgcn_s_waitcnt(kWaitVm0);
-      advance();
-      continue;
-    }
     // This chunk's rows are in LDS once its loads have completed.
     __builtin_amdgcn_s_waitcnt(kWaitVm0);
     bf16x8_t kf[2][S::KB];
