@@ -102,6 +102,21 @@ __device__ __forceinline__ int att_key(const AttParams& p, int slot, int64_t jv)
   return j < p.n ? static_cast<int>(j) : -1;
 }
 
+// att_key for a whole wave without divergent branches (the matrix-core row
+// kernel): `use` marks the slots read; an invalid index among them raises the
+// flag in a branch that only a wave holding one takes.
+template <bool BLK>
+__device__ __forceinline__ int att_key_wave(const AttParams& p, int slot, int64_t jv, bool use) {
+  const bool bad = use && static_cast<uint64_t>(jv) >= static_cast<uint64_t>(BLK ? p.nbk : p.n);
+  if (__ballot(bad) != 0ull && p.err != nullptr && bad) p.err[0] = 1;
+  int key = static_cast<int>(jv);
+  if constexpr (BLK) {
+    const int64_t j = (jv << p.blk_log2) + (slot & ((1 << p.blk_log2) - 1));
+    key = j < p.n ? static_cast<int>(j) : -1;
+  }
+  return !use ? -1 : bad ? -2 : key;
+}
+
 // Row processed by wave slot `lrow` (in (b*h_kv + h)*n_q + slot order): the query
 // row r is the slot itself, or order[lrow] when a processing order is given; it
 // sits at key position i = q_pos0 + r (the causal cut).  An order entry outside
@@ -573,7 +588,8 @@ __device__ __forceinline__ void attend_row_mfma(const AttParams& p, const AttRow
   // check's wait away from the load: a batch of index loads goes out before
   // the first check, and the next chunk's indices fly with its K/V gathers.
   // (two dword loads with no branch on the index type: the low word, and the
-  // high word or, for int32 entries, the same word again)
+  // high word or, for int32 entries, the same word again; a branch here would
+  // make the compiler wait for the load, and with it for the chunk's gathers)
   auto slot_at = [&](int ch, int l) { return row_ok && l < kMfChunk && ch * kMfChunk + l < p.top_k; };
   const int ewords = p.idx_i64 ? 2 : 1;
   const uint32_t* iwords = static_cast<const uint32_t*>(p.idx) + ibase * ewords;
@@ -585,7 +601,7 @@ __device__ __forceinline__ void attend_row_mfma(const AttParams& p, const AttRow
   auto key_at = [&](int ch, int l, uint64_t raw) -> int {
     const int64_t jv = p.idx_i64 ? static_cast<int64_t>(raw)
                                  : static_cast<int64_t>(static_cast<int32_t>(static_cast<uint32_t>(raw)));
-    return slot_at(ch, l) ? att_key<BLK>(p, ch * kMfChunk + l, jv) : -1;
+    return att_key_wave<BLK>(p, ch * kMfChunk + l, jv, slot_at(ch, l));
   };
   auto load_idx = [&](int ch) { return key_at(ch, lane, raw_at(ch, lane)); };
   // Load r of a chunk: lane l fetches the segment stored in slot l % SEGS of
@@ -620,7 +636,9 @@ __device__ __forceinline__ void attend_row_mfma(const AttParams& p, const AttRow
                        ? min(max(p.pfx_x[bh * p.n_q + qr], 0),
                              static_cast<int>(min(static_cast<int64_t>(p.top_k), p.n)))
                        : 0;
-  auto chunk_ok = [&](int j) { return j >= xpre && !(p.causal && j > i); };
+  // (the causal cut as an int: keys and n fit 24 bits)
+  const int icut = p.causal ? static_cast<int>(min(i, static_cast<int64_t>(INT32_MAX))) : INT32_MAX;
+  auto chunk_ok = [&](int j) { return j >= xpre && j <= icut; };
 
   // Fragment addresses (fixed per lane): K tile t, block kb; V^T tile t (rows
   // 4*q4 + c16/4, +16 for the second half of the chunk).
@@ -630,6 +648,8 @@ __device__ __forceinline__ void attend_row_mfma(const AttParams& p, const AttRow
 
   const bool hi_row = c16 < p.g;
   const bool lo_row = c16 >= 8 && c16 < 8 + p.g;
+  const bool cpos = p.qk_scale_log2 > 0.0f && p.qk_scale_log2 <= 3.4e38f;
+  const float cmul = cpos ? p.qk_scale_log2 : 1.0f;
   float m_run = -INFINITY;
   float l_run = 0.0f;
   floatx4_t oacc[S::NT];
@@ -716,7 +736,10 @@ __device__ __forceinline__ void attend_row_mfma(const AttParams& p, const AttRow
     okbits = 0;
     advance();
 
-    // Scores of eight keys of head c16 (keys 16t + 4*q4 + e).
+    // Scores of eight keys of head c16 (keys 16t + 4*q4 + e), unscaled: the
+    // scale c enters through the running maximum (max(s) c is the maximum of
+    // the scaled scores for c > 0) and the exponent's fma.  A caller's scale
+    // that makes c non-positive or infinite scales the scores first (cmul = 1).
     float sc[8];
     const bool full = static_cast<uint32_t>(okb) == 0xFFFFFFFFu;
 #pragma unroll
@@ -727,7 +750,11 @@ __device__ __forceinline__ void attend_row_mfma(const AttParams& p, const AttRow
         for (int kb = 0; kb < S::KB; ++kb) s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[t][kb], qf[kb], s, 0, 0, 0);
       }
 #pragma unroll
-      for (int e = 0; e < 4; ++e) sc[4 * t + e] = s[e] * p.qk_scale_log2;
+      for (int e = 0; e < 4; ++e) sc[4 * t + e] = s[e];
+    }
+    if (!cpos) {
+#pragma unroll
+      for (int x = 0; x < 8; ++x) sc[x] *= p.qk_scale_log2;
     }
     if (!full) {
       // bit 16t + e: key 16t + 4*q4 + e ((lane >> 2) & 12 = 4*q4, recomputed here
@@ -739,11 +766,10 @@ __device__ __forceinline__ void attend_row_mfma(const AttParams& p, const AttRow
         for (int e = 0; e < 4; ++e)
           if (!((mine >> (16 * t + e)) & 1u)) sc[4 * t + e] = -INFINITY;
     }
-    float mx = sc[0];
-#pragma unroll
-    for (int x = 1; x < 8; ++x) mx = fmaxf(mx, sc[x]);
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    // (a NaN score makes the output NaN with either kind of maximum)
+    float mx = max_nan(max_nan(max_nan(sc[0], sc[1]), sc[2]), max_nan(sc[3], sc[4]));
+    mx = max_nan(max_nan(mx, sc[5]), max_nan(sc[6], sc[7]));
+    mx = rows4_reduce(mx, max_nan) * cmul;
     const float mnew = fmaxf(m_run, mx);
     // A head with no valid key yet (mnew = -inf) subtracts 0 instead: its
     // weights exp2(-inf) are 0 and alpha multiplies an all-zero state.
@@ -755,7 +781,7 @@ __device__ __forceinline__ void attend_row_mfma(const AttParams& p, const AttRow
     float ps = 0.0f;
 #pragma unroll
     for (int x = 0; x < 8; ++x) {
-      pr[x] = __builtin_amdgcn_exp2f(sc[x] - mref);
+      pr[x] = __builtin_amdgcn_exp2f(fmaf(sc[x], cmul, -mref));
       ps += pr[x];
     }
     l_run = l_run * alpha + ps;
@@ -784,8 +810,7 @@ __device__ __forceinline__ void attend_row_mfma(const AttParams& p, const AttRow
   }
 
   // l: partial sums of the four lanes holding a head's keys; O: hi row + lo row.
-  float lt = l_run + __shfl_xor(l_run, 16);
-  lt += __shfl_xor(lt, 32);
+  const float lt = rows4_reduce(l_run, [](float a, float b) { return a + b; });
 #pragma unroll
   for (int t = 0; t < S::NT; ++t)
 #pragma unroll

@@ -95,6 +95,23 @@ __device__ __forceinline__ float dpp_from_plus8(float x) {
   return __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(x), 0x108, 0xF, 0xF, false));
 }
 
+// NaN-propagating maximum (v_maximum3_f32 on gfx950): unlike fmaxf it needs no
+// canonicalizing v_max of a matrix-core result first.
+__device__ __forceinline__ float max_nan(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
+// Combine each lane's value with those of lanes l ^ 16, l ^ 32 and l ^ 48
+// (the four 16-lane rows): v_permlane16_swap / v_permlane32_swap exchange
+// whole rows in registers, so no LDS round trip (as a shuffle would take).
+// Each swap leaves lane l with its own value and its partner's, in some
+// order; op is symmetric.
+template <class Op>
+__device__ __forceinline__ float rows4_reduce(float x, Op op) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = op(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return op(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
 // V^T (or K^T) fragment of 16-feature tile t from a chunk's rows in LDS at `l`
 // (the A operand of O^T += V^T P^T): within each 16-lane group, lane p receives
 // element p mod 4 from the rows addressed by lanes p / 4 + 4e, which matches
