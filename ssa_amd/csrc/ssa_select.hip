@@ -267,6 +267,44 @@ __device__ __forceinline__ void rescore_rows2(const T* kr0, const T* kr1, const 
   }
 }
 
+// rescore_rows2 with the group's query rows already in LDS as fp32 (qs[gg * D
+// + t]): each lane reads them as broadcast float4s instead of reloading and
+// converting the bf16 rows for every key pair.  The same fmaf chains.
+template <int GMAX, int D>
+__device__ __forceinline__ void rescore_rows2_qs(const uint16_t* kr0, const uint16_t* kr1, const float* qs, int g,
+                                                 float (&acc0)[GMAX], float (&acc1)[GMAX]) {
+#pragma unroll
+  for (int gg = 0; gg < GMAX; ++gg) {
+    acc0[gg] = 0.0f;
+    acc1[gg] = 0.0f;
+  }
+  constexpr int G = kRescoreLoads;
+#pragma unroll 1
+  for (int t0 = 0; t0 < D; t0 += 8 * G) {
+    float kv0[G][8], kv1[G][8];
+#pragma unroll
+    for (int u = 0; u < G; ++u) {
+      load8(kr0 + t0 + 8 * u, kv0[u]);
+      load8(kr1 + t0 + 8 * u, kv1[u]);
+    }
+#pragma unroll
+    for (int gg = 0; gg < GMAX; ++gg) {
+      if (gg >= g) continue;
+#pragma unroll
+      for (int u = 0; u < G; ++u) {
+        const float4 a = *reinterpret_cast<const float4*>(qs + gg * D + t0 + 8 * u);
+        const float4 b = *reinterpret_cast<const float4*>(qs + gg * D + t0 + 8 * u + 4);
+        const float qv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          acc0[gg] = fma_rn(qv[e], kv0[u][e], acc0[gg]);
+          acc1[gg] = fma_rn(qv[e], kv1[u][e], acc1[gg]);
+        }
+      }
+    }
+  }
+}
+
 // One row ((b * h_kv + h) * n + i) by the whole block.  `heavy`: the row is
 // known to have more than k_eff candidates (index order only), so the counting
 // pass is skipped.
@@ -549,6 +587,9 @@ __device__ __forceinline__ void sort_slots_desc(uint64_t* keys, int lane) {
 template <typename T, int GMAX, int D>
 __global__ __launch_bounds__(64) void select_sort_kernel(SelParams p, const T* __restrict__ qg) {
   __shared__ uint64_t keys[kSortMax];
+  // bf16 inputs of a fixed head dim: the group's query rows as fp32, once per row
+  constexpr bool kQs = sizeof(T) == 2 && D > 0;
+  __shared__ __align__(16) float qs[kQs ? GMAX * D : 4];
   const int lane = threadIdx.x;
   const int64_t row = row_of_slot(p, blockIdx.x);
   if (row < 0) return;
@@ -565,6 +606,16 @@ __global__ __launch_bounds__(64) void select_sort_kernel(SelParams p, const T* _
   int64_t* o64 = static_cast<int64_t*>(p.out) + obase;
   int np = 64;
   while (np < m) np <<= 1;
+  if constexpr (kQs) {
+    for (int x = lane; x < p.g * (D / 8); x += 64) {
+      const int gg = x / (D / 8), t = (x % (D / 8)) * 8;
+      float v[8];
+      load8(reinterpret_cast<const uint16_t*>(q0) + static_cast<int64_t>(gg) * p.q_sh + t, v);
+      *reinterpret_cast<float4*>(qs + gg * D + t) = make_float4(v[0], v[1], v[2], v[3]);
+      *reinterpret_cast<float4*>(qs + gg * D + t + 4) = make_float4(v[4], v[5], v[6], v[7]);
+    }
+    __syncthreads();
+  }
   auto score_of = [&](const float (&acc)[GMAX]) {
     float sc = acc[0] / p.score_div;
 #pragma unroll
@@ -579,9 +630,15 @@ __global__ __launch_bounds__(64) void select_sort_kernel(SelParams p, const T* _
     const int32_t j1 = e2 < m ? (p.out_i64 ? static_cast<int32_t>(o64[e2]) : o32[e2]) : -1;
     if (j0 >= 0) {
       float acc0[GMAX], acc1[GMAX];
-      rescore_rows2<T, GMAX, D>(kbase + static_cast<int64_t>(j0) * p.k_sn,
-                                kbase + static_cast<int64_t>(j1 >= 0 ? j1 : j0) * p.k_sn, q0, p.q_sh, p.g, p.d,
-                                acc0, acc1);
+      if constexpr (kQs)
+        rescore_rows2_qs<GMAX, D>(reinterpret_cast<const uint16_t*>(kbase) + static_cast<int64_t>(j0) * p.k_sn,
+                                  reinterpret_cast<const uint16_t*>(kbase) +
+                                      static_cast<int64_t>(j1 >= 0 ? j1 : j0) * p.k_sn,
+                                  qs, p.g, acc0, acc1);
+      else
+        rescore_rows2<T, GMAX, D>(kbase + static_cast<int64_t>(j0) * p.k_sn,
+                                  kbase + static_cast<int64_t>(j1 >= 0 ? j1 : j0) * p.k_sn, q0, p.q_sh, p.g, p.d,
+                                  acc0, acc1);
       keys[e] = composite_key(score_of(acc0), static_cast<uint32_t>(j0));
       if (e2 < np) keys[e2] = j1 >= 0 ? composite_key(score_of(acc1), static_cast<uint32_t>(j1)) : 0ull;
     } else {
