@@ -266,6 +266,33 @@ def time_gpu(cfg, q, k, v, router, steps, warmup):
     return wall, {key: sum(v_) / len(v_) for key, v_ in stage.items()}
 
 
+def time_code_scoring(cfg, q, k, router, reps=5):
+    """Stage (a)'s codebook scoring alone (the matrix-core screen and its exact
+    rescoring, ssa/router.py:121-141) on the forward's routing vectors: the query
+    side (top a) and the key side (top b) as two ssa_code_topk calls, each with
+    its codebook preparation; the forward runs both screens as one launch."""
+    import torch
+
+    from ssa_amd import kernels
+
+    g = cfg["h_q"] // cfg["h_kv"]
+    qhat = kernels.route_vectors(q, router.W_qr.weight, g)
+    khat = kernels.route_vectors(k, router.W_kr.weight, 1)
+    chat = kernels.normalize_rows(router.codebook.float())
+    kernels.code_topk(qhat, chat, cfg["a"], router.temperature)
+    kernels.code_topk(khat, chat, cfg["b"], router.temperature)
+    ts = []
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        kernels.code_topk(qhat, chat, cfg["a"], router.temperature)
+        kernels.code_topk(khat, chat, cfg["b"], router.temperature)
+        e1.record()
+        torch.cuda.synchronize()
+        ts.append(e0.elapsed_time(e1))
+    return sorted(ts)[len(ts) // 2]
+
+
 def time_sorted_select(q, k, router, reps=5):
     """Stage (c) in reference order (keys by score, as torch.topk returns them)."""
     import torch
@@ -750,6 +777,8 @@ def main():
     # Counter-measured traffic applies only to the profiled workload shape.
     traffic, traffic_src = (measured_traffic(args.config) if args.n is None and args.num_codebook is None and args.seed == 0
                             else (None, None))
+    scoring_gflop = (alg["a_flops"] - alg["a_flops_projection"]) / 1e9
+    scoring_ms = None if is_block else time_code_scoring(cfg, q, k, router)
     stages = {
         "a": {"ms": st["a"], "gflop": alg["a_flops"] / 1e9,
               "gflop_fp32_projection": alg["a_flops_projection"] / 1e9,
@@ -773,6 +802,12 @@ def main():
               "gbs_logical_gather": alg["d_bytes_logical"] / t["d"] / 1e9,
               "tflops": alg["d_flops"] / t["d"] / 1e12},
     }
+    if scoring_ms is not None:
+        stages["a"]["scoring"] = {
+            "ms": scoring_ms, "gflop": scoring_gflop,
+            "frac_mfma_bf16": scoring_gflop / scoring_ms / 1e9 / MFMA_BF16_PEAK_TFLOPS,
+            "calls": "ssa_code_topk for the query codes (top a) and the key codes (top b): codebook "
+                     "preparation, bf16 matrix-core screen, exact fp32 rescoring"}
     spread_ms = time_spread_attention(q, k, v, inter[4])
     if spread_ms is not None:
         stages["d"]["spread_keys"] = {
