@@ -805,7 +805,7 @@ def main():
     if scoring_ms is not None:
         stages["a"]["scoring"] = {
             "ms": scoring_ms, "gflop": scoring_gflop,
-            "frac_mfma_bf16": scoring_gflop / scoring_ms / 1e9 / MFMA_BF16_PEAK_TFLOPS,
+            "tflops": scoring_gflop / scoring_ms, "frac_mfma_bf16": scoring_gflop / scoring_ms / MFMA_BF16_PEAK_TFLOPS,
             "calls": "ssa_code_topk for the query codes (top a) and the key codes (top b): codebook "
                      "preparation, bf16 matrix-core screen, exact fp32 rescoring"}
     spread_ms = time_spread_attention(q, k, v, inter[4])
