@@ -139,9 +139,10 @@ int ssa_build_index(const int32_t* k_codes, int64_t batch, int64_t n, int h_kv, 
                     void* stream);
 
 /* Processing order for ssa_sparse_attention's row_order: the query positions of
- * each (batch, kv head) sorted by their best code q_codes[b][h][i][0] (stable,
- * so ascending positions within a code).  Rows of one code share most of their
- * candidates, so processing them together keeps the gathered K/V rows in cache.
+ * each (batch, kv head) sorted by their smallest code min_t q_codes[b][h][i][t]
+ * (stable, so ascending positions within a code).  Rows that share that code
+ * share its bucket and much of their candidates, so processing them together
+ * keeps the gathered K/V rows in cache.
  * No reference counterpart (the reference has no processing order; results do
  * not depend on it).  q_codes must lie in [0, n_c), as ssa_route_codes writes.
  *   q_codes int32 [batch][h_kv][n][a]; order int32 [batch][h_kv][n] */

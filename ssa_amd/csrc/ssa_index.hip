@@ -30,8 +30,8 @@ int64_t tile_keys_for(int64_t n) {
 }
 
 // Entry e = j*b + r of a head is code r of key j, stored at j*cstride + r
-// (cstride = b for k_codes; the query order reads q_codes[...][0] with b = 1,
-// cstride = a).  Entries of a head number below 2^31 (run_index checks), so the
+// (cstride = b for k_codes; the query order reads each row's smallest code
+// with b = 1, cstride = 1).  Entries of a head number below 2^31 (run_index checks), so the
 // division is 32-bit: no branches between a load's address and its use.
 __device__ __forceinline__ uint32_t key_of(int64_t e, int b) {
   return static_cast<uint32_t>(e) / static_cast<uint32_t>(b);
@@ -281,10 +281,36 @@ extern "C" int ssa_build_index(const int32_t* k_codes, int64_t batch, int64_t n,
   return run_index(k_codes, bh, n, b, b, n_c, offsets, postings, static_cast<int32_t*>(workspace), st);
 }
 
+namespace ssa {
+namespace {
+
+// Smallest code of each query row: min over q_codes[row][0 .. a).  Rows that
+// share their smallest code share that bucket, and with it much of their
+// candidate set; grouping by it measured 2.77 ms for c3's stage (d) against
+// 2.85-2.94 ms grouped by the best code q_codes[row][0].
+__global__ void row_min_code_kernel(const int32_t* __restrict__ q_codes, int64_t rows, int a,
+                                    int32_t* __restrict__ mins) {
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (row >= rows) return;
+  const int32_t* c = q_codes + row * a;
+  int32_t m = c[0];
+  for (int t = 1; t < a; ++t) m = min(m, c[t]);
+  mins[row] = m;
+}
+
+size_t query_order_hist_offsets_bytes(int64_t bh, int64_t n, int n_c) {
+  return hist_bytes(bh, n, n_c) + align_up(sizeof(int32_t) * static_cast<size_t>(bh) * (n_c + 1), 256);
+}
+
+}  // namespace
+}  // namespace ssa
+
+using namespace ssa;
+
 extern "C" size_t ssa_query_order_workspace_bytes(int64_t batch, int64_t n, int h_kv, int n_c) {
   if (batch < 0 || n < 0 || h_kv <= 0 || n_c <= 0) return 0;
-  return hist_bytes(batch * h_kv, n, n_c) +
-         align_up(sizeof(int32_t) * static_cast<size_t>(batch * h_kv) * (n_c + 1), 256);
+  return query_order_hist_offsets_bytes(batch * h_kv, n, n_c) +
+         align_up(sizeof(int32_t) * static_cast<size_t>(batch * h_kv * n), 256);
 }
 
 extern "C" int ssa_query_order(const int32_t* q_codes, int64_t batch, int64_t n, int h_kv, int a,
@@ -303,5 +329,11 @@ extern "C" int ssa_query_order(const int32_t* q_codes, int64_t batch, int64_t n,
   const int64_t bh = batch * h_kv;
   int32_t* hist = static_cast<int32_t*>(workspace);
   int32_t* offsets = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + hist_bytes(bh, n, n_c));
-  return run_index(q_codes, bh, n, 1, a, n_c, offsets, order, hist, as_stream(stream));
+  int32_t* mins = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) +
+                                             query_order_hist_offsets_bytes(bh, n, n_c));
+  hipStream_t st = as_stream(stream);
+  const int64_t rows = bh * n;
+  row_min_code_kernel<<<dim3(static_cast<unsigned>(ceil_div(rows, 256))), 256, 0, st>>>(q_codes, rows, a, mins);
+  if (int s = check_launch("row_min_code_kernel")) return s;
+  return run_index(mins, bh, n, 1, 1, n_c, offsets, order, hist, st);
 }

@@ -149,8 +149,9 @@ def build_index(k_codes: torch.Tensor, n_c: int) -> Tuple[torch.Tensor, torch.Te
 
 
 def query_order(q_codes: torch.Tensor, n_c: int) -> torch.Tensor:
-    """Query positions per (batch, kv head) sorted stably by their best code
-    ``q_codes[..., 0]``: int32 [B, h, n], a processing order for sparse_attention."""
+    """Query positions per (batch, kv head) sorted stably by their smallest code
+    ``q_codes.min(-1)``: int32 [B, h, n], a processing order for sparse_attention
+    (rows sharing that code share its bucket's keys)."""
     _lib.require_device(q_codes)
     q_codes = q_codes.contiguous()
     B, h, n, a = q_codes.shape

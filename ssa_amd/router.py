@@ -124,7 +124,7 @@ class CodebookRouter(nn.Module):
         """Run stages (a)-(c) and keep the intermediates (a RouteResult).
 
         ``with_order`` also returns ``order`` (int32 [B, h_kv, n]): per head, the
-        query positions grouped by their best code (ascending within a code).
+        query positions grouped by their smallest code (ascending within a code).
         Selection already runs its rows in this order, and attention can too:
         rows that share buckets and candidate keys then run together.  It
         changes no result.  ``with_prefix`` also returns ``prefix`` (int32
@@ -182,8 +182,8 @@ class CodebookRouter(nn.Module):
 
 
 def query_order(q_codes: torch.Tensor, num_codebook: int) -> torch.Tensor:
-    """Query positions per (batch, kv head) grouped by their best code: the
-    inverted index of each query's first code, int32 [B, h_kv, n]."""
+    """Query positions per (batch, kv head) grouped by their smallest code: the
+    inverted index of each query's smallest code, int32 [B, h_kv, n]."""
     return kernels.query_order(q_codes, num_codebook)
 
 

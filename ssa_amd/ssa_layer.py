@@ -164,7 +164,7 @@ class SSAAttention(nn.Module):
             # router lists them by index and skips rescoring rows whose
             # candidates all fit in top_k; inside the layer the indices stay
             # int32 (half the bytes of the public int64 output), and the rows
-            # of each head are attended grouped by best code, so rows sharing
+            # of each head are attended grouped by smallest code, so rows sharing
             # candidate keys run together (no result depends on that order).
             res = self.router.route(q, k, causal_mask=True, hard=True, sorted=False,
                                     index_dtype=torch.int32, with_order=True, with_prefix=True)

@@ -158,7 +158,7 @@ def test_screen_int64_output(dev, orc):
 
 @pytest.mark.parametrize("sorted_,ws", [(False, True), (False, False), (True, True)])
 def test_select_row_order(dev, orc, sorted_, ws):
-    """Rows processed in query order (grouped by best code) or reversed: the same
+    """Rows processed in query order (grouped by smallest code) or reversed: the same
     indices and stats.  An order entry outside [0, n) skips its slot, so the one
     query it displaced is not written and every other row is unchanged."""
     _say(f"select row order sorted={sorted_} ws={ws}")

@@ -125,8 +125,9 @@ def test_build_index_bit_exact(dev, orc, n, h_kv, b, n_c):
 
 
 @pytest.mark.parametrize("n,h_kv,a,n_c", [(5000, 2, 16, 256), (70000, 1, 3, 4096), (1, 2, 1, 8)])
-def test_query_order_is_stable_sort_by_best_code(dev, n, h_kv, a, n_c):
-    """The processing order equals numpy's stable argsort of q_codes[..., 0]."""
+def test_query_order_is_stable_sort_by_smallest_code(dev, n, h_kv, a, n_c):
+    """The processing order equals numpy's stable argsort of each row's
+    smallest code."""
     from ssa_amd import kernels
 
     _say(f"query_order n={n} h_kv={h_kv} a={a} n_c={n_c}")
@@ -134,7 +135,7 @@ def test_query_order_is_stable_sort_by_best_code(dev, n, h_kv, a, n_c):
     B = 2
     qc = (torch.rand(B, h_kv, n, a, generator=g) ** 3 * n_c).to(torch.int32)  # skewed buckets
     got = kernels.query_order(qc.to(dev), n_c).cpu().numpy()
-    want = np.argsort(qc[..., 0].numpy(), axis=-1, kind="stable").astype(np.int32)
+    want = np.argsort(qc.numpy().min(-1), axis=-1, kind="stable").astype(np.int32)
     np.testing.assert_array_equal(got, want)
 
 
