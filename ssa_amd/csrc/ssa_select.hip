@@ -78,6 +78,9 @@ struct SelParams {
   int64_t tail_bh;
   int32_t tail_key0;
   int nseg;
+  // Light pass: bitmap words per chunk of a long window (set by the launcher:
+  // kFlatWords, or the whole key range as one chunk).
+  int light_chunk_words;
 };
 
 // Row ((b * h_kv + h) * n_q + r) processed in slot t of the launch
@@ -728,21 +731,25 @@ __global__ __launch_bounds__(kSelThreads) void select_heavy_kernel(SelParams p, 
 
 // Index-order rows, one wave per row, no block barriers: the row's buckets go
 // through the wave's LDS bitmap; a row with at most k_eff candidates writes its
-// candidates ascending and the filler directly.  A row whose causal window
-// spans more than kFlatWords bitmap words also keeps a summary level (bit x:
-// bitmap word x was touched by this row): only the summary is cleared, a word is
-// zeroed by the lane whose summary atomicOr set its bit (a wave's LDS
-// operations run in program order, so that store lands before any lane's
-// atomicOr on the word), and the candidates are read back from the touched
-// words only, so a row costs n / 1024 summary words plus its touched words
-// rather than n / 32 words.  Shorter windows clear and scan the flat bitmap,
-// which costs less than the summary's extra atomic per posting.  A row with
-// more than k_eff candidates writes its list into the workspace for
-// select_screen_kernel when it fits (w.cap), and is listed for the exact pass
-// otherwise.  One wave per block, so no row waits for a longer one before its
-// LDS is released.
+// candidates ascending and the filler directly.  A causal window of up to
+// kFlatWords bitmap words (32768 keys) uses a flat bitmap, cleared and read back
+// whole.  A longer window goes in chunks of 32768 keys through one chunk-sized
+// bitmap with a summary level (bit x: bitmap word x was touched by this row):
+// only the summary is cleared, a word is zeroed by the lane whose summary
+// atomicOr set its bit (a wave's LDS operations run in program order, so that
+// store lands before any lane's atomicOr on the word), and the candidates are
+// read back from the touched words only.  Each bucket keeps a cursor, so its
+// ascending postings are marked once over the chunks; chunk 0's first words
+// are kept for the filler.  The LDS per wave is thus bounded (5.3 KB) for any
+// n: a bitmap of the whole window (16 KB at n = 131072) let only 9 waves of
+// this pass share a CU there.  A row with more than k_eff candidates writes
+// its list into the workspace for select_screen_kernel when it fits (w.cap;
+// a chunked row marks its window a second time for that), and is listed for
+// the exact pass otherwise.  One wave per block, so no row waits for a longer
+// one before its LDS is released.
 constexpr int kFlatWords = 1024;  // windows of up to 32768 keys use the flat bitmap
 constexpr int kLightBatch = 4;    // buckets whose postings load together
+constexpr int kFillWords = 2 * 4096 / 32 + 8;     // filler words kept from chunk 0 (top_k <= 4096)
 
 __device__ __forceinline__ int wave_excl_scan(int v, int lane, int* total) {
   int x = v;
@@ -755,13 +762,31 @@ __device__ __forceinline__ int wave_excl_scan(int v, int lane, int* total) {
   return x - v;
 }
 
-// LDS words per wave: the summary (one bit per bitmap word, padded to 4 words)
-// and the bitmap (one bit per key).
-__host__ __device__ inline int light_summary_words(int64_t n) {
-  return static_cast<int>(((n + 1023) / 1024 + 3) & ~int64_t(3));
+// Summary words of a chunk of `cwords` bitmap words (one bit per word, padded
+// to 4 words).
+__host__ __device__ inline int light_chunk_summary(int cwords) { return ((cwords + 31) / 32 + 3) & ~3; }
+// LDS words per wave: the flat bitmap of a window up to kFlatWords words, and
+// for longer windows one chunk's summary and bitmap plus the filler words.
+__host__ __device__ inline int light_words(int64_t n, int cwords) {
+  const int64_t words = (n + 31) / 32;
+  if (words <= kFlatWords) return static_cast<int>(words);
+  // one chunk over all keys keeps its bitmap for the filler: no copy
+  return light_chunk_summary(cwords) + cwords + (cwords < words ? kFillWords : 0);
 }
-__host__ __device__ inline int light_words(int64_t n) {
-  return light_summary_words(n) + static_cast<int>((n + 31) / 32);
+// Chunk size of the light pass for n keys: kFlatWords when a row's postings are
+// few (estimated nseg * post_bh / n_c <= kLightChunkPostings), so that the
+// small chunk bitmap keeps many waves per CU (n = 131072, 16 codes of 32
+// postings: light pass 5.9 -> 5.1 ms); the whole key range as one chunk when
+// they are many (c5: 32 codes of 64 postings), where the rows are long enough
+// to hide their latency at low occupancy and chunking would mark the windows
+// of the rows with more than k candidates twice.
+constexpr double kLightChunkPostings = 1024.0;
+inline int light_chunk_words(const SelParams& p) {
+  const int64_t words = (p.n + 31) / 32;
+  if (words <= kFlatWords) return kFlatWords;
+  const double ppr = static_cast<double>(p.nseg) * static_cast<double>(p.post_bh + p.tail_bh) /
+                     static_cast<double>(p.n_c);
+  return ppr <= kLightChunkPostings ? kFlatWords : static_cast<int>(words);
 }
 
 // Writes the row's candidates (the set bits of the touched bitmap words) in
@@ -810,8 +835,6 @@ __global__ __launch_bounds__(64) void select_light_kernel(SelParams p, int64_t r
   if (slot >= rows) return;
   const int64_t row = row_of_slot(p, slot);
   if (row < 0) return;
-  uint32_t* sm = lbits;                             // summary
-  uint32_t* bm = lbits + light_summary_words(p.n);  // bitmap
   const int words = static_cast<int>((p.n + 31) >> 5);
   const int64_t r = row % p.n_q;
   const int64_t i = p.q_pos0 + r;
@@ -823,13 +846,16 @@ __global__ __launch_bounds__(64) void select_light_kernel(SelParams p, int64_t r
   const bool causal = p.mask_mode == SSA_MASK_CAUSAL;
   const uint8_t* mrow = (p.mask_mode == SSA_MASK_DENSE) ? p.mask + bb * p.mask_sb + i * p.mask_si : nullptr;
   const int live = causal ? static_cast<int>(i >> 5) + 1 : words;
-  const int slive = (live + 31) >> 5;
   const bool flat = live <= kFlatWords;
-  if (flat) {
-    for (int x = lane; x < live; x += 64) bm[x] = 0u;
-  } else {
-    for (int x = lane; x < slive; x += 64) sm[x] = 0u;
-  }
+  // flat: the bitmap of the window; chunked: one chunk's summary and bitmap,
+  // then the filler words (a copy of chunk 0's first fwn words)
+  const int cwords = p.light_chunk_words;                  // bitmap words per chunk
+  const int csum = light_chunk_summary(cwords);
+  uint32_t* sm = lbits;
+  uint32_t* bm = flat ? lbits : lbits + csum;
+  uint32_t* fw = lbits + csum + cwords;
+  const int fwn = min(words, (2 * p.k_eff + 31) / 32 + 1);
+  const int64_t wend = static_cast<int64_t>(live) * 32;  // keys of the window's words
 
   int32_t lo = 0, len = 0;
   if (lane < p.nseg) {
@@ -842,24 +868,7 @@ __global__ __launch_bounds__(64) void select_light_kernel(SelParams p, int64_t r
       len = min(max(off[c + 1], lo), total) - lo;
     }
   }
-  __builtin_amdgcn_wave_barrier();
   int fresh = 0, seen = 0;  // per lane: new keys, postings inside the window
-  auto add = [&](int32_t j) {
-    const bool in_window = !causal || j <= i;
-    seen += in_window ? 1 : 0;
-    if (static_cast<uint32_t>(j) < static_cast<uint32_t>(p.n) && in_window &&
-        (mrow == nullptr || mrow[j] != 0)) {
-      const int x = j >> 5;
-      if (!flat) {
-        const uint32_t sb = 1u << (x & 31);
-        if (!(atomicOr(&sm[x >> 5], sb) & sb)) bm[x] = 0u;
-      }
-      const uint32_t bit = 1u << (j & 31);
-      if (!(atomicOr(&bm[x], bit) & bit)) ++fresh;
-    }
-  };
-  // Buckets kLightBatch at a time: their postings are loaded together, then
-  // marked (the bitmap, the counts and the summary do not depend on the order).
   // Buffer descriptors of this (batch, kv head)'s postings (the host keeps
   // them below 2^31 entries); no tail index: an empty range.
   const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
@@ -867,28 +876,156 @@ __global__ __launch_bounds__(64) void select_light_kernel(SelParams p, int64_t r
   const __amdgpu_buffer_rsrc_t trs = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<int32_t*>(tp ? tp : pp), 0, tp ? static_cast<int>(min(p.tail_bh * 4, int64_t(0x7FFFFFFF))) : 0,
       kBufferWord3);
-  for (int m0 = 0; m0 < p.nseg; m0 += kLightBatch) {
-    int lo_u[kLightBatch], len_u[kLightBatch], most = 0;
+
+  const int64_t obase = ((bb * p.n_q + r) * p.h_kv + h) * p.top_k;
+  int32_t* o32 = static_cast<int32_t*>(p.out) + obase;
+  int64_t* o64 = static_cast<int64_t*>(p.out) + obase;
+  auto put = [&](int pos, int32_t v) {
+    if (p.out_i64) o64[pos] = v;
+    else o32[pos] = v;
+  };
+
+  // Marks the row's window keys in [kbeg, kend) (bits relative to kbeg) and
+  // counts (when `count`) the new keys and the postings inside the window.
+  // Buckets go kLightBatch at a time, their postings loaded together before
+  // any is marked (the bitmap, the counts and the summary do not depend on the
+  // order).  cur_lo / cur_len (lane m: bucket m) are the bucket cursors: the
+  // postings below kend are consumed and the cursors advance past them, so
+  // chunk after chunk every posting is marked once (postings ascend inside a
+  // bucket).  A flat window is one chunk [0, wend).
+  int32_t cur_lo = lo, cur_len = len;
+  auto mark_range = [&](int64_t kbeg, int64_t kend, bool summary, bool count, bool cursors)
+                        __attribute__((always_inline)) {
+    auto add = [&](int32_t j) __attribute__((always_inline)) {
+      const bool in_window = !causal || j <= i;
+      if (count) seen += in_window ? 1 : 0;
+      if (static_cast<uint32_t>(j) < static_cast<uint32_t>(p.n) && in_window &&
+          (mrow == nullptr || mrow[j] != 0)) {
+        const int jr = static_cast<int>(j - kbeg);
+        const int x = jr >> 5;
+        if (summary) {
+          const uint32_t sb = 1u << (x & 31);
+          if (!(atomicOr(&sm[x >> 5], sb) & sb)) bm[x] = 0u;
+        }
+        const uint32_t bit = 1u << (jr & 31);
+        if (!(atomicOr(&bm[x], bit) & bit) && count) ++fresh;
+      }
+    };
+    if (!cursors) {
+      // the whole window in one chunk: every posting of every bucket
+      for (int m0 = 0; m0 < p.nseg; m0 += kLightBatch) {
+        int lo_u[kLightBatch], len_u[kLightBatch], most = 0;
 #pragma unroll
-    for (int u = 0; u < kLightBatch; ++u) {
-      lo_u[u] = __shfl(lo, min(m0 + u, 63));
-      len_u[u] = (m0 + u < p.nseg) ? __shfl(len, min(m0 + u, 63)) : 0;
-      most = max(most, len_u[u]);
+        for (int u = 0; u < kLightBatch; ++u) {
+          lo_u[u] = __shfl(lo, min(m0 + u, 63));
+          len_u[u] = (m0 + u < p.nseg) ? __shfl(len, min(m0 + u, 63)) : 0;
+          most = max(most, len_u[u]);
+        }
+        for (int base = 0; base < most; base += 64) {
+          // Every lane loads, with no branch (past a bucket's end it reloads
+          // the bucket's last posting; an empty bucket reads out of the
+          // buffer's range, which loads 0), so all kLightBatch loads are out
+          // before the first add.
+          int32_t j_u[kLightBatch];
+#pragma unroll
+          for (int u = 0; u < kLightBatch; ++u) {
+            const int e = lo_u[u] + min(base + lane, len_u[u] - 1);
+            j_u[u] = __builtin_amdgcn_raw_buffer_load_b32(m0 + u < p.a ? prs : trs, e * 4, 0, 0);
+          }
+#pragma unroll
+          for (int u = 0; u < kLightBatch; ++u)
+            if (base + lane < len_u[u]) add(m0 + u < p.a ? j_u[u] : j_u[u] + p.tail_key0);
+        }
+      }
+      return;
     }
-    for (int base = 0; base < most; base += 64) {
-      // Every lane loads, with no branch (past a bucket's end it reloads the
-      // bucket's last posting; an empty bucket reads out of the buffer's range,
-      // which loads 0), so all kLightBatch loads are out before the first add.
-      int32_t j_u[kLightBatch];
+    for (int m0 = 0; m0 < p.nseg; m0 += kLightBatch) {
+      int lo_u[kLightBatch], len_u[kLightBatch], took[kLightBatch];
 #pragma unroll
       for (int u = 0; u < kLightBatch; ++u) {
-        const int e = lo_u[u] + min(base + lane, len_u[u] - 1);
-        j_u[u] = __builtin_amdgcn_raw_buffer_load_b32(m0 + u < p.a ? prs : trs, e * 4, 0, 0);
+        lo_u[u] = __shfl(cur_lo, min(m0 + u, 63));
+        len_u[u] = (m0 + u < p.nseg) ? __shfl(cur_len, min(m0 + u, 63)) : 0;
+        took[u] = 0;
+      }
+      for (int base = 0;; base += 64) {
+        // Every lane loads, with no branch (past a bucket's end it reloads the
+        // bucket's last posting; an empty bucket reads out of the buffer's
+        // range, which loads 0), so all kLightBatch loads are out before the
+        // first add.
+        int32_t j_u[kLightBatch];
+#pragma unroll
+        for (int u = 0; u < kLightBatch; ++u) {
+          const int e = lo_u[u] + min(base + lane, len_u[u] - 1);
+          j_u[u] = __builtin_amdgcn_raw_buffer_load_b32(m0 + u < p.a ? prs : trs, e * 4, 0, 0);
+        }
+        bool more = false;
+#pragma unroll
+        for (int u = 0; u < kLightBatch; ++u) {
+          const int32_t j = m0 + u < p.a ? j_u[u] : j_u[u] + p.tail_key0;
+          const bool in_range = base + lane < len_u[u] && j < kend;
+          const uint64_t bal = __ballot(in_range);
+          took[u] += __popcll(bal);
+          more = more || bal == ~0ull;
+          if (in_range) add(j);
+        }
+        if (!more) break;
       }
 #pragma unroll
       for (int u = 0; u < kLightBatch; ++u)
-        if (base + lane < len_u[u]) add(m0 + u < p.a ? j_u[u] : j_u[u] + p.tail_key0);
+        if (lane == m0 + u) {
+          cur_lo += took[u];
+          cur_len -= took[u];
+        }
     }
+  };
+
+  // Window of more than kFlatWords words: cwords words (32768 keys, or all
+  // keys as one chunk) at a time, each chunk with a summary level (bit x:
+  // bitmap word x was touched by this row): only the summary is cleared, a
+  // word is zeroed by the lane whose summary atomicOr set its bit (a wave's LDS
+  // operations run in program order, so that store lands before any lane's
+  // atomicOr on the word), and the chunk's candidates are read back from the
+  // touched words only.  `sink(pos, key)` receives them ascending; returns
+  // their number.  Chunk 0's first fwn words are kept for the filler.
+  const int64_t ckeys = static_cast<int64_t>(cwords) * 32;
+  const bool one_chunk = wend <= ckeys;
+  int last_cs = 0;  // summary words of the last chunk marked
+  auto run_chunks = [&](bool count, auto&& sink) __attribute__((always_inline)) -> int {
+    cur_lo = lo;
+    cur_len = len;
+    int emitted = 0;
+    for (int64_t kbeg = 0; kbeg < wend; kbeg += ckeys) {
+      const int64_t kend = min(kbeg + ckeys, wend);
+      const int cw = static_cast<int>((kend - kbeg + 31) >> 5);
+      const int cs = (cw + 31) >> 5;
+      last_cs = cs;
+      for (int x = lane; x < cs; x += 64) sm[x] = 0u;
+      __builtin_amdgcn_wave_barrier();
+      mark_range(kbeg, kend, true, count, !one_chunk);
+      if (!(count && one_chunk)) {  // one chunk: emitted once C is known
+        const int base = emitted;
+        emitted += light_emit(sm, bm, cs, lane, [&](int pos, int key) {
+          sink(base + pos, static_cast<int32_t>(kbeg + key));
+        });
+      }
+      if (kbeg == 0 && count && !one_chunk)
+        for (int x = lane; x < fwn; x += 64) fw[x] = ((sm[x >> 5] >> (x & 31)) & 1u) ? bm[x] : 0u;
+    }
+    return emitted;
+  };
+
+  int filled = 0;
+  if (flat) {
+    for (int x = lane; x < live; x += 64) bm[x] = 0u;
+    __builtin_amdgcn_wave_barrier();
+    mark_range(0, wend, false, true, false);
+  } else {
+    // candidates to the output as they come (a row that turns out to have more
+    // than k_eff writes at most top_k of them there; its final row is written
+    // by the screen and pick passes or the exact pass, which run later)
+    filled = run_chunks(true, [&](int pos, int32_t key) {
+      if (pos < p.top_k) put(pos, key);
+    });
   }
   int C = 0, raw = 0;
   wave_excl_scan(fresh, lane, &C);
@@ -921,9 +1058,12 @@ __global__ __launch_bounds__(64) void select_light_kernel(SelParams p, int64_t r
       return;
     }
     int32_t* dst = w.cand + off;
-    auto to_list = [&](int pos, int32_t v) { dst[pos] = v; };
+    auto to_list = [&](int pos, int32_t v) {
+      if (pos < C) dst[pos] = v;
+    };
     if (flat) light_emit_flat(bm, live, lane, to_list);
-    else light_emit(sm, bm, slive, lane, to_list);
+    else if (one_chunk) light_emit(sm, bm, last_cs, lane, to_list);  // the window's bitmap is still there
+    else run_chunks(false, to_list);  // the same marks again, now into the list
     if (lane == 0) {
       const int slot = atomicAdd(&sc[0], 1);
       if (slot >= 0 && slot < w.shard_rows) {
@@ -938,15 +1078,18 @@ __global__ __launch_bounds__(64) void select_light_kernel(SelParams p, int64_t r
     return;
   }
 
-  const int64_t obase = ((bb * p.n_q + r) * p.h_kv + h) * p.top_k;
-  int32_t* o32 = static_cast<int32_t*>(p.out) + obase;
-  int64_t* o64 = static_cast<int64_t*>(p.out) + obase;
-  auto put = [&](int pos, int32_t v) {
-    if (p.out_i64) o64[pos] = v;
-    else o32[pos] = v;
+  // Candidates ascending (already written by a window of several chunks), then
+  // the lowest non-candidates up to k_eff.
+  if (flat) filled = light_emit_flat(bm, live, lane, put);
+  else if (one_chunk) filled = light_emit(sm, bm, last_cs, lane, put);
+  // Keys of word x the row holds: the flat bitmap, the one chunk's touched
+  // words, or chunk 0's copy (the filler lies in the keys below k_eff + C <=
+  // 2 k_eff, inside the copy).
+  auto held = [&](int x) -> uint32_t {
+    if (flat) return x < live ? bm[x] : 0u;
+    if (one_chunk) return (x < live && ((sm[x >> 5] >> (x & 31)) & 1u)) ? bm[x] : 0u;
+    return x < fwn ? fw[x] : 0u;
   };
-  // Candidates ascending, then the lowest non-candidates up to k_eff.
-  int filled = flat ? light_emit_flat(bm, live, lane, put) : light_emit(sm, bm, slive, lane, put);
   // The filler is the k_eff - C lowest keys the row does not hold, so every key
   // up to the last one is in the row, once: X = last filler key + 1 (0 without
   // filler, and 0 when index-0 padding repeats a key).
@@ -962,8 +1105,7 @@ __global__ __launch_bounds__(64) void select_light_kernel(SelParams p, int64_t r
     const int x = w0 + (lane >> 5);
     uint32_t nb = 0u;  // keys of word x the row does not hold (and that exist)
     if (x < words) {
-      const bool set = x < live && (flat || ((sm[x >> 5] >> (x & 31)) & 1u));
-      nb = ~(set ? bm[x] : 0u);
+      nb = ~held(x);
       if (x == words - 1 && (p.n & 31)) nb &= (1u << (p.n & 31)) - 1u;
     }
     const bool mine = (nb >> (lane & 31)) & 1u;
@@ -1439,7 +1581,9 @@ __global__ void zero_ctr_kernel(int32_t* __restrict__ ctr) {
   for (int x = threadIdx.x; x < static_cast<int>(kSelCtrBytes / 4); x += blockDim.x) ctr[x] = 0;
 }
 
-size_t light_smem(int64_t n) { return sizeof(uint32_t) * static_cast<size_t>(light_words(n)); }
+size_t light_smem(const SelParams& p) {
+  return sizeof(uint32_t) * static_cast<size_t>(light_words(p.n, light_chunk_words(p)));
+}
 
 // Rows of the light-pass blocks of one shard (block b -> shard b % kShards).
 int64_t shard_rows_for(int64_t rows) { return ceil_div(rows, kShards); }
@@ -1521,7 +1665,7 @@ int launch_select(const SelParams& p, int64_t rows, size_t smem, void* ws, size_
   // 32-bit buffer offsets of the screen's K gathers
   const bool screen = kScreenable && p.n < (int64_t(1) << 24) && 2 * p.k_sn < (int64_t(1) << 24) &&
                       (p.n - 1) * p.k_sn * 2 + 2 * p.d < (int64_t(1) << 31);
-  if (ws == nullptr || (p.sorted && p.k_eff > kSortMax) || light_smem(p.n) > 64 * 1024) {
+  if (ws == nullptr || (p.sorted && p.k_eff > kSortMax) || light_smem(p) > 64 * 1024) {
     kern<<<dim3(static_cast<unsigned>(rows)), kSelThreads, smem, st>>>(p, qg);
     return check_launch("select_kernel");
   }
@@ -1533,7 +1677,8 @@ int launch_select(const SelParams& p, int64_t rows, size_t smem, void* ws, size_
   pi.cnt = sort_after ? w.cnt : nullptr;
   zero_ctr_kernel<<<1, 256, 0, st>>>(w.ctr);
   if (int s = check_launch("zero_ctr_kernel")) return s;
-  select_light_kernel<<<dim3(static_cast<unsigned>(rows)), 64, light_smem(p.n), st>>>(pi, rows, w);
+  pi.light_chunk_words = light_chunk_words(p);
+  select_light_kernel<<<dim3(static_cast<unsigned>(rows)), 64, light_smem(p), st>>>(pi, rows, w);
   if (int s = check_launch("select_light_kernel")) return s;
   if constexpr (kScreenable) {
     if (w.cap > 0) {
