@@ -51,6 +51,22 @@ __device__ __forceinline__ uint32_t key_index(uint64_t key) {
   return 0xFFFFFFFFu - static_cast<uint32_t>(key & 0xFFFFFFFFull);
 }
 
+// Inclusive prefix sum over the 64 lanes of a wave (all lanes active), in six
+// DPP adds: row_shr 1, 2, 4 (banks 1-3), 8 (banks 2-3) scan each 16-lane row,
+// then row_bcast 15 and 31 carry the row totals into the rows above.  A lane
+// whose DPP source does not exist adds the `old` operand, 0.  (A shuffle
+// ladder costs an LDS round trip and its address arithmetic per step.)
+__device__ __forceinline__ int wave_incl_scan(int x) {
+  int v = x;
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xE, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xC, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);
+  return v;
+}
+
 // fp32 fused multiply-add, single rounding (v_fma_f32).
 __device__ __forceinline__ float fma_rn(float a, float b, float c) { return __builtin_fmaf(a, b, c); }
 

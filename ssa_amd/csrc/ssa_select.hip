@@ -752,13 +752,9 @@ constexpr int kLightBatch = 4;    // buckets whose postings load together
 constexpr int kFillWords = 2 * 4096 / 32 + 8;     // filler words kept from chunk 0 (top_k <= 4096)
 
 __device__ __forceinline__ int wave_excl_scan(int v, int lane, int* total) {
-  int x = v;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int y = __shfl_up(x, o, 64);
-    if (lane >= o) x += y;
-  }
-  *total = __shfl(x, 63);
+  (void)lane;
+  const int x = wave_incl_scan(v);
+  *total = __builtin_amdgcn_readlane(x, 63);
   return x - v;
 }
 
