@@ -106,13 +106,8 @@ __global__ __launch_bounds__(kScanThreads) void index_scan_kernel(int32_t* __res
   int32_t tot = 0;
   if (c < n_c)
     for (int64_t t = 0; t < tiles; ++t) tot += hb[t * n_c + c];
-  int32_t x = tot;
+  const int32_t x = wave_incl_scan(tot);
   const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int32_t y = __shfl_up(x, off, 64);
-    if (lane >= off) x += y;
-  }
   if (lane == 63) wsum[threadIdx.x >> 6] = x;
   __syncthreads();
   int32_t before = carry, all = 0;

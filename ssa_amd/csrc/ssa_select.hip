@@ -146,12 +146,7 @@ __device__ void bitonic_desc(uint64_t* buf, int len) {
 __device__ int block_exclusive_scan(int v, int* scratch, int* total) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  int x = v;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int y = __shfl_up(x, off, 64);
-    if (lane >= off) x += y;
-  }
+  const int x = wave_incl_scan(v);
   if (lane == 63) scratch[wave] = x;
   __syncthreads();
   int base = 0, tot = 0;
@@ -358,12 +353,7 @@ __device__ __forceinline__ void select_row(const SelParams& p, const T* __restri
         len = min(max(off[c + 1], lo), total) - lo;
       }
     }
-    int32_t x = len;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int32_t y = __shfl_up(x, o, 64);
-      if (tid >= o) x += y;
-    }
+    const int32_t x = wave_incl_scan(len);  // the first wave, all lanes active
     if (tid < p.nseg) {
       seg_lo[tid] = lo;
       seg_start[tid + 1] = x;
