@@ -880,6 +880,7 @@ __global__ __launch_bounds__(64) void select_light_kernel(SelParams p, int64_t r
   // chunk after chunk every posting is marked once (postings ascend inside a
   // bucket).  A flat window is one chunk [0, wend).
   int32_t cur_lo = lo, cur_len = len;
+  const bool half_buckets = tp == nullptr && p.post_bh <= int64_t(32) * p.n_c;
   auto mark_range = [&](int64_t kbeg, int64_t kend, bool summary, bool count, bool cursors)
                         __attribute__((always_inline)) {
     auto add = [&](int32_t j) __attribute__((always_inline)) {
@@ -898,7 +899,35 @@ __global__ __launch_bounds__(64) void select_light_kernel(SelParams p, int64_t r
       }
     };
     if (!cursors) {
-      // the whole window in one chunk: every posting of every bucket
+      // The whole window in one chunk: every posting of every bucket.  With
+      // buckets of at most 32 postings on average and no tail index, each
+      // half-wave takes a bucket (two per load), so half the lanes are not
+      // idle on short buckets.
+      if (half_buckets) {
+        const int sub = lane >> 5, ll = lane & 31;
+        for (int m0 = 0; m0 < p.nseg; m0 += 2 * kLightBatch) {
+          int lo_u[kLightBatch], len_u[kLightBatch], most = 0;
+#pragma unroll
+          for (int u = 0; u < kLightBatch; ++u) {
+            const int b = m0 + 2 * u + sub;
+            lo_u[u] = __shfl(lo, min(b, 63));
+            len_u[u] = (b < p.nseg) ? __shfl(len, min(b, 63)) : 0;
+            most = max(most, len_u[u]);
+          }
+          for (int base = 0; __ballot(base + ll < most) != 0ull; base += 32) {
+            int32_t j_u[kLightBatch];
+#pragma unroll
+            for (int u = 0; u < kLightBatch; ++u) {
+              const int e = lo_u[u] + min(base + ll, len_u[u] - 1);
+              j_u[u] = __builtin_amdgcn_raw_buffer_load_b32(prs, e * 4, 0, 0);
+            }
+#pragma unroll
+            for (int u = 0; u < kLightBatch; ++u)
+              if (base + ll < len_u[u]) add(j_u[u]);
+          }
+        }
+        return;
+      }
       for (int m0 = 0; m0 < p.nseg; m0 += kLightBatch) {
         int lo_u[kLightBatch], len_u[kLightBatch], most = 0;
 #pragma unroll
