@@ -78,6 +78,10 @@ struct SelParams {
   int64_t tail_bh;
   int32_t tail_key0;
   int nseg;
+  // Screen and pick passes: each XCD walks its own slice of the listed rows
+  // (set by the launcher when the (batch, kv head) pairs are at least the
+  // XCDs; see shard_walk).
+  int xcd_slices;
   // Light pass: bitmap words per chunk of a long window (set by the launcher:
   // kFlatWords, or the whole key range as one chunk).
   int light_chunk_words;
@@ -701,6 +705,41 @@ __device__ __forceinline__ void push_exact(const SelWs& w, int64_t rows, int64_t
   if (x >= 0 && x < rows) w.exact[x] = static_cast<int32_t>(row);
 }
 
+// The list entries a wave of the screen or pick pass takes (shard, entries
+// first, first + step, ... below end).  The grid is a whole number of kXcds x
+// kShards / kScrWaves blocks.
+//   xcd_slices: each XCD (the launched block b runs on XCD b mod kXcds) walks
+//     the same eighth of every shard's list, and a shard's list is in
+//     light-pass order, so the rows one XCD works on lie in one slice of the
+//     row order (about one (batch, KV head)'s rows when there are at least
+//     kXcds of them) and their key rows share that XCD's L2;
+//   otherwise wave gw of the grid walks shard gw mod kShards from entry
+//     gw / kShards with a step of the grid's waves / kShards, so all XCDs work
+//     in the same part of the row order at a time.
+struct ShardWalk {
+  int shard, first, step, end;
+};
+__device__ __forceinline__ ShardWalk shard_walk(const SelWs& w, int wave, bool xcd_slices) {
+  ShardWalk sw;
+  if (xcd_slices) {
+    const int xcd = static_cast<int>(blockIdx.x % kXcds);
+    const int lw = static_cast<int>(blockIdx.x / kXcds) * kScrWaves + wave;
+    const int wx = static_cast<int>(gridDim.x / kXcds) * kScrWaves;
+    sw.shard = lw % kShards;
+    const int64_t listed = min(static_cast<int64_t>(w.ctr[16 + 4 * sw.shard]), w.shard_rows);
+    sw.first = static_cast<int>(listed * xcd / kXcds) + lw / kShards;
+    sw.step = wx / kShards;
+    sw.end = static_cast<int>(listed * (xcd + 1) / kXcds);
+  } else {
+    const int gw = static_cast<int>(blockIdx.x) * kScrWaves + wave;
+    sw.shard = gw % kShards;
+    sw.first = gw / kShards;
+    sw.step = static_cast<int>(gridDim.x) * kScrWaves / kShards;
+    sw.end = static_cast<int>(min(static_cast<int64_t>(w.ctr[16 + 4 * sw.shard]), w.shard_rows));
+  }
+  return sw;
+}
+
 // The rows listed for the exact pass: each block takes the next listed row
 // until the list is exhausted (ctr[0] rows, cursor ctr[1]).
 template <typename T, int GMAX, int D>
@@ -872,7 +911,9 @@ __global__ __launch_bounds__(64) void select_light_kernel(SelParams p, int64_t r
   };
 
   // Marks the row's window keys in [kbeg, kend) (bits relative to kbeg) and
-  // counts (when `count`) the new keys and the postings inside the window.
+  // counts (when `count`) the postings inside the window and, for a chunk with
+  // a summary, the new keys (a flat window's marks need no atomic's return:
+  // its keys are counted from the bitmap afterwards).
   // Buckets go kLightBatch at a time, their postings loaded together before
   // any is marked (the bitmap, the counts and the summary do not depend on the
   // order).  cur_lo / cur_len (lane m: bucket m) are the bucket cursors: the
@@ -895,7 +936,8 @@ __global__ __launch_bounds__(64) void select_light_kernel(SelParams p, int64_t r
           if (!(atomicOr(&sm[x >> 5], sb) & sb)) bm[x] = 0u;
         }
         const uint32_t bit = 1u << (jr & 31);
-        if (!(atomicOr(&bm[x], bit) & bit) && count) ++fresh;
+        if (!summary) atomicOr(&bm[x], bit);  // flat: no return wait; the new keys are counted after
+        else if (!(atomicOr(&bm[x], bit) & bit) && count) ++fresh;
       }
     };
     if (!cursors) {
@@ -1034,6 +1076,8 @@ __global__ __launch_bounds__(64) void select_light_kernel(SelParams p, int64_t r
     for (int x = lane; x < live; x += 64) bm[x] = 0u;
     __builtin_amdgcn_wave_barrier();
     mark_range(0, wend, false, true, false);
+    __builtin_amdgcn_wave_barrier();
+    for (int x = lane; x < live; x += 64) fresh += __popc(bm[x]);
   } else {
     // candidates to the output as they come (a row that turns out to have more
     // than k_eff writes at most top_k of them there; its final row is written
@@ -1186,9 +1230,7 @@ __device__ __forceinline__ float dpp_from_plus1(float x) {
   return __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(x), 0x101, 0xF, 0xF, false));
 }
 
-// Static assignment of listed rows to waves: wave gw of the grid serves shard
-// gw % kShards, entries r, r + per, ... with r = gw / kShards and per = (waves
-// in the grid) / kShards (the grid holds whole shards of waves).
+// Entry e of a shard's list (the waves' assignment is shard_walk's).
 struct ScrEntry {
   int64_t row, off;  // off: list position of the row's first candidate
   int C;
@@ -1221,15 +1263,13 @@ select_screen_kernel(SelParams p, SelWs w) {
   const int kswz = mf_swz<D>(c16);
   const uint32_t ksn2 = 2u * static_cast<uint32_t>(p.k_sn);
   const int kbytes = static_cast<int>((p.n - 1) * p.k_sn * 2 + 2 * D);
-  const int gw = static_cast<int>(blockIdx.x) * kScrWaves + wave;
-  const int shard = gw % kShards;
-  const int per = static_cast<int>(gridDim.x) * kScrWaves / kShards;
-  const int listed = min(w.ctr[16 + 4 * shard], static_cast<int>(w.shard_rows));
+  const ShardWalk sw = shard_walk(w, wave, p.xcd_slices != 0);
+  const int shard = sw.shard;
   const float gf = static_cast<float>(p.g);
   const float ce = (6.0f * D + 2.0f * static_cast<float>(p.g) + 100.0f) * 5.9604645e-8f * 1.02f *
                    (1.0f + 4.0f * D * 5.9604645e-8f);
   const float rsg = 1.0f / (p.score_div * gf);
-  for (int e = gw / kShards; e < listed; e += per) {
+  for (int e = sw.first; e < sw.end; e += sw.step) {
     const ScrEntry x = scr_entry(p, w, shard, e);
     if (!x.ok) continue;  // the pick pass sends the row to the exact pass
     const int C = x.C;
@@ -1367,12 +1407,10 @@ __global__ __launch_bounds__(64 * kScrWaves) void select_pick_kernel(SelParams p
   float* av = avs[wave];
   int32_t* hs = hst[wave];
   int32_t* bp = bps[wave];
-  const int gw = static_cast<int>(blockIdx.x) * kScrWaves + wave;
-  const int shard = gw % kShards;
-  const int per = static_cast<int>(gridDim.x) * kScrWaves / kShards;
-  const int listed = min(w.ctr[16 + 4 * shard], static_cast<int>(w.shard_rows));
+  const ShardWalk sw = shard_walk(w, wave, p.xcd_slices != 0);
+  const int shard = sw.shard;
   const float gf = static_cast<float>(p.g);
-  for (int e = gw / kShards; e < listed; e += per) {
+  for (int e = sw.first; e < sw.end; e += sw.step) {
     const ScrEntry x = scr_entry(p, w, shard, e);
     if (x.row < 0 || x.row >= p.rows) continue;  // cannot happen: the light pass wrote every entry
     const float emax = w.emax[static_cast<int64_t>(shard) * w.shard_rows + e];
@@ -1649,8 +1687,8 @@ int persistent_grid(int64_t work, int per_cu) {
 }
 
 // Grid of the screen (WHICH = 0) or pick (1) kernel: as many blocks as fit on
-// the device at once, rounded up to whole shards of waves (the grid's wave
-// count is a multiple of kShards).
+// the device at once, rounded up so that each XCD's share of the waves is a
+// multiple of kShards (shard_walk).
 template <int D, int GMAX, int WHICH>
 int shard_grid() {
   static int cached[64] = {0};
@@ -1662,7 +1700,7 @@ int shard_grid() {
                                  : reinterpret_cast<const void*>(select_pick_kernel<D, GMAX>);
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, f, 64 * kScrWaves, 0) != hipSuccess || per_cu <= 0)
       per_cu = 2;
-    constexpr int kBlocksPerShardSet = kShards / kScrWaves;
+    constexpr int kBlocksPerShardSet = kXcds * kShards / kScrWaves;
     cached[dev] = static_cast<int>(ceil_div(persistent_grid(int64_t(1) << 40, per_cu), kBlocksPerShardSet) *
                                    kBlocksPerShardSet);
   }
@@ -1693,6 +1731,10 @@ int launch_select(const SelParams& p, int64_t rows, size_t smem, void* ws, size_
   zero_ctr_kernel<<<1, 256, 0, st>>>(w.ctr);
   if (int s = check_launch("zero_ctr_kernel")) return s;
   pi.light_chunk_words = light_chunk_words(p);
+  // With fewer (batch, kv head) pairs than XCDs the XCDs would share heads:
+  // there the slices measured slower (c5: 2 kv heads), so they are kept for
+  // the case of at least one pair per XCD.
+  pi.xcd_slices = (p.n_q > 0 && rows / p.n_q >= kXcds) ? 1 : 0;
   select_light_kernel<<<dim3(static_cast<unsigned>(rows)), 64, light_smem(p), st>>>(pi, rows, w);
   if (int s = check_launch("select_light_kernel")) return s;
   if constexpr (kScreenable) {
