@@ -859,7 +859,11 @@ sparse_attention_mfma_kernel(AttParams p) {
   using S = MfShape<D>;
   __shared__ __align__(16) unsigned char kv_lds[kMfWaves][2][kMfChunk * S::ROW];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t blk = xcd_block(blockIdx.x, xcd_per(ceil_div(p.rows, kMfWaves)));
+  // With a row order (rows that share codebook buckets, hence keys, next to
+  // each other) XCD x takes a contiguous range of blocks, so its L2 holds the
+  // keys its rows share; without one, consecutive blocks go to different
+  // XCDs, which measured faster for index sets with no such sharing.
+  const int64_t blk = p.order ? xcd_block(blockIdx.x, xcd_per(ceil_div(p.rows, kMfWaves))) : blockIdx.x;
   const AttRow ar = att_row(p, blk * kMfWaves + wave);
   attend_row_mfma<D, BLK>(p, ar, kv_lds[wave][0], kv_lds[wave][1]);
 }
