@@ -937,22 +937,57 @@ __global__ __launch_bounds__(64 * kPfxWaves, 2) void prefix_attention_kernel(Att
     __syncthreads();
     const int top_k = p.top_k;
     const int64_t ib0 = bb * p.idx_sb + r0 * p.idx_sn + static_cast<int64_t>(h) * p.idx_sh;
-    strided_batches<8, 64 * kPfxWaves>(
-        static_cast<int64_t>(nr) * top_k, tid,
-        [&](int64_t e) -> int64_t {
-          const int64_t r = e / top_k;
-          const int64_t a = ib0 + r * p.idx_sn + (e - r * top_k);
-          return p.idx_i64 ? static_cast<const int64_t*>(p.idx)[a]
-                           : static_cast<int64_t>(static_cast<const int32_t*>(p.idx)[a]);
-        },
-        [&](int64_t e, int64_t j) {
-          if (j >= 0 && j < xb) {
-            const int r = static_cast<int>(e / top_k);
-            const uint32_t bit = 1u << (j & 31);
-            const uint32_t old = atomicOr(&bits[r][j >> 5], bit);
-            if (old & bit) atomicMin(&s_dup[r], static_cast<int>(j));
-          }
-        });
+    auto mark = [&](int r, int64_t j) {
+      if (j >= 0 && j < xb) {
+        const uint32_t bit = 1u << (j & 31);
+        const uint32_t old = atomicOr(&bits[r][j >> 5], bit);
+        if (old & bit) atomicMin(&s_dup[r], static_cast<int>(j));
+      }
+    };
+    const int32_t* i32 = static_cast<const int32_t*>(p.idx);
+    if (!p.idx_i64 && (top_k & 3) == 0 && (p.idx_sn & 3) == 0 &&
+        (reinterpret_cast<uintptr_t>(i32 + ib0) & 15) == 0) {
+      // int32 rows in 16-byte pieces: four times the bytes per load in flight
+      const int q = top_k >> 2;
+      strided_batches<8, 64 * kPfxWaves>(
+          static_cast<int64_t>(nr) * q, tid,
+          [&](int64_t e) -> int4 {
+            const int64_t r = e / q;
+            return *reinterpret_cast<const int4*>(i32 + ib0 + r * p.idx_sn + 4 * (e - r * q));
+          },
+          [&](int64_t e, int4 v) {
+            const int r = static_cast<int>(e / q);
+            mark(r, v.x);
+            mark(r, v.y);
+            mark(r, v.z);
+            mark(r, v.w);
+          });
+    } else if (p.idx_i64 && (top_k & 1) == 0 && (p.idx_sn & 1) == 0 &&
+               (reinterpret_cast<uintptr_t>(static_cast<const int64_t*>(p.idx) + ib0) & 15) == 0) {
+      // int64 rows in 16-byte pieces
+      const int64_t* i64 = static_cast<const int64_t*>(p.idx);
+      const int q = top_k >> 1;
+      strided_batches<8, 64 * kPfxWaves>(
+          static_cast<int64_t>(nr) * q, tid,
+          [&](int64_t e) -> longlong2 {
+            const int64_t r = e / q;
+            return *reinterpret_cast<const longlong2*>(i64 + ib0 + r * p.idx_sn + 2 * (e - r * q));
+          },
+          [&](int64_t e, longlong2 v) {
+            const int r = static_cast<int>(e / q);
+            mark(r, v.x);
+            mark(r, v.y);
+          });
+    } else {
+      strided_batches<8, 64 * kPfxWaves>(
+          static_cast<int64_t>(nr) * top_k, tid,
+          [&](int64_t e) -> int64_t {
+            const int64_t r = e / top_k;
+            const int64_t a = ib0 + r * p.idx_sn + (e - r * top_k);
+            return p.idx_i64 ? static_cast<const int64_t*>(p.idx)[a] : static_cast<int64_t>(i32[a]);
+          },
+          [&](int64_t e, int64_t j) { mark(static_cast<int>(e / top_k), j); });
+    }
     __syncthreads();
     if (tid < R) {
       int x = 0;
