@@ -318,9 +318,9 @@ def time_spread_attention(q, k, v, idx_like, reps=5):
     """Stage (d) on an index set with no filler: every (batch, row, kv head)
     attends k distinct keys spread over the whole sequence (a seeded random
     start and odd stride modulo n, distinct because n is a power of two),
-    unmasked, so no slot is a filler key that neighbouring rows share.  Median
-    ms of `reps` calls (HIP events on the launch stream); None when n is not a
-    power of two."""
+    unmasked, so no slot is a filler key that neighbouring rows share.  int32
+    indices, as in the forward's call.  Median ms of `reps` calls (HIP events on
+    the launch stream); None when n is not a power of two."""
     import torch
 
     from ssa_amd import kernels
@@ -334,7 +334,7 @@ def time_spread_attention(q, k, v, idx_like, reps=5):
     stride = torch.randint(0, max(n // 2, 1), shape, device=idx_like.device, generator=gen,
                            dtype=torch.int64) * 2 + 1
     j = torch.arange(kk, device=idx_like.device, dtype=torch.int64)
-    idx = ((start + j * stride) % n).to(idx_like.dtype)
+    idx = ((start + j * stride) % n).to(torch.int32)
     del start, stride
     out = kernels.sparse_attention(q, k, v, idx, None, False)
     ts = []

@@ -1066,6 +1066,25 @@ __global__ __launch_bounds__(64 * kPfxWaves, 2) void prefix_attention_kernel(Att
     for (int t = 0; t < S::NT; ++t) oacc[qt][t] = floatx4_t{0.f, 0.f, 0.f, 0.f};
   const int kswz = mf_swz<D>(c16);
   const int nch = (xmax + kMfChunk - 1) / kMfChunk;
+  // Keys below jfull[qt] (the wave's smallest min(X, position + 1) of tile qt)
+  // need no mask: the chunks below it skip the per-key tests.
+  int jfull[2];
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    int jl = qok[qt] ? min(xr[qt], ilim[qt] == 0x7FFFFFFF ? 0x7FFFFFFF : ilim[qt] + 1) : 0x7FFFFFFF;
+    jl = min(jl, __shfl_xor(jl, 1));
+    jl = min(jl, __shfl_xor(jl, 2));
+    jl = min(jl, __shfl_xor(jl, 4));
+    jl = min(jl, __shfl_xor(jl, 8));
+    jl = min(jl, __shfl_xor(jl, 16));
+    jl = min(jl, __shfl_xor(jl, 32));
+    jfull[qt] = __builtin_amdgcn_readfirstlane(jl);
+  }
+  // The scale c enters through the running maximum and the exponent's fma when
+  // it is positive and finite (max(s) c is the maximum of the scaled scores);
+  // otherwise the scores are scaled first (cmul = 1).
+  const bool cpos = p.qk_scale_log2 > 0.0f && p.qk_scale_log2 <= 3.4e38f;
+  const float cmul = cpos ? p.qk_scale_log2 : 1.0f;
   issue(0);
   if (nch > 1) issue(1);
   for (int u = 0; u < nch; ++u) {
@@ -1096,16 +1115,24 @@ __global__ __launch_bounds__(64 * kPfxWaves, 2) void prefix_attention_kernel(Att
 #pragma unroll
         for (int kb = 0; kb < S::KB; ++kb) sv = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[t][kb], qf[qt][kb], sv, 0, 0, 0);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int j = jbase + 16 * t + e;
-          sc[4 * t + e] = (j < xr[qt] && j <= ilim[qt]) ? sv[e] * p.qk_scale_log2 : -INFINITY;
-        }
+        for (int e = 0; e < 4; ++e) sc[4 * t + e] = sv[e];
       }
-      float mx = sc[0];
+      if (!cpos) {
 #pragma unroll
-      for (int x = 1; x < 8; ++x) mx = fmaxf(mx, sc[x]);
-      mx = fmaxf(mx, __shfl_xor(mx, 16));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
+        for (int x = 0; x < 8; ++x) sc[x] *= p.qk_scale_log2;
+      }
+      if ((u + 1) * kMfChunk > jfull[qt]) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int j = jbase + 16 * t + e;
+            if (!(j < xr[qt] && j <= ilim[qt])) sc[4 * t + e] = -INFINITY;
+          }
+      }
+      float mx = max_nan(max_nan(max_nan(sc[0], sc[1]), sc[2]), max_nan(sc[3], sc[4]));
+      mx = max_nan(max_nan(mx, sc[5]), max_nan(sc[6], sc[7]));
+      mx = rows4_reduce(mx, max_nan) * cmul;
       const float mnew = fmaxf(m_run[qt], mx);
       const float mref = (mnew == -INFINITY) ? 0.0f : mnew;
       const float alpha = __builtin_amdgcn_exp2f(m_run[qt] - mref);
@@ -1114,7 +1141,7 @@ __global__ __launch_bounds__(64 * kPfxWaves, 2) void prefix_attention_kernel(Att
       float ps = 0.0f;
 #pragma unroll
       for (int x = 0; x < 8; ++x) {
-        pr[x] = __builtin_amdgcn_exp2f(sc[x] - mref);
+        pr[x] = __builtin_amdgcn_exp2f(fmaf(sc[x], cmul, -mref));
         ps += pr[x];
       }
       l_run[qt] = l_run[qt] * alpha + ps;
@@ -1142,8 +1169,7 @@ __global__ __launch_bounds__(64 * kPfxWaves, 2) void prefix_attention_kernel(Att
   // 3. the state of each query with a prefix
 #pragma unroll
   for (int qt = 0; qt < 2; ++qt) {
-    float lt = l_run[qt] + __shfl_xor(l_run[qt], 16);
-    lt += __shfl_xor(lt, 32);
+    const float lt = rows4_reduce(l_run[qt], [](float a, float b) { return a + b; });
     if (!qok[qt] || xr[qt] == 0) continue;
     const int qv = 32 * wave + 16 * qt + c16;
     const int r = qv / g, hh = qv - r * g;
