@@ -83,7 +83,7 @@ struct SelParams {
   // XCDs; see shard_walk).
   int xcd_slices;
   // Light pass: bitmap words per chunk of a long window (set by the launcher:
-  // kFlatWords, or the whole key range as one chunk).
+  // kLightChunkWords, or the whole key range as one chunk).
   int light_chunk_words;
 };
 
@@ -762,14 +762,14 @@ __global__ __launch_bounds__(kSelThreads) void select_heavy_kernel(SelParams p, 
 // through the wave's LDS bitmap; a row with at most k_eff candidates writes its
 // candidates ascending and the filler directly.  A causal window of up to
 // kFlatWords bitmap words (32768 keys) uses a flat bitmap, cleared and read back
-// whole.  A longer window goes in chunks of 32768 keys through one chunk-sized
+// whole.  A longer window goes in chunks of 65536 keys through one chunk-sized
 // bitmap with a summary level (bit x: bitmap word x was touched by this row):
 // only the summary is cleared, a word is zeroed by the lane whose summary
 // atomicOr set its bit (a wave's LDS operations run in program order, so that
 // store lands before any lane's atomicOr on the word), and the candidates are
 // read back from the touched words only.  Each bucket keeps a cursor, so its
 // ascending postings are marked once over the chunks; chunk 0's first words
-// are kept for the filler.  The LDS per wave is thus bounded (5.3 KB) for any
+// are kept for the filler.  The LDS per wave is thus bounded (9.5 KB) for any
 // n: a bitmap of the whole window (16 KB at n = 131072) let only 9 waves of
 // this pass share a CU there.  A row with more than k_eff candidates writes
 // its list into the workspace for select_screen_kernel when it fits (w.cap;
@@ -798,20 +798,25 @@ __host__ __device__ inline int light_words(int64_t n, int cwords) {
   // one chunk over all keys keeps its bitmap for the filler: no copy
   return light_chunk_summary(cwords) + cwords + (cwords < words ? kFillWords : 0);
 }
-// Chunk size of the light pass for n keys: kFlatWords when a row's postings are
-// few (estimated nseg * post_bh / n_c <= kLightChunkPostings), so that the
-// small chunk bitmap keeps many waves per CU (n = 131072, 16 codes of 32
-// postings: light pass 5.9 -> 5.1 ms); the whole key range as one chunk when
-// they are many (c5: 32 codes of 64 postings), where the rows are long enough
-// to hide their latency at low occupancy and chunking would mark the windows
-// of the rows with more than k candidates twice.
+// Chunk size of the light pass for n keys: kLightChunkWords (65536 keys, or
+// the whole range when shorter) when a row's postings are few (estimated
+// nseg * post_bh / n_c <= kLightChunkPostings), so that the chunk bitmap keeps
+// enough waves per CU (n = 131072, 16 codes of 32 postings: light pass 5.9 ->
+// 5.1 ms with 32768-key chunks; 65536-key chunks halve the chunk passes, each
+// of which reloads the row's buckets: stage (c) 8.93 -> 8.61 ms there, and
+// 3.50 -> 3.03 ms at n = 65536, one chunk); the whole key range as one chunk
+// when they are many (c5: 32 codes of 64 postings), where the rows are long
+// enough to hide their latency at low occupancy and chunking would mark the
+// windows of the rows with more than k candidates twice.
 constexpr double kLightChunkPostings = 1024.0;
+constexpr int kLightChunkWords = 2 * kFlatWords;
 inline int light_chunk_words(const SelParams& p) {
   const int64_t words = (p.n + 31) / 32;
   if (words <= kFlatWords) return kFlatWords;
   const double ppr = static_cast<double>(p.nseg) * static_cast<double>(p.post_bh + p.tail_bh) /
                      static_cast<double>(p.n_c);
-  return ppr <= kLightChunkPostings ? kFlatWords : static_cast<int>(words);
+  return ppr <= kLightChunkPostings ? static_cast<int>(min(words, static_cast<int64_t>(kLightChunkWords)))
+                                    : static_cast<int>(words);
 }
 
 // Writes the row's candidates (the set bits of the touched bitmap words) in
@@ -1036,7 +1041,7 @@ __global__ __launch_bounds__(64) void select_light_kernel(SelParams p, int64_t r
     }
   };
 
-  // Window of more than kFlatWords words: cwords words (32768 keys, or all
+  // Window of more than kFlatWords words: cwords words (65536 keys, or all
   // keys as one chunk) at a time, each chunk with a summary level (bit x:
   // bitmap word x was touched by this row): only the summary is cleared, a
   // word is zeroed by the lane whose summary atomicOr set its bit (a wave's LDS
