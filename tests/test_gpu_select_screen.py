@@ -73,6 +73,31 @@ def test_screen_equals_block_path_and_oracle(dev, orc, d, g):
     _check_oracle(orc, c, got, top_k, orc.MASK_CAUSAL)
 
 
+@pytest.mark.parametrize("sorted_", [False, True])
+def test_screen_xcd_slices_equal_block_path(dev, orc, sorted_):
+    """B=2, h_kv=4: eight (batch, kv head) pairs, so each XCD's screen and pick
+    waves walk their own slice of every shard's list; with the full workspace
+    and with one that lists only some rows, the indices and stats equal the
+    one-block-per-row kernel's, which the oracle pins on sampled rows."""
+    _say(f"select screen xcd slices sorted={sorted_}")
+    from ssa_amd import _lib, kernels
+
+    B, n, h_kv, top_k = 2, 1400, 4, 64
+    c = _case(orc, dev, B, n, h_kv, 2, 128, 64, 4, 2, 31)
+    args = (c["q"], c["k"], c["qc"], c["off"], c["post"], c["b"], top_k, _lib.MASK_CAUSAL)
+    ref, st_ref = kernels.select(*args, sorted=sorted_, with_stats=True, use_workspace=False)
+    L = _lib.load()
+    base = int(L.ssa_select_workspace_bytes(B, n, h_kv, 0))
+    full = int(L.ssa_select_workspace_bytes(B, n, h_kv, top_k))
+    for ws in (full, base + (full - base) // 5):
+        got, st = kernels.select(*args, sorted=sorted_, with_stats=True, use_workspace=ws)
+        assert int((st[..., 0] > top_k).sum()) > B * h_kv * n // 2, "most rows must be screened"
+        assert torch.equal(got, ref), ws
+        assert torch.equal(st, st_ref), ws
+    if not sorted_:
+        _check_oracle(orc, c, ref, top_k, orc.MASK_CAUSAL, rows=np.arange(0, n, 97))
+
+
 @pytest.mark.parametrize("mode", ["none", "dense"])
 def test_screen_mask_modes(dev, orc, mode):
     _say(f"select screen mask={mode}")
