@@ -1001,6 +1001,54 @@ __global__ __launch_bounds__(64) void select_light_kernel(SelParams p, int64_t r
       }
       return;
     }
+    if (half_buckets) {
+      // The cursor loop with a bucket per half-wave, as above: a half takes
+      // its bucket's postings below kend 32 at a time; its ballot half counts
+      // them, and lane m0 + 2u + s advances bucket m0 + 2u + s's cursor by the
+      // count of half s.
+      const int sub = lane >> 5, ll = lane & 31;
+      for (int m0 = 0; m0 < p.nseg; m0 += 2 * kLightBatch) {
+        int lo_u[kLightBatch], len_u[kLightBatch], took[kLightBatch];
+#pragma unroll
+        for (int u = 0; u < kLightBatch; ++u) {
+          const int b = m0 + 2 * u + sub;
+          lo_u[u] = __shfl(cur_lo, min(b, 63));
+          len_u[u] = (b < p.nseg) ? __shfl(cur_len, min(b, 63)) : 0;
+          took[u] = 0;
+        }
+        for (int base = 0;; base += 32) {
+          int32_t j_u[kLightBatch];
+#pragma unroll
+          for (int u = 0; u < kLightBatch; ++u) {
+            const int e = lo_u[u] + min(base + ll, len_u[u] - 1);
+            j_u[u] = __builtin_amdgcn_raw_buffer_load_b32(prs, e * 4, 0, 0);
+          }
+          bool more = false;
+#pragma unroll
+          for (int u = 0; u < kLightBatch; ++u) {
+            const bool in_range = base + ll < len_u[u] && j_u[u] < kend;
+            const uint32_t half = static_cast<uint32_t>(__ballot(in_range) >> (32 * sub));
+            took[u] += __popc(half);
+            more = more || half == 0xFFFFFFFFu;
+            if (in_range) add(j_u[u]);
+          }
+          if (__ballot(more) == 0ull) break;
+        }
+#pragma unroll
+        for (int u = 0; u < kLightBatch; ++u) {
+          const int t0 = __shfl(took[u], 0), t1 = __shfl(took[u], 32);
+          if (lane == m0 + 2 * u) {
+            cur_lo += t0;
+            cur_len -= t0;
+          }
+          if (lane == m0 + 2 * u + 1) {
+            cur_lo += t1;
+            cur_len -= t1;
+          }
+        }
+      }
+      return;
+    }
     for (int m0 = 0; m0 < p.nseg; m0 += kLightBatch) {
       int lo_u[kLightBatch], len_u[kLightBatch], took[kLightBatch];
 #pragma unroll

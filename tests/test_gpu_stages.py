@@ -359,14 +359,16 @@ def test_code_topk_flagged_rows_batched(dev, orc, top, n_c, temperature):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("mode", ["causal", "none"])
-def test_router_long_rows_bit_exact(dev, orc, dtype, mode):
-    """n = 70000 keys: a row's key bitmap spans more than 64 summary words, so the
-    index-order pass reads its candidates back in two chunks; stats and indices
-    must equal the oracle's."""
+@pytest.mark.parametrize("n_c,a", [(2048, 4), (8192, 8)])
+def test_router_long_rows_bit_exact(dev, orc, dtype, mode, n_c, a):
+    """n = 70000 keys: a row's key bitmap spans more than one 65536-key chunk,
+    so the index-order pass marks and reads its candidates back in two chunks
+    (at N_c = 8192 the buckets hold about 17 postings, and a half-wave marks
+    each); stats and indices must equal the oracle's."""
     from ssa_amd import CodebookRouter
 
-    _say(f"router long rows dtype={dtype} mode={mode}")
-    n, h_q, h_kv, d, d_s, n_c, a, b, k = 70000, 2, 1, 64, 16, 2048, 4, 2, 128
+    _say(f"router long rows dtype={dtype} mode={mode} n_c={n_c} a={a}")
+    n, h_q, h_kv, d, d_s, b, k = 70000, 2, 1, 64, 16, 2, 128
     q, kk, w_qr, w_kr, cb = _route_inputs(n, h_q, h_kv, d, d_s, n_c, 23, dtype, False)
     r = CodebookRouter(head_dim=d, route_dim=d_s, num_kv_heads=h_kv, num_codebook=n_c,
                        codes_per_key=b, codes_per_query=a, top_k=k)
