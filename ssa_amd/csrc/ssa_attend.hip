@@ -75,13 +75,17 @@ struct AttParams {
   float* stats;
   // Matrix-core row kernel: wait for each chunk's gather right after issuing it
   // instead of computing the previous chunk meanwhile.  Set when a (batch, kv
-  // head)'s K and V exceed kGatherWaitBytes: there the gathers come from past L2,
-  // and keeping one in flight during each chunk's MFMAs only adds contention
-  // (n = 131072, d = 128, 64 MB per head: 10.9 ms waiting against 11.6 ms
-  // overlapped; n = 32768, 16 MB: 3.06 against 2.92 ms).
+  // head)'s K and V exceed kGatherWaitBytes but all heads' together fit the
+  // 256 MB Infinity Cache: there the gathers come from past L2 but not from
+  // HBM, and keeping one in flight during each chunk's MFMAs only adds
+  // contention (c5, 64 MB per head and 128 MB in all: stage (d) 9.54 ms waiting
+  // against 10.09 ms overlapped; n = 32768, 16 MB per head: 3.06 against 2.92
+  // ms).  When they do not fit (n = 131072 with 8 kv heads, 512 MB), the
+  // overlap hides HBM latency: 13.48 against 13.65 ms.
   int gather_wait;
 };
 constexpr int64_t kGatherWaitBytes = int64_t(32) << 20;
+constexpr int64_t kInfinityCacheBytes = int64_t(256) << 20;
 
 // Key of slot `slot` given the index entry loaded for it: -1 = none (block mode:
 // past n), -2 = invalid index (reported through the error flag).
@@ -1380,7 +1384,8 @@ int attention_entry(const void* q, const void* k, const void* v, int dtype, int6
     }
   }
   if (blk_log2 == 0) p.stats = row_stats;
-  p.gather_wait = (n * d * 2 * 2 > kGatherWaitBytes) ? 1 : 0;
+  const int64_t head_kv_bytes = n * d * 2 * 2;
+  p.gather_wait = (head_kv_bytes > kGatherWaitBytes && head_kv_bytes * batch * h_kv <= kInfinityCacheBytes) ? 1 : 0;
   hipStream_t st = as_stream(stream);
   if (dtype == SSA_DTYPE_BF16) return launch_att<uint16_t>(p, d, st);
   return launch_att<float>(p, d, st);
