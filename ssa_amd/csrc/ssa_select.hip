@@ -915,10 +915,9 @@ __global__ __launch_bounds__(64) void select_light_kernel(SelParams p, int64_t r
     else o32[pos] = v;
   };
 
-  // Marks the row's window keys in [kbeg, kend) (bits relative to kbeg) and
-  // counts (when `count`) the postings inside the window and, for a chunk with
-  // a summary, the new keys (a flat window's marks need no atomic's return:
-  // its keys are counted from the bitmap afterwards).
+  // Marks the row's window keys in [kbeg, kend) (bits relative to kbeg) and,
+  // for a chunk, its summary, and counts (when `count`) the postings inside the
+  // window.
   // Buckets go kLightBatch at a time, their postings loaded together before
   // any is marked (the bitmap, the counts and the summary do not depend on the
   // order).  cur_lo / cur_len (lane m: bucket m) are the bucket cursors: the
@@ -936,13 +935,10 @@ __global__ __launch_bounds__(64) void select_light_kernel(SelParams p, int64_t r
           (mrow == nullptr || mrow[j] != 0)) {
         const int jr = static_cast<int>(j - kbeg);
         const int x = jr >> 5;
-        if (summary) {
-          const uint32_t sb = 1u << (x & 31);
-          if (!(atomicOr(&sm[x >> 5], sb) & sb)) bm[x] = 0u;
-        }
-        const uint32_t bit = 1u << (jr & 31);
-        if (!summary) atomicOr(&bm[x], bit);  // flat: no return wait; the new keys are counted after
-        else if (!(atomicOr(&bm[x], bit) & bit) && count) ++fresh;
+        // no atomic's return is waited for: the bitmap was cleared before the
+        // marking, and the new keys are counted from it afterwards
+        if (summary) atomicOr(&sm[x >> 5], 1u << (x & 31));
+        atomicOr(&bm[x], 1u << (jr & 31));
       }
     };
     if (!cursors) {
@@ -1091,12 +1087,12 @@ __global__ __launch_bounds__(64) void select_light_kernel(SelParams p, int64_t r
 
   // Window of more than kFlatWords words: cwords words (65536 keys, or all
   // keys as one chunk) at a time, each chunk with a summary level (bit x:
-  // bitmap word x was touched by this row): only the summary is cleared, a
-  // word is zeroed by the lane whose summary atomicOr set its bit (a wave's LDS
-  // operations run in program order, so that store lands before any lane's
-  // atomicOr on the word), and the chunk's candidates are read back from the
-  // touched words only.  `sink(pos, key)` receives them ascending; returns
-  // their number.  Chunk 0's first fwn words are kept for the filler.
+  // bitmap word x was touched by this row): the chunk's bitmap and summary are
+  // cleared (16-byte stores, no waits) and marked with ors whose return no lane
+  // waits for (a wave's LDS operations run in program order), and the chunk's
+  // candidates are read back from the touched words only.  `sink(pos, key)`
+  // receives them ascending; returns their number.  Chunk 0's first fwn words
+  // are kept for the filler.
   const int64_t ckeys = static_cast<int64_t>(cwords) * 32;
   const bool one_chunk = wend <= ckeys;
   int last_cs = 0;  // summary words of the last chunk marked
@@ -1110,6 +1106,9 @@ __global__ __launch_bounds__(64) void select_light_kernel(SelParams p, int64_t r
       const int cs = (cw + 31) >> 5;
       last_cs = cs;
       for (int x = lane; x < cs; x += 64) sm[x] = 0u;
+      // (bm is 16-byte aligned: the summary takes a multiple of 4 words)
+      for (int x = 4 * lane; x + 3 < cw; x += 256) *reinterpret_cast<uint4*>(bm + x) = make_uint4(0u, 0u, 0u, 0u);
+      for (int x = (cw & ~3) + lane; x < cw; x += 64) bm[x] = 0u;
       __builtin_amdgcn_wave_barrier();
       mark_range(kbeg, kend, true, count, !one_chunk);
       if (!(count && one_chunk)) {  // one chunk: emitted once C is known
@@ -1138,6 +1137,13 @@ __global__ __launch_bounds__(64) void select_light_kernel(SelParams p, int64_t r
     filled = run_chunks(true, [&](int pos, int32_t key) {
       if (pos < p.top_k) put(pos, key);
     });
+    if (one_chunk) {
+      // the new keys: the touched words' bits (emitted once C is known)
+      const int cw = static_cast<int>((wend + 31) >> 5);
+      for (int x = lane; x < cw; x += 64) fresh += __popc(bm[x]);
+    } else {
+      fresh = (lane == 0) ? filled : 0;  // every chunk's keys were emitted
+    }
   }
   int C = 0, raw = 0;
   wave_excl_scan(fresh, lane, &C);
