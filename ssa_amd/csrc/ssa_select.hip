@@ -764,9 +764,7 @@ __global__ __launch_bounds__(kSelThreads) void select_heavy_kernel(SelParams p, 
 // kFlatWords bitmap words (32768 keys) uses a flat bitmap, cleared and read back
 // whole.  A longer window goes in chunks of 65536 keys through one chunk-sized
 // bitmap with a summary level (bit x: bitmap word x was touched by this row):
-// only the summary is cleared, a word is zeroed by the lane whose summary
-// atomicOr set its bit (a wave's LDS operations run in program order, so that
-// store lands before any lane's atomicOr on the word), and the candidates are
+// both are cleared per chunk (16-byte stores, no waits), and the candidates are
 // read back from the touched words only.  Each bucket keeps a cursor, so its
 // ascending postings are marked once over the chunks; chunk 0's first words
 // are kept for the filler.  The LDS per wave is thus bounded (9.5 KB) for any
