@@ -1279,9 +1279,6 @@ __device__ __forceinline__ uint16_t bf16_up_bits(float f) {
   const uint32_t u = __float_as_uint(f);
   return static_cast<uint16_t>((u >> 16) + ((u & 0xFFFFu) ? 1u : 0u));
 }
-__device__ __forceinline__ float key_to_score(uint32_t key) {
-  return __uint_as_float((key & 0x80000000u) ? (key & 0x7FFFFFFFu) : ~key);
-}
 // lane p of each 16-lane row reads lane p + 1 (lane 15 reads 0)
 __device__ __forceinline__ float dpp_from_plus1(float x) {
   return __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(x), 0x101, 0xF, 0xF, false));
