@@ -532,6 +532,30 @@ def run_c5(seed, dev, steps, warmup):
             "ms": ms, "tokens_per_s": cfg["B"] * cfg["n"] / (ms / 1000), "stages_ms": st, "steps": steps}
 
 
+def run_c4(seed, dev, steps, warmup):
+    """Config 4 (the decoder block: RMSNorm, projections, RoPE, SSA, o_proj;
+    B 4, n 8192, d_model 4096): whole-block ms and tokens/s and per-phase ms."""
+    import torch
+
+    cfg = dict(CONFIGS["c4"])
+    blk = make_block(cfg, seed, dev)
+    with torch.no_grad():
+        for _ in range(warmup):
+            block_step(blk)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            block_step(blk)
+        torch.cuda.synchronize()
+        ms = 1000 * (time.perf_counter() - t0) / steps
+        phases = block_stages(blk)
+    print(f"c4: {ms:.3f} ms", file=sys.stderr, flush=True)
+    del blk
+    return {"workload": "c4: RMSNorm + SSAAttention forward (projections, RoPE, stages a-d, o_proj), "
+                        "B 4, n 8192, d_model 4096, causal routing",
+            "ms": ms, "tokens_per_s": cfg["B"] * cfg["n"] / (ms / 1000), "phases_ms": phases, "steps": steps}
+
+
 def _cpu_model():
     cpu = platform.processor() or platform.machine()
     try:
@@ -858,10 +882,15 @@ def main():
                      "logical_gather_gbs": alg["d_bytes_logical"] / t["d"] / 1e9},
         "stages": stages,
     }
-    if args.backward:
+    # The default c3 run also records the backward, single-token decoding at
+    # the full cache and config 4 (the flags set other sizes).
+    extras = args.config == "c3" and not args.no_extras and args.n is None and args.num_codebook is None
+    if args.backward or extras:
         line["backward"] = time_backward(cfg, q, k, v, inter)
-    if args.decode > 0:
-        line["decode"] = time_decode(cfg, q, k, v, router, args.decode)
+        print(f"backward: {line['backward']['ms']:.3f} ms", file=sys.stderr, flush=True)
+    if args.decode > 0 or extras:
+        line["decode"] = time_decode(cfg, q, k, v, router, args.decode if args.decode > 0 else 128)
+        print(f"decode: {line['decode']['ms_per_token']:.3f} ms per token", file=sys.stderr, flush=True)
         if args.decode_lens:
             by_len = {}
             for n_ in [int(x) for x in args.decode_lens.split(",")]:
@@ -892,8 +921,10 @@ def main():
         policies = ("scaled", "fixed") if args.sweep_nc == "both" else (args.sweep_nc,)
         steps = max(3, args.steps // 4)
         line["sweep"] = {pol: run_sweep(cfg, ns, pol, args.seed, dev, steps) for pol in policies}
-    if args.config == "c3" and not args.no_extras and args.n is None and args.num_codebook is None:
+    if extras:
+        del q, k, v, inter
         line["c5"] = run_c5(args.seed, dev, max(3, args.steps // 4), 2)
+        line["c4"] = run_c4(args.seed, dev, max(3, args.steps // 4), 2)
     print(json.dumps(line), flush=True)
 
 

@@ -1804,10 +1804,7 @@ int launch_select(const SelParams& p, int64_t rows, size_t smem, void* ws, size_
   }
   auto hk = select_heavy_kernel<T, GMAX, D>;
   if (int s = reserve_lds(reinterpret_cast<const void*>(hk), smem, "select")) return s;
-  // Two blocks per CU take the listed rows in turn: the list is short (none at
-  // c3, a few thousand rows at c5), and every further block only launches,
-  // finds the list exhausted and exits (c3: 26 -> 8 us; c5: 471 -> 449 us).
-  hk<<<dim3(static_cast<unsigned>(persistent_grid(rows, 2))), kSelThreads, smem, st>>>(pi, qg, w);
+  hk<<<dim3(static_cast<unsigned>(persistent_grid(rows, 8))), kSelThreads, smem, st>>>(pi, qg, w);
   if (int s = check_launch("select_heavy_kernel")) return s;
   if (!sort_after) return SSA_OK;
   select_sort_kernel<T, GMAX, D><<<dim3(static_cast<unsigned>(rows)), 64, 0, st>>>(pi, qg);
