@@ -882,11 +882,8 @@ sparse_attention_mfma_kernel(AttParams p) {
 // kPfxQv query vectors (R = kPfxQv / g consecutive rows of one (batch, kv
 // head), all their heads) and streams the keys [0, max X) through LDS once for
 // all of them:
-//   1. X per row: from the selection (ssa_select's row_prefix), or else from
-//      the indices: those below min(top_k, kPfxXMax, n) set bits of an LDS
-//      bitmap, X is the first clear bit, lowered to the smallest index that
-//      occurs twice (duplicates count twice in the reference, so a prefix must
-//      hold each key once); X then goes to pfx_x.
+//   1. X per row from pfx_x: the selection's row_prefix, or else what
+//      prefix_x_kernel found in the indices.
 //   2. Chunks of 32 consecutive keys, three LDS buffers: every wave loads its
 //      share of chunk u + 2 while the block computes chunk u (one barrier per
 //      chunk).  Each wave scores its two 16-query tiles (S^T = K.Q^T on the
@@ -901,14 +898,78 @@ constexpr int kPfxQv = 32 * kPfxWaves;  // query vectors per block: two 16-colum
 constexpr int kPfxXMax = 1024;          // longest prefix looked for in the indices
 constexpr int kPfxBufs = 3;
 
+// X per row from its indices, when the caller gives no row_prefix: one wave per
+// row ((batch, kv head, query) in natural order).  The indices below
+// xb = min(top_k, kPfxXMax, n) set bits of a 32-word LDS bitmap, X is the first
+// clear bit, lowered to the smallest index that occurs twice (duplicates count
+// twice in the reference, so a prefix must hold each key once); X goes to
+// pfx_x.  The rows' index loads are 16-byte pieces where the layout allows.
+constexpr int kPfxXWaves = 4;
+__global__ __launch_bounds__(64 * kPfxXWaves) void prefix_x_kernel(AttParams p) {
+  __shared__ uint32_t bits[kPfxXWaves][kPfxXMax / 32];
+  __shared__ int s_dup[kPfxXWaves];
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int lane = threadIdx.x & 63;
+  const int64_t lrow = min(static_cast<int64_t>(blockIdx.x) * kPfxXWaves + wave, p.rows - 1);
+  const int64_t bh = lrow / p.n_q, r = lrow - bh * p.n_q;
+  const int h = static_cast<int>(bh % p.h_kv);
+  const int64_t bb = bh / p.h_kv;
+  const int xb = static_cast<int>(min(static_cast<int64_t>(min(p.top_k, kPfxXMax)), p.n));
+  const int words = (xb + 31) >> 5;
+  uint32_t* bw = bits[wave];
+  if (lane < kPfxXMax / 32) bw[lane] = 0u;
+  if (lane == 0) s_dup[wave] = 0x7FFFFFFF;
+  __syncthreads();
+  auto mark = [&](int64_t j) {
+    if (j >= 0 && j < xb) {
+      const uint32_t bit = 1u << (j & 31);
+      if (atomicOr(&bw[j >> 5], bit) & bit) atomicMin(&s_dup[wave], static_cast<int>(j));
+    }
+  };
+  const int64_t ib = bb * p.idx_sb + r * p.idx_sn + static_cast<int64_t>(h) * p.idx_sh;
+  const int top_k = p.top_k;
+  if (!p.idx_i64 && (top_k & 3) == 0 &&
+      (reinterpret_cast<uintptr_t>(static_cast<const int32_t*>(p.idx) + ib) & 15) == 0) {
+    const int4* row4 = reinterpret_cast<const int4*>(static_cast<const int32_t*>(p.idx) + ib);
+    for (int e = lane; e < (top_k >> 2); e += 64) {
+      const int4 v = row4[e];
+      mark(v.x);
+      mark(v.y);
+      mark(v.z);
+      mark(v.w);
+    }
+  } else if (p.idx_i64 && (top_k & 1) == 0 &&
+             (reinterpret_cast<uintptr_t>(static_cast<const int64_t*>(p.idx) + ib) & 15) == 0) {
+    const longlong2* row2 = reinterpret_cast<const longlong2*>(static_cast<const int64_t*>(p.idx) + ib);
+    for (int e = lane; e < (top_k >> 1); e += 64) {
+      const longlong2 v = row2[e];
+      mark(v.x);
+      mark(v.y);
+    }
+  } else {
+    for (int e = lane; e < top_k; e += 64)
+      mark(p.idx_i64 ? static_cast<const int64_t*>(p.idx)[ib + e]
+                     : static_cast<int64_t>(static_cast<const int32_t*>(p.idx)[ib + e]));
+  }
+  __syncthreads();
+  // first clear bit below 32 * words: the lowest word that is not full
+  const uint32_t v = (lane < words) ? bw[lane] : 0u;
+  const uint64_t open = __ballot(lane < words && v != 0xFFFFFFFFu);
+  int x = 32 * words;
+  if (open != 0ull) {
+    const int w0 = __ffsll(static_cast<unsigned long long>(open)) - 1;
+    const uint32_t vw = static_cast<uint32_t>(__shfl(static_cast<int>(v), w0));
+    x = 32 * w0 + __ffs(~vw) - 1;
+  }
+  if (lane == 0) p.pfx_x[lrow] = min(min(x, xb), s_dup[wave]);
+}
+
 template <int D>
 __global__ __launch_bounds__(64 * kPfxWaves, 2) void prefix_attention_kernel(AttParams p) {
   using S = MfShape<D>;
   constexpr int kLoadsPerWave = S::NLD / kPfxWaves;  // of K and of V, per chunk
   static_assert(S::NLD % kPfxWaves == 0, "chunk loads split evenly over the waves");
   __shared__ __align__(16) unsigned char kv[kPfxBufs][2][kMfChunk * S::ROW];  // [buffer][K, V]
-  __shared__ uint32_t bits[kPfxQv][kPfxXMax / 32];
-  __shared__ int s_dup[kPfxQv];
   __shared__ int s_x[kPfxQv];
   __shared__ int s_xmax;
   const int g = p.g;
@@ -926,89 +987,12 @@ __global__ __launch_bounds__(64 * kPfxWaves, 2) void prefix_attention_kernel(Att
   const int64_t bb = bh / p.h_kv;
   const int nr = static_cast<int>(min(static_cast<int64_t>(R), p.n_q - r0));
 
-  // 1. X of each row
+  // 1. X of each row (from the selection, or from prefix_x_kernel)
   if (tid == 0) s_xmax = 0;
-  if (p.pfx_given) {
+  {
     const int xcap = static_cast<int>(min(static_cast<int64_t>(p.top_k), p.n));
     if (tid < R) s_x[tid] = (tid < nr) ? min(max(p.pfx_x[bh * p.n_q + r0 + tid], 0), xcap) : 0;
     __syncthreads();
-  } else {
-    const int xb = static_cast<int>(min(static_cast<int64_t>(min(p.top_k, kPfxXMax)), p.n));
-    const int words = (xb + 31) >> 5;
-    for (int e = tid; e < R * (kPfxXMax / 32); e += 64 * kPfxWaves)
-      bits[e / (kPfxXMax / 32)][e % (kPfxXMax / 32)] = 0u;
-    if (tid < kPfxQv) s_dup[tid] = 0x7FFFFFFF;
-    __syncthreads();
-    const int top_k = p.top_k;
-    const int64_t ib0 = bb * p.idx_sb + r0 * p.idx_sn + static_cast<int64_t>(h) * p.idx_sh;
-    auto mark = [&](int r, int64_t j) {
-      if (j >= 0 && j < xb) {
-        const uint32_t bit = 1u << (j & 31);
-        const uint32_t old = atomicOr(&bits[r][j >> 5], bit);
-        if (old & bit) atomicMin(&s_dup[r], static_cast<int>(j));
-      }
-    };
-    const int32_t* i32 = static_cast<const int32_t*>(p.idx);
-    if (!p.idx_i64 && (top_k & 3) == 0 && (p.idx_sn & 3) == 0 &&
-        (reinterpret_cast<uintptr_t>(i32 + ib0) & 15) == 0) {
-      // int32 rows in 16-byte pieces: four times the bytes per load in flight
-      const int q = top_k >> 2;
-      strided_batches<8, 64 * kPfxWaves>(
-          static_cast<int64_t>(nr) * q, tid,
-          [&](int64_t e) -> int4 {
-            const int64_t r = e / q;
-            return *reinterpret_cast<const int4*>(i32 + ib0 + r * p.idx_sn + 4 * (e - r * q));
-          },
-          [&](int64_t e, int4 v) {
-            const int r = static_cast<int>(e / q);
-            mark(r, v.x);
-            mark(r, v.y);
-            mark(r, v.z);
-            mark(r, v.w);
-          });
-    } else if (p.idx_i64 && (top_k & 1) == 0 && (p.idx_sn & 1) == 0 &&
-               (reinterpret_cast<uintptr_t>(static_cast<const int64_t*>(p.idx) + ib0) & 15) == 0) {
-      // int64 rows in 16-byte pieces
-      const int64_t* i64 = static_cast<const int64_t*>(p.idx);
-      const int q = top_k >> 1;
-      strided_batches<8, 64 * kPfxWaves>(
-          static_cast<int64_t>(nr) * q, tid,
-          [&](int64_t e) -> longlong2 {
-            const int64_t r = e / q;
-            return *reinterpret_cast<const longlong2*>(i64 + ib0 + r * p.idx_sn + 2 * (e - r * q));
-          },
-          [&](int64_t e, longlong2 v) {
-            const int r = static_cast<int>(e / q);
-            mark(r, v.x);
-            mark(r, v.y);
-          });
-    } else {
-      strided_batches<8, 64 * kPfxWaves>(
-          static_cast<int64_t>(nr) * top_k, tid,
-          [&](int64_t e) -> int64_t {
-            const int64_t r = e / top_k;
-            const int64_t a = ib0 + r * p.idx_sn + (e - r * top_k);
-            return p.idx_i64 ? static_cast<const int64_t*>(p.idx)[a] : static_cast<int64_t>(i32[a]);
-          },
-          [&](int64_t e, int64_t j) { mark(static_cast<int>(e / top_k), j); });
-    }
-    __syncthreads();
-    if (tid < R) {
-      int x = 0;
-      if (tid < nr) {
-        x = 32 * words;
-        for (int w = 0; w < words; ++w) {
-          const uint32_t v = bits[tid][w];
-          if (v != 0xFFFFFFFFu) {
-            x = 32 * w + __ffs(~v) - 1;
-            break;
-          }
-        }
-        x = min(min(x, xb), s_dup[tid]);
-        p.pfx_x[bh * p.n_q + r0 + tid] = x;
-      }
-      s_x[tid] = x;
-    }
   }
   if (tid < R) atomicMax(&s_xmax, s_x[tid]);
   __syncthreads();
@@ -1250,6 +1234,10 @@ int launch_att_d(const AttParams& p, hipStream_t st) {
       }
       AttParams pr = p;
       if (p.blk_log2 == 0 && p.pfx_x) {
+        if (!p.pfx_given) {
+          prefix_x_kernel<<<dim3(static_cast<unsigned>(ceil_div(p.rows, kPfxXWaves))), 64 * kPfxXWaves, 0, st>>>(p);
+          if (int s = check_launch("prefix_x_kernel")) return s;
+        }
         const int64_t rows_per = kPfxQv / p.g;
         const int64_t pblocks = (p.rows / p.n_q) * ceil_div(p.n_q, rows_per);
         prefix_attention_kernel<D><<<dim3(static_cast<unsigned>(kXcds * xcd_per(pblocks))), 64 * kPfxWaves, 0, st>>>(p);
