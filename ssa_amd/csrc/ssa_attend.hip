@@ -133,7 +133,7 @@ __device__ __forceinline__ AttRow att_row(const AttParams& p, int64_t lrow) {
   AttRow r;
   r.ok = lrow < p.rows;
   const int64_t l = r.ok ? lrow : 0;
-  r.bh = l / p.n_q;
+  r.bh = udiv32(l, p.n_q);
   r.r = l - r.bh * p.n_q;
   if (p.order) {
     const int64_t o = p.order[l];
@@ -308,8 +308,8 @@ __global__ __launch_bounds__(kAttThreads, (AttMinBlocks<T, D, GMAX>::value)) voi
   const int64_t i = ar.i;  // key position (causal cut)
   const int64_t qr = ar.r;  // query row (q, idx, out)
   const int64_t bh = ar.bh;
-  const int h = static_cast<int>(bh % p.h_kv);
-  const int64_t bb = bh / p.h_kv;
+  const int64_t bb = udiv32(bh, p.h_kv);
+  const int h = static_cast<int>(bh - bb * p.h_kv);
 
   const T* qh = static_cast<const T*>(p.q) + bb * p.q_sb + qr * p.q_sn +
                 static_cast<int64_t>(h * p.g + (c16 < p.g ? c16 : 0)) * p.q_sh;
@@ -571,8 +571,8 @@ __device__ __forceinline__ void attend_row_mfma(const AttParams& p, const AttRow
   const int64_t i = ar.i;  // key position (causal cut)
   const int64_t qr = ar.r;  // query row (q, idx, out)
   const int64_t bh = ar.bh;
-  const int h = static_cast<int>(bh % p.h_kv);
-  const int64_t bb = bh / p.h_kv;
+  const int64_t bb = udiv32(bh, p.h_kv);
+  const int h = static_cast<int>(bh - bb * p.h_kv);
 
   const uint16_t* qh = static_cast<const uint16_t*>(p.q) + bb * p.q_sb + qr * p.q_sn +
                        static_cast<int64_t>(h * p.g + (c16 < p.g ? c16 : 0)) * p.q_sh;
@@ -840,14 +840,13 @@ __device__ __forceinline__ void attend_row_mfma(const AttParams& p, const AttRow
   }
   const int64_t ob = bb * p.o_sb + qr * p.o_sn + static_cast<int64_t>(h * p.g + c16) * p.o_sh + 4 * q4;
   if (p.out_bf16) {
+    // v_cvt_pk_bf16_f32: round to nearest even, the bits f32_to_bf16_rne gives
+    // for every non-NaN value, two values per instruction
     uint16_t* dst = static_cast<uint16_t*>(p.out) + ob;
 #pragma unroll
     for (int t = 0; t < S::NT; ++t)
       *reinterpret_cast<uint2*>(dst + 16 * t) =
-          make_uint2(static_cast<uint32_t>(f32_to_bf16_rne(oacc[t][0] * inv)) |
-                         (static_cast<uint32_t>(f32_to_bf16_rne(oacc[t][1] * inv)) << 16),
-                     static_cast<uint32_t>(f32_to_bf16_rne(oacc[t][2] * inv)) |
-                         (static_cast<uint32_t>(f32_to_bf16_rne(oacc[t][3] * inv)) << 16));
+          make_uint2(pack_bf16x2(oacc[t][0] * inv, oacc[t][1] * inv), pack_bf16x2(oacc[t][2] * inv, oacc[t][3] * inv));
   } else {
     float* dst = static_cast<float*>(p.out) + ob;
 #pragma unroll
@@ -911,9 +910,9 @@ __global__ __launch_bounds__(64 * kPfxXWaves) void prefix_x_kernel(AttParams p) 
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int lane = threadIdx.x & 63;
   const int64_t lrow = min(static_cast<int64_t>(blockIdx.x) * kPfxXWaves + wave, p.rows - 1);
-  const int64_t bh = lrow / p.n_q, r = lrow - bh * p.n_q;
-  const int h = static_cast<int>(bh % p.h_kv);
-  const int64_t bb = bh / p.h_kv;
+  const int64_t bh = udiv32(lrow, p.n_q), r = lrow - bh * p.n_q;
+  const int64_t bb = udiv32(bh, p.h_kv);
+  const int h = static_cast<int>(bh - bb * p.h_kv);
   const int xb = static_cast<int>(min(static_cast<int64_t>(min(p.top_k, kPfxXMax)), p.n));
   const int words = (xb + 31) >> 5;
   uint32_t* bw = bits[wave];
@@ -977,14 +976,14 @@ __global__ __launch_bounds__(64 * kPfxWaves, 2) void prefix_attention_kernel(Att
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int q4 = lane >> 4, c16 = lane & 15;
-  const int64_t tiles = ceil_div(p.n_q, R);
-  const int64_t nblk = (p.rows / p.n_q) * tiles;
+  const int64_t tiles = udiv32(p.n_q + R - 1, R);
+  const int64_t nblk = udiv32(p.rows, p.n_q) * tiles;
   const int64_t blk = xcd_block(blockIdx.x, xcd_per(nblk));
   if (blk >= nblk) return;
-  const int64_t bh = blk / tiles;
+  const int64_t bh = udiv32(blk, tiles);
   const int64_t r0 = (blk - bh * tiles) * R;
-  const int h = static_cast<int>(bh % p.h_kv);
-  const int64_t bb = bh / p.h_kv;
+  const int64_t bb = udiv32(bh, p.h_kv);
+  const int h = static_cast<int>(bh - bb * p.h_kv);
   const int nr = static_cast<int>(min(static_cast<int64_t>(R), p.n_q - r0));
 
   // 1. X of each row (from the selection, or from prefix_x_kernel)
@@ -1192,8 +1191,8 @@ __global__ __launch_bounds__(64 * kSplitWaves) void sparse_attention_split_kerne
   attend_row_mfma<D, false, kSplitWaves>(p, ar, kv_lds[wave][0], kv_lds[wave][1], wave, part[wave]);
   __syncthreads();
   if (!ar.ok) return;
-  const int h = static_cast<int>(ar.bh % p.h_kv);
-  const int64_t bb = ar.bh / p.h_kv;
+  const int64_t bb = udiv32(ar.bh, p.h_kv);
+  const int h = static_cast<int>(ar.bh - bb * p.h_kv);
   for (int e = threadIdx.x; e < p.g * D; e += 64 * kSplitWaves) {
     const int hh = e / D, dim = e - hh * D;
     float M = -INFINITY;

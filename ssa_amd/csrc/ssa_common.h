@@ -24,12 +24,22 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint16_t u) {
   return __uint_as_float(static_cast<uint32_t>(u) << 16);
 }
 
-// fp32 -> bf16 bits, round to nearest even; NaN stays a (quiet) NaN.
+// fp32 -> bf16 bits, round to nearest even; NaN stays a (quiet) NaN.  Both
+// results are computed and one is selected: no branch, so no exec-mask
+// sequence per value.
 __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x007FFFFFu)) return static_cast<uint16_t>((u >> 16) | 0x40u);
-  u += 0x7FFFu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t rounded = (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+  const bool nan = (u & 0x7FFFFFFFu) > 0x7F800000u;
+  return static_cast<uint16_t>(nan ? ((u >> 16) | 0x40u) : rounded);
+}
+
+// a / b for 0 <= a < 2^32 and 0 < b < 2^32.  Row, head and query indices are
+// below 2^31 (the launchers check), and the 32-bit unsigned division takes a
+// small fraction of the instructions of the 64-bit sequence (about 130 scalar
+// instructions per division, once per row in the one-row-per-wave kernels).
+__device__ __forceinline__ int64_t udiv32(int64_t a, int64_t b) {
+  return static_cast<int64_t>(static_cast<uint32_t>(a) / static_cast<uint32_t>(b));
 }
 
 // Element loaders: T is the storage type (float or uint16_t holding bf16 bits).

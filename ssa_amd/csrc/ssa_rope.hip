@@ -38,6 +38,7 @@ struct RopeParams {
   int h, d, half, rot, work;    // work = pairs/VEC + copy/VEC per row
   int64_t x_sb, x_sn, x_sh, o_sb, o_sn, o_sh, t_sb, t_sr;
   int by_head, inverse, copy_tail;
+  int narrow;  // rows * work < 2^32: thread indices divide in 32 bits
 };
 
 template <typename T> struct Elem;
@@ -94,12 +95,13 @@ __global__ __launch_bounds__(kRopeThreads) void rope_kernel(RopeParams p) {
   constexpr bool RB = sizeof(TX) == 2 && sizeof(TT) == 2;
   const int64_t t = static_cast<int64_t>(blockIdx.x) * kRopeThreads + threadIdx.x;
   if (t >= p.rows * p.work) return;
-  const int64_t row = t / p.work;
+  // (a 64-bit division is about a hundred instructions per thread)
+  const int64_t row = p.narrow ? udiv32(t, p.work) : t / p.work;
   const int w = static_cast<int>(t - row * p.work);
-  const int hh = static_cast<int>(row % p.h);
-  const int64_t bi = row / p.h;
-  const int64_t i = bi % p.n;
-  const int64_t b = bi / p.n;
+  const int64_t bi = p.narrow ? udiv32(row, p.h) : row / p.h;
+  const int hh = static_cast<int>(row - bi * p.h);
+  const int64_t b = p.narrow ? udiv32(bi, p.n) : bi / p.n;
+  const int64_t i = bi - b * p.n;
   const TX* x = static_cast<const TX*>(p.x) + b * p.x_sb + i * p.x_sn + hh * p.x_sh;
   TO* o = static_cast<TO*>(p.out) + b * p.o_sb + i * p.o_sn + hh * p.o_sh;
   const int pairs = p.half / VEC;
@@ -147,6 +149,7 @@ int launch_rope(const RopeParams& p0, int vec, hipStream_t st) {
   if (total == 0) return SSA_OK;
   const int64_t grid = ceil_div(total, kRopeThreads);
   if (grid > 0x7FFFFFFF) return fail(SSA_ERR_UNSUPPORTED, "ssa_rope: too many rows");
+  p.narrow = total < (int64_t(1) << 32) ? 1 : 0;
   if (vec == 4)
     rope_kernel<TX, TT, TO, 4><<<dim3(static_cast<unsigned>(grid)), dim3(kRopeThreads), 0, st>>>(p);
   else

@@ -31,10 +31,10 @@ __global__ __launch_bounds__(kRouteThreads) void route_vectors_kernel(
 
   const int h_out = h_in / group;
   const int64_t tiles = (n + rb - 1) / rb;
-  const int64_t bh = blockIdx.x / tiles;
-  const int64_t i0 = (blockIdx.x % tiles) * rb;
-  const int64_t b = bh / h_out;
-  const int h = static_cast<int>(bh % h_out);
+  const int64_t bh = udiv32(blockIdx.x, tiles);
+  const int64_t i0 = (blockIdx.x - bh * tiles) * rb;
+  const int64_t b = udiv32(bh, h_out);
+  const int h = static_cast<int>(bh - b * h_out);
   const int tid = threadIdx.x;
 
   for (int e = tid; e < d_s * d; e += kRouteThreads) Ws[(e / d) * dpad + (e % d)] = w[e];
@@ -123,10 +123,10 @@ __global__ __launch_bounds__(256) void route_vectors_tile_kernel(
   float* red = Xs + kRvRows * dpad;   // [kRvRows][32]
   const int h_out = h_in / group;
   const int64_t tiles = (n + kRvRows - 1) / kRvRows;
-  const int64_t bh = blockIdx.x / tiles;
-  const int64_t i0 = (blockIdx.x % tiles) * kRvRows;
-  const int64_t b = bh / h_out;
-  const int h = static_cast<int>(bh % h_out);
+  const int64_t bh = udiv32(blockIdx.x, tiles);
+  const int64_t i0 = (blockIdx.x - bh * tiles) * kRvRows;
+  const int64_t b = udiv32(bh, h_out);
+  const int h = static_cast<int>(bh - b * h_out);
   const int tid = threadIdx.x;
   const int cg = tid & 7;   // coordinates 4*cg .. 4*cg+3
   const int rg = tid >> 3;  // rows 2*rg, 2*rg+1
@@ -243,10 +243,10 @@ __global__ __launch_bounds__(kRrThreads) void route_vectors_row_kernel(
   const int d = DC > 0 ? DC : d_rt;
   const int h_out = h_in / group;
   const int64_t tiles = (n + kRrThreads - 1) / kRrThreads;
-  const int64_t bh = blockIdx.x / tiles;
-  const int64_t i = (blockIdx.x % tiles) * kRrThreads + threadIdx.x;
-  const int64_t b = bh / h_out;
-  const int h = static_cast<int>(bh % h_out);
+  const int64_t bh = udiv32(blockIdx.x, tiles);
+  const int64_t i = (blockIdx.x - bh * tiles) * kRrThreads + threadIdx.x;
+  const int64_t b = udiv32(bh, h_out);
+  const int h = static_cast<int>(bh - b * h_out);
   const int64_t ic = i < n ? i : n - 1;  // lanes past n compute row n-1 and store nothing
   const T* xb = x + b * sb + static_cast<int64_t>(h) * group * sh + ic * sn;
   const int pieces = d / 8;
@@ -355,10 +355,10 @@ __global__ __launch_bounds__(256) void route_vectors_split_kernel(
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int h_out = h_in / group;
   const int64_t tiles = (n + kRsRows - 1) / kRsRows;
-  const int64_t bh = blockIdx.x / tiles;
-  const int64_t i0 = (blockIdx.x % tiles) * kRsRows;
-  const int64_t b = bh / h_out;
-  const int h = static_cast<int>(bh % h_out);
+  const int64_t bh = udiv32(blockIdx.x, tiles);
+  const int64_t i0 = (blockIdx.x - bh * tiles) * kRsRows;
+  const int64_t b = udiv32(bh, h_out);
+  const int h = static_cast<int>(bh - b * h_out);
   const int64_t ic = (i0 + lane < n) ? i0 + lane : n - 1;  // rows past n: row n-1, not stored
   const T* xr = x + b * sb + static_cast<int64_t>(h) * group * sh + ic * sn;
   const int cr = threadIdx.x >> 2, cs0 = 8 * (threadIdx.x & 3);
@@ -467,8 +467,8 @@ __global__ __launch_bounds__(kTopThreads) void code_topk_kernel(
   int* bcnt = cnt + kTopRows;                                    // [rows]
 
   const int64_t tiles = (rows + kTopRows - 1) / kTopRows;
-  const int64_t bh = blockIdx.x / tiles;
-  const int64_t r0 = (blockIdx.x % tiles) * kTopRows;
+  const int64_t bh = udiv32(blockIdx.x, tiles);
+  const int64_t r0 = (blockIdx.x - bh * tiles) * kTopRows;
   const int hh = static_cast<int>(bh % h);
   const float* xb = xhat + bh * rows * d_s;
   const float* cb = chat + static_cast<int64_t>(hh) * n_c * d_s;
@@ -727,9 +727,9 @@ __device__ __forceinline__ void code_topk_mfma_block(
   const int q4 = lane >> 4, c16 = lane & 15;
   const int n_c_pad = n_c_padded(n_c);
   const int64_t tiles = (rows + kMfRows - 1) / kMfRows;
-  const int64_t bh = blk / tiles;
-  const int64_t r0 = (blk % tiles) * kMfRows + wave * 64;
-  const int hh = static_cast<int>(bh % h);
+  const int64_t bh = udiv32(blk, tiles);  // (block indices are below 2^31)
+  const int64_t r0 = (blk - bh * tiles) * kMfRows + wave * 64;
+  const int hh = static_cast<int>(bh - udiv32(bh, h) * h);
   const float* xb = xhat + bh * rows * d_s;
   const uint16_t* cbh = cbf + static_cast<int64_t>(hh) * n_c_pad * 32;
 
@@ -1095,7 +1095,7 @@ __global__ __launch_bounds__(256, 1) void code_topk_mfma_pair_kernel(
   const int64_t tiles = (rows + kMfRows - 1) / kMfRows;
   const int64_t lb = xcd_block(blockIdx.x, xcd_per(2 * grid_a));
   if (lb >= 2 * grid_a) return;
-  const int64_t bh = lb / (2 * tiles), i = lb - bh * 2 * tiles;
+  const int64_t bh = udiv32(lb, 2 * tiles), i = lb - bh * 2 * tiles;
   if (i < tiles)
     code_topk_mfma_block<QA>(xa, rows, h, chat, cbf, cmax_bits, n_c, d_s, temperature, top_a, codes_a, flags_a,
                              bh * tiles + i);

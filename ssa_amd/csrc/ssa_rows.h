@@ -86,13 +86,15 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   const bf16x2_t v = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
   return __builtin_bit_cast(uint32_t, v);
 }
-// lane p of each 16-lane row reads lane p - 8 (lanes p < 8 read 0)
+// lane p of each 16-lane row reads lane p - 8 (lanes p < 8 read 0: bound_ctrl,
+// so no zeroed old value is needed and the compiler may fold the move into
+// the instruction that uses it)
 __device__ __forceinline__ uint32_t dpp_from_minus8(uint32_t x) {
-  return __builtin_amdgcn_update_dpp(0u, x, 0x118, 0xF, 0xF, false);
+  return __builtin_amdgcn_update_dpp(0u, x, 0x118, 0xF, 0xF, true);
 }
 // lane p of each 16-lane row reads lane p + 8 (lanes p >= 8 read 0)
 __device__ __forceinline__ float dpp_from_plus8(float x) {
-  return __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(x), 0x108, 0xF, 0xF, false));
+  return __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(x), 0x108, 0xF, 0xF, true));
 }
 
 // NaN-propagating maximum (v_maximum3_f32 on gfx950): unlike fmaxf it needs no

@@ -95,7 +95,7 @@ __device__ __forceinline__ int64_t row_of_slot(const SelParams& p, int64_t t) {
   if (p.order == nullptr) return t;
   const int32_t o = p.order[t];
   if (static_cast<uint32_t>(o) >= static_cast<uint64_t>(p.n_q)) return -1;
-  return (t / p.n_q) * p.n_q + o;
+  return udiv32(t, p.n_q) * p.n_q + o;
 }
 
 __host__ __device__ inline int pow2_at_least(int v) {
@@ -326,11 +326,11 @@ __device__ __forceinline__ void select_row(const SelParams& p, const T* __restri
   __shared__ int s_scan[kSelThreads / 64];
 
   const int tid = threadIdx.x;
-  const int64_t r = row % p.n_q;
+  const int64_t bh = udiv32(row, p.n_q);
+  const int64_t r = row - bh * p.n_q;
   const int64_t i = p.q_pos0 + r;
-  const int64_t bh = row / p.n_q;
-  const int h = static_cast<int>(bh % p.h_kv);
-  const int64_t bb = bh / p.h_kv;
+  const int64_t bb = udiv32(bh, p.h_kv);
+  const int h = static_cast<int>(bh - bb * p.h_kv);
   const T* q0 = qg + bb * p.q_sb + r * p.q_sn + static_cast<int64_t>(h * p.g) * p.q_sh;
   const T* kbase = static_cast<const T*>(p.k) + bb * p.k_sb + static_cast<int64_t>(h) * p.k_sh;
   const int32_t* pp = p.postings + bh * p.post_bh;
@@ -592,10 +592,10 @@ __global__ __launch_bounds__(64) void select_sort_kernel(SelParams p, const T* _
   if (row < 0) return;
   const int m = min(p.cnt[row], p.k_eff);
   if (m <= 1) return;
-  const int64_t r = row % p.n_q;
-  const int64_t bh = row / p.n_q;
-  const int h = static_cast<int>(bh % p.h_kv);
-  const int64_t bb = bh / p.h_kv;
+  const int64_t bh = udiv32(row, p.n_q);
+  const int64_t r = row - bh * p.n_q;
+  const int64_t bb = udiv32(bh, p.h_kv);
+  const int h = static_cast<int>(bh - bb * p.h_kv);
   const T* q0 = qg + bb * p.q_sb + r * p.q_sn + static_cast<int64_t>(h * p.g) * p.q_sh;
   const T* kbase = static_cast<const T*>(p.k) + bb * p.k_sb + static_cast<int64_t>(h) * p.k_sh;
   const int64_t obase = ((bb * p.n_q + r) * p.h_kv + h) * p.top_k;
@@ -864,11 +864,11 @@ __global__ __launch_bounds__(64) void select_light_kernel(SelParams p, int64_t r
   const int64_t row = row_of_slot(p, slot);
   if (row < 0) return;
   const int words = static_cast<int>((p.n + 31) >> 5);
-  const int64_t r = row % p.n_q;
+  const int64_t bh = udiv32(row, p.n_q);
+  const int64_t r = row - bh * p.n_q;
   const int64_t i = p.q_pos0 + r;
-  const int64_t bh = row / p.n_q;
-  const int h = static_cast<int>(bh % p.h_kv);
-  const int64_t bb = bh / p.h_kv;
+  const int64_t bb = udiv32(bh, p.h_kv);
+  const int h = static_cast<int>(bh - bb * p.h_kv);
   const int32_t* pp = p.postings + bh * p.post_bh;
   const int32_t* tp = p.tail_postings ? p.tail_postings + bh * p.tail_bh : nullptr;
   const bool causal = p.mask_mode == SSA_MASK_CAUSAL;
@@ -1328,10 +1328,10 @@ select_screen_kernel(SelParams p, SelWs w) {
     if (!x.ok) continue;  // the pick pass sends the row to the exact pass
     const int C = x.C;
     const int64_t off = x.off;
-    const int64_t r = x.row % p.n_q;
-    const int64_t bh = x.row / p.n_q;
-    const int h = static_cast<int>(bh % p.h_kv);
-    const int64_t bb = bh / p.h_kv;
+    const int64_t bh = udiv32(x.row, p.n_q);
+    const int64_t r = x.row - bh * p.n_q;
+    const int64_t bb = udiv32(bh, p.h_kv);
+    const int h = static_cast<int>(bh - bb * p.h_kv);
     const uint16_t* q0 = static_cast<const uint16_t*>(p.q) + bb * p.q_sb + r * p.q_sn +
                          static_cast<int64_t>(h * p.g) * p.q_sh;
     const uint16_t* kbase = static_cast<const uint16_t*>(p.k) + bb * p.k_sb + static_cast<int64_t>(h) * p.k_sh;
@@ -1475,10 +1475,10 @@ __global__ __launch_bounds__(64 * kScrWaves) void select_pick_kernel(SelParams p
     const int C = x.C;
     const int64_t off = x.off;
     const int64_t row = x.row;
-    const int64_t r = row % p.n_q;
-    const int64_t bh = row / p.n_q;
-    const int h = static_cast<int>(bh % p.h_kv);
-    const int64_t bb = bh / p.h_kv;
+    const int64_t bh = udiv32(row, p.n_q);
+    const int64_t r = row - bh * p.n_q;
+    const int64_t bb = udiv32(bh, p.h_kv);
+    const int h = static_cast<int>(bh - bb * p.h_kv);
     const int R = (C + 63) / 64;  // positions lane + 64 r, r < R
 
     // The row's scores into LDS (coalesced), with their range: eight loads at

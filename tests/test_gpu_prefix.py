@@ -81,6 +81,8 @@ def test_dense_prefix_matches_row_path(dev, orc, d, g, top_k, causal, n, i64):
 
     bf = kernels.sparse_attention(q, k, v, idx, None, causal)  # bf16 output
     torch.testing.assert_close(bf.float(), out_p, rtol=1e-2, atol=1e-2)
+    # the bf16 store rounds the same fp32 values to nearest even, as torch does
+    assert torch.equal(bf, out_p.to(torch.bfloat16)), "bf16 output must be the fp32 output rounded"
 
     rows = np.unique(np.concatenate([np.arange(0, 8), [40, 41], np.arange(n // 2 - 4, n // 2 + 4),
                                      np.arange(n - 8, n)]))
@@ -176,3 +178,31 @@ def test_backward_dense_prefix(dev, orc, d, g, causal, n):
         err_r = float((a - b).abs().max())
         assert err_o <= 2e-5 * scale, f"{name} vs oracle: {err_o:.3e} > 2e-5 * {scale:.3e}"
         assert err_r <= 2e-5 * scale, f"{name} vs row path: {err_r:.3e} > 2e-5 * {scale:.3e}"
+
+
+def test_nan_query_propagates_to_its_head_only(dev):
+    """A NaN in one query head's vector makes that head's output row NaN in the
+    fp32 and the bf16 output (the bf16 store keeps NaN a NaN), and leaves every
+    other (row, head) finite and the bf16 output the fp32 output rounded."""
+    from ssa_amd import kernels
+
+    print("nan query", flush=True)
+    n, h_kv, g, d, top_k = 300, 2, 4, 128, 64
+    q = randn((1, n, h_kv * g, d), 501, torch.bfloat16)
+    q[0, 10, 5, 7] = float("nan")
+    q = q.to(dev)
+    k = randn((1, n, h_kv, d), 502, torch.bfloat16).to(dev)
+    v = randn((1, n, h_kv, d), 503, torch.bfloat16).to(dev)
+    gen = torch.Generator().manual_seed(504)
+    idx = torch.stack([torch.randperm(n, generator=gen)[:top_k] for _ in range(n * h_kv)])
+    idx = idx.reshape(1, n, h_kv, top_k).to(torch.int32).to(dev)
+    out32 = torch.empty((1, n, h_kv * g, d), device=dev, dtype=torch.float32)
+    kernels.sparse_attention(q, k, v, idx, None, False, out=out32)
+    bf = kernels.sparse_attention(q, k, v, idx, None, False)
+    bad = torch.zeros((1, n, h_kv * g), dtype=torch.bool)
+    bad[0, 10, 5] = True
+    for o in (out32, bf):
+        nan_rows = torch.isnan(o.float()).all(-1).cpu()
+        assert torch.equal(nan_rows, bad), "only the NaN query's head may be NaN"
+        assert bool(torch.isfinite(o.float()[~bad.to(dev)]).all())
+    assert torch.equal(bf[~bad.to(dev)], out32.to(torch.bfloat16)[~bad.to(dev)])
