@@ -957,7 +957,7 @@ __global__ __launch_bounds__(64 * kPfxXWaves) void prefix_x_kernel(AttParams p) 
   int x = 32 * words;
   if (open != 0ull) {
     const int w0 = __ffsll(static_cast<unsigned long long>(open)) - 1;
-    const uint32_t vw = static_cast<uint32_t>(__shfl(static_cast<int>(v), w0));
+    const uint32_t vw = static_cast<uint32_t>(lane_value(static_cast<int>(v), w0));
     x = 32 * w0 + __ffs(~vw) - 1;
   }
   if (lane == 0) p.pfx_x[lrow] = min(min(x, xb), s_dup[wave]);

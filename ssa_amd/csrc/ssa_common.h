@@ -42,6 +42,15 @@ __device__ __forceinline__ int64_t udiv32(int64_t a, int64_t b) {
   return static_cast<int64_t>(static_cast<uint32_t>(a) / static_cast<uint32_t>(b));
 }
 
+// x of lane src for a wave-uniform src (a loop counter, a ballot's first bit):
+// v_readlane, a scalar result with no LDS round trip, where __shfl's
+// ds_bpermute waits on the LDS.  The lane's register is read whatever the
+// exec mask, so x must have been computed by that lane.
+__device__ __forceinline__ int lane_value(int x, int src) { return __builtin_amdgcn_readlane(x, src); }
+__device__ __forceinline__ float lane_value(float x, int src) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), src));
+}
+
 // Element loaders: T is the storage type (float or uint16_t holding bf16 bits).
 __device__ __forceinline__ float ld(const float* p) { return *p; }
 __device__ __forceinline__ float ld(const uint16_t* p) { return bf16_bits_to_f32(*p); }

@@ -114,6 +114,20 @@ __device__ __forceinline__ float rows4_reduce(float x, Op op) {
   return op(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
+// op over all 64 lanes, the result in every lane, with no LDS round trip:
+// DPP quad_perm [1,0,3,2] and [2,3,0,1] within each quad, row_half_mirror
+// (lane i of 8 reads 7 - i: the other quad) and row_mirror (lane i of 16
+// reads 15 - i: the other half), then rows4_reduce across the rows.  op is
+// symmetric and associative (min, max).
+template <class Op>
+__device__ __forceinline__ float wave_allreduce(float x, Op op) {
+  x = op(x, __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(x), 0xB1, 0xF, 0xF, true)));
+  x = op(x, __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(x), 0x4E, 0xF, 0xF, true)));
+  x = op(x, __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(x), 0x141, 0xF, 0xF, true)));
+  x = op(x, __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(x), 0x140, 0xF, 0xF, true)));
+  return rows4_reduce(x, op);
+}
+
 // V^T (or K^T) fragment of 16-feature tile t from a chunk's rows in LDS at `l`
 // (the A operand of O^T += V^T P^T): within each 16-lane group, lane p receives
 // element p mod 4 from the rows addressed by lanes p / 4 + 4e, which matches

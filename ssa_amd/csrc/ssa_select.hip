@@ -1432,8 +1432,7 @@ select_screen_kernel(SelParams p, SelWs w) {
         }
       }
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) emax = fmaxf(emax, __shfl_xor(emax, o));
+    emax = wave_allreduce(emax, [](float a, float b) { return fmaxf(a, b); });
     bad = __ballot(bad) != 0ull;
     if (lane == 0) w.emax[static_cast<int64_t>(shard) * w.shard_rows + e] = bad ? INFINITY : emax;
   }
@@ -1502,11 +1501,8 @@ __global__ __launch_bounds__(64 * kScrWaves) void select_pick_kernel(SelParams p
         }
       }
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      amin = fminf(amin, __shfl_xor(amin, o));
-      amax = fmaxf(amax, __shfl_xor(amax, o));
-    }
+    amin = wave_allreduce(amin, [](float a, float b) { return fminf(a, b); });
+    amax = wave_allreduce(amax, [](float a, float b) { return fmaxf(a, b); });
 
     // Band [lo, hi] holding the k_eff-th largest score: 256 bins over the band
     // (bin = floor((a - lo) * 256 / (hi - lo)), monotone in a), keep the bin
@@ -1547,9 +1543,9 @@ __global__ __launch_bounds__(64 * kScrWaves) void select_pick_kernel(SelParams p
       }
       const int src = __ffsll(static_cast<unsigned long long>(__ballot(bin >= 0))) - 1;
       if (src < 0) break;  // cannot happen: kk <= keys in the band
-      bin = __shfl(bin, src);
-      nk = __shfl(nk, src);
-      inbin = __shfl(inbin, src);
+      bin = lane_value(bin, src);
+      nk = lane_value(nk, src);
+      inbin = lane_value(inbin, src);
       float blo = INFINITY, bhi = -INFINITY;
 #pragma unroll 4
       for (int r = 0; r < R; ++r) {
@@ -1559,11 +1555,8 @@ __global__ __launch_bounds__(64 * kScrWaves) void select_pick_kernel(SelParams p
           bhi = fmaxf(bhi, a);
         }
       }
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) {
-        blo = fminf(blo, __shfl_xor(blo, o));
-        bhi = fmaxf(bhi, __shfl_xor(bhi, o));
-      }
+      blo = wave_allreduce(blo, [](float a, float b) { return fminf(a, b); });
+      bhi = wave_allreduce(bhi, [](float a, float b) { return fmaxf(a, b); });
       lo = blo;
       hi = bhi;
       kk = nk;
@@ -1650,8 +1643,8 @@ __global__ __launch_bounds__(64 * kScrWaves) void select_pick_kernel(SelParams p
     }
     int rank = 0;
     for (int b = 0; b < nb; ++b) {
-      const uint64_t kb = (static_cast<uint64_t>(static_cast<uint32_t>(__shfl(static_cast<int>(key >> 32), b))) << 32) |
-                          static_cast<uint32_t>(__shfl(static_cast<int>(key & 0xFFFFFFFFull), b));
+      const uint64_t kb = (static_cast<uint64_t>(static_cast<uint32_t>(lane_value(static_cast<int>(key >> 32), b))) << 32) |
+                          static_cast<uint32_t>(lane_value(static_cast<int>(key & 0xFFFFFFFFull), b));
       rank += (kb > key) ? 1 : 0;
     }
     if (lane < nb && rank < need) atomicOr(&sm[bp[lane] >> 5], 1u << (bp[lane] & 31));
