@@ -682,6 +682,7 @@ constexpr int kShards = 64;
 constexpr int kScrWaves = 4;    // waves per block of the screen
 constexpr int kScrBorder = 64;  // keys near the k-th score rescored exactly per row (more: exact pass)
 constexpr int kScrRegs = 48;    // scores held per lane: rows of at most 64 * kScrRegs candidates
+constexpr int kPickRegs = 32;   // the pick pass's scores per lane in LDS (longer rows read the workspace)
 
 struct SelWs {
   int32_t* ctr;
@@ -1451,7 +1452,7 @@ __device__ __forceinline__ int band_bin(float a, float lo, float scale) {
 
 template <int D, int GMAX>
 __global__ __launch_bounds__(64 * kScrWaves) void select_pick_kernel(SelParams p, SelWs w) {
-  __shared__ __align__(16) float avs[kScrWaves][64 * kScrRegs];  // position pos at [pos]
+  __shared__ __align__(16) float avs[kScrWaves][64 * kPickRegs];  // position pos at [pos]
   __shared__ int32_t hst[kScrWaves][256];
   __shared__ int32_t bps[kScrWaves][kScrBorder];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1482,18 +1483,22 @@ __global__ __launch_bounds__(64 * kScrWaves) void select_pick_kernel(SelParams p
 
     // The row's scores into LDS (coalesced), with their range: eight loads at
     // a time, all out before the first is used (positions past C reload score
-    // C - 1, C >= 1 for a listed row).
+    // C - 1, C >= 1 for a listed row).  A row longer than 64 * kPickRegs keeps
+    // them in the workspace and the passes below read them there: the smaller
+    // LDS buffer lets 4 blocks share a CU instead of 3.
+    const bool in_lds = C <= 64 * kPickRegs;
+    const float* ag = w.approx + off;
     float amin = INFINITY, amax = -INFINITY;
     for (int r0 = 0; r0 < R; r0 += 8) {
       float a8[8];
 #pragma unroll
-      for (int t = 0; t < 8; ++t) a8[t] = w.approx[off + min(lane + 64 * (r0 + t), C - 1)];
+      for (int t = 0; t < 8; ++t) a8[t] = ag[min(lane + 64 * (r0 + t), C - 1)];
 #pragma unroll
       for (int t = 0; t < 8; ++t) {
         const int pos = lane + 64 * (r0 + t);
         if (r0 + t < R) {
           const float a = (pos < C) ? a8[t] : -INFINITY;
-          av[pos] = a;
+          if (in_lds) av[pos] = a;
           if (pos < C) {
             amin = fminf(amin, a);
             amax = fmaxf(amax, a);
@@ -1504,87 +1509,95 @@ __global__ __launch_bounds__(64 * kScrWaves) void select_pick_kernel(SelParams p
     amin = wave_allreduce(amin, [](float a, float b) { return fminf(a, b); });
     amax = wave_allreduce(amax, [](float a, float b) { return fmaxf(a, b); });
 
-    // Band [lo, hi] holding the k_eff-th largest score: 256 bins over the band
-    // (bin = floor((a - lo) * 256 / (hi - lo)), monotone in a), keep the bin
-    // where the count from the top reaches the rank, shrink the band to the
-    // smallest and largest score in that bin; at most two passes.
-    float lo = amin, hi = amax;
-    int kk = p.k_eff;
-    for (int pass = 0; pass < 2 && hi > lo; ++pass) {
-      const float scale = 256.0f / (hi - lo);
-      for (int xx = lane; xx < 256; xx += 64) hs[xx] = 0;
-      __builtin_amdgcn_wave_barrier();
+    float lo, hi;
+    int m_in, nb;
+    uint32_t* sm = reinterpret_cast<uint32_t*>(hs);
+    auto band_and_classify = [&](auto score_at) {
+      // Band [lo, hi] holding the k_eff-th largest score: 256 bins over the band
+      // (bin = floor((a - lo) * 256 / (hi - lo)), monotone in a), keep the bin
+      // where the count from the top reaches the rank, shrink the band to the
+      // smallest and largest score in that bin; at most two passes.
+      lo = amin;
+      hi = amax;
+      int kk = p.k_eff;
+      for (int pass = 0; pass < 2 && hi > lo; ++pass) {
+        const float scale = 256.0f / (hi - lo);
+        for (int xx = lane; xx < 256; xx += 64) hs[xx] = 0;
+        __builtin_amdgcn_wave_barrier();
 #pragma unroll 4
-      for (int r = 0; r < R; ++r) {
-        const float a = av[lane + 64 * r];
-        if (a >= lo && a <= hi) atomicAdd(&hs[band_bin(a, lo, scale)], 1);
-      }
-      __builtin_amdgcn_wave_barrier();
-      int c4[4], tot = 0;
-#pragma unroll
-      for (int xx = 0; xx < 4; ++xx) {
-        c4[xx] = hs[255 - 4 * lane - xx];  // lanes walk the bins from the top
-        tot += c4[xx];
-      }
-      int all = 0;
-      const int before = wave_excl_scan(tot, lane, &all);
-      int bin = -1, nk = 0, inbin = 0;
-      if (before < kk && kk <= before + tot) {
-        int acc = before;
+        for (int r = 0; r < R; ++r) {
+          const float a = score_at(lane + 64 * r);
+          if (a >= lo && a <= hi) atomicAdd(&hs[band_bin(a, lo, scale)], 1);
+        }
+        __builtin_amdgcn_wave_barrier();
+        int c4[4], tot = 0;
 #pragma unroll
         for (int xx = 0; xx < 4; ++xx) {
-          if (bin < 0 && kk <= acc + c4[xx]) {
-            bin = 255 - 4 * lane - xx;
-            nk = kk - acc;
-            inbin = c4[xx];
+          c4[xx] = hs[255 - 4 * lane - xx];  // lanes walk the bins from the top
+          tot += c4[xx];
+        }
+        int all = 0;
+        const int before = wave_excl_scan(tot, lane, &all);
+        int bin = -1, nk = 0, inbin = 0;
+        if (before < kk && kk <= before + tot) {
+          int acc = before;
+#pragma unroll
+          for (int xx = 0; xx < 4; ++xx) {
+            if (bin < 0 && kk <= acc + c4[xx]) {
+              bin = 255 - 4 * lane - xx;
+              nk = kk - acc;
+              inbin = c4[xx];
+            }
+            acc += c4[xx];
           }
-          acc += c4[xx];
         }
-      }
-      const int src = __ffsll(static_cast<unsigned long long>(__ballot(bin >= 0))) - 1;
-      if (src < 0) break;  // cannot happen: kk <= keys in the band
-      bin = lane_value(bin, src);
-      nk = lane_value(nk, src);
-      inbin = lane_value(inbin, src);
-      float blo = INFINITY, bhi = -INFINITY;
+        const int src = __ffsll(static_cast<unsigned long long>(__ballot(bin >= 0))) - 1;
+        if (src < 0) break;  // cannot happen: kk <= keys in the band
+        bin = lane_value(bin, src);
+        nk = lane_value(nk, src);
+        inbin = lane_value(inbin, src);
+        float blo = INFINITY, bhi = -INFINITY;
 #pragma unroll 4
-      for (int r = 0; r < R; ++r) {
-        const float a = av[lane + 64 * r];
-        if (a >= lo && a <= hi && band_bin(a, lo, scale) == bin) {
-          blo = fminf(blo, a);
-          bhi = fmaxf(bhi, a);
+        for (int r = 0; r < R; ++r) {
+          const float a = score_at(lane + 64 * r);
+          if (a >= lo && a <= hi && band_bin(a, lo, scale) == bin) {
+            blo = fminf(blo, a);
+            bhi = fmaxf(bhi, a);
+          }
         }
+        blo = wave_allreduce(blo, [](float a, float b) { return fminf(a, b); });
+        bhi = wave_allreduce(bhi, [](float a, float b) { return fmaxf(a, b); });
+        lo = blo;
+        hi = bhi;
+        kk = nk;
+        __builtin_amdgcn_wave_barrier();
+        if (inbin <= 32) break;
       }
-      blo = wave_allreduce(blo, [](float a, float b) { return fminf(a, b); });
-      bhi = wave_allreduce(bhi, [](float a, float b) { return fmaxf(a, b); });
-      lo = blo;
-      hi = bhi;
-      kk = nk;
-      __builtin_amdgcn_wave_barrier();
-      if (inbin <= 32) break;
-    }
-    const float e2 = 2.0f * 1.02f * emax + 2e-30f;
-    const float thr_in = hi + e2, thr_out = lo - e2;
+      const float e2 = 2.0f * 1.02f * emax + 2e-30f;
+      const float thr_in = hi + e2, thr_out = lo - e2;
 
-    // Classify: keys surely in the top k_eff go to the selection mask (bit pos
-    // of word pos / 32, in hs), keys within 2 e of the band to bp (ascending).
-    uint32_t* sm = reinterpret_cast<uint32_t*>(hs);
-    int m_in = 0, nb = 0;
-    for (int r = 0; r < R; ++r) {
-      const int pos = lane + 64 * r;
-      const float a = av[pos];
-      const bool in = a > thr_in;
-      const bool border = pos < C && !in && a >= thr_out;
-      m_in += in ? 1 : 0;
-      const uint64_t imask = __ballot(in);
-      const uint64_t bmask = __ballot(border);
-      if (lane < 2) sm[2 * r + lane] = static_cast<uint32_t>(imask >> (32 * lane));
-      if (border) {
-        const int sl = nb + __popcll(bmask & below);
-        if (sl < kScrBorder) bp[sl] = pos;
+      // Classify: keys surely in the top k_eff go to the selection mask (bit pos
+      // of word pos / 32, in hs), keys within 2 e of the band to bp (ascending).
+      m_in = 0;
+      nb = 0;
+      for (int r = 0; r < R; ++r) {
+        const int pos = lane + 64 * r;
+        const float a = score_at(pos);
+        const bool in = a > thr_in;
+        const bool border = pos < C && !in && a >= thr_out;
+        m_in += in ? 1 : 0;
+        const uint64_t imask = __ballot(in);
+        const uint64_t bmask = __ballot(border);
+        if (lane < 2) sm[2 * r + lane] = static_cast<uint32_t>(imask >> (32 * lane));
+        if (border) {
+          const int sl = nb + __popcll(bmask & below);
+          if (sl < kScrBorder) bp[sl] = pos;
+        }
+        nb += __popcll(bmask);
       }
-      nb += __popcll(bmask);
-    }
+    };
+    if (in_lds) band_and_classify([&](int pos) { return av[pos]; });
+    else band_and_classify([&](int pos) { return pos < C ? ag[pos] : -INFINITY; });
     int n_in = 0;
     wave_excl_scan(m_in, lane, &n_in);
     const int need = p.k_eff - n_in;

@@ -138,7 +138,9 @@ def test_screen_workspace_sizes(dev, orc):
 
 def test_screen_rows_longer_than_the_screen(dev, orc):
     """N_c=8, a=4, b=2: late rows have up to ~0.8 i candidates, beyond what one
-    screened row holds (3072), so both the screen and the exact pass run."""
+    screened row holds (3072), so both the screen and the exact pass run; rows
+    of 2049-3072 candidates take the pick pass's workspace reads (its LDS holds
+    2048 scores per row)."""
     _say("select screen long rows")
     from ssa_amd import _lib
 
@@ -148,6 +150,7 @@ def test_screen_rows_longer_than_the_screen(dev, orc):
     ref, st_ref = _select(c, top_k, _lib.MASK_CAUSAL, use_workspace=False)
     cand = st[..., 0]
     assert int((cand > 3072).sum()) > 0 and int(((cand > top_k) & (cand <= 3072)).sum()) > 0
+    assert int(((cand > 2048) & (cand <= 3072)).sum()) > 0
     assert torch.equal(got, ref) and torch.equal(st, st_ref)
     rows = np.array([0, 1, 255, 256, 257, 3000, 3900, 4000, 5998, 5999])
     _check_oracle(orc, c, got, top_k, orc.MASK_CAUSAL, rows=rows)
