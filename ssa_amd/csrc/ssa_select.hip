@@ -544,15 +544,19 @@ __device__ __forceinline__ void wave_sort_desc(uint64_t (&x)[E], int lane) {
   for (int size = 2; size <= 64 * E; size <<= 1) {
 #pragma unroll
     for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      // One 64-bit compare per exchange: the direction enters as an equality
+      // with the comparison (keys are distinct apart from the zero padding,
+      // and equal keys may be swapped).
       if (stride >= E) {  // partner: the same slot of lane ^ (stride / E)
+        // r < E <= stride, so the stride and size bits of lane * E + r are
+        // those of lane * E: one direction for all of the lane's slots
+        const bool keep_max = (((lane * E) & stride) == 0) == (((lane * E) & size) == 0);
 #pragma unroll
         for (int r = 0; r < E; ++r) {
           const uint32_t lo = lane_xor(static_cast<uint32_t>(x[r]), stride / E);
           const uint32_t hi = lane_xor(static_cast<uint32_t>(x[r] >> 32), stride / E);
           const uint64_t y = (static_cast<uint64_t>(hi) << 32) | lo;
-          const int e = lane * E + r;
-          const bool keep_max = ((e & stride) == 0) == ((e & size) == 0);
-          x[r] = keep_max ? (x[r] > y ? x[r] : y) : (x[r] < y ? x[r] : y);
+          x[r] = ((y > x[r]) == keep_max) ? y : x[r];
         }
       } else {  // partner: slot r ^ stride of this lane
 #pragma unroll
@@ -561,7 +565,7 @@ __device__ __forceinline__ void wave_sort_desc(uint64_t (&x)[E], int lane) {
           const int r2 = r | stride;
           const bool desc = ((lane * E + r) & size) == 0;
           const uint64_t a = x[r], b = x[r2];
-          const bool sw = desc ? (a < b) : (a > b);
+          const bool sw = (a < b) == desc;
           x[r] = sw ? b : a;
           x[r2] = sw ? a : b;
         }
