@@ -85,6 +85,10 @@ struct SelParams {
   // Light pass: bitmap words per chunk of a long window (set by the launcher:
   // kLightChunkWords, or the whole key range as one chunk).
   int light_chunk_words;
+  // Light pass: the key positions (q_pos0 + r) of the rows a launch takes,
+  // [light_pos_lo, light_pos_hi); the launcher splits a whole-range chunk by
+  // position so the early rows run with a half-size bitmap.
+  int64_t light_pos_lo, light_pos_hi;
 };
 
 // Row ((b * h_kv + h) * n_q + r) processed in slot t of the launch
@@ -872,6 +876,7 @@ __global__ __launch_bounds__(64) void select_light_kernel(SelParams p, int64_t r
   const int64_t bh = udiv32(row, p.n_q);
   const int64_t r = row - bh * p.n_q;
   const int64_t i = p.q_pos0 + r;
+  if (i < p.light_pos_lo || i >= p.light_pos_hi) return;  // the other launch's row
   const int64_t bb = udiv32(bh, p.h_kv);
   const int h = static_cast<int>(bh - bb * p.h_kv);
   const int32_t* pp = p.postings + bh * p.post_bh;
@@ -1799,6 +1804,22 @@ int launch_select(const SelParams& p, int64_t rows, size_t smem, void* ws, size_
   // there the slices measured slower (c5: 2 kv heads), so they are kept for
   // the case of at least one pair per XCD.
   pi.xcd_slices = (p.n_q > 0 && rows / p.n_q >= kXcds) ? 1 : 0;
+  pi.light_pos_lo = 0;
+  pi.light_pos_hi = INT64_MAX;
+  // A causal window marked as one chunk over all keys (many postings per row)
+  // sizes every wave's bitmap for the whole key range.  The rows whose window
+  // ends in the first half of the keys run first, in a launch of their own
+  // with a half-size bitmap (about twice the waves per CU); the rest follow.
+  const int64_t lwords = (p.n + 31) / 32;
+  if (p.mask_mode == SSA_MASK_CAUSAL && pi.light_chunk_words == lwords && lwords > 2 * kFlatWords) {
+    SelParams pa = pi;
+    pa.light_chunk_words = static_cast<int>(lwords / 2);
+    pa.light_pos_hi = (lwords / 2) * 32;  // window of at most lwords / 2 words: one chunk
+    const size_t smem_a = sizeof(uint32_t) * static_cast<size_t>(light_words(p.n, pa.light_chunk_words));
+    select_light_kernel<<<dim3(static_cast<unsigned>(rows)), 64, smem_a, st>>>(pa, rows, w);
+    if (int s = check_launch("select_light_kernel")) return s;
+    pi.light_pos_lo = pa.light_pos_hi;
+  }
   select_light_kernel<<<dim3(static_cast<unsigned>(rows)), 64, light_smem(p), st>>>(pi, rows, w);
   if (int s = check_launch("select_light_kernel")) return s;
   if constexpr (kScreenable) {
