@@ -816,6 +816,7 @@ __host__ __device__ inline int light_words(int64_t n, int cwords) {
 // enough to hide their latency at low occupancy and chunking would mark the
 // windows of the rows with more than k candidates twice.
 constexpr double kLightChunkPostings = 1024.0;
+constexpr size_t kLdsBytesPerCu = 160 * 1024;
 constexpr int kLightChunkWords = 2 * kFlatWords;
 inline int light_chunk_words(const SelParams& p) {
   const int64_t words = (p.n + 31) / 32;
@@ -865,7 +866,14 @@ __device__ __forceinline__ int light_emit_flat(const uint32_t* bm, int live, int
   return filled;
 }
 
-__global__ __launch_bounds__(64) void select_light_kernel(SelParams p, int64_t rows, SelWs w) {
+// MINW: waves per SIMD the build must allow (amdgpu_waves_per_eu).  8 when a
+// wave's bitmap is small enough for 32 waves per CU (the flat windows of n up
+// to about 40K keys): the build then keeps to 78 SGPRs (spilling some to VGPR
+// lanes) instead of the 106 that allow 7.  Longer windows are bound by their
+// LDS bitmaps and keep the unconstrained build.
+template <int MINW>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(MINW, 8))) void select_light_kernel(
+    SelParams p, int64_t rows, SelWs w) {
   extern __shared__ __align__(16) uint32_t lbits[];
   const int lane = threadIdx.x & 63;
   const int64_t slot = blockIdx.x;
@@ -1816,11 +1824,14 @@ int launch_select(const SelParams& p, int64_t rows, size_t smem, void* ws, size_
     pa.light_chunk_words = static_cast<int>(lwords / 2);
     pa.light_pos_hi = (lwords / 2) * 32;  // window of at most lwords / 2 words: one chunk
     const size_t smem_a = sizeof(uint32_t) * static_cast<size_t>(light_words(p.n, pa.light_chunk_words));
-    select_light_kernel<<<dim3(static_cast<unsigned>(rows)), 64, smem_a, st>>>(pa, rows, w);
+    select_light_kernel<1><<<dim3(static_cast<unsigned>(rows)), 64, smem_a, st>>>(pa, rows, w);
     if (int s = check_launch("select_light_kernel")) return s;
     pi.light_pos_lo = pa.light_pos_hi;
   }
-  select_light_kernel<<<dim3(static_cast<unsigned>(rows)), 64, light_smem(p), st>>>(pi, rows, w);
+  if (light_smem(p) * 32 <= kLdsBytesPerCu)
+    select_light_kernel<8><<<dim3(static_cast<unsigned>(rows)), 64, light_smem(p), st>>>(pi, rows, w);
+  else
+    select_light_kernel<1><<<dim3(static_cast<unsigned>(rows)), 64, light_smem(p), st>>>(pi, rows, w);
   if (int s = check_launch("select_light_kernel")) return s;
   if constexpr (kScreenable) {
     if (w.cap > 0) {
