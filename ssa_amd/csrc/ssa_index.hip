@@ -128,24 +128,53 @@ __global__ __launch_bounds__(kScanThreads) void index_scan_kernel(int32_t* __res
   if (chunk == chunks - 1 && threadIdx.x == 0) ob[n_c] = carry + all;
 }
 
-// One wave per (tile, bh).  Entries are visited in index order e = j*b + r, 64
-// per round; lanes holding the same code are ranked by lane order, so every
-// bucket receives its keys in ascending j.
-__global__ __launch_bounds__(64) void index_scatter_kernel(
+// One block of `waves` waves per (tile, bh); wave s takes the s-th of
+// `waves` contiguous ranges of the tile's entries.  Entries are visited in
+// index order e = j*b + r, 64 per round; lanes holding the same code are
+// ranked by lane order, so every bucket receives its keys in ascending j.
+// With several waves each first counts its range's codes (LDS, [waves][n_c]);
+// wave s's cursor for code c then starts at the tile's base for c plus the
+// counts of the ranges before it, and the waves' round loops run side by side
+// (a tile's 64 rounds in one wave were a chain of memory and LDS latencies).
+__global__ __launch_bounds__(256) void index_scatter_kernel(
     const int32_t* __restrict__ k_codes, int64_t n, int b, int cstride, int n_c, int code_bits,
     int64_t tile_keys, int64_t tiles, const int32_t* __restrict__ base,
     int32_t* __restrict__ postings) {
-  extern __shared__ int32_t cursor[];
+  extern __shared__ int32_t cursors[];
   const int64_t tile = blockIdx.x;
   const int64_t bh = blockIdx.y;
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int wave = static_cast<int>(threadIdx.x >> 6);
+  const int waves = static_cast<int>(blockDim.x >> 6);
   const int32_t* bb = base + (bh * tiles + tile) * static_cast<int64_t>(n_c);
-  for (int c = lane; c < n_c; c += 64) cursor[c] = bb[c];
-  __syncthreads();
-  const int64_t e0 = tile * tile_keys * b;
-  int64_t e1 = (tile + 1) * tile_keys * b;
-  if (e1 > n * b) e1 = n * b;
+  const int64_t t0 = tile * tile_keys * b;
+  int64_t t1 = (tile + 1) * tile_keys * b;
+  if (t1 > n * b) t1 = n * b;
   const int32_t* kc = k_codes + bh * n * cstride;
+  const int64_t per = (t1 - t0 + waves - 1) / waves;
+  const int64_t e0 = min(t0 + wave * per, t1);
+  const int64_t e1 = min(e0 + per, t1);
+  int32_t* cursor = cursors + static_cast<int64_t>(wave) * n_c;
+  if (waves == 1) {
+    for (int c = lane; c < n_c; c += 64) cursor[c] = bb[c];
+  } else {
+    for (int x = threadIdx.x; x < waves * n_c; x += blockDim.x) cursors[x] = 0;
+    __syncthreads();
+    for (int64_t e = e0 + lane; e < e1; e += 64) {
+      const int32_t c = kc[code_at(e, b, cstride)];
+      if (static_cast<uint32_t>(c) < static_cast<uint32_t>(n_c)) atomicAdd(&cursor[c], 1);
+    }
+    __syncthreads();
+    for (int c = threadIdx.x; c < n_c; c += blockDim.x) {
+      int32_t run = bb[c];
+      for (int w = 0; w < waves; ++w) {
+        const int32_t cnt = cursors[static_cast<int64_t>(w) * n_c + c];
+        cursors[static_cast<int64_t>(w) * n_c + c] = run;
+        run += cnt;
+      }
+    }
+  }
+  __syncthreads();
   int32_t* post = postings + bh * n * b;
   const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   // The codes of kScatterBatch rounds are loaded before any is ranked, so a
@@ -221,9 +250,13 @@ int run_index(const int32_t* codes, int64_t bh, int64_t n, int b, int cstride, i
   index_scan_kernel<<<dim3(static_cast<unsigned>(chunks), static_cast<unsigned>(bh)), kScanThreads, 0, st>>>(
       hist, n_c, tiles, chunks, sums, offsets);
   if ((s = check_launch("index_scan_kernel"))) return s;
-  index_scatter_kernel<<<dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(bh)), 64,
-                         sizeof(int32_t) * n_c, st>>>(codes, n, b, cstride, n_c, code_bits, tk,
-                                                      tiles, hist, postings);
+  // waves per tile: as many cursor arrays as fit 64 KB of LDS, at most 4 (N_c =
+  // 4096: 4 waves; 8192: 2; 16384 and more: 1, the single-wave kernel as before)
+  int waves = 4;
+  while (waves > 1 && sizeof(int32_t) * static_cast<size_t>(n_c) * waves > 64 * 1024) waves >>= 1;
+  index_scatter_kernel<<<dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(bh)), 64 * waves,
+                         sizeof(int32_t) * n_c * waves, st>>>(codes, n, b, cstride, n_c, code_bits, tk,
+                                                              tiles, hist, postings);
   return check_launch("index_scatter_kernel");
 }
 
