@@ -4,6 +4,7 @@
 // einsum / temperature, topk).  All arithmetic is exact-order fp32 so that the
 // selected codes are bit-identical with the CPU oracle.
 #include <algorithm>
+#include <type_traits>
 
 #include "ssa_common.h"
 #include "ssa_internal.h"
@@ -994,78 +995,84 @@ __device__ __forceinline__ void code_topk_mfma_block(
 #pragma unroll
     for (int s = 0; s < 32; ++s) xr[s] = (s < d_s) ? xb[row * d_s + s] : 0.0f;
     const float* cb = chat + static_cast<int64_t>(hh) * n_c * d_s;
-    const bool scale = (temperature != 1.0f);
-    const uint16_t* rl = cand + (static_cast<size_t>(wave) * 4 + rt) * CAP * 64 + rc;
-    const int b1 = qn[0], b2 = b1 + qn[1], b3 = b2 + qn[2];  // list starts in row order
-    auto code_at = [&](int i) -> int {  // entry i of the row: list q, position j
-      const int q = (i >= b1 ? 1 : 0) + (i >= b2 ? 1 : 0) + (i >= b3 ? 1 : 0);
-      const int j = i - (q == 0 ? 0 : q == 1 ? b1 : q == 2 ? b2 : b3);
-      return rl[(j * 64) + q * 16];
-    };
-    auto code_row = [&](int c, float4 (&cv)[8]) {
-      const float4* cr = reinterpret_cast<const float4*>(cb + static_cast<int64_t>(c) * d_s);
+    // The temperature division as a compile-time choice: left to a runtime
+    // flag the compiler computed the division for every code and selected.
+    auto rescore = [&](auto scale_c) {
+      const uint16_t* rl = cand + (static_cast<size_t>(wave) * 4 + rt) * CAP * 64 + rc;
+      const int b1 = qn[0], b2 = b1 + qn[1], b3 = b2 + qn[2];  // list starts in row order
+      auto code_at = [&](int i) -> int {  // entry i of the row: list q, position j
+        const int q = (i >= b1 ? 1 : 0) + (i >= b2 ? 1 : 0) + (i >= b3 ? 1 : 0);
+        const int j = i - (q == 0 ? 0 : q == 1 ? b1 : q == 2 ? b2 : b3);
+        return rl[(j * 64) + q * 16];
+      };
+      auto code_row = [&](int c, float4 (&cv)[8]) {
+        const float4* cr = reinterpret_cast<const float4*>(cb + static_cast<int64_t>(c) * d_s);
 #pragma unroll
-      for (int s4 = 0; s4 < 8; ++s4) cv[s4] = (s4 * 4 < d_s) ? cr[s4] : make_float4(0.f, 0.f, 0.f, 0.f);
-    };
-    auto exact_key = [&](int c, const float4 (&cv)[8]) -> uint64_t {
-      float acc = 0.0f;
+        for (int s4 = 0; s4 < 8; ++s4) cv[s4] = (s4 * 4 < d_s) ? cr[s4] : make_float4(0.f, 0.f, 0.f, 0.f);
+      };
+      auto exact_key = [&](int c, const float4 (&cv)[8]) -> uint64_t {
+        float acc = 0.0f;
 #pragma unroll
-      for (int s4 = 0; s4 < 8; ++s4) {
-        if (s4 * 4 < d_s) {
-          acc = fma_rn(xr[s4 * 4 + 0], cv[s4].x, acc);
-          acc = fma_rn(xr[s4 * 4 + 1], cv[s4].y, acc);
-          acc = fma_rn(xr[s4 * 4 + 2], cv[s4].z, acc);
-          acc = fma_rn(xr[s4 * 4 + 3], cv[s4].w, acc);
+        for (int s4 = 0; s4 < 8; ++s4) {
+          if (s4 * 4 < d_s) {
+            acc = fma_rn(xr[s4 * 4 + 0], cv[s4].x, acc);
+            acc = fma_rn(xr[s4 * 4 + 1], cv[s4].y, acc);
+            acc = fma_rn(xr[s4 * 4 + 2], cv[s4].z, acc);
+            acc = fma_rn(xr[s4 * 4 + 3], cv[s4].w, acc);
+          }
         }
-      }
-      if (scale) acc = acc / temperature;
-      return composite_key(acc, static_cast<uint32_t>(c));
-    };
-    // One code row in flight per lane (a second buffer would hold 32 more
-    // VGPRs for the whole kernel; the other resident waves cover the latency).
-    int c = code_at(0);
-    float4 cv[8];
-    code_row(c, cv);
-    int32_t* out = codes + (bh * rows + row) * top;
-    if constexpr (Q <= 4) {
-      // top <= 16: a sorted register list (static indices), insertion by a
-      // compare-and-shift pass from the bottom
-      constexpr int TM = 4 * Q;
-      uint64_t best[TM];
+        if constexpr (decltype(scale_c)::value) acc = acc / temperature;
+        return composite_key(acc, static_cast<uint32_t>(c));
+      };
+      // One code row in flight per lane (a second buffer would hold 32 more
+      // VGPRs for the whole kernel; the other resident waves cover the latency).
+      int c = code_at(0);
+      float4 cv[8];
+      code_row(c, cv);
+      int32_t* out = codes + (bh * rows + row) * top;
+      if constexpr (Q <= 4) {
+        // top <= 16: a sorted register list (static indices), insertion by a
+        // compare-and-shift pass from the bottom
+        constexpr int TM = 4 * Q;
+        uint64_t best[TM];
 #pragma unroll
-      for (int p = 0; p < TM; ++p) best[p] = 0ull;  // below every key
-      for (int i = 0; i < m; ++i) {
-        if (i > 0) { c = code_at(i); code_row(c, cv); }
-        const uint64_t key = exact_key(c, cv);
+        for (int p = 0; p < TM; ++p) best[p] = 0ull;  // below every key
+        for (int i = 0; i < m; ++i) {
+          if (i > 0) { c = code_at(i); code_row(c, cv); }
+          const uint64_t key = exact_key(c, cv);
 #pragma unroll
-        for (int p = TM - 1; p > 0; --p) best[p] = key > best[p - 1] ? best[p - 1] : (key > best[p] ? key : best[p]);
-        best[0] = key > best[0] ? key : best[0];
-      }
-#pragma unroll
-      for (int p = 0; p < TM; ++p)
-        if (p < top) out[p] = static_cast<int32_t>(key_index(best[p]));
-    } else {
-      uint64_t* my = lists + static_cast<int64_t>(wave) * top * 64 + lane;  // entry p at my[p * 64]
-      int nb = 0;
-      for (int i = 0; i < m; ++i) {
-        const int cn = code_at(min(i + 1, m - 1));
-        float4 cvn[8];
-        code_row(cn, cvn);
-        const uint64_t key = exact_key(c, cv);
-        c = cn;
-#pragma unroll
-        for (int s4 = 0; s4 < 8; ++s4) cv[s4] = cvn[s4];
-        if (nb == top && key <= my[(top - 1) * 64]) continue;
-        int p = (nb < top) ? nb++ : top - 1;
-        while (p > 0 && my[(p - 1) * 64] < key) {
-          my[p * 64] = my[(p - 1) * 64];
-          --p;
+          for (int p = TM - 1; p > 0; --p) best[p] = key > best[p - 1] ? best[p - 1] : (key > best[p] ? key : best[p]);
+          best[0] = key > best[0] ? key : best[0];
         }
-        my[p * 64] = key;
+#pragma unroll
+        for (int p = 0; p < TM; ++p)
+          if (p < top) out[p] = static_cast<int32_t>(key_index(best[p]));
+      } else {
+        uint64_t* my = lists + static_cast<int64_t>(wave) * top * 64 + lane;  // entry p at my[p * 64]
+        int nb = 0;
+        for (int i = 0; i < m; ++i) {
+          const int cn = code_at(min(i + 1, m - 1));
+          float4 cvn[8];
+          code_row(cn, cvn);
+          const uint64_t key = exact_key(c, cv);
+          c = cn;
+#pragma unroll
+          for (int s4 = 0; s4 < 8; ++s4) cv[s4] = cvn[s4];
+          if (nb == top && key <= my[(top - 1) * 64]) continue;
+          int p = (nb < top) ? nb++ : top - 1;
+          while (p > 0 && my[(p - 1) * 64] < key) {
+            my[p * 64] = my[(p - 1) * 64];
+            --p;
+          }
+          my[p * 64] = key;
+        }
+        for (int p = 0; p < top; ++p) out[p] = static_cast<int32_t>(key_index(my[p * 64]));
       }
-      for (int p = 0; p < top; ++p) out[p] = static_cast<int32_t>(key_index(my[p * 64]));
-    }
-  }
+  
+    };
+    if (temperature != 1.0f) rescore(std::true_type{});
+    else rescore(std::false_type{});
+}
   if (row < rows) flags[bh * rows + row] = over ? 1 : 0;
 }
 
