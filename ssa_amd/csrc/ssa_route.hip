@@ -302,6 +302,76 @@ __global__ __launch_bounds__(kRrThreads) void route_vectors_row_kernel(
   }
 }
 
+// One head per output row (group == 1, the keys), route_dim == 32, bf16 rows of
+// a fixed head dim: route_vectors_row_kernel with each row's 32 coordinates
+// split over two waves of a block (wave 0: coordinates 0-15, wave 1: 16-31,
+// the same 64 rows), so twice the waves share the same fmaf chains and each
+// wave's W rows are still wave-uniform scalar loads.  The norm chain runs over
+// the coordinates in order: wave 0 passes its partial sum of squares to wave 1
+// through LDS, wave 1 finishes it and passes the denominator back.  Same
+// results as route_vectors_row_kernel, bit for bit.
+constexpr int kRhRows = 64;
+template <int DC>
+__global__ __launch_bounds__(128) void route_vectors_half_kernel(
+    const uint16_t* __restrict__ x, int64_t n, int h_in, int64_t sb, int64_t sn, int64_t sh,
+    const float* __restrict__ w, float* __restrict__ out) {
+  constexpr int HS = 16;  // coordinates per wave
+  constexpr int pieces = DC / 8;
+  constexpr int UNR = pieces % 8 == 0 ? 8 : 1;
+  __shared__ float s_nrm[kRhRows], s_den[kRhRows];
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int lane = threadIdx.x & 63;
+  const int64_t tiles = (n + kRhRows - 1) / kRhRows;
+  const int64_t bh = udiv32(blockIdx.x, tiles);
+  const int64_t i = (blockIdx.x - bh * tiles) * kRhRows + lane;
+  const int64_t b = udiv32(bh, h_in);
+  const int h = static_cast<int>(bh - b * h_in);
+  const int64_t ic = i < n ? i : n - 1;  // lanes past n compute row n-1 and store nothing
+  const uint16_t* xr = x + b * sb + static_cast<int64_t>(h) * sh + ic * sn;
+  const float* wh = w + static_cast<int64_t>(wave * HS) * DC;
+  float acc[HS];
+#pragma unroll
+  for (int s = 0; s < HS; ++s) acc[s] = 0.0f;
+  Piece8 cur = load8(xr);
+#pragma unroll 1
+  for (int c0 = 0; c0 < pieces; c0 += UNR) {
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) {
+      const int c = c0 + u;
+      const int cn = c + 1 < pieces ? c + 1 : c;
+      const Piece8 nxt = load8(xr + cn * 8);
+#pragma unroll
+      for (int s = 0; s < HS; ++s) {
+        const float* ws = wh + s * DC + c * 8;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[s] = fma_rn(cur.v[e], ws[e], acc[s]);
+      }
+      cur = nxt;
+    }
+  }
+  // (the group mean divides by 1: unchanged)
+  float nrm = 0.0f;
+  if (wave == 0) {
+#pragma unroll
+    for (int s = 0; s < HS; ++s) nrm = fma_rn(acc[s], acc[s], nrm);
+    s_nrm[lane] = nrm;
+  }
+  __syncthreads();
+  if (wave == 1) {
+    nrm = s_nrm[lane];
+#pragma unroll
+    for (int s = 0; s < HS; ++s) nrm = fma_rn(acc[s], acc[s], nrm);
+    s_den[lane] = fmaxf(sqrtf(nrm), 1e-12f);
+  }
+  __syncthreads();
+  const float den = s_den[lane];
+  if (i < n) {
+    float* o = out + (bh * n + i) * 32 + wave * HS;
+#pragma unroll
+    for (int s = 0; s < HS; ++s) o[s] = acc[s] / den;
+  }
+}
+
 // GQA groups (group > 1), route_dim == 32, head_dim a multiple of 8: 64 rows
 // per block and the group's heads spread over the block's 4 waves (wave w
 // takes heads w, w+4, ...), so a head's chain runs in a wave of its own with W
@@ -1338,15 +1408,17 @@ int launch_route_vectors(const void* x, int dtype, int64_t batch, int64_t n, int
           static_cast<const float*>(x), n, h_in, group, d, sb, sn, sh, w, out);
     return check_launch("route_vectors_split_kernel");
   }
+  if (d_s == 32 && piece8 && group == 1 && dtype == SSA_DTYPE_BF16 && d == 128) {
+    const int64_t grid = batch * h_in * ceil_div(n, kRhRows);
+    route_vectors_half_kernel<128><<<dim3(static_cast<unsigned>(grid)), 128, 0, st>>>(
+        static_cast<const uint16_t*>(x), n, h_in, sb, sn, sh, w, out);
+    return check_launch("route_vectors_half_kernel");
+  }
   if (d_s == 32 && piece8) {
     const int64_t grid = batch * (h_in / group) * ceil_div(n, kRrThreads);
     if (dtype == SSA_DTYPE_BF16)
-      if (d == 128)
-        route_vectors_row_kernel<uint16_t, 128><<<dim3(static_cast<unsigned>(grid)), kRrThreads, 0, st>>>(
-            static_cast<const uint16_t*>(x), n, h_in, group, d, sb, sn, sh, w, out);
-      else
-        route_vectors_row_kernel<uint16_t, 0><<<dim3(static_cast<unsigned>(grid)), kRrThreads, 0, st>>>(
-            static_cast<const uint16_t*>(x), n, h_in, group, d, sb, sn, sh, w, out);
+      route_vectors_row_kernel<uint16_t, 0><<<dim3(static_cast<unsigned>(grid)), kRrThreads, 0, st>>>(
+          static_cast<const uint16_t*>(x), n, h_in, group, d, sb, sn, sh, w, out);
     else
       route_vectors_row_kernel<float, 0><<<dim3(static_cast<unsigned>(grid)), kRrThreads, 0, st>>>(
           static_cast<const float*>(x), n, h_in, group, d, sb, sn, sh, w, out);

@@ -19,7 +19,7 @@ def _say(msg):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("h_in,group,d,d_s", [(8, 4, 128, 32), (6, 3, 64, 16), (2, 1, 64, 8),
-                                              (16, 8, 128, 32)])
+                                              (16, 8, 128, 32), (8, 1, 128, 32)])
 def test_route_vectors_bit_exact(dev, orc, dtype, h_in, group, d, d_s):
     from ssa_amd import kernels
 
@@ -40,6 +40,7 @@ def test_route_vectors_bit_exact(dev, orc, dtype, h_in, group, d, d_s):
     (17, 1, 8, 1, 128, 48),
     (500, 2, 4, 2, 64, 48),     # route_dim > 32: the general LDS-tiled kernel
     (300, 1, 2, 1, 128, 64),
+    (100, 2, 3, 1, 128, 32),    # the keys' kernel (two waves per 64 rows), a partial tile
 ])
 def test_route_vectors_small_and_wide_bit_exact(dev, orc, dtype, n, batch, h_in, group, d, d_s):
     """Few rows (the lane-per-coordinate kernel of decoding steps) and route
