@@ -62,6 +62,23 @@ __global__ __launch_bounds__(kHistThreads) void index_hist_kernel(
   for (int c = threadIdx.x; c < n_c; c += kHistThreads) hb[c] = lds_hist[c];
 }
 
+// Column c of a head's tile histograms summed over the tiles: eight loads
+// issued before their adds, so a column of T tiles waits on T/8 memory
+// latencies instead of T (integer sums: the order does not matter).
+__device__ __forceinline__ int32_t column_sum(const int32_t* __restrict__ hb, int n_c, int64_t tiles, int c) {
+  int32_t tot = 0;
+  int64_t t = 0;
+  for (; t + 8 <= tiles; t += 8) {
+    int32_t v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = hb[(t + u) * n_c + c];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) tot += v[u];
+  }
+  for (; t < tiles; ++t) tot += hb[t * n_c + c];
+  return tot;
+}
+
 // Entries per chunk of kScanThreads codes: block (chunk, bh), one code per
 // thread summed over the tiles, then a block sum into sums[bh][chunk].
 __global__ __launch_bounds__(kScanThreads) void index_chunk_sum_kernel(const int32_t* __restrict__ hist, int n_c,
@@ -72,9 +89,7 @@ __global__ __launch_bounds__(kScanThreads) void index_chunk_sum_kernel(const int
   const int64_t bh = blockIdx.y;
   const int c = chunk * kScanThreads + static_cast<int>(threadIdx.x);
   const int32_t* hb = hist + bh * tiles * static_cast<int64_t>(n_c);
-  int32_t tot = 0;
-  if (c < n_c)
-    for (int64_t t = 0; t < tiles; ++t) tot += hb[t * n_c + c];
+  int32_t tot = (c < n_c) ? column_sum(hb, n_c, tiles, c) : 0;
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) tot += __shfl_xor(tot, off, 64);
   if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = tot;
@@ -103,9 +118,7 @@ __global__ __launch_bounds__(kScanThreads) void index_scan_kernel(int32_t* __res
   int32_t carry = 0;
   for (int q = 0; q < chunk; ++q) carry += sums[bh * chunks + q];
   const int c = chunk * kScanThreads + static_cast<int>(threadIdx.x);
-  int32_t tot = 0;
-  if (c < n_c)
-    for (int64_t t = 0; t < tiles; ++t) tot += hb[t * n_c + c];
+  const int32_t tot = (c < n_c) ? column_sum(hb, n_c, tiles, c) : 0;
   const int32_t x = wave_incl_scan(tot);
   const int lane = threadIdx.x & 63;
   if (lane == 63) wsum[threadIdx.x >> 6] = x;
@@ -119,7 +132,18 @@ __global__ __launch_bounds__(kScanThreads) void index_scan_kernel(int32_t* __res
   if (c < n_c) {
     int32_t run = before + x - tot;
     ob[c] = run;
-    for (int64_t t = 0; t < tiles; ++t) {
+    int64_t t = 0;
+    for (; t + 8 <= tiles; t += 8) {  // eight loads out before their stores
+      int32_t v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = hb[(t + u) * n_c + c];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        hb[(t + u) * n_c + c] = run;
+        run += v[u];
+      }
+    }
+    for (; t < tiles; ++t) {
       const int32_t v = hb[t * n_c + c];
       hb[t * n_c + c] = run;
       run += v;
