@@ -496,12 +496,35 @@ __global__ __launch_bounds__(256) void route_vectors_split_kernel(
 }
 
 
-// Row-wise F.normalize: one thread per row.
+// Row-wise F.normalize: one thread per row.  Rows of 32 floats (the route
+// dim of every config) at 16-byte aligned addresses take a register copy
+// loaded in 16-byte pieces, all out before the chain starts (one scalar load
+// per element waited on each in turn).
 __global__ void normalize_rows_kernel(const float* __restrict__ x, int64_t rows, int d_s,
                                       float* __restrict__ out) {
   const int64_t r = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (r >= rows) return;
   const float* xr = x + r * d_s;
+  if (d_s == 32 && ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(out)) & 15) == 0) {
+    float v[32];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const float4 f = reinterpret_cast<const float4*>(xr)[q];
+      v[4 * q] = f.x;
+      v[4 * q + 1] = f.y;
+      v[4 * q + 2] = f.z;
+      v[4 * q + 3] = f.w;
+    }
+    float nrm = 0.0f;
+#pragma unroll
+    for (int s = 0; s < 32; ++s) nrm = fma_rn(v[s], v[s], nrm);
+    const float den = fmaxf(sqrtf(nrm), 1e-12f);
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+      reinterpret_cast<float4*>(out + r * 32)[q] =
+          make_float4(v[4 * q] / den, v[4 * q + 1] / den, v[4 * q + 2] / den, v[4 * q + 3] / den);
+    return;
+  }
   float nrm = 0.0f;
   for (int s = 0; s < d_s; ++s) nrm = fma_rn(xr[s], xr[s], nrm);
   const float den = fmaxf(sqrtf(nrm), 1e-12f);

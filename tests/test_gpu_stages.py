@@ -75,6 +75,11 @@ def test_normalize_rows_bit_exact(dev, orc):
     x[0, 0] = 0.0  # eps clamp: 0 / 1e-12 = 0
     got = kernels.normalize_rows(x.to(dev)).cpu().numpy()
     np.testing.assert_array_equal(got, orc.normalize(f32(x)))
+    # rows at an address 4 bytes past 16-byte alignment (the per-element path)
+    buf = torch.empty(x.numel() + 1, device=dev)
+    xm = buf[1:].view(x.shape)
+    xm.copy_(x.to(dev))
+    np.testing.assert_array_equal(kernels.normalize_rows(xm).cpu().numpy(), orc.normalize(f32(x)))
 
 
 @pytest.mark.parametrize("top,temperature,n_c,d_s", [(16, 1.0, 512, 32), (4, 1.0, 4096, 32),
