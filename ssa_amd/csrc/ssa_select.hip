@@ -756,8 +756,15 @@ __global__ __launch_bounds__(kSelThreads) void select_heavy_kernel(SelParams p, 
                                                                    SelWs w) {
   __shared__ int s_next;
   const int listed = static_cast<int>(min(static_cast<int64_t>(w.ctr[0]), p.rows));
+  // Blocks that find the list empty or used up leave without an atomic: the
+  // same-address atomics of a grid of blocks serialize (about 25 us for the
+  // 2048 blocks of an empty list at c3); the cursor is read from L2 first.
+  if (listed <= 0) return;
   for (;;) {
-    if (threadIdx.x == 0) s_next = atomicAdd(&w.ctr[1], 1);
+    if (threadIdx.x == 0) {
+      const int seen = __hip_atomic_load(&w.ctr[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_next = (seen >= listed) ? listed : atomicAdd(&w.ctr[1], 1);
+    }
     __syncthreads();
     const int r = s_next;
     __syncthreads();  // every thread holds r before thread 0 takes the next one
